@@ -1,0 +1,317 @@
+"""Decode-step benchmark of the paged KV-cache path on one MI355X.
+
+Workload (default): Llama-3-8B-shaped KV path -- 32 layers, 32 q / 8 kv
+heads, head_dim 128, fp16 KV, 16-token pages, batch 256, every sequence at
+8192 tokens of context, pool fragmented (pages drawn from a shuffled free
+list, then 10 % of the sequences freed and re-allocated).  One step = for
+each of the 32 layers: append the new token's K/V (position 8191, through
+the block table) then paged decode attention over all 8192 tokens.  Inputs
+(q, k, v, block tables, lengths) are resident in HBM before timing.
+
+Prints one JSON line (see --help).  --config selects other shapes:
+  llama8b_b32     Llama-3-8B shape, batch 32, context U[512, 4096]
+  llama70b_b8     Llama-3-70B shape (64 q / 8 kv), page 32, batch 8 x 32768
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "paged decode-attn+append HBM GB/s (% of peak) and decode tokens/s, 1 MI355X"
+
+CONFIGS = {
+    "llama8b_b256_8k": dict(workload="llama3-8b-shape decode step: append + paged attention",
+                            layers=32, q_heads=32, kv_heads=8, head_dim=128, page_tokens=16,
+                            batch=256, context="8192", frag=True),
+    "llama8b_b32": dict(workload="llama3-8b-shape decode step, ragged context",
+                        layers=32, q_heads=32, kv_heads=8, head_dim=128, page_tokens=16,
+                        batch=32, context="U[512,4096]", frag=True),
+    "llama70b_b8": dict(workload="llama3-70b-shape decode step, long context",
+                        layers=80, q_heads=64, kv_heads=8, head_dim=128, page_tokens=32,
+                        batch=8, context="32768", frag=False),
+}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def seq_lengths(cfg, seed):
+    b = cfg["batch"]
+    c = cfg["context"]
+    if c.startswith("U["):
+        lo, hi = [int(x) for x in c[2:-1].split(",")]
+        return np.random.default_rng(seed).integers(lo, hi + 1, size=b).astype(np.int64)
+    return np.full(b, int(c), np.int64)
+
+
+def build_tables(gi, cfg, lens, seed):
+    """Block tables from the host allocator (PagedKVManager), starting from a
+    shuffled free list; with frag, 10 % of the sequences are then freed and
+    allocated again so their pages come back in a different order."""
+    P = cfg["page_tokens"]
+    need = int(sum((int(n) + P - 1) // P for n in lens))
+    pages = need + (need // 100 + 16 if cfg["frag"] else 0)
+    rng = np.random.default_rng(seed)
+    mgr = gi.PagedKVManager(cfg["layers"], cfg["kv_heads"] * cfg["head_dim"], pages, P)
+    if cfg["frag"]:
+        mgr.SetFreeList(rng.permutation(pages).astype(np.int32))
+    seqs = []
+    for n in lens:
+        s = mgr.AllocateSequence()
+        mgr.AppendTokens(s, int(n))
+        seqs.append(s)
+    if cfg["frag"]:
+        k = max(1, len(seqs) // 10)
+        for i in rng.choice(len(seqs), size=k, replace=False):
+            mgr.FreeSequence(seqs[i])
+            s = mgr.AllocateSequence()
+            mgr.AppendTokens(s, int(lens[i]))
+            seqs[i] = s
+    max_blocks = max((int(n) + P - 1) // P for n in lens)
+    bt = np.zeros((len(lens), max_blocks), np.int32)
+    for i, s in enumerate(seqs):
+        ids = mgr.Tables[s].BlockIDs
+        bt[i, :len(ids)] = ids
+    return mgr, pages, bt
+
+
+def fill_pool(torch, pool, cfg, lens, bt, dev, seed):
+    """Writes every cached token of every layer through the append path
+    (f32 N(0,1) -> truncated fp16), a chunk of sequences at a time."""
+    P = cfg["page_tokens"]
+    kv_dim = cfg["kv_heads"] * cfg["head_dim"]
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    chunk_tok = 1 << 19
+    # (ids, slots) for all tokens of all sequences, in sequence order
+    ids = np.concatenate([np.repeat(bt[i, :(int(n) + P - 1) // P], P)[:int(n)]
+                          for i, n in enumerate(lens)]).astype(np.int32)
+    slots = np.concatenate([np.arange(int(n), dtype=np.int32) % P for n in lens])
+    ids_d = torch.from_numpy(ids).to(dev)
+    slots_d = torch.from_numpy(slots).to(dev)
+    total = ids.size
+    kbuf = torch.empty((min(chunk_tok, total), kv_dim), dtype=torch.float32, device=dev)
+    vbuf = torch.empty_like(kbuf)
+    for l in range(cfg["layers"]):
+        for a in range(0, total, chunk_tok):
+            b = min(total, a + chunk_tok)
+            kb, vb = kbuf[:b - a], vbuf[:b - a]
+            kb.normal_(generator=gen)
+            vb.normal_(generator=gen)
+            pool.Write(l, ids_d[a:b], slots_d[a:b], kb, vb)
+        if l % 8 == 7:
+            pool.synchronize()
+            log("filled layer", l)
+    pool.synchronize()
+    del kbuf, vbuf, ids_d, slots_d
+
+
+def step_bytes(cfg, lens):
+    """Algorithmic HBM bytes of one decode step, split into the attention
+    kernel's and the append kernel's share (per step, all layers)."""
+    P = cfg["page_tokens"]
+    kv_dim = cfg["kv_heads"] * cfg["head_dim"]
+    qd = cfg["q_heads"] * cfg["head_dim"]
+    e = 2  # fp16
+    L = np.asarray(lens, np.int64)
+    attn = (2 * L * kv_dim * e + ((L + P - 1) // P) * 4 + qd * 4 + qd * 4 + 4).sum()
+    append = len(L) * (2 * kv_dim * 4 + 2 * kv_dim * e + 4 + 4)
+    return int(attn) * cfg["layers"], int(append) * cfg["layers"]
+
+
+def cpu_baseline(oracle, cfg, budget_s=12.0):
+    """The oracle's decode (widen fp16 -> f32, then the reference loop of
+    forward.go:242-267) on one host core for a bounded sample of the same
+    workload: whole (sequence, layer) units at the configured context,
+    repeated until about budget_s of CPU work; extrapolated to the full
+    step by the number of units."""
+    H, kvh, hd = cfg["q_heads"], cfg["kv_heads"], cfg["head_dim"]
+    kv_dim = kvh * hd
+    lens = seq_lengths(cfg, 11)
+    L = int(np.median(lens))
+    k = oracle.fp32_to_fp16(oracle.normal(1, (L, kv_dim))).view(np.uint8).reshape(L, 2 * kv_dim)
+    v = oracle.fp32_to_fp16(oracle.normal(2, (L, kv_dim))).view(np.uint8).reshape(L, 2 * kv_dim)
+    q = oracle.normal(3, (1, H * hd))
+    sc = oracle.attn_scale(hd)
+    units, t0 = 0, time.perf_counter()
+    while True:
+        oracle.decode_batch(1, q, k, v, np.zeros(1, np.int64), np.array([L], np.int32), H, kvh,
+                            hd, sc)
+        units += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or units >= 256:
+            break
+    per_unit = el / units
+    full_units = float(np.sum(lens)) / L * cfg["layers"]
+    step_s = per_unit * full_units
+    return {"value": round(cfg["batch"] / step_s, 4), "unit": "tokens/s", "cores": 1,
+            "kind": "port",
+            "sample": "%d (sequence, layer) decode units at L=%d on 1 thread, %.1f s; "
+                      "extrapolated x%.0f to the full step" % (units, L, el, full_units / units),
+            "ms_per_step": round(step_s * 1e3, 1)}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="llama8b_b256_8k", choices=sorted(CONFIGS))
+    ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-parity", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="also run one device copy of this many MiB (counter calibration)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: the paged decode path runs on a single MI355X "
+              "(--gpus %d is not supported; sharding is described in DESIGN.md)" % args.gpus,
+              file=sys.stderr)
+        sys.exit(2)
+
+    import importlib
+    import torch
+    gi = importlib.import_module("go-infer_amd")
+    gi.lib()
+    assert torch.cuda.is_available(), "bench.py needs a HIP device"
+    dev = torch.device("cuda:0")
+    cfg = CONFIGS[args.config]
+    H, kvh, hd, P, layers = (cfg["q_heads"], cfg["kv_heads"], cfg["head_dim"],
+                             cfg["page_tokens"], cfg["layers"])
+    kv_dim = kvh * hd
+    lens = seq_lengths(cfg, args.seed)
+    batch = len(lens)
+
+    t_setup = time.perf_counter()
+    mgr, pages, bt = build_tables(gi, cfg, lens, args.seed)
+    log("tables built: %d pages, max_blocks %d (%.1f s)" % (pages, bt.shape[1],
+                                                           time.perf_counter() - t_setup))
+    stream = torch.cuda.Stream(dev)
+    torch.cuda.set_stream(stream)
+    pool = gi.PagedKVCache(layers, kvh, hd, P, pages, gi.KV_F16, stream=stream)
+    log("pool: %.1f GiB" % (pool.page_bytes()[1] / 2**30))
+    fill_pool(torch, pool, cfg, lens, bt, dev, args.seed)
+    log("pool filled (%.1f s)" % (time.perf_counter() - t_setup))
+
+    bt_d = torch.from_numpy(bt).to(dev)
+    sl_d = torch.from_numpy(lens.astype(np.int32)).to(dev)
+    max_len = int(lens.max())
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed + 1)
+    q = torch.randn((layers, batch, H * hd), generator=gen, device=dev)
+    kn = torch.randn((layers, batch, kv_dim), generator=gen, device=dev)
+    vn = torch.randn((layers, batch, kv_dim), generator=gen, device=dev)
+    out = torch.empty((layers, batch, H * hd), device=dev)
+    scale = gi.attn_scale(hd)
+    n_ev = layers * args.steps
+    ev0 = [torch.cuda.Event(enable_timing=True) for _ in range(n_ev)]
+    ev1 = [torch.cuda.Event(enable_timing=True) for _ in range(n_ev)]
+
+    def step(record=None):
+        for l in range(layers):
+            pool.WriteAtLen(l, bt_d, sl_d, kn[l], vn[l])
+            if record is not None:
+                ev0[record + l].record(stream)
+            pool.AttentionGQA(out[l], q[l], l, bt_d, sl_d, H, scale, max_len)
+            if record is not None:
+                ev1[record + l].record(stream)
+
+    for _ in range(args.warmup):
+        step()
+    pool.synchronize()
+    torch.cuda.synchronize()
+    s0 = torch.cuda.Event(enable_timing=True)
+    s1 = torch.cuda.Event(enable_timing=True)
+    w0 = time.perf_counter()
+    s0.record(stream)
+    for i in range(args.steps):
+        step(record=i * layers)
+    s1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - w0
+    pool.synchronize()
+    ms_step = s0.elapsed_time(s1) / args.steps
+    attn_ms = float(np.mean([a.elapsed_time(b) for a, b in zip(ev0, ev1)]))
+    attn_bytes, app_bytes = step_bytes(cfg, lens)
+    tot_gbs = (attn_bytes + app_bytes) / (ms_step * 1e-3) / 1e9
+    attn_gbs = (attn_bytes / layers) / (attn_ms * 1e-3) / 1e9
+    tok_s = batch / (ms_step * 1e-3)
+    log("step %.3f ms (wall %.3f ms), attention kernel %.3f ms/launch" %
+        (ms_step, wall * 1e3 / args.steps, attn_ms))
+
+    if args.calibrate_copy:
+        n = args.calibrate_copy * 2**20 // 4
+        a = torch.empty(n, dtype=torch.float32, device=dev).fill_(1.0)
+        b = torch.empty_like(a)
+        b.copy_(a)
+        torch.cuda.synchronize()
+        del a, b
+
+    parity = None
+    if not args.no_parity:
+        import oracle
+        rng = np.random.default_rng(args.seed + 7)
+        worst = 0.0
+        checked = []
+        for _ in range(2):
+            i, l = int(rng.integers(batch)), int(rng.integers(layers))
+            n = int(lens[i])
+            kw, vw = pool.Get(l, bt_d[i], n, widen=True)
+            pool.synchronize()
+            want = oracle.attention_decode(q[l, i].cpu().numpy(), kw.cpu().numpy(),
+                                           vw.cpu().numpy(), H, kvh, hd, n, scale)
+            got = out[l, i].cpu().numpy().astype(np.float64).reshape(H, hd)
+            w = want.astype(np.float64).reshape(H, hd)
+            err = (np.abs(got - w).max(axis=1) / np.abs(w).max(axis=1)).max()
+            worst = max(worst, float(err))
+            checked.append([i, l])
+        parity = {"sampled_seq_layer": checked, "max_rel_err": worst, "tol": 1e-3,
+                  "pass": bool(worst <= 1e-3)}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        import oracle
+        cpu = cpu_baseline(oracle, cfg)
+
+    res = {
+        "metric": METRIC,
+        "value": round(tot_gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": cfg["workload"], "layers": layers, "q_heads": H,
+                   "kv_heads": kvh, "head_dim": hd, "kv_dtype": "f16", "page_tokens": P,
+                   "batch": batch, "context": cfg["context"], "pool_pages": pages,
+                   "fragmented_pool": cfg["frag"]},
+        "hbm_frac_of_peak": round(tot_gbs / HBM_PEAK_GBS, 4),
+        "tokens_per_s": round(tok_s, 1),
+        "decode_kernel": ["vector-alu", "matrix-core"][pool.decode_kernel(H)],
+        "roofline": {"bound": "hbm", "achieved": round(attn_gbs, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(attn_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": None, "kernel": "paged decode attention",
+                     "launch_ms": round(attn_ms, 4),
+                     "bytes_per_launch": attn_bytes // layers},
+        "cpu_baseline": cpu,
+        "parity": parity,
+    }
+    print(json.dumps(res), flush=True)
+    pool.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,364 @@
+"""go-infer_amd: MI355X paged KV-cache path for go-infer.
+
+Host-side mirror of the reference's interface for this path, over the C ABI
+in include/goinfer_paged.h (libgoinfer_paged.so, hand-written HIP for gfx950):
+
+  PagedKVManager  pkg/engine/paged_kv.go:49-148 (block allocator, C++ on the
+                  host: NewPagedKVManager / AllocateSequence / AppendToken /
+                  FreeSequence, Tables, FreeBlocks)
+  PagedKVCache    the device page pool; Write / Get restate KVCache.Write /
+                  Get (pkg/engine/kvcache.go:146-214) on pages, AttentionGQA /
+                  AttentionGQABatch restate the decode and chunked-prefill
+                  attention of pkg/engine/forward.go:242-267 / 547-577 (the
+                  seams metal.AttentionGQA / AttentionGQABatch,
+                  pkg/metal/metal_darwin.go:711-727, 963-981).
+
+Errors are raised as GIError carrying the library's negative code, where the
+Go code returns an error value.  Device buffers are torch tensors on the
+pool's device; nothing here falls back to the CPU: if the library is not
+built, loading it raises.
+"""
+import ctypes
+import os
+
+__all__ = ["lib", "GIError", "PagedKVManager", "PagedKVCache", "KV_F32", "KV_F16", "KV_Q8_0",
+           "EXPORTS", "LIB_PATH", "attn_scale"]
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libgoinfer_paged.so")
+
+KV_F32, KV_F16, KV_Q8_0 = 0, 1, 2
+GI_OK = 0
+ERR_NAMES = {-1: "GI_ERR_NO_DEVICE", -2: "GI_ERR_OOM", -3: "GI_ERR_BAD_ARG",
+             -4: "GI_ERR_POOL_EXHAUSTED", -5: "GI_ERR_HIP", -6: "GI_ERR_UNKNOWN_SEQ",
+             -7: "GI_ERR_BAD_PAGE"}
+
+_c_int, _c_i64, _vp = ctypes.c_int, ctypes.c_int64, ctypes.c_void_p
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_intp = ctypes.POINTER(ctypes.c_int)
+
+# Every symbol include/goinfer_paged.h declares, with its ctypes signature.
+EXPORTS = {
+    "gi_last_error": (ctypes.c_char_p, []),
+    "gi_device_count": (_c_int, []),
+    "gi_device_name": (_c_int, [ctypes.c_char_p, _c_int]),
+    "gi_kvmgr_create": (_c_int, [_c_int, _c_int, _c_int, _c_int, ctypes.POINTER(_vp)]),
+    "gi_kvmgr_destroy": (None, [_vp]),
+    "gi_kvmgr_allocate_sequence": (_c_int, [_vp, _intp]),
+    "gi_kvmgr_append_token": (_c_int, [_vp, _c_int, _i32p, _i32p]),
+    "gi_kvmgr_append_tokens": (_c_int, [_vp, _c_int, _c_int, _i32p, _i32p, _intp]),
+    "gi_kvmgr_free_sequence": (_c_int, [_vp, _c_int]),
+    "gi_kvmgr_block_table": (_c_int, [_vp, _c_int, _i32p, _c_int, _intp, _intp]),
+    "gi_kvmgr_free_list": (_c_int, [_vp, _i32p, _c_int, _intp]),
+    "gi_kvmgr_set_free_list": (_c_int, [_vp, _i32p, _c_int]),
+    "gi_paged_create": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_i64, _c_int,
+                                 ctypes.POINTER(_vp)]),
+    "gi_paged_destroy": (None, [_vp]),
+    "gi_paged_page_bytes": (_c_int, [_vp, ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64)]),
+    "gi_paged_set_stream": (_c_int, [_vp, _vp]),
+    "gi_paged_stream": (_vp, [_vp]),
+    "gi_synchronize": (_c_int, [_vp]),
+    "gi_dev_alloc": (_c_int, [_vp, ctypes.c_size_t, ctypes.POINTER(_vp)]),
+    "gi_dev_free": (_c_int, [_vp, _vp]),
+    "gi_memcpy_h2d": (_c_int, [_vp, _vp, _vp, ctypes.c_size_t]),
+    "gi_memcpy_d2h": (_c_int, [_vp, _vp, _vp, ctypes.c_size_t]),
+    "gi_paged_append": (_c_int, [_vp, _c_int, _c_int, _vp, _vp, _vp, _vp]),
+    "gi_paged_append_at_len": (_c_int, [_vp, _c_int, _c_int, _vp, _c_int, _vp, _vp, _vp]),
+    "gi_paged_gather": (_c_int, [_vp, _c_int, _vp, _c_int, _vp, _vp, _c_int]),
+    "gi_paged_decode_attention": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _c_int,
+                                           _vp, _c_int, ctypes.c_float]),
+    "gi_paged_decode_step": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp,
+                                      _c_int, _vp, _c_int, ctypes.c_float]),
+    "gi_paged_prefill_attention": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp,
+                                            _c_int, _vp, ctypes.c_float]),
+    "gi_paged_decode_kernel": (_c_int, [_vp, _c_int]),
+}
+
+_lib = None
+
+
+def lib():
+    """Loads libgoinfer_paged.so (built by go-infer_amd/build.py).  Raises if
+    it is missing: there is no other implementation to fall back to."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError("libgoinfer_paged.so is not built: run python go-infer_amd/build.py")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in EXPORTS.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+class GIError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__("%s (%d): %s" % (ERR_NAMES.get(code, "GI_ERR"), code, msg))
+        self.code = code
+
+
+def _check(rc):
+    if rc != GI_OK:
+        msg = lib().gi_last_error()
+        raise GIError(rc, msg.decode() if msg else "")
+    return rc
+
+
+def attn_scale(head_dim):
+    """float32(1 / math_sqrt(head_dim)) (pkg/engine/forward.go:33, 771-780):
+    ten Newton steps from x/2 in float64, then rounded to float32."""
+    import numpy as np
+    x = float(head_dim)
+    if x <= 0:
+        return np.float32(0.0)
+    z = x / 2
+    for _ in range(10):
+        z = (z + x / z) / 2
+    return np.float32(1.0 / z)
+
+
+class _Table:
+    """BlockTable (paged_kv.go:41-46) snapshot."""
+
+    def __init__(self, seq_id, ids, num_tokens, block_size):
+        self.SequenceID, self.BlockIDs, self.NumTokens, self.BlockSize = (
+            seq_id, ids, num_tokens, block_size)
+
+
+class PagedKVManager:
+    """NewPagedKVManager(numLayers, kvDim, totalBlocks, blockSize)
+    (paged_kv.go:62-87), backed by the C++ allocator in the library."""
+
+    def __init__(self, num_layers, kv_dim, total_blocks, block_size):
+        h = _vp()
+        _check(lib().gi_kvmgr_create(num_layers, kv_dim, total_blocks, block_size,
+                                     ctypes.byref(h)))
+        self._h = h
+        self.NumLayers, self.KVDim = num_layers, kv_dim
+        self.BlockSize = block_size if block_size > 0 else 16
+        self.TotalBlocks = total_blocks if total_blocks > 0 else 256
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h and _lib is not None:
+            _lib.gi_kvmgr_destroy(h)
+            self._h = None
+
+    def AllocateSequence(self):
+        sid = _c_int()
+        _check(lib().gi_kvmgr_allocate_sequence(self._h, ctypes.byref(sid)))
+        return sid.value
+
+    def AppendToken(self, seq_id):
+        """Returns (blockID, slotOffset); raises GIError with
+        GI_ERR_UNKNOWN_SEQ / GI_ERR_POOL_EXHAUSTED (paged_kv.go:111-120)."""
+        b, s = ctypes.c_int32(), ctypes.c_int32()
+        _check(lib().gi_kvmgr_append_token(self._h, seq_id, ctypes.byref(b), ctypes.byref(s)))
+        return b.value, s.value
+
+    def AppendTokens(self, seq_id, n):
+        """n AppendToken calls; returns (block_ids, slots) int32 arrays."""
+        import numpy as np
+        ids = np.zeros(max(n, 1), np.int32)
+        slots = np.zeros(max(n, 1), np.int32)
+        done = _c_int()
+        _check(lib().gi_kvmgr_append_tokens(self._h, seq_id, n, ids.ctypes.data_as(_i32p),
+                                            slots.ctypes.data_as(_i32p), ctypes.byref(done)))
+        return ids[:n], slots[:n]
+
+    def FreeSequence(self, seq_id):
+        _check(lib().gi_kvmgr_free_sequence(self._h, seq_id))
+
+    def BlockTable(self, seq_id):
+        import numpy as np
+        nb, nt = _c_int(), _c_int()
+        _check(lib().gi_kvmgr_block_table(self._h, seq_id, None, 0, ctypes.byref(nb),
+                                          ctypes.byref(nt)))
+        ids = np.zeros(max(nb.value, 1), np.int32)
+        _check(lib().gi_kvmgr_block_table(self._h, seq_id, ids.ctypes.data_as(_i32p), ids.size,
+                                          ctypes.byref(nb), ctypes.byref(nt)))
+        return _Table(seq_id, [int(x) for x in ids[:nb.value]], nt.value, self.BlockSize)
+
+    @property
+    def Tables(self):
+        """Lookup by sequence id: mgr.Tables[seq].BlockIDs / .NumTokens."""
+        mgr = self
+
+        class _View:
+            def __getitem__(self, sid):
+                return mgr.BlockTable(sid)
+
+            def __contains__(self, sid):
+                try:
+                    mgr.BlockTable(sid)
+                    return True
+                except GIError:
+                    return False
+        return _View()
+
+    @property
+    def FreeBlocks(self):
+        import numpy as np
+        n = _c_int()
+        _check(lib().gi_kvmgr_free_list(self._h, None, 0, ctypes.byref(n)))
+        ids = np.zeros(max(n.value, 1), np.int32)
+        _check(lib().gi_kvmgr_free_list(self._h, ids.ctypes.data_as(_i32p), ids.size,
+                                        ctypes.byref(n)))
+        return [int(x) for x in ids[:n.value]]
+
+    def SetFreeList(self, ids):
+        import numpy as np
+        a = np.ascontiguousarray(ids, np.int32)
+        _check(lib().gi_kvmgr_set_free_list(self._h, a.ctypes.data_as(_i32p), a.size))
+
+
+def _ptr(t, dtype=None, what="tensor"):
+    """Device pointer of a contiguous torch tensor (None -> NULL)."""
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise GIError(-3, "%s must be a device tensor" % what)
+    if not t.is_contiguous():
+        raise GIError(-3, "%s must be contiguous" % what)
+    if dtype is not None and t.dtype != dtype:
+        raise GIError(-3, "%s must be %s, got %s" % (what, dtype, t.dtype))
+    return _vp(t.data_ptr())
+
+
+class PagedKVCache:
+    """Device page pool for num_layers layers (one page id covers every
+    layer, like KVBlock in paged_kv.go:13-38).  kv_type: KV_F32, KV_F16 or
+    KV_Q8_0."""
+
+    def __init__(self, num_layers, num_kv_heads, head_dim, page_tokens, num_pages,
+                 kv_type=KV_F32, stream=None):
+        """stream: a torch.cuda.Stream (default: torch's current stream), so
+        the pool's kernels are ordered with the torch work that produces and
+        consumes its device buffers."""
+        import torch
+        h = _vp()
+        _check(lib().gi_paged_create(num_layers, num_kv_heads, head_dim, page_tokens, num_pages,
+                                     kv_type, ctypes.byref(h)))
+        self._h = h
+        if stream is None:
+            stream = torch.cuda.current_stream()
+        self.set_stream(stream.cuda_stream)
+        self.num_layers, self.num_kv_heads, self.head_dim = num_layers, num_kv_heads, head_dim
+        self.page_tokens, self.num_pages, self.kv_type = page_tokens, num_pages, kv_type
+        self.kv_dim = num_kv_heads * head_dim
+
+    def close(self):
+        if getattr(self, "_h", None) and _lib is not None:
+            _lib.gi_paged_destroy(self._h)
+        self._h = None
+
+    def __del__(self):
+        self.close()
+
+    @property
+    def handle(self):
+        return self._h
+
+    def bytes_per_vec(self):
+        """Stored bytes of one token vector (kvcache.go:92: q8_0 is
+        ((kvDim+31)/32)*34)."""
+        if self.kv_type == KV_F32:
+            return 4 * self.kv_dim
+        if self.kv_type == KV_F16:
+            return 2 * self.kv_dim
+        return (self.kv_dim + 31) // 32 * 34
+
+    def page_bytes(self):
+        pb, tot = _c_i64(), _c_i64()
+        _check(lib().gi_paged_page_bytes(self._h, ctypes.byref(pb), ctypes.byref(tot)))
+        return pb.value, tot.value
+
+    def set_stream(self, stream_handle):
+        """Raw hipStream_t value (0 = HIP's default stream)."""
+        _check(lib().gi_paged_set_stream(self._h, _vp(stream_handle) if stream_handle else None))
+
+    def stream(self):
+        return lib().gi_paged_stream(self._h)
+
+    def synchronize(self):
+        _check(lib().gi_synchronize(self._h))
+
+    def decode_kernel(self, num_heads):
+        return lib().gi_paged_decode_kernel(self._h, num_heads)
+
+    # -- KVCache.Write / Get on pages ------------------------------------
+    def Write(self, layer, block_ids, slots, k, v):
+        """Stores token vectors k, v [n, kv_dim] float32 at (block_ids[i],
+        slots[i]) of one layer (KVCache.Write, kvcache.go:146-180)."""
+        import torch
+        n = int(block_ids.numel())
+        _check(lib().gi_paged_append(self._h, layer, n, _ptr(block_ids, torch.int32, "block_ids"),
+                                     _ptr(slots, torch.int32, "slots"),
+                                     _ptr(k, torch.float32, "k"), _ptr(v, torch.float32, "v")))
+
+    def WriteAtLen(self, layer, block_tables, seq_lens, k, v):
+        import torch
+        batch = int(seq_lens.numel())
+        _check(lib().gi_paged_append_at_len(
+            self._h, layer, batch, _ptr(block_tables, torch.int32, "block_tables"),
+            int(block_tables.shape[1]) if batch else 0, _ptr(seq_lens, torch.int32, "seq_lens"),
+            _ptr(k, torch.float32, "k"), _ptr(v, torch.float32, "v")))
+
+    def Get(self, layer, block_table, n_tok, widen=False):
+        """Contiguous K, V of tokens [0, n_tok) (KVCache.Get/ForkAt layout).
+        widen=False: stored bytes as uint8 [n_tok, bytes_per_vec];
+        widen=True: float32 [n_tok, kv_dim]."""
+        import torch
+        dev = block_table.device
+        if widen:
+            ko = torch.empty((n_tok, self.kv_dim), dtype=torch.float32, device=dev)
+        else:
+            ko = torch.empty((n_tok, self.bytes_per_vec()), dtype=torch.uint8, device=dev)
+        vo = torch.empty_like(ko)
+        _check(lib().gi_paged_gather(self._h, layer, _ptr(block_table, torch.int32, "block_table"),
+                                     n_tok, _ptr(ko), _ptr(vo), 1 if widen else 0))
+        return ko, vo
+
+    # -- attention -------------------------------------------------------
+    def AttentionGQA(self, out, q, layer, block_tables, seq_lens, num_heads, attn_scale,
+                     max_seq_len=None):
+        """Decode attention of forward.go:242-267 for a batch; q/out
+        [batch, num_heads*head_dim] float32."""
+        import torch
+        batch = int(seq_lens.numel())
+        if max_seq_len is None:
+            max_seq_len = int(seq_lens.max().item()) if batch else 0
+        _check(lib().gi_paged_decode_attention(
+            self._h, layer, batch, num_heads, _ptr(q, torch.float32, "q"),
+            _ptr(out, torch.float32, "out"), _ptr(block_tables, torch.int32, "block_tables"),
+            int(block_tables.shape[1]) if batch else 0, _ptr(seq_lens, torch.int32, "seq_lens"),
+            int(max_seq_len), float(attn_scale)))
+
+    def DecodeStep(self, out, q, k, v, layer, block_tables, seq_lens, num_heads, attn_scale,
+                   max_seq_len=None):
+        """Append the new token at position seq_lens[b]-1, then decode
+        attention over seq_lens[b] tokens (forward.go:236-267)."""
+        import torch
+        batch = int(seq_lens.numel())
+        if max_seq_len is None:
+            max_seq_len = int(seq_lens.max().item()) if batch else 0
+        _check(lib().gi_paged_decode_step(
+            self._h, layer, batch, num_heads, _ptr(q, torch.float32, "q"),
+            _ptr(k, torch.float32, "k"), _ptr(v, torch.float32, "v"),
+            _ptr(out, torch.float32, "out"), _ptr(block_tables, torch.int32, "block_tables"),
+            int(block_tables.shape[1]) if batch else 0, _ptr(seq_lens, torch.int32, "seq_lens"),
+            int(max_seq_len), float(attn_scale)))
+
+    def AttentionGQABatch(self, out, q, layer, block_tables, start_pos, num_heads, attn_scale,
+                          chunk_len):
+        """Chunked-prefill causal attention of forward.go:547-577; q/out
+        [batch, chunk_len, num_heads*head_dim] float32."""
+        import torch
+        batch = int(start_pos.numel())
+        _check(lib().gi_paged_prefill_attention(
+            self._h, layer, batch, chunk_len, num_heads, _ptr(q, torch.float32, "q"),
+            _ptr(out, torch.float32, "out"), _ptr(block_tables, torch.int32, "block_tables"),
+            int(block_tables.shape[1]) if batch else 0, _ptr(start_pos, torch.int32, "start_pos"),
+            float(attn_scale)))

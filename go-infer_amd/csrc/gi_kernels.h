@@ -1,0 +1,79 @@
+// Launchers of the paged KV-cache kernels (internal to the library; the
+// public C ABI is include/goinfer_paged.h).
+#pragma once
+
+#include "gi_common.h"
+
+namespace gi {
+
+hipError_t launch_append(const PoolLayout &L, uint8_t *base, int n_tok, const int32_t *block_ids,
+                         const int32_t *slots, const float *k, const float *v, int *status,
+                         hipStream_t st);
+
+hipError_t launch_append_at_len(const PoolLayout &L, uint8_t *base, int batch,
+                                const int32_t *block_tables, int max_blocks,
+                                const int32_t *seq_lens, const float *k, const float *v,
+                                int *status, hipStream_t st);
+
+hipError_t launch_gather(const PoolLayout &L, const uint8_t *base, const int32_t *table, int n_tok,
+                         void *k_out, void *v_out, int widen, int *status, hipStream_t st);
+
+// Attention over paged context.  Decode: q/out are [batch][num_heads][head_dim]
+// float32, block_tables is [batch][max_blocks], sequence b attends its first
+// seq_lens[b] tokens.  The same kernels serve chunked prefill on the vector
+// path: n_q queries per sequence, query i of sequence b attends
+// start_pos[b] + i + 1 tokens, q/out are [batch][n_q][num_heads][head_dim].
+struct DecodeArgs {
+    PoolLayout L;
+    const uint8_t *base;
+    const float *q;
+    float *out;
+    const int32_t *block_tables;
+    int max_blocks;
+    const int32_t *seq_lens;
+    int batch;
+    int n_q;                  // queries per sequence (1 for decode)
+    const int32_t *start_pos; // prefill only: tokens cached before the chunk
+    int num_heads;
+    float scale;
+    int split_tokens; // tokens per split, a multiple of the page size
+    int num_splits;
+    float *ws; // partials when num_splits > 1
+    int *status;
+};
+
+// Bytes of split-K workspace needed for a decode launch.
+size_t decode_workspace_bytes(const PoolLayout &L, int batch, int num_heads, int num_splits);
+
+// Picks (split_tokens, num_splits) for a batch whose longest sequence has
+// max_len tokens, so the grid fills the device.
+void decode_plan(const PoolLayout &L, int batch, int num_heads, int max_len, int num_cus,
+                 int *split_tokens, int *num_splits);
+
+// Returns hipErrorInvalidValue for shapes without a kernel instance.
+hipError_t launch_decode(const DecodeArgs &a, hipStream_t st);
+
+// Which kernel launch_decode uses for a layout/head count: 0 vector-ALU,
+// 1 matrix-core.  Exposed for tests and the bench.
+int decode_kernel_kind(const PoolLayout &L, int num_heads);
+
+// Chunked-prefill causal attention over paged context: query i of sequence b
+// (i < chunk_len) attends tokens [0, start_pos[b] + i + 1).
+struct PrefillArgs {
+    PoolLayout L;
+    const uint8_t *base;
+    const float *q; // [batch][chunk_len][num_heads][head_dim]
+    float *out;
+    const int32_t *block_tables;
+    int max_blocks;
+    const int32_t *start_pos;
+    int batch;
+    int chunk_len;
+    int num_heads;
+    float scale;
+    int *status;
+};
+
+hipError_t launch_prefill(const PrefillArgs &a, hipStream_t st);
+
+} // namespace gi

@@ -1,0 +1,322 @@
+// Per-token K/V append into pages and block gather back to the reference's
+// contiguous layout.
+//
+// Append restates, on the page layout of gi_common.h, what the reference does
+// when it stores one token vector:
+//   f32  : copy            (pkg/engine/kvcache.go:173-178, forward.go:236-240)
+//   f16  : FP32ToFP16 per element, truncating (pkg/quant/fp16.go:38-69)
+//   q8_0 : QuantizeQ8_0 of the whole kv_dim vector (kvcache.go:152-161,
+//          pkg/quant/quant.go:407-456), blocks of 32 never straddle a head
+//          because head_dim % 32 == 0.
+// Gather (KVCache.Get / ForkAt, kvcache.go:183-284) rebuilds tokens [0, n)
+// of one sequence from its block table: token t lives at
+// (block_table[t / page_tokens], t % page_tokens) (paged_kv.go:107-131).
+#include "gi_common.h"
+#include "gi_kernels.h"
+
+namespace gi {
+
+namespace {
+
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ void raise_flag(int *status, int bit)
+{
+    if (status)
+        atomicOr(status, bit);
+}
+
+// Resolves token i's destination page and slot.  Explicit mode reads the
+// caller's (block id, slot) arrays, as returned by AppendToken; decode mode
+// appends at position seq_lens[i]-1 of sequence i through its block table.
+struct Dest {
+    const int32_t *block_ids;
+    const int32_t *slots;
+    const int32_t *block_tables;
+    const int32_t *seq_lens;
+    int max_blocks;
+};
+
+__device__ __forceinline__ bool resolve(const Dest &D, const PoolLayout &L, int i,
+                                        int64_t *page, int *slot, int *status)
+{
+    int64_t p;
+    int s;
+    if (D.block_ids) {
+        p = D.block_ids[i];
+        s = D.slots[i];
+    } else {
+        int len = D.seq_lens[i];
+        int pos = len - 1;
+        int blk = pos >= 0 ? pos / L.page_tokens : -1;
+        if (blk < 0 || blk >= D.max_blocks) {
+            raise_flag(status, FLAG_BAD_SLOT);
+            return false;
+        }
+        p = D.block_tables[(int64_t)i * D.max_blocks + blk];
+        s = pos % L.page_tokens;
+    }
+    if (p < 0 || p >= L.num_pages) {
+        raise_flag(status, FLAG_BAD_PAGE);
+        return false;
+    }
+    if (s < 0 || s >= L.page_tokens) {
+        raise_flag(status, FLAG_BAD_SLOT);
+        return false;
+    }
+    *page = p;
+    *slot = s;
+    return true;
+}
+
+// f32 / f16 append: one thread per (token, element); K and V both.
+template <int KT>
+__global__ __launch_bounds__(kThreads) void append_plain(PoolLayout L, uint8_t *base, int n_tok,
+                                                         Dest D, const float *__restrict__ k,
+                                                         const float *__restrict__ v, int *status)
+{
+    const int hd = L.head_dim;
+    const int kv_dim = L.num_kv_heads * hd;
+    const int64_t total = (int64_t)n_tok * kv_dim;
+    for (int64_t e = (int64_t)blockIdx.x * kThreads + threadIdx.x; e < total;
+         e += (int64_t)gridDim.x * kThreads) {
+        int i = (int)(e / kv_dim);
+        int j = (int)(e - (int64_t)i * kv_dim);
+        int64_t page;
+        int s;
+        // Every thread of a token resolves the same destination; only the
+        // token's first element raises a flag so each bad token counts once.
+        int *st = j == 0 ? status : nullptr;
+        if (!resolve(D, L, i, &page, &s, st))
+            continue;
+        int kvh = j / hd;
+        int d = j - kvh * hd;
+        uint8_t *pg = base + page * L.page_bytes;
+        int64_t ki = ((int64_t)kvh * L.page_tokens + s) * hd + d;
+        int64_t vi = ((int64_t)kvh * hd + d) * L.page_tokens + s;
+        float kx = k[e], vx = v[e];
+        if (KT == KV_F32) {
+            reinterpret_cast<float *>(pg + L.k_off)[ki] = kx;
+            reinterpret_cast<float *>(pg + L.v_off)[vi] = vx;
+        } else {
+            reinterpret_cast<uint16_t *>(pg + L.k_off)[ki] = (uint16_t)float_to_half_bits_rtz(kx);
+            reinterpret_cast<uint16_t *>(pg + L.v_off)[vi] = (uint16_t)float_to_half_bits_rtz(vx);
+        }
+    }
+}
+
+// 32-lane maximum of an unsigned key (lanes of one Q8_0 block).
+__device__ __forceinline__ uint32_t max32(uint32_t x)
+{
+#pragma unroll
+    for (int m = 16; m >= 1; m >>= 1) {
+        uint32_t y = (uint32_t)__shfl_xor((int)x, m, 32);
+        x = x > y ? x : y;
+    }
+    return x;
+}
+
+// q8_0 append: 32 consecutive threads quantise one block of 32 elements.
+__global__ __launch_bounds__(kThreads) void append_q8(PoolLayout L, uint8_t *base, int n_tok,
+                                                      Dest D, const float *__restrict__ k,
+                                                      const float *__restrict__ v, int *status)
+{
+    const int hd = L.head_dim;
+    const int nb = hd / 32;
+    const int kv_dim = L.num_kv_heads * hd;
+    const int64_t total = (int64_t)n_tok * kv_dim; // multiple of 32
+    for (int64_t e0 = (int64_t)blockIdx.x * kThreads; e0 < total;
+         e0 += (int64_t)gridDim.x * kThreads) {
+        int64_t e = e0 + threadIdx.x;
+        // total and kThreads are multiples of 32, so a 32-lane group is
+        // either wholly in range or wholly out: the shuffles below see only
+        // complete groups.
+        if (e >= total)
+            break;
+        int i = (int)(e / kv_dim);
+        int j = (int)(e - (int64_t)i * kv_dim);
+        int64_t page;
+        int s;
+        int *st = j == 0 ? status : nullptr;
+        bool ok = resolve(D, L, i, &page, &s, st);
+        float kx = k[e], vx = v[e];
+        float kinv, vinv;
+        uint32_t kd = q8_scale(__builtin_bit_cast(float, max32(abs_key(kx))), &kinv);
+        uint32_t vd = q8_scale(__builtin_bit_cast(float, max32(abs_key(vx))), &vinv);
+        if (!ok)
+            continue;
+        int kvh = j / hd;
+        int d = j - kvh * hd;
+        int blk = d >> 5;
+        uint8_t *pg = base + page * L.page_bytes;
+        int64_t ki = ((int64_t)kvh * L.page_tokens + s) * hd + d;
+        int64_t vi = ((int64_t)kvh * hd + d) * L.page_tokens + s;
+        reinterpret_cast<int8_t *>(pg + L.k_off)[ki] = (int8_t)q8_quant(kx, kinv);
+        reinterpret_cast<int8_t *>(pg + L.v_off)[vi] = (int8_t)q8_quant(vx, vinv);
+        if ((d & 31) == 0) {
+            reinterpret_cast<uint16_t *>(pg + L.ks_off)[((int64_t)kvh * L.page_tokens + s) * nb + blk] =
+                (uint16_t)kd;
+            reinterpret_cast<uint16_t *>(pg + L.vs_off)[((int64_t)kvh * nb + blk) * L.page_tokens + s] =
+                (uint16_t)vd;
+        }
+    }
+}
+
+// Gather one sequence's tokens [0, n_tok) of one layer.
+//   widen == 0: stored format, the reference's bytes per token vector
+//               (f32: 4*kv_dim, f16: 2*kv_dim, q8_0: kv_dim/32 blocks of
+//               34 bytes = LE fp16 scale + 32 int8, quant.go:38-41).
+//   widen == 1: float32 values (FP16ToFP32 / DequantizeQ8_0).
+template <int KT, int WIDEN>
+__global__ __launch_bounds__(kThreads) void gather_kernel(PoolLayout L, const uint8_t *base,
+                                                          const int32_t *__restrict__ table,
+                                                          int n_tok, uint8_t *kout, uint8_t *vout,
+                                                          int *status)
+{
+    const int hd = L.head_dim;
+    const int kv_dim = L.num_kv_heads * hd;
+    const int P = L.page_tokens;
+    const int nb = hd / 32;
+    // Units per token: one per element, except raw q8_0: one per byte.
+    const int per_tok = (KT == KV_Q8_0 && !WIDEN) ? (kv_dim / 32) * 34 : kv_dim;
+    const int64_t total = (int64_t)n_tok * per_tok;
+    for (int64_t e = (int64_t)blockIdx.x * kThreads + threadIdx.x; e < total;
+         e += (int64_t)gridDim.x * kThreads) {
+        int t = (int)(e / per_tok);
+        int u = (int)(e - (int64_t)t * per_tok);
+        int64_t page = table[t / P];
+        int s = t % P;
+        if (page < 0 || page >= L.num_pages) {
+            if (u == 0)
+                raise_flag(status, FLAG_BAD_PAGE);
+            continue;
+        }
+        const uint8_t *pg = base + page * L.page_bytes;
+        if (KT == KV_Q8_0 && !WIDEN) {
+            int b = u / 34, r = u - b * 34; // global 32-block index and byte
+            int kvh = b / nb, blk = b - kvh * nb;
+            uint8_t kb, vb;
+            if (r < 2) {
+                uint16_t ks = reinterpret_cast<const uint16_t *>(pg + L.ks_off)
+                    [((int64_t)kvh * P + s) * nb + blk];
+                uint16_t vs = reinterpret_cast<const uint16_t *>(pg + L.vs_off)
+                    [((int64_t)kvh * nb + blk) * P + s];
+                kb = (uint8_t)(r == 0 ? ks & 0xFF : ks >> 8);
+                vb = (uint8_t)(r == 0 ? vs & 0xFF : vs >> 8);
+            } else {
+                int d = blk * 32 + (r - 2);
+                kb = (pg + L.k_off)[((int64_t)kvh * P + s) * hd + d];
+                vb = (pg + L.v_off)[((int64_t)kvh * hd + d) * P + s];
+            }
+            kout[e] = kb;
+            vout[e] = vb;
+            continue;
+        }
+        int kvh = u / hd;
+        int d = u - kvh * hd;
+        int64_t ki = ((int64_t)kvh * P + s) * hd + d;
+        int64_t vi = ((int64_t)kvh * hd + d) * P + s;
+        if (KT == KV_F32) {
+            reinterpret_cast<float *>(kout)[e] = reinterpret_cast<const float *>(pg + L.k_off)[ki];
+            reinterpret_cast<float *>(vout)[e] = reinterpret_cast<const float *>(pg + L.v_off)[vi];
+        } else if (KT == KV_F16) {
+            uint16_t kh = reinterpret_cast<const uint16_t *>(pg + L.k_off)[ki];
+            uint16_t vh = reinterpret_cast<const uint16_t *>(pg + L.v_off)[vi];
+            if (WIDEN) {
+                reinterpret_cast<float *>(kout)[e] = half_bits_to_float(kh);
+                reinterpret_cast<float *>(vout)[e] = half_bits_to_float(vh);
+            } else {
+                reinterpret_cast<uint16_t *>(kout)[e] = kh;
+                reinterpret_cast<uint16_t *>(vout)[e] = vh;
+            }
+        } else { // q8_0 widened: float32(int8 q) * FP16ToFP32(d) (quant.go:207)
+            int blk = d >> 5;
+            float ks = half_bits_to_float(reinterpret_cast<const uint16_t *>(pg + L.ks_off)
+                                              [((int64_t)kvh * P + s) * nb + blk]);
+            float vs = half_bits_to_float(reinterpret_cast<const uint16_t *>(pg + L.vs_off)
+                                              [((int64_t)kvh * nb + blk) * P + s]);
+            int8_t kq = reinterpret_cast<const int8_t *>(pg + L.k_off)[ki];
+            int8_t vq = reinterpret_cast<const int8_t *>(pg + L.v_off)[vi];
+            reinterpret_cast<float *>(kout)[e] = (float)kq * ks;
+            reinterpret_cast<float *>(vout)[e] = (float)vq * vs;
+        }
+    }
+}
+
+int grid_for(int64_t units)
+{
+    int64_t g = (units + kThreads - 1) / kThreads;
+    if (g > 65536)
+        g = 65536;
+    return g < 1 ? 1 : (int)g;
+}
+
+hipError_t append_any(const PoolLayout &L, uint8_t *base, int n_tok, const Dest &D,
+                      const float *k, const float *v, int *status, hipStream_t st)
+{
+    if (n_tok <= 0)
+        return hipSuccess;
+    int64_t units = (int64_t)n_tok * L.num_kv_heads * L.head_dim;
+    dim3 grid(grid_for(units)), block(kThreads);
+    switch (L.kv_type) {
+    case KV_F32:
+        hipLaunchKernelGGL(append_plain<KV_F32>, grid, block, 0, st, L, base, n_tok, D, k, v, status);
+        break;
+    case KV_F16:
+        hipLaunchKernelGGL(append_plain<KV_F16>, grid, block, 0, st, L, base, n_tok, D, k, v, status);
+        break;
+    default:
+        hipLaunchKernelGGL(append_q8, grid, block, 0, st, L, base, n_tok, D, k, v, status);
+        break;
+    }
+    return hipGetLastError();
+}
+
+} // namespace
+
+hipError_t launch_append(const PoolLayout &L, uint8_t *base, int n_tok, const int32_t *block_ids,
+                         const int32_t *slots, const float *k, const float *v, int *status,
+                         hipStream_t st)
+{
+    Dest D{block_ids, slots, nullptr, nullptr, 0};
+    return append_any(L, base, n_tok, D, k, v, status, st);
+}
+
+hipError_t launch_append_at_len(const PoolLayout &L, uint8_t *base, int batch,
+                                const int32_t *block_tables, int max_blocks,
+                                const int32_t *seq_lens, const float *k, const float *v,
+                                int *status, hipStream_t st)
+{
+    Dest D{nullptr, nullptr, block_tables, seq_lens, max_blocks};
+    return append_any(L, base, batch, D, k, v, status, st);
+}
+
+hipError_t launch_gather(const PoolLayout &L, const uint8_t *base, const int32_t *table, int n_tok,
+                         void *k_out, void *v_out, int widen, int *status, hipStream_t st)
+{
+    if (n_tok <= 0)
+        return hipSuccess;
+    int kv_dim = L.num_kv_heads * L.head_dim;
+    int64_t per_tok = (L.kv_type == KV_Q8_0 && !widen) ? (kv_dim / 32) * 34 : kv_dim;
+    dim3 grid(grid_for((int64_t)n_tok * per_tok)), block(kThreads);
+    uint8_t *ko = (uint8_t *)k_out, *vo = (uint8_t *)v_out;
+#define GI_GATHER(KT, W) \
+    hipLaunchKernelGGL((gather_kernel<KT, W>), grid, block, 0, st, L, base, table, n_tok, ko, vo, status)
+    if (L.kv_type == KV_F32) {
+        GI_GATHER(KV_F32, 0);
+    } else if (L.kv_type == KV_F16) {
+        if (widen)
+            GI_GATHER(KV_F16, 1);
+        else
+            GI_GATHER(KV_F16, 0);
+    } else {
+        if (widen)
+            GI_GATHER(KV_Q8_0, 1);
+        else
+            GI_GATHER(KV_Q8_0, 0);
+    }
+#undef GI_GATHER
+    return hipGetLastError();
+}
+
+} // namespace gi

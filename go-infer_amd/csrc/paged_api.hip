@@ -1,0 +1,489 @@
+// C ABI of the paged KV-cache library: device pool handle, stream, errors,
+// argument checks, and dispatch to the kernels.  Declarations and the
+// reference interfaces each entry point replaces are in
+// include/goinfer_paged.h.
+#include "../../include/goinfer_paged.h"
+#include "gi_host.h"
+#include "gi_kernels.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <string>
+#include <vector>
+
+namespace gi {
+
+static thread_local std::string g_last_error;
+
+int set_error(int code, const std::string &msg)
+{
+    g_last_error = msg;
+    return code;
+}
+
+void clear_error() { g_last_error.clear(); }
+
+} // namespace gi
+
+struct gi_paged {
+    std::mutex mu;
+    gi::PoolLayout L{};
+    int device = 0;
+    int num_cus = 256;
+    std::vector<uint8_t *> layer_base;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    int *d_status = nullptr;
+    void *ws = nullptr;
+    size_t ws_bytes = 0;
+};
+
+namespace {
+
+int hip_fail(hipError_t e, const char *what)
+{
+    return gi::set_error(GI_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+// Makes the handle's device current for this thread.
+int enter(gi_paged *h, const char *what)
+{
+    if (!h)
+        return gi::set_error(GI_ERR_BAD_ARG, std::string(what) + ": NULL handle");
+    hipError_t e = hipSetDevice(h->device);
+    if (e != hipSuccess)
+        return hip_fail(e, what);
+    return GI_OK;
+}
+
+int check_layer(const gi_paged *h, int layer, const char *what)
+{
+    if (layer < 0 || layer >= h->L.num_layers)
+        return gi::set_error(GI_ERR_BAD_ARG, std::string(what) + ": layer " + std::to_string(layer) +
+                                                 " out of range");
+    return GI_OK;
+}
+
+// Grows the split-K workspace.  Work already queued may still read the old
+// buffer, so the stream is drained before it is released.
+int ensure_ws(gi_paged *h, size_t bytes)
+{
+    if (bytes <= h->ws_bytes)
+        return GI_OK;
+    if (h->ws) {
+        hipError_t e = hipStreamSynchronize(h->stream);
+        if (e != hipSuccess)
+            return hip_fail(e, "workspace resize");
+        (void)hipFree(h->ws);
+        h->ws = nullptr;
+        h->ws_bytes = 0;
+    }
+    size_t want = bytes + bytes / 4;
+    hipError_t e = hipMalloc(&h->ws, want);
+    if (e != hipSuccess) {
+        h->ws = nullptr;
+        return gi::set_error(GI_ERR_OOM, "decode workspace: hipMalloc failed");
+    }
+    h->ws_bytes = want;
+    return GI_OK;
+}
+
+bool supported_heads(const gi::PoolLayout &L, int num_heads)
+{
+    if (num_heads <= 0 || num_heads % L.num_kv_heads)
+        return false;
+    int G = num_heads / L.num_kv_heads;
+    return (L.head_dim == 64 || L.head_dim == 128) && (G == 1 || G == 2 || G == 4 || G == 8);
+}
+
+} // namespace
+
+extern "C" {
+
+const char *gi_last_error(void) { return gi::g_last_error.c_str(); }
+
+int gi_device_count(void)
+{
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess)
+        return 0;
+    return n;
+}
+
+int gi_device_name(char *buf, int cap)
+{
+    if (!buf || cap <= 0)
+        return gi::set_error(GI_ERR_BAD_ARG, "gi_device_name: bad buffer");
+    buf[0] = 0;
+    int dev = 0;
+    if (gi_device_count() <= 0 || hipGetDevice(&dev) != hipSuccess)
+        return gi::set_error(GI_ERR_NO_DEVICE, "no HIP device");
+    hipDeviceProp_t p;
+    hipError_t e = hipGetDeviceProperties(&p, dev);
+    if (e != hipSuccess)
+        return hip_fail(e, "gi_device_name");
+    snprintf(buf, (size_t)cap, "%s (%s, %d CUs)", p.name, p.gcnArchName, p.multiProcessorCount);
+    return GI_OK;
+}
+
+int gi_paged_create(int num_layers, int num_kv_heads, int head_dim, int page_tokens,
+                    int64_t num_pages, int kv_type, gi_paged **out)
+{
+    if (!out)
+        return gi::set_error(GI_ERR_BAD_ARG, "gi_paged_create: out is NULL");
+    *out = nullptr;
+    gi::PoolLayout L;
+    if (gi::make_layout(kv_type, num_layers, num_kv_heads, head_dim, page_tokens, num_pages, &L))
+        return gi::set_error(GI_ERR_BAD_ARG, "gi_paged_create: unsupported shape or kv type");
+    if (gi_device_count() <= 0)
+        return gi::set_error(GI_ERR_NO_DEVICE, "gi_paged_create: no HIP device");
+    gi_paged *h = new (std::nothrow) gi_paged();
+    if (!h)
+        return gi::set_error(GI_ERR_OOM, "gi_paged_create: out of host memory");
+    h->L = L;
+    hipError_t e = hipGetDevice(&h->device);
+    if (e == hipSuccess) {
+        hipDeviceProp_t p;
+        if (hipGetDeviceProperties(&p, h->device) == hipSuccess)
+            h->num_cus = p.multiProcessorCount;
+        e = hipStreamCreateWithFlags(&h->own_stream, hipStreamNonBlocking);
+    }
+    if (e != hipSuccess) {
+        int rc = hip_fail(e, "gi_paged_create");
+        delete h;
+        return rc;
+    }
+    h->stream = h->own_stream;
+    int rc = GI_OK;
+    if (hipMalloc((void **)&h->d_status, sizeof(int)) != hipSuccess) {
+        h->d_status = nullptr;
+        rc = gi::set_error(GI_ERR_OOM, "gi_paged_create: status word");
+    }
+    const size_t layer_bytes = (size_t)(L.page_bytes * L.num_pages);
+    for (int l = 0; rc == GI_OK && l < num_layers; l++) {
+        void *p = nullptr;
+        if (hipMalloc(&p, layer_bytes) != hipSuccess) {
+            rc = gi::set_error(GI_ERR_OOM, "gi_paged_create: cannot allocate layer " + std::to_string(l) +
+                                               " (" + std::to_string(layer_bytes) + " bytes)");
+            break;
+        }
+        h->layer_base.push_back((uint8_t *)p);
+        e = hipMemsetAsync(p, 0, layer_bytes, h->stream);
+        if (e != hipSuccess)
+            rc = hip_fail(e, "gi_paged_create: clear");
+    }
+    if (rc == GI_OK) {
+        e = hipMemsetAsync(h->d_status, 0, sizeof(int), h->stream);
+        if (e == hipSuccess)
+            e = hipStreamSynchronize(h->stream);
+        if (e != hipSuccess)
+            rc = hip_fail(e, "gi_paged_create: clear");
+    }
+    if (rc != GI_OK) {
+        gi_paged_destroy(h);
+        return rc;
+    }
+    *out = h;
+    gi::clear_error();
+    return GI_OK;
+}
+
+void gi_paged_destroy(gi_paged *h)
+{
+    if (!h)
+        return;
+    (void)hipSetDevice(h->device);
+    if (h->own_stream)
+        (void)hipStreamSynchronize(h->own_stream);
+    if (h->stream && h->stream != h->own_stream)
+        (void)hipStreamSynchronize(h->stream);
+    for (uint8_t *p : h->layer_base)
+        (void)hipFree(p);
+    if (h->d_status)
+        (void)hipFree(h->d_status);
+    if (h->ws)
+        (void)hipFree(h->ws);
+    if (h->own_stream)
+        (void)hipStreamDestroy(h->own_stream);
+    delete h;
+}
+
+int gi_paged_page_bytes(const gi_paged *h, int64_t *page_bytes, int64_t *pool_bytes)
+{
+    if (!h)
+        return gi::set_error(GI_ERR_BAD_ARG, "gi_paged_page_bytes: NULL handle");
+    if (page_bytes)
+        *page_bytes = h->L.page_bytes;
+    if (pool_bytes)
+        *pool_bytes = h->L.page_bytes * h->L.num_pages * h->L.num_layers;
+    return GI_OK;
+}
+
+int gi_paged_set_stream(gi_paged *h, void *stream)
+{
+    int rc = enter(h, "gi_paged_set_stream");
+    if (rc)
+        return rc;
+    std::lock_guard<std::mutex> g(h->mu);
+    hipStream_t next = (hipStream_t)stream;
+    if (next != h->stream) {
+        // Work queued on the old stream finishes before the new one runs.
+        hipError_t e = hipStreamSynchronize(h->stream);
+        if (e != hipSuccess)
+            return hip_fail(e, "gi_paged_set_stream");
+    }
+    h->stream = next;
+    return GI_OK;
+}
+
+void *gi_paged_stream(gi_paged *h) { return h ? (void *)h->stream : nullptr; }
+
+int gi_synchronize(gi_paged *h)
+{
+    int rc = enter(h, "gi_synchronize");
+    if (rc)
+        return rc;
+    std::lock_guard<std::mutex> g(h->mu);
+    hipError_t e = hipStreamSynchronize(h->stream);
+    if (e != hipSuccess)
+        return hip_fail(e, "gi_synchronize");
+    int flags = 0;
+    e = hipMemcpy(&flags, h->d_status, sizeof(int), hipMemcpyDeviceToHost);
+    if (e != hipSuccess)
+        return hip_fail(e, "gi_synchronize: status");
+    if (flags) {
+        const int zero = 0;
+        e = hipMemcpy(h->d_status, &zero, sizeof(int), hipMemcpyHostToDevice);
+        if (e != hipSuccess)
+            return hip_fail(e, "gi_synchronize: status reset");
+        std::string why;
+        if (flags & gi::FLAG_BAD_PAGE)
+            why += " page id outside the pool;";
+        if (flags & gi::FLAG_BAD_SLOT)
+            why += " slot or position outside the block table;";
+        return gi::set_error(GI_ERR_BAD_PAGE, "kernel saw:" + why + " affected tokens were skipped");
+    }
+    return GI_OK;
+}
+
+int gi_dev_alloc(gi_paged *h, size_t bytes, void **dptr)
+{
+    int rc = enter(h, "gi_dev_alloc");
+    if (rc)
+        return rc;
+    if (!dptr)
+        return gi::set_error(GI_ERR_BAD_ARG, "gi_dev_alloc: dptr is NULL");
+    *dptr = nullptr;
+    if (hipMalloc(dptr, bytes ? bytes : 1) != hipSuccess) {
+        *dptr = nullptr;
+        return gi::set_error(GI_ERR_OOM, "gi_dev_alloc: hipMalloc(" + std::to_string(bytes) + ") failed");
+    }
+    return GI_OK;
+}
+
+int gi_dev_free(gi_paged *h, void *dptr)
+{
+    int rc = enter(h, "gi_dev_free");
+    if (rc)
+        return rc;
+    std::lock_guard<std::mutex> g(h->mu);
+    hipError_t e = hipStreamSynchronize(h->stream);
+    if (e == hipSuccess && dptr)
+        e = hipFree(dptr);
+    return e == hipSuccess ? GI_OK : hip_fail(e, "gi_dev_free");
+}
+
+int gi_memcpy_h2d(gi_paged *h, void *dst, const void *src, size_t bytes)
+{
+    int rc = enter(h, "gi_memcpy_h2d");
+    if (rc)
+        return rc;
+    std::lock_guard<std::mutex> g(h->mu);
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, h->stream);
+    if (e == hipSuccess)
+        e = hipStreamSynchronize(h->stream);
+    return e == hipSuccess ? GI_OK : hip_fail(e, "gi_memcpy_h2d");
+}
+
+int gi_memcpy_d2h(gi_paged *h, void *dst, const void *src, size_t bytes)
+{
+    int rc = enter(h, "gi_memcpy_d2h");
+    if (rc)
+        return rc;
+    std::lock_guard<std::mutex> g(h->mu);
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, h->stream);
+    if (e == hipSuccess)
+        e = hipStreamSynchronize(h->stream);
+    return e == hipSuccess ? GI_OK : hip_fail(e, "gi_memcpy_d2h");
+}
+
+int gi_paged_append(gi_paged *h, int layer, int n_tok, const int32_t *block_ids,
+                    const int32_t *slots, const float *k, const float *v)
+{
+    int rc = enter(h, "gi_paged_append");
+    if (rc || (rc = check_layer(h, layer, "gi_paged_append")))
+        return rc;
+    if (n_tok < 0 || (n_tok > 0 && (!block_ids || !slots || !k || !v)))
+        return gi::set_error(GI_ERR_BAD_ARG, "gi_paged_append: bad argument");
+    std::lock_guard<std::mutex> g(h->mu);
+    hipError_t e = gi::launch_append(h->L, h->layer_base[(size_t)layer], n_tok, block_ids, slots, k, v,
+                                     h->d_status, h->stream);
+    return e == hipSuccess ? GI_OK : hip_fail(e, "gi_paged_append");
+}
+
+int gi_paged_append_at_len(gi_paged *h, int layer, int batch, const int32_t *block_tables,
+                           int max_blocks, const int32_t *seq_lens, const float *k, const float *v)
+{
+    int rc = enter(h, "gi_paged_append_at_len");
+    if (rc || (rc = check_layer(h, layer, "gi_paged_append_at_len")))
+        return rc;
+    if (batch < 0 || (batch > 0 && (!block_tables || !seq_lens || !k || !v || max_blocks <= 0)))
+        return gi::set_error(GI_ERR_BAD_ARG, "gi_paged_append_at_len: bad argument");
+    std::lock_guard<std::mutex> g(h->mu);
+    hipError_t e = gi::launch_append_at_len(h->L, h->layer_base[(size_t)layer], batch, block_tables,
+                                            max_blocks, seq_lens, k, v, h->d_status, h->stream);
+    return e == hipSuccess ? GI_OK : hip_fail(e, "gi_paged_append_at_len");
+}
+
+int gi_paged_gather(gi_paged *h, int layer, const int32_t *block_table, int n_tok, void *k_out,
+                    void *v_out, int widen)
+{
+    int rc = enter(h, "gi_paged_gather");
+    if (rc || (rc = check_layer(h, layer, "gi_paged_gather")))
+        return rc;
+    if (n_tok < 0 || (n_tok > 0 && (!block_table || !k_out || !v_out)))
+        return gi::set_error(GI_ERR_BAD_ARG, "gi_paged_gather: bad argument");
+    std::lock_guard<std::mutex> g(h->mu);
+    hipError_t e = gi::launch_gather(h->L, h->layer_base[(size_t)layer], block_table, n_tok, k_out,
+                                     v_out, widen ? 1 : 0, h->d_status, h->stream);
+    return e == hipSuccess ? GI_OK : hip_fail(e, "gi_paged_gather");
+}
+
+static int decode_locked(gi_paged *h, int layer, int batch, int num_heads, const float *q,
+                         float *out, const int32_t *block_tables, int max_blocks,
+                         const int32_t *seq_lens, int max_seq_len, float scale)
+{
+    gi::DecodeArgs a{};
+    a.L = h->L;
+    a.base = h->layer_base[(size_t)layer];
+    a.q = q;
+    a.out = out;
+    a.block_tables = block_tables;
+    a.max_blocks = max_blocks;
+    a.seq_lens = seq_lens;
+    a.batch = batch;
+    a.n_q = 1;
+    a.start_pos = nullptr;
+    a.num_heads = num_heads;
+    a.scale = scale;
+    a.status = h->d_status;
+    int max_len = max_seq_len;
+    if ((int64_t)max_len > (int64_t)max_blocks * h->L.page_tokens)
+        max_len = max_blocks * h->L.page_tokens;
+    gi::decode_plan(h->L, batch, num_heads, max_len, h->num_cus, &a.split_tokens, &a.num_splits);
+    int rc = ensure_ws(h, gi::decode_workspace_bytes(h->L, batch, num_heads, a.num_splits));
+    if (rc)
+        return rc;
+    a.ws = (float *)h->ws;
+    hipError_t e = gi::launch_decode(a, h->stream);
+    return e == hipSuccess ? GI_OK : hip_fail(e, "decode attention");
+}
+
+static int check_decode_args(gi_paged *h, int layer, int batch, int num_heads, const void *q,
+                             const void *out, const int32_t *block_tables, int max_blocks,
+                             const int32_t *seq_lens, int max_seq_len, float scale,
+                             const char *what)
+{
+    int rc = check_layer(h, layer, what);
+    if (rc)
+        return rc;
+    if (batch < 0 || max_seq_len < 0 || !std::isfinite(scale))
+        return gi::set_error(GI_ERR_BAD_ARG, std::string(what) + ": bad argument");
+    if (batch > 0 && (!q || !out || !block_tables || !seq_lens || max_blocks <= 0))
+        return gi::set_error(GI_ERR_BAD_ARG, std::string(what) + ": NULL buffer or max_blocks <= 0");
+    if (!supported_heads(h->L, num_heads))
+        return gi::set_error(GI_ERR_BAD_ARG, std::string(what) +
+                                                 ": unsupported head layout (head_dim 64/128, "
+                                                 "num_heads/num_kv_heads in {1,2,4,8})");
+    return GI_OK;
+}
+
+int gi_paged_decode_attention(gi_paged *h, int layer, int batch, int num_heads, const float *q,
+                              float *out, const int32_t *block_tables, int max_blocks,
+                              const int32_t *seq_lens, int max_seq_len, float scale)
+{
+    int rc = enter(h, "gi_paged_decode_attention");
+    if (rc || (rc = check_decode_args(h, layer, batch, num_heads, q, out, block_tables, max_blocks,
+                                      seq_lens, max_seq_len, scale, "gi_paged_decode_attention")))
+        return rc;
+    if (batch == 0)
+        return GI_OK;
+    std::lock_guard<std::mutex> g(h->mu);
+    return decode_locked(h, layer, batch, num_heads, q, out, block_tables, max_blocks, seq_lens,
+                         max_seq_len, scale);
+}
+
+int gi_paged_decode_step(gi_paged *h, int layer, int batch, int num_heads, const float *q,
+                         const float *k, const float *v, float *out, const int32_t *block_tables,
+                         int max_blocks, const int32_t *seq_lens, int max_seq_len, float scale)
+{
+    int rc = enter(h, "gi_paged_decode_step");
+    if (rc || (rc = check_decode_args(h, layer, batch, num_heads, q, out, block_tables, max_blocks,
+                                      seq_lens, max_seq_len, scale, "gi_paged_decode_step")))
+        return rc;
+    if (batch == 0)
+        return GI_OK;
+    if (!k || !v)
+        return gi::set_error(GI_ERR_BAD_ARG, "gi_paged_decode_step: NULL k or v");
+    std::lock_guard<std::mutex> g(h->mu);
+    hipError_t e = gi::launch_append_at_len(h->L, h->layer_base[(size_t)layer], batch, block_tables,
+                                            max_blocks, seq_lens, k, v, h->d_status, h->stream);
+    if (e != hipSuccess)
+        return hip_fail(e, "gi_paged_decode_step: append");
+    return decode_locked(h, layer, batch, num_heads, q, out, block_tables, max_blocks, seq_lens,
+                         max_seq_len, scale);
+}
+
+int gi_paged_prefill_attention(gi_paged *h, int layer, int batch, int chunk_len, int num_heads,
+                               const float *q, float *out, const int32_t *block_tables,
+                               int max_blocks, const int32_t *start_pos, float scale)
+{
+    int rc = enter(h, "gi_paged_prefill_attention");
+    if (rc || (rc = check_decode_args(h, layer, batch, num_heads, q, out, block_tables, max_blocks,
+                                      start_pos, 0, scale, "gi_paged_prefill_attention")))
+        return rc;
+    if (chunk_len < 0)
+        return gi::set_error(GI_ERR_BAD_ARG, "gi_paged_prefill_attention: chunk_len < 0");
+    if (batch == 0 || chunk_len == 0)
+        return GI_OK;
+    std::lock_guard<std::mutex> g(h->mu);
+    gi::PrefillArgs p{};
+    p.L = h->L;
+    p.base = h->layer_base[(size_t)layer];
+    p.q = q;
+    p.out = out;
+    p.block_tables = block_tables;
+    p.max_blocks = max_blocks;
+    p.start_pos = start_pos;
+    p.batch = batch;
+    p.chunk_len = chunk_len;
+    p.num_heads = num_heads;
+    p.scale = scale;
+    p.status = h->d_status;
+    hipError_t e = gi::launch_prefill(p, h->stream);
+    return e == hipSuccess ? GI_OK : hip_fail(e, "gi_paged_prefill_attention");
+}
+
+int gi_paged_decode_kernel(const gi_paged *h, int num_heads)
+{
+    if (!h)
+        return gi::set_error(GI_ERR_BAD_ARG, "gi_paged_decode_kernel: NULL handle");
+    return gi::decode_kernel_kind(h->L, num_heads);
+}
+
+} // extern "C"

@@ -1,0 +1,201 @@
+/*
+ * goinfer_paged.h -- C ABI of the MI355X paged KV-cache library
+ * (libgoinfer_paged.so).
+ *
+ * This is the device boundary that go-infer's Go engine binds through cgo, in
+ * the same way c_bridge_cgo.go binds inference_core.h.  It replaces:
+ *   - the block allocator pkg/engine/paged_kv.go:49-148 (PagedKVManager),
+ *     kept host-side and mirrored here as gi_kvmgr_*;
+ *   - the KV store of pkg/engine/kvcache.go:146-180 (KVCache.Write) and the
+ *     inline stores of pkg/engine/forward.go:236-240 / 527-545, and the GPU
+ *     seams metal.KVWrite / metal.KVWriteBatch (pkg/metal/metal_darwin.go:
+ *     601-614, 984-999) -> gi_paged_append / gi_paged_append_at_len;
+ *   - KVCache.Get / Clone / ForkAt (kvcache.go:183-284) -> gi_paged_gather;
+ *   - the decode attention loop of forward.go:242-267 and metal.AttentionGQA
+ *     (metal_darwin.go:711-727) -> gi_paged_decode_attention /
+ *     gi_paged_decode_step;
+ *   - the chunked-prefill attention of forward.go:547-577 and
+ *     metal.AttentionGQABatch (metal_darwin.go:963-981) ->
+ *     gi_paged_prefill_attention.
+ *
+ * Conventions (as in pkg/metal/metal_bridge.h and inference_core.h):
+ *   - every call returns int: GI_OK (0) or a negative GI_ERR_* code, and a
+ *     text reason is kept per thread for gi_last_error();
+ *   - creation returns NULL-equivalent failure through the code, never
+ *     aborts;
+ *   - buffers passed to the compute entry points are DEVICE pointers (from
+ *     gi_dev_alloc or any HIP allocation on the handle's device); work is
+ *     queued on the handle's stream and gi_synchronize() waits for it and
+ *     reports asynchronous errors (bad page ids seen by a kernel);
+ *   - calls on one handle are serialised internally; distinct handles may be
+ *     used from different threads;
+ *   - no pointer passed in is retained after the call returns (cgo rules).
+ */
+#ifndef GOINFER_PAGED_H
+#define GOINFER_PAGED_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Return codes.  metal_bridge.h uses 0 / -1 unavailable / -2 buffer failure
+ * (metal_bridge_darwin.m:3218, 3223); the same meanings are kept. */
+#define GI_OK 0
+#define GI_ERR_NO_DEVICE (-1)      /* no HIP device / not initialised      */
+#define GI_ERR_OOM (-2)            /* device or host allocation failed     */
+#define GI_ERR_BAD_ARG (-3)        /* invalid argument or unsupported shape */
+#define GI_ERR_POOL_EXHAUSTED (-4) /* paged_kv.go:118-120 "out of paged KV memory" */
+#define GI_ERR_HIP (-5)            /* HIP launch / runtime error            */
+#define GI_ERR_UNKNOWN_SEQ (-6)    /* paged_kv.go:111-114 "sequence %d not found" */
+#define GI_ERR_BAD_PAGE (-7)       /* a kernel saw a page id outside the pool */
+
+/* KV storage types.  f32 and q8_0 are kvcache.go:11-15's KVTypeF32 and
+ * KVTypeQ8_0; f16 stores FP32ToFP16 (pkg/quant/fp16.go:38-69) halves. */
+#define GI_KV_F32 0
+#define GI_KV_F16 1
+#define GI_KV_Q8_0 2
+
+/* ---- library / device ------------------------------------------------- */
+
+/* Text of the last error raised on the calling thread ("" if none). */
+const char *gi_last_error(void);
+
+/* Number of visible HIP devices (0 when none); never fails. */
+int gi_device_count(void);
+
+/* Name of the current device, like model_device_name (inference_core.c:
+ * 117-122).  Writes at most cap bytes including the terminator. */
+int gi_device_name(char *buf, int cap);
+
+/* ---- host block allocator: PagedKVManager (paged_kv.go:49-148) ---------- */
+
+typedef struct gi_kvmgr gi_kvmgr;
+
+/* NewPagedKVManager (paged_kv.go:62-87): block_size <= 0 -> 16,
+ * total_blocks <= 0 -> 256; FreeBlocks = [0..total_blocks). */
+int gi_kvmgr_create(int num_layers, int kv_dim, int total_blocks, int block_size,
+                    gi_kvmgr **out);
+void gi_kvmgr_destroy(gi_kvmgr *m);
+
+/* AllocateSequence (paged_kv.go:90-104): ids count up from 1. */
+int gi_kvmgr_allocate_sequence(gi_kvmgr *m, int *seq_id);
+
+/* AppendToken (paged_kv.go:107-132): reserves the next token slot, popping a
+ * block from the tail of the free list when the sequence needs one; returns
+ * GI_ERR_UNKNOWN_SEQ or GI_ERR_POOL_EXHAUSTED like the reference's errors. */
+int gi_kvmgr_append_token(gi_kvmgr *m, int seq_id, int32_t *block_id, int32_t *slot);
+
+/* n calls of AppendToken in one go; writes n block ids and slots.  On an
+ * error the tokens already reserved stay reserved and *done says how many. */
+int gi_kvmgr_append_tokens(gi_kvmgr *m, int seq_id, int n, int32_t *block_ids, int32_t *slots,
+                           int *done);
+
+/* FreeSequence (paged_kv.go:135-148): pushes the table's ids back onto the
+ * free list in table order; unknown ids are ignored. */
+int gi_kvmgr_free_sequence(gi_kvmgr *m, int seq_id);
+
+/* Block table of a sequence: copies up to cap ids, sets *n_blocks and
+ * *n_tokens (BlockTable.BlockIDs / NumTokens, paged_kv.go:41-46). */
+int gi_kvmgr_block_table(gi_kvmgr *m, int seq_id, int32_t *ids, int cap, int *n_blocks,
+                         int *n_tokens);
+
+/* Free list (FreeBlocks, bottom to top): copies up to cap ids, sets *n. */
+int gi_kvmgr_free_list(gi_kvmgr *m, int32_t *ids, int cap, int *n);
+
+/* Replaces the free list (bottom to top); ids must be distinct, in range and
+ * not held by a sequence.  Lets a caller start from a shuffled pool. */
+int gi_kvmgr_set_free_list(gi_kvmgr *m, const int32_t *ids, int n);
+
+/* ---- device page pool -------------------------------------------------- */
+
+typedef struct gi_paged gi_paged;
+
+/* Creates a pool of num_pages pages on the current device, each page holding
+ * page_tokens tokens of every layer (KVBlock, paged_kv.go:13-38), plus one
+ * HIP stream (default priority).  kv_type is GI_KV_*.  head_dim must be a
+ * multiple of 8 (32 for q8_0).  Pages are zero filled. */
+int gi_paged_create(int num_layers, int num_kv_heads, int head_dim, int page_tokens,
+                    int64_t num_pages, int kv_type, gi_paged **out);
+void gi_paged_destroy(gi_paged *h);
+
+/* Bytes of one page of one layer, and of the whole pool. */
+int gi_paged_page_bytes(const gi_paged *h, int64_t *page_bytes, int64_t *pool_bytes);
+
+/* Queue all further work of this handle on the given HIP stream
+ * (hipStream_t as void*; NULL is HIP's default stream, which orders with
+ * the work of other blocking streams).  A handle starts on a stream of its
+ * own; gi_paged_stream returns the current one, so a caller can save it and
+ * switch back.  Work queued before the switch completes first. */
+int gi_paged_set_stream(gi_paged *h, void *stream);
+void *gi_paged_stream(gi_paged *h);
+
+/* Waits for queued work; returns GI_ERR_BAD_PAGE if a kernel saw a page id
+ * or slot outside the pool since the last call (and clears the flag). */
+int gi_synchronize(gi_paged *h);
+
+/* Device memory helpers for callers without their own allocator. */
+int gi_dev_alloc(gi_paged *h, size_t bytes, void **dptr);
+int gi_dev_free(gi_paged *h, void *dptr);
+int gi_memcpy_h2d(gi_paged *h, void *dst, const void *src, size_t bytes);
+int gi_memcpy_d2h(gi_paged *h, void *dst, const void *src, size_t bytes);
+
+/* ---- hot path (device pointers, queued on the handle's stream) --------- */
+
+/* Appends n_tok token vectors of one layer: token i goes to page
+ * block_ids[i], slot slots[i] (the pair AppendToken returned).  k and v are
+ * [n_tok][num_kv_heads*head_dim] float32; f16 pages store the truncated
+ * halves, q8_0 pages the QuantizeQ8_0 blocks of each whole vector.
+ * Replaces KVCache.Write (kvcache.go:146-180) and metal.KVWrite[Batch]. */
+int gi_paged_append(gi_paged *h, int layer, int n_tok, const int32_t *block_ids,
+                    const int32_t *slots, const float *k, const float *v);
+
+/* Decode-step append: token b goes to position seq_lens[b]-1 of sequence b
+ * through block_tables ([batch][max_blocks] int32). */
+int gi_paged_append_at_len(gi_paged *h, int layer, int batch, const int32_t *block_tables,
+                           int max_blocks, const int32_t *seq_lens, const float *k,
+                           const float *v);
+
+/* Gathers tokens [0, n_tok) of one layer of one sequence into the contiguous
+ * [n_tok][kv_dim] layout that KVCache indexes (kvcache.go:183-284).
+ * widen == 0: stored bytes (f32 4*kv_dim, f16 2*kv_dim, q8_0 kv_dim/32
+ * blocks of 34 bytes: little-endian fp16 scale then 32 int8, quant.go:38-41);
+ * widen == 1: float32 values (FP16ToFP32 / DequantizeQ8_0). */
+int gi_paged_gather(gi_paged *h, int layer, const int32_t *block_table, int n_tok, void *k_out,
+                    void *v_out, int widen);
+
+/* Decode attention (forward.go:242-267) of one layer for a batch read
+ * directly from pages: q, out [batch][num_heads][head_dim] float32; sequence
+ * b attends its first seq_lens[b] tokens; max_seq_len bounds seq_lens and
+ * sizes the context split.  q-head h reads kv head h / (num_heads /
+ * num_kv_heads) (forward.go:249). */
+int gi_paged_decode_attention(gi_paged *h, int layer, int batch, int num_heads, const float *q,
+                              float *out, const int32_t *block_tables, int max_blocks,
+                              const int32_t *seq_lens, int max_seq_len, float scale);
+
+/* One decode step of one layer: gi_paged_append_at_len of k/v, then
+ * gi_paged_decode_attention over seq_lens[b] tokens (the new token
+ * included), as Forward stores then attends (forward.go:236-267). */
+int gi_paged_decode_step(gi_paged *h, int layer, int batch, int num_heads, const float *q,
+                         const float *k, const float *v, float *out, const int32_t *block_tables,
+                         int max_blocks, const int32_t *seq_lens, int max_seq_len, float scale);
+
+/* Chunked-prefill causal attention (forward.go:547-577) of one layer: the
+ * chunk's K/V are already appended; query i of sequence b attends tokens
+ * [0, start_pos[b] + i + 1).  q, out [batch][chunk_len][num_heads][head_dim]
+ * float32. */
+int gi_paged_prefill_attention(gi_paged *h, int layer, int batch, int chunk_len, int num_heads,
+                               const float *q, float *out, const int32_t *block_tables,
+                               int max_blocks, const int32_t *start_pos, float scale);
+
+/* Which decode kernel serves this pool and head count: 0 vector ALU,
+ * 1 matrix core (diagnostic). */
+int gi_paged_decode_kernel(const gi_paged *h, int num_heads);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GOINFER_PAGED_H */

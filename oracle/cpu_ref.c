@@ -1,0 +1,403 @@
+/*
+ * oracle/cpu_ref.c -- CPU restatement of go-infer's paged-KV / attention
+ * arithmetic.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the checker that the HIP path is
+ * compared against (tests/, __graft_entry__.smoke() and the cpu_baseline leg
+ * of bench.py).  No product code links, loads or calls it.
+ *
+ * The reference is Go (module go-inference).  Go is not available here, so
+ * every routine below restates, in C11, the Go function cited beside it.
+ * Built with -O2 -ffp-contract=off (see oracle/build.py) so that float
+ * arithmetic is evaluated exactly as written with no fused multiply-add,
+ * which is what Go's default amd64 code generation (GOAMD64=v1) does.
+ *
+ * Pinning (how each function is checked independently of this file):
+ *   ref_fp32_to_fp16 / ref_fp16_to_fp32  -- numpy float16 conversion adjusted
+ *       to round-toward-zero, all 65536 halves, boundary sweeps;
+ *       pkg/quant/quant_test.go:10-19 restated.
+ *   ref_quantize_q8_0 / ref_dequantize_q8_0 -- exact-rational closed form per
+ *       element, max-element-maps-to-127 invariant, hand-built special cases;
+ *       quant_test.go:129-143 and engine_test.go:251-273 restated.
+ *   ref_dot_vec_f32 -- an input where the 8-wide chunk order gives a
+ *       different float32 result from a sequential sum.
+ *   ref_softmax -- kernels_test.go:23-37 restated, float64 closed form.
+ *   ref_math_sqrt -- bit patterns of 1/sqrt(64) and 1/sqrt(128).
+ *   ref_attention_* -- float64 textbook softmax(QK^T * scale) V in numpy,
+ *       and prefill == per-token decode (engine_test.go:219-249 restated).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ---- fp16 <-> fp32 ------------------------------------------------------ */
+
+/* pkg/quant/fp16.go:8-35 FP16ToFP32: exact widening, subnormals normalised
+ * by shifting, Inf/NaN keep their mantissa bits. */
+float ref_fp16_to_fp32(uint16_t h)
+{
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t ex = (uint32_t)(h & 0x7C00u) >> 10;
+    uint32_t mant = (uint32_t)(h & 0x03FFu);
+    uint32_t f;
+    if (ex == 0) {
+        if (mant == 0) {
+            f = sign;
+        } else {
+            ex = 1;
+            while ((mant & 0x0400u) == 0) {
+                mant <<= 1;
+                ex--; /* unsigned wrap is intended: ex+(127-15) fixes it */
+            }
+            mant &= 0x03FFu;
+            f = sign | ((ex + (127u - 15u)) << 23) | (mant << 13);
+        }
+    } else if (ex == 0x1F) {
+        f = sign | 0x7F800000u | (mant << 13);
+    } else {
+        f = sign | ((ex + (127u - 15u)) << 23) | (mant << 13);
+    }
+    float out;
+    memcpy(&out, &f, 4);
+    return out;
+}
+
+/* pkg/quant/fp16.go:38-69 FP32ToFP16: mantissa bits are dropped (round toward
+ * zero); NaN -> sign|0x7E00, Inf and every |x| >= 65536 -> sign|0x7C00;
+ * |x| < 2^-25 -> signed zero; subnormals shift the implicit-one mantissa. */
+uint16_t ref_fp32_to_fp16(float val)
+{
+    uint32_t bits;
+    memcpy(&bits, &val, 4);
+    uint32_t sign = (bits >> 16) & 0x8000u;
+    int ex = (int)((bits >> 23) & 0xFFu);
+    uint32_t mant = bits & 0x007FFFFFu;
+    if (ex == 255) {
+        if (mant != 0)
+            return (uint16_t)(sign | 0x7E00u);
+        return (uint16_t)(sign | 0x7C00u);
+    }
+    ex = ex - 127 + 15;
+    if (ex >= 31)
+        return (uint16_t)(sign | 0x7C00u);
+    if (ex <= 0) {
+        if (ex < -10)
+            return (uint16_t)sign;
+        mant = (mant | 0x00800000u) >> (1 - ex);
+        return (uint16_t)(sign | (mant >> 13));
+    }
+    return (uint16_t)(sign | ((uint32_t)ex << 10) | (mant >> 13));
+}
+
+void ref_fp32_to_fp16_array(const float *src, uint16_t *dst, int64_t n)
+{
+    for (int64_t i = 0; i < n; i++)
+        dst[i] = ref_fp32_to_fp16(src[i]);
+}
+
+void ref_fp16_to_fp32_array(const uint16_t *src, float *dst, int64_t n)
+{
+    for (int64_t i = 0; i < n; i++)
+        dst[i] = ref_fp16_to_fp32(src[i]);
+}
+
+/* ---- Q8_0 ---------------------------------------------------------------- */
+
+/* Go's math.Round: nearest integer, halves away from zero.  C's round() has
+ * the same definition. */
+static double go_round(double x) { return round(x); }
+
+/* Go's int8(float64) conversion of a value already clamped to [-128, 127].
+ * A NaN (NaN inputs pass the clamp untouched) converts to 0 on amd64, where
+ * Go converts through CVTTSD2SQ and keeps the low byte; C leaves it
+ * undefined, so it is spelled out. */
+static int8_t go_int8(double x)
+{
+    if (x != x)
+        return 0;
+    return (int8_t)(int)x;
+}
+
+/* pkg/quant/quant.go:407-456 QuantizeQ8_0.  Blocks of 32; a short final
+ * block is zero padded.  out must hold ((n+31)/32)*34 bytes. */
+void ref_quantize_q8_0(const float *src, int64_t n, uint8_t *out)
+{
+    int64_t nblocks = (n + 31) / 32;
+    memset(out, 0, (size_t)(nblocks * 34));
+    for (int64_t b = 0; b < nblocks; b++) {
+        int64_t start = b * 32;
+        int64_t end = start + 32;
+        if (end > n)
+            end = n;
+        float maxv = 0.0f;
+        for (int64_t i = start; i < end; i++) {
+            /* float32(math.Abs(float64(x))) == fabsf(x) exactly */
+            float v = (float)fabs((double)src[i]);
+            if (v > maxv)
+                maxv = v;
+        }
+        float scale = maxv / 127.0f;
+        uint16_t d16 = 0;
+        if (scale > 0) {
+            d16 = ref_fp32_to_fp16(scale);
+            scale = ref_fp16_to_fp32(d16);
+        }
+        float inv = 0.0f;
+        if (scale > 0)
+            inv = 1.0f / scale;
+        uint8_t *blk = out + b * 34;
+        blk[0] = (uint8_t)(d16 & 0xFF); /* little endian */
+        blk[1] = (uint8_t)(d16 >> 8);
+        for (int i = 0; i < 32; i++) {
+            int8_t q = 0;
+            if (start + i < n && inv > 0) {
+                float v = src[start + i] * inv;
+                if (v > 127.0f)
+                    v = 127.0f;
+                else if (v < -128.0f)
+                    v = -128.0f;
+                q = go_int8(go_round((double)v));
+            }
+            blk[2 + i] = (uint8_t)q;
+        }
+    }
+}
+
+/* pkg/quant/quant.go:196-213 DequantizeQ8_0: out = float32(int8 q) * d. */
+void ref_dequantize_q8_0(const uint8_t *data, int64_t n, float *out)
+{
+    int64_t nblocks = n / 32;
+    for (int64_t b = 0; b < nblocks; b++) {
+        const uint8_t *blk = data + b * 34;
+        float d = ref_fp16_to_fp32((uint16_t)(blk[0] | (blk[1] << 8)));
+        for (int j = 0; j < 32; j++)
+            out[b * 32 + j] = (float)(int8_t)blk[2 + j] * d;
+    }
+}
+
+/* ---- dot / softmax / scale ---------------------------------------------- */
+
+/* pkg/quant/quant.go:548-567 DotVecF32: 8-wide chunks summed left to right,
+ * each chunk added to the running sum, then a scalar tail. */
+float ref_dot_vec_f32(const float *x, const float *w, int n)
+{
+    float sum = 0.0f;
+    int i = 0;
+    for (; i <= n - 8; i += 8) {
+        float c = x[i] * w[i];
+        c = c + x[i + 1] * w[i + 1];
+        c = c + x[i + 2] * w[i + 2];
+        c = c + x[i + 3] * w[i + 3];
+        c = c + x[i + 4] * w[i + 4];
+        c = c + x[i + 5] * w[i + 5];
+        c = c + x[i + 6] * w[i + 6];
+        c = c + x[i + 7] * w[i + 7];
+        sum += c;
+    }
+    for (; i < n; i++)
+        sum += x[i] * w[i];
+    return sum;
+}
+
+/* pkg/math/kernels.go:48-70 Softmax: two passes, exp evaluated in float64
+ * and rounded to float32, float32 running sum, multiply by 1/sum. */
+void ref_softmax(float *x, int n)
+{
+    if (n <= 0)
+        return;
+    float maxv = x[0];
+    for (int i = 1; i < n; i++)
+        if (x[i] > maxv)
+            maxv = x[i];
+    float sum = 0.0f;
+    for (int i = 0; i < n; i++) {
+        float v = (float)exp((double)(x[i] - maxv));
+        x[i] = v;
+        sum += v;
+    }
+    if (sum > 0) {
+        float inv = 1.0f / sum;
+        for (int i = 0; i < n; i++)
+            x[i] *= inv;
+    }
+}
+
+/* pkg/engine/forward.go:771-780 math_sqrt: ten Newton steps from x/2. */
+double ref_math_sqrt(double x)
+{
+    if (x <= 0)
+        return 0;
+    double z = x / 2;
+    for (int i = 0; i < 10; i++)
+        z = (z + x / z) / 2;
+    return z;
+}
+
+/* pkg/engine/forward.go:33 attnScale = float32(1.0 / math_sqrt(headDim)). */
+float ref_attn_scale(int head_dim)
+{
+    return (float)(1.0 / ref_math_sqrt((double)head_dim));
+}
+
+/* ---- attention over a contiguous per-layer cache ------------------------ */
+
+/* pkg/engine/forward.go:242-267 (decode).  kc/vc are [L][kv_dim] float32 as
+ * indexed by kv.Key[l][t*kvDim + kvHead*headDim]; q/out are [H][hd].
+ * q-head h reads kv head h / (H/KVH) (forward.go:249, config.go:59-64).
+ * scores must hold L floats. */
+void ref_attention_decode(const float *q, const float *kc, const float *vc,
+                          float *out, int H, int KVH, int hd, int L,
+                          float scale, float *scores)
+{
+    int kv_dim = KVH * hd;
+    int kv_mul = H / KVH;
+    for (int i = 0; i < H * hd; i++)
+        out[i] = 0.0f;
+    for (int h = 0; h < H; h++) {
+        const float *qh = q + (int64_t)h * hd;
+        int kvh = h / kv_mul;
+        for (int t = 0; t < L; t++)
+            scores[t] = ref_dot_vec_f32(qh, kc + (int64_t)t * kv_dim + kvh * hd, hd) * scale;
+        ref_softmax(scores, L);
+        float *oh = out + (int64_t)h * hd;
+        for (int t = 0; t < L; t++) {
+            const float *vt = vc + (int64_t)t * kv_dim + kvh * hd;
+            float wgt = scores[t];
+            for (int d = 0; d < hd; d++)
+                oh[d] += wgt * vt[d];
+        }
+    }
+}
+
+/* pkg/engine/forward.go:547-577 (chunked prefill, causal).  The chunk's own
+ * K/V are already stored (forward.go:527-545).  Token b of the chunk attends
+ * over activeContext = min(start_pos+b+1, max_seq) cached tokens.  q/out are
+ * [chunk][H][hd].  scores must hold min(start_pos+chunk, max_seq) floats. */
+void ref_attention_prefill(const float *q, const float *kc, const float *vc,
+                           float *out, int H, int KVH, int hd, int start_pos,
+                           int chunk, int max_seq, float scale, float *scores)
+{
+    for (int b = 0; b < chunk; b++) {
+        int active = start_pos + b + 1;
+        if (active > max_seq)
+            active = max_seq;
+        ref_attention_decode(q + (int64_t)b * H * hd, kc, vc,
+                             out + (int64_t)b * H * hd, H, KVH, hd, active,
+                             scale, scores);
+    }
+}
+
+/* ---- KVCache.Write / Get on one contiguous layer ------------------------- */
+
+/* Stored-format bytes per token vector for kv type t (0 f32, 1 f16, 2 q8_0).
+ * Q8_0 is ((kvDim+31)/32)*34 (pkg/engine/kvcache.go:92, 152). */
+int64_t ref_bytes_per_vec(int kv_type, int kv_dim)
+{
+    if (kv_type == 0)
+        return (int64_t)kv_dim * 4;
+    if (kv_type == 1)
+        return (int64_t)kv_dim * 2;
+    return (int64_t)((kv_dim + 31) / 32) * 34;
+}
+
+/* pkg/engine/kvcache.go:146-180 Write for one layer.  f32: copy; q8_0:
+ * QuantizeQ8_0 over the whole kvDim vector.  fp16 (no reference type; the
+ * reference's only f32->f16 routine is FP32ToFP16, fp16.go:38-69) stores the
+ * truncated halves.  Out-of-range slots are ignored (kvcache.go:147-149).
+ * cache is [max_seq][bytes_per_vec]. */
+void ref_kv_write(int kv_type, int kv_dim, int max_seq, uint8_t *kcache,
+                  uint8_t *vcache, int slot, const float *k, const float *v)
+{
+    if (slot < 0 || slot >= max_seq)
+        return;
+    int64_t bpv = ref_bytes_per_vec(kv_type, kv_dim);
+    uint8_t *kd = kcache + (int64_t)slot * bpv;
+    uint8_t *vd = vcache + (int64_t)slot * bpv;
+    if (kv_type == 0) {
+        memcpy(kd, k, (size_t)bpv);
+        memcpy(vd, v, (size_t)bpv);
+    } else if (kv_type == 1) {
+        ref_fp32_to_fp16_array(k, (uint16_t *)kd, kv_dim);
+        ref_fp32_to_fp16_array(v, (uint16_t *)vd, kv_dim);
+    } else {
+        ref_quantize_q8_0(k, kv_dim, kd);
+        ref_quantize_q8_0(v, kv_dim, vd);
+    }
+}
+
+/* pkg/engine/kvcache.go:183-214 Get, widened to float32 for n tokens:
+ * the attention loops read exactly these values. */
+void ref_kv_widen(int kv_type, int kv_dim, const uint8_t *src, int64_t n_tok,
+                  float *dst)
+{
+    int64_t bpv = ref_bytes_per_vec(kv_type, kv_dim);
+    for (int64_t t = 0; t < n_tok; t++) {
+        const uint8_t *s = src + t * bpv;
+        float *d = dst + t * kv_dim;
+        if (kv_type == 0)
+            memcpy(d, s, (size_t)bpv);
+        else if (kv_type == 1)
+            ref_fp16_to_fp32_array((const uint16_t *)s, d, kv_dim);
+        else
+            ref_dequantize_q8_0(s, kv_dim, d);
+    }
+}
+
+/* ---- paged pool in the reference layout ---------------------------------- */
+
+/* pkg/engine/paged_kv.go:13-38 KVBlock: one block holds every layer,
+ * Key[layer][token_idx*kvDim].  Here a pool of stored-format bytes laid out
+ * [block][layer][token_in_block][bytes_per_vec] for K and V separately.
+ * ref_paged_store writes token vectors at (block_id, slot) for one layer,
+ * ref_paged_gather materialises logical tokens [0, n_tok) of one layer from a
+ * block table into the contiguous [n_tok][bytes_per_vec] layout that
+ * KVCache indexes (token t -> block_table[t/bs], slot t%bs). */
+void ref_paged_store(int kv_type, int num_layers, int block_size, int kv_dim,
+                     uint8_t *kpool, uint8_t *vpool, int layer, int n_tok,
+                     const int32_t *block_ids, const int32_t *slots,
+                     const float *k, const float *v)
+{
+    int64_t bpv = ref_bytes_per_vec(kv_type, kv_dim);
+    for (int i = 0; i < n_tok; i++) {
+        int64_t off = (((int64_t)block_ids[i] * num_layers + layer) * block_size + slots[i]) * bpv;
+        ref_kv_write(kv_type, kv_dim, 1, kpool + off, vpool + off, 0,
+                     k + (int64_t)i * kv_dim, v + (int64_t)i * kv_dim);
+    }
+}
+
+void ref_paged_gather(int kv_type, int num_layers, int block_size, int kv_dim,
+                      const uint8_t *kpool, const uint8_t *vpool, int layer,
+                      const int32_t *block_table, int n_tok, uint8_t *kout,
+                      uint8_t *vout)
+{
+    int64_t bpv = ref_bytes_per_vec(kv_type, kv_dim);
+    for (int t = 0; t < n_tok; t++) {
+        int64_t off = (((int64_t)block_table[t / block_size] * num_layers + layer) * block_size + t % block_size) * bpv;
+        memcpy(kout + (int64_t)t * bpv, kpool + off, (size_t)bpv);
+        memcpy(vout + (int64_t)t * bpv, vpool + off, (size_t)bpv);
+    }
+}
+
+/* Decode attention for a batch of sequences whose caches are stored-format
+ * contiguous [L_b][bytes_per_vec] arrays concatenated in kcat/vcat (token
+ * offsets tok_off[b]).  Widens per a8/a7 then runs ref_attention_decode.
+ * Used as the CPU baseline of the decode step.  wk/wv must hold
+ * max(L)*kv_dim floats, scores max(L). */
+void ref_decode_batch(int kv_type, const float *q, const uint8_t *kcat,
+                      const uint8_t *vcat, const int64_t *tok_off,
+                      const int32_t *seq_lens, int batch, float *out, int H,
+                      int KVH, int hd, float scale, float *wk, float *wv,
+                      float *scores)
+{
+    int kv_dim = KVH * hd;
+    int64_t bpv = ref_bytes_per_vec(kv_type, kv_dim);
+    for (int b = 0; b < batch; b++) {
+        int L = seq_lens[b];
+        ref_kv_widen(kv_type, kv_dim, kcat + tok_off[b] * bpv, L, wk);
+        ref_kv_widen(kv_type, kv_dim, vcat + tok_off[b] * bpv, L, wv);
+        ref_attention_decode(q + (int64_t)b * H * hd, wk, wv,
+                             out + (int64_t)b * H * hd, H, KVH, hd, L, scale,
+                             scores);
+    }
+}

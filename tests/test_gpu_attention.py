@@ -1,0 +1,168 @@
+"""GPU parity of paged attention against the oracle.
+
+Decode follows pkg/engine/forward.go:242-267, chunked prefill
+forward.go:547-577; the oracle is fed the same stored K/V bits (f32, the
+truncated halves, or Q8_0 blocks -- checked bit-exact by test_gpu_kv.py), so
+the tolerance only covers reduction order, the online softmax and exp.
+
+Tolerance (relative, per (query, head) row): max|gpu - oracle| <= tol *
+max|oracle|, with tol = 1e-5 for f32 KV and 1e-3 for f16 / q8_0 KV."""
+import numpy as np
+import pytest
+
+from gpu_util import Populated, rel_err_rows, seeded
+
+pytestmark = pytest.mark.gpu
+
+TOL = {0: 1e-5, 1: 1e-3, 2: 1e-3}
+
+
+def oracle_decode(oracle, pop, layer, q, H, lens, scale):
+    out = np.zeros((len(lens), H * pop.hd), np.float32)
+    for i, n in enumerate(lens):
+        if n == 0:
+            continue
+        ks, vs = pop.stored(layer, i)
+        kw = oracle.widen(pop.kv_type, pop.kv_dim, ks[:n])
+        vw = oracle.widen(pop.kv_type, pop.kv_dim, vs[:n])
+        out[i] = oracle.attention_decode(q[i], kw, vw, H, pop.kvh, pop.hd, n, scale)
+    return out
+
+
+def run_decode(gi, oracle, dev, kv_type, H, kvh, hd, P, lens, layers=1, seed=1, max_seq_len=None):
+    import torch
+    pop = Populated(gi, dev, kv_type, layers, kvh, hd, P, lens, seed=seed)
+    bt = pop.block_tables()
+    sl = torch.tensor(lens, dtype=torch.int32, device=dev)
+    scale = oracle.attn_scale(hd)
+    worst = 0.0
+    for l in range(layers):
+        qd, q = seeded((len(lens), H * hd), seed * 31 + l, dev)
+        out = torch.full_like(qd, float("nan"))
+        pop.pool.AttentionGQA(out, qd, l, bt, sl, H, scale, max_seq_len)
+        pop.pool.synchronize()
+        want = oracle_decode(oracle, pop, l, q, H, lens, scale)
+        err = rel_err_rows(out.cpu().numpy(), want, H, hd)
+        worst = max(worst, float(err.max()))
+    assert worst <= TOL[kv_type], worst
+    return pop, worst
+
+
+@pytest.mark.parametrize("kv_type", [0, 1, 2], ids=["f32", "f16", "q8_0"])
+def test_decode_small_shapes(gi, oracle, dev, kv_type):
+    # ragged lengths including 1, page edges and a multi-split sequence
+    for (H, kvh, hd, P) in [(32, 4, 64, 16), (32, 8, 128, 16), (64, 8, 128, 32), (8, 8, 128, 16),
+                            (16, 8, 64, 16)]:
+        run_decode(gi, oracle, dev, kv_type, H, kvh, hd, P, [1, P, P + 1, 37, 300, 1500],
+                   layers=2, seed=3 + kv_type)
+
+
+def test_decode_tinyllama_prompt_then_128_steps(gi, oracle, dev):
+    """TinyLlama KV path (22 layers, 32 q / 4 kv heads, hd 64, f32 KV, page
+    16, batch 1): 128-token prompt appended, then 128 decode steps, each
+    appending its token then attending over the whole context, every layer
+    checked against the oracle."""
+    import torch
+    H, kvh, hd, P, layers = 32, 4, 64, 16, 22
+    kv_dim = kvh * hd
+    total = 256
+    pages = total // P
+    mgr = gi.PagedKVManager(layers, kv_dim, pages, P)   # pages allocated in order (LIFO)
+    pool = gi.PagedKVCache(layers, kvh, hd, P, pages, 0)
+    sid = mgr.AllocateSequence()
+    ids, slots = mgr.AppendTokens(sid, 128)
+    K = {l: oracle.normal(1000 + l, (total, kv_dim)) for l in range(layers)}
+    V = {l: oracle.normal(2000 + l, (total, kv_dim)) for l in range(layers)}
+    for l in range(layers):
+        pool.Write(l, torch.from_numpy(ids).to(dev), torch.from_numpy(slots).to(dev),
+                   torch.from_numpy(K[l][:128].copy()).to(dev),
+                   torch.from_numpy(V[l][:128].copy()).to(dev))
+    scale = oracle.attn_scale(hd)
+    worst = 0.0
+    for step in range(128):
+        n = 129 + step
+        mgr.AppendToken(sid)
+        bt = torch.tensor([mgr.Tables[sid].BlockIDs], dtype=torch.int32, device=dev)
+        sl = torch.tensor([n], dtype=torch.int32, device=dev)
+        for l in range(layers):
+            q = oracle.normal(3000 + 100 * step + l, (1, H * hd))
+            out = torch.empty((1, H * hd), dtype=torch.float32, device=dev)
+            pool.DecodeStep(out, torch.from_numpy(q).to(dev),
+                            torch.from_numpy(K[l][n - 1:n].copy()).to(dev),
+                            torch.from_numpy(V[l][n - 1:n].copy()).to(dev), l, bt, sl, H, scale)
+            want = oracle.attention_decode(q[0], K[l][:n], V[l][:n], H, kvh, hd, n, scale)
+            err = rel_err_rows(out.cpu().numpy(), want, H, hd)
+            worst = max(worst, float(err.max()))
+    pool.synchronize()
+    assert worst <= 1e-5, worst
+
+
+def test_decode_llama8b_batch32_random_pool(gi, oracle, dev):
+    """Llama-3-8B KV shape (32 q / 8 kv heads, hd 128, fp16, page 16), batch
+    32, per-sequence context U[512, 4096], block tables a random permutation
+    of a shared pool; two layers."""
+    rng = np.random.default_rng(2024)
+    lens = [int(x) for x in rng.integers(512, 4097, size=32)]
+    run_decode(gi, oracle, dev, 1, 32, 8, 128, 16, lens, layers=2, seed=8)
+
+
+def test_decode_llama70b_long_context_split(gi, oracle, dev):
+    """Llama-3-70B KV shape (64 q / 8 kv heads, hd 128, fp16, page 32), two
+    sequences at 32768 context: the split-K partitions and their merge."""
+    run_decode(gi, oracle, dev, 1, 64, 8, 128, 32, [32768, 20001], layers=1, seed=9)
+
+
+def test_decode_empty_and_short(gi, oracle, dev):
+    import torch
+    pop = Populated(gi, dev, 1, 1, 8, 128, 16, [0, 1, 2], seed=4)
+    bt = pop.block_tables()
+    sl = torch.tensor([0, 1, 2], dtype=torch.int32, device=dev)
+    qd, q = seeded((3, 32 * 128), 5, dev)
+    out = torch.full_like(qd, float("nan"))
+    scale = oracle.attn_scale(128)
+    pop.pool.AttentionGQA(out, qd, 0, bt, sl, 32, scale)
+    pop.pool.synchronize()
+    o = out.cpu().numpy()
+    assert not o[0].any()                                   # empty context -> zeros
+    ks, vs = pop.stored(0, 1)
+    v1 = oracle.widen(1, 1024, vs)[0]
+    # one token: softmax weight 1, output = V of that token for every head
+    for h in range(32):
+        assert np.array_equal(o[1, h * 128:(h + 1) * 128], v1[(h // 4) * 128:(h // 4 + 1) * 128])
+    want = oracle_decode(oracle, pop, 0, q, 32, [0, 1, 2], scale)
+    assert rel_err_rows(o[2], want[2], 32, 128).max() <= 1e-3
+
+
+def prefill_case(gi, oracle, dev, kv_type, H, kvh, hd, P, starts, chunk, seed):
+    import torch
+    lens = [s + chunk for s in starts]
+    pop = Populated(gi, dev, kv_type, 1, kvh, hd, P, lens, seed=seed, append_chunk=chunk,
+                    outliers=True)
+    bt = pop.block_tables()
+    sp = torch.tensor(starts, dtype=torch.int32, device=dev)
+    qd, q = seeded((len(starts), chunk, H * hd), seed + 50, dev, outliers=True)
+    out = torch.full_like(qd, float("nan"))
+    scale = oracle.attn_scale(hd)
+    pop.pool.AttentionGQABatch(out, qd, 0, bt, sp, H, scale, chunk)
+    pop.pool.synchronize()
+    o = out.cpu().numpy()
+    worst = 0.0
+    for i, s in enumerate(starts):
+        ks, vs = pop.stored(0, i)
+        kw = oracle.widen(kv_type, pop.kv_dim, ks)
+        vw = oracle.widen(kv_type, pop.kv_dim, vs)
+        want = oracle.attention_prefill(q[i], kw, vw, H, kvh, hd, s, chunk, 1 << 30, scale)
+        worst = max(worst, float(rel_err_rows(o[i], want, H, hd).max()))
+    assert worst <= TOL[kv_type], worst
+
+
+@pytest.mark.parametrize("kv_type", [0, 1, 2], ids=["f32", "f16", "q8_0"])
+def test_prefill_chunk(gi, oracle, dev, kv_type):
+    prefill_case(gi, oracle, dev, kv_type, 32, 8, 128, 16, [0, 100, 509], 64, seed=60 + kv_type)
+
+
+def test_prefill_q8_llama8b_chunks(gi, oracle, dev):
+    """Llama-3-8B shape, Q8_0 KV, 512-token chunks appended with on-the-fly
+    quantisation, N(0,1) inputs with 1 % outliers at +-8 sigma: the last
+    chunk of a 1536-token prefill, batch 2."""
+    prefill_case(gi, oracle, dev, 2, 32, 8, 128, 16, [1024, 512], 512, seed=70)
