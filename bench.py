@@ -168,6 +168,8 @@ def main():
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
+    ap.add_argument("--decode-kernel", type=int, default=-1, choices=[-1, 0, 1],
+                    help="-1 automatic, 0 vector ALU, 1 matrix core")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="also run one device copy of this many MiB (counter calibration)")
     args = ap.parse_args()
@@ -197,6 +199,7 @@ def main():
     stream = torch.cuda.Stream(dev)
     torch.cuda.set_stream(stream)
     pool = gi.PagedKVCache(layers, kvh, hd, P, pages, gi.KV_F16, stream=stream)
+    pool.set_decode_kernel(args.decode_kernel)
     log("pool: %.1f GiB" % (pool.page_bytes()[1] / 2**30))
     fill_pool(torch, pool, cfg, lens, bt, dev, args.seed)
     log("pool filled (%.1f s)" % (time.perf_counter() - t_setup))

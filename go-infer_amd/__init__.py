@@ -72,6 +72,7 @@ EXPORTS = {
     "gi_paged_prefill_attention": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp,
                                             _c_int, _vp, ctypes.c_float]),
     "gi_paged_decode_kernel": (_c_int, [_vp, _c_int]),
+    "gi_paged_set_decode_kernel": (_c_int, [_vp, _c_int]),
 }
 
 _lib = None
@@ -286,7 +287,12 @@ class PagedKVCache:
         _check(lib().gi_synchronize(self._h))
 
     def decode_kernel(self, num_heads):
+        """0: vector-ALU kernel, 1: matrix-core kernel."""
         return lib().gi_paged_decode_kernel(self._h, num_heads)
+
+    def set_decode_kernel(self, kind):
+        """-1 automatic, 0 vector ALU, 1 matrix core where supported."""
+        _check(lib().gi_paged_set_decode_kernel(self._h, kind))
 
     # -- KVCache.Write / Get on pages ------------------------------------
     def Write(self, layer, block_ids, slots, k, v):

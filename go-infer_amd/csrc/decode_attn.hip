@@ -334,11 +334,12 @@ void decode_plan(const PoolLayout &L, int batch, int num_heads, int max_len, int
     *num_splits = splits;
 }
 
-int decode_kernel_kind(const PoolLayout &L, int num_heads)
+int decode_kernel_kind(const PoolLayout &L, int num_heads, int requested)
 {
-    (void)L;
-    (void)num_heads;
-    return 0;
+    const bool mfma = mfma_decode_supported(L, num_heads);
+    if (requested == 0 || !mfma)
+        return 0;
+    return 1;
 }
 
 hipError_t launch_decode(const DecodeArgs &a, hipStream_t st)
@@ -347,12 +348,16 @@ hipError_t launch_decode(const DecodeArgs &a, hipStream_t st)
     if (a.num_heads % L.num_kv_heads)
         return hipErrorInvalidValue;
     const int n_q = a.n_q > 0 ? a.n_q : 1;
-    dim3 grid(a.num_splits, L.num_kv_heads, a.batch * n_q);
     hipError_t e;
-    switch (L.kv_type) {
-    case KV_F32: e = launch_valu_kt<KV_F32>(a, grid, st); break;
-    case KV_F16: e = launch_valu_kt<KV_F16>(a, grid, st); break;
-    default: e = launch_valu_kt<KV_Q8_0>(a, grid, st); break;
+    if (n_q == 1 && !a.start_pos && decode_kernel_kind(L, a.num_heads, a.kernel) == 1) {
+        e = launch_decode_mfma(a, st);
+    } else {
+        dim3 grid(a.num_splits, L.num_kv_heads, a.batch * n_q);
+        switch (L.kv_type) {
+        case KV_F32: e = launch_valu_kt<KV_F32>(a, grid, st); break;
+        case KV_F16: e = launch_valu_kt<KV_F16>(a, grid, st); break;
+        default: e = launch_valu_kt<KV_Q8_0>(a, grid, st); break;
+        }
     }
     if (e != hipSuccess || a.num_splits <= 1)
         return e;
@@ -380,6 +385,7 @@ hipError_t launch_prefill(const PrefillArgs &p, hipStream_t st)
     a.num_splits = 1;
     a.ws = nullptr;
     a.status = p.status;
+    a.kernel = 0;
     if (p.chunk_len <= 0 || p.batch <= 0)
         return hipSuccess;
     return launch_decode(a, st);

@@ -40,6 +40,7 @@ struct DecodeArgs {
     int num_splits;
     float *ws; // partials when num_splits > 1
     int *status;
+    int kernel; // -1 automatic, 0 vector ALU, 1 matrix core
 };
 
 // Bytes of split-K workspace needed for a decode launch.
@@ -53,9 +54,12 @@ void decode_plan(const PoolLayout &L, int batch, int num_heads, int max_len, int
 // Returns hipErrorInvalidValue for shapes without a kernel instance.
 hipError_t launch_decode(const DecodeArgs &a, hipStream_t st);
 
-// Which kernel launch_decode uses for a layout/head count: 0 vector-ALU,
-// 1 matrix-core.  Exposed for tests and the bench.
-int decode_kernel_kind(const PoolLayout &L, int num_heads);
+// Which kernel launch_decode uses for a layout/head count and a requested
+// kind (-1 automatic): 0 vector ALU, 1 matrix core.
+int decode_kernel_kind(const PoolLayout &L, int num_heads, int requested);
+
+bool mfma_decode_supported(const PoolLayout &L, int num_heads);
+hipError_t launch_decode_mfma(const DecodeArgs &a, hipStream_t st);
 
 // Chunked-prefill causal attention over paged context: query i of sequence b
 // (i < chunk_len) attends tokens [0, start_pos[b] + i + 1).

@@ -41,6 +41,7 @@ struct gi_paged {
     int *d_status = nullptr;
     void *ws = nullptr;
     size_t ws_bytes = 0;
+    int decode_kernel = -1; // -1 automatic, 0 vector ALU, 1 matrix core
 };
 
 namespace {
@@ -382,6 +383,7 @@ static int decode_locked(gi_paged *h, int layer, int batch, int num_heads, const
     a.num_heads = num_heads;
     a.scale = scale;
     a.status = h->d_status;
+    a.kernel = h->decode_kernel;
     int max_len = max_seq_len;
     if ((int64_t)max_len > (int64_t)max_blocks * h->L.page_tokens)
         max_len = max_blocks * h->L.page_tokens;
@@ -483,7 +485,16 @@ int gi_paged_decode_kernel(const gi_paged *h, int num_heads)
 {
     if (!h)
         return gi::set_error(GI_ERR_BAD_ARG, "gi_paged_decode_kernel: NULL handle");
-    return gi::decode_kernel_kind(h->L, num_heads);
+    return gi::decode_kernel_kind(h->L, num_heads, h->decode_kernel);
+}
+
+int gi_paged_set_decode_kernel(gi_paged *h, int kind)
+{
+    if (!h || kind < -1 || kind > 1)
+        return gi::set_error(GI_ERR_BAD_ARG, "gi_paged_set_decode_kernel: bad argument");
+    std::lock_guard<std::mutex> g(h->mu);
+    h->decode_kernel = kind;
+    return GI_OK;
 }
 
 } // extern "C"

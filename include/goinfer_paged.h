@@ -162,7 +162,8 @@ int gi_paged_append_at_len(gi_paged *h, int layer, int batch, const int32_t *blo
  * [n_tok][kv_dim] layout that KVCache indexes (kvcache.go:183-284).
  * widen == 0: stored bytes (f32 4*kv_dim, f16 2*kv_dim, q8_0 kv_dim/32
  * blocks of 34 bytes: little-endian fp16 scale then 32 int8, quant.go:38-41);
- * widen == 1: float32 values (FP16ToFP32 / DequantizeQ8_0). */
+ * widen == 1: float32 values (FP16ToFP32 / DequantizeQ8_0).  block_table
+ * must hold ceil(n_tok / page_tokens) ids. */
 int gi_paged_gather(gi_paged *h, int layer, const int32_t *block_table, int n_tok, void *k_out,
                     void *v_out, int widen);
 
@@ -191,8 +192,13 @@ int gi_paged_prefill_attention(gi_paged *h, int layer, int batch, int chunk_len,
                                int max_blocks, const int32_t *start_pos, float scale);
 
 /* Which decode kernel serves this pool and head count: 0 vector ALU,
- * 1 matrix core (diagnostic). */
+ * 1 matrix core (fp16 pages, head_dim 64/128, page_tokens % 16 == 0). */
 int gi_paged_decode_kernel(const gi_paged *h, int num_heads);
+
+/* Selects the decode kernel: -1 automatic (default), 0 vector ALU, 1 matrix
+ * core where supported.  For comparisons; results agree within the
+ * attention tolerance. */
+int gi_paged_set_decode_kernel(gi_paged *h, int kind);
 
 #ifdef __cplusplus
 }
