@@ -127,6 +127,21 @@ def step_bytes(cfg, lens):
     return int(attn) * cfg["layers"], int(append) * cfg["layers"]
 
 
+def profiled_traffic(kernel, workload):
+    """HBM bytes per launch of a kernel on a workload, from the rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary committed under profiles/ (a line
+    'TRAFFIC kernel=... workload=... bytes_per_launch=N'), or None."""
+    import glob
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*.md"))):
+        for line in open(path):
+            if not line.startswith("TRAFFIC "):
+                continue
+            kv = dict(x.split("=", 1) for x in line.split()[1:])
+            if kv.get("kernel") == kernel and kv.get("workload") == workload:
+                return int(kv["bytes_per_launch"]), os.path.relpath(path, ROOT)
+    return None
+
+
 def cpu_baseline(oracle, cfg, budget_s=12.0):
     """The oracle's decode (widen fp16 -> f32, then the reference loop of
     forward.go:242-267) on one host core for a bounded sample of the same
@@ -284,6 +299,9 @@ def main():
         import oracle
         cpu = cpu_baseline(oracle, cfg)
 
+    kind = pool.decode_kernel(H)
+    kname = ("attn_mfma_f16<%d>" % hd) if kind == 1 else ("attn_valu<1,%d,%d>" % (hd, H // kvh))
+    traffic = profiled_traffic(kname, args.config)
     res = {
         "metric": METRIC,
         "value": round(tot_gbs, 2),
@@ -303,10 +321,12 @@ def main():
                    "fragmented_pool": cfg["frag"]},
         "hbm_frac_of_peak": round(tot_gbs / HBM_PEAK_GBS, 4),
         "tokens_per_s": round(tok_s, 1),
-        "decode_kernel": ["vector-alu", "matrix-core"][pool.decode_kernel(H)],
+        "decode_kernel": ["vector-alu", "matrix-core"][kind],
         "roofline": {"bound": "hbm", "achieved": round(attn_gbs, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(attn_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": None, "kernel": "paged decode attention",
+                     "traffic": traffic[0] if traffic else None,
+                     "traffic_source": traffic[1] if traffic else None,
+                     "kernel": kname,
                      "launch_ms": round(attn_ms, 4),
                      "bytes_per_launch": attn_bytes // layers},
         "cpu_baseline": cpu,

@@ -8,15 +8,20 @@
 //   O[head][d]      += P[head][token] * V[token][d]    (B = V from the
 //                                                       dimension-major page)
 //
-// A wave walks 32-token blocks (two 16-token MFMA row tiles).  The query is
-// split into hi + lo halves (q = hi + lo exactly up to 2^-22 |q|) and the
-// probabilities likewise, so both products keep float32 accuracy while K/V
-// feed the MFMA in their stored fp16 form: no conversion instructions on the
-// bandwidth path.  The k-slot -> token assignment of the P*V product is
-// chosen to equal the token layout the S tile comes out in, so P never moves
-// between lanes.  Each of the 4 waves keeps its own running max/sum and the
-// workgroup merges them at the end (and split-K partials are merged by
-// merge_splits in decode_attn.hip).
+// A wave walks 32-token blocks as two 16-row MFMA tiles.  The query is split
+// into hi + lo halves (q = hi + lo up to 2^-22 |q|) and the probabilities
+// likewise, so both products keep float32 accuracy while K/V feed the MFMA in
+// their stored fp16 form: no conversion instructions on the bandwidth path.
+//
+// Token order inside a block: tile 0 row i holds token 8*(i/4) + i%4, tile 1
+// row i token 8*(i/4) + 4 + i%4.  The S tile then leaves lane (col j, group
+// g = lane/16) with the scores of tokens 8g .. 8g+7 -- exactly the eight
+// k-slots that lane feeds to the P*V product -- so P never moves between
+// lanes, and the lane's V operand (dimension 16*nb + j, tokens 8g .. 8g+7) is
+// one contiguous 16-byte run of the dimension-major page.
+//
+// Each of the 4 waves keeps its own running max / sum; the workgroup merges
+// them at the end, and split-K partials are merged by merge_splits.
 #include "gi_common.h"
 #include "gi_kernels.h"
 
@@ -25,10 +30,9 @@
 namespace gi {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
-namespace {
+namespace mfma_decode {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -37,15 +41,208 @@ __device__ __forceinline__ f4 mfma(h8 a, h8 b, f4 c)
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-template <int HD>
-__global__ __launch_bounds__(256) void attn_mfma_f16(DecodeArgs a)
+template <bool NT>
+__device__ __forceinline__ h8 ld16(const uint8_t *p)
 {
-    constexpr int KK = HD / 32; // k-steps of the score product
-    constexpr int NB = HD / 16; // 16-column blocks of the output
+    if (NT)
+        return __builtin_nontemporal_load(reinterpret_cast<const h8 *>(p));
+    return *reinterpret_cast<const h8 *>(p);
+}
+
+// Pages holding tokens base and base+16 of a 32-token block (equal when one
+// page holds both or the second half is past the end).  Ids outside the pool
+// are reported and replaced by page 0; their tokens are masked.
+// (Plain scalars rather than a struct: a struct carried across the loop is
+// not promoted to registers by the compiler.)
+__device__ __forceinline__ void block_pages(const DecodeArgs &a, const int32_t *bt, int base, int t1,
+                                            int j, int g, int64_t &pA, int64_t &pB, bool &ok)
+{
+    const PoolLayout &L = a.L;
+    const int P = L.page_tokens;
+    pA = bt[base / P];
+    pB = base + 16 < t1 ? (int64_t)bt[(base + 16) / P] : pA;
+    const bool okA = pA >= 0 && pA < L.num_pages;
+    const bool okB = pB >= 0 && pB < L.num_pages;
+    ok = okA && okB;
+    if (!ok) {
+        if (j == 0 && g == 0 && a.status)
+            atomicOr(a.status, FLAG_BAD_PAGE);
+        if (!okA)
+            pA = 0;
+        if (!okB)
+            pB = 0;
+    }
+}
+
+// K rows: tile 0 row j is token 8*(j/4) + j%4 of the block, tile 1 adds 4.
+template <int HD, bool NT>
+__device__ __forceinline__ void load_k(const DecodeArgs &a, int64_t pA, int64_t pB, int base,
+                                       int64_t koff, int j, int g, h8 *k0, h8 *k1)
+{
+    const PoolLayout &L = a.L;
+    const int P = L.page_tokens;
+    const int tk0 = 8 * (j >> 2) + (j & 3), tk1 = tk0 + 4;
+    const int64_t pk0 = tk0 < 16 ? pA : pB, pk1 = tk1 < 16 ? pA : pB;
+    const uint8_t *r0 = a.base + pk0 * L.page_bytes + koff + (int64_t)((base + tk0) % P) * HD * 2;
+    const uint8_t *r1 = a.base + pk1 * L.page_bytes + koff + (int64_t)((base + tk1) % P) * HD * 2;
+#pragma unroll
+    for (int kk = 0; kk < HD / 32; kk++) {
+        k0[kk] = ld16<NT>(r0 + (32 * kk + 8 * g) * 2);
+        k1[kk] = ld16<NT>(r1 + (32 * kk + 8 * g) * 2);
+    }
+}
+
+// V: tokens 8g .. 8g+7 of the block, dimension 16*nb + j.
+template <int HD, bool NT>
+__device__ __forceinline__ void load_v(const DecodeArgs &a, int64_t pA, int64_t pB, int base,
+                                       int64_t voff, int j, int g, h8 *v)
+{
+    const PoolLayout &L = a.L;
+    const int P = L.page_tokens;
+    const int64_t pv = g < 2 ? pA : pB;
+    const uint8_t *vr = a.base + pv * L.page_bytes + voff + (int64_t)((base + 8 * g) % P) * 2;
+#pragma unroll
+    for (int nb = 0; nb < HD / 16; nb++)
+        v[nb] = ld16<NT>(vr + (int64_t)(16 * nb + j) * P * 2);
+}
+
+// Running state of one wave for head column j.
+template <int HD>
+struct State {
+    float m2;   // running max, log2 units
+    float lsum; // this lane's share of the running denominator
+    f4 o[HD / 16];
+};
+
+// Scores of one block: lane holds column j, block-local tokens 8g + r (s0[r])
+// and 8g + 4 + r (s1[r]).  Unpacked (GP == 0): column j is head j and the
+// hi and lo query halves are accumulated by two products.  Packed (GP = G):
+// column j < G holds q_hi of head j and column 2G-1-j holds q_lo of head j,
+// so one product covers both and a lane-mirror add (partner j ^ (2G-1))
+// completes every score in both columns.
+template <int GP>
+__device__ __forceinline__ float mirror(float x)
+{
+    // DPP within 16-lane rows: quad_perm [1,0,3,2] (^1), quad_perm [3,2,1,0]
+    // (^3), row_half_mirror (^7 within 8 lanes), row_mirror (^15).
+    constexpr int ctrl = GP == 1 ? 0xB1 : GP == 2 ? 0x1B : GP == 4 ? 0x141 : 0x140;
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), ctrl,
+                                                               0xF, 0xF, false));
+}
+
+template <int HD, int GP>
+__device__ __forceinline__ void qk(const h8 *k0, const h8 *k1, const h8 *qh, const h8 *ql, f4 &s0,
+                                   f4 &s1)
+{
+    s0 = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    s1 = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int kk = 0; kk < HD / 32; kk++) {
+        s0 = mfma(k0[kk], qh[kk], s0);
+        s1 = mfma(k1[kk], qh[kk], s1);
+        if (GP == 0) {
+            s0 = mfma(k0[kk], ql[kk], s0);
+            s1 = mfma(k1[kk], ql[kk], s1);
+        }
+    }
+    if (GP != 0) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            s0[r] += mirror<GP>(s0[r]);
+            s1[r] += mirror<GP>(s1[r]);
+        }
+    }
+}
+
+// Online-softmax update and P*V for one block whose scores are s0/s1.
+// Unpacked: P rows are heads, hi and lo halves in two products.  Packed: row
+// j < G carries p_hi of head j and row 2G-1-j p_lo of head j (the lane of
+// that column already holds the head's full score), one product; the two
+// output rows of a head are added in the final merge.
+template <int HD, int GP>
+__device__ __forceinline__ void softmax_pv(f4 s0, f4 s1, h8 *v, int base, bool ok, int t1, int j,
+                                           int g, float c, State<HD> &S)
+{
+    constexpr int NB = HD / 16;
+    float sc[8];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        sc[r] = s0[r] * c;
+        sc[4 + r] = s1[r] * c;
+    }
+    if (base + 32 > t1 || !ok) {
+        // Tokens past the end (or on a rejected page) get weight 0, and
+        // their V values -- whatever the slot holds -- are zeroed so they
+        // cannot turn 0 * V into NaN.
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            if (!(base + 8 * g + i < t1 && ok)) {
+                sc[i] = -INFINITY;
+#pragma unroll
+                for (int nb = 0; nb < NB; nb++)
+                    v[nb][i] = (_Float16)0.0f;
+            }
+        }
+    }
+    float mx = sc[0];
+#pragma unroll
+    for (int i = 1; i < 8; i++)
+        mx = fmaxf(mx, sc[i]);
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float mnew = fmaxf(S.m2, mx);
+    const float alpha = exp2f(S.m2 - mnew);
+    S.m2 = mnew;
+    float ps = 0.0f;
+    h8 ph, pl;
+    const bool lo_row = GP != 0 && j >= GP;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float p = exp2f(sc[i] - mnew);
+        ps += p;
+        const _Float16 hi = (_Float16)p;
+        const _Float16 lo = (_Float16)(p - (float)hi);
+        if (GP == 0) {
+            ph[i] = hi;
+            pl[i] = lo;
+        } else {
+            ph[i] = lo_row ? lo : hi;
+        }
+    }
+    S.lsum = S.lsum * alpha + ps;
+    // Output rows of this lane are 4g + r; their factor is the alpha of the
+    // head of column 4g + r.  Skipped when no running max moved (a multiply
+    // by exactly 1).
+    if (__any(alpha != 1.0f)) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float ar = __shfl(alpha, 4 * g + r);
+#pragma unroll
+            for (int nb = 0; nb < NB; nb++)
+                S.o[nb][r] *= ar;
+        }
+    }
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++) {
+        S.o[nb] = mfma(ph, v[nb], S.o[nb]);
+        if (GP == 0)
+            S.o[nb] = mfma(pl, v[nb], S.o[nb]);
+    }
+}
+
+// GP: 0 for any group size up to 16 (hi/lo halves in separate products),
+// or the group size G in {1, 2, 4, 8} for the packed form.  NT:
+// non-temporal (streaming) loads of K/V.  PREFETCH: the next block's loads
+// are issued as soon as this block's K (then V) registers are consumed.
+// OCC: minimum waves per SIMD requested from the register allocator.
+template <int HD, int GP, bool NT, bool PREFETCH, int OCC>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void attn_mfma_f16(DecodeArgs a)
+{
+    constexpr int KK = HD / 32, NB = HD / 16;
     const PoolLayout &L = a.L;
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int j = lane & 15, q4 = lane >> 4;
+    const int j = lane & 15, g = lane >> 4;
     const int H = a.num_heads, KVH = L.num_kv_heads, G = H / KVH, P = L.page_tokens;
     const int h0 = kvh * G;
     int len = a.seq_lens[b];
@@ -80,152 +277,87 @@ __global__ __launch_bounds__(256) void attn_mfma_f16(DecodeArgs a)
     }
 
     // Q^T operand: column j = head h0 + j (zero beyond the group), k-slot
-    // (q4, v) of step kk = dimension 32*kk + 8*q4 + v.
+    // (g, v) of step kk = dimension 32*kk + 8*g + v.
+    // Packed: column j < G is q_hi of head j, column 2G-1-j is q_lo of head j.
+    const int qhead = GP == 0 ? j : (j < G ? j : 2 * G - 1 - j);
+    const bool qvalid = GP == 0 ? j < G : j < 2 * G;
+    const bool qlo = GP != 0 && j >= G;
     h8 qh[KK], ql[KK];
 #pragma unroll
     for (int kk = 0; kk < KK; kk++)
 #pragma unroll
         for (int v = 0; v < 8; v++) {
-            float x = j < G ? a.q[(qrow + j) * HD + 32 * kk + 8 * q4 + v] : 0.0f;
+            float x = qvalid ? a.q[(qrow + qhead) * HD + 32 * kk + 8 * g + v] : 0.0f;
             _Float16 hi = (_Float16)x;
-            qh[kk][v] = hi;
-            ql[kk][v] = (_Float16)(x - (float)hi);
+            _Float16 lo = (_Float16)(x - (float)hi);
+            qh[kk][v] = qlo ? lo : hi;
+            ql[kk][v] = lo;
         }
 
     const float c = a.scale * kLog2e;
-    float m2 = -INFINITY; // running max of head j, log2 units
-    float lsum = 0.0f;    // this lane's share of the running denominator
-    f4 o[NB];
+    State<HD> S;
+    S.m2 = -INFINITY;
+    S.lsum = 0.0f;
 #pragma unroll
     for (int nb = 0; nb < NB; nb++)
-        o[nb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        S.o[nb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 
     const int64_t koff = L.k_off + (int64_t)kvh * P * HD * 2;
     const int64_t voff = L.v_off + (int64_t)kvh * HD * P * 2;
     const int32_t *bt = a.block_tables + (int64_t)b * a.max_blocks;
+    const int stride = 32 * 4;
 
-    for (int base = t0 + 32 * w; base < t1; base += 128) {
-        const int tA = base, tB = base + 16;
-        int64_t pA = bt[tA / P];
-        int64_t pB = tB < t1 ? (int64_t)bt[tB / P] : pA;
-        bool okA = pA >= 0 && pA < L.num_pages;
-        bool okB = pB >= 0 && pB < L.num_pages;
-        if (!(okA && okB)) {
-            if (lane == 0 && a.status)
-                atomicOr(a.status, FLAG_BAD_PAGE);
-            if (!okA)
-                pA = 0;
-            if (!okB)
-                pB = 0;
-        }
-        const int sA = tA % P, sB = tB % P;
-        const uint8_t *gA = a.base + pA * L.page_bytes;
-        const uint8_t *gB = a.base + pB * L.page_bytes;
-
-        h8 k0[KK], k1[KK];
-#pragma unroll
-        for (int kk = 0; kk < KK; kk++) {
-            k0[kk] = *reinterpret_cast<const h8 *>(gA + koff + ((int64_t)(sA + j) * HD + 32 * kk + 8 * q4) * 2);
-            k1[kk] = *reinterpret_cast<const h8 *>(gB + koff + ((int64_t)(sB + j) * HD + 32 * kk + 8 * q4) * 2);
-        }
-        h4 v0[NB], v1[NB];
-#pragma unroll
-        for (int nb = 0; nb < NB; nb++) {
-            v0[nb] = *reinterpret_cast<const h4 *>(gA + voff + ((int64_t)(16 * nb + j) * P + sA + 4 * q4) * 2);
-            v1[nb] = *reinterpret_cast<const h4 *>(gB + voff + ((int64_t)(16 * nb + j) * P + sB + 4 * q4) * 2);
-        }
-
-        f4 s0 = {0.0f, 0.0f, 0.0f, 0.0f}, s1 = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int kk = 0; kk < KK; kk++) {
-            s0 = mfma(k0[kk], qh[kk], s0);
-            s0 = mfma(k0[kk], ql[kk], s0);
-            s1 = mfma(k1[kk], qh[kk], s1);
-            s1 = mfma(k1[kk], ql[kk], s1);
-        }
-
-        // lane holds head j, tokens base + 4*q4 + r (sc[r]) and
-        // base + 16 + 4*q4 + r (sc[4 + r])
-        float sc[8];
-        const bool tail = base + 32 > t1 || !(okA && okB);
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            sc[r] = s0[r] * c;
-            sc[4 + r] = s1[r] * c;
-        }
-        if (tail) {
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int ta = base + 4 * q4 + r, tb = base + 16 + 4 * q4 + r;
-                if (!(ta < t1 && okA)) {
-                    sc[r] = -INFINITY;
-#pragma unroll
-                    for (int nb = 0; nb < NB; nb++)
-                        v0[nb][r] = (_Float16)0.0f;
-                }
-                if (!(tb < t1 && okB)) {
-                    sc[4 + r] = -INFINITY;
-#pragma unroll
-                    for (int nb = 0; nb < NB; nb++)
-                        v1[nb][r] = (_Float16)0.0f;
-                }
+    int base = t0 + 32 * w;
+    if (base < t1) {
+        h8 k0[KK], k1[KK], v[NB];
+        int64_t pA, pB;
+        bool ok;
+        block_pages(a, bt, base, t1, j, g, pA, pB, ok);
+        load_k<HD, NT>(a, pA, pB, base, koff, j, g, k0, k1);
+        load_v<HD, NT>(a, pA, pB, base, voff, j, g, v);
+        for (;;) {
+            f4 s0, s1;
+            qk<HD, GP>(k0, k1, qh, ql, s0, s1);
+            const int next = base + stride;
+            const bool more = next < t1;
+            int64_t nA = pA, nB = pB;
+            bool nok = ok;
+            if (PREFETCH && more) {
+                // K registers are free once the scores exist: start the next
+                // block's K loads before the softmax and P*V of this one.
+                block_pages(a, bt, next, t1, j, g, nA, nB, nok);
+                load_k<HD, NT>(a, nA, nB, next, koff, j, g, k0, k1);
             }
-        }
-        float mx = sc[0];
-#pragma unroll
-        for (int i = 1; i < 8; i++)
-            mx = fmaxf(mx, sc[i]);
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float mnew = fmaxf(m2, mx);
-        const float alpha = exp2f(m2 - mnew);
-        m2 = mnew;
-        float ps = 0.0f;
-        h8 ph, pl;
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const float p = exp2f(sc[i] - mnew);
-            ps += p;
-            const _Float16 hi = (_Float16)p;
-            ph[i] = hi;
-            pl[i] = (_Float16)(p - (float)hi);
-        }
-        lsum = lsum * alpha + ps;
-        // output rows of this lane are heads 4*q4 + r; their rescale factor
-        // lives in lane 4*q4 + r (any lane whose column is that head)
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const float ar = __shfl(alpha, 4 * q4 + r);
-#pragma unroll
-            for (int nb = 0; nb < NB; nb++)
-                o[nb][r] *= ar;
-        }
-#pragma unroll
-        for (int nb = 0; nb < NB; nb++) {
-            h8 vv;
-#pragma unroll
-            for (int v = 0; v < 4; v++) {
-                vv[v] = v0[nb][v];
-                vv[4 + v] = v1[nb][v];
+            softmax_pv<HD, GP>(s0, s1, v, base, ok, t1, j, g, c, S);
+            if (!more)
+                break;
+            if (PREFETCH) {
+                load_v<HD, NT>(a, nA, nB, next, voff, j, g, v);
+            } else {
+                block_pages(a, bt, next, t1, j, g, nA, nB, nok);
+                load_k<HD, NT>(a, nA, nB, next, koff, j, g, k0, k1);
+                load_v<HD, NT>(a, nA, nB, next, voff, j, g, v);
             }
-            o[nb] = mfma(ph, vv, o[nb]);
-            o[nb] = mfma(pl, vv, o[nb]);
+            pA = nA;
+            pB = nB;
+            ok = nok;
+            base = next;
         }
     }
 
     // wave totals -> LDS
-    float lt = lsum;
+    float lt = S.lsum;
     lt += __shfl_xor(lt, 16);
     lt += __shfl_xor(lt, 32);
-    if (q4 == 0) {
-        s_m[w][j] = m2;
+    if (g == 0) {
+        s_m[w][j] = S.m2;
         s_l[w][j] = lt;
     }
 #pragma unroll
     for (int nb = 0; nb < NB; nb++)
 #pragma unroll
         for (int r = 0; r < 4; r++)
-            s_o[w][4 * q4 + r][16 * nb + j] = o[nb][r];
+            s_o[w][4 * g + r][16 * nb + j] = S.o[nb][r];
     __syncthreads();
 
     for (int e = threadIdx.x; e < G * HD; e += 256) {
@@ -239,7 +371,10 @@ __global__ __launch_bounds__(256) void attn_mfma_f16(DecodeArgs a)
         for (int x = 0; x < 4; x++) {
             const float mx2 = s_m[x][hh];
             const float f = mx2 == -INFINITY ? 0.0f : exp2f(mx2 - M);
-            num = fmaf(s_o[x][hh][d], f, num);
+            float o = s_o[x][hh][d];
+            if (GP != 0)
+                o += s_o[x][2 * G - 1 - hh][d];
+            num = fmaf(o, f, num);
             den = fmaf(s_l[x][hh], f, den);
         }
         if (wsp) {
@@ -254,7 +389,7 @@ __global__ __launch_bounds__(256) void attn_mfma_f16(DecodeArgs a)
     }
 }
 
-} // namespace
+} // namespace mfma_decode
 
 bool mfma_decode_supported(const PoolLayout &L, int num_heads)
 {
@@ -268,13 +403,46 @@ bool mfma_decode_supported(const PoolLayout &L, int num_heads)
     return G >= 1 && G <= 16;
 }
 
+#ifndef GI_MFMA_DECODE_NT
+#define GI_MFMA_DECODE_NT true
+#endif
+#ifndef GI_MFMA_DECODE_PREFETCH
+#define GI_MFMA_DECODE_PREFETCH true
+#endif
+#ifndef GI_MFMA_DECODE_OCC
+#define GI_MFMA_DECODE_OCC 1
+#endif
+#ifndef GI_MFMA_DECODE_PACK
+#define GI_MFMA_DECODE_PACK true
+#endif
+
+template <int HD, int GP>
+static void launch_mfma_hd(const DecodeArgs &a, dim3 grid, hipStream_t st)
+{
+    hipLaunchKernelGGL((mfma_decode::attn_mfma_f16<HD, GP, GI_MFMA_DECODE_NT, GI_MFMA_DECODE_PREFETCH,
+                                                   GI_MFMA_DECODE_OCC>),
+                       grid, dim3(256), 0, st, a);
+}
+
+template <int HD>
+static void launch_mfma_g(const DecodeArgs &a, dim3 grid, hipStream_t st)
+{
+    switch (a.num_heads / a.L.num_kv_heads) {
+    case 1: launch_mfma_hd<HD, GI_MFMA_DECODE_PACK ? 1 : 0>(a, grid, st); break;
+    case 2: launch_mfma_hd<HD, GI_MFMA_DECODE_PACK ? 2 : 0>(a, grid, st); break;
+    case 4: launch_mfma_hd<HD, GI_MFMA_DECODE_PACK ? 4 : 0>(a, grid, st); break;
+    case 8: launch_mfma_hd<HD, GI_MFMA_DECODE_PACK ? 8 : 0>(a, grid, st); break;
+    default: launch_mfma_hd<HD, 0>(a, grid, st); break;
+    }
+}
+
 hipError_t launch_decode_mfma(const DecodeArgs &a, hipStream_t st)
 {
     dim3 grid(a.num_splits, a.L.num_kv_heads, a.batch);
     if (a.L.head_dim == 128)
-        hipLaunchKernelGGL(attn_mfma_f16<128>, grid, dim3(256), 0, st, a);
+        launch_mfma_g<128>(a, grid, st);
     else
-        hipLaunchKernelGGL(attn_mfma_f16<64>, grid, dim3(256), 0, st, a);
+        launch_mfma_g<64>(a, grid, st);
     return hipGetLastError();
 }
 

@@ -70,7 +70,9 @@ __device__ __forceinline__ bool resolve(const Dest &D, const PoolLayout &L, int 
 }
 
 // f32 / f16 append: one thread per (token, element); K and V both.
-template <int KT>
+// AT_LEN selects the decode-step form (position from seq_lens); it only
+// names the instance so profiles tell the per-step append from bulk writes.
+template <int KT, bool AT_LEN>
 __global__ __launch_bounds__(kThreads) void append_plain(PoolLayout L, uint8_t *base, int n_tok,
                                                          Dest D, const float *__restrict__ k,
                                                          const float *__restrict__ v, int *status)
@@ -117,6 +119,7 @@ __device__ __forceinline__ uint32_t max32(uint32_t x)
 }
 
 // q8_0 append: 32 consecutive threads quantise one block of 32 elements.
+template <bool AT_LEN>
 __global__ __launch_bounds__(kThreads) void append_q8(PoolLayout L, uint8_t *base, int n_tok,
                                                       Dest D, const float *__restrict__ k,
                                                       const float *__restrict__ v, int *status)
@@ -258,17 +261,30 @@ hipError_t append_any(const PoolLayout &L, uint8_t *base, int n_tok, const Dest 
         return hipSuccess;
     int64_t units = (int64_t)n_tok * L.num_kv_heads * L.head_dim;
     dim3 grid(grid_for(units)), block(kThreads);
+    const bool at_len = D.block_ids == nullptr;
+#define GI_APPEND(KERNEL)                                                                    \
+    hipLaunchKernelGGL(KERNEL, grid, block, 0, st, L, base, n_tok, D, k, v, status)
     switch (L.kv_type) {
     case KV_F32:
-        hipLaunchKernelGGL(append_plain<KV_F32>, grid, block, 0, st, L, base, n_tok, D, k, v, status);
+        if (at_len)
+            GI_APPEND((append_plain<KV_F32, true>));
+        else
+            GI_APPEND((append_plain<KV_F32, false>));
         break;
     case KV_F16:
-        hipLaunchKernelGGL(append_plain<KV_F16>, grid, block, 0, st, L, base, n_tok, D, k, v, status);
+        if (at_len)
+            GI_APPEND((append_plain<KV_F16, true>));
+        else
+            GI_APPEND((append_plain<KV_F16, false>));
         break;
     default:
-        hipLaunchKernelGGL(append_q8, grid, block, 0, st, L, base, n_tok, D, k, v, status);
+        if (at_len)
+            GI_APPEND(append_q8<true>);
+        else
+            GI_APPEND(append_q8<false>);
         break;
     }
+#undef GI_APPEND
     return hipGetLastError();
 }
 
