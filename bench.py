@@ -9,8 +9,12 @@ the block table) then paged decode attention over all 8192 tokens.  Inputs
 (q, k, v, block tables, lengths) are resident in HBM before timing.
 
 Prints one JSON line (see --help).  --config selects other shapes:
-  llama8b_b32     Llama-3-8B shape, batch 32, context U[512, 4096]
-  llama70b_b8     Llama-3-70B shape (64 q / 8 kv), page 32, batch 8 x 32768
+  llama8b_b32         Llama-3-8B shape, batch 32, context U[512, 4096]
+  llama70b_b8         Llama-3-70B shape (64 q / 8 kv), page 32, batch 8 x 32768
+  llama8b_q8_prefill  Llama-3-8B shape, Q8_0 KV: a 4096-token prefill of batch 4
+                      in 512-token chunks (append with on-the-fly quantisation,
+                      then causal paged attention over the context so far), all
+                      32 layers; reports TFLOP/s of the attention
 """
 import argparse
 import json
@@ -36,6 +40,10 @@ CONFIGS = {
     "llama70b_b8": dict(workload="llama3-70b-shape decode step, long context",
                         layers=80, q_heads=64, kv_heads=8, head_dim=128, page_tokens=32,
                         batch=8, context="32768", frag=False),
+    "llama8b_q8_prefill": dict(workload="llama3-8b-shape q8_0 chunked prefill: append + causal "
+                                        "paged attention", layers=32, q_heads=32, kv_heads=8,
+                               head_dim=128, page_tokens=16, batch=4, context="4096", chunk=512,
+                               frag=True, prefill=True),
 }
 
 
@@ -174,6 +182,125 @@ def cpu_baseline(oracle, cfg, budget_s=12.0):
             "ms_per_step": round(step_s * 1e3, 1)}
 
 
+def prefill_flops(cfg):
+    """Exact causal attention flops of the whole prefill: per sequence and
+    layer 2 products x 2 flops x head_dim x q_heads x sum_{i=1..L} i."""
+    L = int(cfg["context"])
+    return (4 * cfg["head_dim"] * cfg["q_heads"] * (L * (L + 1) // 2) * cfg["layers"]
+            * cfg["batch"])
+
+
+def run_prefill(args, gi, torch, dev, cfg):
+    """Config E: whole 4096-token prefill in 512-token chunks, all layers."""
+    H, kvh, hd, P, layers = (cfg["q_heads"], cfg["kv_heads"], cfg["head_dim"],
+                             cfg["page_tokens"], cfg["layers"])
+    kv_dim = kvh * hd
+    B, Ltot, C = cfg["batch"], int(cfg["context"]), cfg["chunk"]
+    lens = np.full(B, Ltot, np.int64)
+    mgr, pages, bt = build_tables(gi, cfg, lens, args.seed)
+    stream = torch.cuda.Stream(dev)
+    torch.cuda.set_stream(stream)
+    pool = gi.PagedKVCache(layers, kvh, hd, P, pages, gi.KV_Q8_0, stream=stream)
+    pool.set_decode_kernel(args.decode_kernel)
+    bt_d = torch.from_numpy(bt).to(dev)
+    # per-chunk (ids, slots) of the batch's tokens, sequence-major
+    ids = np.stack([np.repeat(bt[i], P)[:Ltot] for i in range(B)])
+    slots = np.tile(np.arange(Ltot, dtype=np.int32) % P, (B, 1))
+    chunk_ids = [torch.from_numpy(np.ascontiguousarray(ids[:, c:c + C]).reshape(-1)).to(dev)
+                 for c in range(0, Ltot, C)]
+    chunk_slots = [torch.from_numpy(np.ascontiguousarray(slots[:, c:c + C]).reshape(-1)).to(dev)
+                   for c in range(0, Ltot, C)]
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+
+    def outl(t):
+        # N(0,1) with 1 % of entries at +-8 sigma
+        m = torch.rand(t.shape, generator=gen, device=dev) < 0.01
+        sgn = torch.where(torch.rand(t.shape, generator=gen, device=dev) < 0.5, -8.0, 8.0)
+        return torch.where(m, sgn, t)
+
+    q = outl(torch.randn((layers, B, C, H * hd), generator=gen, device=dev))
+    kn = outl(torch.randn((layers, B * C, kv_dim), generator=gen, device=dev))
+    vn = outl(torch.randn((layers, B * C, kv_dim), generator=gen, device=dev))
+    out = torch.empty((layers, B, C, H * hd), device=dev)
+    scale = gi.attn_scale(hd)
+    nch = Ltot // C
+    ev = []
+
+    def prefill(record):
+        for ci in range(nch):
+            sp = torch.full((B,), ci * C, dtype=torch.int32, device=dev)
+            for l in range(layers):
+                pool.Write(l, chunk_ids[ci], chunk_slots[ci], kn[l], vn[l])
+                if record:
+                    e0 = torch.cuda.Event(enable_timing=True)
+                    e1 = torch.cuda.Event(enable_timing=True)
+                    e0.record(stream)
+                pool.AttentionGQABatch(out[l], q[l], l, bt_d, sp, H, scale, C)
+                if record:
+                    e1.record(stream)
+                    ev.append((e0, e1))
+
+    for _ in range(args.warmup):
+        prefill(False)
+    pool.synchronize()
+    torch.cuda.synchronize()
+    s0 = torch.cuda.Event(enable_timing=True)
+    s1 = torch.cuda.Event(enable_timing=True)
+    s0.record(stream)
+    for _ in range(args.steps):
+        prefill(True)
+    s1.record(stream)
+    torch.cuda.synchronize()
+    pool.synchronize()
+    ms_step = s0.elapsed_time(s1) / args.steps
+    attn_ms = sum(a.elapsed_time(b) for a, b in ev) / args.steps
+    flops = prefill_flops(cfg)
+    tflops = flops / (attn_ms * 1e-3) / 1e12
+    log("prefill %.3f ms (attention %.3f ms, %.1f TFLOP/s)" % (ms_step, attn_ms, tflops))
+
+    parity = None
+    if not args.no_parity:
+        import oracle
+        # last chunk of sequence 0, layer 5: the oracle over the gathered pages
+        i, l = 0, 5
+        kw, vw = pool.Get(l, bt_d[i], Ltot, widen=True)
+        pool.synchronize()
+        want = oracle.attention_prefill(q[l, i].cpu().numpy(), kw.cpu().numpy(), vw.cpu().numpy(),
+                                        H, kvh, hd, Ltot - C, C, 1 << 30, scale)
+        got = out[l, i].cpu().numpy().astype(np.float64).reshape(-1, hd)
+        w = want.astype(np.float64).reshape(-1, hd)
+        err = float((np.abs(got - w).max(axis=1) / np.abs(w).max(axis=1)).max())
+        parity = {"sampled_seq_layer_chunk": [i, l, nch - 1], "max_rel_err": err, "tol": 1e-3,
+                  "pass": bool(err <= 1e-3)}
+    res = {
+        "metric": METRIC,
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (N(0,1) with 1% outliers at +-8 sigma)",
+        "config": {"workload": cfg["workload"], "layers": layers, "q_heads": H, "kv_heads": kvh,
+                   "head_dim": hd, "kv_dtype": "q8_0", "page_tokens": P, "batch": B,
+                   "context": Ltot, "chunk": C},
+        "attention_ms_per_step": round(attn_ms, 4),
+        "append_and_gaps_ms_per_step": round(ms_step - attn_ms, 4),
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": 2500.0,
+                     "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4), "traffic": None,
+                     "kernel": "paged prefill attention",
+                     "flops_per_step": flops},
+        "parity": parity,
+    }
+    print(json.dumps(res), flush=True)
+    pool.close()
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -201,6 +328,9 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
     dev = torch.device("cuda:0")
     cfg = CONFIGS[args.config]
+    if cfg.get("prefill"):
+        run_prefill(args, gi, torch, dev, cfg)
+        return
     H, kvh, hd, P, layers = (cfg["q_heads"], cfg["kv_heads"], cfg["head_dim"],
                              cfg["page_tokens"], cfg["layers"])
     kv_dim = kvh * hd

@@ -293,7 +293,7 @@ hipError_t launch_valu_kt(const DecodeArgs &a, dim3 grid, hipStream_t st)
         return hipGetLastError();                                                            \
     }
     GI_VALU(64, 1) GI_VALU(64, 2) GI_VALU(64, 4) GI_VALU(64, 8)
-    GI_VALU(128, 1) GI_VALU(128, 2) GI_VALU(128, 4) GI_VALU(128, 8)
+    GI_VALU(128, 1) GI_VALU(128, 2) GI_VALU(128, 4) GI_VALU(128, 8) GI_VALU(128, 16)
 #undef GI_VALU
     return hipErrorInvalidValue;
 }
@@ -368,6 +368,10 @@ hipError_t launch_decode(const DecodeArgs &a, hipStream_t st)
 
 hipError_t launch_prefill(const PrefillArgs &p, hipStream_t st)
 {
+    if (p.chunk_len <= 0 || p.batch <= 0)
+        return hipSuccess;
+    if (p.kernel != 0 && mfma_prefill_supported(p.L, p.num_heads))
+        return launch_prefill_mfma(p, st);
     DecodeArgs a{};
     a.L = p.L;
     a.base = p.base;

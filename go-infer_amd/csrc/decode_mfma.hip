@@ -193,12 +193,14 @@ __device__ __forceinline__ void softmax_pv(f4 s0, f4 s1, h8 *v, int base, bool o
     const float mnew = fmaxf(S.m2, mx);
     const float alpha = exp2f(S.m2 - mnew);
     S.m2 = mnew;
+    // p carries a factor 2^14 (its lo half stays a normal fp16); the running
+    // sum carries the same factor, which cancels in the final division.
     float ps = 0.0f;
     h8 ph, pl;
     const bool lo_row = GP != 0 && j >= GP;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-        const float p = exp2f(sc[i] - mnew);
+        const float p = exp2f(sc[i] - mnew + 14.0f);
         ps += p;
         const _Float16 hi = (_Float16)p;
         const _Float16 lo = (_Float16)(p - (float)hi);
@@ -282,19 +284,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
     const int qhead = GP == 0 ? j : (j < G ? j : 2 * G - 1 - j);
     const bool qvalid = GP == 0 ? j < G : j < 2 * G;
     const bool qlo = GP != 0 && j >= G;
+    // Each head's query is scaled by 2^qe (from its largest |q|) so both fp16
+    // halves stay normal -- the matrix cores read fp16 denormals as zero --
+    // and the scores are scaled back through c.  The hi and lo columns of a
+    // head see the same values, so they pick the same qe.
     h8 qh[KK], ql[KK];
+    float qv[KK][8];
+    float mq = 0.0f;
 #pragma unroll
     for (int kk = 0; kk < KK; kk++)
 #pragma unroll
         for (int v = 0; v < 8; v++) {
-            float x = qvalid ? a.q[(qrow + qhead) * HD + 32 * kk + 8 * g + v] : 0.0f;
+            qv[kk][v] = qvalid ? a.q[(qrow + qhead) * HD + 32 * kk + 8 * g + v] : 0.0f;
+            mq = fmaxf(mq, fabsf(qv[kk][v]));
+        }
+    mq = fmaxf(mq, __shfl_xor(mq, 16));
+    mq = fmaxf(mq, __shfl_xor(mq, 32));
+    const int qe = pow2_exponent_for(mq);
+    const float up = ldexpf(1.0f, qe);
+#pragma unroll
+    for (int kk = 0; kk < KK; kk++)
+#pragma unroll
+        for (int v = 0; v < 8; v++) {
+            const float x = qv[kk][v] * up;
             _Float16 hi = (_Float16)x;
             _Float16 lo = (_Float16)(x - (float)hi);
             qh[kk][v] = qlo ? lo : hi;
             ql[kk][v] = lo;
         }
 
-    const float c = a.scale * kLog2e;
+    const float c = a.scale * kLog2e * ldexpf(1.0f, -qe);
     State<HD> S;
     S.m2 = -INFINITY;
     S.lsum = 0.0f;

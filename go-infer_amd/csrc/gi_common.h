@@ -179,6 +179,21 @@ __device__ __host__ __forceinline__ uint32_t abs_key(float x)
     return a > 0x7F800000u ? 0u : a;
 }
 
+// Power-of-two exponent e such that max_abs * 2^e <= 2^14, clamped to
+// [-60, 60] (0 for a zero or non-finite input).  Multiplying by 2^e is exact,
+// and it keeps both halves of an fp16 hi/lo split in the normal range: the
+// matrix cores treat fp16 denormal operands as zero.
+__device__ __host__ __forceinline__ int pow2_exponent_for(float max_abs)
+{
+    uint32_t bits = __builtin_bit_cast(uint32_t, max_abs);
+    int ex = (int)((bits >> 23) & 0xFF);
+    if (ex == 0 || ex == 255)
+        return 0;
+    int ceil_log2 = ex - 127 + ((bits & 0x7FFFFFu) ? 1 : 0);
+    int e = 14 - ceil_log2;
+    return e < -60 ? -60 : (e > 60 ? 60 : e);
+}
+
 // Error flag bits raised by kernels into the handle's device status word.
 enum : int { FLAG_BAD_PAGE = 1, FLAG_BAD_SLOT = 2 };
 

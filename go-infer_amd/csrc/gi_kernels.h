@@ -76,8 +76,12 @@ struct PrefillArgs {
     int num_heads;
     float scale;
     int *status;
+    int kernel; // -1 automatic, 0 vector ALU, 1 matrix core
 };
 
 hipError_t launch_prefill(const PrefillArgs &a, hipStream_t st);
+
+bool mfma_prefill_supported(const PoolLayout &L, int num_heads);
+hipError_t launch_prefill_mfma(const PrefillArgs &a, hipStream_t st);
 
 } // namespace gi

@@ -99,6 +99,8 @@ bool supported_heads(const gi::PoolLayout &L, int num_heads)
     if (num_heads <= 0 || num_heads % L.num_kv_heads)
         return false;
     int G = num_heads / L.num_kv_heads;
+    if (L.head_dim == 128 && G == 16)
+        return true;
     return (L.head_dim == 64 || L.head_dim == 128) && (G == 1 || G == 2 || G == 4 || G == 8);
 }
 
@@ -411,7 +413,8 @@ static int check_decode_args(gi_paged *h, int layer, int batch, int num_heads, c
     if (!supported_heads(h->L, num_heads))
         return gi::set_error(GI_ERR_BAD_ARG, std::string(what) +
                                                  ": unsupported head layout (head_dim 64/128, "
-                                                 "num_heads/num_kv_heads in {1,2,4,8})");
+                                                 "num_heads/num_kv_heads in {1,2,4,8}, or 16 "
+                                                 "with head_dim 128)");
     return GI_OK;
 }
 
@@ -477,6 +480,7 @@ int gi_paged_prefill_attention(gi_paged *h, int layer, int batch, int chunk_len,
     p.num_heads = num_heads;
     p.scale = scale;
     p.status = h->d_status;
+    p.kernel = h->decode_kernel;
     hipError_t e = gi::launch_prefill(p, h->stream);
     return e == hipSuccess ? GI_OK : hip_fail(e, "gi_paged_prefill_attention");
 }

@@ -195,9 +195,9 @@ int gi_paged_prefill_attention(gi_paged *h, int layer, int batch, int chunk_len,
  * 1 matrix core (fp16 pages, head_dim 64/128, page_tokens % 16 == 0). */
 int gi_paged_decode_kernel(const gi_paged *h, int num_heads);
 
-/* Selects the decode kernel: -1 automatic (default), 0 vector ALU, 1 matrix
- * core where supported.  For comparisons; results agree within the
- * attention tolerance. */
+/* Selects the attention kernels (decode and prefill): -1 automatic
+ * (default), 0 vector ALU, 1 matrix core where supported.  For
+ * comparisons; results agree within the attention tolerance. */
 int gi_paged_set_decode_kernel(gi_paged *h, int kind);
 
 #ifdef __cplusplus

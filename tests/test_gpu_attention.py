@@ -187,24 +187,43 @@ def prefill_case(gi, oracle, dev, kv_type, H, kvh, hd, P, starts, chunk, seed):
     bt = pop.block_tables()
     sp = torch.tensor(starts, dtype=torch.int32, device=dev)
     qd, q = seeded((len(starts), chunk, H * hd), seed + 50, dev, outliers=True)
-    out = torch.full_like(qd, float("nan"))
     scale = oracle.attn_scale(hd)
-    pop.pool.AttentionGQABatch(out, qd, 0, bt, sp, H, scale, chunk)
-    pop.pool.synchronize()
-    o = out.cpu().numpy()
-    worst = 0.0
+    wants = []
     for i, s in enumerate(starts):
         ks, vs = pop.stored(0, i)
         kw = oracle.widen(kv_type, pop.kv_dim, ks)
         vw = oracle.widen(kv_type, pop.kv_dim, vs)
-        want = oracle.attention_prefill(q[i], kw, vw, H, kvh, hd, s, chunk, 1 << 30, scale)
-        worst = max(worst, float(rel_err_rows(o[i], want, H, hd).max()))
-    assert worst <= TOL[kv_type], worst
+        wants.append(oracle.attention_prefill(q[i], kw, vw, H, kvh, hd, s, chunk, 1 << 30, scale))
+    # both attention kernels: vector ALU (0) and, for fp16 / q8_0 pages, the
+    # matrix-core prefill (1)
+    kinds = [0, 1] if kv_type in (1, 2) else [0]
+    worst = {}
+    for kern in kinds:
+        pop.pool.set_decode_kernel(kern)
+        out = torch.full_like(qd, float("nan"))
+        pop.pool.AttentionGQABatch(out, qd, 0, bt, sp, H, scale, chunk)
+        pop.pool.synchronize()
+        o = out.cpu().numpy()
+        for i in range(len(starts)):
+            e = float(rel_err_rows(o[i], wants[i], H, hd).max())
+            worst[kern] = max(worst.get(kern, 0.0), e)
+    pop.pool.set_decode_kernel(-1)
+    print("prefill max rel err by kernel:", worst)
+    assert max(worst.values()) <= TOL[kv_type], worst
 
 
 @pytest.mark.parametrize("kv_type", [0, 1, 2], ids=["f32", "f16", "q8_0"])
 def test_prefill_chunk(gi, oracle, dev, kv_type):
     prefill_case(gi, oracle, dev, kv_type, 32, 8, 128, 16, [0, 100, 509], 64, seed=60 + kv_type)
+
+
+@pytest.mark.parametrize("kv_type", [1, 2], ids=["f16", "q8_0"])
+@pytest.mark.parametrize("H,kvh,hd,P", [(8, 8, 64, 16), (16, 8, 64, 32), (64, 8, 128, 32),
+                                        (32, 2, 128, 16)])
+def test_prefill_shapes(gi, oracle, dev, kv_type, H, kvh, hd, P):
+    """Group sizes 1, 2, 8, 16 and head_dim 64 on the matrix-core prefill;
+    ragged chunk (37 queries) and start positions off the page grid."""
+    prefill_case(gi, oracle, dev, kv_type, H, kvh, hd, P, [3, 45], 37, seed=80 + kv_type)
 
 
 def test_prefill_q8_llama8b_chunks(gi, oracle, dev):
