@@ -15,6 +15,7 @@ Prints one JSON line (see --help).  --config selects other shapes:
                       in 512-token chunks (append with on-the-fly quantisation,
                       then causal paged attention over the context so far), all
                       32 layers; reports TFLOP/s of the attention
+  llama8b_f16_prefill the same prefill over fp16 pages
 """
 import argparse
 import json
@@ -43,7 +44,11 @@ CONFIGS = {
     "llama8b_q8_prefill": dict(workload="llama3-8b-shape q8_0 chunked prefill: append + causal "
                                         "paged attention", layers=32, q_heads=32, kv_heads=8,
                                head_dim=128, page_tokens=16, batch=4, context="4096", chunk=512,
-                               frag=True, prefill=True),
+                               frag=True, prefill=True, kv_dtype="q8_0"),
+    "llama8b_f16_prefill": dict(workload="llama3-8b-shape fp16 chunked prefill: append + causal "
+                                         "paged attention", layers=32, q_heads=32, kv_heads=8,
+                                head_dim=128, page_tokens=16, batch=4, context="4096", chunk=512,
+                                frag=True, prefill=True, kv_dtype="f16"),
 }
 
 
@@ -191,7 +196,7 @@ def prefill_flops(cfg):
 
 
 def run_prefill(args, gi, torch, dev, cfg):
-    """Config E: whole 4096-token prefill in 512-token chunks, all layers."""
+    """Whole 4096-token prefill in 512-token chunks, all layers."""
     H, kvh, hd, P, layers = (cfg["q_heads"], cfg["kv_heads"], cfg["head_dim"],
                              cfg["page_tokens"], cfg["layers"])
     kv_dim = kvh * hd
@@ -200,7 +205,8 @@ def run_prefill(args, gi, torch, dev, cfg):
     mgr, pages, bt = build_tables(gi, cfg, lens, args.seed)
     stream = torch.cuda.Stream(dev)
     torch.cuda.set_stream(stream)
-    pool = gi.PagedKVCache(layers, kvh, hd, P, pages, gi.KV_Q8_0, stream=stream)
+    kv_type = gi.KV_Q8_0 if cfg["kv_dtype"] == "q8_0" else gi.KV_F16
+    pool = gi.PagedKVCache(layers, kvh, hd, P, pages, kv_type, stream=stream)
     pool.set_decode_kernel(args.decode_kernel)
     bt_d = torch.from_numpy(bt).to(dev)
     # per-chunk (ids, slots) of the batch's tokens, sequence-major
@@ -287,7 +293,7 @@ def run_prefill(args, gi, torch, dev, cfg):
         "dtype": "f16",
         "data": "synthetic (N(0,1) with 1% outliers at +-8 sigma)",
         "config": {"workload": cfg["workload"], "layers": layers, "q_heads": H, "kv_heads": kvh,
-                   "head_dim": hd, "kv_dtype": "q8_0", "page_tokens": P, "batch": B,
+                   "head_dim": hd, "kv_dtype": cfg["kv_dtype"], "page_tokens": P, "batch": B,
                    "context": Ltot, "chunk": C},
         "attention_ms_per_step": round(attn_ms, 4),
         "append_and_gaps_ms_per_step": round(ms_step - attn_ms, 4),

@@ -417,218 +417,199 @@ __global__ __launch_bounds__(256) void attn_prefill(PrefillArgs a)
 
 
 // ---------------------------------------------------------------------------
-// LDS-staged form.  A workgroup owns 4 x NCG x 16 (query, head) columns of one
-// kv head and streams the context in 64-token blocks through double-buffered
-// LDS: all 256 threads load a block (one 16-byte global load per chunk,
-// int8 converted to exact fp16 on the way), then every wave reads its MFMA
+// LDS-staged form (page size dividing 64).  A workgroup owns 64 (query, head)
+// columns of one kv head -- 16 per wave -- and streams the context in 64-token
+// blocks through LDS: all 256 threads load a block with one 16-byte global
+// load per chunk, convert it, and store it; every wave then reads its MFMA
 // operands from LDS.  The next block's global loads are in flight while the
-// current block is computed.  Used when the page size divides 64.
+// current block is computed.
+//
+// Page ids come from one block-table load per lane (lane l: token l of a
+// block), issued a block ahead; each chunk of a wave lies inside one page, so
+// its page id is read out of that register as a wave-uniform value.  A 64-bit
+// ballot of the same register marks the block's tokens that are cached and on
+// a valid page.
+//
+// q8_0 V is dequantised while staging into an exact pair of fp16 halves:
+// hi = fp16(q * s) and lo = fma(q, s, -hi), whose exact value fits a half
+// because q * s has at most 19 significant bits.  P * V then takes three
+// products (P_hi V_hi, P_lo V_hi, P_hi V_lo).  The K block scale multiplies
+// the partial scores of its 32-wide k-step.
 constexpr int kTB = 64; // tokens per staged block
 
 template <int HD, int KT>
 struct StageRegs {
-    // 16-byte chunks per thread: fp16 K and V rows of 8 elements, or int8 K
-    // rows / V columns of 16 elements.
+    // 16-byte chunks per thread and block: fp16 K rows / V columns of 8
+    // elements, or int8 K rows / V columns of 16 elements.
     static constexpr int NC = KT == KV_F16 ? HD / 32 : HD / 64;
     u4 k[NC], v[NC];
-    uint32_t ks[HD / 64 > 0 ? HD / 64 : 1]; // q8_0: K scales of one token, packed halves
-    uint32_t vs;                            // q8_0: one V scale (low half)
+    u4 vs[KT == KV_Q8_0 ? 2 * NC : 1]; // q8_0: the 16 V scales of each V chunk
+    uint32_t ks[HD / 64];              // q8_0: K scales of token tid (tid < 64)
 };
 
-template <int HD, int KT>
+template <int HD, int KT, int NBUF>
 struct Lds {
-    __attribute__((aligned(16))) _Float16 k[2][kTB][HD + 8]; // token-major K, rows padded
-    __attribute__((aligned(16))) _Float16 v[2][HD][kTB + 8]; // dimension-major V
-    __attribute__((aligned(16))) float ksc[2][kTB][HD / 32]; // q8_0 K scales
-    __attribute__((aligned(16))) float vsc[2][HD / 32][kTB]; // q8_0 V scales
-    uint8_t valid[2][kTB];                                   // token on a page inside the pool
+    static constexpr bool Q8 = KT == KV_Q8_0;
+    __attribute__((aligned(16))) _Float16 k[NBUF][kTB][HD + 8];  // token-major K, rows padded
+    __attribute__((aligned(16))) _Float16 v[NBUF][HD][kTB + 8];  // dimension-major V (q8_0: hi)
+    __attribute__((aligned(16))) _Float16 vl[Q8 ? NBUF : 1][Q8 ? HD : 1][kTB + 8]; // q8_0: V lo
+    __attribute__((aligned(16))) float ksc[Q8 ? NBUF : 1][kTB][HD / 32];            // q8_0: K scales
 };
 
-template <int HD, int KT>
-__device__ __forceinline__ void stage_load(const PrefillArgs &a, const int32_t *bt, int base,
-                                           int wg_len, int kvh, int tid, StageRegs<HD, KT> &R)
+// Chunk -> (token, column) of K and (page segment, dimension, token group)
+// of V inside one block.  F16: 8 elements per chunk, q8_0: 16.
+template <int HD, int KT, int P>
+struct ChunkMap {
+    static constexpr int E = KT == KV_F16 ? 8 : 16;  // elements per chunk
+    static constexpr int KPR = HD / E;               // K chunks per token row
+    static constexpr int VPD = P / E;                // V chunks per dimension and page
+    static constexpr int VPS = HD * VPD;             // V chunks per page segment
+    static_assert(VPS % 64 == 0 && (64 * E / HD) <= P, "a wave's chunks must share one page");
+    __device__ static int k_tok(int ch) { return ch / KPR; }
+    __device__ static int k_col(int ch) { return E * (ch % KPR); }
+    __device__ static int v_seg(int ch) { return ch / VPS; }
+    __device__ static int v_dim(int ch) { return (ch % VPS) / VPD; }
+    __device__ static int v_tok(int ch) { return E * ((ch % VPS) % VPD); } // within the page
+};
+
+// Page id of token `t` of the context (lane-wise), -1 past the cached range.
+template <int P>
+__device__ __forceinline__ int table_entry(const int32_t *bt, int t, int wg_len)
 {
+    return t < wg_len ? bt[t / P] : -1;
+}
+
+template <int HD, int KT, int P>
+__device__ __forceinline__ void stage_load(const PrefillArgs &a, int kvh, int tid, int w, int tb,
+                                           StageRegs<HD, KT> &R)
+{
+    using M = ChunkMap<HD, KT, P>;
     const PoolLayout &L = a.L;
-    const int P = L.page_tokens;
-    auto page_of = [&](int t) -> int64_t {
-        if (t >= wg_len)
-            return -1;
-        int64_t pg = bt[t / P];
-        return (pg >= 0 && pg < L.num_pages) ? pg : -1;
+    const int64_t np = L.num_pages;
+    auto page = [&](int tok) -> int64_t { // wave-uniform
+        const int pg = __builtin_amdgcn_readlane(tb, tok);
+        return (pg >= 0 && pg < np) ? pg : 0;
     };
 #pragma unroll
     for (int c = 0; c < R.NC; c++) {
-        const int ch = tid + 256 * c;
+        const int ch = tid + 256 * c, ch0 = 64 * w + 256 * c;
+        const uint8_t *kp = a.base + page(M::k_tok(ch0)) * L.page_bytes + L.k_off;
+        const int tk = M::k_tok(ch);
+        const uint8_t *vp = a.base + page(M::v_seg(ch0) * P) * L.page_bytes;
+        const int d = M::v_dim(ch), tv = M::v_tok(ch);
         if (KT == KV_F16) {
-            // K: token ch / (HD/8), 8 elements at column 8*(ch % (HD/8))
-            const int tok = ch / (HD / 8), col = ch % (HD / 8);
-            const int t = base + tok;
-            const int64_t pg = page_of(t);
-            R.k[c] = pg < 0 ? u4{0, 0, 0, 0}
-                            : __builtin_nontemporal_load(reinterpret_cast<const u4 *>(
-                                  a.base + pg * L.page_bytes + L.k_off +
-                                  (((int64_t)kvh * P + t % P) * HD + 8 * col) * 2));
-            // V: page segment, dimension, group of 8 tokens
-            const int per_seg = HD * P / 8;
-            const int seg = ch / per_seg, rem = ch % per_seg;
-            const int d = rem / (P / 8), tg = rem % (P / 8);
-            const int tv = base + seg * P + 8 * tg;
-            const int64_t pv = page_of(tv);
-            R.v[c] = pv < 0 ? u4{0, 0, 0, 0}
-                            : __builtin_nontemporal_load(reinterpret_cast<const u4 *>(
-                                  a.base + pv * L.page_bytes + L.v_off +
-                                  (((int64_t)kvh * HD + d) * P + 8 * tg) * 2));
+            R.k[c] = *reinterpret_cast<const u4 *>(kp + (((int64_t)kvh * P + tk % P) * HD + M::k_col(ch)) * 2);
+            R.v[c] = *reinterpret_cast<const u4 *>(vp + L.v_off + (((int64_t)kvh * HD + d) * P + tv) * 2);
         } else {
-            const int tok = ch / (HD / 16), col = ch % (HD / 16);
-            const int t = base + tok;
-            const int64_t pg = page_of(t);
-            R.k[c] = pg < 0 ? u4{0, 0, 0, 0}
-                            : __builtin_nontemporal_load(reinterpret_cast<const u4 *>(
-                                  a.base + pg * L.page_bytes + L.k_off +
-                                  ((int64_t)kvh * P + t % P) * HD + 16 * col));
-            const int per_seg = HD * P / 16;
-            const int seg = ch / per_seg, rem = ch % per_seg;
-            const int d = rem / (P / 16), tg = rem % (P / 16);
-            const int tv = base + seg * P + 16 * tg;
-            const int64_t pv = page_of(tv);
-            R.v[c] = pv < 0 ? u4{0, 0, 0, 0}
-                            : __builtin_nontemporal_load(reinterpret_cast<const u4 *>(
-                                  a.base + pv * L.page_bytes + L.v_off +
-                                  ((int64_t)kvh * HD + d) * P + 16 * tg));
+            R.k[c] = *reinterpret_cast<const u4 *>(kp + ((int64_t)kvh * P + tk % P) * HD + M::k_col(ch));
+            R.v[c] = *reinterpret_cast<const u4 *>(vp + L.v_off + ((int64_t)kvh * HD + d) * P + tv);
+            const u4 *sp = reinterpret_cast<const u4 *>(
+                vp + L.vs_off + (((int64_t)kvh * (HD / 32) + d / 32) * P + tv) * 2);
+            R.vs[2 * c] = sp[0];
+            R.vs[2 * c + 1] = sp[1];
         }
     }
-    if (KT == KV_Q8_0) {
-        if (tid < kTB) {
-            const int t = base + tid;
-            const int64_t pg = page_of(t);
-            const uint16_t *src = reinterpret_cast<const uint16_t *>(
-                a.base + (pg < 0 ? 0 : pg) * L.page_bytes + L.ks_off) +
-                ((int64_t)kvh * P + t % P) * (HD / 32);
+    if (KT == KV_Q8_0 && w == 0) {
+        // lane tid holds the page of block token tid
+        const int64_t pg = (tb >= 0 && tb < np) ? tb : 0;
+        const uint32_t *src = reinterpret_cast<const uint32_t *>(
+            a.base + pg * L.page_bytes + L.ks_off + ((int64_t)kvh * P + tid % P) * (HD / 32) * 2);
 #pragma unroll
-            for (int i = 0; i < HD / 64; i++)
-                R.ks[i] = pg < 0 ? 0u : (uint32_t)src[2 * i] | ((uint32_t)src[2 * i + 1] << 16);
-        }
-        if (tid < kTB * (HD / 32)) {
-            const int db = tid / kTB, tok = tid % kTB;
-            const int t = base + tok;
-            const int64_t pg = page_of(t);
-            R.vs = pg < 0 ? 0u
-                          : reinterpret_cast<const uint16_t *>(a.base + pg * L.page_bytes + L.vs_off)
-                                [((int64_t)kvh * (HD / 32) + db) * P + t % P];
-        }
+        for (int i = 0; i < HD / 64; i++)
+            R.ks[i] = src[i];
     }
 }
 
-template <int HD, int KT>
-__device__ __forceinline__ void stage_store(const PrefillArgs &a, const int32_t *bt, int base,
-                                            int wg_len, int tid, int buf,
-                                            const StageRegs<HD, KT> &R, Lds<HD, KT> &S)
+// Converts and stores a staged block.  `vmask` bit l: block token l is cached
+// and on a valid page; V of other tokens is stored as zero (their scores are
+// masked, and stale values must not reach O through 0 * NaN).
+template <int HD, int KT, int P, int NBUF>
+__device__ __forceinline__ void stage_store(int tid, int w, int buf, uint64_t vmask,
+                                            const StageRegs<HD, KT> &R, Lds<HD, KT, NBUF> &S)
 {
-    const PoolLayout &L = a.L;
-    const int P = L.page_tokens;
+    using M = ChunkMap<HD, KT, P>;
 #pragma unroll
     for (int c = 0; c < R.NC; c++) {
         const int ch = tid + 256 * c;
+        const int tk = M::k_tok(ch), col = M::k_col(ch);
+        const int d = M::v_dim(ch), t0 = M::v_seg(ch) * P + M::v_tok(ch); // block-local token
+        const uint32_t live = (uint32_t)(vmask >> t0) & ((1u << M::E) - 1u);
         if (KT == KV_F16) {
-            const int tok = ch / (HD / 8), col = ch % (HD / 8);
-            *reinterpret_cast<u4 *>(&S.k[buf][tok][8 * col]) = R.k[c];
-            const int per_seg = HD * P / 8;
-            const int seg = ch / per_seg, rem = ch % per_seg;
-            const int d = rem / (P / 8), tg = rem % (P / 8);
-            const int t0 = seg * P + 8 * tg; // block-local first token
+            *reinterpret_cast<u4 *>(&S.k[buf][tk][col]) = R.k[c];
             u4 vv = R.v[c];
-            if (base + t0 + 8 > wg_len) {
-                // tokens past the cached range read as zero
+            if (live != 0xFFu) {
 #pragma unroll
                 for (int i = 0; i < 8; i++)
-                    if (base + t0 + i >= wg_len)
+                    if (!((live >> i) & 1u))
                         vv[i / 2] &= (i & 1) ? 0x0000FFFFu : 0xFFFF0000u;
             }
             *reinterpret_cast<u4 *>(&S.v[buf][d][t0]) = vv;
         } else {
-            const int tok = ch / (HD / 16), col = ch % (HD / 16);
-            const h8 lo8 = i8x8_to_h8(uint2{R.k[c][0], R.k[c][1]});
-            const h8 hi8 = i8x8_to_h8(uint2{R.k[c][2], R.k[c][3]});
-            *reinterpret_cast<h8 *>(&S.k[buf][tok][16 * col]) = lo8;
-            *reinterpret_cast<h8 *>(&S.k[buf][tok][16 * col + 8]) = hi8;
-            const int per_seg = HD * P / 16;
-            const int seg = ch / per_seg, rem = ch % per_seg;
-            const int d = rem / (P / 16), tg = rem % (P / 16);
-            const int t0 = seg * P + 16 * tg;
-            h8 v0 = i8x8_to_h8(uint2{R.v[c][0], R.v[c][1]});
-            h8 v1 = i8x8_to_h8(uint2{R.v[c][2], R.v[c][3]});
-            if (base + t0 + 16 > wg_len) {
+            *reinterpret_cast<h8 *>(&S.k[buf][tk][col]) = i8x8_to_h8(uint2{R.k[c][0], R.k[c][1]});
+            *reinterpret_cast<h8 *>(&S.k[buf][tk][col + 8]) = i8x8_to_h8(uint2{R.k[c][2], R.k[c][3]});
 #pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    if (base + t0 + i >= wg_len)
-                        v0[i] = (_Float16)0.0f;
-                    if (base + t0 + 8 + i >= wg_len)
-                        v1[i] = (_Float16)0.0f;
+            for (int half = 0; half < 2; half++) {
+                const h8 q = i8x8_to_h8(uint2{R.v[c][2 * half], R.v[c][2 * half + 1]});
+                const h8 s = __builtin_bit_cast(h8, R.vs[2 * c + half]);
+                h8 hi = q * s;
+                h8 lo = __builtin_elementwise_fma(q, s, -hi);
+                const uint32_t lv = live >> (8 * half);
+                if ((lv & 0xFFu) != 0xFFu) {
+#pragma unroll
+                    for (int i = 0; i < 8; i++)
+                        if (!((lv >> i) & 1u)) {
+                            hi[i] = (_Float16)0.0f;
+                            lo[i] = (_Float16)0.0f;
+                        }
                 }
+                *reinterpret_cast<h8 *>(&S.v[buf][d][t0 + 8 * half]) = hi;
+                *reinterpret_cast<h8 *>(&S.vl[buf][d][t0 + 8 * half]) = lo;
             }
-            *reinterpret_cast<h8 *>(&S.v[buf][d][t0]) = v0;
-            *reinterpret_cast<h8 *>(&S.v[buf][d][t0 + 8]) = v1;
         }
     }
-    if (tid < kTB) {
-        const int t = base + tid;
-        bool ok = t < wg_len;
-        if (ok) {
-            const int64_t pg = bt[t / P];
-            ok = pg >= 0 && pg < L.num_pages;
-            if (!ok && a.status)
-                atomicOr(a.status, FLAG_BAD_PAGE);
-        }
-        S.valid[buf][tid] = ok ? 1 : 0;
-        if (KT == KV_Q8_0) {
+    if (KT == KV_Q8_0 && w == 0) {
 #pragma unroll
-            for (int i = 0; i < HD / 64; i++) {
-                S.ksc[buf][tid][2 * i] = half_bits_to_float(R.ks[i] & 0xFFFFu);
-                S.ksc[buf][tid][2 * i + 1] = half_bits_to_float(R.ks[i] >> 16);
-            }
+        for (int i = 0; i < HD / 64; i++) {
+            const h2 s = __builtin_bit_cast(h2, R.ks[i]);
+            S.ksc[buf][tid][2 * i] = (float)s[0];
+            S.ksc[buf][tid][2 * i + 1] = (float)s[1];
         }
     }
-    if (KT == KV_Q8_0 && tid < kTB * (HD / 32))
-        S.vsc[buf][tid / kTB][tid % kTB] = half_bits_to_float(R.vs);
 }
 
-template <int HD, int KT, int NCG>
+template <int HD, int KT, int P, int NBUF>
 __global__ __launch_bounds__(256) void attn_prefill_lds(PrefillArgs a)
 {
-    constexpr int KK = HD / 32, NB = HD / 16, NDB = HD / 32;
+    constexpr int KK = HD / 32, NB = HD / 16;
     const PoolLayout &L = a.L;
+    // heaviest (latest-query) workgroups first
+    const int wx = gridDim.x - 1 - blockIdx.x;
     const int kvh = blockIdx.y, b = blockIdx.z;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int j = lane & 15, g = lane >> 4;
-    const int H = a.num_heads, G = H / L.num_kv_heads, P = L.page_tokens;
+    const int H = a.num_heads, G = H / L.num_kv_heads;
     const int start = a.start_pos[b];
     const int chunk = a.chunk_len;
     const int32_t *bt = a.block_tables + (int64_t)b * a.max_blocks;
     const int mapped = a.max_blocks * P;
 
-    __shared__ Lds<HD, KT> S;
+    __shared__ Lds<HD, KT, NBUF> S;
 
-    int col0[NCG], qlen[NCG];
-    int wave_len = 0;
-#pragma unroll
-    for (int cg = 0; cg < NCG; cg++) {
-        col0[cg] = ((blockIdx.x * 4 + w) * NCG + cg) * 16;
-        const int qi = min((col0[cg] + j) / G, chunk - 1);
-        qlen[cg] = min(start + qi + 1, mapped);
-        wave_len = max(wave_len, min(start + min((col0[cg] + 15) / G, chunk - 1) + 1, mapped));
-    }
+    const int col0 = (wx * 4 + w) * 16;
+    const int qlen = min(start + min((col0 + j) / G, chunk - 1) + 1, mapped);
+    const int wave_len = min(start + min((col0 + 15) / G, chunk - 1) + 1, mapped);
+    const int wave_full = min(start + col0 / G + 1, mapped); // shortest column of the wave
     if (start + chunk > mapped && tid == 0 && a.status)
         atomicOr(a.status, FLAG_BAD_SLOT);
-    const int wg_last = (blockIdx.x * 4 * NCG + 4 * NCG) * 16 - 1;
-    const int wg_len = min(start + min(wg_last / G, chunk - 1) + 1, mapped);
-    const bool wave_active = col0[0] / G < chunk;
+    const int wg_len = min(start + min((wx * 64 + 63) / G, chunk - 1) + 1, mapped);
+    const bool wave_active = col0 / G < chunk;
 
     // Q^T operands (hi, lo) scaled per column by 2^qe.
-    h8 qh[NCG][KK], ql[NCG][KK];
-    float c2s[NCG];
-#pragma unroll
-    for (int cg = 0; cg < NCG; cg++) {
-        const int c = col0[cg] + j;
+    h8 qh[KK], ql[KK];
+    float c2s;
+    {
+        const int c = col0 + j;
         const int qi = min(c / G, chunk - 1);
         const float *qp = a.q + (((int64_t)b * chunk + qi) * H + kvh * G + c % G) * HD;
         float qv[KK][8];
@@ -644,60 +625,58 @@ __global__ __launch_bounds__(256) void attn_prefill_lds(PrefillArgs a)
         mq = fmaxf(mq, __shfl_xor(mq, 32));
         const int qe = pow2_exponent_for(mq);
         const float up = ldexpf(1.0f, qe);
-        c2s[cg] = a.scale * kLog2e * ldexpf(1.0f, -qe);
+        c2s = a.scale * kLog2e * ldexpf(1.0f, -qe);
 #pragma unroll
-        for (int kk = 0; kk < KK; kk++)
+        for (int kk = 0; kk < KK; kk++) {
+            float x[8];
 #pragma unroll
-            for (int v = 0; v < 8; v++) {
-                _Float16 hi, lo;
-                split_hilo(qv[kk][v] * up, hi, lo);
-                qh[cg][kk][v] = hi;
-                ql[cg][kk][v] = lo;
-            }
+            for (int v = 0; v < 8; v++)
+                x[v] = qv[kk][v] * up;
+            split8(x, qh[kk], ql[kk]);
+        }
     }
 
-    float m2[NCG], lsum[NCG];
-    f4 o[NCG][NB];
+    float m2 = -INFINITY, lsum = 0.0f;
+    f4 o[NB];
 #pragma unroll
-    for (int cg = 0; cg < NCG; cg++) {
-        m2[cg] = -INFINITY;
-        lsum[cg] = 0.0f;
-#pragma unroll
-        for (int nb = 0; nb < NB; nb++)
-            o[cg][nb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-    }
-    float vnorm[NDB];
-#pragma unroll
-    for (int db = 0; db < NDB; db++)
-        vnorm[db] = 0.0f;
+    for (int nb = 0; nb < NB; nb++)
+        o[nb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    auto valid_mask = [&](int tb, int base) -> uint64_t {
+        const bool bad = base + lane < wg_len && !(tb >= 0 && tb < L.num_pages);
+        if (__ballot(bad) && w == 0 && lane == 0 && a.status)
+            atomicOr(a.status, FLAG_BAD_PAGE);
+        return __ballot(tb >= 0 && tb < L.num_pages);
+    };
 
     StageRegs<HD, KT> R;
-    stage_load<HD, KT>(a, bt, 0, wg_len, kvh, tid, R);
-    stage_store<HD, KT>(a, bt, 0, wg_len, tid, 0, R, S);
+    int tb = table_entry<P>(bt, lane, wg_len);
+    uint64_t mask_c = valid_mask(tb, 0);
+    stage_load<HD, KT, P>(a, kvh, tid, w, tb, R);
+    tb = table_entry<P>(bt, kTB + lane, wg_len);
+    stage_store<HD, KT, P, NBUF>(tid, w, 0, mask_c, R, S);
     __syncthreads();
 
     for (int base = 0, it = 0; base < wg_len; base += kTB, it++) {
-        const int buf = it & 1;
+        const int buf = NBUF == 2 ? (it & 1) : 0;
         const bool more = base + kTB < wg_len;
-        if (more)
-            stage_load<HD, KT>(a, bt, base + kTB, wg_len, kvh, tid, R);
+        uint64_t mask_n = 0;
+        if (more) {
+            mask_n = valid_mask(tb, base + kTB);
+            stage_load<HD, KT, P>(a, kvh, tid, w, tb, R);
+            tb = table_entry<P>(bt, base + 2 * kTB + lane, wg_len);
+        }
 
         if (wave_active && base < wave_len) {
             // ---- scores: tiles (h, t), row j = token 32h + 8(j/4) + j%4 + 4t ----
-            f4 s[NCG][2][2];
-#pragma unroll
-            for (int cg = 0; cg < NCG; cg++)
-#pragma unroll
-                for (int h = 0; h < 2; h++)
-#pragma unroll
-                    for (int t = 0; t < 2; t++)
-                        s[cg][h][t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+            f4 s[2][2];
 #pragma unroll
             for (int h = 0; h < 2; h++)
 #pragma unroll
                 for (int t = 0; t < 2; t++) {
+                    s[h][t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
                     const int row = 32 * h + 8 * (j >> 2) + (j & 3) + 4 * t;
-                    float ks[4][KK]; // q8_0: scale of output row token 32h + 8g + 4t + r
+                    float ks[4][KK]; // q8_0: K scales of output row token 32h + 8g + 4t + r
                     if (KT == KV_Q8_0) {
 #pragma unroll
                         for (int r = 0; r < 4; r++)
@@ -708,164 +687,112 @@ __global__ __launch_bounds__(256) void attn_prefill_lds(PrefillArgs a)
 #pragma unroll
                     for (int kk = 0; kk < KK; kk++) {
                         const h8 ka = *reinterpret_cast<const h8 *>(&S.k[buf][row][32 * kk + 8 * g]);
+                        if (KT == KV_F16) {
+                            s[h][t] = mfma(ka, qh[kk], s[h][t]);
+                            s[h][t] = mfma(ka, ql[kk], s[h][t]);
+                        } else {
+                            f4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+                            z = mfma(ka, qh[kk], z);
+                            z = mfma(ka, ql[kk], z);
 #pragma unroll
-                        for (int cg = 0; cg < NCG; cg++) {
-                            if (KT == KV_F16) {
-                                s[cg][h][t] = mfma(ka, qh[cg][kk], s[cg][h][t]);
-                                s[cg][h][t] = mfma(ka, ql[cg][kk], s[cg][h][t]);
-                            } else {
-                                f4 z = {0.0f, 0.0f, 0.0f, 0.0f};
-                                z = mfma(ka, qh[cg][kk], z);
-                                z = mfma(ka, ql[cg][kk], z);
-#pragma unroll
-                                for (int r = 0; r < 4; r++)
-                                    s[cg][h][t][r] = fmaf(z[r], ks[r][kk], s[cg][h][t][r]);
-                            }
+                            for (int r = 0; r < 4; r++)
+                                s[h][t][r] = fmaf(z[r], ks[r][kk], s[h][t][r]);
                         }
                     }
                 }
 
-            // q8_0: running power-of-two normaliser of each V block's scales
-            float vmul[NDB];
-            if (KT == KV_Q8_0) {
+            // ---- online softmax of column j over this lane's 16 tokens ----
+            float sc[16]; // [8h + v]: token 32h + 8g + v
 #pragma unroll
-                for (int db = 0; db < NDB; db++) {
-                    float mv = 0.0f;
+            for (int h = 0; h < 2; h++)
 #pragma unroll
-                    for (int h = 0; h < 2; h++)
+                for (int t = 0; t < 2; t++)
 #pragma unroll
-                        for (int v = 0; v < 8; v++)
-                            mv = fmaxf(mv, S.vsc[buf][db][32 * h + 8 * g + v]);
-                    mv = fmaxf(mv, __shfl_xor(mv, 16));
-                    mv = fmaxf(mv, __shfl_xor(mv, 32));
-                    uint32_t bits = __builtin_bit_cast(uint32_t, mv);
-                    if (bits & 0x7FFFFFu)
-                        bits = (bits & 0xFF800000u) + 0x800000u;
-                    const float pw = __builtin_bit_cast(float, bits);
-                    if (pw > vnorm[db]) {
-                        const float f = vnorm[db] / pw;
-#pragma unroll
-                        for (int cg = 0; cg < NCG; cg++)
-#pragma unroll
-                            for (int hh = 0; hh < 2; hh++)
-                                o[cg][2 * db + hh] *= f;
-                        vnorm[db] = pw;
-                    }
-                    vmul[db] = vnorm[db] > 0.0f ? 1.0f / vnorm[db] : 0.0f;
-                }
-            }
-
-            // ---- online softmax per column ----
-            float p[NCG][16]; // [8h + v]: token 32h + 8g + v
-#pragma unroll
-            for (int cg = 0; cg < NCG; cg++) {
-                float sc[16];
-#pragma unroll
-                for (int h = 0; h < 2; h++)
-#pragma unroll
-                    for (int t = 0; t < 2; t++)
-#pragma unroll
-                        for (int r = 0; r < 4; r++)
-                            sc[8 * h + 4 * t + r] = s[cg][h][t][r] * c2s[cg];
-                const int lim = qlen[cg];
+                    for (int r = 0; r < 4; r++)
+                        sc[8 * h + 4 * t + r] = s[h][t][r] * c2s;
+            if (!(mask_c == ~0ull && base + kTB <= wave_full)) {
+                const uint32_t lm = (uint32_t)(mask_c >> (8 * g));
+                const uint32_t hm = (uint32_t)(mask_c >> (32 + 8 * g));
 #pragma unroll
                 for (int i = 0; i < 16; i++) {
                     const int tl = 32 * (i / 8) + 8 * g + (i % 8);
-                    if (!(base + tl < lim && S.valid[buf][tl]))
+                    const uint32_t bit = ((i < 8 ? lm : hm) >> (i % 8)) & 1u;
+                    if (!(bit && base + tl < qlen))
                         sc[i] = -INFINITY;
                 }
-                float mx = sc[0];
+            }
+            float mx = sc[0];
 #pragma unroll
-                for (int i = 1; i < 16; i++)
-                    mx = fmaxf(mx, sc[i]);
-                mx = fmaxf(mx, __shfl_xor(mx, 16));
-                mx = fmaxf(mx, __shfl_xor(mx, 32));
-                const float mnew = fmaxf(m2[cg], mx);
-                const float alpha = mnew == -INFINITY ? 1.0f : exp2f(m2[cg] - mnew);
-                m2[cg] = mnew;
-                float ps = 0.0f;
+            for (int i = 1; i < 16; i++)
+                mx = fmaxf(mx, sc[i]);
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const float mnew = fmaxf(m2, mx);
+            const float alpha = mnew == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m2 - mnew);
+            // p carries a factor 2^14 so that its lo half stays normal
+            const float msub = mnew == -INFINITY ? 0.0f : mnew - 14.0f;
+            m2 = mnew;
+            float p[16], ps = 0.0f;
 #pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    p[cg][i] = mnew == -INFINITY ? 0.0f : exp2f(sc[i] - mnew + 14.0f);
-                    ps += p[cg][i];
-                }
-                lsum[cg] = lsum[cg] * alpha + ps;
-                if (__any(alpha != 1.0f)) {
+            for (int i = 0; i < 16; i++) {
+                p[i] = __builtin_amdgcn_exp2f(sc[i] - msub);
+                ps += p[i];
+            }
+            lsum = lsum * alpha + ps;
+            if (__any(alpha != 1.0f)) {
 #pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        const float ar = __shfl(alpha, 4 * g + r);
+                for (int r = 0; r < 4; r++) {
+                    const float ar = __shfl(alpha, 4 * g + r);
 #pragma unroll
-                        for (int nb = 0; nb < NB; nb++)
-                            o[cg][nb][r] *= ar;
-                    }
+                    for (int nb = 0; nb < NB; nb++)
+                        o[nb][r] *= ar;
                 }
             }
 
             // ---- P * V, V operand: dimension 16nb + j, tokens 32h + 8g .. +7 ----
 #pragma unroll
             for (int h = 0; h < 2; h++) {
-                h8 ph[NCG], pl[NCG];
-                if (KT == KV_F16) {
-#pragma unroll
-                    for (int cg = 0; cg < NCG; cg++)
-                        split8(&p[cg][8 * h], ph[cg], pl[cg]);
-                }
+                h8 ph, pl;
+                split8(&p[8 * h], ph, pl);
 #pragma unroll
                 for (int nb = 0; nb < NB; nb++) {
-                    if (KT == KV_Q8_0 && (nb & 1) == 0) {
-                        const int db = nb / 2;
-                        float vs8[8];
-#pragma unroll
-                        for (int v = 0; v < 8; v++)
-                            vs8[v] = S.vsc[buf][db][32 * h + 8 * g + v] * vmul[db];
-#pragma unroll
-                        for (int cg = 0; cg < NCG; cg++) {
-                            float x[8];
-#pragma unroll
-                            for (int v = 0; v < 8; v++)
-                                x[v] = p[cg][8 * h + v] * vs8[v];
-                            split8(x, ph[cg], pl[cg]);
-                        }
-                    }
                     const h8 vb = *reinterpret_cast<const h8 *>(&S.v[buf][16 * nb + j][32 * h + 8 * g]);
-#pragma unroll
-                    for (int cg = 0; cg < NCG; cg++) {
-                        o[cg][nb] = mfma(ph[cg], vb, o[cg][nb]);
-                        o[cg][nb] = mfma(pl[cg], vb, o[cg][nb]);
+                    o[nb] = mfma(ph, vb, o[nb]);
+                    o[nb] = mfma(pl, vb, o[nb]);
+                    if (KT == KV_Q8_0) {
+                        const h8 vl = *reinterpret_cast<const h8 *>(&S.vl[buf][16 * nb + j][32 * h + 8 * g]);
+                        o[nb] = mfma(ph, vl, o[nb]);
                     }
                 }
             }
         }
 
-        if (more)
-            stage_store<HD, KT>(a, bt, base + kTB, wg_len, tid, buf ^ 1, R, S);
+        if (more) {
+            if (NBUF == 1)
+                __syncthreads();
+            stage_store<HD, KT, P, NBUF>(tid, w, NBUF == 2 ? (buf ^ 1) : 0, mask_n, R, S);
+        }
+        mask_c = mask_n;
         __syncthreads();
     }
 
     if (!wave_active)
         return;
+    float lt = lsum;
+    lt += __shfl_xor(lt, 16);
+    lt += __shfl_xor(lt, 32);
 #pragma unroll
-    for (int cg = 0; cg < NCG; cg++) {
-        float lt = lsum[cg];
-        lt += __shfl_xor(lt, 16);
-        lt += __shfl_xor(lt, 32);
+    for (int r = 0; r < 4; r++) {
+        const float l = __shfl(lt, 4 * g + r);
+        const int c = col0 + 4 * g + r;
+        const int qi = c / G;
+        if (qi >= chunk)
+            continue;
+        float *op = a.out + (((int64_t)b * chunk + qi) * H + kvh * G + c % G) * HD;
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const float l = __shfl(lt, 4 * g + r);
-            const int c = col0[cg] + 4 * g + r;
-            const int qi = c / G;
-            if (qi >= chunk)
-                continue;
-            float *op = a.out + (((int64_t)b * chunk + qi) * H + kvh * G + c % G) * HD;
-            const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-#pragma unroll
-            for (int nb = 0; nb < NB; nb++) {
-                float x = o[cg][nb][r];
-                if (KT == KV_Q8_0)
-                    x *= vnorm[nb / 2];
-                op[16 * nb + j] = x * inv;
-            }
-        }
+        for (int nb = 0; nb < NB; nb++)
+            op[16 * nb + j] = o[nb][r] * inv;
     }
 }
 
@@ -892,9 +819,33 @@ constexpr int prefill_ncg()
     return HD == 64 ? 2 : 1;
 }
 
-#ifndef GI_PREFILL_LDS_NCG
-#define GI_PREFILL_LDS_NCG 1
+// LDS buffers of the staged kernel: two (one barrier per block) for fp16
+// pages; one for q8_0, whose V hi/lo planes would otherwise leave room for a
+// single workgroup per CU.
+#ifndef GI_PREFILL_NBUF_F16
+#define GI_PREFILL_NBUF_F16 2
 #endif
+#ifndef GI_PREFILL_NBUF_Q8
+#define GI_PREFILL_NBUF_Q8 1
+#endif
+
+template <int HD, int KT>
+static void launch_lds(const PrefillArgs &a, dim3 grid, hipStream_t st)
+{
+    using namespace mfma_prefill;
+    constexpr int NBUF = KT == KV_F16 ? GI_PREFILL_NBUF_F16 : GI_PREFILL_NBUF_Q8;
+    switch (a.L.page_tokens) {
+    case 16:
+        hipLaunchKernelGGL((attn_prefill_lds<HD, KT, 16, NBUF>), grid, dim3(256), 0, st, a);
+        break;
+    case 32:
+        hipLaunchKernelGGL((attn_prefill_lds<HD, KT, 32, NBUF>), grid, dim3(256), 0, st, a);
+        break;
+    default:
+        hipLaunchKernelGGL((attn_prefill_lds<HD, KT, 64, NBUF>), grid, dim3(256), 0, st, a);
+        break;
+    }
+}
 
 hipError_t launch_prefill_mfma(const PrefillArgs &a, hipStream_t st)
 {
@@ -902,23 +853,19 @@ hipError_t launch_prefill_mfma(const PrefillArgs &a, hipStream_t st)
     const int G = a.num_heads / a.L.num_kv_heads;
     const int64_t cols = (int64_t)a.chunk_len * G;
     const int P = a.L.page_tokens;
-    if (64 % P == 0) {
-        constexpr int ncg = GI_PREFILL_LDS_NCG;
-        const int per_wg = 4 * 16 * ncg;
-        dim3 grid((unsigned)((cols + per_wg - 1) / per_wg), a.L.num_kv_heads, a.batch);
-#define GI_PFL(HD, KT) hipLaunchKernelGGL((attn_prefill_lds<HD, KT, ncg>), grid, dim3(256), 0, st, a)
+    if (P == 16 || P == 32 || P == 64) {
+        dim3 grid((unsigned)((cols + 63) / 64), a.L.num_kv_heads, a.batch);
         if (a.L.head_dim == 128) {
             if (a.L.kv_type == KV_F16)
-                GI_PFL(128, KV_F16);
+                launch_lds<128, KV_F16>(a, grid, st);
             else
-                GI_PFL(128, KV_Q8_0);
+                launch_lds<128, KV_Q8_0>(a, grid, st);
         } else {
             if (a.L.kv_type == KV_F16)
-                GI_PFL(64, KV_F16);
+                launch_lds<64, KV_F16>(a, grid, st);
             else
-                GI_PFL(64, KV_Q8_0);
+                launch_lds<64, KV_Q8_0>(a, grid, st);
         }
-#undef GI_PFL
         return hipGetLastError();
     }
     const int per_wg = 4 * 16 * (a.L.head_dim == 64 ? prefill_ncg<64>() : prefill_ncg<128>());
