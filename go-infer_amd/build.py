@@ -24,6 +24,9 @@ ARCH = "gfx950"
 HIP_FLAGS = [
     "--offload-arch=" + ARCH, "-O3", "-fPIC", "-std=c++17", "-Wall",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # matrix-core accumulators in ordinary VGPRs: the online softmax rescales
+    # them between products, which in AGPRs costs a read and a write each
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-I" + CSRC, "-I" + INC,
 ]
 CXX_FLAGS = ["-O2", "-fPIC", "-std=c++17", "-Wall", "-Wextra", "-I" + CSRC, "-I" + INC]

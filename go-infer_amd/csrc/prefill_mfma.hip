@@ -436,6 +436,9 @@ __global__ __launch_bounds__(256) void attn_prefill(PrefillArgs a)
 // products (P_hi V_hi, P_lo V_hi, P_hi V_lo).  The K block scale multiplies
 // the partial scores of its 32-wide k-step.
 constexpr int kTB = 64; // tokens per staged block
+// Online softmax: p = 2^(score - m + kPExp) with the reference maximum m
+// lagging the true one by at most kLazy, so p <= 2^14 stays well inside fp16.
+constexpr float kPExp = 6.0f, kLazy = 8.0f;
 
 template <int HD, int KT>
 struct StageRegs {
@@ -702,14 +705,18 @@ __global__ __launch_bounds__(256) void attn_prefill_lds(PrefillArgs a)
                 }
 
             // ---- online softmax of column j over this lane's 16 tokens ----
-            float sc[16]; // [8h + v]: token 32h + 8g + v
+            // Scores in log2 units are s * c2s (c2s > 0).  The reference
+            // maximum m2 is raised only when a block's maximum passes it by
+            // more than kLazy, so most blocks leave O and l unscaled; every
+            // p = 2^(s c2s - m2 + kPExp) is then at most 2^(kPExp + kLazy).
+            float sv[16]; // [8h + v]: token 32h + 8g + v
 #pragma unroll
             for (int h = 0; h < 2; h++)
 #pragma unroll
                 for (int t = 0; t < 2; t++)
 #pragma unroll
                     for (int r = 0; r < 4; r++)
-                        sc[8 * h + 4 * t + r] = s[h][t][r] * c2s;
+                        sv[8 * h + 4 * t + r] = s[h][t][r];
             if (!(mask_c == ~0ull && base + kTB <= wave_full)) {
                 const uint32_t lm = (uint32_t)(mask_c >> (8 * g));
                 const uint32_t hm = (uint32_t)(mask_c >> (32 + 8 * g));
@@ -718,28 +725,22 @@ __global__ __launch_bounds__(256) void attn_prefill_lds(PrefillArgs a)
                     const int tl = 32 * (i / 8) + 8 * g + (i % 8);
                     const uint32_t bit = ((i < 8 ? lm : hm) >> (i % 8)) & 1u;
                     if (!(bit && base + tl < qlen))
-                        sc[i] = -INFINITY;
+                        sv[i] = -INFINITY;
                 }
             }
-            float mx = sc[0];
+            float mx = sv[0];
 #pragma unroll
             for (int i = 1; i < 16; i++)
-                mx = fmaxf(mx, sc[i]);
+                mx = fmaxf(mx, sv[i]);
             mx = fmaxf(mx, __shfl_xor(mx, 16));
             mx = fmaxf(mx, __shfl_xor(mx, 32));
-            const float mnew = fmaxf(m2, mx);
-            const float alpha = mnew == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m2 - mnew);
-            // p carries a factor 2^14 so that its lo half stays normal
-            const float msub = mnew == -INFINITY ? 0.0f : mnew - 14.0f;
-            m2 = mnew;
-            float p[16], ps = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                p[i] = __builtin_amdgcn_exp2f(sc[i] - msub);
-                ps += p[i];
-            }
-            lsum = lsum * alpha + ps;
-            if (__any(alpha != 1.0f)) {
+            mx *= c2s;
+            const bool grow = mx > m2 + kLazy;
+            if (__any(grow)) {
+                const float mref = grow ? mx : m2;
+                const float alpha = mref == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m2 - mref);
+                m2 = mref;
+                lsum *= alpha;
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
                     const float ar = __shfl(alpha, 4 * g + r);
@@ -747,6 +748,13 @@ __global__ __launch_bounds__(256) void attn_prefill_lds(PrefillArgs a)
                     for (int nb = 0; nb < NB; nb++)
                         o[nb][r] *= ar;
                 }
+            }
+            const float msub = m2 == -INFINITY ? 0.0f : m2 - kPExp;
+            float p[16];
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                p[i] = __builtin_amdgcn_exp2f(fmaf(sv[i], c2s, -msub));
+                lsum += p[i];
             }
 
             // ---- P * V, V operand: dimension 16nb + j, tokens 32h + 8g .. +7 ----
