@@ -14,9 +14,10 @@
 // fp16 hi + lo halves, so results keep float32 accuracy.
 //
 // q8_0 pages stay exact: int8 values are exact in fp16 (converted with a
-// byte permute: 0x64XX is 1024 + XX), the K block scale of each 32-wide
-// k-step multiplies that step's partial scores, and the V block scale of
-// each 32 dimensions is folded into P for the products of those dimensions.
+// byte permute: 0x64XX is 1024 + XX).  The LDS-staged kernel turns value x
+// scale into exact hi + lo half pairs; the direct kernel multiplies each
+// 32-wide k-step's partial scores by its K block scale and folds the V block
+// scale of each 32 dimensions into P for the products of those dimensions.
 #include "gi_common.h"
 #include "gi_kernels.h"
 
@@ -417,9 +418,10 @@ __global__ __launch_bounds__(256) void attn_prefill(PrefillArgs a)
 
 
 // ---------------------------------------------------------------------------
-// LDS-staged form (page size dividing 64).  A workgroup owns 64 (query, head)
-// columns of one kv head -- 16 per wave -- and streams the context in 64-token
-// blocks through LDS: all 256 threads load a block with one 16-byte global
+// LDS-staged form (pages of 16, 32 or 64 tokens).  A workgroup owns 4 x 16 x
+// NCG (query, head) columns of one kv head -- NCG groups of 16 per wave, so
+// each operand read from LDS feeds 2 NCG (q8_0: 3 NCG) products -- and streams
+// the context in 64-token blocks through LDS: all 256 threads load a block with one 16-byte global
 // load per chunk, convert it, and store it; every wave then reads its MFMA
 // operands from LDS.  The next block's global loads are in flight while the
 // current block is computed.
@@ -430,11 +432,10 @@ __global__ __launch_bounds__(256) void attn_prefill(PrefillArgs a)
 // ballot of the same register marks the block's tokens that are cached and on
 // a valid page.
 //
-// q8_0 V is dequantised while staging into an exact pair of fp16 halves:
-// hi = fp16(q * s) and lo = fma(q, s, -hi), whose exact value fits a half
-// because q * s has at most 19 significant bits.  P * V then takes three
-// products (P_hi V_hi, P_lo V_hi, P_hi V_lo).  The K block scale multiplies
-// the partial scores of its 32-wide k-step.
+// q8_0 K and V are dequantised while staging into exact pairs of fp16
+// halves: hi = fp16(q * s) and lo = fma(q, s, -hi), whose exact value fits a
+// half because q * s has at most 19 significant bits.  Q K^T and P V then take
+// three products each (hi x hi, lo x hi, hi x lo).
 constexpr int kTB = 64; // tokens per staged block
 // Online softmax: p = 2^(score - m + kPExp) with the reference maximum m
 // lagging the true one by at most kLazy, so p <= 2^14 stays well inside fp16.
@@ -446,17 +447,18 @@ struct StageRegs {
     // elements, or int8 K rows / V columns of 16 elements.
     static constexpr int NC = KT == KV_F16 ? HD / 32 : HD / 64;
     u4 k[NC], v[NC];
-    u4 vs[KT == KV_Q8_0 ? 2 * NC : 1]; // q8_0: the 16 V scales of each V chunk
-    uint32_t ks[HD / 64];              // q8_0: K scales of token tid (tid < 64)
+    int64_t kpage[KT == KV_Q8_0 ? NC : 1]; // q8_0: page of each chunk (wave-uniform)
+    int64_t vpage[KT == KV_Q8_0 ? NC : 1];
 };
 
+// q8_0 K and V are stored dequantised as exact hi + lo fp16 pairs.
 template <int HD, int KT, int NBUF>
 struct Lds {
     static constexpr bool Q8 = KT == KV_Q8_0;
     __attribute__((aligned(16))) _Float16 k[NBUF][kTB][HD + 8];  // token-major K, rows padded
-    __attribute__((aligned(16))) _Float16 v[NBUF][HD][kTB + 8];  // dimension-major V (q8_0: hi)
+    __attribute__((aligned(16))) _Float16 v[NBUF][HD][kTB + 8];  // dimension-major V
+    __attribute__((aligned(16))) _Float16 kl[Q8 ? NBUF : 1][Q8 ? kTB : 1][HD + 8]; // q8_0: K lo
     __attribute__((aligned(16))) _Float16 vl[Q8 ? NBUF : 1][Q8 ? HD : 1][kTB + 8]; // q8_0: V lo
-    __attribute__((aligned(16))) float ksc[Q8 ? NBUF : 1][kTB][HD / 32];            // q8_0: K scales
 };
 
 // Chunk -> (token, column) of K and (page segment, dimension, token group)
@@ -506,31 +508,48 @@ __device__ __forceinline__ void stage_load(const PrefillArgs &a, int kvh, int ti
         } else {
             R.k[c] = *reinterpret_cast<const u4 *>(kp + ((int64_t)kvh * P + tk % P) * HD + M::k_col(ch));
             R.v[c] = *reinterpret_cast<const u4 *>(vp + L.v_off + ((int64_t)kvh * HD + d) * P + tv);
-            const u4 *sp = reinterpret_cast<const u4 *>(
-                vp + L.vs_off + (((int64_t)kvh * (HD / 32) + d / 32) * P + tv) * 2);
-            R.vs[2 * c] = sp[0];
-            R.vs[2 * c + 1] = sp[1];
+            R.kpage[c] = page(M::k_tok(ch0));
+            R.vpage[c] = page(M::v_seg(ch0) * P);
         }
     }
-    if (KT == KV_Q8_0 && w == 0) {
-        // lane tid holds the page of block token tid
-        const int64_t pg = (tb >= 0 && tb < np) ? tb : 0;
-        const uint32_t *src = reinterpret_cast<const uint32_t *>(
-            a.base + pg * L.page_bytes + L.ks_off + ((int64_t)kvh * P + tid % P) * (HD / 32) * 2);
-#pragma unroll
-        for (int i = 0; i < HD / 64; i++)
-            R.ks[i] = src[i];
-    }
+}
+
+// q8_0 element pairs: hi = fp16(q * s), lo = fma(q, s, -hi).  q * s has at
+// most 19 significant bits, so lo holds the rest exactly and hi + lo == q * s.
+__device__ __forceinline__ void dequant_pair(h8 q, h8 s, h8 &hi, h8 &lo)
+{
+    hi = q * s;
+    lo = __builtin_elementwise_fma(q, s, -hi);
 }
 
 // Converts and stores a staged block.  `vmask` bit l: block token l is cached
 // and on a valid page; V of other tokens is stored as zero (their scores are
 // masked, and stale values must not reach O through 0 * NaN).
 template <int HD, int KT, int P, int NBUF>
-__device__ __forceinline__ void stage_store(int tid, int w, int buf, uint64_t vmask,
-                                            const StageRegs<HD, KT> &R, Lds<HD, KT, NBUF> &S)
+__device__ __forceinline__ void stage_store(const PrefillArgs &a, int kvh, int tid, int w, int buf,
+                                            uint64_t vmask, const StageRegs<HD, KT> &R,
+                                            Lds<HD, KT, NBUF> &S)
 {
     using M = ChunkMap<HD, KT, P>;
+    // q8_0 block scales: one per K chunk, 16 per V chunk.  Loaded here rather
+    // than with the chunk so that they hold no registers through the block's
+    // compute (they are shared by many chunks and come from the caches).
+    constexpr int NCS = KT == KV_Q8_0 ? StageRegs<HD, KT>::NC : 1;
+    u4 vs[2 * NCS];
+    _Float16 ks[NCS];
+    if (KT == KV_Q8_0) {
+#pragma unroll
+        for (int c = 0; c < R.NC; c++) {
+            const int ch = tid + 256 * c;
+            const u4 *sp = reinterpret_cast<const u4 *>(
+                a.base + R.vpage[c] * a.L.page_bytes + a.L.vs_off +
+                (((int64_t)kvh * (HD / 32) + M::v_dim(ch) / 32) * P + M::v_tok(ch)) * 2);
+            vs[2 * c] = sp[0];
+            vs[2 * c + 1] = sp[1];
+            ks[c] = reinterpret_cast<const _Float16 *>(a.base + R.kpage[c] * a.L.page_bytes + a.L.ks_off)
+                [((int64_t)kvh * P + M::k_tok(ch) % P) * (HD / 32) + M::k_col(ch) / 32];
+        }
+    }
 #pragma unroll
     for (int c = 0; c < R.NC; c++) {
         const int ch = tid + 256 * c;
@@ -548,14 +567,19 @@ __device__ __forceinline__ void stage_store(int tid, int w, int buf, uint64_t vm
             }
             *reinterpret_cast<u4 *>(&S.v[buf][d][t0]) = vv;
         } else {
-            *reinterpret_cast<h8 *>(&S.k[buf][tk][col]) = i8x8_to_h8(uint2{R.k[c][0], R.k[c][1]});
-            *reinterpret_cast<h8 *>(&S.k[buf][tk][col + 8]) = i8x8_to_h8(uint2{R.k[c][2], R.k[c][3]});
+            const h8 ksp = ks[c]; // splat
 #pragma unroll
             for (int half = 0; half < 2; half++) {
-                const h8 q = i8x8_to_h8(uint2{R.v[c][2 * half], R.v[c][2 * half + 1]});
-                const h8 s = __builtin_bit_cast(h8, R.vs[2 * c + half]);
-                h8 hi = q * s;
-                h8 lo = __builtin_elementwise_fma(q, s, -hi);
+                h8 hi, lo;
+                dequant_pair(i8x8_to_h8(uint2{R.k[c][2 * half], R.k[c][2 * half + 1]}), ksp, hi, lo);
+                *reinterpret_cast<h8 *>(&S.k[buf][tk][col + 8 * half]) = hi;
+                *reinterpret_cast<h8 *>(&S.kl[buf][tk][col + 8 * half]) = lo;
+            }
+#pragma unroll
+            for (int half = 0; half < 2; half++) {
+                h8 hi, lo;
+                dequant_pair(i8x8_to_h8(uint2{R.v[c][2 * half], R.v[c][2 * half + 1]}),
+                             __builtin_bit_cast(h8, vs[2 * c + half]), hi, lo);
                 const uint32_t lv = live >> (8 * half);
                 if ((lv & 0xFFu) != 0xFFu) {
 #pragma unroll
@@ -570,20 +594,13 @@ __device__ __forceinline__ void stage_store(int tid, int w, int buf, uint64_t vm
             }
         }
     }
-    if (KT == KV_Q8_0 && w == 0) {
-#pragma unroll
-        for (int i = 0; i < HD / 64; i++) {
-            const h2 s = __builtin_bit_cast(h2, R.ks[i]);
-            S.ksc[buf][tid][2 * i] = (float)s[0];
-            S.ksc[buf][tid][2 * i + 1] = (float)s[1];
-        }
-    }
 }
 
-template <int HD, int KT, int P, int NBUF>
+template <int HD, int KT, int P, int NBUF, int NCG>
 __global__ __launch_bounds__(256) void attn_prefill_lds(PrefillArgs a)
 {
     constexpr int KK = HD / 32, NB = HD / 16;
+    constexpr int WCOLS = 16 * NCG; // (query, head) columns per wave
     const PoolLayout &L = a.L;
     // heaviest (latest-query) workgroups first
     const int wx = gridDim.x - 1 - blockIdx.x;
@@ -599,20 +616,25 @@ __global__ __launch_bounds__(256) void attn_prefill_lds(PrefillArgs a)
 
     __shared__ Lds<HD, KT, NBUF> S;
 
-    const int col0 = (wx * 4 + w) * 16;
-    const int qlen = min(start + min((col0 + j) / G, chunk - 1) + 1, mapped);
-    const int wave_len = min(start + min((col0 + 15) / G, chunk - 1) + 1, mapped);
+    // column group cg of this wave: columns col0 + 16 cg .. + 15
+    const int col0 = (wx * 4 + w) * WCOLS;
+    int qlen[NCG];
+#pragma unroll
+    for (int cg = 0; cg < NCG; cg++)
+        qlen[cg] = min(start + min((col0 + 16 * cg + j) / G, chunk - 1) + 1, mapped);
+    const int wave_len = min(start + min((col0 + WCOLS - 1) / G, chunk - 1) + 1, mapped);
     const int wave_full = min(start + col0 / G + 1, mapped); // shortest column of the wave
     if (start + chunk > mapped && tid == 0 && a.status)
         atomicOr(a.status, FLAG_BAD_SLOT);
-    const int wg_len = min(start + min((wx * 64 + 63) / G, chunk - 1) + 1, mapped);
+    const int wg_len = min(start + min((wx * 4 * WCOLS + 4 * WCOLS - 1) / G, chunk - 1) + 1, mapped);
     const bool wave_active = col0 / G < chunk;
 
     // Q^T operands (hi, lo) scaled per column by 2^qe.
-    h8 qh[KK], ql[KK];
-    float c2s;
-    {
-        const int c = col0 + j;
+    h8 qh[NCG][KK], ql[NCG][KK];
+    float c2s[NCG];
+#pragma unroll
+    for (int cg = 0; cg < NCG; cg++) {
+        const int c = col0 + 16 * cg + j;
         const int qi = min(c / G, chunk - 1);
         const float *qp = a.q + (((int64_t)b * chunk + qi) * H + kvh * G + c % G) * HD;
         float qv[KK][8];
@@ -628,22 +650,27 @@ __global__ __launch_bounds__(256) void attn_prefill_lds(PrefillArgs a)
         mq = fmaxf(mq, __shfl_xor(mq, 32));
         const int qe = pow2_exponent_for(mq);
         const float up = ldexpf(1.0f, qe);
-        c2s = a.scale * kLog2e * ldexpf(1.0f, -qe);
+        c2s[cg] = a.scale * kLog2e * ldexpf(1.0f, -qe);
 #pragma unroll
         for (int kk = 0; kk < KK; kk++) {
             float x[8];
 #pragma unroll
             for (int v = 0; v < 8; v++)
                 x[v] = qv[kk][v] * up;
-            split8(x, qh[kk], ql[kk]);
+            split8(x, qh[cg][kk], ql[cg][kk]);
         }
     }
 
-    float m2 = -INFINITY, lsum = 0.0f;
-    f4 o[NB];
+    float m2[NCG], lsum[NCG];
+    f4 o[NCG][NB];
 #pragma unroll
-    for (int nb = 0; nb < NB; nb++)
-        o[nb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int cg = 0; cg < NCG; cg++) {
+        m2[cg] = -INFINITY;
+        lsum[cg] = 0.0f;
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++)
+            o[cg][nb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
 
     auto valid_mask = [&](int tb, int base) -> uint64_t {
         const bool bad = base + lane < wg_len && !(tb >= 0 && tb < L.num_pages);
@@ -657,7 +684,7 @@ __global__ __launch_bounds__(256) void attn_prefill_lds(PrefillArgs a)
     uint64_t mask_c = valid_mask(tb, 0);
     stage_load<HD, KT, P>(a, kvh, tid, w, tb, R);
     tb = table_entry<P>(bt, kTB + lane, wg_len);
-    stage_store<HD, KT, P, NBUF>(tid, w, 0, mask_c, R, S);
+    stage_store<HD, KT, P, NBUF>(a, kvh, tid, w, 0, mask_c, R, S);
     __syncthreads();
 
     for (int base = 0, it = 0; base < wg_len; base += kTB, it++) {
@@ -672,104 +699,107 @@ __global__ __launch_bounds__(256) void attn_prefill_lds(PrefillArgs a)
 
         if (wave_active && base < wave_len) {
             // ---- scores: tiles (h, t), row j = token 32h + 8(j/4) + j%4 + 4t ----
-            f4 s[2][2];
+            f4 s[NCG][2][2];
 #pragma unroll
             for (int h = 0; h < 2; h++)
 #pragma unroll
                 for (int t = 0; t < 2; t++) {
-                    s[h][t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int cg = 0; cg < NCG; cg++)
+                        s[cg][h][t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
                     const int row = 32 * h + 8 * (j >> 2) + (j & 3) + 4 * t;
-                    float ks[4][KK]; // q8_0: K scales of output row token 32h + 8g + 4t + r
-                    if (KT == KV_Q8_0) {
-#pragma unroll
-                        for (int r = 0; r < 4; r++)
-#pragma unroll
-                            for (int kk = 0; kk < KK; kk++)
-                                ks[r][kk] = S.ksc[buf][32 * h + 8 * g + 4 * t + r][kk];
-                    }
 #pragma unroll
                     for (int kk = 0; kk < KK; kk++) {
                         const h8 ka = *reinterpret_cast<const h8 *>(&S.k[buf][row][32 * kk + 8 * g]);
-                        if (KT == KV_F16) {
-                            s[h][t] = mfma(ka, qh[kk], s[h][t]);
-                            s[h][t] = mfma(ka, ql[kk], s[h][t]);
-                        } else {
-                            f4 z = {0.0f, 0.0f, 0.0f, 0.0f};
-                            z = mfma(ka, qh[kk], z);
-                            z = mfma(ka, ql[kk], z);
+                        h8 kl;
+                        if (KT == KV_Q8_0)
+                            kl = *reinterpret_cast<const h8 *>(&S.kl[buf][row][32 * kk + 8 * g]);
 #pragma unroll
-                            for (int r = 0; r < 4; r++)
-                                s[h][t][r] = fmaf(z[r], ks[r][kk], s[h][t][r]);
+                        for (int cg = 0; cg < NCG; cg++) {
+                            s[cg][h][t] = mfma(ka, qh[cg][kk], s[cg][h][t]);
+                            s[cg][h][t] = mfma(ka, ql[cg][kk], s[cg][h][t]);
+                            if (KT == KV_Q8_0)
+                                s[cg][h][t] = mfma(kl, qh[cg][kk], s[cg][h][t]);
                         }
                     }
                 }
 
-            // ---- online softmax of column j over this lane's 16 tokens ----
+            // ---- online softmax of column 16 cg + j over this lane's 16 tokens ----
             // Scores in log2 units are s * c2s (c2s > 0).  The reference
             // maximum m2 is raised only when a block's maximum passes it by
             // more than kLazy, so most blocks leave O and l unscaled; every
             // p = 2^(s c2s - m2 + kPExp) is then at most 2^(kPExp + kLazy).
-            float sv[16]; // [8h + v]: token 32h + 8g + v
+            const bool full = mask_c == ~0ull && base + kTB <= wave_full;
+            float p[NCG][16]; // [8h + v]: token 32h + 8g + v
 #pragma unroll
-            for (int h = 0; h < 2; h++)
+            for (int cg = 0; cg < NCG; cg++) {
+                float sv[16];
 #pragma unroll
-                for (int t = 0; t < 2; t++)
+                for (int h = 0; h < 2; h++)
 #pragma unroll
-                    for (int r = 0; r < 4; r++)
-                        sv[8 * h + 4 * t + r] = s[h][t][r];
-            if (!(mask_c == ~0ull && base + kTB <= wave_full)) {
-                const uint32_t lm = (uint32_t)(mask_c >> (8 * g));
-                const uint32_t hm = (uint32_t)(mask_c >> (32 + 8 * g));
+                    for (int t = 0; t < 2; t++)
+#pragma unroll
+                        for (int r = 0; r < 4; r++)
+                            sv[8 * h + 4 * t + r] = s[cg][h][t][r];
+                if (!full) {
+                    const uint32_t lm = (uint32_t)(mask_c >> (8 * g));
+                    const uint32_t hm = (uint32_t)(mask_c >> (32 + 8 * g));
+#pragma unroll
+                    for (int i = 0; i < 16; i++) {
+                        const int tl = 32 * (i / 8) + 8 * g + (i % 8);
+                        const uint32_t bit = ((i < 8 ? lm : hm) >> (i % 8)) & 1u;
+                        if (!(bit && base + tl < qlen[cg]))
+                            sv[i] = -INFINITY;
+                    }
+                }
+                float mx = sv[0];
+#pragma unroll
+                for (int i = 1; i < 16; i++)
+                    mx = fmaxf(mx, sv[i]);
+                mx = fmaxf(mx, __shfl_xor(mx, 16));
+                mx = fmaxf(mx, __shfl_xor(mx, 32));
+                mx *= c2s[cg];
+                const bool grow = mx > m2[cg] + kLazy;
+                if (__any(grow)) {
+                    const float mref = grow ? mx : m2[cg];
+                    const float alpha = mref == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m2[cg] - mref);
+                    m2[cg] = mref;
+                    lsum[cg] *= alpha;
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const float ar = __shfl(alpha, 4 * g + r);
+#pragma unroll
+                        for (int nb = 0; nb < NB; nb++)
+                            o[cg][nb][r] *= ar;
+                    }
+                }
+                const float msub = m2[cg] == -INFINITY ? 0.0f : m2[cg] - kPExp;
 #pragma unroll
                 for (int i = 0; i < 16; i++) {
-                    const int tl = 32 * (i / 8) + 8 * g + (i % 8);
-                    const uint32_t bit = ((i < 8 ? lm : hm) >> (i % 8)) & 1u;
-                    if (!(bit && base + tl < qlen))
-                        sv[i] = -INFINITY;
+                    p[cg][i] = __builtin_amdgcn_exp2f(fmaf(sv[i], c2s[cg], -msub));
+                    lsum[cg] += p[cg][i];
                 }
-            }
-            float mx = sv[0];
-#pragma unroll
-            for (int i = 1; i < 16; i++)
-                mx = fmaxf(mx, sv[i]);
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            mx *= c2s;
-            const bool grow = mx > m2 + kLazy;
-            if (__any(grow)) {
-                const float mref = grow ? mx : m2;
-                const float alpha = mref == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m2 - mref);
-                m2 = mref;
-                lsum *= alpha;
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const float ar = __shfl(alpha, 4 * g + r);
-#pragma unroll
-                    for (int nb = 0; nb < NB; nb++)
-                        o[nb][r] *= ar;
-                }
-            }
-            const float msub = m2 == -INFINITY ? 0.0f : m2 - kPExp;
-            float p[16];
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                p[i] = __builtin_amdgcn_exp2f(fmaf(sv[i], c2s, -msub));
-                lsum += p[i];
             }
 
             // ---- P * V, V operand: dimension 16nb + j, tokens 32h + 8g .. +7 ----
 #pragma unroll
             for (int h = 0; h < 2; h++) {
-                h8 ph, pl;
-                split8(&p[8 * h], ph, pl);
+                h8 ph[NCG], pl[NCG];
+#pragma unroll
+                for (int cg = 0; cg < NCG; cg++)
+                    split8(&p[cg][8 * h], ph[cg], pl[cg]);
 #pragma unroll
                 for (int nb = 0; nb < NB; nb++) {
                     const h8 vb = *reinterpret_cast<const h8 *>(&S.v[buf][16 * nb + j][32 * h + 8 * g]);
-                    o[nb] = mfma(ph, vb, o[nb]);
-                    o[nb] = mfma(pl, vb, o[nb]);
-                    if (KT == KV_Q8_0) {
-                        const h8 vl = *reinterpret_cast<const h8 *>(&S.vl[buf][16 * nb + j][32 * h + 8 * g]);
-                        o[nb] = mfma(ph, vl, o[nb]);
+                    h8 vl;
+                    if (KT == KV_Q8_0)
+                        vl = *reinterpret_cast<const h8 *>(&S.vl[buf][16 * nb + j][32 * h + 8 * g]);
+#pragma unroll
+                    for (int cg = 0; cg < NCG; cg++) {
+                        o[cg][nb] = mfma(ph[cg], vb, o[cg][nb]);
+                        o[cg][nb] = mfma(pl[cg], vb, o[cg][nb]);
+                        if (KT == KV_Q8_0)
+                            o[cg][nb] = mfma(ph[cg], vl, o[cg][nb]);
                     }
                 }
             }
@@ -778,7 +808,7 @@ __global__ __launch_bounds__(256) void attn_prefill_lds(PrefillArgs a)
         if (more) {
             if (NBUF == 1)
                 __syncthreads();
-            stage_store<HD, KT, P, NBUF>(tid, w, NBUF == 2 ? (buf ^ 1) : 0, mask_n, R, S);
+            stage_store<HD, KT, P, NBUF>(a, kvh, tid, w, NBUF == 2 ? (buf ^ 1) : 0, mask_n, R, S);
         }
         mask_c = mask_n;
         __syncthreads();
@@ -786,21 +816,24 @@ __global__ __launch_bounds__(256) void attn_prefill_lds(PrefillArgs a)
 
     if (!wave_active)
         return;
-    float lt = lsum;
-    lt += __shfl_xor(lt, 16);
-    lt += __shfl_xor(lt, 32);
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const float l = __shfl(lt, 4 * g + r);
-        const int c = col0 + 4 * g + r;
-        const int qi = c / G;
-        if (qi >= chunk)
-            continue;
-        float *op = a.out + (((int64_t)b * chunk + qi) * H + kvh * G + c % G) * HD;
-        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    for (int cg = 0; cg < NCG; cg++) {
+        float lt = lsum[cg];
+        lt += __shfl_xor(lt, 16);
+        lt += __shfl_xor(lt, 32);
 #pragma unroll
-        for (int nb = 0; nb < NB; nb++)
-            op[16 * nb + j] = o[nb][r] * inv;
+        for (int r = 0; r < 4; r++) {
+            const float l = __shfl(lt, 4 * g + r);
+            const int c = col0 + 16 * cg + 4 * g + r;
+            const int qi = c / G;
+            if (qi >= chunk)
+                continue;
+            float *op = a.out + (((int64_t)b * chunk + qi) * H + kvh * G + c % G) * HD;
+            const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+#pragma unroll
+            for (int nb = 0; nb < NB; nb++)
+                op[16 * nb + j] = o[cg][nb][r] * inv;
+        }
     }
 }
 
@@ -837,22 +870,44 @@ constexpr int prefill_ncg()
 #define GI_PREFILL_NBUF_Q8 1
 #endif
 
+// Column groups per wave: two halve the LDS reads per matrix-core product;
+// taken where the kernel then still fits two waves per SIMD (256 VGPRs).
+template <int HD, int KT, int P>
+constexpr int prefill_lds_ncg()
+{
+#ifdef GI_PREFILL_NCG
+    return GI_PREFILL_NCG;
+#else
+    return (HD == 64 || P == 16 || (KT == KV_Q8_0 && P == 32)) ? 2 : 1;
+#endif
+}
+
 template <int HD, int KT>
-static void launch_lds(const PrefillArgs &a, dim3 grid, hipStream_t st)
+static void launch_lds(const PrefillArgs &a, hipStream_t st)
 {
     using namespace mfma_prefill;
     constexpr int NBUF = KT == KV_F16 ? GI_PREFILL_NBUF_F16 : GI_PREFILL_NBUF_Q8;
+    const int G = a.num_heads / a.L.num_kv_heads;
+    const int64_t cols = (int64_t)a.chunk_len * G;
+    auto grid = [&](int ncg) {
+        const int64_t per_wg = 4 * 16 * ncg;
+        return dim3((unsigned)((cols + per_wg - 1) / per_wg), a.L.num_kv_heads, a.batch);
+    };
+#define GI_PFL(PT)                                                                           \
+    hipLaunchKernelGGL((attn_prefill_lds<HD, KT, PT, NBUF, prefill_lds_ncg<HD, KT, PT>()>), \
+                       grid(prefill_lds_ncg<HD, KT, PT>()), dim3(256), 0, st, a)
     switch (a.L.page_tokens) {
     case 16:
-        hipLaunchKernelGGL((attn_prefill_lds<HD, KT, 16, NBUF>), grid, dim3(256), 0, st, a);
+        GI_PFL(16);
         break;
     case 32:
-        hipLaunchKernelGGL((attn_prefill_lds<HD, KT, 32, NBUF>), grid, dim3(256), 0, st, a);
+        GI_PFL(32);
         break;
     default:
-        hipLaunchKernelGGL((attn_prefill_lds<HD, KT, 64, NBUF>), grid, dim3(256), 0, st, a);
+        GI_PFL(64);
         break;
     }
+#undef GI_PFL
 }
 
 hipError_t launch_prefill_mfma(const PrefillArgs &a, hipStream_t st)
@@ -862,17 +917,16 @@ hipError_t launch_prefill_mfma(const PrefillArgs &a, hipStream_t st)
     const int64_t cols = (int64_t)a.chunk_len * G;
     const int P = a.L.page_tokens;
     if (P == 16 || P == 32 || P == 64) {
-        dim3 grid((unsigned)((cols + 63) / 64), a.L.num_kv_heads, a.batch);
         if (a.L.head_dim == 128) {
             if (a.L.kv_type == KV_F16)
-                launch_lds<128, KV_F16>(a, grid, st);
+                launch_lds<128, KV_F16>(a, st);
             else
-                launch_lds<128, KV_Q8_0>(a, grid, st);
+                launch_lds<128, KV_Q8_0>(a, st);
         } else {
             if (a.L.kv_type == KV_F16)
-                launch_lds<64, KV_F16>(a, grid, st);
+                launch_lds<64, KV_F16>(a, st);
             else
-                launch_lds<64, KV_Q8_0>(a, grid, st);
+                launch_lds<64, KV_Q8_0>(a, st);
         }
         return hipGetLastError();
     }
