@@ -596,245 +596,440 @@ __device__ __forceinline__ void stage_store(const PrefillArgs &a, int kvh, int t
     }
 }
 
-template <int HD, int KT, int P, int NBUF, int NCG>
-__global__ __launch_bounds__(256) void attn_prefill_lds(PrefillArgs a)
+// Fragment accessors of the register-staged layout (rows padded by 16 bytes).
+template <int HD, int KT, int NBUF>
+__device__ __forceinline__ h8 k_frag(const Lds<HD, KT, NBUF> &S, int buf, int row, int c)
 {
-    constexpr int KK = HD / 32, NB = HD / 16;
-    constexpr int WCOLS = 16 * NCG; // (query, head) columns per wave
-    const PoolLayout &L = a.L;
-    // heaviest (latest-query) workgroups first
-    const int wx = gridDim.x - 1 - blockIdx.x;
-    const int kvh = blockIdx.y, b = blockIdx.z;
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int j = lane & 15, g = lane >> 4;
-    const int H = a.num_heads, G = H / L.num_kv_heads;
-    const int start = a.start_pos[b];
-    const int chunk = a.chunk_len;
-    const int32_t *bt = a.block_tables + (int64_t)b * a.max_blocks;
-    const int mapped = a.max_blocks * P;
+    return *reinterpret_cast<const h8 *>(&S.k[buf][row][8 * c]);
+}
+template <int HD, int KT, int NBUF>
+__device__ __forceinline__ h8 kl_frag(const Lds<HD, KT, NBUF> &S, int buf, int row, int c)
+{
+    return *reinterpret_cast<const h8 *>(&S.kl[buf][row][8 * c]);
+}
+template <int HD, int KT, int NBUF>
+__device__ __forceinline__ h8 v_frag(const Lds<HD, KT, NBUF> &S, int buf, int d, int c)
+{
+    return *reinterpret_cast<const h8 *>(&S.v[buf][d][8 * c]);
+}
+template <int HD, int KT, int NBUF>
+__device__ __forceinline__ h8 vl_frag(const Lds<HD, KT, NBUF> &S, int buf, int d, int c)
+{
+    return *reinterpret_cast<const h8 *>(&S.vl[buf][d][8 * c]);
+}
 
-    __shared__ Lds<HD, KT, NBUF> S;
+// Layout written by direct global->LDS loads (fp16 pages).  One load
+// instruction fills 1 KiB of LDS with its lanes' 16 bytes in lane order, so
+// rows are unpadded; 16-byte chunks are XOR-swizzled inside each row instead,
+// which keeps the MFMA operand reads of 8 consecutive lanes on distinct banks.
+template <int HD>
+struct LdsDirect {
+    __attribute__((aligned(16))) _Float16 k[2][kTB * HD]; // [token][HD], chunk c at c ^ kswz(token)
+    __attribute__((aligned(16))) _Float16 v[2][HD * kTB]; // [dim][kTB], chunk c at c ^ (dim & 7)
+    __device__ static int kswz(int row) { return ((row & 3) | (((row >> 3) & 3) << 2)) & (HD / 8 - 1); }
+};
+template <int HD>
+__device__ __forceinline__ h8 k_frag(const LdsDirect<HD> &S, int buf, int row, int c)
+{
+    return *reinterpret_cast<const h8 *>(&S.k[buf][row * HD + 8 * (c ^ LdsDirect<HD>::kswz(row))]);
+}
+template <int HD>
+__device__ __forceinline__ h8 kl_frag(const LdsDirect<HD> &, int, int, int)
+{
+    return h8{};
+}
+template <int HD>
+__device__ __forceinline__ h8 v_frag(const LdsDirect<HD> &S, int buf, int d, int c)
+{
+    return *reinterpret_cast<const h8 *>(&S.v[buf][d * kTB + 8 * (c ^ (d & 7))]);
+}
+template <int HD>
+__device__ __forceinline__ h8 vl_frag(const LdsDirect<HD> &, int, int, int)
+{
+    return h8{};
+}
 
-    // column group cg of this wave: columns col0 + 16 cg .. + 15
-    const int col0 = (wx * 4 + w) * WCOLS;
-    int qlen[NCG];
-#pragma unroll
-    for (int cg = 0; cg < NCG; cg++)
-        qlen[cg] = min(start + min((col0 + 16 * cg + j) / G, chunk - 1) + 1, mapped);
-    const int wave_len = min(start + min((col0 + WCOLS - 1) / G, chunk - 1) + 1, mapped);
-    const int wave_full = min(start + col0 / G + 1, mapped); // shortest column of the wave
-    if (start + chunk > mapped && tid == 0 && a.status)
-        atomicOr(a.status, FLAG_BAD_SLOT);
-    const int wg_len = min(start + min((wx * 4 * WCOLS + 4 * WCOLS - 1) / G, chunk - 1) + 1, mapped);
-    const bool wave_active = col0 / G < chunk;
-
-    // Q^T operands (hi, lo) scaled per column by 2^qe.
+// Per-wave attention state over NCG column groups of 16 (query, head)
+// columns: Q^T operands, running maximum and sum, and the O accumulators.
+template <int HD, int KT, int NCG>
+struct WaveAttn {
+    static constexpr int KK = HD / 32, NB = HD / 16;
     h8 qh[NCG][KK], ql[NCG][KK];
-    float c2s[NCG];
-#pragma unroll
-    for (int cg = 0; cg < NCG; cg++) {
-        const int c = col0 + 16 * cg + j;
-        const int qi = min(c / G, chunk - 1);
-        const float *qp = a.q + (((int64_t)b * chunk + qi) * H + kvh * G + c % G) * HD;
-        float qv[KK][8];
-        float mq = 0.0f;
-#pragma unroll
-        for (int kk = 0; kk < KK; kk++)
-#pragma unroll
-            for (int v = 0; v < 8; v++) {
-                qv[kk][v] = wave_active ? qp[32 * kk + 8 * g + v] : 0.0f;
-                mq = fmaxf(mq, fabsf(qv[kk][v]));
-            }
-        mq = fmaxf(mq, __shfl_xor(mq, 16));
-        mq = fmaxf(mq, __shfl_xor(mq, 32));
-        const int qe = pow2_exponent_for(mq);
-        const float up = ldexpf(1.0f, qe);
-        c2s[cg] = a.scale * kLog2e * ldexpf(1.0f, -qe);
-#pragma unroll
-        for (int kk = 0; kk < KK; kk++) {
-            float x[8];
-#pragma unroll
-            for (int v = 0; v < 8; v++)
-                x[v] = qv[kk][v] * up;
-            split8(x, qh[cg][kk], ql[cg][kk]);
-        }
-    }
-
-    float m2[NCG], lsum[NCG];
+    float c2s[NCG], m2[NCG], lsum[NCG];
     f4 o[NCG][NB];
+    int qlen[NCG];
+
+    // Loads Q of columns col0 + 16 cg + j, split into hi + lo halves scaled
+    // per column by 2^qe.
+    __device__ __forceinline__ void init(const PrefillArgs &a, int b, int kvh, int col0, int start,
+                                         int mapped, bool active, int j, int g)
+    {
+        const int H = a.num_heads, G = H / a.L.num_kv_heads, chunk = a.chunk_len;
 #pragma unroll
-    for (int cg = 0; cg < NCG; cg++) {
-        m2[cg] = -INFINITY;
-        lsum[cg] = 0.0f;
+        for (int cg = 0; cg < NCG; cg++) {
+            const int c = col0 + 16 * cg + j;
+            const int qi = min(c / G, chunk - 1);
+            qlen[cg] = min(start + qi + 1, mapped);
+            const float *qp = a.q + (((int64_t)b * chunk + qi) * H + kvh * G + c % G) * HD;
+            float qv[KK][8];
+            float mq = 0.0f;
 #pragma unroll
-        for (int nb = 0; nb < NB; nb++)
-            o[cg][nb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int kk = 0; kk < KK; kk++)
+#pragma unroll
+                for (int v = 0; v < 8; v++) {
+                    qv[kk][v] = active ? qp[32 * kk + 8 * g + v] : 0.0f;
+                    mq = fmaxf(mq, fabsf(qv[kk][v]));
+                }
+            mq = fmaxf(mq, __shfl_xor(mq, 16));
+            mq = fmaxf(mq, __shfl_xor(mq, 32));
+            const int qe = pow2_exponent_for(mq);
+            const float up = ldexpf(1.0f, qe);
+            c2s[cg] = a.scale * kLog2e * ldexpf(1.0f, -qe);
+#pragma unroll
+            for (int kk = 0; kk < KK; kk++) {
+                float x[8];
+#pragma unroll
+                for (int v = 0; v < 8; v++)
+                    x[v] = qv[kk][v] * up;
+                split8(x, qh[cg][kk], ql[cg][kk]);
+            }
+            m2[cg] = -INFINITY;
+            lsum[cg] = 0.0f;
+#pragma unroll
+            for (int nb = 0; nb < NB; nb++)
+                o[cg][nb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
     }
 
-    auto valid_mask = [&](int tb, int base) -> uint64_t {
-        const bool bad = base + lane < wg_len && !(tb >= 0 && tb < L.num_pages);
-        if (__ballot(bad) && w == 0 && lane == 0 && a.status)
-            atomicOr(a.status, FLAG_BAD_PAGE);
-        return __ballot(tb >= 0 && tb < L.num_pages);
-    };
+    // One 64-token block from LDS buffer `buf`.  `mask` bit l: block token l
+    // is cached and on a valid page; `full`: every token of the block is
+    // valid for every column of the wave (no masking needed).
+    template <class LDS>
+    __device__ __forceinline__ void block(const LDS &S, int buf, int base, uint64_t mask, bool full,
+                                          int j, int g)
+    {
+        // ---- scores: tiles (h, t), row j = token 32h + 8(j/4) + j%4 + 4t ----
+        f4 s[NCG][2][2];
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+#pragma unroll
+                for (int cg = 0; cg < NCG; cg++)
+                    s[cg][h][t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+                const int row = 32 * h + 8 * (j >> 2) + (j & 3) + 4 * t;
+#pragma unroll
+                for (int kk = 0; kk < KK; kk++) {
+                    const h8 ka = k_frag(S, buf, row, 4 * kk + g);
+                    h8 kl;
+                    if (KT == KV_Q8_0)
+                        kl = kl_frag(S, buf, row, 4 * kk + g);
+#pragma unroll
+                    for (int cg = 0; cg < NCG; cg++) {
+                        s[cg][h][t] = mfma(ka, qh[cg][kk], s[cg][h][t]);
+                        s[cg][h][t] = mfma(ka, ql[cg][kk], s[cg][h][t]);
+                        if (KT == KV_Q8_0)
+                            s[cg][h][t] = mfma(kl, qh[cg][kk], s[cg][h][t]);
+                    }
+                }
+            }
 
-    StageRegs<HD, KT> R;
-    int tb = table_entry<P>(bt, lane, wg_len);
-    uint64_t mask_c = valid_mask(tb, 0);
-    stage_load<HD, KT, P>(a, kvh, tid, w, tb, R);
-    tb = table_entry<P>(bt, kTB + lane, wg_len);
-    stage_store<HD, KT, P, NBUF>(a, kvh, tid, w, 0, mask_c, R, S);
-    __syncthreads();
-
-    for (int base = 0, it = 0; base < wg_len; base += kTB, it++) {
-        const int buf = NBUF == 2 ? (it & 1) : 0;
-        const bool more = base + kTB < wg_len;
-        uint64_t mask_n = 0;
-        if (more) {
-            mask_n = valid_mask(tb, base + kTB);
-            stage_load<HD, KT, P>(a, kvh, tid, w, tb, R);
-            tb = table_entry<P>(bt, base + 2 * kTB + lane, wg_len);
-        }
-
-        if (wave_active && base < wave_len) {
-            // ---- scores: tiles (h, t), row j = token 32h + 8(j/4) + j%4 + 4t ----
-            f4 s[NCG][2][2];
+        // ---- online softmax of column 16 cg + j over this lane's 16 tokens ----
+        // Scores in log2 units are s * c2s (c2s > 0).  The reference maximum
+        // m2 is raised only when a block's maximum passes it by more than
+        // kLazy, so most blocks leave O and l unscaled; every
+        // p = 2^(s c2s - m2 + kPExp) is then at most 2^(kPExp + kLazy).
+        float p[NCG][16]; // [8h + v]: token 32h + 8g + v
+#pragma unroll
+        for (int cg = 0; cg < NCG; cg++) {
+            float sv[16];
 #pragma unroll
             for (int h = 0; h < 2; h++)
 #pragma unroll
-                for (int t = 0; t < 2; t++) {
+                for (int t = 0; t < 2; t++)
 #pragma unroll
-                    for (int cg = 0; cg < NCG; cg++)
-                        s[cg][h][t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-                    const int row = 32 * h + 8 * (j >> 2) + (j & 3) + 4 * t;
-#pragma unroll
-                    for (int kk = 0; kk < KK; kk++) {
-                        const h8 ka = *reinterpret_cast<const h8 *>(&S.k[buf][row][32 * kk + 8 * g]);
-                        h8 kl;
-                        if (KT == KV_Q8_0)
-                            kl = *reinterpret_cast<const h8 *>(&S.kl[buf][row][32 * kk + 8 * g]);
-#pragma unroll
-                        for (int cg = 0; cg < NCG; cg++) {
-                            s[cg][h][t] = mfma(ka, qh[cg][kk], s[cg][h][t]);
-                            s[cg][h][t] = mfma(ka, ql[cg][kk], s[cg][h][t]);
-                            if (KT == KV_Q8_0)
-                                s[cg][h][t] = mfma(kl, qh[cg][kk], s[cg][h][t]);
-                        }
-                    }
-                }
-
-            // ---- online softmax of column 16 cg + j over this lane's 16 tokens ----
-            // Scores in log2 units are s * c2s (c2s > 0).  The reference
-            // maximum m2 is raised only when a block's maximum passes it by
-            // more than kLazy, so most blocks leave O and l unscaled; every
-            // p = 2^(s c2s - m2 + kPExp) is then at most 2^(kPExp + kLazy).
-            const bool full = mask_c == ~0ull && base + kTB <= wave_full;
-            float p[NCG][16]; // [8h + v]: token 32h + 8g + v
-#pragma unroll
-            for (int cg = 0; cg < NCG; cg++) {
-                float sv[16];
-#pragma unroll
-                for (int h = 0; h < 2; h++)
-#pragma unroll
-                    for (int t = 0; t < 2; t++)
-#pragma unroll
-                        for (int r = 0; r < 4; r++)
-                            sv[8 * h + 4 * t + r] = s[cg][h][t][r];
-                if (!full) {
-                    const uint32_t lm = (uint32_t)(mask_c >> (8 * g));
-                    const uint32_t hm = (uint32_t)(mask_c >> (32 + 8 * g));
-#pragma unroll
-                    for (int i = 0; i < 16; i++) {
-                        const int tl = 32 * (i / 8) + 8 * g + (i % 8);
-                        const uint32_t bit = ((i < 8 ? lm : hm) >> (i % 8)) & 1u;
-                        if (!(bit && base + tl < qlen[cg]))
-                            sv[i] = -INFINITY;
-                    }
-                }
-                float mx = sv[0];
-#pragma unroll
-                for (int i = 1; i < 16; i++)
-                    mx = fmaxf(mx, sv[i]);
-                mx = fmaxf(mx, __shfl_xor(mx, 16));
-                mx = fmaxf(mx, __shfl_xor(mx, 32));
-                mx *= c2s[cg];
-                const bool grow = mx > m2[cg] + kLazy;
-                if (__any(grow)) {
-                    const float mref = grow ? mx : m2[cg];
-                    const float alpha = mref == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m2[cg] - mref);
-                    m2[cg] = mref;
-                    lsum[cg] *= alpha;
-#pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        const float ar = __shfl(alpha, 4 * g + r);
-#pragma unroll
-                        for (int nb = 0; nb < NB; nb++)
-                            o[cg][nb][r] *= ar;
-                    }
-                }
-                const float msub = m2[cg] == -INFINITY ? 0.0f : m2[cg] - kPExp;
+                    for (int r = 0; r < 4; r++)
+                        sv[8 * h + 4 * t + r] = s[cg][h][t][r];
+            if (!full) {
+                const uint32_t lm = (uint32_t)(mask >> (8 * g));
+                const uint32_t hm = (uint32_t)(mask >> (32 + 8 * g));
 #pragma unroll
                 for (int i = 0; i < 16; i++) {
-                    p[cg][i] = __builtin_amdgcn_exp2f(fmaf(sv[i], c2s[cg], -msub));
-                    lsum[cg] += p[cg][i];
+                    const int tl = 32 * (i / 8) + 8 * g + (i % 8);
+                    const uint32_t bit = ((i < 8 ? lm : hm) >> (i % 8)) & 1u;
+                    if (!(bit && base + tl < qlen[cg]))
+                        sv[i] = -INFINITY;
                 }
             }
-
-            // ---- P * V, V operand: dimension 16nb + j, tokens 32h + 8g .. +7 ----
+            float mx = sv[0];
 #pragma unroll
-            for (int h = 0; h < 2; h++) {
-                h8 ph[NCG], pl[NCG];
+            for (int i = 1; i < 16; i++)
+                mx = fmaxf(mx, sv[i]);
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            mx *= c2s[cg];
+            const bool grow = mx > m2[cg] + kLazy;
+            if (__any(grow)) {
+                const float mref = grow ? mx : m2[cg];
+                const float alpha = mref == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m2[cg] - mref);
+                m2[cg] = mref;
+                lsum[cg] *= alpha;
 #pragma unroll
-                for (int cg = 0; cg < NCG; cg++)
-                    split8(&p[cg][8 * h], ph[cg], pl[cg]);
+                for (int r = 0; r < 4; r++) {
+                    const float ar = __shfl(alpha, 4 * g + r);
 #pragma unroll
-                for (int nb = 0; nb < NB; nb++) {
-                    const h8 vb = *reinterpret_cast<const h8 *>(&S.v[buf][16 * nb + j][32 * h + 8 * g]);
-                    h8 vl;
-                    if (KT == KV_Q8_0)
-                        vl = *reinterpret_cast<const h8 *>(&S.vl[buf][16 * nb + j][32 * h + 8 * g]);
-#pragma unroll
-                    for (int cg = 0; cg < NCG; cg++) {
-                        o[cg][nb] = mfma(ph[cg], vb, o[cg][nb]);
-                        o[cg][nb] = mfma(pl[cg], vb, o[cg][nb]);
-                        if (KT == KV_Q8_0)
-                            o[cg][nb] = mfma(ph[cg], vl, o[cg][nb]);
-                    }
+                    for (int nb = 0; nb < NB; nb++)
+                        o[cg][nb][r] *= ar;
                 }
+            }
+            const float msub = m2[cg] == -INFINITY ? 0.0f : m2[cg] - kPExp;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                p[cg][i] = __builtin_amdgcn_exp2f(fmaf(sv[i], c2s[cg], -msub));
+                lsum[cg] += p[cg][i];
             }
         }
 
+        // ---- P * V, V operand: dimension 16nb + j, tokens 32h + 8g .. +7 ----
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            h8 ph[NCG], pl[NCG];
+#pragma unroll
+            for (int cg = 0; cg < NCG; cg++)
+                split8(&p[cg][8 * h], ph[cg], pl[cg]);
+#pragma unroll
+            for (int nb = 0; nb < NB; nb++) {
+                const h8 vb = v_frag(S, buf, 16 * nb + j, 4 * h + g);
+                h8 vl;
+                if (KT == KV_Q8_0)
+                    vl = vl_frag(S, buf, 16 * nb + j, 4 * h + g);
+#pragma unroll
+                for (int cg = 0; cg < NCG; cg++) {
+                    o[cg][nb] = mfma(ph[cg], vb, o[cg][nb]);
+                    o[cg][nb] = mfma(pl[cg], vb, o[cg][nb]);
+                    if (KT == KV_Q8_0)
+                        o[cg][nb] = mfma(ph[cg], vl, o[cg][nb]);
+                }
+            }
+        }
+    }
+
+    __device__ __forceinline__ void finish(const PrefillArgs &a, int b, int kvh, int col0, int j, int g)
+    {
+        const int H = a.num_heads, G = H / a.L.num_kv_heads, chunk = a.chunk_len;
+#pragma unroll
+        for (int cg = 0; cg < NCG; cg++) {
+            float lt = lsum[cg];
+            lt += __shfl_xor(lt, 16);
+            lt += __shfl_xor(lt, 32);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float l = __shfl(lt, 4 * g + r);
+                const int c = col0 + 16 * cg + 4 * g + r;
+                const int qi = c / G;
+                if (qi >= chunk)
+                    continue;
+                float *op = a.out + (((int64_t)b * chunk + qi) * H + kvh * G + c % G) * HD;
+                const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+#pragma unroll
+                for (int nb = 0; nb < NB; nb++)
+                    op[16 * nb + j] = o[cg][nb][r] * inv;
+            }
+        }
+    }
+};
+
+// Work split shared by both staged kernels: the workgroup's columns, the
+// context each wave and the workgroup must cover, and the block-table reads.
+template <int P, int NCG>
+struct PrefillWork {
+    int wx, kvh, b, tid, lane, w, j, g, start, mapped, col0, wave_len, wave_full, wg_len;
+    bool wave_active;
+    const int32_t *bt;
+
+    __device__ __forceinline__ PrefillWork(const PrefillArgs &a)
+    {
+        constexpr int WCOLS = 16 * NCG;
+        wx = gridDim.x - 1 - blockIdx.x; // heaviest (latest-query) workgroups first
+        kvh = blockIdx.y;
+        b = blockIdx.z;
+        tid = threadIdx.x;
+        lane = tid & 63;
+        w = __builtin_amdgcn_readfirstlane(tid >> 6);
+        j = lane & 15;
+        g = lane >> 4;
+        const int G = a.num_heads / a.L.num_kv_heads, chunk = a.chunk_len;
+        start = a.start_pos[b];
+        bt = a.block_tables + (int64_t)b * a.max_blocks;
+        mapped = a.max_blocks * P;
+        col0 = (wx * 4 + w) * WCOLS;
+        wave_len = min(start + min((col0 + WCOLS - 1) / G, chunk - 1) + 1, mapped);
+        wave_full = min(start + col0 / G + 1, mapped); // shortest column of the wave
+        wg_len = min(start + min((wx * 4 * WCOLS + 4 * WCOLS - 1) / G, chunk - 1) + 1, mapped);
+        wave_active = col0 / G < chunk;
+        if (start + chunk > mapped && tid == 0 && a.status)
+            atomicOr(a.status, FLAG_BAD_SLOT);
+    }
+
+    // Page id of block token `lane` of the block at `base` (-1 past wg_len).
+    __device__ __forceinline__ int table(int base) const { return table_entry<P>(bt, base + lane, wg_len); }
+
+    // Ballot of the block's valid tokens; flags page ids outside the pool.
+    __device__ __forceinline__ uint64_t valid_mask(const PrefillArgs &a, int tb, int base) const
+    {
+        const bool ok = tb >= 0 && tb < a.L.num_pages;
+        const bool bad = base + lane < wg_len && !ok;
+        if (__ballot(bad) && w == 0 && lane == 0 && a.status)
+            atomicOr(a.status, FLAG_BAD_PAGE);
+        return __ballot(ok);
+    }
+};
+
+template <int HD, int KT, int P, int NBUF, int NCG>
+__global__ __launch_bounds__(256) void attn_prefill_lds(PrefillArgs a)
+{
+    const PrefillWork<P, NCG> W(a);
+    __shared__ Lds<HD, KT, NBUF> S;
+    WaveAttn<HD, KT, NCG> A;
+    A.init(a, W.b, W.kvh, W.col0, W.start, W.mapped, W.wave_active, W.j, W.g);
+
+    StageRegs<HD, KT> R;
+    int tb = W.table(0);
+    uint64_t mask_c = W.valid_mask(a, tb, 0);
+    stage_load<HD, KT, P>(a, W.kvh, W.tid, W.w, tb, R);
+    tb = W.table(kTB);
+    stage_store<HD, KT, P, NBUF>(a, W.kvh, W.tid, W.w, 0, mask_c, R, S);
+    __syncthreads();
+
+    for (int base = 0, it = 0; base < W.wg_len; base += kTB, it++) {
+        const int buf = NBUF == 2 ? (it & 1) : 0;
+        const bool more = base + kTB < W.wg_len;
+        uint64_t mask_n = 0;
+        if (more) {
+            mask_n = W.valid_mask(a, tb, base + kTB);
+            stage_load<HD, KT, P>(a, W.kvh, W.tid, W.w, tb, R);
+            tb = W.table(base + 2 * kTB);
+        }
+        if (W.wave_active && base < W.wave_len)
+            A.block(S, buf, base, mask_c, mask_c == ~0ull && base + kTB <= W.wave_full, W.j, W.g);
         if (more) {
             if (NBUF == 1)
                 __syncthreads();
-            stage_store<HD, KT, P, NBUF>(a, kvh, tid, w, NBUF == 2 ? (buf ^ 1) : 0, mask_n, R, S);
+            stage_store<HD, KT, P, NBUF>(a, W.kvh, W.tid, W.w, NBUF == 2 ? (buf ^ 1) : 0, mask_n, R, S);
         }
         mask_c = mask_n;
         __syncthreads();
     }
+    if (W.wave_active)
+        A.finish(a, W.b, W.kvh, W.col0, W.j, W.g);
+}
 
-    if (!wave_active)
-        return;
+// Issues the direct global->LDS loads of one fp16 block into buffer `buf`.
+// K: 1 KiB segments of 512/HD tokens (one page each); V: segments of 8
+// dimensions x 64 tokens, where lane l always fetches logical chunk
+// (l & 7) ^ ((l >> 3) & 7), i.e. the same 8 tokens of every segment.
+template <int HD, int P>
+__device__ __forceinline__ void issue_direct(const PrefillArgs &a, int kvh, int w, int lane, int tb,
+                                             LdsDirect<HD> &S, int buf)
+{
+    const PoolLayout &L = a.L;
+    const int64_t np = L.num_pages;
+    constexpr int KROWS = 512 / HD, KSEG = kTB / KROWS, VSEG = HD / 8;
 #pragma unroll
-    for (int cg = 0; cg < NCG; cg++) {
-        float lt = lsum[cg];
-        lt += __shfl_xor(lt, 16);
-        lt += __shfl_xor(lt, 32);
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const float l = __shfl(lt, 4 * g + r);
-            const int c = col0 + 16 * cg + 4 * g + r;
-            const int qi = c / G;
-            if (qi >= chunk)
-                continue;
-            float *op = a.out + (((int64_t)b * chunk + qi) * H + kvh * G + c % G) * HD;
-            const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-#pragma unroll
-            for (int nb = 0; nb < NB; nb++)
-                op[16 * nb + j] = o[cg][nb][r] * inv;
-        }
+    for (int q = 0; q < KSEG / 4; q++) {
+        const int seg = 4 * q + w;
+        const int row = seg * KROWS + lane / (HD / 8);
+        const int c = (lane % (HD / 8)) ^ LdsDirect<HD>::kswz(row);
+        const int pr = __builtin_amdgcn_readlane(tb, seg * KROWS);
+        const int64_t pg = (pr >= 0 && pr < np) ? pr : 0;
+        const uint8_t *src = a.base + pg * L.page_bytes + L.k_off +
+                             (((int64_t)kvh * P + row % P) * HD + 8 * c) * 2;
+        __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)&S.k[buf][seg * KROWS * HD],
+                                         16, 0, 0);
     }
+    const int vtok = 8 * ((lane & 7) ^ ((lane >> 3) & 7));
+    const int vr = __shfl(tb, vtok);
+    const int64_t vpg = (vr >= 0 && vr < np) ? vr : 0;
+    const uint8_t *vsrc = a.base + vpg * L.page_bytes + L.v_off + (int64_t)(vtok % P) * 2;
+#pragma unroll
+    for (int q = 0; q < VSEG / 4; q++) {
+        const int seg = 4 * q + w;
+        const int d = 8 * seg + (lane >> 3);
+        __builtin_amdgcn_global_load_lds(vsrc + ((int64_t)kvh * HD + d) * P * 2,
+                                         (__attribute__((address_space(3))) void *)&S.v[buf][seg * 8 * kTB],
+                                         16, 0, 0);
+    }
+}
+
+// Zeroes V of the tokens whose `vmask` bit is clear (past the cached range or
+// on an invalid page) after a direct load; their scores are masked, and stale
+// values must not reach O through 0 * NaN.
+template <int HD>
+__device__ __forceinline__ void zero_dead_v(LdsDirect<HD> &S, int buf, uint64_t vmask, int tid)
+{
+    for (int e = tid; e < HD * (kTB / 8); e += 256) {
+        const int d = e / (kTB / 8), c = e % (kTB / 8);
+        const uint32_t live = (uint32_t)(vmask >> (8 * c)) & 0xFFu;
+        if (live == 0xFFu)
+            continue;
+        u4 *p = reinterpret_cast<u4 *>(&S.v[buf][d * kTB + 8 * (c ^ (d & 7))]);
+        u4 x = *p;
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            if (!((live >> i) & 1u))
+                x[i / 2] &= (i & 1) ? 0x0000FFFFu : 0xFFFF0000u;
+        *p = x;
+    }
+}
+
+__device__ __forceinline__ void wait_direct_loads()
+{
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
+// fp16 pages through direct global->LDS loads: no staging registers and no
+// LDS store instructions; two LDS buffers, one barrier per block (two more on
+// blocks with tokens to zero).
+template <int HD, int P, int NCG>
+__global__ __launch_bounds__(256) void attn_prefill_dlds(PrefillArgs a)
+{
+    const PrefillWork<P, NCG> W(a);
+    __shared__ LdsDirect<HD> S;
+    WaveAttn<HD, KV_F16, NCG> A;
+    A.init(a, W.b, W.kvh, W.col0, W.start, W.mapped, W.wave_active, W.j, W.g);
+
+    int tb = W.table(0);
+    uint64_t mask_c = W.valid_mask(a, tb, 0);
+    issue_direct<HD, P>(a, W.kvh, W.w, W.lane, tb, S, 0);
+    tb = W.table(kTB);
+    wait_direct_loads();
+    __syncthreads();
+    if (mask_c != ~0ull) {
+        zero_dead_v<HD>(S, 0, mask_c, W.tid);
+        __syncthreads();
+    }
+
+    for (int base = 0, it = 0; base < W.wg_len; base += kTB, it++) {
+        const int buf = it & 1;
+        const bool more = base + kTB < W.wg_len;
+        uint64_t mask_n = 0;
+        if (more) {
+            mask_n = W.valid_mask(a, tb, base + kTB);
+            issue_direct<HD, P>(a, W.kvh, W.w, W.lane, tb, S, buf ^ 1);
+            tb = W.table(base + 2 * kTB);
+        }
+        if (W.wave_active && base < W.wave_len)
+            A.block(S, buf, base, mask_c, mask_c == ~0ull && base + kTB <= W.wave_full, W.j, W.g);
+        wait_direct_loads();
+        __syncthreads();
+        if (more && mask_n != ~0ull) {
+            zero_dead_v<HD>(S, buf ^ 1, mask_n, W.tid);
+            __syncthreads();
+        }
+        mask_c = mask_n;
+    }
+    if (W.wave_active)
+        A.finish(a, W.b, W.kvh, W.col0, W.j, W.g);
 }
 
 } // namespace mfma_prefill
@@ -882,6 +1077,15 @@ constexpr int prefill_lds_ncg()
 #endif
 }
 
+// fp16 pages use the direct global->LDS kernel (no staging registers, so
+// two column groups always fit).
+#ifndef GI_PREFILL_DIRECT
+#define GI_PREFILL_DIRECT 1
+#endif
+#ifndef GI_PREFILL_DIRECT_NCG
+#define GI_PREFILL_DIRECT_NCG 2
+#endif
+
 template <int HD, int KT>
 static void launch_lds(const PrefillArgs &a, hipStream_t st)
 {
@@ -893,6 +1097,21 @@ static void launch_lds(const PrefillArgs &a, hipStream_t st)
         const int64_t per_wg = 4 * 16 * ncg;
         return dim3((unsigned)((cols + per_wg - 1) / per_wg), a.L.num_kv_heads, a.batch);
     };
+    if (KT == KV_F16 && GI_PREFILL_DIRECT) {
+        constexpr int NCG = GI_PREFILL_DIRECT_NCG;
+        switch (a.L.page_tokens) {
+        case 16:
+            hipLaunchKernelGGL((attn_prefill_dlds<HD, 16, NCG>), grid(NCG), dim3(256), 0, st, a);
+            break;
+        case 32:
+            hipLaunchKernelGGL((attn_prefill_dlds<HD, 32, NCG>), grid(NCG), dim3(256), 0, st, a);
+            break;
+        default:
+            hipLaunchKernelGGL((attn_prefill_dlds<HD, 64, NCG>), grid(NCG), dim3(256), 0, st, a);
+            break;
+        }
+        return;
+    }
 #define GI_PFL(PT)                                                                           \
     hipLaunchKernelGGL((attn_prefill_lds<HD, KT, PT, NBUF, prefill_lds_ncg<HD, KT, PT>()>), \
                        grid(prefill_lds_ncg<HD, KT, PT>()), dim3(256), 0, st, a)
