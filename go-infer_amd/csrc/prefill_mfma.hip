@@ -22,6 +22,7 @@
 #include "gi_kernels.h"
 
 #include <math.h>
+#include <type_traits>
 
 namespace gi {
 
@@ -596,57 +597,83 @@ __device__ __forceinline__ void stage_store(const PrefillArgs &a, int kvh, int t
     }
 }
 
-// Fragment accessors of the register-staged layout (rows padded by 16 bytes).
+// MFMA operand addresses.  A lane's K operand of tile (h, t) and k-step kk
+// is row 32h + 8(j/4) + j%4 + 4t, 16-byte chunk 4kk + g; its V operand of
+// half h and output tile nb is dimension 16nb + j, chunk 4h + g.  Each
+// layout splits these addresses into a per-lane base, computed once per
+// block, and a compile-time offset, so that the reads use immediate offsets.
+
+// Register-staged layout (rows padded by 16 bytes).
 template <int HD, int KT, int NBUF>
-__device__ __forceinline__ h8 k_frag(const Lds<HD, KT, NBUF> &S, int buf, int row, int c)
+__device__ __forceinline__ const uint8_t *k_lane(const Lds<HD, KT, NBUF> &S, int buf, int j, int g, bool lo)
 {
-    return *reinterpret_cast<const h8 *>(&S.k[buf][row][8 * c]);
+    return reinterpret_cast<const uint8_t *>(lo ? &S.kl[buf][8 * (j >> 2) + (j & 3)][8 * g]
+                                                : &S.k[buf][8 * (j >> 2) + (j & 3)][8 * g]);
 }
 template <int HD, int KT, int NBUF>
-__device__ __forceinline__ h8 kl_frag(const Lds<HD, KT, NBUF> &S, int buf, int row, int c)
+__device__ __forceinline__ const uint8_t *v_lane(const Lds<HD, KT, NBUF> &S, int buf, int h, int j, int g,
+                                                 bool lo)
 {
-    return *reinterpret_cast<const h8 *>(&S.kl[buf][row][8 * c]);
+    return reinterpret_cast<const uint8_t *>(lo ? &S.vl[buf][j][32 * h + 8 * g] : &S.v[buf][j][32 * h + 8 * g]);
 }
 template <int HD, int KT, int NBUF>
-__device__ __forceinline__ h8 v_frag(const Lds<HD, KT, NBUF> &S, int buf, int d, int c)
+__device__ constexpr int k_const(const Lds<HD, KT, NBUF> *, int h, int t, int kk)
 {
-    return *reinterpret_cast<const h8 *>(&S.v[buf][d][8 * c]);
+    return ((32 * h + 4 * t) * (HD + 8) + 32 * kk) * 2;
 }
 template <int HD, int KT, int NBUF>
-__device__ __forceinline__ h8 vl_frag(const Lds<HD, KT, NBUF> &S, int buf, int d, int c)
+__device__ constexpr int v_const(const Lds<HD, KT, NBUF> *, int nb)
 {
-    return *reinterpret_cast<const h8 *>(&S.vl[buf][d][8 * c]);
+    return 16 * nb * (kTB + 8) * 2;
 }
 
 // Layout written by direct global->LDS loads (fp16 pages).  One load
-// instruction fills 1 KiB of LDS with its lanes' 16 bytes in lane order, so
-// rows are unpadded; 16-byte chunks are XOR-swizzled inside each row instead,
-// which keeps the MFMA operand reads of 8 consecutive lanes on distinct banks.
+// instruction fills a 1 KiB segment of LDS with its lanes' 16 bytes in lane
+// order, so rows inside a segment are unpadded.  K: segments of 512/HD token
+// rows, each followed by 4096/HD bytes of padding, and the low two bits of a
+// row's 16-byte chunk index XORed with row % 4; V: segments of 8 dimensions,
+// chunk index XORed with dim % 8.  The MFMA operand reads of 8 consecutive
+// lanes then fall on distinct banks.
 template <int HD>
 struct LdsDirect {
-    __attribute__((aligned(16))) _Float16 k[2][kTB * HD]; // [token][HD], chunk c at c ^ kswz(token)
+    static constexpr int KROWS = 512 / HD;             // K rows per segment
+    static constexpr int KSEGB = 1024 + 4096 / HD;     // bytes per K segment, padded
+    static constexpr int KBYTES = kTB / KROWS * KSEGB; // bytes of one K buffer
+    __attribute__((aligned(16))) uint8_t k[2][KBYTES];
     __attribute__((aligned(16))) _Float16 v[2][HD * kTB]; // [dim][kTB], chunk c at c ^ (dim & 7)
-    __device__ static int kswz(int row) { return ((row & 3) | (((row >> 3) & 3) << 2)) & (HD / 8 - 1); }
+    __device__ static int koff(int row, int c)
+    {
+        return row / KROWS * KSEGB + row % KROWS * HD * 2 + 16 * (c ^ (row & 3));
+    }
 };
 template <int HD>
-__device__ __forceinline__ h8 k_frag(const LdsDirect<HD> &S, int buf, int row, int c)
+__device__ __forceinline__ const uint8_t *k_lane(const LdsDirect<HD> &S, int buf, int j, int g, bool)
 {
-    return *reinterpret_cast<const h8 *>(&S.k[buf][row * HD + 8 * (c ^ LdsDirect<HD>::kswz(row))]);
+    // row 8(j/4) + j%4 (+ 32h + 4t): segment and row inside it
+    constexpr int KR = LdsDirect<HD>::KROWS;
+    const int seg = KR == 4 ? 2 * (j >> 2) : (j >> 2);
+    return &S.k[buf][seg * LdsDirect<HD>::KSEGB + (j & 3) * HD * 2 + 16 * (g ^ (j & 3))];
 }
 template <int HD>
-__device__ __forceinline__ h8 kl_frag(const LdsDirect<HD> &, int, int, int)
+__device__ __forceinline__ const uint8_t *v_lane(const LdsDirect<HD> &S, int buf, int h, int j, int g, bool)
 {
-    return h8{};
+    return reinterpret_cast<const uint8_t *>(&S.v[buf][j * kTB + 8 * ((4 * h + g) ^ (j & 7))]);
 }
 template <int HD>
-__device__ __forceinline__ h8 v_frag(const LdsDirect<HD> &S, int buf, int d, int c)
+__device__ constexpr int k_const(const LdsDirect<HD> *, int h, int t, int kk)
 {
-    return *reinterpret_cast<const h8 *>(&S.v[buf][d * kTB + 8 * (c ^ (d & 7))]);
+    constexpr int KR = LdsDirect<HD>::KROWS, SB = LdsDirect<HD>::KSEGB;
+    return (KR == 4 ? (8 * h + t) * SB : 4 * h * SB + 4 * t * HD * 2) + 64 * kk;
 }
 template <int HD>
-__device__ __forceinline__ h8 vl_frag(const LdsDirect<HD> &, int, int, int)
+__device__ constexpr int v_const(const LdsDirect<HD> *, int nb)
 {
-    return h8{};
+    return 16 * nb * kTB * 2;
+}
+
+__device__ __forceinline__ h8 ld_frag(const uint8_t *p, int off)
+{
+    return *reinterpret_cast<const h8 *>(p + off);
 }
 
 // Per-wave attention state over NCG column groups of 16 (query, head)
@@ -671,15 +698,17 @@ struct WaveAttn {
             const int qi = min(c / G, chunk - 1);
             qlen[cg] = min(start + qi + 1, mapped);
             const float *qp = a.q + (((int64_t)b * chunk + qi) * H + kvh * G + c % G) * HD;
-            float qv[KK][8];
+            // two passes over q (the second from the caches), so that only
+            // 8 of its values are live at a time next to the split halves
             float mq = 0.0f;
 #pragma unroll
-            for (int kk = 0; kk < KK; kk++)
+            for (int kk = 0; kk < KK; kk++) {
+                const f4 x0 = active ? *reinterpret_cast<const f4 *>(qp + 32 * kk + 8 * g) : f4{};
+                const f4 x1 = active ? *reinterpret_cast<const f4 *>(qp + 32 * kk + 8 * g + 4) : f4{};
 #pragma unroll
-                for (int v = 0; v < 8; v++) {
-                    qv[kk][v] = active ? qp[32 * kk + 8 * g + v] : 0.0f;
-                    mq = fmaxf(mq, fabsf(qv[kk][v]));
-                }
+                for (int v = 0; v < 4; v++)
+                    mq = fmaxf(mq, fmaxf(fabsf(x0[v]), fabsf(x1[v])));
+            }
             mq = fmaxf(mq, __shfl_xor(mq, 16));
             mq = fmaxf(mq, __shfl_xor(mq, 32));
             const int qe = pow2_exponent_for(mq);
@@ -687,10 +716,14 @@ struct WaveAttn {
             c2s[cg] = a.scale * kLog2e * ldexpf(1.0f, -qe);
 #pragma unroll
             for (int kk = 0; kk < KK; kk++) {
+                const f4 x0 = active ? *reinterpret_cast<const f4 *>(qp + 32 * kk + 8 * g) : f4{};
+                const f4 x1 = active ? *reinterpret_cast<const f4 *>(qp + 32 * kk + 8 * g + 4) : f4{};
                 float x[8];
 #pragma unroll
-                for (int v = 0; v < 8; v++)
-                    x[v] = qv[kk][v] * up;
+                for (int v = 0; v < 4; v++) {
+                    x[v] = x0[v] * up;
+                    x[4 + v] = x1[v] * up;
+                }
                 split8(x, qh[cg][kk], ql[cg][kk]);
             }
             m2[cg] = -INFINITY;
@@ -701,14 +734,77 @@ struct WaveAttn {
         }
     }
 
+    // Online softmax of column 16 cg + j over this lane's 16 tokens of a
+    // block (sv[8h + v]: token 32h + 8g + v), producing P as fp16 hi + lo per
+    // half.  Scores in log2 units are s * c2s (c2s > 0).  The reference
+    // maximum m2 is raised only when a block's maximum passes it by more than
+    // kLazy, so O and l are rarely rescaled; every p = 2^(s c2s - m2 + kPExp)
+    // is at most 2^(kPExp + kLazy).  Returns whether any column of the wave
+    // grew, in which case the caller rescales O by `alpha`.
+    template <bool FULL>
+    __device__ __forceinline__ bool softmax16(int cg, float (&sv)[16], int base, uint64_t mask, h8 &ph0,
+                                              h8 &pl0, h8 &ph1, h8 &pl1, float &alpha, int g)
+    {
+        if (!FULL) {
+            const uint32_t lm = (uint32_t)(mask >> (8 * g));
+            const uint32_t hm = (uint32_t)(mask >> (32 + 8 * g));
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int tl = 32 * (i / 8) + 8 * g + (i % 8);
+                const uint32_t bit = ((i < 8 ? lm : hm) >> (i % 8)) & 1u;
+                if (!(bit && base + tl < qlen[cg]))
+                    sv[i] = -INFINITY;
+            }
+        }
+        float mx = sv[0];
+#pragma unroll
+        for (int i = 1; i < 16; i++)
+            mx = fmaxf(mx, sv[i]);
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        mx *= c2s[cg];
+        const bool grow = mx > m2[cg] + kLazy;
+        const float mref = grow ? mx : m2[cg];
+        alpha = grow ? __builtin_amdgcn_exp2f(m2[cg] - mref) : 1.0f;
+        m2[cg] = mref;
+        const float msub = mref == -INFINITY ? 0.0f : mref - kPExp;
+        float p[16];
+        float ps = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            p[i] = __builtin_amdgcn_exp2f(fmaf(sv[i], c2s[cg], -msub));
+            ps += p[i];
+        }
+        lsum[cg] = lsum[cg] * alpha + ps;
+        split8(&p[0], ph0, pl0);
+        split8(&p[8], ph1, pl1);
+        return __any(grow);
+    }
+
+    // O rows (columns 4g + r of each group) times the alpha of their column.
+    __device__ __forceinline__ void rescale(const float (&alpha)[NCG], int g)
+    {
+#pragma unroll
+        for (int cg = 0; cg < NCG; cg++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float ar = __shfl(alpha[cg], 4 * g + r);
+#pragma unroll
+                for (int nb = 0; nb < NB; nb++)
+                    o[cg][nb][r] *= ar;
+            }
+    }
+
     // One 64-token block from LDS buffer `buf`.  `mask` bit l: block token l
-    // is cached and on a valid page; `full`: every token of the block is
-    // valid for every column of the wave (no masking needed).
-    template <class LDS>
-    __device__ __forceinline__ void block(const LDS &S, int buf, int base, uint64_t mask, bool full,
-                                          int j, int g)
+    // is cached and on a valid page.  FULL: every token of the block is valid
+    // for every column of the wave (a separate instantiation, with no masking
+    // code).
+    template <bool FULL, class LDS>
+    __device__ __forceinline__ void block(const LDS &S, int buf, int base, uint64_t mask, int j, int g)
     {
         // ---- scores: tiles (h, t), row j = token 32h + 8(j/4) + j%4 + 4t ----
+        const uint8_t *kp = k_lane(S, buf, j, g, false);
+        const uint8_t *klp = KT == KV_Q8_0 ? k_lane(S, buf, j, g, true) : kp;
         f4 s[NCG][2][2];
 #pragma unroll
         for (int h = 0; h < 2; h++)
@@ -717,13 +813,13 @@ struct WaveAttn {
 #pragma unroll
                 for (int cg = 0; cg < NCG; cg++)
                     s[cg][h][t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-                const int row = 32 * h + 8 * (j >> 2) + (j & 3) + 4 * t;
 #pragma unroll
                 for (int kk = 0; kk < KK; kk++) {
-                    const h8 ka = k_frag(S, buf, row, 4 * kk + g);
+                    const int off = k_const(&S, h, t, kk);
+                    const h8 ka = ld_frag(kp, off);
                     h8 kl;
                     if (KT == KV_Q8_0)
-                        kl = kl_frag(S, buf, row, 4 * kk + g);
+                        kl = ld_frag(klp, off);
 #pragma unroll
                     for (int cg = 0; cg < NCG; cg++) {
                         s[cg][h][t] = mfma(ka, qh[cg][kk], s[cg][h][t]);
@@ -734,15 +830,13 @@ struct WaveAttn {
                 }
             }
 
-        // ---- online softmax of column 16 cg + j over this lane's 16 tokens ----
-        // Scores in log2 units are s * c2s (c2s > 0).  The reference maximum
-        // m2 is raised only when a block's maximum passes it by more than
-        // kLazy, so most blocks leave O and l unscaled; every
-        // p = 2^(s c2s - m2 + kPExp) is then at most 2^(kPExp + kLazy).
-        float p[NCG][16]; // [8h + v]: token 32h + 8g + v
+        // ---- online softmax of each column over this lane's 16 tokens ----
+        h8 ph[2][NCG], pl[2][NCG];
+        float alpha[NCG];
+        bool grow = false;
 #pragma unroll
         for (int cg = 0; cg < NCG; cg++) {
-            float sv[16];
+            float sv[16]; // [8h + v]: token 32h + 8g + v
 #pragma unroll
             for (int h = 0; h < 2; h++)
 #pragma unroll
@@ -750,65 +844,29 @@ struct WaveAttn {
 #pragma unroll
                     for (int r = 0; r < 4; r++)
                         sv[8 * h + 4 * t + r] = s[cg][h][t][r];
-            if (!full) {
-                const uint32_t lm = (uint32_t)(mask >> (8 * g));
-                const uint32_t hm = (uint32_t)(mask >> (32 + 8 * g));
-#pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    const int tl = 32 * (i / 8) + 8 * g + (i % 8);
-                    const uint32_t bit = ((i < 8 ? lm : hm) >> (i % 8)) & 1u;
-                    if (!(bit && base + tl < qlen[cg]))
-                        sv[i] = -INFINITY;
-                }
-            }
-            float mx = sv[0];
-#pragma unroll
-            for (int i = 1; i < 16; i++)
-                mx = fmaxf(mx, sv[i]);
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            mx *= c2s[cg];
-            const bool grow = mx > m2[cg] + kLazy;
-            if (__any(grow)) {
-                const float mref = grow ? mx : m2[cg];
-                const float alpha = mref == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m2[cg] - mref);
-                m2[cg] = mref;
-                lsum[cg] *= alpha;
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const float ar = __shfl(alpha, 4 * g + r);
-#pragma unroll
-                    for (int nb = 0; nb < NB; nb++)
-                        o[cg][nb][r] *= ar;
-                }
-            }
-            const float msub = m2[cg] == -INFINITY ? 0.0f : m2[cg] - kPExp;
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                p[cg][i] = __builtin_amdgcn_exp2f(fmaf(sv[i], c2s[cg], -msub));
-                lsum[cg] += p[cg][i];
-            }
+            grow |= softmax16<FULL>(cg, sv, base, mask, ph[0][cg], pl[0][cg], ph[1][cg], pl[1][cg],
+                                    alpha[cg], g);
         }
+        if (grow)
+            rescale(alpha, g);
 
-        // ---- P * V, V operand: dimension 16nb + j, tokens 32h + 8g .. +7 ----
+        // ---- P V, V operand: dimension 16nb + j, tokens 32h + 8g .. +7 ----
 #pragma unroll
         for (int h = 0; h < 2; h++) {
-            h8 ph[NCG], pl[NCG];
-#pragma unroll
-            for (int cg = 0; cg < NCG; cg++)
-                split8(&p[cg][8 * h], ph[cg], pl[cg]);
+            const uint8_t *vp = v_lane(S, buf, h, j, g, false);
+            const uint8_t *vlp = KT == KV_Q8_0 ? v_lane(S, buf, h, j, g, true) : vp;
 #pragma unroll
             for (int nb = 0; nb < NB; nb++) {
-                const h8 vb = v_frag(S, buf, 16 * nb + j, 4 * h + g);
+                const h8 vb = ld_frag(vp, v_const(&S, nb));
                 h8 vl;
                 if (KT == KV_Q8_0)
-                    vl = vl_frag(S, buf, 16 * nb + j, 4 * h + g);
+                    vl = ld_frag(vlp, v_const(&S, nb));
 #pragma unroll
                 for (int cg = 0; cg < NCG; cg++) {
-                    o[cg][nb] = mfma(ph[cg], vb, o[cg][nb]);
-                    o[cg][nb] = mfma(pl[cg], vb, o[cg][nb]);
+                    o[cg][nb] = mfma(ph[h][cg], vb, o[cg][nb]);
+                    o[cg][nb] = mfma(pl[h][cg], vb, o[cg][nb]);
                     if (KT == KV_Q8_0)
-                        o[cg][nb] = mfma(ph[cg], vl, o[cg][nb]);
+                        o[cg][nb] = mfma(ph[h][cg], vl, o[cg][nb]);
                 }
             }
         }
@@ -843,7 +901,7 @@ struct WaveAttn {
 // context each wave and the workgroup must cover, and the block-table reads.
 template <int P, int NCG>
 struct PrefillWork {
-    int wx, kvh, b, tid, lane, w, j, g, start, mapped, col0, wave_len, wave_full, wg_len;
+    int wx, kvh, b, tid, lane, w, j, g, start, mapped, col0, wave_len, wg_full, wg_len;
     bool wave_active;
     const int32_t *bt;
 
@@ -864,11 +922,18 @@ struct PrefillWork {
         mapped = a.max_blocks * P;
         col0 = (wx * 4 + w) * WCOLS;
         wave_len = min(start + min((col0 + WCOLS - 1) / G, chunk - 1) + 1, mapped);
-        wave_full = min(start + col0 / G + 1, mapped); // shortest column of the wave
+        wg_full = min(start + wx * 4 * WCOLS / G + 1, mapped); // shortest column of the workgroup
         wg_len = min(start + min((wx * 4 * WCOLS + 4 * WCOLS - 1) / G, chunk - 1) + 1, mapped);
         wave_active = col0 / G < chunk;
         if (start + chunk > mapped && tid == 0 && a.status)
             atomicOr(a.status, FLAG_BAD_SLOT);
+    }
+
+    // Whether the block at `base` is whole for every column of the
+    // workgroup: all its tokens valid and before the shortest column's end.
+    __device__ __forceinline__ bool block_full(int base, uint64_t mask) const
+    {
+        return mask == ~0ull && base + kTB <= wg_full;
     }
 
     // Page id of block token `lane` of the block at `base` (-1 past wg_len).
@@ -901,7 +966,10 @@ __global__ __launch_bounds__(256) void attn_prefill_lds(PrefillArgs a)
     stage_store<HD, KT, P, NBUF>(a, W.kvh, W.tid, W.w, 0, mask_c, R, S);
     __syncthreads();
 
-    for (int base = 0, it = 0; base < W.wg_len; base += kTB, it++) {
+    // One staged block; FULL: no column of the workgroup needs masking.
+    int base = 0, it = 0;
+    auto step = [&](auto full) {
+        constexpr bool FULL = decltype(full)::value;
         const int buf = NBUF == 2 ? (it & 1) : 0;
         const bool more = base + kTB < W.wg_len;
         uint64_t mask_n = 0;
@@ -911,7 +979,7 @@ __global__ __launch_bounds__(256) void attn_prefill_lds(PrefillArgs a)
             tb = W.table(base + 2 * kTB);
         }
         if (W.wave_active && base < W.wave_len)
-            A.block(S, buf, base, mask_c, mask_c == ~0ull && base + kTB <= W.wave_full, W.j, W.g);
+            A.template block<FULL>(S, buf, base, mask_c, W.j, W.g);
         if (more) {
             if (NBUF == 1)
                 __syncthreads();
@@ -919,7 +987,16 @@ __global__ __launch_bounds__(256) void attn_prefill_lds(PrefillArgs a)
         }
         mask_c = mask_n;
         __syncthreads();
-    }
+        base += kTB;
+        it++;
+    };
+    // blocks every column of the workgroup sees whole, then the rest (the
+    // causal diagonal, the partial last block, and any block after a page
+    // id outside the pool)
+    while (base < W.wg_len && W.block_full(base, mask_c))
+        step(std::true_type{});
+    while (base < W.wg_len)
+        step(std::false_type{});
     if (W.wave_active)
         A.finish(a, W.b, W.kvh, W.col0, W.j, W.g);
 }
@@ -934,18 +1011,18 @@ __device__ __forceinline__ void issue_direct(const PrefillArgs &a, int kvh, int 
 {
     const PoolLayout &L = a.L;
     const int64_t np = L.num_pages;
-    constexpr int KROWS = 512 / HD, KSEG = kTB / KROWS, VSEG = HD / 8;
+    constexpr int KROWS = LdsDirect<HD>::KROWS, KSEG = kTB / KROWS, VSEG = HD / 8;
 #pragma unroll
     for (int q = 0; q < KSEG / 4; q++) {
         const int seg = 4 * q + w;
         const int row = seg * KROWS + lane / (HD / 8);
-        const int c = (lane % (HD / 8)) ^ LdsDirect<HD>::kswz(row);
+        const int c = (lane % (HD / 8)) ^ (row & 3);
         const int pr = __builtin_amdgcn_readlane(tb, seg * KROWS);
         const int64_t pg = (pr >= 0 && pr < np) ? pr : 0;
         const uint8_t *src = a.base + pg * L.page_bytes + L.k_off +
                              (((int64_t)kvh * P + row % P) * HD + 8 * c) * 2;
-        __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)&S.k[buf][seg * KROWS * HD],
-                                         16, 0, 0);
+        __builtin_amdgcn_global_load_lds(
+            src, (__attribute__((address_space(3))) void *)&S.k[buf][seg * LdsDirect<HD>::KSEGB], 16, 0, 0);
     }
     const int vtok = 8 * ((lane & 7) ^ ((lane >> 3) & 7));
     const int vr = __shfl(tb, vtok);
@@ -1009,7 +1086,10 @@ __global__ __launch_bounds__(256) void attn_prefill_dlds(PrefillArgs a)
         __syncthreads();
     }
 
-    for (int base = 0, it = 0; base < W.wg_len; base += kTB, it++) {
+    // One block; FULL: no column of the workgroup needs masking.
+    int base = 0, it = 0;
+    auto step = [&](auto full) {
+        constexpr bool FULL = decltype(full)::value;
         const int buf = it & 1;
         const bool more = base + kTB < W.wg_len;
         uint64_t mask_n = 0;
@@ -1019,7 +1099,7 @@ __global__ __launch_bounds__(256) void attn_prefill_dlds(PrefillArgs a)
             tb = W.table(base + 2 * kTB);
         }
         if (W.wave_active && base < W.wave_len)
-            A.block(S, buf, base, mask_c, mask_c == ~0ull && base + kTB <= W.wave_full, W.j, W.g);
+            A.template block<FULL>(S, buf, base, mask_c, W.j, W.g);
         wait_direct_loads();
         __syncthreads();
         if (more && mask_n != ~0ull) {
@@ -1027,7 +1107,13 @@ __global__ __launch_bounds__(256) void attn_prefill_dlds(PrefillArgs a)
             __syncthreads();
         }
         mask_c = mask_n;
-    }
+        base += kTB;
+        it++;
+    };
+    while (base < W.wg_len && W.block_full(base, mask_c))
+        step(std::true_type{});
+    while (base < W.wg_len)
+        step(std::false_type{});
     if (W.wave_active)
         A.finish(a, W.b, W.kvh, W.col0, W.j, W.g);
 }
