@@ -187,6 +187,36 @@ def cpu_baseline(oracle, cfg, budget_s=12.0):
             "ms_per_step": round(step_s * 1e3, 1)}
 
 
+def cpu_baseline_prefill(oracle, cfg, budget_s=10.0):
+    """The oracle's chunked-prefill attention (forward.go:547-577, over
+    f32 K/V: q8_0 pages dequantised first, a pass over the context that is
+    under 0.1 % of the work and left out) on one host core for a bounded
+    sample: 16 queries at the end of the last chunk (context 4096), repeated
+    until about budget_s of CPU work.  Reported as TFLOP/s of the same
+    algorithmic flop count as the GPU figure."""
+    H, kvh, hd = cfg["q_heads"], cfg["kv_heads"], cfg["head_dim"]
+    Ltot = int(cfg["context"])
+    nq, start = 16, Ltot - 16
+    k = oracle.normal(11, (Ltot, kvh * hd))
+    v = oracle.normal(12, (Ltot, kvh * hd))
+    q = oracle.normal(13, (nq, H * hd))
+    sc = oracle.attn_scale(hd)
+    flops = 4 * hd * H * sum(start + i + 1 for i in range(nq))
+    units, t0 = 0, time.perf_counter()
+    while True:
+        oracle.attention_prefill(q, k, v, H, kvh, hd, start, nq, 1 << 30, sc)
+        units += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or units >= 64:
+            break
+    tflops = flops * units / el / 1e12
+    full_s = prefill_flops(cfg) / (tflops * 1e12)
+    return {"value": round(tflops, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "sample": "%d units of 16 queries at positions %d..%d over f32 K/V (%.2f GFLOP each) "
+                      "on 1 thread, %.1f s; the whole prefill would take %.0f s"
+                      % (units, start, Ltot - 1, flops / 1e9, el, full_s)}
+
+
 def prefill_flops(cfg):
     """Exact causal attention flops of the whole prefill: per sequence and
     layer 2 products x 2 flops x head_dim x q_heads x sum_{i=1..L} i."""
@@ -279,6 +309,10 @@ def run_prefill(args, gi, torch, dev, cfg):
         err = float((np.abs(got - w).max(axis=1) / np.abs(w).max(axis=1)).max())
         parity = {"sampled_seq_layer_chunk": [i, l, nch - 1], "max_rel_err": err, "tol": 1e-3,
                   "pass": bool(err <= 1e-3)}
+    cpu = None
+    if not args.no_cpu_baseline:
+        import oracle
+        cpu = cpu_baseline_prefill(oracle, cfg)
     res = {
         "metric": METRIC,
         "value": round(tflops, 2),
@@ -301,6 +335,7 @@ def run_prefill(args, gi, torch, dev, cfg):
                      "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4), "traffic": None,
                      "kernel": "paged prefill attention",
                      "flops_per_step": flops},
+        "cpu_baseline": cpu,
         "parity": parity,
     }
     print(json.dumps(res), flush=True)

@@ -181,8 +181,8 @@ __device__ __host__ __forceinline__ uint32_t abs_key(float x)
 
 // Power-of-two exponent e such that max_abs * 2^e <= 2^14, clamped to
 // [-60, 60] (0 for a zero or non-finite input).  Multiplying by 2^e is exact,
-// and it keeps both halves of an fp16 hi/lo split in the normal range: the
-// matrix cores treat fp16 denormal operands as zero.
+// and it keeps both halves of an fp16 hi/lo split in the normal range, where
+// each carries the full 11-bit significand.
 __device__ __host__ __forceinline__ int pow2_exponent_for(float max_abs)
 {
     uint32_t bits = __builtin_bit_cast(uint32_t, max_abs);
