@@ -308,6 +308,18 @@ size_t decode_workspace_bytes(const PoolLayout &L, int batch, int num_heads, int
     return (size_t)batch * L.num_kv_heads * num_splits * G * (L.head_dim + 2) * sizeof(float);
 }
 
+// Split-K planning: enough (split, kv head, sequence) workgroups for about
+// GI_DECODE_WG_PER_CU per CU, each split at least GI_DECODE_MIN_SPLIT tokens.
+// Measured on MI355X: 2 and 1024 beat finer splits (4/512, 8/256, 16/128) on
+// both 32 ragged sequences of 512-4096 tokens and 8 sequences of 32768, since
+// every workgroup pays a fixed cost (query load, cross-wave merge, partials).
+#ifndef GI_DECODE_WG_PER_CU
+#define GI_DECODE_WG_PER_CU 2
+#endif
+#ifndef GI_DECODE_MIN_SPLIT
+#define GI_DECODE_MIN_SPLIT 1024
+#endif
+
 void decode_plan(const PoolLayout &L, int batch, int num_heads, int max_len, int num_cus,
                  int *split_tokens, int *num_splits)
 {
@@ -319,10 +331,10 @@ void decode_plan(const PoolLayout &L, int batch, int num_heads, int max_len, int
     if (max_len < 1)
         max_len = 1;
     const int64_t pairs = (int64_t)batch * L.num_kv_heads;
-    const int64_t target = 4LL * (num_cus > 0 ? num_cus : 256);
+    const int64_t target = (int64_t)GI_DECODE_WG_PER_CU * (num_cus > 0 ? num_cus : 256);
     int splits = (int)((target + pairs - 1) / pairs);
-    // At least ~512 tokens per split so the merge stays negligible.
-    int max_splits = (max_len + 511) / 512;
+    // A minimum of tokens per split keeps the merge negligible.
+    int max_splits = (max_len + GI_DECODE_MIN_SPLIT - 1) / GI_DECODE_MIN_SPLIT;
     if (splits > max_splits)
         splits = max_splits;
     if (splits < 1)
