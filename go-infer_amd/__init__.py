@@ -21,8 +21,8 @@ built, loading it raises.
 import ctypes
 import os
 
-__all__ = ["lib", "GIError", "PagedKVManager", "PagedKVCache", "KV_F32", "KV_F16", "KV_Q8_0",
-           "EXPORTS", "LIB_PATH", "attn_scale"]
+__all__ = ["lib", "GIError", "PagedKVManager", "PagedKVCache", "PrefixCache", "KV_F32", "KV_F16",
+           "KV_Q8_0", "EXPORTS", "LIB_PATH", "attn_scale"]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libgoinfer_paged.so")
@@ -31,7 +31,7 @@ KV_F32, KV_F16, KV_Q8_0 = 0, 1, 2
 GI_OK = 0
 ERR_NAMES = {-1: "GI_ERR_NO_DEVICE", -2: "GI_ERR_OOM", -3: "GI_ERR_BAD_ARG",
              -4: "GI_ERR_POOL_EXHAUSTED", -5: "GI_ERR_HIP", -6: "GI_ERR_UNKNOWN_SEQ",
-             -7: "GI_ERR_BAD_PAGE"}
+             -7: "GI_ERR_BAD_PAGE", -8: "GI_ERR_SHARED_PAGE"}
 
 _c_int, _c_i64, _vp = ctypes.c_int, ctypes.c_int64, ctypes.c_void_p
 _i32p = ctypes.POINTER(ctypes.c_int32)
@@ -51,6 +51,16 @@ EXPORTS = {
     "gi_kvmgr_block_table": (_c_int, [_vp, _c_int, _i32p, _c_int, _intp, _intp]),
     "gi_kvmgr_free_list": (_c_int, [_vp, _i32p, _c_int, _intp]),
     "gi_kvmgr_set_free_list": (_c_int, [_vp, _i32p, _c_int]),
+    "gi_kvmgr_fork_sequence": (_c_int, [_vp, _c_int, _c_int, _intp]),
+    "gi_kvmgr_append_token_cow": (_c_int, [_vp, _c_int, _i32p, _i32p, _i32p]),
+    "gi_kvmgr_append_tokens_cow": (_c_int, [_vp, _c_int, _c_int, _i32p, _i32p, _i32p, _i32p, _intp]),
+    "gi_kvmgr_block_refs": (_c_int, [_vp, ctypes.c_int32, _intp]),
+    "gi_prefix_create": (_c_int, [_vp, _c_int, ctypes.POINTER(_vp)]),
+    "gi_prefix_destroy": (None, [_vp]),
+    "gi_prefix_store": (_c_int, [_vp, _i32p, _c_int, _c_int]),
+    "gi_prefix_find_longest": (_c_int, [_vp, _i32p, _c_int, _intp, _intp]),
+    "gi_prefix_size": (_c_int, [_vp, _intp]),
+    "gi_paged_copy_pages": (_c_int, [_vp, _c_int, _vp, _vp]),
     "gi_paged_create": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_i64, _c_int,
                                  ctypes.POINTER(_vp)]),
     "gi_paged_destroy": (None, [_vp]),
@@ -214,6 +224,81 @@ class PagedKVManager:
         a = np.ascontiguousarray(ids, np.int32)
         _check(lib().gi_kvmgr_set_free_list(self._h, a.ctypes.data_as(_i32p), a.size))
 
+    # -- copy-on-write prefix sharing (replaces KVCache.ForkAt deep copies) --
+    def ForkSequence(self, src_seq, n_tokens):
+        """ForkAt(n_tokens) (kvcache.go:225-284) over shared pages: a new
+        sequence holding src_seq's first n_tokens tokens."""
+        sid = _c_int()
+        _check(lib().gi_kvmgr_fork_sequence(self._h, src_seq, n_tokens, ctypes.byref(sid)))
+        return sid.value
+
+    def AppendTokenCOW(self, seq_id):
+        """AppendToken with copy-on-write: (blockID, slot, copy_from), where
+        copy_from is -1 or the shared block to copy into blockID first."""
+        b, s, c = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+        _check(lib().gi_kvmgr_append_token_cow(self._h, seq_id, ctypes.byref(b), ctypes.byref(s),
+                                               ctypes.byref(c)))
+        return b.value, s.value, c.value
+
+    def AppendTokensCOW(self, seq_id, n):
+        """n tokens: (block_ids, slots, (copy_src, copy_dst)), the copy pair
+        (-1, -1) when no shared block was touched."""
+        import numpy as np
+        ids = np.zeros(max(n, 1), np.int32)
+        slots = np.zeros(max(n, 1), np.int32)
+        cs, cd = ctypes.c_int32(), ctypes.c_int32()
+        done = _c_int()
+        _check(lib().gi_kvmgr_append_tokens_cow(self._h, seq_id, n, ids.ctypes.data_as(_i32p),
+                                                slots.ctypes.data_as(_i32p), ctypes.byref(cs),
+                                                ctypes.byref(cd), ctypes.byref(done)))
+        return ids[:n], slots[:n], (cs.value, cd.value)
+
+    def BlockRefs(self, block_id):
+        r = _c_int()
+        _check(lib().gi_kvmgr_block_refs(self._h, block_id, ctypes.byref(r)))
+        return r.value
+
+
+class PrefixCache:
+    """NewPrefixCache(maxSize) (prefix_cache.go:20-28) over a PagedKVManager:
+    entries share pages with the sequences they were stored from, and a hit
+    returns a new sequence forked from the entry instead of a deep copy."""
+
+    def __init__(self, mgr, max_size):
+        h = _vp()
+        _check(lib().gi_prefix_create(mgr._h, max_size, ctypes.byref(h)))
+        self._h, self._mgr = h, mgr
+
+    def close(self):
+        if self._h and _lib is not None:
+            _lib.gi_prefix_destroy(self._h)
+        self._h = None
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            self.close()
+
+    def Store(self, tokens, seq_id):
+        """Store(tokens, kv) (prefix_cache.go:97-119); kv is the sequence."""
+        import numpy as np
+        a = np.ascontiguousarray(tokens, np.int32)
+        _check(lib().gi_prefix_store(self._h, a.ctypes.data_as(_i32p), a.size, seq_id))
+
+    def FindLongestPrefix(self, tokens):
+        """(matched length, new sequence id) or (0, None)
+        (prefix_cache.go:76-95)."""
+        import numpy as np
+        a = np.ascontiguousarray(tokens, np.int32)
+        m, sid = _c_int(), _c_int()
+        _check(lib().gi_prefix_find_longest(self._h, a.ctypes.data_as(_i32p), a.size,
+                                            ctypes.byref(m), ctypes.byref(sid)))
+        return (m.value, sid.value) if m.value else (0, None)
+
+    def __len__(self):
+        n = _c_int()
+        _check(lib().gi_prefix_size(self._h, ctypes.byref(n)))
+        return n.value
+
 
 def _ptr(t, dtype=None, what="tensor"):
     """Device pointer of a contiguous torch tensor (None -> NULL)."""
@@ -326,6 +411,16 @@ class PagedKVCache:
         _check(lib().gi_paged_gather(self._h, layer, _ptr(block_table, torch.int32, "block_table"),
                                      n_tok, _ptr(ko), _ptr(vo), 1 if widen else 0))
         return ko, vo
+
+    def CopyPages(self, src_ids, dst_ids):
+        """Page dst_ids[i] <- page src_ids[i] in every layer (device int32
+        tensors): the copy a copy-on-write append asks for."""
+        import torch
+        n = int(src_ids.numel())
+        if int(dst_ids.numel()) != n:
+            raise GIError(-3, "CopyPages: src_ids and dst_ids differ in length")
+        _check(lib().gi_paged_copy_pages(self._h, n, _ptr(src_ids, torch.int32, "src_ids"),
+                                         _ptr(dst_ids, torch.int32, "dst_ids")))
 
     # -- attention -------------------------------------------------------
     def AttentionGQA(self, out, q, layer, block_tables, seq_lens, num_heads, attn_scale,

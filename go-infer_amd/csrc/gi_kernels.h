@@ -18,6 +18,10 @@ hipError_t launch_append_at_len(const PoolLayout &L, uint8_t *base, int batch,
 hipError_t launch_gather(const PoolLayout &L, const uint8_t *base, const int32_t *table, int n_tok,
                          void *k_out, void *v_out, int widen, int *status, hipStream_t st);
 
+// Whole-page copies in every layer: page dst[i] <- page src[i].
+hipError_t launch_copy_pages(const PoolLayout &L, uint8_t *const *layer_base, int n, const int32_t *src,
+                             const int32_t *dst, int *status, hipStream_t st);
+
 // Attention over paged context.  Decode: q/out are [batch][num_heads][head_dim]
 // float32, block_tables is [batch][max_blocks], sequence b attends its first
 // seq_lens[b] tokens.  The same kernels serve chunked prefill on the vector

@@ -14,6 +14,8 @@
 #include "gi_common.h"
 #include "gi_kernels.h"
 
+#include <algorithm>
+
 namespace gi {
 
 namespace {
@@ -333,6 +335,50 @@ hipError_t launch_gather(const PoolLayout &L, const uint8_t *base, const int32_t
     }
 #undef GI_GATHER
     return hipGetLastError();
+}
+
+namespace {
+
+// Page copy: grid (chunks, pairs, layers), 16 bytes per thread and step.
+// Pairs with an id outside the pool are skipped and flagged.
+__global__ __launch_bounds__(kThreads) void copy_pages_kernel(uint8_t *const *layer_base, int64_t page_bytes,
+                                                              int64_t num_pages, const int32_t *src,
+                                                              const int32_t *dst, int *status)
+{
+    const int pair = blockIdx.y, layer = blockIdx.z;
+    const int64_t s = src[pair], d = dst[pair];
+    if (s < 0 || s >= num_pages || d < 0 || d >= num_pages) {
+        if (blockIdx.x == 0 && threadIdx.x == 0 && status)
+            atomicOr(status, FLAG_BAD_PAGE);
+        return;
+    }
+    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+    uint8_t *base = layer_base[layer];
+    const u4 *sp = reinterpret_cast<const u4 *>(base + s * page_bytes);
+    u4 *dp = reinterpret_cast<u4 *>(base + d * page_bytes);
+    const int64_t n16 = page_bytes / 16;
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n16; i += (int64_t)gridDim.x * kThreads)
+        dp[i] = sp[i];
+}
+
+} // namespace
+
+hipError_t launch_copy_pages(const PoolLayout &L, uint8_t *const *layer_base, int n, const int32_t *src,
+                             const int32_t *dst, int *status, hipStream_t st)
+{
+    if (n <= 0)
+        return hipSuccess;
+    const int64_t n16 = L.page_bytes / 16;
+    const unsigned gx = (unsigned)std::min<int64_t>((n16 + kThreads - 1) / kThreads, 64);
+    for (int i0 = 0; i0 < n; i0 += 65535) { // grid y limit
+        const int cnt = std::min(n - i0, 65535);
+        hipLaunchKernelGGL(copy_pages_kernel, dim3(gx, (unsigned)cnt, (unsigned)L.num_layers), dim3(kThreads),
+                           0, st, layer_base, L.page_bytes, L.num_pages, src + i0, dst + i0, status);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess)
+            return e;
+    }
+    return hipSuccess;
 }
 
 } // namespace gi

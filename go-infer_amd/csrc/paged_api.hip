@@ -36,6 +36,7 @@ struct gi_paged {
     int device = 0;
     int num_cus = 256;
     std::vector<uint8_t *> layer_base;
+    uint8_t **d_layer_base = nullptr; // the same pointers in device memory
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
     int *d_status = nullptr;
@@ -181,6 +182,16 @@ int gi_paged_create(int num_layers, int num_kv_heads, int head_dim, int page_tok
             rc = hip_fail(e, "gi_paged_create: clear");
     }
     if (rc == GI_OK) {
+        const size_t pb = sizeof(uint8_t *) * (size_t)num_layers;
+        if (hipMalloc((void **)&h->d_layer_base, pb) != hipSuccess) {
+            h->d_layer_base = nullptr;
+            rc = gi::set_error(GI_ERR_OOM, "gi_paged_create: layer table");
+        } else if ((e = hipMemcpy(h->d_layer_base, h->layer_base.data(), pb, hipMemcpyHostToDevice)) !=
+                   hipSuccess) {
+            rc = hip_fail(e, "gi_paged_create: layer table");
+        }
+    }
+    if (rc == GI_OK) {
         e = hipMemsetAsync(h->d_status, 0, sizeof(int), h->stream);
         if (e == hipSuccess)
             e = hipStreamSynchronize(h->stream);
@@ -209,6 +220,8 @@ void gi_paged_destroy(gi_paged *h)
         (void)hipFree(p);
     if (h->d_status)
         (void)hipFree(h->d_status);
+    if (h->d_layer_base)
+        (void)hipFree(h->d_layer_base);
     if (h->ws)
         (void)hipFree(h->ws);
     if (h->own_stream)
@@ -351,6 +364,20 @@ int gi_paged_append_at_len(gi_paged *h, int layer, int batch, const int32_t *blo
     hipError_t e = gi::launch_append_at_len(h->L, h->layer_base[(size_t)layer], batch, block_tables,
                                             max_blocks, seq_lens, k, v, h->d_status, h->stream);
     return e == hipSuccess ? GI_OK : hip_fail(e, "gi_paged_append_at_len");
+}
+
+int gi_paged_copy_pages(gi_paged *h, int n, const int32_t *src_ids, const int32_t *dst_ids)
+{
+    int rc = enter(h, "gi_paged_copy_pages");
+    if (rc)
+        return rc;
+    if (n < 0 || (n > 0 && (!src_ids || !dst_ids)))
+        return gi::set_error(GI_ERR_BAD_ARG, "gi_paged_copy_pages: bad argument");
+    if (n == 0)
+        return GI_OK;
+    std::lock_guard<std::mutex> g(h->mu);
+    hipError_t e = gi::launch_copy_pages(h->L, h->d_layer_base, n, src_ids, dst_ids, h->d_status, h->stream);
+    return e == hipSuccess ? GI_OK : hip_fail(e, "gi_paged_copy_pages");
 }
 
 int gi_paged_gather(gi_paged *h, int layer, const int32_t *block_table, int n_tok, void *k_out,

@@ -51,6 +51,7 @@ extern "C" {
 #define GI_ERR_HIP (-5)            /* HIP launch / runtime error            */
 #define GI_ERR_UNKNOWN_SEQ (-6)    /* paged_kv.go:111-114 "sequence %d not found" */
 #define GI_ERR_BAD_PAGE (-7)       /* a kernel saw a page id outside the pool */
+#define GI_ERR_SHARED_PAGE (-8)    /* the append would write a page another sequence shares */
 
 /* KV storage types.  f32 and q8_0 are kvcache.go:11-15's KVTypeF32 and
  * KVTypeQ8_0; f16 stores FP32ToFP16 (pkg/quant/fp16.go:38-69) halves. */
@@ -109,6 +110,58 @@ int gi_kvmgr_free_list(gi_kvmgr *m, int32_t *ids, int cap, int *n);
  * not held by a sequence.  Lets a caller start from a shuffled pool. */
 int gi_kvmgr_set_free_list(gi_kvmgr *m, const int32_t *ids, int n);
 
+/* ---- copy-on-write prefix sharing -------------------------------------- *
+ * Replaces the deep copies of KVCache.Clone / ForkAt (kvcache.go:217-284)
+ * and of PrefixCache's cloneKVCachePrefix (prefix_cache.go:122-150) with
+ * shared pages.  Every block carries a reference count: a fork takes a
+ * reference to the pages of its prefix, FreeSequence returns a block to the
+ * free list only when its last reference goes, and an append that would
+ * write a block with more than one reference first moves the appending
+ * sequence to a fresh copy of it (the caller copies the page on the device
+ * with gi_paged_copy_pages before writing). */
+
+/* ForkAt(n_tokens) (kvcache.go:225-284): a new sequence (*new_seq) whose
+ * first n_tokens tokens are src_seq's, sharing its pages.  n_tokens is
+ * clamped to [0, src length] as ForkAt clamps maxSlot to [0, MaxSeq]. */
+int gi_kvmgr_fork_sequence(gi_kvmgr *m, int src_seq, int n_tokens, int *new_seq);
+
+/* AppendToken with copy-on-write: as gi_kvmgr_append_token, and *copy_from
+ * is -1, or the shared block whose contents the caller must copy into
+ * *block_id (all layers, gi_paged_copy_pages) before writing the token.
+ * gi_kvmgr_append_token and gi_kvmgr_append_tokens return
+ * GI_ERR_SHARED_PAGE, changing nothing, where this call would copy. */
+int gi_kvmgr_append_token_cow(gi_kvmgr *m, int seq_id, int32_t *block_id, int32_t *slot,
+                              int32_t *copy_from);
+
+/* n tokens with copy-on-write; at most the first can need a copy, reported
+ * as *copy_src -> *copy_dst (both -1 when none). */
+int gi_kvmgr_append_tokens_cow(gi_kvmgr *m, int seq_id, int n, int32_t *block_ids,
+                               int32_t *slots, int32_t *copy_src, int32_t *copy_dst, int *done);
+
+/* References held on a block (0 when it is free). */
+int gi_kvmgr_block_refs(gi_kvmgr *m, int32_t block_id, int *refs);
+
+/* PrefixCache (prefix_cache.go:7-150) over shared pages.  max_size <= 0 ->
+ * 32 entries.  The cache holds a forked sequence per entry (its pages stay
+ * referenced until the entry is evicted or the cache destroyed). */
+typedef struct gi_prefix gi_prefix;
+int gi_prefix_create(gi_kvmgr *m, int max_size, gi_prefix **out);
+void gi_prefix_destroy(gi_prefix *pc);
+
+/* Store (prefix_cache.go:97-119): keeps tokens[0..n) of seq_id under the
+ * key tokens; no-op for n < 4.  A full cache first evicts one entry (the
+ * oldest; the reference drops whichever its map iteration yields). */
+int gi_prefix_store(gi_prefix *pc, const int32_t *tokens, int n, int seq_id);
+
+/* FindLongestPrefix (prefix_cache.go:76-95): the longest l in [1, n-1]
+ * with an entry keyed tokens[0..l); *matched = l and *new_seq = a new
+ * sequence forked from that entry (sharing its pages), or 0 and 0. */
+int gi_prefix_find_longest(gi_prefix *pc, const int32_t *tokens, int n, int *matched,
+                           int *new_seq);
+
+/* Number of entries. */
+int gi_prefix_size(gi_prefix *pc, int *n);
+
 /* ---- device page pool -------------------------------------------------- */
 
 typedef struct gi_paged gi_paged;
@@ -157,6 +210,11 @@ int gi_paged_append(gi_paged *h, int layer, int n_tok, const int32_t *block_ids,
 int gi_paged_append_at_len(gi_paged *h, int layer, int batch, const int32_t *block_tables,
                            int max_blocks, const int32_t *seq_lens, const float *k,
                            const float *v);
+
+/* Copies whole pages, every layer: page dst_ids[i] becomes a copy of page
+ * src_ids[i] (device int32 arrays of n ids; the copy-on-write step of a
+ * forked sequence, see gi_kvmgr_append_token_cow). */
+int gi_paged_copy_pages(gi_paged *h, int n, const int32_t *src_ids, const int32_t *dst_ids);
 
 /* Gathers tokens [0, n_tok) of one layer of one sequence into the contiguous
  * [n_tok][kv_dim] layout that KVCache indexes (kvcache.go:183-284).

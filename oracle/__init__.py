@@ -306,6 +306,65 @@ class PagedKVManager:
             self.FreeBlocks.extend(t["BlockIDs"])
 
 
+class RefKVCache:
+    """KVCache of pkg/engine/kvcache.go restated over stored bytes: per layer
+    a contiguous [MaxSeq][bytes_per_vec] K and V (f32, FP32ToFP16 halves or
+    34-byte q8_0 blocks, the formats of Write, kvcache.go:146-180).  ForkAt
+    (225-284) is a deep copy of slots [0, maxSlot), the rest zero.  Used as
+    the model that paged prefix sharing must reproduce."""
+
+    def __init__(self, kv_type, num_layers, kv_dim, max_seq):
+        self.kv_type, self.num_layers, self.kv_dim, self.max_seq = kv_type, num_layers, kv_dim, max_seq
+        self.bpv = bytes_per_vec(kv_type, kv_dim)
+        self.K = np.zeros((num_layers, max_seq, self.bpv), np.uint8)
+        self.V = np.zeros_like(self.K)
+        self.CurPos = 0
+
+    def Write(self, layer, slot, k, v):
+        if 0 <= layer < self.num_layers and 0 <= slot < self.max_seq:   # kvcache.go:147-149
+            self.K[layer, slot] = store_vectors(self.kv_type, np.reshape(k, (1, -1)))[0]
+            self.V[layer, slot] = store_vectors(self.kv_type, np.reshape(v, (1, -1)))[0]
+
+    def ForkAt(self, max_slot):
+        c = RefKVCache(self.kv_type, self.num_layers, self.kv_dim, self.max_seq)
+        c.CurPos = self.CurPos
+        n = min(max(max_slot, 0), self.max_seq)                          # kvcache.go:241-246
+        c.K[:, :n] = self.K[:, :n]
+        c.V[:, :n] = self.V[:, :n]
+        return c
+
+    def Clone(self):
+        return self.ForkAt(self.max_seq)                                 # kvcache.go:217-222
+
+
+class RefPrefixCache:
+    """PrefixCache of pkg/engine/prefix_cache.go:7-150: entries keyed by the
+    whole token list; FindLongestPrefix tries l = len-1 .. 1 (85-93); Store
+    ignores lists shorter than 4 (99-101) and, when full, drops one entry
+    first (106-112: whichever Go's randomised map iteration yields; here the
+    oldest, the choice the paged cache makes)."""
+
+    def __init__(self, max_size):
+        self.max_size = max_size if max_size > 0 else 32
+        self.entries = {}
+
+    def FindLongestPrefix(self, tokens):
+        for l in range(len(tokens) - 1, 0, -1):
+            e = self.entries.get(tuple(tokens[:l]))
+            if e is not None:
+                return l, e
+        return 0, None
+
+    def Store(self, tokens, kv):
+        if len(tokens) < 4:
+            return
+        if len(self.entries) >= self.max_size:
+            del self.entries[next(iter(self.entries))]
+        key = tuple(tokens)
+        self.entries.pop(key, None)
+        self.entries[key] = kv
+
+
 # ---- seeded synthetic inputs ------------------------------------------------
 
 _GOLDEN = np.uint64(0x9E3779B97F4A7C15)

@@ -360,3 +360,60 @@ def test_generator_is_counter_based(oracle):
     x = oracle.normal_with_outliers(5, (100000,))
     frac = float(np.mean(np.abs(x) == 8.0))
     assert 0.008 < frac < 0.012
+
+
+@pytest.mark.parametrize("kv_type", [0, 2])
+def test_kvcache_clone_and_fork_reference_test(oracle, kv_type):
+    # pkg/engine/kvcache_test.go:7-71 on the restated KVCache (f32 and q8_0)
+    c = oracle.RefKVCache(kv_type, 2, 64, 16)
+    c.CurPos = 4
+    k = np.arange(1, 65, dtype=np.float32)
+    v = k * 2
+    c.Write(0, 0, k, v)
+    c.Write(1, 1, k, v)
+    clone = c.Clone()
+    assert clone.CurPos == 4
+    got_k = oracle.widen(kv_type, 64, clone.K[0, 0:1])
+    want_k = oracle.widen(kv_type, 64, oracle.store_vectors(kv_type, k[None]))
+    assert np.array_equal(got_k, want_k)
+    if kv_type == 0:
+        assert got_k[0, 0] == 1.0 and oracle.widen(0, 64, clone.V[0, 0:1])[0, 0] == 2.0
+    forked = c.ForkAt(1)
+    assert np.array_equal(forked.K[0, 0], c.K[0, 0])
+    assert not forked.K[1, 1].any()  # slot 1 is past maxSlot: not copied
+    newk = np.zeros(64, np.float32)
+    newk[0] = 999.0
+    clone.Write(0, 0, newk, newk)
+    assert oracle.widen(kv_type, 64, c.K[0, 0:1])[0, 0] != 999.0
+    # out-of-range writes are ignored (kvcache.go:147-149)
+    before = c.K.copy()
+    c.Write(5, 0, k, v)
+    c.Write(0, 16, k, v)
+    assert np.array_equal(before, c.K)
+
+
+def test_prefix_cache_reference_tests(oracle):
+    # pkg/engine/prefix_cache_test.go:7-47 on the restated PrefixCache
+    pc = oracle.RefPrefixCache(10)
+    kv = oracle.RefKVCache(0, 4, 64, 128)
+    for l in range(4):
+        for t in range(10):
+            vals = np.arange(t * 64 + 1, t * 64 + 65, dtype=np.float32)
+            kv.Write(l, t, vals, vals + 1)
+    pc.Store([101, 202, 303, 404, 505], kv.Clone())
+    n, got = pc.FindLongestPrefix([101, 202, 303, 404, 505, 606, 707])
+    assert n == 5 and got is not None
+    assert np.array_equal(got.K[0, 0], kv.K[0, 0])
+    assert pc.FindLongestPrefix([999, 888, 777]) == (0, None)
+    # short lists are not stored; a full cache drops one entry first
+    pc2 = oracle.RefPrefixCache(2)
+    pc2.Store([1, 2, 3], kv)
+    assert len(pc2.entries) == 0
+    pc2.Store([1, 2, 3, 4], kv)
+    pc2.Store([1, 2, 3, 4, 5], kv)
+    pc2.Store([5, 6, 7, 8], kv)
+    assert len(pc2.entries) == 2 and (1, 2, 3, 4) not in pc2.entries
+    # the longest stored prefix wins; a query equal to a key does not match it
+    assert pc2.FindLongestPrefix([1, 2, 3, 4, 5, 6])[0] == 5
+    assert pc2.FindLongestPrefix([1, 2, 3, 4, 5])[0] == 0
+    assert oracle.RefPrefixCache(0).max_size == 32
