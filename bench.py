@@ -16,6 +16,9 @@ Prints one JSON line (see --help).  --config selects other shapes:
                       then causal paged attention over the context so far), all
                       32 layers; reports TFLOP/s of the attention
   llama8b_f16_prefill the same prefill over fp16 pages
+  llama8b_fork_b256   copy-on-write forks of 256 Llama-3-8B sequences (8197
+                      tokens, fp16): the page copy each fork's first append needs;
+                      reports GB/s of the copy against the reference's deep copy
 """
 import argparse
 import json
@@ -45,6 +48,11 @@ CONFIGS = {
                                         "paged attention", layers=32, q_heads=32, kv_heads=8,
                                head_dim=128, page_tokens=16, batch=4, context="4096", chunk=512,
                                frag=True, prefill=True, kv_dtype="q8_0"),
+    "llama8b_fork_b256": dict(workload="llama3-8b-shape copy-on-write fork: 256 sequences forked "
+                                        "mid-page, one append each (one page copy per fork, all "
+                                        "layers, whatever the context length)",
+                              layers=32, q_heads=32, kv_heads=8, head_dim=128, page_tokens=16,
+                              batch=256, context="8192", fork=True),
     "llama8b_f16_prefill": dict(workload="llama3-8b-shape fp16 chunked prefill: append + causal "
                                          "paged attention", layers=32, q_heads=32, kv_heads=8,
                                 head_dim=128, page_tokens=16, batch=4, context="4096", chunk=512,
@@ -225,6 +233,101 @@ def prefill_flops(cfg):
             * cfg["batch"])
 
 
+def run_fork(args, gi, torch, dev, cfg):
+    """Forks each of `batch` sequences at its full length (a partial last
+    page) and appends one token to every fork: the allocator hands out one
+    copy-on-write pair per fork, and gi_paged_copy_pages copies those pages in
+    all layers.  Times the device copy; the reference instead deep-copies the
+    whole contiguous cache per fork (KVCache.ForkAt, kvcache.go:225-284)."""
+    H, kvh, hd, P, layers = (cfg["q_heads"], cfg["kv_heads"], cfg["head_dim"],
+                             cfg["page_tokens"], cfg["layers"])
+    B, L = cfg["batch"], int(cfg["context"])
+    # only the partial last page is copied, so the sequences here hold 5
+    # tokens (one page each); the context length matters to the reference's
+    # deep copy, timed below at L tokens
+    tail = 5
+    need = 2 * B + 16
+    mgr = gi.PagedKVManager(layers, kvh * hd, need, P)
+    pool = gi.PagedKVCache(layers, kvh, hd, P, need, gi.KV_F16)
+    seqs = [mgr.AllocateSequence() for _ in range(B)]
+    for s in seqs:
+        mgr.AppendTokens(s, tail)
+    forks = [mgr.ForkSequence(s, tail) for s in seqs]
+    pairs = []
+    for f in forks:
+        _, _, (src, dst) = mgr.AppendTokensCOW(f, 1)
+        pairs.append((src, dst))
+    assert all(p[0] >= 0 for p in pairs), "every fork of a mid-page sequence copies one page"
+    src = torch.tensor([p[0] for p in pairs], dtype=torch.int32, device=dev)
+    dst = torch.tensor([p[1] for p in pairs], dtype=torch.int32, device=dev)
+    page_bytes = pool.page_bytes()[0]
+    moved = 2 * B * layers * page_bytes  # read + write
+    stream = torch.cuda.current_stream()
+    for _ in range(args.warmup):
+        pool.CopyPages(src, dst)
+    pool.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.steps):
+        pool.CopyPages(src, dst)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    pool.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    gbs = moved / (ms * 1e-3) / 1e9
+    log("fork copy %.3f ms for %d forks (%.1f MB moved, %.1f GB/s)" % (ms, B, moved / 1e6, gbs))
+    # parity: the copied page equals its source in every layer (sampled)
+    ok = True
+    if not args.no_parity:
+        for l in (0, layers - 1):
+            a, _ = pool.Get(l, src[:1].contiguous(), P)
+            b, _ = pool.Get(l, dst[:1].contiguous(), P)
+            pool.synchronize()
+            ok = ok and bool(torch.equal(a, b))
+    cpu = None
+    if not args.no_cpu_baseline:
+        # the reference's deep copy of one fork: ForkAt copies the contiguous
+        # f32 cache, 2 x MaxSeq x kvDim x 4 B per layer (timed for one layer)
+        kvd = kvh * hd
+        srcb = np.ones(L * kvd, np.float32)
+        dstb = np.empty_like(srcb)
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < 3.0:
+            np.copyto(dstb, srcb)
+            np.copyto(dstb, srcb)
+            n += 1
+        per_layer = (time.perf_counter() - t0) / n
+        per_fork = per_layer * layers
+        cpu = {"value": round(1.0 / per_fork, 4), "unit": "forks/s", "cores": 1, "kind": "port",
+               "sample": "%d deep copies of one layer's K and V (%d tokens x %d f32 each) on 1 "
+                         "thread, %.3f s per fork of %d layers" % (n, L, kvd, per_fork, layers)}
+    res = {
+        "metric": METRIC,
+        "value": round(B / (ms * 1e-3), 1),
+        "unit": "forks/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": cfg["workload"], "layers": layers, "kv_heads": kvh,
+                   "head_dim": hd, "kv_dtype": "f16", "page_tokens": P, "batch": B,
+                   "context": L},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "copy_pages_kernel", "bytes_per_launch": moved},
+        "cpu_baseline": cpu,
+        "parity": {"copied_pages_equal": ok, "pass": ok},
+    }
+    print(json.dumps(res), flush=True)
+    pool.close()
+
+
 def run_prefill(args, gi, torch, dev, cfg):
     """Whole 4096-token prefill in 512-token chunks, all layers."""
     H, kvh, hd, P, layers = (cfg["q_heads"], cfg["kv_heads"], cfg["head_dim"],
@@ -369,6 +472,9 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
     dev = torch.device("cuda:0")
     cfg = CONFIGS[args.config]
+    if cfg.get("fork"):
+        run_fork(args, gi, torch, dev, cfg)
+        return
     if cfg.get("prefill"):
         run_prefill(args, gi, torch, dev, cfg)
         return
