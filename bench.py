@@ -16,6 +16,12 @@ Prints one JSON line (see --help).  --config selects other shapes:
                       then causal paged attention over the context so far), all
                       32 layers; reports TFLOP/s of the attention
   llama8b_f16_prefill the same prefill over fp16 pages
+  llama8b_b256_8k_rope the headline step with RoPE fused into the append: per
+                      layer, q and k turned at position 8191 (theta 5e5) while
+                      k/v are stored, then the same paged attention
+  llama8b_b256_8k_q4  the headline step over Q4_0 pages (blocks of 32 4-bit
+                      values + fp16 scale, kvcache.go's KVTypeQ4_0): append
+                      with on-the-fly quantisation + paged attention
   llama8b_fork_b256   copy-on-write forks of 256 Llama-3-8B sequences (8197
                       tokens, fp16): the page copy each fork's first append needs;
                       reports GB/s of the copy against the reference's deep copy
@@ -38,6 +44,14 @@ CONFIGS = {
     "llama8b_b256_8k": dict(workload="llama3-8b-shape decode step: append + paged attention",
                             layers=32, q_heads=32, kv_heads=8, head_dim=128, page_tokens=16,
                             batch=256, context="8192", frag=True),
+    "llama8b_b256_8k_rope": dict(workload="llama3-8b-shape decode step: RoPE + append + paged "
+                                          "attention", layers=32, q_heads=32, kv_heads=8,
+                                 head_dim=128, page_tokens=16, batch=256, context="8192",
+                                 frag=True, rope_theta=500000.0),
+    "llama8b_b256_8k_q4": dict(workload="llama3-8b-shape decode step over q4_0 pages: append + "
+                                        "paged attention", layers=32, q_heads=32, kv_heads=8,
+                               head_dim=128, page_tokens=16, batch=256, context="8192",
+                               frag=True, kv_dtype="q4_0"),
     "llama8b_b32": dict(workload="llama3-8b-shape decode step, ragged context",
                         layers=32, q_heads=32, kv_heads=8, head_dim=128, page_tokens=16,
                         batch=32, context="U[512,4096]", frag=True),
@@ -135,16 +149,35 @@ def fill_pool(torch, pool, cfg, lens, bt, dev, seed):
     del kbuf, vbuf, ids_d, slots_d
 
 
+def vec_bytes(kv_dtype, kv_dim):
+    """Stored bytes of one token vector (kvcache.go:92-105)."""
+    return {"f32": 4 * kv_dim, "f16": 2 * kv_dim, "q8_0": kv_dim // 32 * 34,
+            "q4_0": kv_dim // 32 * 18}[kv_dtype]
+
+
+def kv_type_of(gi, kv_dtype):
+    return {"f32": gi.KV_F32, "f16": gi.KV_F16, "q8_0": gi.KV_Q8_0, "q4_0": gi.KV_Q4_0}[kv_dtype]
+
+
+def append_kernel_name(gi, kv_dtype, rope):
+    if rope:
+        return "rope_append<%d,true>" % kv_type_of(gi, kv_dtype)
+    return {"f32": "append_plain<0,true>", "f16": "append_plain<1,true>",
+            "q8_0": "append_q8<true>", "q4_0": "append_q4<true>"}[kv_dtype]
+
+
 def step_bytes(cfg, lens):
     """Algorithmic HBM bytes of one decode step, split into the attention
     kernel's and the append kernel's share (per step, all layers)."""
     P = cfg["page_tokens"]
     kv_dim = cfg["kv_heads"] * cfg["head_dim"]
     qd = cfg["q_heads"] * cfg["head_dim"]
-    e = 2  # fp16
+    bpv = vec_bytes(cfg.get("kv_dtype", "f16"), kv_dim)
     L = np.asarray(lens, np.int64)
-    attn = (2 * L * kv_dim * e + ((L + P - 1) // P) * 4 + qd * 4 + qd * 4 + 4).sum()
-    append = len(L) * (2 * kv_dim * 4 + 2 * kv_dim * e + 4 + 4)
+    attn = (2 * L * bpv + ((L + P - 1) // P) * 4 + qd * 4 + qd * 4 + 4).sum()
+    append = len(L) * (2 * kv_dim * 4 + 2 * bpv + 4 + 4)
+    if cfg.get("rope_theta"):
+        append += len(L) * (2 * qd * 4 + (kv_dim // 2) * 8)   # q read + written, cos/sin row
     return int(attn) * cfg["layers"], int(append) * cfg["layers"]
 
 
@@ -164,8 +197,8 @@ def profiled_traffic(kernel, workload):
 
 
 def cpu_baseline(oracle, cfg, budget_s=12.0):
-    """The oracle's decode (widen fp16 -> f32, then the reference loop of
-    forward.go:242-267) on one host core for a bounded sample of the same
+    """The oracle's decode (widen the stored vectors -> f32, then the
+    reference loop of forward.go:242-267) on one host core for a bounded sample of the same
     workload: whole (sequence, layer) units at the configured context,
     repeated until about budget_s of CPU work; extrapolated to the full
     step by the number of units."""
@@ -173,13 +206,14 @@ def cpu_baseline(oracle, cfg, budget_s=12.0):
     kv_dim = kvh * hd
     lens = seq_lengths(cfg, 11)
     L = int(np.median(lens))
-    k = oracle.fp32_to_fp16(oracle.normal(1, (L, kv_dim))).view(np.uint8).reshape(L, 2 * kv_dim)
-    v = oracle.fp32_to_fp16(oracle.normal(2, (L, kv_dim))).view(np.uint8).reshape(L, 2 * kv_dim)
+    kt = {"f32": 0, "f16": 1, "q8_0": 2, "q4_0": 3}[cfg.get("kv_dtype", "f16")]
+    k = oracle.store_vectors(kt, oracle.normal(1, (L, kv_dim)))
+    v = oracle.store_vectors(kt, oracle.normal(2, (L, kv_dim)))
     q = oracle.normal(3, (1, H * hd))
     sc = oracle.attn_scale(hd)
     units, t0 = 0, time.perf_counter()
     while True:
-        oracle.decode_batch(1, q, k, v, np.zeros(1, np.int64), np.array([L], np.int32), H, kvh,
+        oracle.decode_batch(kt, q, k, v, np.zeros(1, np.int64), np.array([L], np.int32), H, kvh,
                             hd, sc)
         units += 1
         el = time.perf_counter() - t0
@@ -490,7 +524,8 @@ def main():
                                                            time.perf_counter() - t_setup))
     stream = torch.cuda.Stream(dev)
     torch.cuda.set_stream(stream)
-    pool = gi.PagedKVCache(layers, kvh, hd, P, pages, gi.KV_F16, stream=stream)
+    kv_dtype = cfg.get("kv_dtype", "f16")
+    pool = gi.PagedKVCache(layers, kvh, hd, P, pages, kv_type_of(gi, kv_dtype), stream=stream)
     pool.set_decode_kernel(args.decode_kernel)
     log("pool: %.1f GiB" % (pool.page_bytes()[1] / 2**30))
     fill_pool(torch, pool, cfg, lens, bt, dev, args.seed)
@@ -509,10 +544,20 @@ def main():
     n_ev = layers * args.steps
     ev0 = [torch.cuda.Event(enable_timing=True) for _ in range(n_ev)]
     ev1 = [torch.cuda.Event(enable_timing=True) for _ in range(n_ev)]
+    eva = [torch.cuda.Event(enable_timing=True) for _ in range(n_ev)]
+    rope = cfg.get("rope_theta")
+    if rope:
+        pool.SetRoPE(rope, 0, max_len)
 
     def step(record=None):
         for l in range(layers):
-            pool.WriteAtLen(l, bt_d, sl_d, kn[l], vn[l])
+            if record is not None:
+                eva[record + l].record(stream)
+            if rope:
+                # q turned in place at position seq_lens-1, k turned and stored
+                pool.RoPEWriteAtLen(l, bt_d, sl_d, q[l], kn[l], vn[l])
+            else:
+                pool.WriteAtLen(l, bt_d, sl_d, kn[l], vn[l])
             if record is not None:
                 ev0[record + l].record(stream)
             pool.AttentionGQA(out[l], q[l], l, bt_d, sl_d, H, scale, max_len)
@@ -535,6 +580,7 @@ def main():
     pool.synchronize()
     ms_step = s0.elapsed_time(s1) / args.steps
     attn_ms = float(np.mean([a.elapsed_time(b) for a, b in zip(ev0, ev1)]))
+    app_ms = float(np.mean([a.elapsed_time(b) for a, b in zip(eva, ev0)]))
     attn_bytes, app_bytes = step_bytes(cfg, lens)
     tot_gbs = (attn_bytes + app_bytes) / (ms_step * 1e-3) / 1e9
     attn_gbs = (attn_bytes / layers) / (attn_ms * 1e-3) / 1e9
@@ -577,7 +623,8 @@ def main():
         cpu = cpu_baseline(oracle, cfg)
 
     kind = pool.decode_kernel(H)
-    kname = ("attn_mfma_f16<%d>" % hd) if kind == 1 else ("attn_valu<1,%d,%d>" % (hd, H // kvh))
+    kname = (("attn_mfma_f16<%d>" % hd) if kind == 1 else
+             ("attn_valu<%d,%d,%d>" % (kv_type_of(gi, kv_dtype), hd, H // kvh)))
     traffic = profiled_traffic(kname, args.config)
     res = {
         "metric": METRIC,
@@ -590,15 +637,18 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16",
+        "dtype": {"f32": "f32", "f16": "f16"}.get(kv_dtype, "f32 (%s pages)" % kv_dtype),
         "data": "synthetic",
         "config": {"workload": cfg["workload"], "layers": layers, "q_heads": H,
-                   "kv_heads": kvh, "head_dim": hd, "kv_dtype": "f16", "page_tokens": P,
+                   "kv_heads": kvh, "head_dim": hd, "kv_dtype": kv_dtype, "page_tokens": P,
                    "batch": batch, "context": cfg["context"], "pool_pages": pages,
-                   "fragmented_pool": cfg["frag"]},
+                   "fragmented_pool": cfg["frag"], "rope_theta": rope},
         "hbm_frac_of_peak": round(tot_gbs / HBM_PEAK_GBS, 4),
         "tokens_per_s": round(tok_s, 1),
         "decode_kernel": ["vector-alu", "matrix-core"][kind],
+        "append_kernel": append_kernel_name(gi, kv_dtype, rope),
+        "append_ms_per_launch": round(app_ms, 4),
+        "append_gbs": round((app_bytes / layers) / (app_ms * 1e-3) / 1e9, 1),
         "roofline": {"bound": "hbm", "achieved": round(attn_gbs, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(attn_gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic[0] if traffic else None,

@@ -22,12 +22,12 @@ import ctypes
 import os
 
 __all__ = ["lib", "GIError", "PagedKVManager", "PagedKVCache", "PrefixCache", "KV_F32", "KV_F16",
-           "KV_Q8_0", "EXPORTS", "LIB_PATH", "attn_scale"]
+           "KV_Q8_0", "KV_Q4_0", "EXPORTS", "LIB_PATH", "attn_scale"]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libgoinfer_paged.so")
 
-KV_F32, KV_F16, KV_Q8_0 = 0, 1, 2
+KV_F32, KV_F16, KV_Q8_0, KV_Q4_0 = 0, 1, 2, 3
 GI_OK = 0
 ERR_NAMES = {-1: "GI_ERR_NO_DEVICE", -2: "GI_ERR_OOM", -3: "GI_ERR_BAD_ARG",
              -4: "GI_ERR_POOL_EXHAUSTED", -5: "GI_ERR_HIP", -6: "GI_ERR_UNKNOWN_SEQ",
@@ -81,6 +81,13 @@ EXPORTS = {
                                       _c_int, _vp, _c_int, ctypes.c_float]),
     "gi_paged_prefill_attention": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp,
                                             _c_int, _vp, ctypes.c_float]),
+    "gi_paged_set_rope": (_c_int, [_vp, ctypes.c_float, _c_int, _c_int]),
+    "gi_paged_rope_append": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp,
+                                      _vp]),
+    "gi_paged_rope_append_at_len": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _c_int, _vp, _vp,
+                                             _vp, _vp, _vp]),
+    "gi_paged_rope_decode_step": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp,
+                                           _c_int, _vp, _c_int, ctypes.c_float]),
     "gi_paged_decode_kernel": (_c_int, [_vp, _c_int]),
     "gi_paged_set_decode_kernel": (_c_int, [_vp, _c_int]),
 }
@@ -315,8 +322,8 @@ def _ptr(t, dtype=None, what="tensor"):
 
 class PagedKVCache:
     """Device page pool for num_layers layers (one page id covers every
-    layer, like KVBlock in paged_kv.go:13-38).  kv_type: KV_F32, KV_F16 or
-    KV_Q8_0."""
+    layer, like KVBlock in paged_kv.go:13-38).  kv_type: KV_F32, KV_F16,
+    KV_Q8_0 or KV_Q4_0."""
 
     def __init__(self, num_layers, num_kv_heads, head_dim, page_tokens, num_pages,
                  kv_type=KV_F32, stream=None):
@@ -348,12 +355,14 @@ class PagedKVCache:
         return self._h
 
     def bytes_per_vec(self):
-        """Stored bytes of one token vector (kvcache.go:92: q8_0 is
-        ((kvDim+31)/32)*34)."""
+        """Stored bytes of one token vector (kvcache.go:92-105: q8_0 is
+        ((kvDim+31)/32)*34, q4_0 ((kvDim+31)/32)*18)."""
         if self.kv_type == KV_F32:
             return 4 * self.kv_dim
         if self.kv_type == KV_F16:
             return 2 * self.kv_dim
+        if self.kv_type == KV_Q4_0:
+            return (self.kv_dim + 31) // 32 * 18
         return (self.kv_dim + 31) // 32 * 34
 
     def page_bytes(self):
@@ -446,6 +455,58 @@ class PagedKVCache:
         if max_seq_len is None:
             max_seq_len = int(seq_lens.max().item()) if batch else 0
         _check(lib().gi_paged_decode_step(
+            self._h, layer, batch, num_heads, _ptr(q, torch.float32, "q"),
+            _ptr(k, torch.float32, "k"), _ptr(v, torch.float32, "v"),
+            _ptr(out, torch.float32, "out"), _ptr(block_tables, torch.int32, "block_tables"),
+            int(block_tables.shape[1]) if batch else 0, _ptr(seq_lens, torch.int32, "seq_lens"),
+            int(max_seq_len), float(attn_scale)))
+
+    # -- RoPE fused with the append (forward.go:228-240, 527-545) ------------
+    def SetRoPE(self, theta, rope_dim=0, max_positions=8192):
+        """Table of ApplyRoPE's (cos, sin) (pkg/math/kernels.go:22-35) for
+        positions [0, max_positions); rope_dim 0 means head_dim."""
+        _check(lib().gi_paged_set_rope(self._h, float(theta), int(rope_dim), int(max_positions)))
+
+    def RoPEWrite(self, layer, positions, block_ids, slots, q, k, v, q_out=None):
+        """ApplyRoPE on q [n, num_heads*head_dim] (into q_out, default in
+        place) and k [n, kv_dim] at positions[i], then Write of k, v."""
+        import torch
+        n = int(block_ids.numel())
+        num_heads = 0
+        if q is not None:
+            num_heads = int(q.shape[-1]) // self.head_dim
+            if q_out is None:
+                q_out = q
+        _check(lib().gi_paged_rope_append(
+            self._h, layer, n, num_heads, _ptr(positions, torch.int32, "positions"),
+            _ptr(block_ids, torch.int32, "block_ids"), _ptr(slots, torch.int32, "slots"),
+            _ptr(q, torch.float32, "q"), _ptr(q_out, torch.float32, "q_out"),
+            _ptr(k, torch.float32, "k"), _ptr(v, torch.float32, "v")))
+
+    def RoPEWriteAtLen(self, layer, block_tables, seq_lens, q, k, v, q_out=None):
+        """Decode form: token b at position seq_lens[b]-1 of sequence b."""
+        import torch
+        batch = int(seq_lens.numel())
+        num_heads = 0
+        if q is not None:
+            num_heads = int(q.shape[-1]) // self.head_dim
+            if q_out is None:
+                q_out = q
+        _check(lib().gi_paged_rope_append_at_len(
+            self._h, layer, batch, num_heads, _ptr(block_tables, torch.int32, "block_tables"),
+            int(block_tables.shape[1]) if batch else 0, _ptr(seq_lens, torch.int32, "seq_lens"),
+            _ptr(q, torch.float32, "q"), _ptr(q_out, torch.float32, "q_out"),
+            _ptr(k, torch.float32, "k"), _ptr(v, torch.float32, "v")))
+
+    def RoPEDecodeStep(self, out, q, k, v, layer, block_tables, seq_lens, num_heads, attn_scale,
+                       max_seq_len=None):
+        """forward.go:228-267 for a batch: q (rotated in place) and k turned
+        at position seq_lens[b]-1, k/v appended, then decode attention."""
+        import torch
+        batch = int(seq_lens.numel())
+        if max_seq_len is None:
+            max_seq_len = int(seq_lens.max().item()) if batch else 0
+        _check(lib().gi_paged_rope_decode_step(
             self._h, layer, batch, num_heads, _ptr(q, torch.float32, "q"),
             _ptr(k, torch.float32, "k"), _ptr(v, torch.float32, "v"),
             _ptr(out, torch.float32, "out"), _ptr(block_tables, torch.int32, "block_tables"),

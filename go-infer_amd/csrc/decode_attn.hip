@@ -40,6 +40,17 @@ __device__ __forceinline__ void load8_k(const uint8_t *pg, const PoolLayout &L, 
             o[2 * i] = half_bits_to_float(u[i] & 0xFFFFu);
             o[2 * i + 1] = half_bits_to_float(u[i] >> 16);
         }
+    } else if (KT == KV_Q4_0) {
+        // dims d0..d0+7 of one block: the low nibbles of bytes j..j+7 when
+        // d0 % 32 < 16, else the high nibbles of bytes j-16..j-9
+        const int blk = d0 >> 5, j = d0 & 31;
+        uint2 w = *reinterpret_cast<const uint2 *>(pg + L.k_off + (row * (HD / 32) + blk) * 16 + (j & 15));
+        float sc = half_bits_to_float(reinterpret_cast<const uint16_t *>(pg + L.ks_off)[row * (HD / 32) + blk]);
+        const int sh = j & 16 ? 4 : 0;
+        uint32_t u[2] = {w.x, w.y};
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            o[i] = (float)((int)((u[i >> 2] >> (8 * (i & 3) + sh)) & 15) - 8) * sc;
     } else {
         uint2 w = *reinterpret_cast<const uint2 *>(pg + L.k_off + row * HD + d0);
         float sc = half_bits_to_float(
@@ -63,6 +74,13 @@ __device__ __forceinline__ float load_v(const uint8_t *pg, const PoolLayout &L, 
         return reinterpret_cast<const float *>(pg + L.v_off)[idx];
     if (KT == KV_F16)
         return half_bits_to_float(reinterpret_cast<const uint16_t *>(pg + L.v_off)[idx]);
+    if (KT == KV_Q4_0) {
+        const int blk = d >> 5, j = d & 31;
+        const int64_t bi = (int64_t)kvh * (HD / 32) + blk;
+        const uint8_t b = pg[L.v_off + (bi * 16 + (j & 15)) * L.page_tokens + s];
+        const float sc = half_bits_to_float(reinterpret_cast<const uint16_t *>(pg + L.vs_off)[bi * L.page_tokens + s]);
+        return (float)((int)((j & 16 ? b >> 4 : b) & 15) - 8) * sc;
+    }
     float sc = half_bits_to_float(reinterpret_cast<const uint16_t *>(
         pg + L.vs_off)[((int64_t)kvh * (HD / 32) + (d >> 5)) * L.page_tokens + s]);
     return (float)reinterpret_cast<const int8_t *>(pg + L.v_off)[idx] * sc;
@@ -368,6 +386,7 @@ hipError_t launch_decode(const DecodeArgs &a, hipStream_t st)
         switch (L.kv_type) {
         case KV_F32: e = launch_valu_kt<KV_F32>(a, grid, st); break;
         case KV_F16: e = launch_valu_kt<KV_F16>(a, grid, st); break;
+        case KV_Q4_0: e = launch_valu_kt<KV_Q4_0>(a, grid, st); break;
         default: e = launch_valu_kt<KV_Q8_0>(a, grid, st); break;
         }
     }

@@ -11,6 +11,11 @@
 //               V  int8 [kv_head][head_dim][token]
 //               KS fp16 [kv_head][token][head_dim/32]      block scales
 //               VS fp16 [kv_head][head_dim/32][token]      block scales
+//   q4_0        K  u8 [kv_head][token][head_dim/32][16]    byte j of a block:
+//                                                          dim j | dim j+16 << 4
+//               V  u8 [kv_head][head_dim/32][16][token]    the same pairs,
+//                                                          token fastest
+//               KS, VS fp16 as q8_0
 //
 // K is token-major so a (page, kv_head) K tile is one contiguous run whose
 // rows feed the matrix-core A operand directly; V is stored dimension-major
@@ -24,7 +29,7 @@
 
 namespace gi {
 
-enum KvType : int { KV_F32 = 0, KV_F16 = 1, KV_Q8_0 = 2 };
+enum KvType : int { KV_F32 = 0, KV_F16 = 1, KV_Q8_0 = 2, KV_Q4_0 = 3 };
 
 struct PoolLayout {
     int kv_type;
@@ -33,11 +38,11 @@ struct PoolLayout {
     int head_dim;
     int page_tokens;
     int64_t num_pages;
-    int elt_bytes;      // 4, 2 or 1
+    int elt_bytes;      // 4, 2 or 1 (q4_0: 1, two values per byte)
     int64_t k_off;      // byte offsets inside one (layer, page) block
     int64_t v_off;
-    int64_t ks_off;     // q8_0 only
-    int64_t vs_off;     // q8_0 only
+    int64_t ks_off;     // q8_0 / q4_0 only
+    int64_t vs_off;     // q8_0 / q4_0 only
     int64_t page_bytes; // bytes of one (layer, page) block, 256-aligned
 };
 
@@ -47,11 +52,11 @@ inline int make_layout(int kv_type, int num_layers, int kvh, int hd, int P,
 {
     if (num_layers <= 0 || kvh <= 0 || hd <= 0 || P <= 0 || num_pages <= 0)
         return -1;
-    if (kv_type != KV_F32 && kv_type != KV_F16 && kv_type != KV_Q8_0)
+    if (kv_type != KV_F32 && kv_type != KV_F16 && kv_type != KV_Q8_0 && kv_type != KV_Q4_0)
         return -1;
     if (hd % 8 != 0)
         return -1;
-    if (kv_type == KV_Q8_0 && hd % 32 != 0)
+    if ((kv_type == KV_Q8_0 || kv_type == KV_Q4_0) && hd % 32 != 0)
         return -1;
     PoolLayout L{};
     L.kv_type = kv_type;
@@ -62,10 +67,12 @@ inline int make_layout(int kv_type, int num_layers, int kvh, int hd, int P,
     L.num_pages = num_pages;
     L.elt_bytes = kv_type == KV_F32 ? 4 : (kv_type == KV_F16 ? 2 : 1);
     int64_t tile = (int64_t)kvh * P * hd * L.elt_bytes;
+    if (kv_type == KV_Q4_0)
+        tile /= 2;
     L.k_off = 0;
     L.v_off = tile;
     int64_t end = 2 * tile;
-    if (kv_type == KV_Q8_0) {
+    if (kv_type == KV_Q8_0 || kv_type == KV_Q4_0) {
         int64_t sc = (int64_t)kvh * P * (hd / 32) * 2;
         L.ks_off = end;
         L.vs_off = end + sc;
@@ -171,6 +178,45 @@ __device__ __host__ __forceinline__ int q8_quant(float x, float inv)
     return (int)t;
 }
 
+// Q4_0 block scale (pkg/quant/quant.go:478-490): scale = amax/7 in float,
+// truncated to fp16 and widened back, inverse = 1/scale; the divisions are
+// done in double and rounded once, as for q8_scale.
+__device__ __host__ __forceinline__ uint32_t q4_scale(float amax, float *inv)
+{
+    float scale = (float)((double)amax / 7.0);
+    uint32_t d16 = 0;
+    if (scale > 0.0f) {
+        d16 = float_to_half_bits_rtz(scale);
+        scale = half_bits_to_float(d16);
+    }
+    float iv = 0.0f;
+    if (scale > 0.0f)
+        iv = (float)(1.0 / (double)scale);
+    *inv = iv;
+    return d16;
+}
+
+// One Q4_0 nibble (quant.go:494-502): int(math.Round(x*inv)) + 8 clamped to
+// [0, 15], 8 when the inverse is 0.  Go's amd64 int() of a NaN is the
+// minimum int64, which clamps to 0.  |x*inv| stays below 15 for finite x
+// (the fp16 scale is at least half of amax/7), so the rounding is exact.
+__device__ __host__ __forceinline__ int q4_quant(float x, float inv)
+{
+    if (!(inv > 0.0f))
+        return 8;
+    float v = x * inv;
+    if (v != v)
+        return 0;
+    float t = __builtin_truncf(v);
+    float fr = v - t;
+    if (fr >= 0.5f)
+        t += 1.0f;
+    else if (fr <= -0.5f)
+        t -= 1.0f;
+    int q = (int)t + 8;
+    return q < 0 ? 0 : (q > 15 ? 15 : q);
+}
+
 // |x| as an orderable key for the block maximum.  NaN inputs are skipped by
 // the reference's `v > maxVal` compare (quant.go:420-423), so they map to 0.
 __device__ __host__ __forceinline__ uint32_t abs_key(float x)
@@ -195,6 +241,6 @@ __device__ __host__ __forceinline__ int pow2_exponent_for(float max_abs)
 }
 
 // Error flag bits raised by kernels into the handle's device status word.
-enum : int { FLAG_BAD_PAGE = 1, FLAG_BAD_SLOT = 2 };
+enum : int { FLAG_BAD_PAGE = 1, FLAG_BAD_SLOT = 2, FLAG_BAD_POS = 4 };
 
 } // namespace gi

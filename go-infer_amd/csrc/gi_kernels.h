@@ -15,6 +15,28 @@ hipError_t launch_append_at_len(const PoolLayout &L, uint8_t *base, int batch,
                                 const int32_t *seq_lens, const float *k, const float *v,
                                 int *status, hipStream_t st);
 
+// Fused rotary embedding + append (pkg/math/kernels.go:22-35 ApplyRoPE on
+// every q and k head, then the store of forward.go:236-240 / 527-545).
+// table holds (cos, sin) of pair j at position p at table[p * rope_half + j]
+// for p < max_pos.  Token i's position is positions[i] (explicit form, with
+// block_ids/slots) or seq_lens[i] - 1 (decode form, with block_tables).
+// q [n_tok][num_heads][head_dim] is rotated into q_out (q_out may be q);
+// num_heads may be 0 (no q).  K is rotated and stored, V stored as is.
+struct RopeArgs {
+    const float2 *table;
+    int rope_half; // rope_dim / 2
+    int max_pos;
+    int num_heads;
+    const int32_t *positions; // explicit form only
+    const float *q;
+    float *q_out;
+};
+
+hipError_t launch_rope_append(const PoolLayout &L, uint8_t *base, int n_tok, const int32_t *block_ids,
+                              const int32_t *slots, const int32_t *block_tables, int max_blocks,
+                              const int32_t *seq_lens, const RopeArgs &R, const float *k,
+                              const float *v, int *status, hipStream_t st);
+
 hipError_t launch_gather(const PoolLayout &L, const uint8_t *base, const int32_t *table, int n_tok,
                          void *k_out, void *v_out, int widen, int *status, hipStream_t st);
 

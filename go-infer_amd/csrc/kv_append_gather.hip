@@ -8,6 +8,9 @@
 //   q8_0 : QuantizeQ8_0 of the whole kv_dim vector (kvcache.go:152-161,
 //          pkg/quant/quant.go:407-456), blocks of 32 never straddle a head
 //          because head_dim % 32 == 0.
+//   q4_0 : QuantizeQ4_0 likewise (kvcache.go:162-171, quant.go:458-521).
+// The fused form applies RoPE (pkg/math/kernels.go:22-35) to q and K first,
+// as Forward does before its store (forward.go:228-240, 527-545).
 // Gather (KVCache.Get / ForkAt, kvcache.go:183-284) rebuilds tokens [0, n)
 // of one sequence from its block table: token t lives at
 // (block_table[t / page_tokens], t % page_tokens) (paged_kv.go:107-131).
@@ -167,6 +170,57 @@ __global__ __launch_bounds__(kThreads) void append_q8(PoolLayout L, uint8_t *bas
     }
 }
 
+// Q4_0 quantise-and-store of element e of one token vector (slot s of page
+// pg), called by all 32 lanes of the block's lane group: lane j < 16 writes
+// byte j of the K and of the V block (element j low, element j + 16 high,
+// quant.go:504), lane 0 the two fp16 scales.  ok == false only joins the
+// shuffles.
+__device__ __forceinline__ void quant_store_q4(const PoolLayout &L, uint8_t *pg, int s, int e, float kx,
+                                               float vx, bool ok)
+{
+    const int hd = L.head_dim, nb = hd / 32, P = L.page_tokens;
+    float kinv, vinv;
+    uint32_t kd = q4_scale(__builtin_bit_cast(float, max32(abs_key(kx))), &kinv);
+    uint32_t vd = q4_scale(__builtin_bit_cast(float, max32(abs_key(vx))), &vinv);
+    const int kq = q4_quant(kx, kinv), vq = q4_quant(vx, vinv);
+    const int kq_hi = __shfl_down(kq, 16, 32), vq_hi = __shfl_down(vq, 16, 32);
+    if (!ok)
+        return;
+    const int kvh = e / hd, d = e - kvh * hd, blk = d >> 5, j = d & 31;
+    if (j < 16) {
+        pg[L.k_off + (((int64_t)kvh * P + s) * nb + blk) * 16 + j] = (uint8_t)(kq | (kq_hi << 4));
+        pg[L.v_off + (((int64_t)kvh * nb + blk) * 16 + j) * P + s] = (uint8_t)(vq | (vq_hi << 4));
+    }
+    if (j == 0) {
+        reinterpret_cast<uint16_t *>(pg + L.ks_off)[((int64_t)kvh * P + s) * nb + blk] = (uint16_t)kd;
+        reinterpret_cast<uint16_t *>(pg + L.vs_off)[((int64_t)kvh * nb + blk) * P + s] = (uint16_t)vd;
+    }
+}
+
+// q4_0 append: 32 consecutive threads quantise one block of 32 elements
+// (QuantizeQ4_0 of the whole kv_dim vector, kvcache.go:162-171).
+template <bool AT_LEN>
+__global__ __launch_bounds__(kThreads) void append_q4(PoolLayout L, uint8_t *base, int n_tok,
+                                                      Dest D, const float *__restrict__ k,
+                                                      const float *__restrict__ v, int *status)
+{
+    const int kv_dim = L.num_kv_heads * L.head_dim;
+    const int64_t total = (int64_t)n_tok * kv_dim; // multiple of 32
+    for (int64_t e0 = (int64_t)blockIdx.x * kThreads; e0 < total;
+         e0 += (int64_t)gridDim.x * kThreads) {
+        int64_t e = e0 + threadIdx.x;
+        // whole 32-lane groups are in or out of range (see append_q8)
+        if (e >= total)
+            break;
+        int i = (int)(e / kv_dim);
+        int j = (int)(e - (int64_t)i * kv_dim);
+        int64_t page = 0;
+        int s = 0;
+        bool ok = resolve(D, L, i, &page, &s, j == 0 ? status : nullptr);
+        quant_store_q4(L, base + page * L.page_bytes, s, j, k[e], v[e], ok);
+    }
+}
+
 // Gather one sequence's tokens [0, n_tok) of one layer.
 //   widen == 0: stored format, the reference's bytes per token vector
 //               (f32: 4*kv_dim, f16: 2*kv_dim, q8_0: kv_dim/32 blocks of
@@ -182,8 +236,10 @@ __global__ __launch_bounds__(kThreads) void gather_kernel(PoolLayout L, const ui
     const int kv_dim = L.num_kv_heads * hd;
     const int P = L.page_tokens;
     const int nb = hd / 32;
-    // Units per token: one per element, except raw q8_0: one per byte.
-    const int per_tok = (KT == KV_Q8_0 && !WIDEN) ? (kv_dim / 32) * 34 : kv_dim;
+    // Units per token: one per element, except raw q8_0 / q4_0: one per byte.
+    const int per_tok = (KT == KV_Q8_0 && !WIDEN) ? (kv_dim / 32) * 34
+                        : (KT == KV_Q4_0 && !WIDEN) ? (kv_dim / 32) * 18
+                                                    : kv_dim;
     const int64_t total = (int64_t)n_tok * per_tok;
     for (int64_t e = (int64_t)blockIdx.x * kThreads + threadIdx.x; e < total;
          e += (int64_t)gridDim.x * kThreads) {
@@ -197,6 +253,34 @@ __global__ __launch_bounds__(kThreads) void gather_kernel(PoolLayout L, const ui
             continue;
         }
         const uint8_t *pg = base + page * L.page_bytes;
+        if (KT == KV_Q4_0) {
+            // 18-byte blocks: LE fp16 scale, then byte j = dim j | dim j+16 << 4
+            int b, r;
+            if (WIDEN) {
+                b = u >> 5;
+                r = 2 + (u & 15); // the byte holding dim u & 31
+            } else {
+                b = u / 18;
+                r = u - b * 18;
+            }
+            const int kvh = b / nb, blk = b - kvh * nb;
+            const uint16_t ks = reinterpret_cast<const uint16_t *>(pg + L.ks_off)[((int64_t)kvh * P + s) * nb + blk];
+            const uint16_t vs = reinterpret_cast<const uint16_t *>(pg + L.vs_off)[((int64_t)kvh * nb + blk) * P + s];
+            uint8_t kb = 0, vb = 0;
+            if (r >= 2) {
+                kb = pg[L.k_off + (((int64_t)kvh * P + s) * nb + blk) * 16 + (r - 2)];
+                vb = pg[L.v_off + (((int64_t)kvh * nb + blk) * 16 + (r - 2)) * P + s];
+            }
+            if (WIDEN) { // (nibble - 8) * d (quant.go:103-110)
+                const int sh = (u & 16) ? 4 : 0;
+                reinterpret_cast<float *>(kout)[e] = (float)(((kb >> sh) & 15) - 8) * half_bits_to_float(ks);
+                reinterpret_cast<float *>(vout)[e] = (float)(((vb >> sh) & 15) - 8) * half_bits_to_float(vs);
+            } else {
+                kout[e] = r == 0 ? (uint8_t)(ks & 0xFF) : r == 1 ? (uint8_t)(ks >> 8) : kb;
+                vout[e] = r == 0 ? (uint8_t)(vs & 0xFF) : r == 1 ? (uint8_t)(vs >> 8) : vb;
+            }
+            continue;
+        }
         if (KT == KV_Q8_0 && !WIDEN) {
             int b = u / 34, r = u - b * 34; // global 32-block index and byte
             int kvh = b / nb, blk = b - kvh * nb;
@@ -279,6 +363,12 @@ hipError_t append_any(const PoolLayout &L, uint8_t *base, int n_tok, const Dest 
         else
             GI_APPEND((append_plain<KV_F16, false>));
         break;
+    case KV_Q4_0:
+        if (at_len)
+            GI_APPEND(append_q4<true>);
+        else
+            GI_APPEND(append_q4<false>);
+        break;
     default:
         if (at_len)
             GI_APPEND(append_q8<true>);
@@ -288,6 +378,128 @@ hipError_t append_any(const PoolLayout &L, uint8_t *base, int n_tok, const Dest 
     }
 #undef GI_APPEND
     return hipGetLastError();
+}
+
+// One rotated pair of ApplyRoPE (kernels.go:31-33): each product is rounded
+// before the sum or difference, as Go's amd64 code evaluates it, so no
+// multiply-add may be contracted here.
+__device__ __forceinline__ void rope_pair(float x0, float x1, float c, float s, float *y0, float *y1)
+{
+#pragma clang fp contract(off)
+    float a = x0 * c;
+    float b = x1 * s;
+    float e = x0 * s;
+    float f = x1 * c;
+    *y0 = a - b;
+    *y1 = e + f;
+}
+
+// Rotates the first 2*rh dims of each of n_heads heads of x (head stride hd)
+// into y; the dims past 2*rh are copied.  Pair p = (head, j) is (j, j + rh)
+// of that head.  Pairs [p0, p0 + step * k) go to the threads of the
+// workgroup in turn, and y may alias x: every element is read and written
+// by the one thread that owns its pair.
+__device__ __forceinline__ void rope_rows(const float *x, float *y, int n_heads, int hd, int rh,
+                                          const float2 *cs, int p0, int step)
+{
+    for (int p = p0 + threadIdx.x; p < n_heads * rh; p += step) {
+        int h = p / rh, j = p - h * rh;
+        const float *xh = x + (int64_t)h * hd;
+        float *yh = y + (int64_t)h * hd;
+        float2 t = cs[j];
+        float y0, y1;
+        rope_pair(xh[j], xh[j + rh], t.x, t.y, &y0, &y1);
+        yh[j] = y0;
+        yh[j + rh] = y1;
+    }
+    const int rest = hd - 2 * rh;
+    if (rest > 0) {
+        for (int p = p0 + threadIdx.x; p < n_heads * rest; p += step) {
+            int h = p / rest, j = 2 * rh + (p - h * rest);
+            y[(int64_t)h * hd + j] = x[(int64_t)h * hd + j];
+        }
+    }
+}
+
+// Fused RoPE + append.  Grid (n_tok, 1 + q_blocks): block (i, 0) turns
+// token i's K into LDS and stores K (in the pool's format: f32 copy,
+// truncated fp16, or Q8_0 blocks of the rotated vector) and V; block
+// (i, 1 + b) turns kThreads pairs of token i's q into q_out, one pair per
+// thread, so no thread waits on a chain of dependent loads.  A token whose
+// position is outside the table is skipped whole (its q_out row is not
+// written); one whose page or slot is bad has its q turned but nothing
+// stored.
+template <int KT, bool AT_LEN>
+__global__ __launch_bounds__(kThreads) void rope_append(PoolLayout L, uint8_t *base, Dest D, RopeArgs R,
+                                                        const float *__restrict__ k,
+                                                        const float *__restrict__ v, int *status)
+{
+    extern __shared__ float sk[]; // kv_dim rotated K values
+    const int i = blockIdx.x;
+    const int hd = L.head_dim;
+    const int kv_dim = L.num_kv_heads * hd;
+    const int pos = AT_LEN ? D.seq_lens[i] - 1 : R.positions[i];
+    if (pos < 0 || pos >= R.max_pos) {
+        if (threadIdx.x == 0 && blockIdx.y == 0)
+            raise_flag(status, FLAG_BAD_POS);
+        return;
+    }
+    const float2 *cs = R.table + (int64_t)pos * R.rope_half;
+    if (blockIdx.y > 0) {
+        const int64_t qo = (int64_t)i * R.num_heads * hd;
+        const int nqb = gridDim.y - 1;
+        rope_rows(R.q + qo, R.q_out + qo, R.num_heads, hd, R.rope_half, cs,
+                  (int)(blockIdx.y - 1) * kThreads, nqb * kThreads);
+        return;
+    }
+    const float *kx = k + (int64_t)i * kv_dim;
+    const float *vx = v + (int64_t)i * kv_dim;
+    rope_rows(kx, sk, L.num_kv_heads, hd, R.rope_half, cs, 0, kThreads);
+    __syncthreads();
+    int64_t page;
+    int s;
+    // every thread resolves the same destination; thread 0 reports
+    if (!resolve(D, L, i, &page, &s, threadIdx.x == 0 ? status : nullptr))
+        return;
+    uint8_t *pg = base + page * L.page_bytes;
+    const int P = L.page_tokens;
+    if (KT == KV_Q4_0) {
+        // 32-lane groups are whole blocks in every iteration (see below)
+        for (int e = threadIdx.x; e < kv_dim; e += kThreads)
+            quant_store_q4(L, pg, s, e, sk[e], vx[e], true);
+        return;
+    }
+    if (KT == KV_Q8_0) {
+        const int nb = hd / 32;
+        // kv_dim and kThreads are multiples of 32: a 32-lane group (one
+        // Q8_0 block) is wholly in or out of range in every iteration.
+        for (int e = threadIdx.x; e < kv_dim; e += kThreads) {
+            float kv0 = sk[e], vv0 = vx[e];
+            float kinv, vinv;
+            uint32_t kd = q8_scale(__builtin_bit_cast(float, max32(abs_key(kv0))), &kinv);
+            uint32_t vd = q8_scale(__builtin_bit_cast(float, max32(abs_key(vv0))), &vinv);
+            int kvh = e / hd, d = e - kvh * hd, blk = d >> 5;
+            reinterpret_cast<int8_t *>(pg + L.k_off)[((int64_t)kvh * P + s) * hd + d] = (int8_t)q8_quant(kv0, kinv);
+            reinterpret_cast<int8_t *>(pg + L.v_off)[((int64_t)kvh * hd + d) * P + s] = (int8_t)q8_quant(vv0, vinv);
+            if ((d & 31) == 0) {
+                reinterpret_cast<uint16_t *>(pg + L.ks_off)[((int64_t)kvh * P + s) * nb + blk] = (uint16_t)kd;
+                reinterpret_cast<uint16_t *>(pg + L.vs_off)[((int64_t)kvh * nb + blk) * P + s] = (uint16_t)vd;
+            }
+        }
+        return;
+    }
+    for (int e = threadIdx.x; e < kv_dim; e += kThreads) {
+        int kvh = e / hd, d = e - kvh * hd;
+        int64_t ki = ((int64_t)kvh * P + s) * hd + d;
+        int64_t vi = ((int64_t)kvh * hd + d) * P + s;
+        if (KT == KV_F32) {
+            reinterpret_cast<float *>(pg + L.k_off)[ki] = sk[e];
+            reinterpret_cast<float *>(pg + L.v_off)[vi] = vx[e];
+        } else {
+            reinterpret_cast<uint16_t *>(pg + L.k_off)[ki] = (uint16_t)float_to_half_bits_rtz(sk[e]);
+            reinterpret_cast<uint16_t *>(pg + L.v_off)[vi] = (uint16_t)float_to_half_bits_rtz(vx[e]);
+        }
+    }
 }
 
 } // namespace
@@ -309,13 +521,57 @@ hipError_t launch_append_at_len(const PoolLayout &L, uint8_t *base, int batch,
     return append_any(L, base, batch, D, k, v, status, st);
 }
 
+hipError_t launch_rope_append(const PoolLayout &L, uint8_t *base, int n_tok, const int32_t *block_ids,
+                              const int32_t *slots, const int32_t *block_tables, int max_blocks,
+                              const int32_t *seq_lens, const RopeArgs &R, const float *k,
+                              const float *v, int *status, hipStream_t st)
+{
+    if (n_tok <= 0)
+        return hipSuccess;
+    Dest D{block_ids, slots, block_tables, seq_lens, max_blocks};
+    const bool at_len = block_ids == nullptr;
+    const size_t lds = sizeof(float) * (size_t)L.num_kv_heads * L.head_dim;
+    // q blocks: one rotated pair (or copied dim past rope_dim) per thread
+    const int64_t q_units = (int64_t)R.num_heads *
+                            std::max(R.rope_half, L.head_dim - 2 * R.rope_half);
+    const int nqb = (int)((q_units + kThreads - 1) / kThreads);
+    dim3 grid((unsigned)n_tok, (unsigned)(1 + nqb)), block(kThreads);
+#define GI_ROPE(KT)                                                                                \
+    do {                                                                                           \
+        if (at_len)                                                                                \
+            hipLaunchKernelGGL((rope_append<KT, true>), grid, block, lds, st, L, base, D, R, k, v, \
+                               status);                                                            \
+        else                                                                                       \
+            hipLaunchKernelGGL((rope_append<KT, false>), grid, block, lds, st, L, base, D, R, k,   \
+                               v, status);                                                         \
+    } while (0)
+    switch (L.kv_type) {
+    case KV_F32:
+        GI_ROPE(KV_F32);
+        break;
+    case KV_F16:
+        GI_ROPE(KV_F16);
+        break;
+    case KV_Q4_0:
+        GI_ROPE(KV_Q4_0);
+        break;
+    default:
+        GI_ROPE(KV_Q8_0);
+        break;
+    }
+#undef GI_ROPE
+    return hipGetLastError();
+}
+
 hipError_t launch_gather(const PoolLayout &L, const uint8_t *base, const int32_t *table, int n_tok,
                          void *k_out, void *v_out, int widen, int *status, hipStream_t st)
 {
     if (n_tok <= 0)
         return hipSuccess;
     int kv_dim = L.num_kv_heads * L.head_dim;
-    int64_t per_tok = (L.kv_type == KV_Q8_0 && !widen) ? (kv_dim / 32) * 34 : kv_dim;
+    int64_t per_tok = (L.kv_type == KV_Q8_0 && !widen) ? (kv_dim / 32) * 34
+                      : (L.kv_type == KV_Q4_0 && !widen) ? (kv_dim / 32) * 18
+                                                         : kv_dim;
     dim3 grid(grid_for((int64_t)n_tok * per_tok)), block(kThreads);
     uint8_t *ko = (uint8_t *)k_out, *vo = (uint8_t *)v_out;
 #define GI_GATHER(KT, W) \
@@ -327,6 +583,11 @@ hipError_t launch_gather(const PoolLayout &L, const uint8_t *base, const int32_t
             GI_GATHER(KV_F16, 1);
         else
             GI_GATHER(KV_F16, 0);
+    } else if (L.kv_type == KV_Q4_0) {
+        if (widen)
+            GI_GATHER(KV_Q4_0, 1);
+        else
+            GI_GATHER(KV_Q4_0, 0);
     } else {
         if (widen)
             GI_GATHER(KV_Q8_0, 1);

@@ -43,6 +43,9 @@ struct gi_paged {
     void *ws = nullptr;
     size_t ws_bytes = 0;
     int decode_kernel = -1; // -1 automatic, 0 vector ALU, 1 matrix core
+    float2 *d_rope = nullptr; // (cos, sin) [rope_max_pos][rope_half]
+    int rope_half = 0;
+    int rope_max_pos = 0;
 };
 
 namespace {
@@ -224,6 +227,8 @@ void gi_paged_destroy(gi_paged *h)
         (void)hipFree(h->d_layer_base);
     if (h->ws)
         (void)hipFree(h->ws);
+    if (h->d_rope)
+        (void)hipFree(h->d_rope);
     if (h->own_stream)
         (void)hipStreamDestroy(h->own_stream);
     delete h;
@@ -282,6 +287,8 @@ int gi_synchronize(gi_paged *h)
             why += " page id outside the pool;";
         if (flags & gi::FLAG_BAD_SLOT)
             why += " slot or position outside the block table;";
+        if (flags & gi::FLAG_BAD_POS)
+            why += " position outside the RoPE table;";
         return gi::set_error(GI_ERR_BAD_PAGE, "kernel saw:" + why + " affected tokens were skipped");
     }
     return GI_OK;
@@ -364,6 +371,124 @@ int gi_paged_append_at_len(gi_paged *h, int layer, int batch, const int32_t *blo
     hipError_t e = gi::launch_append_at_len(h->L, h->layer_base[(size_t)layer], batch, block_tables,
                                             max_blocks, seq_lens, k, v, h->d_status, h->stream);
     return e == hipSuccess ? GI_OK : hip_fail(e, "gi_paged_append_at_len");
+}
+
+int gi_paged_set_rope(gi_paged *h, float theta, int rope_dim, int max_positions)
+{
+    int rc = enter(h, "gi_paged_set_rope");
+    if (rc)
+        return rc;
+    const int hd = h->L.head_dim;
+    if (rope_dim <= 0)
+        rope_dim = hd;
+    if (!std::isfinite(theta) || !(theta > 0.0f) || rope_dim > hd || rope_dim % 2 ||
+        max_positions <= 0)
+        return gi::set_error(GI_ERR_BAD_ARG, "gi_paged_set_rope: need theta > 0, an even rope_dim "
+                                             "<= head_dim and max_positions > 0");
+    const int rh = rope_dim / 2;
+    const size_t n = (size_t)max_positions * (size_t)rh;
+    // ApplyRoPE's angles (pkg/math/kernels.go:24-28): freq = 1/theta^(2j/d)
+    // and pos*freq in float64, cos and sin rounded to float32.
+    std::vector<float2> tab;
+    try {
+        tab.resize(n);
+    } catch (const std::bad_alloc &) {
+        return gi::set_error(GI_ERR_OOM, "gi_paged_set_rope: out of host memory");
+    }
+    std::vector<double> freq((size_t)rh);
+    for (int j = 0; j < rh; j++)
+        freq[(size_t)j] = 1.0 / std::pow((double)theta, (double)(2 * j) / (double)rope_dim);
+    for (int p = 0; p < max_positions; p++) {
+        for (int j = 0; j < rh; j++) {
+            double val = (double)p * freq[(size_t)j];
+            tab[(size_t)p * rh + j] = make_float2((float)std::cos(val), (float)std::sin(val));
+        }
+    }
+    std::lock_guard<std::mutex> g(h->mu);
+    hipError_t e = hipStreamSynchronize(h->stream); // queued work may read the old table
+    if (e != hipSuccess)
+        return hip_fail(e, "gi_paged_set_rope");
+    if (h->d_rope) {
+        (void)hipFree(h->d_rope);
+        h->d_rope = nullptr;
+        h->rope_half = h->rope_max_pos = 0;
+    }
+    float2 *d = nullptr;
+    if (hipMalloc((void **)&d, n * sizeof(float2)) != hipSuccess)
+        return gi::set_error(GI_ERR_OOM, "gi_paged_set_rope: hipMalloc of the table failed");
+    e = hipMemcpy(d, tab.data(), n * sizeof(float2), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(d);
+        return hip_fail(e, "gi_paged_set_rope: upload");
+    }
+    h->d_rope = d;
+    h->rope_half = rh;
+    h->rope_max_pos = max_positions;
+    return GI_OK;
+}
+
+static int check_rope(gi_paged *h, int layer, int n_tok, int num_heads, const float *q, const float *q_out,
+                      const float *k, const float *v, const char *what)
+{
+    int rc = check_layer(h, layer, what);
+    if (rc)
+        return rc;
+    if (!h->d_rope)
+        return gi::set_error(GI_ERR_BAD_ARG, std::string(what) + ": no RoPE table (gi_paged_set_rope)");
+    if (n_tok < 0 || num_heads < 0)
+        return gi::set_error(GI_ERR_BAD_ARG, std::string(what) + ": bad argument");
+    if (n_tok > 0 && (!k || !v || (num_heads > 0 && (!q || !q_out))))
+        return gi::set_error(GI_ERR_BAD_ARG, std::string(what) + ": NULL buffer");
+    if ((size_t)h->L.num_kv_heads * h->L.head_dim * sizeof(float) > 65536)
+        return gi::set_error(GI_ERR_BAD_ARG, std::string(what) + ": kv_dim above 16384");
+    return GI_OK;
+}
+
+static gi::RopeArgs rope_args(const gi_paged *h, int num_heads, const int32_t *positions, const float *q,
+                              float *q_out)
+{
+    gi::RopeArgs R{};
+    R.table = h->d_rope;
+    R.rope_half = h->rope_half;
+    R.max_pos = h->rope_max_pos;
+    R.num_heads = num_heads;
+    R.positions = positions;
+    R.q = q;
+    R.q_out = q_out;
+    return R;
+}
+
+int gi_paged_rope_append(gi_paged *h, int layer, int n_tok, int num_heads, const int32_t *positions,
+                         const int32_t *block_ids, const int32_t *slots, const float *q, float *q_out,
+                         const float *k, const float *v)
+{
+    int rc = enter(h, "gi_paged_rope_append");
+    if (rc || (rc = check_rope(h, layer, n_tok, num_heads, q, q_out, k, v, "gi_paged_rope_append")))
+        return rc;
+    if (n_tok > 0 && (!positions || !block_ids || !slots))
+        return gi::set_error(GI_ERR_BAD_ARG, "gi_paged_rope_append: NULL positions, block_ids or slots");
+    std::lock_guard<std::mutex> g(h->mu);
+    hipError_t e = gi::launch_rope_append(h->L, h->layer_base[(size_t)layer], n_tok, block_ids, slots, nullptr,
+                                          0, nullptr, rope_args(h, num_heads, positions, q, q_out), k, v,
+                                          h->d_status, h->stream);
+    return e == hipSuccess ? GI_OK : hip_fail(e, "gi_paged_rope_append");
+}
+
+int gi_paged_rope_append_at_len(gi_paged *h, int layer, int batch, int num_heads,
+                                const int32_t *block_tables, int max_blocks, const int32_t *seq_lens,
+                                const float *q, float *q_out, const float *k, const float *v)
+{
+    int rc = enter(h, "gi_paged_rope_append_at_len");
+    if (rc || (rc = check_rope(h, layer, batch, num_heads, q, q_out, k, v, "gi_paged_rope_append_at_len")))
+        return rc;
+    if (batch > 0 && (!block_tables || !seq_lens || max_blocks <= 0))
+        return gi::set_error(GI_ERR_BAD_ARG, "gi_paged_rope_append_at_len: bad block tables");
+    std::lock_guard<std::mutex> g(h->mu);
+    hipError_t e = gi::launch_rope_append(h->L, h->layer_base[(size_t)layer], batch, nullptr, nullptr,
+                                          block_tables, max_blocks, seq_lens,
+                                          rope_args(h, num_heads, nullptr, q, q_out), k, v, h->d_status,
+                                          h->stream);
+    return e == hipSuccess ? GI_OK : hip_fail(e, "gi_paged_rope_append_at_len");
 }
 
 int gi_paged_copy_pages(gi_paged *h, int n, const int32_t *src_ids, const int32_t *dst_ids)
@@ -477,6 +602,28 @@ int gi_paged_decode_step(gi_paged *h, int layer, int batch, int num_heads, const
                                             max_blocks, seq_lens, k, v, h->d_status, h->stream);
     if (e != hipSuccess)
         return hip_fail(e, "gi_paged_decode_step: append");
+    return decode_locked(h, layer, batch, num_heads, q, out, block_tables, max_blocks, seq_lens,
+                         max_seq_len, scale);
+}
+
+int gi_paged_rope_decode_step(gi_paged *h, int layer, int batch, int num_heads, float *q, const float *k,
+                              const float *v, float *out, const int32_t *block_tables, int max_blocks,
+                              const int32_t *seq_lens, int max_seq_len, float scale)
+{
+    int rc = enter(h, "gi_paged_rope_decode_step");
+    if (rc || (rc = check_decode_args(h, layer, batch, num_heads, q, out, block_tables, max_blocks,
+                                      seq_lens, max_seq_len, scale, "gi_paged_rope_decode_step")) ||
+        (rc = check_rope(h, layer, batch, num_heads, q, q, k, v, "gi_paged_rope_decode_step")))
+        return rc;
+    if (batch == 0)
+        return GI_OK;
+    std::lock_guard<std::mutex> g(h->mu);
+    hipError_t e = gi::launch_rope_append(h->L, h->layer_base[(size_t)layer], batch, nullptr, nullptr,
+                                          block_tables, max_blocks, seq_lens,
+                                          rope_args(h, num_heads, nullptr, q, q), k, v, h->d_status,
+                                          h->stream);
+    if (e != hipSuccess)
+        return hip_fail(e, "gi_paged_rope_decode_step: rope + append");
     return decode_locked(h, layer, batch, num_heads, q, out, block_tables, max_blocks, seq_lens,
                          max_seq_len, scale);
 }

@@ -16,7 +16,10 @@
  *     gi_paged_decode_step;
  *   - the chunked-prefill attention of forward.go:547-577 and
  *     metal.AttentionGQABatch (metal_darwin.go:963-981) ->
- *     gi_paged_prefill_attention.
+ *     gi_paged_prefill_attention;
+ *   - ApplyRoPE on q/k before the store (forward.go:228-240, 527-545,
+ *     pkg/math/kernels.go:22-35) -> gi_paged_rope_append[_at_len] /
+ *     gi_paged_rope_decode_step.
  *
  * Conventions (as in pkg/metal/metal_bridge.h and inference_core.h):
  *   - every call returns int: GI_OK (0) or a negative GI_ERR_* code, and a
@@ -53,11 +56,14 @@ extern "C" {
 #define GI_ERR_BAD_PAGE (-7)       /* a kernel saw a page id outside the pool */
 #define GI_ERR_SHARED_PAGE (-8)    /* the append would write a page another sequence shares */
 
-/* KV storage types.  f32 and q8_0 are kvcache.go:11-15's KVTypeF32 and
- * KVTypeQ8_0; f16 stores FP32ToFP16 (pkg/quant/fp16.go:38-69) halves. */
+/* KV storage types.  f32, q8_0 and q4_0 are kvcache.go:11-15's KVTypeF32,
+ * KVTypeQ8_0 and KVTypeQ4_0 (QuantizeQ8_0 / QuantizeQ4_0 of each token
+ * vector, pkg/quant/quant.go:407-521); f16 stores FP32ToFP16
+ * (pkg/quant/fp16.go:38-69) halves. */
 #define GI_KV_F32 0
 #define GI_KV_F16 1
 #define GI_KV_Q8_0 2
+#define GI_KV_Q4_0 3
 
 /* ---- library / device ------------------------------------------------- */
 
@@ -169,7 +175,7 @@ typedef struct gi_paged gi_paged;
 /* Creates a pool of num_pages pages on the current device, each page holding
  * page_tokens tokens of every layer (KVBlock, paged_kv.go:13-38), plus one
  * HIP stream (default priority).  kv_type is GI_KV_*.  head_dim must be a
- * multiple of 8 (32 for q8_0).  Pages are zero filled. */
+ * multiple of 8 (32 for q8_0 and q4_0).  Pages are zero filled. */
 int gi_paged_create(int num_layers, int num_kv_heads, int head_dim, int page_tokens,
                     int64_t num_pages, int kv_type, gi_paged **out);
 void gi_paged_destroy(gi_paged *h);
@@ -200,7 +206,8 @@ int gi_memcpy_d2h(gi_paged *h, void *dst, const void *src, size_t bytes);
 /* Appends n_tok token vectors of one layer: token i goes to page
  * block_ids[i], slot slots[i] (the pair AppendToken returned).  k and v are
  * [n_tok][num_kv_heads*head_dim] float32; f16 pages store the truncated
- * halves, q8_0 pages the QuantizeQ8_0 blocks of each whole vector.
+ * halves, q8_0 / q4_0 pages the QuantizeQ8_0 / QuantizeQ4_0 blocks of each
+ * whole vector.
  * Replaces KVCache.Write (kvcache.go:146-180) and metal.KVWrite[Batch]. */
 int gi_paged_append(gi_paged *h, int layer, int n_tok, const int32_t *block_ids,
                     const int32_t *slots, const float *k, const float *v);
@@ -219,8 +226,10 @@ int gi_paged_copy_pages(gi_paged *h, int n, const int32_t *src_ids, const int32_
 /* Gathers tokens [0, n_tok) of one layer of one sequence into the contiguous
  * [n_tok][kv_dim] layout that KVCache indexes (kvcache.go:183-284).
  * widen == 0: stored bytes (f32 4*kv_dim, f16 2*kv_dim, q8_0 kv_dim/32
- * blocks of 34 bytes: little-endian fp16 scale then 32 int8, quant.go:38-41);
- * widen == 1: float32 values (FP16ToFP32 / DequantizeQ8_0).  block_table
+ * blocks of 34 bytes: little-endian fp16 scale then 32 int8, quant.go:38-41;
+ * q4_0 kv_dim/32 blocks of 18 bytes: the scale, then byte j = element j |
+ * element j+16 << 4, quant.go:9-13, 504);
+ * widen == 1: float32 values (FP16ToFP32 / DequantizeQ8_0 / DequantizeQ4_0).  block_table
  * must hold ceil(n_tok / page_tokens) ids. */
 int gi_paged_gather(gi_paged *h, int layer, const int32_t *block_table, int n_tok, void *k_out,
                     void *v_out, int widen);
@@ -240,6 +249,47 @@ int gi_paged_decode_attention(gi_paged *h, int layer, int batch, int num_heads, 
 int gi_paged_decode_step(gi_paged *h, int layer, int batch, int num_heads, const float *q,
                          const float *k, const float *v, float *out, const int32_t *block_tables,
                          int max_blocks, const int32_t *seq_lens, int max_seq_len, float scale);
+
+/* ---- rotary embedding fused with the append ---------------------------- *
+ * Forward turns q and k with ApplyRoPE (pkg/math/kernels.go:22-35) on every
+ * head right before it stores k/v (forward.go:228-240 decode, 527-545
+ * prefill; with a rope dimension below head_dim only the first rope_dim dims
+ * of each head turn, forward.go:945-977).  These entry points do both in one
+ * pass, so the rotated K is never written back to the caller and read again.
+ * The rotation is bit-exact with ApplyRoPE: cos/sin come from a table built
+ * as ApplyRoPE computes them (float64, rounded to float32) and each pair is
+ * rotated with rounded products (no fused multiply-add). */
+
+/* Builds the pool's RoPE table for positions [0, max_positions): theta is
+ * llama.rope.freq_base (Config.RopeTheta, pkg/engine/config.go:13), rope_dim
+ * (even, <= head_dim; <= 0 means head_dim) is rope.dimension_count
+ * (engine.go:112-113).  Replaces any earlier table. */
+int gi_paged_set_rope(gi_paged *h, float theta, int rope_dim, int max_positions);
+
+/* RoPE + append, explicit form (the prefill store, forward.go:527-545):
+ * token i is at position positions[i] and goes to (block_ids[i], slots[i]).
+ * q [n_tok][num_heads][head_dim] float32 is rotated into q_out (which may be
+ * q; num_heads 0 with q == q_out == NULL turns only k); k is rotated, then
+ * k and v are stored as gi_paged_append stores them.  A position outside the
+ * table skips the token (q_out row untouched) and is reported by
+ * gi_synchronize as GI_ERR_BAD_PAGE. */
+int gi_paged_rope_append(gi_paged *h, int layer, int n_tok, int num_heads, const int32_t *positions,
+                         const int32_t *block_ids, const int32_t *slots, const float *q, float *q_out,
+                         const float *k, const float *v);
+
+/* RoPE + append, decode form: token b is at position seq_lens[b]-1 of
+ * sequence b, stored through block_tables (as gi_paged_append_at_len). */
+int gi_paged_rope_append_at_len(gi_paged *h, int layer, int batch, int num_heads,
+                                const int32_t *block_tables, int max_blocks, const int32_t *seq_lens,
+                                const float *q, float *q_out, const float *k, const float *v);
+
+/* One decode step of one layer from the projections: q (rotated in place,
+ * as ApplyRoPE turns a.Q) and k are turned at position seq_lens[b]-1, k/v
+ * appended, then gi_paged_decode_attention over seq_lens[b] tokens
+ * (forward.go:228-267). */
+int gi_paged_rope_decode_step(gi_paged *h, int layer, int batch, int num_heads, float *q, const float *k,
+                              const float *v, float *out, const int32_t *block_tables, int max_blocks,
+                              const int32_t *seq_lens, int max_seq_len, float scale);
 
 /* Chunked-prefill causal attention (forward.go:547-577) of one layer: the
  * chunk's K/V are already appended; query i of sequence b attends tokens

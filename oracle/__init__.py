@@ -21,7 +21,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "libcpuref.so")
 _lib = None
 
-KV_F32, KV_F16, KV_Q8_0 = 0, 1, 2
+KV_F32, KV_F16, KV_Q8_0, KV_Q4_0 = 0, 1, 2, 3
 
 _f32p = ctypes.POINTER(ctypes.c_float)
 _u16p = ctypes.POINTER(ctypes.c_uint16)
@@ -47,6 +47,8 @@ def lib():
             "ref_fp16_to_fp32_array": (None, [_u16p, _f32p, _i64]),
             "ref_quantize_q8_0": (None, [_f32p, _i64, _u8p]),
             "ref_dequantize_q8_0": (None, [_u8p, _i64, _f32p]),
+            "ref_quantize_q4_0": (None, [_f32p, _i64, _u8p]),
+            "ref_dequantize_q4_0": (None, [_u8p, _i64, _f32p]),
             "ref_dot_vec_f32": (ctypes.c_float, [_f32p, _f32p, _int]),
             "ref_softmax": (None, [_f32p, _int]),
             "ref_math_sqrt": (ctypes.c_double, [ctypes.c_double]),
@@ -64,6 +66,9 @@ def lib():
                                         _u8p, _u8p]),
             "ref_decode_batch": (None, [_int, _f32p, _u8p, _u8p, _i64p, _i32p, _int, _f32p, _int,
                                         _int, _int, ctypes.c_float, _f32p, _f32p, _f32p]),
+            "ref_apply_rope": (None, [_f32p, _int, _int, ctypes.c_float]),
+            "ref_rope_heads": (None, [_f32p, _int, _int, _int, _int, ctypes.c_float]),
+            "ref_rope_table": (None, [ctypes.c_float, _int, _int, _int, _f32p]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -117,6 +122,22 @@ def dequantize_q8_0(data, n):
     return out
 
 
+def quantize_q4_0(x):
+    """QuantizeQ4_0 (quant.go:458-521) of a 1-D float32 vector -> bytes."""
+    x = _c(x, np.float32).ravel()
+    out = np.empty(((x.size + 31) // 32) * 18, np.uint8)
+    lib().ref_quantize_q4_0(_p(x, _f32p), x.size, _p(out, _u8p))
+    return out
+
+
+def dequantize_q4_0(data, n):
+    """DequantizeQ4_0 (quant.go:96-116) -> float32[n]."""
+    data = _c(data, np.uint8)
+    out = np.zeros(n, np.float32)
+    lib().ref_dequantize_q4_0(_p(data, _u8p), n, _p(out, _f32p))
+    return out
+
+
 def dot_vec_f32(x, w):
     x = _c(x, np.float32)
     w = _c(w, np.float32)
@@ -137,6 +158,34 @@ def attn_scale(head_dim):
     return np.float32(lib().ref_attn_scale(int(head_dim)))
 
 
+# ---- rotary position embedding (pkg/math/kernels.go:22-35) -----------------
+
+def apply_rope(vec, pos, head_dim, theta):
+    """ApplyRoPE(vec, pos, headDim, theta) on a copy of one float32 vector."""
+    x = _c(vec, np.float32).copy()
+    lib().ref_apply_rope(_p(x, _f32p), int(pos), int(head_dim), float(theta))
+    return x
+
+
+def rope_heads(x, positions, n_heads, head_dim, rope_dim, theta):
+    """RoPE of token vectors x [n, n_heads*head_dim] at positions[n], every
+    head turned as Forward does (forward.go:228-234; rope_dim < head_dim as in
+    forward.go:945-977).  Returns a new array."""
+    x = _c(x, np.float32).copy()
+    n = x.shape[0]
+    for i in range(n):
+        lib().ref_rope_heads(_p(x[i], _f32p), n_heads, head_dim, rope_dim, int(positions[i]),
+                             float(theta))
+    return x
+
+
+def rope_table(theta, rope_dim, pos0, n_pos):
+    """float32 [n_pos, rope_dim/2, 2] (cos, sin) pairs ApplyRoPE uses."""
+    out = np.empty((n_pos, rope_dim // 2, 2), np.float32)
+    lib().ref_rope_table(float(theta), rope_dim, pos0, n_pos, _p(out, _f32p))
+    return out
+
+
 # ---- KVCache semantics ------------------------------------------------------
 
 def bytes_per_vec(kv_type, kv_dim):
@@ -155,8 +204,9 @@ def store_vectors(kv_type, x):
     if kv_type == KV_F16:
         return fp32_to_fp16(x).view(np.uint8).reshape(n, bpv)
     if kv_dim % 32 == 0:
-        # Q8_0 blocks never straddle token vectors: one call over all rows
-        return quantize_q8_0(x).reshape(n, bpv)
+        # quantised blocks never straddle token vectors: one call over all rows
+        q = quantize_q4_0 if kv_type == KV_Q4_0 else quantize_q8_0
+        return q(x).reshape(n, bpv)
     out = np.zeros((n, bpv), np.uint8)
     dummy = np.zeros((1, bpv), np.uint8)
     for i in range(n):

@@ -25,6 +25,14 @@
  *   ref_math_sqrt -- bit patterns of 1/sqrt(64) and 1/sqrt(128).
  *   ref_attention_* -- float64 textbook softmax(QK^T * scale) V in numpy,
  *       and prefill == per-token decode (engine_test.go:219-249 restated).
+ *   ref_quantize_q4_0 / ref_dequantize_q4_0 -- exact-rational closed form
+ *       per element, hand-built special cases (NaN -> nibble 0, Inf block ->
+ *       all 8, ties away from zero, subnormal-scale clamps);
+ *       quant_test.go:21-54, 145-160 and engine_test.go:275-297 restated.
+ *   ref_apply_rope / ref_rope_table -- kernels_test.go:39-46 restated;
+ *       cos/sin against a 50-digit evaluation of cos(pos * theta^(-2i/d));
+ *       the rotation of (1, 0) lands at angle +pos*freq (sign and pairing);
+ *       pair norms and the relative-position property of q.k.
  */
 #include <math.h>
 #include <stdint.h>
@@ -176,6 +184,92 @@ void ref_dequantize_q8_0(const uint8_t *data, int64_t n, float *out)
     }
 }
 
+/* ---- Q4_0 ---------------------------------------------------------------- */
+
+/* Go's int(float64) on amd64 (CVTTSD2SQ): truncation toward zero, and the
+ * "integer indefinite" 0x8000000000000000 for NaN and for values outside
+ * int64 -- C leaves both undefined, so they are spelled out. */
+static int64_t go_int(double x)
+{
+    if (x != x || x >= 9223372036854775808.0 || x < -9223372036854775808.0)
+        return INT64_MIN;
+    return (int64_t)x;
+}
+
+/* One Q4_0 element (quant.go:481-502): int(math.Round(float64(x*inv))) + 8,
+ * clamped to [0, 15]; an element past the vector's end, or a zero inverse,
+ * gives 8.  A NaN product converts to INT64_MIN, so it clamps to 0. */
+static int q4_element(const float *src, int64_t idx, int64_t n, float inv)
+{
+    if (idx >= n || !(inv > 0))
+        return 8;
+    float v = src[idx] * inv;
+    int64_t q = go_int(go_round((double)v));
+    if (q != INT64_MIN)
+        q += 8;
+    if (q < 0)
+        q = 0;
+    else if (q > 15)
+        q = 15;
+    return (int)q;
+}
+
+/* pkg/quant/quant.go:458-521 QuantizeQ4_0: per block of 32, amax as in
+ * Q8_0, scale = amax / 7 (float32), truncated to fp16 and widened back,
+ * inv = 1 / scale; byte j of the block's 16 holds element j in its low
+ * nibble and element j + 16 in its high nibble.  out must hold
+ * ((n+31)/32)*18 bytes. */
+void ref_quantize_q4_0(const float *src, int64_t n, uint8_t *out)
+{
+    int64_t nblocks = (n + 31) / 32;
+    for (int64_t b = 0; b < nblocks; b++) {
+        int64_t start = b * 32;
+        int64_t end = start + 32;
+        if (end > n)
+            end = n;
+        float maxv = 0.0f;
+        for (int64_t i = start; i < end; i++) {
+            float v = (float)fabs((double)src[i]);
+            if (v > maxv)
+                maxv = v;
+        }
+        float scale = maxv / 7.0f;
+        uint16_t d16 = 0;
+        if (scale > 0) {
+            d16 = ref_fp32_to_fp16(scale);
+            scale = ref_fp16_to_fp32(d16);
+        }
+        float inv = 0.0f;
+        if (scale > 0)
+            inv = 1.0f / scale;
+        uint8_t *blk = out + b * 18;
+        blk[0] = (uint8_t)(d16 & 0xFF);
+        blk[1] = (uint8_t)(d16 >> 8);
+        for (int j = 0; j < 16; j++) {
+            int q0 = q4_element(src, start + j, n, inv);
+            int q1 = q4_element(src, start + j + 16, n, inv);
+            blk[2 + j] = (uint8_t)(q0 | (q1 << 4));
+        }
+    }
+}
+
+/* pkg/quant/quant.go:96-116 DequantizeQ4_0: element j = (low nibble of byte
+ * j - 8) * d, element j + 16 = (high nibble - 8) * d. */
+void ref_dequantize_q4_0(const uint8_t *data, int64_t n, float *out)
+{
+    int64_t nblocks = n / 32;
+    for (int64_t b = 0; b < nblocks; b++) {
+        const uint8_t *blk = data + b * 18;
+        float d = ref_fp16_to_fp32((uint16_t)(blk[0] | (blk[1] << 8)));
+        for (int j = 0; j < 16; j++) {
+            int x0 = (int)(blk[2 + j] & 0x0F) - 8;
+            int x1 = (int)((blk[2 + j] >> 4) & 0x0F) - 8;
+            out[b * 32 + j] = (float)x0 * d;
+            out[b * 32 + j + 16] = (float)x1 * d;
+        }
+    }
+}
+
 /* ---- dot / softmax / scale ---------------------------------------------- */
 
 /* pkg/quant/quant.go:548-567 DotVecF32: 8-wide chunks summed left to right,
@@ -290,19 +384,22 @@ void ref_attention_prefill(const float *q, const float *kc, const float *vc,
 
 /* ---- KVCache.Write / Get on one contiguous layer ------------------------- */
 
-/* Stored-format bytes per token vector for kv type t (0 f32, 1 f16, 2 q8_0).
- * Q8_0 is ((kvDim+31)/32)*34 (pkg/engine/kvcache.go:92, 152). */
+/* Stored-format bytes per token vector for kv type t (0 f32, 1 f16, 2 q8_0,
+ * 3 q4_0).  Q8_0 is ((kvDim+31)/32)*34, Q4_0 ((kvDim+31)/32)*18
+ * (pkg/engine/kvcache.go:92-105, 152, 164). */
 int64_t ref_bytes_per_vec(int kv_type, int kv_dim)
 {
     if (kv_type == 0)
         return (int64_t)kv_dim * 4;
     if (kv_type == 1)
         return (int64_t)kv_dim * 2;
+    if (kv_type == 3)
+        return (int64_t)((kv_dim + 31) / 32) * 18;
     return (int64_t)((kv_dim + 31) / 32) * 34;
 }
 
-/* pkg/engine/kvcache.go:146-180 Write for one layer.  f32: copy; q8_0:
- * QuantizeQ8_0 over the whole kvDim vector.  fp16 (no reference type; the
+/* pkg/engine/kvcache.go:146-180 Write for one layer.  f32: copy; q8_0 /
+ * q4_0: QuantizeQ8_0 / QuantizeQ4_0 over the whole kvDim vector.  fp16 (no reference type; the
  * reference's only f32->f16 routine is FP32ToFP16, fp16.go:38-69) stores the
  * truncated halves.  Out-of-range slots are ignored (kvcache.go:147-149).
  * cache is [max_seq][bytes_per_vec]. */
@@ -320,6 +417,9 @@ void ref_kv_write(int kv_type, int kv_dim, int max_seq, uint8_t *kcache,
     } else if (kv_type == 1) {
         ref_fp32_to_fp16_array(k, (uint16_t *)kd, kv_dim);
         ref_fp32_to_fp16_array(v, (uint16_t *)vd, kv_dim);
+    } else if (kv_type == 3) {
+        ref_quantize_q4_0(k, kv_dim, kd);
+        ref_quantize_q4_0(v, kv_dim, vd);
     } else {
         ref_quantize_q8_0(k, kv_dim, kd);
         ref_quantize_q8_0(v, kv_dim, vd);
@@ -339,6 +439,8 @@ void ref_kv_widen(int kv_type, int kv_dim, const uint8_t *src, int64_t n_tok,
             memcpy(d, s, (size_t)bpv);
         else if (kv_type == 1)
             ref_fp16_to_fp32_array((const uint16_t *)s, d, kv_dim);
+        else if (kv_type == 3)
+            ref_dequantize_q4_0(s, kv_dim, d);
         else
             ref_dequantize_q8_0(s, kv_dim, d);
     }
@@ -399,5 +501,54 @@ void ref_decode_batch(int kv_type, const float *q, const uint8_t *kcat,
         ref_attention_decode(q + (int64_t)b * H * hd, wk, wv,
                              out + (int64_t)b * H * hd, H, KVH, hd, L, scale,
                              scores);
+    }
+}
+
+/* ---- rotary position embedding ------------------------------------------- */
+
+/* pkg/math/kernels.go:22-35 ApplyRoPE: for i < half = head_dim/2,
+ * freq = 1 / theta^(2i/head_dim) and angle = pos*freq in float64, cos and sin
+ * rounded to float32, then the pair (vec[i], vec[i+half]) is rotated in
+ * float32 with each product rounded before the sum (no fused multiply-add). */
+void ref_apply_rope(float *vec, int pos, int head_dim, float theta)
+{
+    int half = head_dim / 2;
+    for (int i = 0; i < half; i++) {
+        double freq = 1.0 / pow((double)theta, (double)(2 * i) / (double)head_dim);
+        double val = (double)pos * freq;
+        float c = (float)cos(val);
+        float s = (float)sin(val);
+        float v0 = vec[i];
+        float v1 = vec[i + half];
+        vec[i] = v0 * c - v1 * s;
+        vec[i + half] = v0 * s + v1 * c;
+    }
+}
+
+/* RoPE of every head of a [n_heads][head_dim] vector, as Forward applies it
+ * per q head and per kv head (pkg/engine/forward.go:228-234, 527-539).  With
+ * rope_dim < head_dim only the first rope_dim dims of each head turn, at
+ * frequencies of rope_dim (ApplyRoPE(head[:ropeDim], pos, ropeDim, theta),
+ * forward.go:945-977). */
+void ref_rope_heads(float *x, int n_heads, int head_dim, int rope_dim, int pos, float theta)
+{
+    if (rope_dim <= 0 || rope_dim > head_dim)
+        rope_dim = head_dim;
+    for (int h = 0; h < n_heads; h++)
+        ref_apply_rope(x + (int64_t)h * head_dim, pos, rope_dim, theta);
+}
+
+/* The float32 (cos, sin) pairs ApplyRoPE uses at positions [pos0, pos0+n_pos)
+ * for rope_dim: out[(p - pos0) * (rope_dim/2) + i] = {cos, sin}. */
+void ref_rope_table(float theta, int rope_dim, int pos0, int n_pos, float *out)
+{
+    int half = rope_dim / 2;
+    for (int p = 0; p < n_pos; p++) {
+        for (int i = 0; i < half; i++) {
+            double freq = 1.0 / pow((double)theta, (double)(2 * i) / (double)rope_dim);
+            double val = (double)(pos0 + p) * freq;
+            out[2 * ((int64_t)p * half + i)] = (float)cos(val);
+            out[2 * ((int64_t)p * half + i) + 1] = (float)sin(val);
+        }
     }
 }

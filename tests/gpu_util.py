@@ -26,8 +26,8 @@ def with_specials(x, kv_type, rng):
                          1e-40, -1e-45, 0.0, -0.0, 2.5, 1 + 2**-11 + 2**-12], np.float32)
     idx = rng.choice(n, size=min(n, 4 * specials.size), replace=False)
     flat[idx] = np.resize(specials, idx.size)
-    if kv_type == 2:
-        # whole Q8_0 blocks that are all zero, tiny (scale underflow) or huge
+    if kv_type in (2, 3):
+        # whole Q8_0 / Q4_0 blocks that are all zero, tiny (scale underflow) or huge
         nb = n // 32
         for j, val in zip(rng.choice(nb, size=min(nb, 3), replace=False), (0.0, 1e-7, 1e9)):
             flat[32 * j:32 * j + 32] = val

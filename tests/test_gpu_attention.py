@@ -6,7 +6,7 @@ truncated halves, or Q8_0 blocks -- checked bit-exact by test_gpu_kv.py), so
 the tolerance only covers reduction order, the online softmax and exp.
 
 Tolerance (relative, per (query, head) row): max|gpu - oracle| <= tol *
-max|oracle|, with tol = 1e-5 for f32 KV and 1e-3 for f16 / q8_0 KV."""
+max|oracle|, with tol = 1e-5 for f32 KV and 1e-3 for f16 / q8_0 / q4_0 KV."""
 import numpy as np
 import pytest
 
@@ -14,7 +14,7 @@ from gpu_util import Populated, rel_err_rows, seeded
 
 pytestmark = pytest.mark.gpu
 
-TOL = {0: 1e-5, 1: 1e-3, 2: 1e-3}
+TOL = {0: 1e-5, 1: 1e-3, 2: 1e-3, 3: 1e-3}
 
 
 def oracle_decode(oracle, pop, layer, q, H, lens, scale):
@@ -61,7 +61,7 @@ def run_decode(gi, oracle, dev, kv_type, H, kvh, hd, P, lens, layers=1, seed=1, 
     return pop, worst
 
 
-@pytest.mark.parametrize("kv_type", [0, 1, 2], ids=["f32", "f16", "q8_0"])
+@pytest.mark.parametrize("kv_type", [0, 1, 2, 3], ids=["f32", "f16", "q8_0", "q4_0"])
 def test_decode_small_shapes(gi, oracle, dev, kv_type):
     # ragged lengths including 1, page edges and a multi-split sequence
     for (H, kvh, hd, P) in [(32, 4, 64, 16), (32, 8, 128, 16), (64, 8, 128, 32), (8, 8, 128, 16),
@@ -212,7 +212,7 @@ def prefill_case(gi, oracle, dev, kv_type, H, kvh, hd, P, starts, chunk, seed):
     assert max(worst.values()) <= TOL[kv_type], worst
 
 
-@pytest.mark.parametrize("kv_type", [0, 1, 2], ids=["f32", "f16", "q8_0"])
+@pytest.mark.parametrize("kv_type", [0, 1, 2, 3], ids=["f32", "f16", "q8_0", "q4_0"])
 def test_prefill_chunk(gi, oracle, dev, kv_type):
     prefill_case(gi, oracle, dev, kv_type, 32, 8, 128, 16, [0, 100, 509], 64, seed=60 + kv_type)
 

@@ -17,7 +17,7 @@ SHAPES = {
 }
 
 
-@pytest.mark.parametrize("kv_type", [0, 1, 2], ids=["f32", "f16", "q8_0"])
+@pytest.mark.parametrize("kv_type", [0, 1, 2, 3], ids=["f32", "f16", "q8_0", "q4_0"])
 @pytest.mark.parametrize("shape", list(SHAPES))
 def test_append_gather_bit_exact(gi, oracle, dev, kv_type, shape):
     kvh, hd, P = SHAPES[shape]
@@ -81,7 +81,7 @@ def test_decode_step_append_at_len(gi, oracle, dev):
     block table, bit-exact with an explicit append."""
     import torch
     kvh, hd, P = 8, 128, 16
-    for kv_type in (1, 2):
+    for kv_type in (1, 2, 3):
         lens = [17, 32, 5, 100]
         pop = Populated(gi, dev, kv_type, 1, kvh, hd, P, lens, seed=77, slack_pages=8)
         bt = pop.block_tables()
@@ -104,6 +104,34 @@ def test_decode_step_append_at_len(gi, oracle, dev):
             ks = oracle.store_vectors(kv_type, np.concatenate([pop.k[(0, i)], kn[i:i + 1]]))
             vs = oracle.store_vectors(kv_type, np.concatenate([pop.v[(0, i)], vn[i:i + 1]]))
             assert np.array_equal(ko, ks) and np.array_equal(vo, vs)
+
+
+def test_reference_q4_0_kvcache_tests_on_pages(gi, oracle, dev):
+    """engine_test.go:275-297 (Q4_0, kvDim 32, k[i] = i, |deq[10] - 10| <=
+    3) and kvcache_test.go:7-71 (values i+1 / 2(i+1), kvDim 64) on pages,
+    bit-exact with the oracle's QuantizeQ4_0 blocks."""
+    import torch
+    pool = gi.PagedKVCache(1, 1, 32, 4, 2, gi.KV_Q4_0)
+    k = np.arange(32, dtype=np.float32)[None, :]
+    z = torch.tensor([1], dtype=torch.int32, device=dev)
+    pool.Write(0, z, torch.tensor([2], dtype=torch.int32, device=dev),
+               torch.from_numpy(k).to(dev), torch.from_numpy(2 * k).to(dev))
+    kw, vw = pool.Get(0, z, 3, widen=True)
+    kr, vr = pool.Get(0, z, 3)
+    pool.synchronize()
+    assert abs(float(kw[2, 10]) - 10.0) <= 3.0
+    assert np.array_equal(kr.cpu().numpy()[2], oracle.quantize_q4_0(k[0]))
+    assert np.array_equal(vr.cpu().numpy()[2], oracle.quantize_q4_0(2 * k[0]))
+    assert not kr.cpu().numpy()[:2].any()
+    pool64 = gi.PagedKVCache(2, 1, 64, 16, 2, gi.KV_Q4_0)
+    k = (np.arange(64, dtype=np.float32) + 1)[None, :]
+    pool64.Write(1, z, torch.tensor([0], dtype=torch.int32, device=dev),
+                 torch.from_numpy(k).to(dev), torch.from_numpy(2 * k).to(dev))
+    kr, vr = pool64.Get(1, z, 1)
+    pool64.synchronize()
+    assert kr.shape == (1, 36)
+    assert np.array_equal(kr.cpu().numpy()[0], oracle.quantize_q4_0(k[0]))
+    assert np.array_equal(vr.cpu().numpy()[0], oracle.quantize_q4_0(2 * k[0]))
 
 
 def test_bad_page_ids_are_reported(gi, dev):

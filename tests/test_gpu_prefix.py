@@ -47,7 +47,7 @@ class DevPool:
         return k.cpu().numpy(), v.cpu().numpy()
 
 
-@pytest.mark.parametrize("kv_type", [0, 1, 2], ids=["f32", "f16", "q8_0"])
+@pytest.mark.parametrize("kv_type", [0, 1, 2, 3], ids=["f32", "f16", "q8_0", "q4_0"])
 def test_fork_cow_differential_on_device(gi, oracle, dev, kv_type):
     rng = random.Random(3 + kv_type)
     L, kvh, hd, P, N = 2, 2, 64, 16, 64

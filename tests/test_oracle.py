@@ -314,7 +314,7 @@ def test_kv_context_wrap(oracle):
     assert kc[1].view(np.float32)[0] == 90.0 and vc[1].view(np.float32)[0] == 900.0
 
 
-@pytest.mark.parametrize("kv_type", [0, 1, 2])
+@pytest.mark.parametrize("kv_type", [0, 1, 2, 3])
 def test_paged_store_gather_roundtrip(oracle, kv_type):
     layers, kv_dim, P, nb = 3, 64, 16, 12
     pool = oracle.RefPagedPool(kv_type, layers, kv_dim, nb, P)

@@ -157,7 +157,7 @@ def test_plain_append_refuses_shared_page(gi, oracle):
     assert cs == m.Tables[b].BlockIDs[0] and cd == ids[0] and list(slots) == [3, 0, 1]
 
 
-@pytest.mark.parametrize("kv_type", [0, 1, 2])
+@pytest.mark.parametrize("kv_type", [0, 1, 2, 3])
 def test_fork_cow_differential(gi, oracle, kv_type):
     """Random allocate / append / fork / free: every live sequence's pages hold
     exactly what the reference's deep-copied KVCache would (ForkAt semantics),
