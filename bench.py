@@ -19,6 +19,8 @@ Prints one JSON line (see --help).  --config selects other shapes:
   llama8b_b256_8k_rope the headline step with RoPE fused into the append: per
                       layer, q and k turned at position 8191 (theta 5e5) while
                       k/v are stored, then the same paged attention
+  llama8b_b256_8k_q8  the headline step over Q8_0 pages (blocks of 32 int8 + fp16
+                      scale, kvcache.go's KVTypeQ8_0)
   llama8b_b256_8k_q4  the headline step over Q4_0 pages (blocks of 32 4-bit
                       values + fp16 scale, kvcache.go's KVTypeQ4_0): append
                       with on-the-fly quantisation + paged attention
@@ -52,6 +54,10 @@ CONFIGS = {
                                         "paged attention", layers=32, q_heads=32, kv_heads=8,
                                head_dim=128, page_tokens=16, batch=256, context="8192",
                                frag=True, kv_dtype="q4_0"),
+    "llama8b_b256_8k_q8": dict(workload="llama3-8b-shape decode step over q8_0 pages: append + "
+                                        "paged attention", layers=32, q_heads=32, kv_heads=8,
+                               head_dim=128, page_tokens=16, batch=256, context="8192",
+                               frag=True, kv_dtype="q8_0"),
     "llama8b_b32": dict(workload="llama3-8b-shape decode step, ragged context",
                         layers=32, q_heads=32, kv_heads=8, head_dim=128, page_tokens=16,
                         batch=32, context="U[512,4096]", frag=True),
@@ -623,8 +629,11 @@ def main():
         cpu = cpu_baseline(oracle, cfg)
 
     kind = pool.decode_kernel(H)
-    kname = (("attn_mfma_f16<%d>" % hd) if kind == 1 else
-             ("attn_valu<%d,%d,%d>" % (kv_type_of(gi, kv_dtype), hd, H // kvh)))
+    if kind == 1:
+        kname = ("attn_mfma_f16<%d>" % hd) if kv_dtype == "f16" else \
+            ("attn_mfma_q<%d,%d>" % (kv_type_of(gi, kv_dtype), hd))
+    else:
+        kname = "attn_valu<%d,%d,%d>" % (kv_type_of(gi, kv_dtype), hd, H // kvh)
     traffic = profiled_traffic(kname, args.config)
     res = {
         "metric": METRIC,

@@ -1,4 +1,4 @@
-// Paged GQA decode attention on the matrix cores, fp16 pages.
+// Paged GQA decode attention on the matrix cores: fp16, q8_0 and q4_0 pages.
 //
 // Same semantics as the vector-ALU kernel (pkg/engine/forward.go:242-267
 // with the online softmax), arranged for CDNA4's 16x16x32 f16 MFMA:
@@ -22,6 +22,17 @@
 //
 // Each of the 4 waves keeps its own running max / sum; the workgroup merges
 // them at the end, and split-K partials are merged by merge_splits.
+//
+// Quantised pages (q8_0, q4_0) stay exact.  Their integer codes are exact
+// fp16 values (a byte or nibble permute into 0x64XX, then a bias), and one
+// 32-wide k-step of S^T is exactly one quantisation block of K, so each
+// k-step's partial scores are multiplied by their K block scale in float32.
+// The V block scale varies along the P*V reduction (tokens), so it is folded
+// into P: w = p * vscale / vnorm, where vnorm is a running power of two >=
+// every V scale the wave has seen for that 32-dimension block (the
+// accumulators hold O / vnorm and are rescaled exactly when it grows).  w is
+// split into hi + lo halves like p, the lo rows carrying a further 2^11 so
+// they keep full precision; both factors are taken out in the final merge.
 #include "gi_common.h"
 #include "gi_kernels.h"
 
@@ -30,7 +41,10 @@
 namespace gi {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
 namespace mfma_decode {
 
@@ -128,6 +142,165 @@ __device__ __forceinline__ float mirror(float x)
     constexpr int ctrl = GP == 1 ? 0xB1 : GP == 2 ? 0x1B : GP == 4 ? 0x141 : 0x140;
     return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), ctrl,
                                                                0xF, 0xF, false));
+}
+
+template <bool NT, typename T>
+__device__ __forceinline__ T ldq(const uint8_t *p)
+{
+    if (NT)
+        return __builtin_nontemporal_load(reinterpret_cast<const T *>(p));
+    return *reinterpret_cast<const T *>(p);
+}
+
+// Eight int8 codes -> eight exact fp16 values: (x ^ 0x80) is x + 128 as an
+// unsigned byte, 0x64 above it makes the half 1024 + x + 128, and the bias
+// 1152 is subtracted.
+__device__ __forceinline__ h8 i8x8_to_h8(u2 w)
+{
+    const uint32_t x0 = w.x ^ 0x80808080u, x1 = w.y ^ 0x80808080u;
+    const uint32_t c = 0x64646464u;
+    const uint32_t u[4] = {__builtin_amdgcn_perm(c, x0, 0x04010400u), __builtin_amdgcn_perm(c, x0, 0x04030402u),
+                           __builtin_amdgcn_perm(c, x1, 0x04010400u), __builtin_amdgcn_perm(c, x1, 0x04030402u)};
+    const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    h8 r;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const h2 t = __builtin_bit_cast(h2, u[i]) - bias;
+        r[2 * i] = t[0];
+        r[2 * i + 1] = t[1];
+    }
+    return r;
+}
+
+// Eight Q4_0 nibbles n (the low nibbles of w's bytes when sh == 0, the high
+// ones when sh == 4) -> eight exact fp16 values n - 8: 0x64 above the
+// nibble makes the half 1024 + n, and the bias 1032 is subtracted.
+__device__ __forceinline__ h8 u4x8_to_h8(u2 w, int sh)
+{
+    const uint32_t x0 = (w.x >> sh) & 0x0F0F0F0Fu, x1 = (w.y >> sh) & 0x0F0F0F0Fu;
+    const uint32_t c = 0x64646464u;
+    const uint32_t u[4] = {__builtin_amdgcn_perm(c, x0, 0x04010400u), __builtin_amdgcn_perm(c, x0, 0x04030402u),
+                           __builtin_amdgcn_perm(c, x1, 0x04010400u), __builtin_amdgcn_perm(c, x1, 0x04030402u)};
+    const h2 bias = {(_Float16)1032.0f, (_Float16)1032.0f};
+    h8 r;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const h2 t = __builtin_bit_cast(h2, u[i]) - bias;
+        r[2 * i] = t[0];
+        r[2 * i + 1] = t[1];
+    }
+    return r;
+}
+
+// Half i of a run of uint32 words, widened to float by the hardware
+// conversion: exact for every finite half, subnormals included, since these
+// kernels run with fp16 denormals preserved (the default float mode, which
+// the code object's kernel descriptor records as float_denorm_mode_16_64 3).
+// Block scales are never NaN.
+__device__ __forceinline__ float half_at(const u4 *w, int i)
+{
+    const h8 v = __builtin_bit_cast(h8, w[i >> 3]);
+    return (float)v[i & 7];
+}
+
+// Codes and scales of one 32-token block of a quantised page, as this lane
+// feeds them to the products.
+//   k0/k1[kk]: 8 codes of K tile 0/1 row j (token 8*(j/4) + j%4, + 4 for
+//              tile 1), dimensions 32*kk + 8*g .. + 7;
+//   ks:        K scales of tokens 8g .. 8g+7, half t*KK + kk;
+//   v[..]:     8 codes of V, tokens 8g .. 8g+7: q8_0 dimension 16*nb + j for
+//              tile nb; q4_0 the byte of dimensions 32*db + j (low nibble,
+//              tile 2*db) and 32*db + 16 + j (high nibble, tile 2*db + 1);
+//   vs[db]:    V scales of block db, tokens 8g .. 8g+7.
+template <int KT, int HD>
+struct QBlock {
+    static constexpr int KK = HD / 32;
+    u2 k0[KK], k1[KK];
+    u4 ks[KK];
+    u2 v[KT == KV_Q4_0 ? KK : 2 * KK];
+    u4 vs[KK];
+};
+
+template <int KT, int HD, bool NT>
+__device__ __forceinline__ void load_kq(const DecodeArgs &a, int64_t pA, int64_t pB, int base, int64_t koff,
+                                        int64_t ksoff, int j, int g, QBlock<KT, HD> &B)
+{
+    constexpr int KK = HD / 32;
+    const PoolLayout &L = a.L;
+    const int P = L.page_tokens;
+    const int tk0 = 8 * (j >> 2) + (j & 3), tk1 = tk0 + 4;
+    const int64_t pk0 = tk0 < 16 ? pA : pB, pk1 = tk1 < 16 ? pA : pB;
+    // bytes of one token's K codes
+    constexpr int RB = KT == KV_Q4_0 ? HD / 2 : HD;
+    const uint8_t *r0 = a.base + pk0 * L.page_bytes + koff + (int64_t)((base + tk0) % P) * RB;
+    const uint8_t *r1 = a.base + pk1 * L.page_bytes + koff + (int64_t)((base + tk1) % P) * RB;
+#pragma unroll
+    for (int kk = 0; kk < KK; kk++) {
+        // q4_0: dims 8g..8g+7 of a block are the low (g < 2) or high
+        // (g >= 2) nibbles of bytes 8*(g%2) .. + 7 of its 16
+        const int off = KT == KV_Q4_0 ? 16 * kk + 8 * (g & 1) : 32 * kk + 8 * g;
+        B.k0[kk] = ldq<NT, u2>(r0 + off);
+        B.k1[kk] = ldq<NT, u2>(r1 + off);
+    }
+    const int64_t pv = g < 2 ? pA : pB;
+    const uint8_t *ksr = a.base + pv * L.page_bytes + ksoff + (int64_t)((base + 8 * g) % P) * KK * 2;
+#pragma unroll
+    for (int x = 0; x < KK; x++)
+        B.ks[x] = ldq<NT, u4>(ksr + 16 * x);
+}
+
+template <int KT, int HD, bool NT>
+__device__ __forceinline__ void load_vq(const DecodeArgs &a, int64_t pA, int64_t pB, int base, int64_t voff,
+                                        int64_t vsoff, int j, int g, QBlock<KT, HD> &B)
+{
+    constexpr int KK = HD / 32;
+    const PoolLayout &L = a.L;
+    const int P = L.page_tokens;
+    const int64_t pv = g < 2 ? pA : pB;
+    const int sv = (base + 8 * g) % P;
+    const uint8_t *pg = a.base + pv * L.page_bytes;
+    if (KT == KV_Q4_0) {
+#pragma unroll
+        for (int db = 0; db < KK; db++)
+            B.v[db] = ldq<NT, u2>(pg + voff + (int64_t)(16 * db + j) * P + sv);
+    } else {
+#pragma unroll
+        for (int nb = 0; nb < 2 * KK; nb++)
+            B.v[nb] = ldq<NT, u2>(pg + voff + (int64_t)(16 * nb + j) * P + sv);
+    }
+#pragma unroll
+    for (int db = 0; db < KK; db++)
+        B.vs[db] = ldq<NT, u4>(pg + vsoff + ((int64_t)db * P + sv) * 2);
+}
+
+// Scores of one block from quantised K: per k-step a fresh product of the
+// codes, scaled by the K block scale of its row's token, then the packed
+// hi/lo columns are completed with the lane mirror.
+template <int KT, int HD, int GP>
+__device__ __forceinline__ void qk_q(const QBlock<KT, HD> &B, const h8 *qh, int g, f4 &s0, f4 &s1)
+{
+    constexpr int KK = HD / 32;
+    s0 = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    s1 = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    const int sh = (g & 2) ? 4 : 0;
+#pragma unroll
+    for (int kk = 0; kk < KK; kk++) {
+        const h8 a0 = KT == KV_Q4_0 ? u4x8_to_h8(B.k0[kk], sh) : i8x8_to_h8(B.k0[kk]);
+        const h8 a1 = KT == KV_Q4_0 ? u4x8_to_h8(B.k1[kk], sh) : i8x8_to_h8(B.k1[kk]);
+        const f4 z0 = mfma(a0, qh[kk], f4{0.0f, 0.0f, 0.0f, 0.0f});
+        const f4 z1 = mfma(a1, qh[kk], f4{0.0f, 0.0f, 0.0f, 0.0f});
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            // output row 4g + r of tile 0 is token 8g + r, of tile 1 8g + 4 + r
+            s0[r] = fmaf(z0[r], half_at(B.ks, r * KK + kk), s0[r]);
+            s1[r] = fmaf(z1[r], half_at(B.ks, (4 + r) * KK + kk), s1[r]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        s0[r] += mirror<GP>(s0[r]);
+        s1[r] += mirror<GP>(s1[r]);
+    }
 }
 
 template <int HD, int GP>
@@ -232,15 +405,119 @@ __device__ __forceinline__ void softmax_pv(f4 s0, f4 s1, h8 *v, int base, bool o
     }
 }
 
-// GP: 0 for any group size up to 16 (hi/lo halves in separate products),
-// or the group size G in {1, 2, 4, 8} for the packed form.  NT:
-// non-temporal (streaming) loads of K/V.  PREFETCH: the next block's loads
-// are issued as soon as this block's K (then V) registers are consumed.
-// OCC: minimum waves per SIMD requested from the register allocator.
-template <int HD, int GP, bool NT, bool PREFETCH, int OCC>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void attn_mfma_f16(DecodeArgs a)
+// Online softmax and P*V for one block of a quantised page.  Rows of P are
+// packed as in softmax_pv (row j < G: hi half of head j, row 2G-1-j: lo half
+// times 2^11).  For V block db the rows carry w = p * vscale / vnorm[db].
+// Tokens past the end or on a rejected page get w = 0 (their scale may hold
+// anything) and take no part in the vnorm maxima.
+template <int KT, int HD, int GP>
+__device__ __forceinline__ void softmax_pv_q(f4 s0, f4 s1, const QBlock<KT, HD> &B, int base, bool ok, int t1,
+                                             int j, int g, float c, State<HD> &S, float *vnorm)
+{
+    constexpr int KK = HD / 32;
+    float sc[8];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        sc[r] = s0[r] * c;
+        sc[4 + r] = s1[r] * c;
+    }
+    // V scales of the lane's 8 tokens per block; in a block with tokens past
+    // the end (or on a rejected page) those get score -inf and scale 0, so
+    // whatever their slots hold takes no part in w or in the vnorm maxima.
+    float vsc[KK][8];
+#pragma unroll
+    for (int db = 0; db < KK; db++)
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            vsc[db][i] = half_at(&B.vs[db], i);
+    if (base + 32 > t1 || !ok) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            if (!(base + 8 * g + i < t1 && ok)) {
+                sc[i] = -INFINITY;
+#pragma unroll
+                for (int db = 0; db < KK; db++)
+                    vsc[db][i] = 0.0f;
+            }
+        }
+    }
+    float mx = sc[0];
+#pragma unroll
+    for (int i = 1; i < 8; i++)
+        mx = fmaxf(mx, sc[i]);
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float mnew = fmaxf(S.m2, mx);
+    const float alpha = exp2f(S.m2 - mnew);
+    S.m2 = mnew;
+    float p[8], ps = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        p[i] = exp2f(sc[i] - mnew + 14.0f);
+        ps += p[i];
+    }
+    S.lsum = S.lsum * alpha + ps;
+    if (__any(alpha != 1.0f)) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float ar = __shfl(alpha, 4 * g + r);
+#pragma unroll
+            for (int nb = 0; nb < 2 * KK; nb++)
+                S.o[nb][r] *= ar;
+        }
+    }
+    const bool lo_row = j >= GP;
+#pragma unroll
+    for (int db = 0; db < KK; db++) {
+        float mv = vsc[db][0];
+#pragma unroll
+        for (int i = 1; i < 8; i++)
+            mv = fmaxf(mv, vsc[db][i]);
+        mv = fmaxf(mv, __shfl_xor(mv, 16));
+        mv = fmaxf(mv, __shfl_xor(mv, 32));
+        // smallest power of two >= mv (a widened half or 0: never NaN)
+        uint32_t bits = __builtin_bit_cast(uint32_t, mv);
+        if (bits & 0x7FFFFFu)
+            bits = (bits & 0xFF800000u) + 0x800000u;
+        const float pw = __builtin_bit_cast(float, bits);
+        if (pw > vnorm[db]) { // uniform across the wave
+            const float f = vnorm[db] / pw;
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+                S.o[2 * db + h] *= f;
+            vnorm[db] = pw;
+        }
+        const float inv = vnorm[db] > 0.0f ? 1.0f / vnorm[db] : 0.0f; // a power of two
+        uint32_t pk[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float x0 = p[2 * k] * (vsc[db][2 * k] * inv);
+            const float x1 = p[2 * k + 1] * (vsc[db][2 * k + 1] * inv);
+            // hi by one packed round-toward-zero conversion, so lo is
+            // computed against the very value the product reads
+            const h2 hi = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(x0, x1));
+            const float l0 = fmaf(x0, 2048.0f, -2048.0f * (float)hi[0]);
+            const float l1 = fmaf(x1, 2048.0f, -2048.0f * (float)hi[1]);
+            const uint32_t lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(l0, l1));
+            pk[k] = lo_row ? lo : __builtin_bit_cast(uint32_t, hi);
+        }
+        const h8 pw8 = __builtin_bit_cast(h8, u4{pk[0], pk[1], pk[2], pk[3]});
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const h8 vv = KT == KV_Q4_0 ? u4x8_to_h8(B.v[db], 4 * h) : i8x8_to_h8(B.v[2 * db + h]);
+            S.o[2 * db + h] = mfma(pw8, vv, S.o[2 * db + h]);
+        }
+    }
+}
+
+// Body of the decode kernels.  KT: KV_F16, or KV_Q8_0 / KV_Q4_0 (packed GP
+// only).
+template <int KT, int HD, int GP, bool NT, bool PREFETCH>
+__device__ __forceinline__ void decode_body(const DecodeArgs &a)
 {
     constexpr int KK = HD / 32, NB = HD / 16;
+    constexpr bool QUANT = KT != KV_F16;
+    static_assert(!QUANT || GP != 0, "quantised pages use the packed hi/lo form");
     const PoolLayout &L = a.L;
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -320,14 +597,57 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
 #pragma unroll
     for (int nb = 0; nb < NB; nb++)
         S.o[nb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    float vnorm[KK]; // quantised pages: running power of two per V block
+#pragma unroll
+    for (int db = 0; db < KK; db++)
+        vnorm[db] = 0.0f;
 
-    const int64_t koff = L.k_off + (int64_t)kvh * P * HD * 2;
-    const int64_t voff = L.v_off + (int64_t)kvh * HD * P * 2;
+    // bytes per stored element: fp16 2, q8_0 1, q4_0 1/2
+    constexpr int EB_NUM = KT == KV_F16 ? 2 : 1, EB_DEN = KT == KV_Q4_0 ? 2 : 1;
+    const int64_t koff = L.k_off + (int64_t)kvh * P * HD * EB_NUM / EB_DEN;
+    const int64_t voff = L.v_off + (int64_t)kvh * HD * P * EB_NUM / EB_DEN;
     const int32_t *bt = a.block_tables + (int64_t)b * a.max_blocks;
     const int stride = 32 * 4;
 
     int base = t0 + 32 * w;
-    if (base < t1) {
+    if constexpr (QUANT) {
+        const int64_t ksoff = L.ks_off + (int64_t)kvh * P * KK * 2;
+        const int64_t vsoff = L.vs_off + (int64_t)kvh * KK * P * 2;
+        if (base < t1) {
+            QBlock<KT, HD> B;
+            int64_t pA, pB;
+            bool ok;
+            block_pages(a, bt, base, t1, j, g, pA, pB, ok);
+            load_kq<KT, HD, NT>(a, pA, pB, base, koff, ksoff, j, g, B);
+            load_vq<KT, HD, NT>(a, pA, pB, base, voff, vsoff, j, g, B);
+            for (;;) {
+                f4 s0, s1;
+                qk_q<KT, HD, GP>(B, qh, g, s0, s1);
+                const int next = base + stride;
+                const bool more = next < t1;
+                int64_t nA = pA, nB = pB;
+                bool nok = ok;
+                if (PREFETCH && more) {
+                    block_pages(a, bt, next, t1, j, g, nA, nB, nok);
+                    load_kq<KT, HD, NT>(a, nA, nB, next, koff, ksoff, j, g, B);
+                }
+                softmax_pv_q<KT, HD, GP>(s0, s1, B, base, ok, t1, j, g, c, S, vnorm);
+                if (!more)
+                    break;
+                if (PREFETCH) {
+                    load_vq<KT, HD, NT>(a, nA, nB, next, voff, vsoff, j, g, B);
+                } else {
+                    block_pages(a, bt, next, t1, j, g, nA, nB, nok);
+                    load_kq<KT, HD, NT>(a, nA, nB, next, koff, ksoff, j, g, B);
+                    load_vq<KT, HD, NT>(a, nA, nB, next, voff, vsoff, j, g, B);
+                }
+                pA = nA;
+                pB = nB;
+                ok = nok;
+                base = next;
+            }
+        }
+    } else if (base < t1) {
         h8 k0[KK], k1[KK], v[NB];
         int64_t pA, pB;
         bool ok;
@@ -375,8 +695,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
 #pragma unroll
     for (int nb = 0; nb < NB; nb++)
 #pragma unroll
-        for (int r = 0; r < 4; r++)
-            s_o[w][4 * g + r][16 * nb + j] = S.o[nb][r];
+        for (int r = 0; r < 4; r++) {
+            float o = S.o[nb][r];
+            if constexpr (QUANT) {
+                // rows G .. 2G-1 hold lo halves carrying 2^11; every row
+                // holds O / vnorm of its dimension block
+                const int row = 4 * g + r;
+                o *= vnorm[nb / 2] * (row >= G && row < 2 * G ? 1.0f / 2048.0f : 1.0f);
+            }
+            s_o[w][4 * g + r][16 * nb + j] = o;
+        }
     __syncthreads();
 
     for (int e = threadIdx.x; e < G * HD; e += 256) {
@@ -408,18 +736,40 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
     }
 }
 
+// GP: 0 for any group size up to 16 (hi/lo halves in separate products),
+// or the group size G in {1, 2, 4, 8} for the packed form.  NT:
+// non-temporal (streaming) loads of K/V.  PREFETCH: the next block's loads
+// are issued as soon as this block's K (then V) registers are consumed.
+// OCC: minimum waves per SIMD requested from the register allocator.
+template <int HD, int GP, bool NT, bool PREFETCH, int OCC>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void attn_mfma_f16(DecodeArgs a)
+{
+    decode_body<KV_F16, HD, GP, NT, PREFETCH>(a);
+}
+
+// q8_0 / q4_0 pages, packed form (GP = G in {1, 2, 4, 8}).
+template <int KT, int HD, int GP, bool NT, bool PREFETCH, int OCC>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void attn_mfma_q(DecodeArgs a)
+{
+    decode_body<KT, HD, GP, NT, PREFETCH>(a);
+}
+
 } // namespace mfma_decode
 
 bool mfma_decode_supported(const PoolLayout &L, int num_heads)
 {
-    if (L.kv_type != KV_F16 || L.page_tokens % 16 != 0)
+    if (L.page_tokens % 16 != 0)
         return false;
     if (L.head_dim != 64 && L.head_dim != 128)
         return false;
     if (num_heads % L.num_kv_heads)
         return false;
     const int G = num_heads / L.num_kv_heads;
-    return G >= 1 && G <= 16;
+    if (L.kv_type == KV_F16)
+        return G >= 1 && G <= 16;
+    if (L.kv_type == KV_Q8_0 || L.kv_type == KV_Q4_0)
+        return G == 1 || G == 2 || G == 4 || G == 8;
+    return false;
 }
 
 #ifndef GI_MFMA_DECODE_NT
@@ -443,6 +793,22 @@ static void launch_mfma_hd(const DecodeArgs &a, dim3 grid, hipStream_t st)
                        grid, dim3(256), 0, st, a);
 }
 
+template <int KT, int HD>
+static void launch_mfma_q(const DecodeArgs &a, dim3 grid, hipStream_t st)
+{
+#define GI_Q(GPv)                                                                                        \
+    hipLaunchKernelGGL((mfma_decode::attn_mfma_q<KT, HD, GPv, GI_MFMA_DECODE_NT, GI_MFMA_DECODE_PREFETCH, \
+                                                 GI_MFMA_DECODE_OCC>),                                  \
+                       grid, dim3(256), 0, st, a)
+    switch (a.num_heads / a.L.num_kv_heads) {
+    case 1: GI_Q(1); break;
+    case 2: GI_Q(2); break;
+    case 4: GI_Q(4); break;
+    default: GI_Q(8); break;
+    }
+#undef GI_Q
+}
+
 template <int HD>
 static void launch_mfma_g(const DecodeArgs &a, dim3 grid, hipStream_t st)
 {
@@ -458,10 +824,27 @@ static void launch_mfma_g(const DecodeArgs &a, dim3 grid, hipStream_t st)
 hipError_t launch_decode_mfma(const DecodeArgs &a, hipStream_t st)
 {
     dim3 grid(a.num_splits, a.L.num_kv_heads, a.batch);
-    if (a.L.head_dim == 128)
-        launch_mfma_g<128>(a, grid, st);
-    else
-        launch_mfma_g<64>(a, grid, st);
+    const bool h128 = a.L.head_dim == 128;
+    switch (a.L.kv_type) {
+    case KV_Q8_0:
+        if (h128)
+            launch_mfma_q<KV_Q8_0, 128>(a, grid, st);
+        else
+            launch_mfma_q<KV_Q8_0, 64>(a, grid, st);
+        break;
+    case KV_Q4_0:
+        if (h128)
+            launch_mfma_q<KV_Q4_0, 128>(a, grid, st);
+        else
+            launch_mfma_q<KV_Q4_0, 64>(a, grid, st);
+        break;
+    default:
+        if (h128)
+            launch_mfma_g<128>(a, grid, st);
+        else
+            launch_mfma_g<64>(a, grid, st);
+        break;
+    }
     return hipGetLastError();
 }
 

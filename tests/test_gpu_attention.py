@@ -31,7 +31,8 @@ def oracle_decode(oracle, pop, layer, q, H, lens, scale):
 
 def kernels_for(pool, H):
     """Every decode kernel that can serve this pool: the vector-ALU one
-    always, the matrix-core one where supported (fp16 pages)."""
+    always, the matrix-core one where supported (fp16, q8_0 and q4_0 pages
+    of 16-token multiples; quantised pages with groups of 1, 2, 4 or 8)."""
     pool.set_decode_kernel(1)
     ks = [0, 1] if pool.decode_kernel(H) == 1 else [0]
     pool.set_decode_kernel(-1)
@@ -149,25 +150,28 @@ def test_decode_empty_and_short(gi, oracle, dev):
         assert rel_err_rows(o[2], want[2], 32, 128).max() <= 1e-3
 
 
-def test_decode_stale_nan_beyond_length_is_ignored(gi, oracle, dev):
+@pytest.mark.parametrize("kv_type", [1, 2, 3], ids=["f16", "q8_0", "q4_0"])
+def test_decode_stale_nan_beyond_length_is_ignored(gi, oracle, dev, kv_type):
     """Slots past a sequence's length may hold anything (a freed page's old
-    contents): NaN there must not reach the output, as the reference never
+    contents): NaN there (for quantised pages, values of 1e30 whose fp16
+    block scales are Inf) must not reach the output, as the reference never
     reads past activeContext (forward.go:252, 259)."""
     import torch
     H, kvh, hd, P = 32, 8, 128, 16
-    pop = Populated(gi, dev, 1, 1, kvh, hd, P, [40, 40], seed=12)
-    # poison slots 20..39 of sequence 0 with NaN through the append path
+    pop = Populated(gi, dev, kv_type, 1, kvh, hd, P, [40, 40], seed=12)
+    # poison slots 20..39 of sequence 0 through the append path
     t = pop.table(0)
     ids = torch.from_numpy(np.repeat(t, P)[20:40].copy()).to(dev)
     slots = torch.from_numpy((np.arange(20, 40) % P).astype(np.int32)).to(dev)
-    nan = torch.full((20, kvh * hd), float("nan"), device=dev)
+    bad = float("nan") if kv_type == 1 else 1e30
+    nan = torch.full((20, kvh * hd), bad, device=dev)
     pop.pool.Write(0, ids, slots, nan, nan)
     bt = pop.block_tables()
     sl = torch.tensor([20, 40], dtype=torch.int32, device=dev)
     qd, q = seeded((2, H * hd), 13, dev)
     scale = oracle.attn_scale(hd)
     ks, vs = pop.stored(0, 0)
-    kw, vw = oracle.widen(1, 1024, ks[:20]), oracle.widen(1, 1024, vs[:20])
+    kw, vw = oracle.widen(kv_type, 1024, ks[:20]), oracle.widen(kv_type, 1024, vs[:20])
     want = oracle.attention_decode(q[0], kw, vw, H, kvh, hd, 20, scale)
     for kern in kernels_for(pop.pool, H):
         pop.pool.set_decode_kernel(kern)
