@@ -29,8 +29,8 @@
 // k-step's partial scores are multiplied by their K block scale in float32.
 // The V block scale varies along the P*V reduction (tokens), so it is folded
 // into P: w = p * vscale / vnorm, where vnorm is a running power of two >=
-// every V scale the wave has seen for that 32-dimension block (the
-// accumulators hold O / vnorm and are rescaled exactly when it grows).  w is
+// every V scale the wave has seen (the accumulators hold O / vnorm and are
+// rescaled exactly when it grows).  w is
 // split into hi + lo halves like p, the lo rows carrying a further 2^11 so
 // they keep full precision; both factors are taken out in the final merge.
 #include "gi_common.h"
@@ -45,6 +45,7 @@ typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+typedef uint16_t us2 __attribute__((ext_vector_type(2)));
 
 namespace mfma_decode {
 
@@ -407,12 +408,15 @@ __device__ __forceinline__ void softmax_pv(f4 s0, f4 s1, h8 *v, int base, bool o
 
 // Online softmax and P*V for one block of a quantised page.  Rows of P are
 // packed as in softmax_pv (row j < G: hi half of head j, row 2G-1-j: lo half
-// times 2^11).  For V block db the rows carry w = p * vscale / vnorm[db].
-// Tokens past the end or on a rejected page get w = 0 (their scale may hold
-// anything) and take no part in the vnorm maxima.
+// times 2^11).  For V block db the rows carry w = p * vscale / vnorm, vnorm
+// being the wave's running power-of-two cap over every V scale it has seen
+// (one cap for all blocks: the lo rows' extra 2^11 keeps 22 significant
+// bits for any scale within 2^10 of the cap).  Tokens past the end or on a
+// rejected page get score -inf and scale 0, so whatever their slots hold
+// takes no part in w or in the cap.
 template <int KT, int HD, int GP>
-__device__ __forceinline__ void softmax_pv_q(f4 s0, f4 s1, const QBlock<KT, HD> &B, int base, bool ok, int t1,
-                                             int j, int g, float c, State<HD> &S, float *vnorm)
+__device__ __forceinline__ void softmax_pv_q(f4 s0, f4 s1, QBlock<KT, HD> &B, int base, bool ok, int t1, int j,
+                                             int g, float c, State<HD> &S, float &vnorm)
 {
     constexpr int KK = HD / 32;
     float sc[8];
@@ -421,26 +425,30 @@ __device__ __forceinline__ void softmax_pv_q(f4 s0, f4 s1, const QBlock<KT, HD> 
         sc[r] = s0[r] * c;
         sc[4 + r] = s1[r] * c;
     }
-    // V scales of the lane's 8 tokens per block; in a block with tokens past
-    // the end (or on a rejected page) those get score -inf and scale 0, so
-    // whatever their slots hold takes no part in w or in the vnorm maxima.
-    float vsc[KK][8];
-#pragma unroll
-    for (int db = 0; db < KK; db++)
-#pragma unroll
-        for (int i = 0; i < 8; i++)
-            vsc[db][i] = half_at(&B.vs[db], i);
     if (base + 32 > t1 || !ok) {
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             if (!(base + 8 * g + i < t1 && ok)) {
                 sc[i] = -INFINITY;
+                const uint32_t keep = (i & 1) ? 0x0000FFFFu : 0xFFFF0000u;
 #pragma unroll
                 for (int db = 0; db < KK; db++)
-                    vsc[db][i] = 0.0f;
+                    B.vs[db][i >> 1] &= keep;
             }
         }
     }
+    // cap: the largest V scale of the block.  Scales are non-negative
+    // halves, whose bit patterns order like the values.
+    uint32_t mw = 0;
+#pragma unroll
+    for (int db = 0; db < KK; db++)
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            mw = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(us2, mw),
+                                                                         __builtin_bit_cast(us2, B.vs[db][k])));
+    uint32_t mh = max(mw & 0xFFFFu, mw >> 16);
+    mh = max(mh, (uint32_t)__shfl_xor((int)mh, 16));
+    mh = max(mh, (uint32_t)__shfl_xor((int)mh, 32));
     float mx = sc[0];
 #pragma unroll
     for (int i = 1; i < 8; i++)
@@ -457,47 +465,46 @@ __device__ __forceinline__ void softmax_pv_q(f4 s0, f4 s1, const QBlock<KT, HD> 
         ps += p[i];
     }
     S.lsum = S.lsum * alpha + ps;
-    if (__any(alpha != 1.0f)) {
+    // smallest power of two >= the largest scale (never NaN: scales come
+    // from the append's truncation, which maps NaN away)
+    uint32_t bits = __builtin_bit_cast(uint32_t, (float)__builtin_bit_cast(_Float16, (uint16_t)mh));
+    if (bits & 0x7FFFFFu)
+        bits = (bits & 0xFF800000u) + 0x800000u;
+    const float pw = __builtin_bit_cast(float, bits);
+    const bool grow = pw > vnorm; // uniform across the wave
+    const float f = grow ? vnorm / pw : 1.0f;
+    if (grow)
+        vnorm = pw;
+    if (__any(alpha != 1.0f) || grow) {
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            const float ar = __shfl(alpha, 4 * g + r);
+            const float ar = __shfl(alpha, 4 * g + r) * f;
 #pragma unroll
             for (int nb = 0; nb < 2 * KK; nb++)
                 S.o[nb][r] *= ar;
         }
     }
+    const float inv = vnorm > 0.0f ? 1.0f / vnorm : 0.0f; // a power of two
+    float pp[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+        pp[i] = p[i] * inv;
     const bool lo_row = j >= GP;
 #pragma unroll
     for (int db = 0; db < KK; db++) {
-        float mv = vsc[db][0];
-#pragma unroll
-        for (int i = 1; i < 8; i++)
-            mv = fmaxf(mv, vsc[db][i]);
-        mv = fmaxf(mv, __shfl_xor(mv, 16));
-        mv = fmaxf(mv, __shfl_xor(mv, 32));
-        // smallest power of two >= mv (a widened half or 0: never NaN)
-        uint32_t bits = __builtin_bit_cast(uint32_t, mv);
-        if (bits & 0x7FFFFFu)
-            bits = (bits & 0xFF800000u) + 0x800000u;
-        const float pw = __builtin_bit_cast(float, bits);
-        if (pw > vnorm[db]) { // uniform across the wave
-            const float f = vnorm[db] / pw;
-#pragma unroll
-            for (int h = 0; h < 2; h++)
-                S.o[2 * db + h] *= f;
-            vnorm[db] = pw;
-        }
-        const float inv = vnorm[db] > 0.0f ? 1.0f / vnorm[db] : 0.0f; // a power of two
+        const h8 vh = __builtin_bit_cast(h8, B.vs[db]);
         uint32_t pk[4];
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            const float x0 = p[2 * k] * (vsc[db][2 * k] * inv);
-            const float x1 = p[2 * k + 1] * (vsc[db][2 * k + 1] * inv);
+            // x = p / vnorm * vscale, the scale read as a half by the
+            // mixed-precision multiply-add (exact widening)
+            const float x0 = fmaf(pp[2 * k], (float)vh[2 * k], 0.0f);
+            const float x1 = fmaf(pp[2 * k + 1], (float)vh[2 * k + 1], 0.0f);
             // hi by one packed round-toward-zero conversion, so lo is
             // computed against the very value the product reads
             const h2 hi = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(x0, x1));
-            const float l0 = fmaf(x0, 2048.0f, -2048.0f * (float)hi[0]);
-            const float l1 = fmaf(x1, 2048.0f, -2048.0f * (float)hi[1]);
+            const float l0 = fmaf((float)hi[0], -2048.0f, x0 * 2048.0f);
+            const float l1 = fmaf((float)hi[1], -2048.0f, x1 * 2048.0f);
             const uint32_t lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(l0, l1));
             pk[k] = lo_row ? lo : __builtin_bit_cast(uint32_t, hi);
         }
@@ -597,10 +604,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
 #pragma unroll
     for (int nb = 0; nb < NB; nb++)
         S.o[nb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-    float vnorm[KK]; // quantised pages: running power of two per V block
-#pragma unroll
-    for (int db = 0; db < KK; db++)
-        vnorm[db] = 0.0f;
+    float vnorm = 0.0f; // quantised pages: running power-of-two cap of the V scales
 
     // bytes per stored element: fp16 2, q8_0 1, q4_0 1/2
     constexpr int EB_NUM = KT == KV_F16 ? 2 : 1, EB_DEN = KT == KV_Q4_0 ? 2 : 1;
@@ -701,7 +705,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
                 // rows G .. 2G-1 hold lo halves carrying 2^11; every row
                 // holds O / vnorm of its dimension block
                 const int row = 4 * g + r;
-                o *= vnorm[nb / 2] * (row >= G && row < 2 * G ? 1.0f / 2048.0f : 1.0f);
+                o *= vnorm * (row >= G && row < 2 * G ? 1.0f / 2048.0f : 1.0f);
             }
             s_o[w][4 * g + r][16 * nb + j] = o;
         }
