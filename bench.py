@@ -24,6 +24,10 @@ Prints one JSON line (see --help).  --config selects other shapes:
   llama8b_b256_8k_q4  the headline step over Q4_0 pages (blocks of 32 4-bit
                       values + fp16 scale, kvcache.go's KVTypeQ4_0): append
                       with on-the-fly quantisation + paged attention
+  llama8b_b256_8k_driver the headline step driven by the continuous-batching
+                      decoder (gi_batch): Step() reserves one token per sequence
+                      and updates the device tables in place, then per layer
+                      RoPE + append + paged attention for the whole batch
   llama8b_fork_b256   copy-on-write forks of 256 Llama-3-8B sequences (8197
                       tokens, fp16): the page copy each fork's first append needs;
                       reports GB/s of the copy against the reference's deep copy
@@ -58,6 +62,11 @@ CONFIGS = {
                                         "paged attention", layers=32, q_heads=32, kv_heads=8,
                                head_dim=128, page_tokens=16, batch=256, context="8192",
                                frag=True, kv_dtype="q8_0"),
+    "llama8b_b256_8k_driver": dict(workload="llama3-8b-shape decode step through the batch driver: "
+                                            "token reservation + RoPE + append + paged attention",
+                                   layers=32, q_heads=32, kv_heads=8, head_dim=128, page_tokens=16,
+                                   batch=256, context="8192", frag=True, rope_theta=500000.0,
+                                   driver=True),
     "llama8b_b32": dict(workload="llama3-8b-shape decode step, ragged context",
                         layers=32, q_heads=32, kv_heads=8, head_dim=128, page_tokens=16,
                         batch=32, context="U[512,4096]", frag=True),
@@ -93,7 +102,7 @@ def seq_lengths(cfg, seed):
     return np.full(b, int(c), np.int64)
 
 
-def build_tables(gi, cfg, lens, seed):
+def build_tables(gi, cfg, lens, seed, held=None):
     """Block tables from the host allocator (PagedKVManager), starting from a
     shuffled free list; with frag, 10 % of the sequences are then freed and
     allocated again so their pages come back in a different order."""
@@ -105,7 +114,8 @@ def build_tables(gi, cfg, lens, seed):
     if cfg["frag"]:
         mgr.SetFreeList(rng.permutation(pages).astype(np.int32))
     seqs = []
-    for n in lens:
+    held = lens if held is None else held
+    for n in held:
         s = mgr.AllocateSequence()
         mgr.AppendTokens(s, int(n))
         seqs.append(s)
@@ -114,13 +124,15 @@ def build_tables(gi, cfg, lens, seed):
         for i in rng.choice(len(seqs), size=k, replace=False):
             mgr.FreeSequence(seqs[i])
             s = mgr.AllocateSequence()
-            mgr.AppendTokens(s, int(lens[i]))
+            mgr.AppendTokens(s, int(held[i]))
             seqs[i] = s
     max_blocks = max((int(n) + P - 1) // P for n in lens)
     bt = np.zeros((len(lens), max_blocks), np.int32)
     for i, s in enumerate(seqs):
         ids = mgr.Tables[s].BlockIDs
         bt[i, :len(ids)] = ids
+    if held is not lens:
+        return mgr, pages, bt, seqs
     return mgr, pages, bt
 
 
@@ -485,6 +497,129 @@ def run_prefill(args, gi, torch, dev, cfg):
     pool.close()
 
 
+def run_driver(args, gi, torch, dev, cfg):
+    """The headline decode step through the continuous-batching driver:
+    every sequence holds 8191 tokens; each step gi_batch_step reserves token
+    8191 + i for all 256 sequences (one batched AppendToken, device tables
+    updated in place), then per layer RoPE + append + paged attention for the
+    whole batch.  Lengths grow by one per step, from 8192 at the first
+    step."""
+    H, kvh, hd, P, layers = (cfg["q_heads"], cfg["kv_heads"], cfg["head_dim"],
+                             cfg["page_tokens"], cfg["layers"])
+    kv_dim = kvh * hd
+    extra = 10                                      # isolated Step() timings after the run
+    grow = args.warmup + args.steps + extra
+    lens = seq_lengths(cfg, args.seed) + grow       # pages for the whole run
+    held = lens - grow - 1                          # 8191 tokens cached
+    mgr, pages, bt, seqs = build_tables(gi, cfg, lens, args.seed, held=held)
+    batch = len(seqs)
+    stream = torch.cuda.Stream(dev)
+    torch.cuda.set_stream(stream)
+    pool = gi.PagedKVCache(layers, kvh, hd, P, pages, gi.KV_F16, stream=stream)
+    pool.set_decode_kernel(args.decode_kernel)
+    t0 = time.perf_counter()
+    fill_pool(torch, pool, cfg, held, bt, dev, args.seed)
+    log("pool filled (%.1f s)" % (time.perf_counter() - t0))
+    max_len = int(held.max()) + grow
+    pool.SetRoPE(cfg["rope_theta"], 0, max_len + 1)
+    drv = gi.BatchDecoder(mgr, pool, batch, (max_len + P - 1) // P)
+    for sq in seqs:
+        drv.Add(sq)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed + 1)
+    q = torch.randn((layers, batch, H * hd), generator=gen, device=dev)
+    kn = torch.randn((layers, batch, kv_dim), generator=gen, device=dev)
+    vn = torch.randn((layers, batch, kv_dim), generator=gen, device=dev)
+    out = torch.empty((layers, batch, H * hd), device=dev)
+    scale = gi.attn_scale(hd)
+    def step():
+        drv.Step()
+        for l in range(layers):
+            drv.DecodeLayer(l, H, q[l], kn[l], vn[l], out[l], scale, rope=True)
+
+    for _ in range(args.warmup):
+        step()
+    pool.synchronize()
+    torch.cuda.synchronize()
+    _, lens0 = drv.Rows()
+    s0 = torch.cuda.Event(enable_timing=True)
+    s1 = torch.cuda.Event(enable_timing=True)
+    w0 = time.perf_counter()
+    s0.record(stream)
+    for _ in range(args.steps):
+        step()
+    s1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - w0
+    pool.synchronize()
+    ms_step = s0.elapsed_time(s1) / args.steps
+    # algorithmic bytes at the mean length of the timed steps
+    mean_lens = lens0.astype(np.int64) + (args.steps + 1) // 2
+    attn_bytes, app_bytes = step_bytes(cfg, mean_lens)
+    tot_gbs = (attn_bytes + app_bytes) / (ms_step * 1e-3) / 1e9
+    tok_s = batch / (ms_step * 1e-3)
+    _, lens_done = drv.Rows()    # what the last timed step attended
+    # host cost of Step() alone (256 reservations, mirror updates, uploads
+    # queued): isolated calls on an idle device; their tokens are reserved
+    # but never written, and the parity check below uses lens_done
+    host = []
+    for _ in range(extra):
+        torch.cuda.synchronize()
+        h0 = time.perf_counter()
+        drv.Step()
+        host.append(time.perf_counter() - h0)
+    torch.cuda.synchronize()
+    log("driver step %.3f ms (wall %.3f ms), host Step() median %.1f us" %
+        (ms_step, wall * 1e3 / args.steps, 1e6 * float(np.median(host))))
+    parity = None
+    if not args.no_parity:
+        import oracle
+        lens_now = lens_done
+        rng = np.random.default_rng(args.seed + 7)
+        worst, checked = 0.0, []
+        for _ in range(2):
+            r, l = int(rng.integers(batch)), int(rng.integers(layers))
+            n = int(lens_now[r])
+            t = torch.from_numpy(drv.RowTable(r)).to(dev)
+            kw, vw = pool.Get(l, t, n, widen=True)
+            pool.synchronize()
+            want = oracle.attention_decode(q[l, r].cpu().numpy(), kw.cpu().numpy(), vw.cpu().numpy(),
+                                           H, kvh, hd, n, scale)
+            got = out[l, r].cpu().numpy().astype(np.float64).reshape(H, hd)
+            w = want.astype(np.float64).reshape(H, hd)
+            worst = max(worst, float((np.abs(got - w).max(axis=1) / np.abs(w).max(axis=1)).max()))
+            checked.append([r, l])
+        parity = {"sampled_row_layer": checked, "max_rel_err": worst, "tol": 1e-3,
+                  "pass": bool(worst <= 1e-3)}
+    res = {
+        "metric": METRIC,
+        "value": round(tot_gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": cfg["workload"], "layers": layers, "q_heads": H, "kv_heads": kvh,
+                   "head_dim": hd, "kv_dtype": "f16", "page_tokens": P, "batch": batch,
+                   "context": "8191 + 1 per step", "pool_pages": pages,
+                   "fragmented_pool": cfg["frag"], "rope_theta": cfg["rope_theta"]},
+        "hbm_frac_of_peak": round(tot_gbs / HBM_PEAK_GBS, 4),
+        "tokens_per_s": round(tok_s, 1),
+        "driver_host_us_per_step_median": round(1e6 * float(np.median(host)), 1),
+        "parity": parity,
+        "cpu_baseline": None,
+        "roofline": None,
+    }
+    print(json.dumps(res), flush=True)
+    drv.close()
+    pool.close()
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -514,6 +649,9 @@ def main():
     cfg = CONFIGS[args.config]
     if cfg.get("fork"):
         run_fork(args, gi, torch, dev, cfg)
+        return
+    if cfg.get("driver"):
+        run_driver(args, gi, torch, dev, cfg)
         return
     if cfg.get("prefill"):
         run_prefill(args, gi, torch, dev, cfg)

@@ -21,7 +21,7 @@ built, loading it raises.
 import ctypes
 import os
 
-__all__ = ["lib", "GIError", "PagedKVManager", "PagedKVCache", "PrefixCache", "KV_F32", "KV_F16",
+__all__ = ["lib", "GIError", "PagedKVManager", "PagedKVCache", "PrefixCache", "BatchDecoder", "KV_F32", "KV_F16",
            "KV_Q8_0", "KV_Q4_0", "EXPORTS", "LIB_PATH", "attn_scale"]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -55,6 +55,18 @@ EXPORTS = {
     "gi_kvmgr_append_token_cow": (_c_int, [_vp, _c_int, _i32p, _i32p, _i32p]),
     "gi_kvmgr_append_tokens_cow": (_c_int, [_vp, _c_int, _c_int, _i32p, _i32p, _i32p, _i32p, _intp]),
     "gi_kvmgr_block_refs": (_c_int, [_vp, ctypes.c_int32, _intp]),
+    "gi_kvmgr_block_size": (_c_int, [_vp]),
+    "gi_kvmgr_append_batch": (_c_int, [_vp, _c_int, _intp, _i32p, _i32p, _i32p]),
+    "gi_batch_create": (_c_int, [_vp, _vp, _c_int, _c_int, ctypes.POINTER(_vp)]),
+    "gi_batch_destroy": (None, [_vp]),
+    "gi_batch_add": (_c_int, [_vp, _c_int, _intp]),
+    "gi_batch_remove": (_c_int, [_vp, _c_int]),
+    "gi_batch_step": (_c_int, [_vp, _intp]),
+    "gi_batch_rows": (_c_int, [_vp, _i32p, _i32p, _c_int, _intp]),
+    "gi_batch_row_table": (_c_int, [_vp, _c_int, _i32p, _c_int, _intp]),
+    "gi_batch_device_tables": (_c_int, [_vp, ctypes.POINTER(_vp), ctypes.POINTER(_vp), _intp]),
+    "gi_batch_decode_layer": (_c_int, [_vp, _c_int, _c_int, _vp, _vp, _vp, _vp, ctypes.c_float,
+                                       _c_int]),
     "gi_prefix_create": (_c_int, [_vp, _c_int, ctypes.POINTER(_vp)]),
     "gi_prefix_destroy": (None, [_vp]),
     "gi_prefix_store": (_c_int, [_vp, _i32p, _c_int, _c_int]),
@@ -264,6 +276,21 @@ class PagedKVManager:
         r = _c_int()
         _check(lib().gi_kvmgr_block_refs(self._h, block_id, ctypes.byref(r)))
         return r.value
+
+    def AppendBatch(self, seq_ids):
+        """One copy-on-write AppendToken per sequence, all or nothing:
+        (block_ids, slots, copy_src) int32 arrays, copy_src -1 where no
+        shared block was copied."""
+        import numpy as np
+        ids = np.ascontiguousarray(seq_ids, np.int32)
+        n = ids.size
+        b = np.zeros(max(n, 1), np.int32)
+        sl = np.zeros(max(n, 1), np.int32)
+        cf = np.zeros(max(n, 1), np.int32)
+        _check(lib().gi_kvmgr_append_batch(self._h, n, ids.ctypes.data_as(_intp),
+                                           b.ctypes.data_as(_i32p), sl.ctypes.data_as(_i32p),
+                                           cf.ctypes.data_as(_i32p)))
+        return b[:n], sl[:n], cf[:n]
 
 
 class PrefixCache:
@@ -524,3 +551,71 @@ class PagedKVCache:
             _ptr(out, torch.float32, "out"), _ptr(block_tables, torch.int32, "block_tables"),
             int(block_tables.shape[1]) if batch else 0, _ptr(start_pos, torch.int32, "start_pos"),
             float(attn_scale)))
+
+
+class BatchDecoder:
+    """Continuous-batching decode driver (gi_batch_*): a dense running set of
+    sequences over a PagedKVManager and (optionally) a PagedKVCache, with
+    device-resident block tables updated in place each step.  Replaces the
+    reference's one-sequence-at-a-time decode under Engine.mu
+    (pkg/engine/engine.go:417)."""
+
+    def __init__(self, mgr, pool, max_batch, max_blocks):
+        h = _vp()
+        _check(lib().gi_batch_create(mgr._h, pool.handle if pool is not None else None, max_batch,
+                                     max_blocks, ctypes.byref(h)))
+        self._h, self._mgr, self._pool = h, mgr, pool
+        self.max_batch, self.max_blocks = max_batch, max_blocks
+
+    def close(self):
+        if getattr(self, "_h", None) and _lib is not None:
+            _lib.gi_batch_destroy(self._h)
+        self._h = None
+
+    def __del__(self):
+        self.close()
+
+    def Add(self, seq_id):
+        r = _c_int()
+        _check(lib().gi_batch_add(self._h, seq_id, ctypes.byref(r)))
+        return r.value
+
+    def Remove(self, seq_id):
+        _check(lib().gi_batch_remove(self._h, seq_id))
+
+    def Step(self):
+        n = _c_int()
+        _check(lib().gi_batch_step(self._h, ctypes.byref(n)))
+        return n.value
+
+    def Rows(self):
+        """(sequence ids, lengths) by row."""
+        import numpy as np
+        n = _c_int()
+        ids = np.zeros(self.max_batch, np.int32)
+        lens = np.zeros(self.max_batch, np.int32)
+        _check(lib().gi_batch_rows(self._h, ids.ctypes.data_as(_i32p), lens.ctypes.data_as(_i32p),
+                                   self.max_batch, ctypes.byref(n)))
+        return ids[:n.value].copy(), lens[:n.value].copy()
+
+    def RowTable(self, row):
+        import numpy as np
+        n = _c_int()
+        ids = np.zeros(self.max_blocks, np.int32)
+        _check(lib().gi_batch_row_table(self._h, row, ids.ctypes.data_as(_i32p), self.max_blocks,
+                                        ctypes.byref(n)))
+        return ids[:n.value].copy()
+
+    def DeviceTables(self):
+        """Raw device pointers (block tables, lengths) and max_blocks."""
+        t, l, mb = _vp(), _vp(), _c_int()
+        _check(lib().gi_batch_device_tables(self._h, ctypes.byref(t), ctypes.byref(l),
+                                            ctypes.byref(mb)))
+        return t.value, l.value, mb.value
+
+    def DecodeLayer(self, layer, num_heads, q, k, v, out, attn_scale, rope=False):
+        import torch
+        _check(lib().gi_batch_decode_layer(
+            self._h, layer, num_heads, _ptr(q, torch.float32, "q"), _ptr(k, torch.float32, "k"),
+            _ptr(v, torch.float32, "v"), _ptr(out, torch.float32, "out"), float(attn_scale),
+            1 if rope else 0))

@@ -17,6 +17,7 @@
 #include "../../include/goinfer_paged.h"
 #include "gi_host.h"
 
+#include <algorithm>
 #include <deque>
 #include <mutex>
 #include <new>
@@ -310,6 +311,52 @@ int gi_kvmgr_append_tokens_cow(gi_kvmgr *m, int seq_id, int n, int32_t *block_id
         }
         if (done)
             *done = i + 1;
+    }
+    return GI_OK;
+}
+
+int gi_kvmgr_block_size(const gi_kvmgr *m) { return m ? m->block_size : 0; }
+
+int gi_kvmgr_append_batch(gi_kvmgr *m, int n, const int *seq_ids, int32_t *block_ids, int32_t *slots,
+                          int32_t *copy_src)
+{
+    if (!m || n < 0 || (n > 0 && (!seq_ids || !block_ids || !slots || !copy_src)))
+        return gi::set_error(GI_ERR_BAD_ARG, "gi_kvmgr_append_batch: bad argument");
+    std::lock_guard<std::mutex> g(m->mu);
+    // Check every sequence and count the blocks the step takes before
+    // changing anything: a new block at a block boundary, a fresh copy of a
+    // shared last block.
+    // A last block shared by c sequences of the step and held r times takes
+    // min(c, r - 1) copies: each copy drops a reference, and the last holder
+    // writes in place.
+    std::vector<gi_kvmgr::Table *> ts((size_t)n);
+    std::unordered_map<int, int> seen;
+    std::unordered_map<int32_t, uint32_t> sharers; // shared last block -> sequences of the step
+    size_t need = 0;
+    for (int i = 0; i < n; i++) {
+        auto it = m->tables.find(seq_ids[i]);
+        if (it == m->tables.end())
+            return gi::set_error(GI_ERR_UNKNOWN_SEQ, "sequence " + std::to_string(seq_ids[i]) + " not found");
+        if (!seen.emplace(seq_ids[i], i).second)
+            return gi::set_error(GI_ERR_BAD_ARG, "gi_kvmgr_append_batch: sequence " +
+                                                     std::to_string(seq_ids[i]) + " listed twice");
+        gi_kvmgr::Table &t = it->second;
+        ts[(size_t)i] = &t;
+        if (t.ids.size() < (size_t)(t.num_tokens / m->block_size) + 1)
+            need++;
+        else if (m->refs[(size_t)t.ids.back()] > 1)
+            sharers[t.ids.back()]++;
+    }
+    for (const auto &kv : sharers)
+        need += std::min<size_t>(kv.second, m->refs[(size_t)kv.first] - 1);
+    if (need > m->free_blocks.size())
+        return gi::set_error(GI_ERR_POOL_EXHAUSTED, "out of paged KV memory (the step needs " +
+                                                        std::to_string(need) + " blocks, " +
+                                                        std::to_string(m->free_blocks.size()) + " free)");
+    for (int i = 0; i < n; i++) {
+        int rc = append_locked(m, *ts[(size_t)i], seq_ids[i], block_ids + i, slots + i, copy_src + i);
+        if (rc != GI_OK) // cannot happen after the checks above
+            return rc;
     }
     return GI_OK;
 }

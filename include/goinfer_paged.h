@@ -100,6 +100,10 @@ int gi_kvmgr_append_token(gi_kvmgr *m, int seq_id, int32_t *block_id, int32_t *s
 int gi_kvmgr_append_tokens(gi_kvmgr *m, int seq_id, int n, int32_t *block_ids, int32_t *slots,
                            int *done);
 
+/* BlockSize of the manager (paged_kv.go:54, the value NewPagedKVManager
+ * settled on); 0 for NULL. */
+int gi_kvmgr_block_size(const gi_kvmgr *m);
+
 /* FreeSequence (paged_kv.go:135-148): pushes the table's ids back onto the
  * free list in table order; unknown ids are ignored. */
 int gi_kvmgr_free_sequence(gi_kvmgr *m, int seq_id);
@@ -143,6 +147,18 @@ int gi_kvmgr_append_token_cow(gi_kvmgr *m, int seq_id, int32_t *block_id, int32_
  * as *copy_src -> *copy_dst (both -1 when none). */
 int gi_kvmgr_append_tokens_cow(gi_kvmgr *m, int seq_id, int n, int32_t *block_ids,
                                int32_t *slots, int32_t *copy_src, int32_t *copy_dst, int *done);
+
+/* One copy-on-write AppendToken for each of n distinct sequences, the
+ * decode step of a running batch (Forward appends one token per sequence,
+ * forward.go:236-240).  All or nothing: if the free list cannot cover the
+ * blocks the step takes (a new block for each sequence at a block boundary,
+ * a fresh copy for each whose last block is shared), nothing changes and
+ * GI_ERR_POOL_EXHAUSTED is returned; an unknown or repeated id changes
+ * nothing either.  block_ids[i] / slots[i] are AppendToken's results for
+ * seq_ids[i]; copy_src[i] is -1, or the shared block the caller copies into
+ * block_ids[i] before writing. */
+int gi_kvmgr_append_batch(gi_kvmgr *m, int n, const int *seq_ids, int32_t *block_ids, int32_t *slots,
+                          int32_t *copy_src);
 
 /* References held on a block (0 when it is free). */
 int gi_kvmgr_block_refs(gi_kvmgr *m, int32_t block_id, int *refs);
@@ -307,6 +323,60 @@ int gi_paged_decode_kernel(const gi_paged *h, int num_heads);
  * (default), 0 vector ALU, 1 matrix core where supported.  For
  * comparisons; results agree within the attention tolerance. */
 int gi_paged_set_decode_kernel(gi_paged *h, int kind);
+
+/* ---- continuous-batching decode driver ---------------------------------- *
+ * The reference decodes one sequence at a time under Engine.mu
+ * (pkg/engine/engine.go:417), each token a full Forward of that sequence.  A
+ * gi_batch steps a running set of sequences together over one manager and
+ * one pool:
+ *   - gi_batch_step reserves one token for every running sequence
+ *     (gi_kvmgr_append_batch, all or nothing) and updates the device-resident
+ *     block tables and lengths in place (only changed entries are uploaded),
+ *     queueing the page copies of copy-on-write appends;
+ *   - gi_batch_decode_layer then runs the RoPE + append + paged attention of
+ *     one layer (forward.go:228-267) for the whole set.
+ * Rows are dense: row i of the q/k/v/out buffers is the i-th running
+ * sequence (gi_batch_rows); removing a sequence moves the last row into its
+ * place.  With h == NULL the driver keeps host bookkeeping only (for hosts
+ * that drive their own kernels, and for tests). */
+typedef struct gi_batch gi_batch;
+
+/* max_batch running sequences of up to max_blocks blocks each.  Destroy it
+ * before the pool and the manager it uses. */
+int gi_batch_create(gi_kvmgr *m, gi_paged *h, int max_batch, int max_blocks, gi_batch **out);
+void gi_batch_destroy(gi_batch *b);
+
+/* Adds an allocated sequence (its tokens so far already in the pool) as the
+ * last row; *row receives its row. */
+int gi_batch_add(gi_batch *b, int seq_id, int *row);
+
+/* Removes a running sequence (it stays allocated; FreeSequence is the
+ * caller's).  GI_ERR_UNKNOWN_SEQ if it is not running. */
+int gi_batch_remove(gi_batch *b, int seq_id);
+
+/* One token for every running sequence; *n_rows = the running count.  After
+ * it, row i's length (gi_batch_rows) includes the new token, which
+ * gi_batch_decode_layer appends at position length-1.  On
+ * GI_ERR_POOL_EXHAUSTED nothing changed: remove (preempt) a sequence and
+ * step again. */
+int gi_batch_step(gi_batch *b, int *n_rows);
+
+/* Host view: running sequence ids and lengths by row (up to cap rows). */
+int gi_batch_rows(gi_batch *b, int32_t *seq_ids, int32_t *seq_lens, int cap, int *n);
+
+/* Host mirror of one row's block table. */
+int gi_batch_row_table(gi_batch *b, int row, int32_t *ids, int cap, int *n_blocks);
+
+/* The device table ([max_batch][max_blocks] int32) and lengths, for callers
+ * that launch the attention entry points themselves. */
+int gi_batch_device_tables(gi_batch *b, int32_t **block_tables, int32_t **seq_lens, int *max_blocks);
+
+/* One layer of the step for every running row: q [n][num_heads][head_dim]
+ * (rotated in place when rope != 0, which needs gi_paged_set_rope), k, v
+ * [n][kv_dim], out [n][num_heads][head_dim]; gi_paged_rope_decode_step or
+ * gi_paged_decode_step over the driver's tables. */
+int gi_batch_decode_layer(gi_batch *b, int layer, int num_heads, float *q, const float *k, const float *v,
+                          float *out, float scale, int rope);
 
 #ifdef __cplusplus
 }
