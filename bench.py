@@ -28,6 +28,11 @@ Prints one JSON line (see --help).  --config selects other shapes:
                       decoder (gi_batch): Step() reserves one token per sequence
                       and updates the device tables in place, then per layer
                       RoPE + append + paged attention for the whole batch
+  llama8b_oproj_b256_f16 / _q8
+                      the O-projection after attention for the same batch:
+                      y = x W^T with W 4096 x 4096 (blk.N.attn_output.weight,
+                      F16 or Q8_0 GGUF bytes), batch 256, one distinct weight
+                      matrix per layer; reports TFLOP/s of the product
   llama8b_fork_b256   copy-on-write forks of 256 Llama-3-8B sequences (8197
                       tokens, fp16): the page copy each fork's first append needs;
                       reports GB/s of the copy against the reference's deep copy
@@ -67,6 +72,12 @@ CONFIGS = {
                                    layers=32, q_heads=32, kv_heads=8, head_dim=128, page_tokens=16,
                                    batch=256, context="8192", frag=True, rope_theta=500000.0,
                                    driver=True),
+    "llama8b_oproj_b256_f16": dict(workload="llama3-8b-shape O-projection: 256 x 4096 activations "
+                                            "times 4096 x 4096 F16 weights, all 32 layers",
+                                   layers=32, dim=4096, batch=256, wtype="f16"),
+    "llama8b_oproj_b256_q8": dict(workload="llama3-8b-shape O-projection: 256 x 4096 activations "
+                                           "times 4096 x 4096 Q8_0 weights, all 32 layers",
+                                  layers=32, dim=4096, batch=256, wtype="q8_0"),
     "llama8b_b32": dict(workload="llama3-8b-shape decode step, ragged context",
                         layers=32, q_heads=32, kv_heads=8, head_dim=128, page_tokens=16,
                         batch=32, context="U[512,4096]", frag=True),
@@ -620,6 +631,105 @@ def run_driver(args, gi, torch, dev, cfg):
     pool.close()
 
 
+def run_oproj(args, gi, torch, dev, cfg):
+    """y = x W^T per layer (gi_matmul_batch), W uploaded from GGUF bytes,
+    one matrix per layer so nothing is served from the caches across
+    layers."""
+    import oracle
+    D, B, layers = cfg["dim"], cfg["batch"], cfg["layers"]
+    t = {"f16": gi.GGML_F16, "q8_0": gi.GGML_Q8_0}[cfg["wtype"]]
+    stream = torch.cuda.Stream(dev)
+    torch.cuda.set_stream(stream)
+    pool = gi.PagedKVCache(1, 1, 32, 16, 1, gi.KV_F16, stream=stream)
+    W = oracle.normal(args.seed, (D, D)) * np.float32(1.0 / 64)
+    raw = oracle.quantize_weights(t, W)
+    t0 = time.perf_counter()
+    ws = [gi.Weights(pool, t, D, D, raw) for _ in range(layers)]
+    log("weights uploaded (%d x %.1f MB, %.1f s)" % (layers, raw.nbytes / 1e6, time.perf_counter() - t0))
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed + 1)
+    x = torch.randn((layers, B, D), generator=gen, device=dev)
+    y = torch.empty((layers, B, D), device=dev)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(layers * args.steps)]
+
+    def step(rec=None):
+        for l in range(layers):
+            if rec is not None:
+                ev[rec + l][0].record(stream)
+            ws[l].MatMulBatch(y[l], x[l])
+            if rec is not None:
+                ev[rec + l][1].record(stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    s0 = torch.cuda.Event(enable_timing=True)
+    s1 = torch.cuda.Event(enable_timing=True)
+    s0.record(stream)
+    for i in range(args.steps):
+        step(i * layers)
+    s1.record(stream)
+    torch.cuda.synchronize()
+    pool.synchronize()
+    ms_step = s0.elapsed_time(s1) / args.steps
+    launch_ms = float(np.mean([a.elapsed_time(b) for a, b in ev]))
+    flops = 2.0 * B * D * D
+    tflops = flops / (launch_ms * 1e-3) / 1e12
+    wbytes = raw.nbytes
+    log("oproj %.3f ms per step, %.4f ms per launch, %.1f TFLOP/s, weights %.0f GB/s" %
+        (ms_step, launch_ms, tflops, wbytes / (launch_ms * 1e-3) / 1e9))
+    parity = None
+    if not args.no_parity:
+        l = layers - 1
+        rows = [0, B // 2, B - 1]
+        xs = x[l, rows].cpu().numpy()
+        want = oracle.matmul(t, raw, xs, D, D)
+        got = y[l, rows].cpu().numpy()
+        err = float((np.abs(got - want).max(axis=1) / np.abs(want).max(axis=1)).max())
+        parity = {"sampled_layer_rows": [l, rows], "max_rel_err": err, "tol": 1e-5,
+                  "pass": bool(err <= 1e-5)}
+    cpu = None
+    if not args.no_cpu_baseline:
+        xs = x[0, :1].cpu().numpy()
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < 8.0:
+            oracle.matmul(t, raw, xs, D, D)
+            n += 1
+        el = time.perf_counter() - t0
+        cpu_tf = 2.0 * D * D * n / el / 1e12
+        cpu = {"value": round(cpu_tf, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+               "sample": "%d single-row MatMul calls (4096 x 4096 %s) on 1 thread, %.1f s"
+                         % (n, cfg["wtype"], el)}
+    res = {
+        "metric": METRIC,
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32 (%s weights)" % cfg["wtype"],
+        "data": "synthetic",
+        "config": {"workload": cfg["workload"], "layers": layers, "dim": D, "batch": B,
+                   "weight_type": cfg["wtype"]},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": 2500.0, "unit": "TFLOP/s",
+                     "frac": round(tflops / 2500.0, 4), "traffic": None,
+                     "kernel": "matmul_tile<%d>" % t, "launch_ms": round(launch_ms, 4),
+                     "flops_per_launch": flops, "weight_bytes_per_launch": wbytes,
+                     "weight_gbs": round(wbytes / (launch_ms * 1e-3) / 1e9, 1)},
+        "cpu_baseline": cpu,
+        "parity": parity,
+    }
+    print(json.dumps(res), flush=True)
+    for w in ws:
+        w.close()
+    pool.close()
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -652,6 +762,9 @@ def main():
         return
     if cfg.get("driver"):
         run_driver(args, gi, torch, dev, cfg)
+        return
+    if cfg.get("wtype"):
+        run_oproj(args, gi, torch, dev, cfg)
         return
     if cfg.get("prefill"):
         run_prefill(args, gi, torch, dev, cfg)

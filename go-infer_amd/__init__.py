@@ -21,13 +21,15 @@ built, loading it raises.
 import ctypes
 import os
 
-__all__ = ["lib", "GIError", "PagedKVManager", "PagedKVCache", "PrefixCache", "BatchDecoder", "KV_F32", "KV_F16",
+__all__ = ["lib", "GIError", "PagedKVManager", "PagedKVCache", "PrefixCache", "BatchDecoder", "Weights",
+           "GGML_F32", "GGML_F16", "GGML_Q4_0", "GGML_Q8_0", "KV_F32", "KV_F16",
            "KV_Q8_0", "KV_Q4_0", "EXPORTS", "LIB_PATH", "attn_scale"]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libgoinfer_paged.so")
 
 KV_F32, KV_F16, KV_Q8_0, KV_Q4_0 = 0, 1, 2, 3
+GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q8_0 = 0, 1, 2, 8    # pkg/gguf/types.go:25-31
 GI_OK = 0
 ERR_NAMES = {-1: "GI_ERR_NO_DEVICE", -2: "GI_ERR_OOM", -3: "GI_ERR_BAD_ARG",
              -4: "GI_ERR_POOL_EXHAUSTED", -5: "GI_ERR_HIP", -6: "GI_ERR_UNKNOWN_SEQ",
@@ -57,6 +59,9 @@ EXPORTS = {
     "gi_kvmgr_block_refs": (_c_int, [_vp, ctypes.c_int32, _intp]),
     "gi_kvmgr_block_size": (_c_int, [_vp]),
     "gi_kvmgr_append_batch": (_c_int, [_vp, _c_int, _intp, _i32p, _i32p, _i32p]),
+    "gi_weights_upload": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, ctypes.POINTER(_vp)]),
+    "gi_weights_destroy": (None, [_vp]),
+    "gi_matmul_batch": (_c_int, [_vp, _c_int, _vp, _vp]),
     "gi_batch_create": (_c_int, [_vp, _vp, _c_int, _c_int, ctypes.POINTER(_vp)]),
     "gi_batch_destroy": (None, [_vp]),
     "gi_batch_add": (_c_int, [_vp, _c_int, _intp]),
@@ -304,7 +309,12 @@ class PrefixCache:
         self._h, self._mgr = h, mgr
 
     def close(self):
-        if self._h and _lib is not None:
+        # The entries hold pages of the manager; if the garbage collector
+        # finalised the manager first (objects in one reference cycle are
+        # finalised in no set order), those pages went with it and the
+        # cache's own destroy, which releases them through the manager, is
+        # skipped.
+        if self._h and _lib is not None and getattr(self._mgr, "_h", None):
             _lib.gi_prefix_destroy(self._h)
         self._h = None
 
@@ -619,3 +629,33 @@ class BatchDecoder:
             self._h, layer, num_heads, _ptr(q, torch.float32, "q"), _ptr(k, torch.float32, "k"),
             _ptr(v, torch.float32, "v"), _ptr(out, torch.float32, "out"), float(attn_scale),
             1 if rope else 0))
+
+
+class Weights:
+    """A weight matrix [rows][cols] uploaded from its GGUF bytes (numpy uint8
+    or float32 array on the host) for gi_matmul_batch on the pool's device:
+    MatMul / MatMulBatch of pkg/engine/weights.go:237-350."""
+
+    def __init__(self, pool, ggml_type, rows, cols, raw):
+        import numpy as np
+        buf = np.ascontiguousarray(raw)
+        h = _vp()
+        _check(lib().gi_weights_upload(pool.handle, ggml_type, rows, cols, _vp(buf.ctypes.data),
+                                       ctypes.byref(h)))
+        self._h, self._pool = h, pool
+        self.ggml_type, self.rows, self.cols = ggml_type, rows, cols
+
+    def close(self):
+        if getattr(self, "_h", None) and _lib is not None:
+            _lib.gi_weights_destroy(self._h)
+        self._h = None
+
+    def __del__(self):
+        self.close()
+
+    def MatMulBatch(self, y, x):
+        """y [batch, rows] = x [batch, cols] W^T (device float32 tensors)."""
+        import torch
+        batch = int(x.shape[0]) if x.dim() > 1 else 1
+        _check(lib().gi_matmul_batch(self._h, batch, _ptr(x, torch.float32, "x"),
+                                     _ptr(y, torch.float32, "y")))

@@ -44,6 +44,7 @@ struct gi_batch {
     std::mutex mu;
     gi_kvmgr *m = nullptr;
     gi_paged *h = nullptr; // NULL: host bookkeeping only
+    int device = 0;        // frees need only this, so destroy does not use h
     int max_batch = 0;
     int max_blocks = 0;
     int page_tokens = 16;
@@ -158,6 +159,7 @@ int gi_batch_create(gi_kvmgr *m, gi_paged *h, int max_batch, int max_blocks, gi_
         void *p = nullptr;
         if ((rc = gi_dev_alloc(h, tb, &p)) == GI_OK) {
             b->d_tables = (int32_t *)p;
+            (void)hipGetDevice(&b->device); // the pool's, made current by gi_dev_alloc
             if ((rc = gi_dev_alloc(h, sizeof(int32_t) * (size_t)max_batch, &p)) == GI_OK)
                 b->d_lens = (int32_t *)p;
         }
@@ -190,11 +192,13 @@ void gi_batch_destroy(gi_batch *b)
     if (!b)
         return;
     if (b->h) {
-        // wait for queued uploads without consuming the pool's error flags
-        (void)hipStreamSynchronize(stream_of(b));
+        // Does not touch the pool handle, which may be gone already; waits
+        // for the device's queued work (uploads, kernels reading the tables).
+        if (hipSetDevice(b->device) == hipSuccess)
+            (void)hipDeviceSynchronize();
         for (int32_t *p : {b->d_tables, b->d_lens, b->d_pairs, b->d_copy})
             if (p)
-                (void)gi_dev_free(b->h, p);
+                (void)hipFree(p);
         if (b->h_stage)
             (void)hipHostFree(b->h_stage);
         for (hipEvent_t e : b->staged)

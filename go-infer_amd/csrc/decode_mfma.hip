@@ -35,16 +35,19 @@
 // they keep full precision; both factors are taken out in the final merge.
 #include "gi_common.h"
 #include "gi_kernels.h"
+#include "mfma_ops.h"
 
 #include <math.h>
 
 namespace gi {
 
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-typedef float f4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u2 __attribute__((ext_vector_type(2)));
-typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+using mfma_ops::h2;
+using mfma_ops::h8;
+using mfma_ops::f4;
+using mfma_ops::u2;
+using mfma_ops::u4;
+using mfma_ops::i8x8_to_h8;
+using mfma_ops::u4x8_to_h8;
 typedef uint16_t us2 __attribute__((ext_vector_type(2)));
 
 namespace mfma_decode {
@@ -151,46 +154,6 @@ __device__ __forceinline__ T ldq(const uint8_t *p)
     if (NT)
         return __builtin_nontemporal_load(reinterpret_cast<const T *>(p));
     return *reinterpret_cast<const T *>(p);
-}
-
-// Eight int8 codes -> eight exact fp16 values: (x ^ 0x80) is x + 128 as an
-// unsigned byte, 0x64 above it makes the half 1024 + x + 128, and the bias
-// 1152 is subtracted.
-__device__ __forceinline__ h8 i8x8_to_h8(u2 w)
-{
-    const uint32_t x0 = w.x ^ 0x80808080u, x1 = w.y ^ 0x80808080u;
-    const uint32_t c = 0x64646464u;
-    const uint32_t u[4] = {__builtin_amdgcn_perm(c, x0, 0x04010400u), __builtin_amdgcn_perm(c, x0, 0x04030402u),
-                           __builtin_amdgcn_perm(c, x1, 0x04010400u), __builtin_amdgcn_perm(c, x1, 0x04030402u)};
-    const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
-    h8 r;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const h2 t = __builtin_bit_cast(h2, u[i]) - bias;
-        r[2 * i] = t[0];
-        r[2 * i + 1] = t[1];
-    }
-    return r;
-}
-
-// Eight Q4_0 nibbles n (the low nibbles of w's bytes when sh == 0, the high
-// ones when sh == 4) -> eight exact fp16 values n - 8: 0x64 above the
-// nibble makes the half 1024 + n, and the bias 1032 is subtracted.
-__device__ __forceinline__ h8 u4x8_to_h8(u2 w, int sh)
-{
-    const uint32_t x0 = (w.x >> sh) & 0x0F0F0F0Fu, x1 = (w.y >> sh) & 0x0F0F0F0Fu;
-    const uint32_t c = 0x64646464u;
-    const uint32_t u[4] = {__builtin_amdgcn_perm(c, x0, 0x04010400u), __builtin_amdgcn_perm(c, x0, 0x04030402u),
-                           __builtin_amdgcn_perm(c, x1, 0x04010400u), __builtin_amdgcn_perm(c, x1, 0x04030402u)};
-    const h2 bias = {(_Float16)1032.0f, (_Float16)1032.0f};
-    h8 r;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const h2 t = __builtin_bit_cast(h2, u[i]) - bias;
-        r[2 * i] = t[0];
-        r[2 * i + 1] = t[1];
-    }
-    return r;
 }
 
 // Half i of a run of uint32 words, widened to float by the hardware

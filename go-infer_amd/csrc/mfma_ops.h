@@ -1,0 +1,64 @@
+// Matrix-core helpers shared by the decode and matmul kernels: operand
+// types, the 16x16x32 f16 product, and exact conversions of quantised codes
+// (int8 and Q4_0 nibbles) into fp16 operands.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace gi {
+namespace mfma_ops {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f4 mfma16(h8 a, h8 b, f4 c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// Eight int8 codes -> eight exact fp16 values: (x ^ 0x80) is x + 128 as an
+// unsigned byte, 0x64 above it makes the half 1024 + x + 128, and the bias
+// 1152 is subtracted.
+__device__ __forceinline__ h8 i8x8_to_h8(u2 w)
+{
+    const uint32_t x0 = w.x ^ 0x80808080u, x1 = w.y ^ 0x80808080u;
+    const uint32_t c = 0x64646464u;
+    const uint32_t u[4] = {__builtin_amdgcn_perm(c, x0, 0x04010400u), __builtin_amdgcn_perm(c, x0, 0x04030402u),
+                           __builtin_amdgcn_perm(c, x1, 0x04010400u), __builtin_amdgcn_perm(c, x1, 0x04030402u)};
+    const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    h8 r;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const h2 t = __builtin_bit_cast(h2, u[i]) - bias;
+        r[2 * i] = t[0];
+        r[2 * i + 1] = t[1];
+    }
+    return r;
+}
+
+// Eight Q4_0 nibbles n (the low nibbles of w's bytes when sh == 0, the high
+// ones when sh == 4) -> eight exact fp16 values n - 8: 0x64 above the
+// nibble makes the half 1024 + n, and the bias 1032 is subtracted.
+__device__ __forceinline__ h8 u4x8_to_h8(u2 w, int sh)
+{
+    const uint32_t x0 = (w.x >> sh) & 0x0F0F0F0Fu, x1 = (w.y >> sh) & 0x0F0F0F0Fu;
+    const uint32_t c = 0x64646464u;
+    const uint32_t u[4] = {__builtin_amdgcn_perm(c, x0, 0x04010400u), __builtin_amdgcn_perm(c, x0, 0x04030402u),
+                           __builtin_amdgcn_perm(c, x1, 0x04010400u), __builtin_amdgcn_perm(c, x1, 0x04030402u)};
+    const h2 bias = {(_Float16)1032.0f, (_Float16)1032.0f};
+    h8 r;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const h2 t = __builtin_bit_cast(h2, u[i]) - bias;
+        r[2 * i] = t[0];
+        r[2 * i + 1] = t[1];
+    }
+    return r;
+}
+
+} // namespace mfma_ops
+} // namespace gi

@@ -324,6 +324,37 @@ int gi_paged_decode_kernel(const gi_paged *h, int num_heads);
  * comparisons; results agree within the attention tolerance. */
 int gi_paged_set_decode_kernel(gi_paged *h, int kind);
 
+/* ---- weight matrix times activations: the O-projection ------------------ *
+ * After attention, Forward projects AttnOut through blk.%d.attn_output.weight
+ * (pkg/engine/forward.go:270, 580: Weights.MatMul / MatMulBatch,
+ * pkg/engine/weights.go:237-350), y = W x with W [rows][cols] in GGUF layout.
+ * The GPU seam it replaces is metal.MatMulBatch(y, x, rawW, qType,
+ * batchSize, rows, cols) (pkg/metal/metal_darwin.go:849-880).  Weights are
+ * uploaded once into an operand layout (gi_weights), as the reference keeps
+ * GPU buffers per tensor (Weights.GPUBufs, metal.MatMulBatchBuf). */
+
+/* GGML type ids (pkg/gguf/types.go:25-31) with a device kernel. */
+#define GI_GGML_F32 0
+#define GI_GGML_F16 1
+#define GI_GGML_Q4_0 2
+#define GI_GGML_Q8_0 8
+
+typedef struct gi_weights gi_weights;
+
+/* Uploads a [rows][cols] weight matrix given as its GGUF bytes (host memory:
+ * F32 / F16 rows, or rows of cols/32 Q4_0 / Q8_0 blocks) to the pool's
+ * device.  cols must be a multiple of 32.  Other types: GI_ERR_BAD_ARG.
+ * gi_matmul_batch needs the pool alive; gi_weights_destroy does not (it
+ * waits for the device and frees the buffers itself). */
+int gi_weights_upload(gi_paged *h, int ggml_type, int rows, int cols, const void *raw, gi_weights **out);
+void gi_weights_destroy(gi_weights *w);
+
+/* y[b][r] = sum_c W[r][c] x[b][c] for b < batch (DotVecF32 / DotVecF16 /
+ * DotVecQ4_0 / DotVecQ8_0 of each row, pkg/math/gemv.go), on the pool's
+ * stream; x [batch][cols], y [batch][rows] float32 device buffers.  Results
+ * agree with the reference's float32 loops up to summation order. */
+int gi_matmul_batch(gi_weights *w, int batch, const float *x, float *y);
+
 /* ---- continuous-batching decode driver ---------------------------------- *
  * The reference decodes one sequence at a time under Engine.mu
  * (pkg/engine/engine.go:417), each token a full Forward of that sequence.  A
@@ -341,8 +372,8 @@ int gi_paged_set_decode_kernel(gi_paged *h, int kind);
  * that drive their own kernels, and for tests). */
 typedef struct gi_batch gi_batch;
 
-/* max_batch running sequences of up to max_blocks blocks each.  Destroy it
- * before the pool and the manager it uses. */
+/* max_batch running sequences of up to max_blocks blocks each.  Steps need
+ * the manager and pool alive; gi_batch_destroy needs neither. */
 int gi_batch_create(gi_kvmgr *m, gi_paged *h, int max_batch, int max_blocks, gi_batch **out);
 void gi_batch_destroy(gi_batch *b);
 

@@ -69,6 +69,11 @@ def lib():
             "ref_apply_rope": (None, [_f32p, _int, _int, ctypes.c_float]),
             "ref_rope_heads": (None, [_f32p, _int, _int, _int, _int, ctypes.c_float]),
             "ref_rope_table": (None, [ctypes.c_float, _int, _int, _int, _f32p]),
+            "ref_dot_vec_f16": (ctypes.c_float, [_f32p, _u16p, _int]),
+            "ref_dot_vec_q8_0": (ctypes.c_float, [_f32p, _u8p, _int]),
+            "ref_dot_vec_q4_0": (ctypes.c_float, [_f32p, _u8p, _int]),
+            "ref_weight_row_bytes": (_i64, [_int, _int]),
+            "ref_matmul": (None, [_int, _int, _int, _int, _u8p, _f32p, _f32p]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -184,6 +189,43 @@ def rope_table(theta, rope_dim, pos0, n_pos):
     out = np.empty((n_pos, rope_dim // 2, 2), np.float32)
     lib().ref_rope_table(float(theta), rope_dim, pos0, n_pos, _p(out, _f32p))
     return out
+
+
+# ---- weight matrices (pkg/math/gemv.go, pkg/quant/quant.go DotVec*) --------
+
+GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q8_0 = 0, 1, 2, 8     # pkg/gguf/types.go:25-31
+
+
+def weight_row_bytes(ggml_type, cols):
+    return int(lib().ref_weight_row_bytes(ggml_type, cols))
+
+
+def quantize_weights(ggml_type, wf):
+    """GGUF bytes of a float32 matrix [rows, cols] stored as ggml_type (F32
+    bits, FP32ToFP16 halves, or QuantizeQ8_0 / QuantizeQ4_0 blocks per row)."""
+    wf = _c(wf, np.float32)
+    rows, cols = wf.shape
+    if ggml_type == GGML_F32:
+        return wf.view(np.uint8).reshape(rows, -1).copy()
+    if ggml_type == GGML_F16:
+        return fp32_to_fp16(wf).view(np.uint8).reshape(rows, -1)
+    q = quantize_q8_0 if ggml_type == GGML_Q8_0 else quantize_q4_0
+    return q(wf).reshape(rows, -1)
+
+
+def matmul(ggml_type, w_raw, x, rows, cols):
+    """MatMul of gemv.go for every row of x [batch, cols] -> y [batch, rows]."""
+    w_raw = _c(w_raw, np.uint8)
+    x = _c(x, np.float32).reshape(-1, cols)
+    y = np.empty((x.shape[0], rows), np.float32)
+    lib().ref_matmul(ggml_type, x.shape[0], rows, cols, _p(w_raw, _u8p), _p(x, _f32p), _p(y, _f32p))
+    return y
+
+
+def dot_vec_q4_0(x, blocks):
+    x = _c(x, np.float32)
+    blocks = _c(blocks, np.uint8)
+    return np.float32(lib().ref_dot_vec_q4_0(_p(x, _f32p), _p(blocks, _u8p), x.size))
 
 
 # ---- KVCache semantics ------------------------------------------------------

@@ -552,3 +552,88 @@ void ref_rope_table(float theta, int rope_dim, int pos0, int n_pos, float *out)
         }
     }
 }
+
+/* ---- weight matrix times activations (the O-projection after attention) -- */
+
+/* pkg/quant/quant.go:569-577 DotVecF16: sequential float32 sum of
+ * x[i] * FP16ToFP32(w[i]). */
+float ref_dot_vec_f16(const float *x, const uint16_t *w, int n)
+{
+    float sum = 0.0f;
+    for (int i = 0; i < n; i++)
+        sum += x[i] * ref_fp16_to_fp32(w[i]);
+    return sum;
+}
+
+/* quant.go:320-339 DotVecQ8_0: per block of 32, blockSum += float32(q) * x in
+ * order, then total += blockSum * d. */
+float ref_dot_vec_q8_0(const float *x, const uint8_t *blocks, int n)
+{
+    float total = 0.0f;
+    for (int b = 0; b < n / 32; b++) {
+        const uint8_t *blk = blocks + (int64_t)b * 34;
+        float d = ref_fp16_to_fp32((uint16_t)(blk[0] | (blk[1] << 8)));
+        float bs = 0.0f;
+        for (int j = 0; j < 32; j++)
+            bs += (float)(int8_t)blk[2 + j] * x[b * 32 + j];
+        total += bs * d;
+    }
+    return total;
+}
+
+/* quant.go:294-317 DotVecQ4_0: per block, blockSum += v0*x[j] + v1*x[j+16]
+ * for byte j (v0 low nibble - 8, v1 high nibble - 8), then total +=
+ * blockSum * d. */
+float ref_dot_vec_q4_0(const float *x, const uint8_t *blocks, int n)
+{
+    float total = 0.0f;
+    for (int b = 0; b < n / 32; b++) {
+        const uint8_t *blk = blocks + (int64_t)b * 18;
+        float d = ref_fp16_to_fp32((uint16_t)(blk[0] | (blk[1] << 8)));
+        float bs = 0.0f;
+        for (int j = 0; j < 16; j++) {
+            float v0 = (float)((int)(blk[2 + j] & 0x0F) - 8);
+            float v1 = (float)((int)((blk[2 + j] >> 4) & 0x0F) - 8);
+            bs += v0 * x[b * 32 + j] + v1 * x[b * 32 + j + 16];
+        }
+        total += bs * d;
+    }
+    return total;
+}
+
+/* Bytes of one weight row of a GGML type (0 F32, 1 F16, 2 Q4_0, 8 Q8_0;
+ * pkg/gguf/types.go:25-31), 0 for other types. */
+int64_t ref_weight_row_bytes(int ggml_type, int cols)
+{
+    switch (ggml_type) {
+    case 0: return (int64_t)cols * 4;
+    case 1: return (int64_t)cols * 2;
+    case 2: return (int64_t)(cols / 32) * 18;
+    case 8: return (int64_t)(cols / 32) * 34;
+    }
+    return 0;
+}
+
+/* pkg/math/gemv.go:27-59 (MatMulF32), 62-96 (Q4_0), 98-132 (Q8_0), 206-240
+ * (F16): y[r] = DotVec<type>(x, row r of w), for each of batch rows of x
+ * (the batch of metal.MatMulBatch, pkg/metal/metal_darwin.go:849-880, is a
+ * row-by-row repetition of the GEMV).  x [batch][cols], y [batch][rows]. */
+void ref_matmul(int ggml_type, int batch, int rows, int cols, const uint8_t *w, const float *x,
+                float *y)
+{
+    int64_t rb = ref_weight_row_bytes(ggml_type, cols);
+    for (int b = 0; b < batch; b++) {
+        const float *xb = x + (int64_t)b * cols;
+        for (int r = 0; r < rows; r++) {
+            const uint8_t *wr = w + (int64_t)r * rb;
+            float v = 0.0f;
+            switch (ggml_type) {
+            case 0: v = ref_dot_vec_f32(xb, (const float *)wr, cols); break;
+            case 1: v = ref_dot_vec_f16(xb, (const uint16_t *)wr, cols); break;
+            case 2: v = ref_dot_vec_q4_0(xb, wr, cols); break;
+            case 8: v = ref_dot_vec_q8_0(xb, wr, cols); break;
+            }
+            y[(int64_t)b * rows + r] = v;
+        }
+    }
+}
