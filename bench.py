@@ -33,6 +33,13 @@ Prints one JSON line (see --help).  --config selects other shapes:
                       y = x W^T with W 4096 x 4096 (blk.N.attn_output.weight,
                       F16 or Q8_0 GGUF bytes), batch 256, one distinct weight
                       matrix per layer; reports TFLOP/s of the product
+  tinyllama_b1        the reference's CPU-runnable case: TinyLlama-1.1B-shaped KV
+                      (22 layers, 32 q / 4 kv heads, head_dim 64), f32 pages of
+                      16 tokens allocated in order, batch 1; one step = a
+                      128-token prompt appended, then 128 decode tokens (append
+                      + attention over 129..256 tokens, every layer); reports
+                      decode tokens/s, timed beside the oracle running the
+                      whole case on one core
   llama8b_fork_b256   copy-on-write forks of 256 Llama-3-8B sequences (8197
                       tokens, fp16): the page copy each fork's first append needs;
                       reports GB/s of the copy against the reference's deep copy
@@ -78,6 +85,10 @@ CONFIGS = {
     "llama8b_oproj_b256_q8": dict(workload="llama3-8b-shape O-projection: 256 x 4096 activations "
                                            "times 4096 x 4096 Q8_0 weights, all 32 layers",
                                   layers=32, dim=4096, batch=256, wtype="q8_0"),
+    "tinyllama_b1": dict(workload="tinyllama-1.1b-shape KV path, batch 1: 128-token prompt then 128 "
+                                  "decode steps (append + paged attention), all 22 layers",
+                         layers=22, q_heads=32, kv_heads=4, head_dim=64, page_tokens=16, batch=1,
+                         prompt=128, decode=128, tiny=True),
     "llama8b_b32": dict(workload="llama3-8b-shape decode step, ragged context",
                         layers=32, q_heads=32, kv_heads=8, head_dim=128, page_tokens=16,
                         batch=32, context="U[512,4096]", frag=True),
@@ -730,6 +741,120 @@ def run_oproj(args, gi, torch, dev, cfg):
     pool.close()
 
 
+def run_tinyllama(args, gi, torch, dev, cfg):
+    """Config A end to end on the device, step = prompt + 128 decode tokens."""
+    import oracle
+    H, kvh, hd, P, layers = (cfg["q_heads"], cfg["kv_heads"], cfg["head_dim"],
+                             cfg["page_tokens"], cfg["layers"])
+    kv_dim = kvh * hd
+    T0, ND = cfg["prompt"], cfg["decode"]
+    total = T0 + ND
+    pages = total // P
+    stream = torch.cuda.Stream(dev)
+    torch.cuda.set_stream(stream)
+    pool = gi.PagedKVCache(layers, kvh, hd, P, pages, gi.KV_F32, stream=stream)
+    pool.set_decode_kernel(args.decode_kernel)
+    K = torch.from_numpy(np.stack([oracle.normal(1000 + l, (total, kv_dim)) for l in range(layers)])).to(dev)
+    V = torch.from_numpy(np.stack([oracle.normal(2000 + l, (total, kv_dim)) for l in range(layers)])).to(dev)
+    Q = torch.from_numpy(oracle.normal(3000, (ND, layers, H * hd))).to(dev)
+    out = torch.empty((ND, layers, H * hd), device=dev)
+    scale = gi.attn_scale(hd)
+    # pages allocated in order, as the reference's allocator hands them out
+    mgr = gi.PagedKVManager(layers, kv_dim, pages, P)
+    sid = mgr.AllocateSequence()
+    ids, slots = mgr.AppendTokens(sid, total)
+    bt = torch.tensor(mgr.Tables[sid].BlockIDs, dtype=torch.int32, device=dev)[None, :].contiguous()
+    ids_d = torch.from_numpy(ids[:T0].copy()).to(dev)
+    slots_d = torch.from_numpy(slots[:T0].copy()).to(dev)
+    lens = [torch.tensor([T0 + i + 1], dtype=torch.int32, device=dev) for i in range(ND)]
+
+    def run():
+        for l in range(layers):
+            pool.Write(l, ids_d, slots_d, K[l, :T0], V[l, :T0])
+        for i in range(ND):
+            n = T0 + i + 1
+            for l in range(layers):
+                pool.DecodeStep(out[i, l], Q[i, l], K[l, n - 1:n], V[l, n - 1:n], l, bt, lens[i], H, scale,
+                                max_seq_len=n)
+
+    for _ in range(max(1, args.warmup)):
+        run()
+    torch.cuda.synchronize()
+    s0 = torch.cuda.Event(enable_timing=True)
+    s1 = torch.cuda.Event(enable_timing=True)
+    w0 = time.perf_counter()
+    s0.record(stream)
+    for _ in range(args.steps):
+        run()
+    s1.record(stream)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - w0) / args.steps
+    pool.synchronize()
+    ms_step = s0.elapsed_time(s1) / args.steps
+    tok_s = ND / (ms_step * 1e-3)
+    # algorithmic bytes of one step: the prompt's append, then per decode
+    # token and layer K+V over n tokens, q/out, the appended K/V
+    e = 4
+    byt = layers * T0 * 2 * kv_dim * (4 + e)
+    for i in range(ND):
+        n = T0 + i + 1
+        byt += layers * (2 * n * kv_dim * e + ((n + P - 1) // P) * 4 + 2 * H * hd * 4
+                         + 2 * kv_dim * (4 + e))
+    gbs = byt / (ms_step * 1e-3) / 1e9
+    log("tinyllama step %.3f ms (wall %.3f ms): %.0f decode tokens/s" % (ms_step, wall * 1e3, tok_s))
+    parity = None
+    if not args.no_parity:
+        Kh, Vh, Qh, Oh = K.cpu().numpy(), V.cpu().numpy(), Q.cpu().numpy(), out.cpu().numpy()
+        worst = 0.0
+        for i in (0, ND // 2, ND - 1):
+            n = T0 + i + 1
+            for l in (0, layers - 1):
+                want = oracle.attention_decode(Qh[i, l], Kh[l, :n], Vh[l, :n], H, kvh, hd, n, scale)
+                g = Oh[i, l].astype(np.float64).reshape(H, hd)
+                w = want.astype(np.float64).reshape(H, hd)
+                worst = max(worst, float((np.abs(g - w).max(axis=1) / np.abs(w).max(axis=1)).max()))
+        parity = {"sampled_steps": [0, ND // 2, ND - 1], "max_rel_err": worst, "tol": 1e-5,
+                  "pass": bool(worst <= 1e-5)}
+    cpu = None
+    if not args.no_cpu_baseline:
+        # the whole case on one core: the reference's store and decode loop
+        Kh, Vh, Qh = K.cpu().numpy(), V.cpu().numpy(), Q.cpu().numpy()
+        t0 = time.perf_counter()
+        for i in range(ND):
+            n = T0 + i + 1
+            for l in range(layers):
+                oracle.attention_decode(Qh[i, l], Kh[l, :n], Vh[l, :n], H, kvh, hd, n, scale)
+        el = time.perf_counter() - t0
+        cpu = {"value": round(ND / el, 2), "unit": "tokens/s", "cores": 1, "kind": "port",
+               "sample": "the whole case (128 decode tokens x 22 layers, 129..256 tokens of "
+                         "context) on 1 thread: %.2f s" % el}
+    res = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": cfg["workload"], "layers": layers, "q_heads": H, "kv_heads": kvh,
+                   "head_dim": hd, "kv_dtype": "f32", "page_tokens": P, "batch": 1,
+                   "prompt": T0, "decode": ND},
+        "tokens_per_s": round(tok_s, 1),
+        "us_per_token": round(ms_step * 1e3 / ND, 2),
+        "hbm_frac_of_peak": round(gbs / HBM_PEAK_GBS, 5),
+        "roofline": None,
+        "cpu_baseline": cpu,
+        "parity": parity,
+    }
+    print(json.dumps(res), flush=True)
+    pool.close()
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -765,6 +890,9 @@ def main():
         return
     if cfg.get("wtype"):
         run_oproj(args, gi, torch, dev, cfg)
+        return
+    if cfg.get("tiny"):
+        run_tinyllama(args, gi, torch, dev, cfg)
         return
     if cfg.get("prefill"):
         run_prefill(args, gi, torch, dev, cfg)
