@@ -68,22 +68,34 @@ __device__ __forceinline__ h8 ld16(const uint8_t *p)
 }
 
 // Pages holding tokens base and base+16 of a 32-token block (equal when one
-// page holds both or the second half is past the end).  Ids outside the pool
-// are reported and replaced by page 0; their tokens are masked.
+// page holds both or the second half is past the end), and the in-page slots
+// of those two tokens.  Each 16-token half lies inside one page (pages hold a
+// multiple of 16 tokens, blocks start at multiples of 32), so token t < 32 of
+// the block sits in slot sA + t (t < 16) or sB + t - 16.  Everything here is
+// wave-uniform: the table entries are read through the scalar cache (the
+// tables are not written while a decode kernel runs), so fetching them never
+// waits for the vector loads in flight.  Ids outside the pool are reported
+// and replaced by page 0; their tokens are masked.
 // (Plain scalars rather than a struct: a struct carried across the loop is
 // not promoted to registers by the compiler.)
 __device__ __forceinline__ void block_pages(const DecodeArgs &a, const int32_t *bt, int base, int t1,
-                                            int j, int g, int64_t &pA, int64_t &pB, bool &ok)
+                                            int64_t &pA, int64_t &pB, int &sA, int &sB, bool &ok)
 {
+    typedef const __attribute__((address_space(4))) int32_t *const_i32;
     const PoolLayout &L = a.L;
     const int P = L.page_tokens;
-    pA = bt[base / P];
-    pB = base + 16 < t1 ? (int64_t)bt[(base + 16) / P] : pA;
+    base = __builtin_amdgcn_readfirstlane(base);
+    const int ia = base / P, ib = (base + 16) / P;
+    sA = base - ia * P;
+    sB = base + 16 - ib * P;
+    const const_i32 cb = (const_i32)bt;
+    pA = cb[ia];
+    pB = base + 16 < t1 ? (int64_t)cb[ib] : pA;
     const bool okA = pA >= 0 && pA < L.num_pages;
     const bool okB = pB >= 0 && pB < L.num_pages;
     ok = okA && okB;
     if (!ok) {
-        if (j == 0 && g == 0 && a.status)
+        if ((threadIdx.x & 63) == 0 && a.status)
             atomicOr(a.status, FLAG_BAD_PAGE);
         if (!okA)
             pA = 0;
@@ -94,15 +106,15 @@ __device__ __forceinline__ void block_pages(const DecodeArgs &a, const int32_t *
 
 // K rows: tile 0 row j is token 8*(j/4) + j%4 of the block, tile 1 adds 4.
 template <int HD, bool NT>
-__device__ __forceinline__ void load_k(const DecodeArgs &a, int64_t pA, int64_t pB, int base,
+__device__ __forceinline__ void load_k(const DecodeArgs &a, int64_t pA, int64_t pB, int sA, int sB,
                                        int64_t koff, int j, int g, h8 *k0, h8 *k1)
 {
     const PoolLayout &L = a.L;
-    const int P = L.page_tokens;
     const int tk0 = 8 * (j >> 2) + (j & 3), tk1 = tk0 + 4;
     const int64_t pk0 = tk0 < 16 ? pA : pB, pk1 = tk1 < 16 ? pA : pB;
-    const uint8_t *r0 = a.base + pk0 * L.page_bytes + koff + (int64_t)((base + tk0) % P) * HD * 2;
-    const uint8_t *r1 = a.base + pk1 * L.page_bytes + koff + (int64_t)((base + tk1) % P) * HD * 2;
+    const int sk0 = (tk0 < 16 ? sA : sB) + (tk0 & 15), sk1 = (tk1 < 16 ? sA : sB) + (tk1 & 15);
+    const uint8_t *r0 = a.base + pk0 * L.page_bytes + koff + sk0 * HD * 2;
+    const uint8_t *r1 = a.base + pk1 * L.page_bytes + koff + sk1 * HD * 2;
 #pragma unroll
     for (int kk = 0; kk < HD / 32; kk++) {
         k0[kk] = ld16<NT>(r0 + (32 * kk + 8 * g) * 2);
@@ -112,13 +124,14 @@ __device__ __forceinline__ void load_k(const DecodeArgs &a, int64_t pA, int64_t 
 
 // V: tokens 8g .. 8g+7 of the block, dimension 16*nb + j.
 template <int HD, bool NT>
-__device__ __forceinline__ void load_v(const DecodeArgs &a, int64_t pA, int64_t pB, int base,
+__device__ __forceinline__ void load_v(const DecodeArgs &a, int64_t pA, int64_t pB, int sA, int sB,
                                        int64_t voff, int j, int g, h8 *v)
 {
     const PoolLayout &L = a.L;
     const int P = L.page_tokens;
     const int64_t pv = g < 2 ? pA : pB;
-    const uint8_t *vr = a.base + pv * L.page_bytes + voff + (int64_t)((base + 8 * g) % P) * 2;
+    const int sv = (g < 2 ? sA : sB) + 8 * (g & 1);
+    const uint8_t *vr = a.base + pv * L.page_bytes + voff + sv * 2;
 #pragma unroll
     for (int nb = 0; nb < HD / 16; nb++)
         v[nb] = ld16<NT>(vr + (int64_t)(16 * nb + j) * P * 2);
@@ -186,18 +199,18 @@ struct QBlock {
 };
 
 template <int KT, int HD, bool NT>
-__device__ __forceinline__ void load_kq(const DecodeArgs &a, int64_t pA, int64_t pB, int base, int64_t koff,
+__device__ __forceinline__ void load_kq(const DecodeArgs &a, int64_t pA, int64_t pB, int sA, int sB, int64_t koff,
                                         int64_t ksoff, int j, int g, QBlock<KT, HD> &B)
 {
     constexpr int KK = HD / 32;
     const PoolLayout &L = a.L;
-    const int P = L.page_tokens;
     const int tk0 = 8 * (j >> 2) + (j & 3), tk1 = tk0 + 4;
     const int64_t pk0 = tk0 < 16 ? pA : pB, pk1 = tk1 < 16 ? pA : pB;
+    const int sk0 = (tk0 < 16 ? sA : sB) + (tk0 & 15), sk1 = (tk1 < 16 ? sA : sB) + (tk1 & 15);
     // bytes of one token's K codes
     constexpr int RB = KT == KV_Q4_0 ? HD / 2 : HD;
-    const uint8_t *r0 = a.base + pk0 * L.page_bytes + koff + (int64_t)((base + tk0) % P) * RB;
-    const uint8_t *r1 = a.base + pk1 * L.page_bytes + koff + (int64_t)((base + tk1) % P) * RB;
+    const uint8_t *r0 = a.base + pk0 * L.page_bytes + koff + sk0 * RB;
+    const uint8_t *r1 = a.base + pk1 * L.page_bytes + koff + sk1 * RB;
 #pragma unroll
     for (int kk = 0; kk < KK; kk++) {
         // q4_0: dims 8g..8g+7 of a block are the low (g < 2) or high
@@ -207,21 +220,22 @@ __device__ __forceinline__ void load_kq(const DecodeArgs &a, int64_t pA, int64_t
         B.k1[kk] = ldq<NT, u2>(r1 + off);
     }
     const int64_t pv = g < 2 ? pA : pB;
-    const uint8_t *ksr = a.base + pv * L.page_bytes + ksoff + (int64_t)((base + 8 * g) % P) * KK * 2;
+    const int sv = (g < 2 ? sA : sB) + 8 * (g & 1);
+    const uint8_t *ksr = a.base + pv * L.page_bytes + ksoff + sv * KK * 2;
 #pragma unroll
     for (int x = 0; x < KK; x++)
         B.ks[x] = ldq<NT, u4>(ksr + 16 * x);
 }
 
 template <int KT, int HD, bool NT>
-__device__ __forceinline__ void load_vq(const DecodeArgs &a, int64_t pA, int64_t pB, int base, int64_t voff,
+__device__ __forceinline__ void load_vq(const DecodeArgs &a, int64_t pA, int64_t pB, int sA, int sB, int64_t voff,
                                         int64_t vsoff, int j, int g, QBlock<KT, HD> &B)
 {
     constexpr int KK = HD / 32;
     const PoolLayout &L = a.L;
     const int P = L.page_tokens;
     const int64_t pv = g < 2 ? pA : pB;
-    const int sv = (base + 8 * g) % P;
+    const int sv = (g < 2 ? sA : sB) + 8 * (g & 1);
     const uint8_t *pg = a.base + pv * L.page_bytes;
     if (KT == KV_Q4_0) {
 #pragma unroll
@@ -576,79 +590,85 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
     const int32_t *bt = a.block_tables + (int64_t)b * a.max_blocks;
     const int stride = 32 * 4;
 
-    int base = t0 + 32 * w;
+    // Block starts are wave-uniform (scalar registers), so the loop test is a
+    // scalar branch.  Every block but the last runs inside the loop, where
+    // the next block's loads are issued unconditionally (K once this block's
+    // scores exist, V once its P*V has consumed the V registers): the wait
+    // counters then see one pattern of loads in flight on every path, and a
+    // wait for this block's V never waits for the next block's K.
+    int base = __builtin_amdgcn_readfirstlane(t0 + 32 * w);
     if constexpr (QUANT) {
         const int64_t ksoff = L.ks_off + (int64_t)kvh * P * KK * 2;
         const int64_t vsoff = L.vs_off + (int64_t)kvh * KK * P * 2;
         if (base < t1) {
             QBlock<KT, HD> B;
             int64_t pA, pB;
+            int sA, sB;
             bool ok;
-            block_pages(a, bt, base, t1, j, g, pA, pB, ok);
-            load_kq<KT, HD, NT>(a, pA, pB, base, koff, ksoff, j, g, B);
-            load_vq<KT, HD, NT>(a, pA, pB, base, voff, vsoff, j, g, B);
+            block_pages(a, bt, base, t1, pA, pB, sA, sB, ok);
+            load_kq<KT, HD, NT>(a, pA, pB, sA, sB, koff, ksoff, j, g, B);
+            load_vq<KT, HD, NT>(a, pA, pB, sA, sB, voff, vsoff, j, g, B);
+            f4 s0, s1;
             for (;;) {
-                f4 s0, s1;
                 qk_q<KT, HD, GP>(B, qh, g, s0, s1);
                 const int next = base + stride;
-                const bool more = next < t1;
-                int64_t nA = pA, nB = pB;
-                bool nok = ok;
-                if (PREFETCH && more) {
-                    block_pages(a, bt, next, t1, j, g, nA, nB, nok);
-                    load_kq<KT, HD, NT>(a, nA, nB, next, koff, ksoff, j, g, B);
-                }
-                softmax_pv_q<KT, HD, GP>(s0, s1, B, base, ok, t1, j, g, c, S, vnorm);
-                if (!more)
+                if (next >= t1)
                     break;
-                if (PREFETCH) {
-                    load_vq<KT, HD, NT>(a, nA, nB, next, voff, vsoff, j, g, B);
-                } else {
-                    block_pages(a, bt, next, t1, j, g, nA, nB, nok);
-                    load_kq<KT, HD, NT>(a, nA, nB, next, koff, ksoff, j, g, B);
-                    load_vq<KT, HD, NT>(a, nA, nB, next, voff, vsoff, j, g, B);
-                }
+                int64_t nA, nB;
+                int nsA, nsB;
+                bool nok;
+                block_pages(a, bt, next, t1, nA, nB, nsA, nsB, nok);
+                if (PREFETCH)
+                    load_kq<KT, HD, NT>(a, nA, nB, nsA, nsB, koff, ksoff, j, g, B);
+                softmax_pv_q<KT, HD, GP>(s0, s1, B, base, ok, t1, j, g, c, S, vnorm);
+                if (!PREFETCH)
+                    load_kq<KT, HD, NT>(a, nA, nB, nsA, nsB, koff, ksoff, j, g, B);
+                // keep the V loads below this block's P*V: hoisted above it
+                // they would need a second set of V registers
+                __builtin_amdgcn_sched_barrier(0);
+                load_vq<KT, HD, NT>(a, nA, nB, nsA, nsB, voff, vsoff, j, g, B);
                 pA = nA;
                 pB = nB;
+                sA = nsA;
+                sB = nsB;
                 ok = nok;
                 base = next;
             }
+            softmax_pv_q<KT, HD, GP>(s0, s1, B, base, ok, t1, j, g, c, S, vnorm);
         }
     } else if (base < t1) {
         h8 k0[KK], k1[KK], v[NB];
         int64_t pA, pB;
+        int sA, sB;
         bool ok;
-        block_pages(a, bt, base, t1, j, g, pA, pB, ok);
-        load_k<HD, NT>(a, pA, pB, base, koff, j, g, k0, k1);
-        load_v<HD, NT>(a, pA, pB, base, voff, j, g, v);
+        block_pages(a, bt, base, t1, pA, pB, sA, sB, ok);
+        load_k<HD, NT>(a, pA, pB, sA, sB, koff, j, g, k0, k1);
+        load_v<HD, NT>(a, pA, pB, sA, sB, voff, j, g, v);
+        f4 s0, s1;
         for (;;) {
-            f4 s0, s1;
             qk<HD, GP>(k0, k1, qh, ql, s0, s1);
             const int next = base + stride;
-            const bool more = next < t1;
-            int64_t nA = pA, nB = pB;
-            bool nok = ok;
-            if (PREFETCH && more) {
-                // K registers are free once the scores exist: start the next
-                // block's K loads before the softmax and P*V of this one.
-                block_pages(a, bt, next, t1, j, g, nA, nB, nok);
-                load_k<HD, NT>(a, nA, nB, next, koff, j, g, k0, k1);
-            }
-            softmax_pv<HD, GP>(s0, s1, v, base, ok, t1, j, g, c, S);
-            if (!more)
+            if (next >= t1)
                 break;
-            if (PREFETCH) {
-                load_v<HD, NT>(a, nA, nB, next, voff, j, g, v);
-            } else {
-                block_pages(a, bt, next, t1, j, g, nA, nB, nok);
-                load_k<HD, NT>(a, nA, nB, next, koff, j, g, k0, k1);
-                load_v<HD, NT>(a, nA, nB, next, voff, j, g, v);
-            }
+            int64_t nA, nB;
+            int nsA, nsB;
+            bool nok;
+            block_pages(a, bt, next, t1, nA, nB, nsA, nsB, nok);
+            if (PREFETCH)
+                load_k<HD, NT>(a, nA, nB, nsA, nsB, koff, j, g, k0, k1);
+            softmax_pv<HD, GP>(s0, s1, v, base, ok, t1, j, g, c, S);
+            if (!PREFETCH)
+                load_k<HD, NT>(a, nA, nB, nsA, nsB, koff, j, g, k0, k1);
+            __builtin_amdgcn_sched_barrier(0);
+            load_v<HD, NT>(a, nA, nB, nsA, nsB, voff, j, g, v);
             pA = nA;
             pB = nB;
+            sA = nsA;
+            sB = nsB;
             ok = nok;
             base = next;
         }
+        softmax_pv<HD, GP>(s0, s1, v, base, ok, t1, j, g, c, S);
     }
 
     // wave totals -> LDS
