@@ -50,6 +50,12 @@ using mfma_ops::i8x8_to_h8;
 using mfma_ops::u4x8_to_h8;
 typedef uint16_t us2 __attribute__((ext_vector_type(2)));
 
+// Quantised pages through per-wave LDS staging (1) or straight into
+// registers (0).
+#ifndef GI_MFMA_DECODE_QSTAGE
+#define GI_MFMA_DECODE_QSTAGE 1
+#endif
+
 namespace mfma_decode {
 
 constexpr float kLog2e = 1.4426950408889634f;
@@ -249,6 +255,106 @@ __device__ __forceinline__ void load_vq(const DecodeArgs &a, int64_t pA, int64_t
 #pragma unroll
     for (int db = 0; db < KK; db++)
         B.vs[db] = ldq<NT, u4>(pg + vsoff + ((int64_t)db * P + sv) * 2);
+}
+
+// One wave's staging area for a block of a quantised page, filled by direct
+// global->LDS loads (16 bytes per lane for codes, 4 for scales) and read back
+// into the QBlock operand registers.  Reading pages through LDS lets every
+// global load fetch long contiguous runs -- the K operand otherwise makes each
+// quarter-wave touch 16 token rows per load -- and the next block's loads
+// need no registers, so they are issued a whole block ahead.
+//   k:  16-byte slot ((kk*2 + t)*16 + j)*NS + (gp ^ x(j)) holds token row
+//       tk_t(j) bytes kk*CB + 16*gp .. + 16 (CB = bytes of 32 codes, NS =
+//       CB / 16, x(j) = (j >> 3) & 1 when NS == 2, else 0: the swizzle keeps
+//       the 8-byte operand reads of j and j + 8 on different banks);
+//   v:  slot (r*16 + j)*2 + (h ^ x(j)) holds the 16 tokens of half h of code
+//       row 16r + j (q8_0: dimension 16r + j; q4_0: the byte row of
+//       dimensions 32r + j and 32r + 16 + j);
+//   ks: [half][16 tokens][KK halves], 128 bytes per half;
+//   vs: [half][db][16 tokens], 32 bytes per block row, 128 per half.
+template <int KT, int HD>
+struct QStage {
+    static constexpr int KK = HD / 32;
+    static constexpr int RB = KT == KV_Q4_0 ? HD / 2 : HD; // bytes of one token's codes
+    static constexpr int CB = RB / KK, NS = CB / 16;
+    static constexpr int CODE_BYTES = 32 * RB;              // of K (and of V) per block
+    static constexpr int NLOAD = CODE_BYTES / 1024;         // 16-byte loads of 64 lanes
+    uint8_t k[CODE_BYTES];
+    uint8_t v[CODE_BYTES];
+    uint8_t ks[256];
+    uint8_t vs[256];
+};
+
+typedef __attribute__((address_space(3))) void *lds_ptr;
+
+template <int KT, int HD>
+__device__ __forceinline__ void issue_q(const DecodeArgs &a, int64_t pA, int64_t pB, int sA, int sB,
+                                        int64_t koff, int64_t ksoff, int64_t voff, int64_t vsoff, int lane,
+                                        QStage<KT, HD> &S)
+{
+    typedef QStage<KT, HD> Q;
+    constexpr int KK = Q::KK, RB = Q::RB, CB = Q::CB, NS = Q::NS;
+    const PoolLayout &L = a.L;
+    const int P = L.page_tokens;
+    const uint8_t *gA = a.base + pA * L.page_bytes, *gB = a.base + pB * L.page_bytes;
+#pragma unroll
+    for (int q = 0; q < Q::NLOAD; q++) {
+        const int sl = 64 * q + lane;
+        const int jj = (sl / NS) & 15, kt = sl / (NS * 16);
+        const int gp = NS == 2 ? (sl & 1) ^ ((jj >> 3) & 1) : 0;
+        const int kk = kt >> 1, tk = 8 * (jj >> 2) + (jj & 3) + 4 * (kt & 1);
+        const uint8_t *src = (tk < 16 ? gA + (int64_t)(sA + tk) * RB : gB + (int64_t)(sB + tk - 16) * RB) +
+                             koff + kk * CB + 16 * gp;
+        __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.k[1024 * q], 16, 0, 0);
+    }
+#pragma unroll
+    for (int q = 0; q < Q::NLOAD; q++) {
+        const int sl = 64 * q + lane;
+        const int jj = (sl >> 1) & 15, r = sl >> 5;
+        const int h = (sl & 1) ^ ((jj >> 3) & 1);
+        const uint8_t *src = (h ? gB + sB : gA + sA) + voff + (int64_t)(16 * r + jj) * P;
+        __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.v[1024 * q], 16, 0, 0);
+    }
+    {
+        // 16 tokens x KK halves = 8*KK words per half; spare lanes repeat
+        const int h = lane >> 5, wd = min(lane & 31, 8 * KK - 1);
+        const uint8_t *src = (h ? gB + (int64_t)sB * KK * 2 : gA + (int64_t)sA * KK * 2) + ksoff + 4 * wd;
+        __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.ks[0], 4, 0, 0);
+    }
+    {
+        const int h = lane >> 5, db = min((lane >> 3) & 3, KK - 1), wd = lane & 7;
+        const uint8_t *src = (h ? gB : gA) + vsoff + ((int64_t)db * P + (h ? sB : sA)) * 2 + 4 * wd;
+        __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.vs[0], 4, 0, 0);
+    }
+}
+
+template <int KT, int HD>
+__device__ __forceinline__ void read_q(const QStage<KT, HD> &S, int j, int g, QBlock<KT, HD> &B)
+{
+    typedef QStage<KT, HD> Q;
+    constexpr int KK = Q::KK, CB = Q::CB, NS = Q::NS;
+    const int x = (j >> 3) & 1;
+#pragma unroll
+    for (int kk = 0; kk < KK; kk++)
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const int row = (kk * 2 + t) * 16 + j;
+            const int off = NS == 2 ? (row * 2 + ((g >> 1) ^ x)) * 16 + 8 * (g & 1) : row * CB + 8 * (g & 1);
+            const u2 c = *reinterpret_cast<const u2 *>(&S.k[off]);
+            if (t)
+                B.k1[kk] = c;
+            else
+                B.k0[kk] = c;
+        }
+#pragma unroll
+    for (int r = 0; r < (KT == KV_Q4_0 ? KK : 2 * KK); r++)
+        B.v[r] = *reinterpret_cast<const u2 *>(&S.v[((r * 16 + j) * 2 + ((g >> 1) ^ x)) * 16 + 8 * (g & 1)]);
+#pragma unroll
+    for (int i = 0; i < KK; i++)
+        B.ks[i] = *reinterpret_cast<const u4 *>(&S.ks[128 * (g >> 1) + 16 * KK * (g & 1) + 16 * i]);
+#pragma unroll
+    for (int db = 0; db < KK; db++)
+        B.vs[db] = *reinterpret_cast<const u4 *>(&S.vs[128 * (g >> 1) + 32 * db + 16 * (g & 1)]);
 }
 
 // Scores of one block from quantised K: per k-step a fresh product of the
@@ -600,7 +706,44 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
     if constexpr (QUANT) {
         const int64_t ksoff = L.ks_off + (int64_t)kvh * P * KK * 2;
         const int64_t vsoff = L.vs_off + (int64_t)kvh * KK * P * 2;
-        if (base < t1) {
+        if (GI_MFMA_DECODE_QSTAGE && base < t1) {
+            __shared__ __align__(16) QStage<KT, HD> s_q[4];
+            QStage<KT, HD> &Sq = s_q[w];
+            int64_t pA, pB;
+            int sA, sB;
+            bool ok;
+            block_pages(a, bt, base, t1, pA, pB, sA, sB, ok);
+            issue_q<KT, HD>(a, pA, pB, sA, sB, koff, ksoff, voff, vsoff, lane, Sq);
+            for (;;) {
+                QBlock<KT, HD> B;
+                // the only vector loads in flight are this block's
+                __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0)
+                read_q<KT, HD>(Sq, j, g, B);
+                const int next = base + stride;
+                const bool more = next < t1;
+                int64_t nA = pA, nB = pB;
+                int nsA = sA, nsB = sB;
+                bool nok = ok;
+                if (more) {
+                    block_pages(a, bt, next, t1, nA, nB, nsA, nsB, nok);
+                    // every read of this block has returned before its
+                    // slots are refilled
+                    __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0)
+                    issue_q<KT, HD>(a, nA, nB, nsA, nsB, koff, ksoff, voff, vsoff, lane, Sq);
+                }
+                f4 s0, s1;
+                qk_q<KT, HD, GP>(B, qh, g, s0, s1);
+                softmax_pv_q<KT, HD, GP>(s0, s1, B, base, ok, t1, j, g, c, S, vnorm);
+                if (!more)
+                    break;
+                pA = nA;
+                pB = nB;
+                sA = nsA;
+                sB = nsB;
+                ok = nok;
+                base = next;
+            }
+        } else if (base < t1) {
             QBlock<KT, HD> B;
             int64_t pA, pB;
             int sA, sB;
