@@ -33,6 +33,8 @@
 // rescaled exactly when it grows).  w is
 // split into hi + lo halves like p, the lo rows carrying a further 2^11 so
 // they keep full precision; both factors are taken out in the final merge.
+// Quantised blocks reach the registers through a per-wave LDS staging area
+// filled by direct global->LDS loads.
 #include "gi_common.h"
 #include "gi_kernels.h"
 #include "mfma_ops.h"
@@ -50,10 +52,10 @@ using mfma_ops::i8x8_to_h8;
 using mfma_ops::u4x8_to_h8;
 typedef uint16_t us2 __attribute__((ext_vector_type(2)));
 
-// Quantised pages through per-wave LDS staging (1) or straight into
-// registers (0).
-#ifndef GI_MFMA_DECODE_QSTAGE
-#define GI_MFMA_DECODE_QSTAGE 1
+// Cache policy of the direct global->LDS loads (2: non-temporal, which
+// measured slower for q8_0 pages and within noise for q4_0).
+#ifndef GI_DECODE_LDS_AUX
+#define GI_DECODE_LDS_AUX 0
 #endif
 
 namespace mfma_decode {
@@ -167,14 +169,6 @@ __device__ __forceinline__ float mirror(float x)
                                                                0xF, 0xF, false));
 }
 
-template <bool NT, typename T>
-__device__ __forceinline__ T ldq(const uint8_t *p)
-{
-    if (NT)
-        return __builtin_nontemporal_load(reinterpret_cast<const T *>(p));
-    return *reinterpret_cast<const T *>(p);
-}
-
 // Half i of a run of uint32 words, widened to float by the hardware
 // conversion: exact for every finite half, subnormals included, since these
 // kernels run with fp16 denormals preserved (the default float mode, which
@@ -203,59 +197,6 @@ struct QBlock {
     u2 v[KT == KV_Q4_0 ? KK : 2 * KK];
     u4 vs[KK];
 };
-
-template <int KT, int HD, bool NT>
-__device__ __forceinline__ void load_kq(const DecodeArgs &a, int64_t pA, int64_t pB, int sA, int sB, int64_t koff,
-                                        int64_t ksoff, int j, int g, QBlock<KT, HD> &B)
-{
-    constexpr int KK = HD / 32;
-    const PoolLayout &L = a.L;
-    const int tk0 = 8 * (j >> 2) + (j & 3), tk1 = tk0 + 4;
-    const int64_t pk0 = tk0 < 16 ? pA : pB, pk1 = tk1 < 16 ? pA : pB;
-    const int sk0 = (tk0 < 16 ? sA : sB) + (tk0 & 15), sk1 = (tk1 < 16 ? sA : sB) + (tk1 & 15);
-    // bytes of one token's K codes
-    constexpr int RB = KT == KV_Q4_0 ? HD / 2 : HD;
-    const uint8_t *r0 = a.base + pk0 * L.page_bytes + koff + sk0 * RB;
-    const uint8_t *r1 = a.base + pk1 * L.page_bytes + koff + sk1 * RB;
-#pragma unroll
-    for (int kk = 0; kk < KK; kk++) {
-        // q4_0: dims 8g..8g+7 of a block are the low (g < 2) or high
-        // (g >= 2) nibbles of bytes 8*(g%2) .. + 7 of its 16
-        const int off = KT == KV_Q4_0 ? 16 * kk + 8 * (g & 1) : 32 * kk + 8 * g;
-        B.k0[kk] = ldq<NT, u2>(r0 + off);
-        B.k1[kk] = ldq<NT, u2>(r1 + off);
-    }
-    const int64_t pv = g < 2 ? pA : pB;
-    const int sv = (g < 2 ? sA : sB) + 8 * (g & 1);
-    const uint8_t *ksr = a.base + pv * L.page_bytes + ksoff + sv * KK * 2;
-#pragma unroll
-    for (int x = 0; x < KK; x++)
-        B.ks[x] = ldq<NT, u4>(ksr + 16 * x);
-}
-
-template <int KT, int HD, bool NT>
-__device__ __forceinline__ void load_vq(const DecodeArgs &a, int64_t pA, int64_t pB, int sA, int sB, int64_t voff,
-                                        int64_t vsoff, int j, int g, QBlock<KT, HD> &B)
-{
-    constexpr int KK = HD / 32;
-    const PoolLayout &L = a.L;
-    const int P = L.page_tokens;
-    const int64_t pv = g < 2 ? pA : pB;
-    const int sv = (g < 2 ? sA : sB) + 8 * (g & 1);
-    const uint8_t *pg = a.base + pv * L.page_bytes;
-    if (KT == KV_Q4_0) {
-#pragma unroll
-        for (int db = 0; db < KK; db++)
-            B.v[db] = ldq<NT, u2>(pg + voff + (int64_t)(16 * db + j) * P + sv);
-    } else {
-#pragma unroll
-        for (int nb = 0; nb < 2 * KK; nb++)
-            B.v[nb] = ldq<NT, u2>(pg + voff + (int64_t)(16 * nb + j) * P + sv);
-    }
-#pragma unroll
-    for (int db = 0; db < KK; db++)
-        B.vs[db] = ldq<NT, u4>(pg + vsoff + ((int64_t)db * P + sv) * 2);
-}
 
 // One wave's staging area for a block of a quantised page, filled by direct
 // global->LDS loads (16 bytes per lane for codes, 4 for scales) and read back
@@ -305,7 +246,7 @@ __device__ __forceinline__ void issue_q(const DecodeArgs &a, int64_t pA, int64_t
         const int kk = kt >> 1, tk = 8 * (jj >> 2) + (jj & 3) + 4 * (kt & 1);
         const uint8_t *src = (tk < 16 ? gA + (int64_t)(sA + tk) * RB : gB + (int64_t)(sB + tk - 16) * RB) +
                              koff + kk * CB + 16 * gp;
-        __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.k[1024 * q], 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.k[1024 * q], 16, 0, GI_DECODE_LDS_AUX);
     }
 #pragma unroll
     for (int q = 0; q < Q::NLOAD; q++) {
@@ -313,18 +254,18 @@ __device__ __forceinline__ void issue_q(const DecodeArgs &a, int64_t pA, int64_t
         const int jj = (sl >> 1) & 15, r = sl >> 5;
         const int h = (sl & 1) ^ ((jj >> 3) & 1);
         const uint8_t *src = (h ? gB + sB : gA + sA) + voff + (int64_t)(16 * r + jj) * P;
-        __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.v[1024 * q], 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.v[1024 * q], 16, 0, GI_DECODE_LDS_AUX);
     }
     {
         // 16 tokens x KK halves = 8*KK words per half; spare lanes repeat
         const int h = lane >> 5, wd = min(lane & 31, 8 * KK - 1);
         const uint8_t *src = (h ? gB + (int64_t)sB * KK * 2 : gA + (int64_t)sA * KK * 2) + ksoff + 4 * wd;
-        __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.ks[0], 4, 0, 0);
+        __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.ks[0], 4, 0, GI_DECODE_LDS_AUX);
     }
     {
         const int h = lane >> 5, db = min((lane >> 3) & 3, KK - 1), wd = lane & 7;
         const uint8_t *src = (h ? gB : gA) + vsoff + ((int64_t)db * P + (h ? sB : sA)) * 2 + 4 * wd;
-        __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.vs[0], 4, 0, 0);
+        __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.vs[0], 4, 0, GI_DECODE_LDS_AUX);
     }
 }
 
@@ -555,7 +496,9 @@ __device__ __forceinline__ void softmax_pv_q(f4 s0, f4 s1, QBlock<KT, HD> &B, in
         bits = (bits & 0xFF800000u) + 0x800000u;
     const float pw = __builtin_bit_cast(float, bits);
     const bool grow = pw > vnorm; // uniform across the wave
-    const float f = grow ? vnorm / pw : 1.0f;
+    // vnorm and pw are 0 or powers of two in [2^-24, 2^16]: their quotient
+    // and reciprocal are exact exponent arithmetic
+    const float f = grow ? vnorm * __builtin_bit_cast(float, 0x7F000000u - bits) : 1.0f;
     if (grow)
         vnorm = pw;
     if (__any(alpha != 1.0f) || grow) {
@@ -567,29 +510,32 @@ __device__ __forceinline__ void softmax_pv_q(f4 s0, f4 s1, QBlock<KT, HD> &B, in
                 S.o[nb][r] *= ar;
         }
     }
-    const float inv = vnorm > 0.0f ? 1.0f / vnorm : 0.0f; // a power of two
+    const bool lo_row = j >= GP;
+    // lo rows carry 2^11 from the start: x = 2^11 w there, and its lo half is
+    // x minus x cut to 11 significant bits (the value its hi half
+    // round-toward-zero converts to), exact in float32
+    const float inv = vnorm > 0.0f ? __builtin_bit_cast(float, 0x7F000000u - __builtin_bit_cast(uint32_t, vnorm)) *
+                                         (lo_row ? 2048.0f : 1.0f)
+                                   : 0.0f;
+    const uint32_t cut = lo_row ? 0xFFFFE000u : 0u;
     float pp[8];
 #pragma unroll
     for (int i = 0; i < 8; i++)
         pp[i] = p[i] * inv;
-    const bool lo_row = j >= GP;
 #pragma unroll
     for (int db = 0; db < KK; db++) {
         const h8 vh = __builtin_bit_cast(h8, B.vs[db]);
         uint32_t pk[4];
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            // x = p / vnorm * vscale, the scale read as a half by the
-            // mixed-precision multiply-add (exact widening)
+            // x = p / vnorm * vscale (times 2^11 on lo rows), the scale read
+            // as a half by the mixed-precision multiply-add (exact widening)
             const float x0 = fmaf(pp[2 * k], (float)vh[2 * k], 0.0f);
             const float x1 = fmaf(pp[2 * k + 1], (float)vh[2 * k + 1], 0.0f);
-            // hi by one packed round-toward-zero conversion, so lo is
-            // computed against the very value the product reads
-            const h2 hi = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(x0, x1));
-            const float l0 = fmaf((float)hi[0], -2048.0f, x0 * 2048.0f);
-            const float l1 = fmaf((float)hi[1], -2048.0f, x1 * 2048.0f);
-            const uint32_t lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(l0, l1));
-            pk[k] = lo_row ? lo : __builtin_bit_cast(uint32_t, hi);
+            // hi rows: x itself; lo rows: x - trunc11(x)
+            const float y0 = x0 - __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, x0) & cut);
+            const float y1 = x1 - __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, x1) & cut);
+            pk[k] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(y0, y1));
         }
         const h8 pw8 = __builtin_bit_cast(h8, u4{pk[0], pk[1], pk[2], pk[3]});
 #pragma unroll
@@ -624,7 +570,14 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
     const int t1 = min(len, t0 + a.split_tokens);
     const int64_t qrow = (int64_t)b * H + h0;
 
-    __shared__ float s_o[4][16][HD];
+    // The per-wave staging areas of the block loop (quantised pages) and,
+    // after it, the cross-wave merge share one LDS allocation.  (fp16 pages
+    // load straight into registers: staging them through LDS measured
+    // slower.)
+    constexpr int STAGE_BYTES = QUANT ? 4 * (int)sizeof(QStage<KT == KV_F16 ? KV_Q8_0 : KT, HD>) : 0;
+    constexpr int MERGE_BYTES = 4 * 16 * HD * (int)sizeof(float);
+    __shared__ __align__(16) uint8_t s_stage[STAGE_BYTES > MERGE_BYTES ? STAGE_BYTES : MERGE_BYTES];
+    float(*s_o)[16][HD] = reinterpret_cast<float(*)[16][HD]>(s_stage);
     __shared__ float s_m[4][16], s_l[4][16];
 
     float *wsp = nullptr;
@@ -706,9 +659,8 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
     if constexpr (QUANT) {
         const int64_t ksoff = L.ks_off + (int64_t)kvh * P * KK * 2;
         const int64_t vsoff = L.vs_off + (int64_t)kvh * KK * P * 2;
-        if (GI_MFMA_DECODE_QSTAGE && base < t1) {
-            __shared__ __align__(16) QStage<KT, HD> s_q[4];
-            QStage<KT, HD> &Sq = s_q[w];
+        if (base < t1) {
+            QStage<KT, HD> &Sq = reinterpret_cast<QStage<KT, HD> *>(s_stage)[w];
             int64_t pA, pB;
             int sA, sB;
             bool ok;
@@ -743,41 +695,6 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
                 ok = nok;
                 base = next;
             }
-        } else if (base < t1) {
-            QBlock<KT, HD> B;
-            int64_t pA, pB;
-            int sA, sB;
-            bool ok;
-            block_pages(a, bt, base, t1, pA, pB, sA, sB, ok);
-            load_kq<KT, HD, NT>(a, pA, pB, sA, sB, koff, ksoff, j, g, B);
-            load_vq<KT, HD, NT>(a, pA, pB, sA, sB, voff, vsoff, j, g, B);
-            f4 s0, s1;
-            for (;;) {
-                qk_q<KT, HD, GP>(B, qh, g, s0, s1);
-                const int next = base + stride;
-                if (next >= t1)
-                    break;
-                int64_t nA, nB;
-                int nsA, nsB;
-                bool nok;
-                block_pages(a, bt, next, t1, nA, nB, nsA, nsB, nok);
-                if (PREFETCH)
-                    load_kq<KT, HD, NT>(a, nA, nB, nsA, nsB, koff, ksoff, j, g, B);
-                softmax_pv_q<KT, HD, GP>(s0, s1, B, base, ok, t1, j, g, c, S, vnorm);
-                if (!PREFETCH)
-                    load_kq<KT, HD, NT>(a, nA, nB, nsA, nsB, koff, ksoff, j, g, B);
-                // keep the V loads below this block's P*V: hoisted above it
-                // they would need a second set of V registers
-                __builtin_amdgcn_sched_barrier(0);
-                load_vq<KT, HD, NT>(a, nA, nB, nsA, nsB, voff, vsoff, j, g, B);
-                pA = nA;
-                pB = nB;
-                sA = nsA;
-                sB = nsB;
-                ok = nok;
-                base = next;
-            }
-            softmax_pv_q<KT, HD, GP>(s0, s1, B, base, ok, t1, j, g, c, S, vnorm);
         }
     } else if (base < t1) {
         h8 k0[KK], k1[KK], v[NB];
@@ -814,6 +731,8 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
         softmax_pv<HD, GP>(s0, s1, v, base, ok, t1, j, g, c, S);
     }
 
+    // every wave is done with its staging area before the merge reuses it
+    __syncthreads();
     // wave totals -> LDS
     float lt = S.lsum;
     lt += __shfl_xor(lt, 16);
