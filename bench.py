@@ -16,6 +16,7 @@ Prints one JSON line (see --help).  --config selects other shapes:
                       then causal paged attention over the context so far), all
                       32 layers; reports TFLOP/s of the attention
   llama8b_f16_prefill the same prefill over fp16 pages
+  llama8b_q4_prefill  the same prefill over Q4_0 pages
   llama8b_b256_8k_rope the headline step with RoPE fused into the append: per
                       layer, q and k turned at position 8191 (theta 5e5) while
                       k/v are stored, then the same paged attention
@@ -99,6 +100,10 @@ CONFIGS = {
                                         "paged attention", layers=32, q_heads=32, kv_heads=8,
                                head_dim=128, page_tokens=16, batch=4, context="4096", chunk=512,
                                frag=True, prefill=True, kv_dtype="q8_0"),
+    "llama8b_q4_prefill": dict(workload="llama3-8b-shape q4_0 chunked prefill: append + causal "
+                                        "paged attention", layers=32, q_heads=32, kv_heads=8,
+                               head_dim=128, page_tokens=16, batch=4, context="4096", chunk=512,
+                               frag=True, prefill=True, kv_dtype="q4_0"),
     "llama8b_fork_b256": dict(workload="llama3-8b-shape copy-on-write fork: 256 sequences forked "
                                         "mid-page, one append each (one page copy per fork, all "
                                         "layers, whatever the context length)",
@@ -271,7 +276,7 @@ def cpu_baseline(oracle, cfg, budget_s=12.0):
 
 def cpu_baseline_prefill(oracle, cfg, budget_s=10.0):
     """The oracle's chunked-prefill attention (forward.go:547-577, over
-    f32 K/V: q8_0 pages dequantised first, a pass over the context that is
+    f32 K/V: quantised pages dequantised first, a pass over the context that is
     under 0.1 % of the work and left out) on one host core for a bounded
     sample: 16 queries at the end of the last chunk (context 4096), repeated
     until about budget_s of CPU work.  Reported as TFLOP/s of the same
@@ -412,7 +417,7 @@ def run_prefill(args, gi, torch, dev, cfg):
     mgr, pages, bt = build_tables(gi, cfg, lens, args.seed)
     stream = torch.cuda.Stream(dev)
     torch.cuda.set_stream(stream)
-    kv_type = gi.KV_Q8_0 if cfg["kv_dtype"] == "q8_0" else gi.KV_F16
+    kv_type = kv_type_of(gi, cfg["kv_dtype"])
     pool = gi.PagedKVCache(layers, kvh, hd, P, pages, kv_type, stream=stream)
     pool.set_decode_kernel(args.decode_kernel)
     bt_d = torch.from_numpy(bt).to(dev)

@@ -20,6 +20,7 @@
 // scale of each 32 dimensions into P for the products of those dimensions.
 #include "gi_common.h"
 #include "gi_kernels.h"
+#include "mfma_ops.h"
 
 #include <math.h>
 #include <type_traits>
@@ -28,10 +29,13 @@ namespace gi {
 
 namespace mfma_prefill {
 
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-typedef float f4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+using mfma_ops::f4;
+using mfma_ops::h2;
+using mfma_ops::h8;
+using mfma_ops::i8x8_to_h8;
+using mfma_ops::u2;
+using mfma_ops::u4;
+using mfma_ops::u4x8_to_h8;
 
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -43,26 +47,6 @@ __device__ __forceinline__ f4 mfma(h8 a, h8 b, f4 c)
 __device__ __forceinline__ h8 ld16(const uint8_t *p)
 {
     return __builtin_nontemporal_load(reinterpret_cast<const h8 *>(p));
-}
-
-// Eight int8 values -> eight exact fp16 values.  (x ^ 0x80) is x + 128 as an
-// unsigned byte; 0x64 in the high byte makes the half 1024 + (x + 128);
-// subtracting 1152 leaves x.
-__device__ __forceinline__ h8 i8x8_to_h8(uint2 w)
-{
-    const uint32_t x0 = w.x ^ 0x80808080u, x1 = w.y ^ 0x80808080u;
-    const uint32_t c = 0x64646464u;
-    uint32_t u[4] = {__builtin_amdgcn_perm(c, x0, 0x04010400u), __builtin_amdgcn_perm(c, x0, 0x04030402u),
-                     __builtin_amdgcn_perm(c, x1, 0x04010400u), __builtin_amdgcn_perm(c, x1, 0x04030402u)};
-    const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
-    h8 r;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        h2 t = __builtin_bit_cast(h2, u[i]) - bias;
-        r[2 * i] = t[0];
-        r[2 * i + 1] = t[1];
-    }
-    return r;
 }
 
 __device__ __forceinline__ void split_hilo(float x, _Float16 &hi, _Float16 &lo)
@@ -215,8 +199,8 @@ __global__ __launch_bounds__(256) void attn_prefill(PrefillArgs a)
                 k0[kk] = ld16(g0 + koff + ((int64_t)s0 * HD + 32 * kk + 8 * g) * 2);
                 k1[kk] = ld16(g1 + koff + ((int64_t)s1 * HD + 32 * kk + 8 * g) * 2);
             } else {
-                k0[kk] = i8x8_to_h8(*reinterpret_cast<const uint2 *>(g0 + koff + (int64_t)s0 * HD + 32 * kk + 8 * g));
-                k1[kk] = i8x8_to_h8(*reinterpret_cast<const uint2 *>(g1 + koff + (int64_t)s1 * HD + 32 * kk + 8 * g));
+                k0[kk] = i8x8_to_h8(*reinterpret_cast<const u2 *>(g0 + koff + (int64_t)s0 * HD + 32 * kk + 8 * g));
+                k1[kk] = i8x8_to_h8(*reinterpret_cast<const u2 *>(g1 + koff + (int64_t)s1 * HD + 32 * kk + 8 * g));
             }
         }
         if (KT == KV_Q8_0) {
@@ -238,7 +222,7 @@ __global__ __launch_bounds__(256) void attn_prefill(PrefillArgs a)
             if (KT == KV_F16)
                 vv[nb] = ld16(gv + voff + ((int64_t)(16 * nb + j) * P + sv) * 2);
             else
-                vv[nb] = i8x8_to_h8(*reinterpret_cast<const uint2 *>(gv + voff + (int64_t)(16 * nb + j) * P + sv));
+                vv[nb] = i8x8_to_h8(*reinterpret_cast<const u2 *>(gv + voff + (int64_t)(16 * nb + j) * P + sv));
         }
         if (KT == KV_Q8_0) {
             const uint16_t *vs = reinterpret_cast<const uint16_t *>(gv + vsoff);
@@ -445,37 +429,46 @@ constexpr float kPExp = 6.0f, kLazy = 8.0f;
 template <int HD, int KT>
 struct StageRegs {
     // 16-byte chunks per thread and block: fp16 K rows / V columns of 8
-    // elements, or int8 K rows / V columns of 16 elements.
-    static constexpr int NC = KT == KV_F16 ? HD / 32 : HD / 64;
+    // elements, int8 K rows / V columns of 16 elements, or q4_0 K rows of 32
+    // nibbles (one quantisation block) / V byte rows of 16 tokens (two
+    // dimensions each).
+    static constexpr bool QUANT = KT != KV_F16;
+    static constexpr int NC = KT == KV_F16 ? HD / 32 : KT == KV_Q8_0 ? HD / 64 : HD / 128;
+    static_assert(NC >= 1, "q4_0 staging needs head_dim 128");
     u4 k[NC], v[NC];
-    int64_t kpage[KT == KV_Q8_0 ? NC : 1]; // q8_0: page of each chunk (wave-uniform)
-    int64_t vpage[KT == KV_Q8_0 ? NC : 1];
+    int64_t kpage[QUANT ? NC : 1]; // quantised pages: page of each chunk (wave-uniform)
+    int64_t vpage[QUANT ? NC : 1];
 };
 
-// q8_0 K and V are stored dequantised as exact hi + lo fp16 pairs.
+// Quantised K and V are stored dequantised as exact hi + lo fp16 pairs.
 template <int HD, int KT, int NBUF>
 struct Lds {
-    static constexpr bool Q8 = KT == KV_Q8_0;
+    static constexpr bool Q8 = KT != KV_F16;
     __attribute__((aligned(16))) _Float16 k[NBUF][kTB][HD + 8];  // token-major K, rows padded
     __attribute__((aligned(16))) _Float16 v[NBUF][HD][kTB + 8];  // dimension-major V
     __attribute__((aligned(16))) _Float16 kl[Q8 ? NBUF : 1][Q8 ? kTB : 1][HD + 8]; // q8_0: K lo
     __attribute__((aligned(16))) _Float16 vl[Q8 ? NBUF : 1][Q8 ? HD : 1][kTB + 8]; // q8_0: V lo
 };
 
-// Chunk -> (token, column) of K and (page segment, dimension, token group)
-// of V inside one block.  F16: 8 elements per chunk, q8_0: 16.
+// Chunk -> (token, column) of K and (page segment, code row, token group)
+// of V inside one block.  K chunks hold EK dimensions of one token (fp16 8,
+// q8_0 16, q4_0 32); V chunks EV tokens of one code row (fp16 8, quantised
+// 16), a code row being a dimension (fp16, q8_0) or the byte row of
+// dimensions 32r' + r'' and 32r' + 16 + r'' (q4_0 row 16r' + r'').
 template <int HD, int KT, int P>
 struct ChunkMap {
-    static constexpr int E = KT == KV_F16 ? 8 : 16;  // elements per chunk
-    static constexpr int KPR = HD / E;               // K chunks per token row
-    static constexpr int VPD = P / E;                // V chunks per dimension and page
-    static constexpr int VPS = HD * VPD;             // V chunks per page segment
-    static_assert(VPS % 64 == 0 && (64 * E / HD) <= P, "a wave's chunks must share one page");
+    static constexpr int EK = KT == KV_F16 ? 8 : KT == KV_Q8_0 ? 16 : 32;
+    static constexpr int EV = KT == KV_F16 ? 8 : 16;
+    static constexpr int VROWS = KT == KV_Q4_0 ? HD / 2 : HD;
+    static constexpr int KPR = HD / EK;  // K chunks per token row
+    static constexpr int VPD = P / EV;   // V chunks per code row and page
+    static constexpr int VPS = VROWS * VPD; // V chunks per page segment
+    static_assert(VPS % 64 == 0 && (64 * EK / HD) <= P, "a wave's chunks must share one page");
     __device__ static int k_tok(int ch) { return ch / KPR; }
-    __device__ static int k_col(int ch) { return E * (ch % KPR); }
+    __device__ static int k_col(int ch) { return EK * (ch % KPR); }
     __device__ static int v_seg(int ch) { return ch / VPS; }
-    __device__ static int v_dim(int ch) { return (ch % VPS) / VPD; }
-    __device__ static int v_tok(int ch) { return E * ((ch % VPS) % VPD); } // within the page
+    __device__ static int v_dim(int ch) { return (ch % VPS) / VPD; } // the code row
+    __device__ static int v_tok(int ch) { return EV * ((ch % VPS) % VPD); } // within the page
 };
 
 // Page id of token `t` of the context (lane-wise), -1 past the cached range.
@@ -506,9 +499,15 @@ __device__ __forceinline__ void stage_load(const PrefillArgs &a, int kvh, int ti
         if (KT == KV_F16) {
             R.k[c] = *reinterpret_cast<const u4 *>(kp + (((int64_t)kvh * P + tk % P) * HD + M::k_col(ch)) * 2);
             R.v[c] = *reinterpret_cast<const u4 *>(vp + L.v_off + (((int64_t)kvh * HD + d) * P + tv) * 2);
-        } else {
+        } else if (KT == KV_Q8_0) {
             R.k[c] = *reinterpret_cast<const u4 *>(kp + ((int64_t)kvh * P + tk % P) * HD + M::k_col(ch));
             R.v[c] = *reinterpret_cast<const u4 *>(vp + L.v_off + ((int64_t)kvh * HD + d) * P + tv);
+            R.kpage[c] = page(M::k_tok(ch0));
+            R.vpage[c] = page(M::v_seg(ch0) * P);
+        } else {
+            // q4_0: K rows of HD/2 bytes, 16 per block; V byte rows of P bytes
+            R.k[c] = *reinterpret_cast<const u4 *>(kp + ((int64_t)kvh * P + tk % P) * (HD / 2) + M::k_col(ch) / 2);
+            R.v[c] = *reinterpret_cast<const u4 *>(vp + L.v_off + ((int64_t)kvh * (HD / 2) + d) * P + tv);
             R.kpage[c] = page(M::k_tok(ch0));
             R.vpage[c] = page(M::v_seg(ch0) * P);
         }
@@ -535,16 +534,16 @@ __device__ __forceinline__ void stage_store(const PrefillArgs &a, int kvh, int t
     // q8_0 block scales: one per K chunk, 16 per V chunk.  Loaded here rather
     // than with the chunk so that they hold no registers through the block's
     // compute (they are shared by many chunks and come from the caches).
-    constexpr int NCS = KT == KV_Q8_0 ? StageRegs<HD, KT>::NC : 1;
+    constexpr int NCS = KT != KV_F16 ? StageRegs<HD, KT>::NC : 1;
     u4 vs[2 * NCS];
     _Float16 ks[NCS];
-    if (KT == KV_Q8_0) {
+    if (KT != KV_F16) {
 #pragma unroll
         for (int c = 0; c < R.NC; c++) {
             const int ch = tid + 256 * c;
             const u4 *sp = reinterpret_cast<const u4 *>(
                 a.base + R.vpage[c] * a.L.page_bytes + a.L.vs_off +
-                (((int64_t)kvh * (HD / 32) + M::v_dim(ch) / 32) * P + M::v_tok(ch)) * 2);
+                (((int64_t)kvh * (HD / 32) + M::v_dim(ch) / (KT == KV_Q4_0 ? 16 : 32)) * P + M::v_tok(ch)) * 2);
             vs[2 * c] = sp[0];
             vs[2 * c + 1] = sp[1];
             ks[c] = reinterpret_cast<const _Float16 *>(a.base + R.kpage[c] * a.L.page_bytes + a.L.ks_off)
@@ -556,7 +555,7 @@ __device__ __forceinline__ void stage_store(const PrefillArgs &a, int kvh, int t
         const int ch = tid + 256 * c;
         const int tk = M::k_tok(ch), col = M::k_col(ch);
         const int d = M::v_dim(ch), t0 = M::v_seg(ch) * P + M::v_tok(ch); // block-local token
-        const uint32_t live = (uint32_t)(vmask >> t0) & ((1u << M::E) - 1u);
+        const uint32_t live = (uint32_t)(vmask >> t0) & ((1u << M::EV) - 1u);
         if (KT == KV_F16) {
             *reinterpret_cast<u4 *>(&S.k[buf][tk][col]) = R.k[c];
             u4 vv = R.v[c];
@@ -567,19 +566,54 @@ __device__ __forceinline__ void stage_store(const PrefillArgs &a, int kvh, int t
                         vv[i / 2] &= (i & 1) ? 0x0000FFFFu : 0xFFFF0000u;
             }
             *reinterpret_cast<u4 *>(&S.v[buf][d][t0]) = vv;
+        } else if (KT == KV_Q4_0) {
+            // K: the chunk is one block; low nibbles are dimensions col ..
+            // col + 15, high nibbles col + 16 .. col + 31
+            const h8 ksp = ks[c]; // splat
+#pragma unroll
+            for (int m = 0; m < 4; m++) {
+                h8 hi, lo;
+                const u2 w = u2{R.k[c][2 * (m & 1)], R.k[c][2 * (m & 1) + 1]};
+                dequant_pair(u4x8_to_h8(w, 4 * (m >> 1)), ksp, hi, lo);
+                *reinterpret_cast<h8 *>(&S.k[buf][tk][col + 8 * m]) = hi;
+                *reinterpret_cast<h8 *>(&S.kl[buf][tk][col + 8 * m]) = lo;
+            }
+            // V: byte row d = 16 db + r holds dimension 32 db + r (low
+            // nibble) and 32 db + 16 + r (high nibble) of 16 tokens
+            const int dl = 32 * (d >> 4) + (d & 15);
+#pragma unroll
+            for (int half = 0; half < 2; half++) {
+                const u2 w = u2{R.v[c][2 * half], R.v[c][2 * half + 1]};
+                const uint32_t lv = live >> (8 * half);
+#pragma unroll
+                for (int nib = 0; nib < 2; nib++) {
+                    h8 hi, lo;
+                    dequant_pair(u4x8_to_h8(w, 4 * nib), __builtin_bit_cast(h8, vs[2 * c + half]), hi, lo);
+                    if ((lv & 0xFFu) != 0xFFu) {
+#pragma unroll
+                        for (int i = 0; i < 8; i++)
+                            if (!((lv >> i) & 1u)) {
+                                hi[i] = (_Float16)0.0f;
+                                lo[i] = (_Float16)0.0f;
+                            }
+                    }
+                    *reinterpret_cast<h8 *>(&S.v[buf][dl + 16 * nib][t0 + 8 * half]) = hi;
+                    *reinterpret_cast<h8 *>(&S.vl[buf][dl + 16 * nib][t0 + 8 * half]) = lo;
+                }
+            }
         } else {
             const h8 ksp = ks[c]; // splat
 #pragma unroll
             for (int half = 0; half < 2; half++) {
                 h8 hi, lo;
-                dequant_pair(i8x8_to_h8(uint2{R.k[c][2 * half], R.k[c][2 * half + 1]}), ksp, hi, lo);
+                dequant_pair(i8x8_to_h8(u2{R.k[c][2 * half], R.k[c][2 * half + 1]}), ksp, hi, lo);
                 *reinterpret_cast<h8 *>(&S.k[buf][tk][col + 8 * half]) = hi;
                 *reinterpret_cast<h8 *>(&S.kl[buf][tk][col + 8 * half]) = lo;
             }
 #pragma unroll
             for (int half = 0; half < 2; half++) {
                 h8 hi, lo;
-                dequant_pair(i8x8_to_h8(uint2{R.v[c][2 * half], R.v[c][2 * half + 1]}),
+                dequant_pair(i8x8_to_h8(u2{R.v[c][2 * half], R.v[c][2 * half + 1]}),
                              __builtin_bit_cast(h8, vs[2 * c + half]), hi, lo);
                 const uint32_t lv = live >> (8 * half);
                 if ((lv & 0xFFu) != 0xFFu) {
@@ -804,7 +838,7 @@ struct WaveAttn {
     {
         // ---- scores: tiles (h, t), row j = token 32h + 8(j/4) + j%4 + 4t ----
         const uint8_t *kp = k_lane(S, buf, j, g, false);
-        const uint8_t *klp = KT == KV_Q8_0 ? k_lane(S, buf, j, g, true) : kp;
+        const uint8_t *klp = KT != KV_F16 ? k_lane(S, buf, j, g, true) : kp;
         f4 s[NCG][2][2];
 #pragma unroll
         for (int h = 0; h < 2; h++)
@@ -818,13 +852,13 @@ struct WaveAttn {
                     const int off = k_const(&S, h, t, kk);
                     const h8 ka = ld_frag(kp, off);
                     h8 kl;
-                    if (KT == KV_Q8_0)
+                    if (KT != KV_F16)
                         kl = ld_frag(klp, off);
 #pragma unroll
                     for (int cg = 0; cg < NCG; cg++) {
                         s[cg][h][t] = mfma(ka, qh[cg][kk], s[cg][h][t]);
                         s[cg][h][t] = mfma(ka, ql[cg][kk], s[cg][h][t]);
-                        if (KT == KV_Q8_0)
+                        if (KT != KV_F16)
                             s[cg][h][t] = mfma(kl, qh[cg][kk], s[cg][h][t]);
                     }
                 }
@@ -854,18 +888,18 @@ struct WaveAttn {
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             const uint8_t *vp = v_lane(S, buf, h, j, g, false);
-            const uint8_t *vlp = KT == KV_Q8_0 ? v_lane(S, buf, h, j, g, true) : vp;
+            const uint8_t *vlp = KT != KV_F16 ? v_lane(S, buf, h, j, g, true) : vp;
 #pragma unroll
             for (int nb = 0; nb < NB; nb++) {
                 const h8 vb = ld_frag(vp, v_const(&S, nb));
                 h8 vl;
-                if (KT == KV_Q8_0)
+                if (KT != KV_F16)
                     vl = ld_frag(vlp, v_const(&S, nb));
 #pragma unroll
                 for (int cg = 0; cg < NCG; cg++) {
                     o[cg][nb] = mfma(ph[h][cg], vb, o[cg][nb]);
                     o[cg][nb] = mfma(pl[h][cg], vb, o[cg][nb]);
-                    if (KT == KV_Q8_0)
+                    if (KT != KV_F16)
                         o[cg][nb] = mfma(ph[h][cg], vl, o[cg][nb]);
                 }
             }
@@ -1122,7 +1156,11 @@ __global__ __launch_bounds__(256) void attn_prefill_dlds(PrefillArgs a)
 
 bool mfma_prefill_supported(const PoolLayout &L, int num_heads)
 {
-    if (L.kv_type != KV_F16 && L.kv_type != KV_Q8_0)
+    // q4_0: the staged kernel, head_dim 128, pages of 16/32/64 tokens
+    if (L.kv_type == KV_Q4_0 &&
+        (L.head_dim != 128 || (L.page_tokens != 16 && L.page_tokens != 32 && L.page_tokens != 64)))
+        return false;
+    if (L.kv_type != KV_F16 && L.kv_type != KV_Q8_0 && L.kv_type != KV_Q4_0)
         return false;
     if (L.page_tokens % 16 != 0 || (L.head_dim != 64 && L.head_dim != 128))
         return false;
@@ -1159,7 +1197,7 @@ constexpr int prefill_lds_ncg()
 #ifdef GI_PREFILL_NCG
     return GI_PREFILL_NCG;
 #else
-    return (HD == 64 || P == 16 || (KT == KV_Q8_0 && P == 32)) ? 2 : 1;
+    return (HD == 64 || P == 16 || (KT != KV_F16 && P == 32)) ? 2 : 1;
 #endif
 }
 
@@ -1225,6 +1263,8 @@ hipError_t launch_prefill_mfma(const PrefillArgs &a, hipStream_t st)
         if (a.L.head_dim == 128) {
             if (a.L.kv_type == KV_F16)
                 launch_lds<128, KV_F16>(a, st);
+            else if (a.L.kv_type == KV_Q4_0)
+                launch_lds<128, KV_Q4_0>(a, st);
             else
                 launch_lds<128, KV_Q8_0>(a, st);
         } else {

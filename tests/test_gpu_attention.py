@@ -183,6 +183,39 @@ def test_decode_stale_nan_beyond_length_is_ignored(gi, oracle, dev, kv_type):
         assert rel_err_rows(o[0], want, H, hd).max() <= 1e-3
 
 
+@pytest.mark.parametrize("kv_type", [1, 2, 3], ids=["f16", "q8_0", "q4_0"])
+def test_prefill_stale_nan_beyond_context_is_ignored(gi, oracle, dev, kv_type):
+    """Prefill of 12 queries at start 16 reads 28 tokens; slots 28..39 hold
+    NaN (fp16) or 1e30 (quantised: Inf block scales), inside the last read
+    page and beyond it.  Both kernels must ignore them (forward.go:547-577
+    never reads past start + i)."""
+    import torch
+    H, kvh, hd, P = 32, 8, 128, 16
+    pop = Populated(gi, dev, kv_type, 1, kvh, hd, P, [40], seed=17)
+    t = pop.table(0)
+    ids = torch.from_numpy(np.repeat(t, P)[28:40].copy()).to(dev)
+    slots = torch.from_numpy((np.arange(28, 40) % P).astype(np.int32)).to(dev)
+    bad = float("nan") if kv_type == 1 else 1e30
+    poison = torch.full((12, kvh * hd), bad, device=dev)
+    pop.pool.Write(0, ids, slots, poison, poison)
+    bt = pop.block_tables()
+    sp = torch.tensor([16], dtype=torch.int32, device=dev)
+    qd, q = seeded((1, 12, H * hd), 18, dev)
+    scale = oracle.attn_scale(hd)
+    ks, vs = pop.stored(0, 0)
+    kw, vw = oracle.widen(kv_type, kvh * hd, ks[:28]), oracle.widen(kv_type, kvh * hd, vs[:28])
+    want = oracle.attention_prefill(q[0], kw, vw, H, kvh, hd, 16, 12, 1 << 30, scale)
+    for kern in (0, 1):
+        pop.pool.set_decode_kernel(kern)
+        out = torch.full_like(qd, float("nan"))
+        pop.pool.AttentionGQABatch(out, qd, 0, bt, sp, H, scale, 12)
+        pop.pool.synchronize()
+        o = out.cpu().numpy()[0]
+        assert np.isfinite(o).all(), kern
+        assert rel_err_rows(o, want, H, hd).max() <= 1e-3, kern
+    pop.pool.set_decode_kernel(-1)
+
+
 def prefill_case(gi, oracle, dev, kv_type, H, kvh, hd, P, starts, chunk, seed):
     import torch
     lens = [s + chunk for s in starts]
@@ -198,9 +231,10 @@ def prefill_case(gi, oracle, dev, kv_type, H, kvh, hd, P, starts, chunk, seed):
         kw = oracle.widen(kv_type, pop.kv_dim, ks)
         vw = oracle.widen(kv_type, pop.kv_dim, vs)
         wants.append(oracle.attention_prefill(q[i], kw, vw, H, kvh, hd, s, chunk, 1 << 30, scale))
-    # both attention kernels: vector ALU (0) and, for fp16 / q8_0 pages, the
-    # matrix-core prefill (1)
-    kinds = [0, 1] if kv_type in (1, 2) else [0]
+    # both attention kernels: vector ALU (0) and, for fp16 / q8_0 / q4_0
+    # pages, the matrix-core prefill (1; q4_0 with head_dim 128 only, other
+    # shapes fall back to the vector kernel)
+    kinds = [0, 1] if kv_type in (1, 2, 3) else [0]
     worst = {}
     for kern in kinds:
         pop.pool.set_decode_kernel(kern)
@@ -221,13 +255,20 @@ def test_prefill_chunk(gi, oracle, dev, kv_type):
     prefill_case(gi, oracle, dev, kv_type, 32, 8, 128, 16, [0, 100, 509], 64, seed=60 + kv_type)
 
 
-@pytest.mark.parametrize("kv_type", [1, 2], ids=["f16", "q8_0"])
+@pytest.mark.parametrize("kv_type", [1, 2, 3], ids=["f16", "q8_0", "q4_0"])
 @pytest.mark.parametrize("H,kvh,hd,P", [(8, 8, 64, 16), (16, 8, 64, 32), (64, 8, 128, 32),
-                                        (32, 2, 128, 16)])
+                                        (32, 2, 128, 16), (16, 4, 128, 64)])
 def test_prefill_shapes(gi, oracle, dev, kv_type, H, kvh, hd, P):
-    """Group sizes 1, 2, 8, 16 and head_dim 64 on the matrix-core prefill;
-    ragged chunk (37 queries) and start positions off the page grid."""
+    """Group sizes 1, 2, 4, 8, 16, head_dim 64 and pages of 16/32/64 tokens on
+    the matrix-core prefill; ragged chunk (37 queries) and start positions
+    off the page grid."""
     prefill_case(gi, oracle, dev, kv_type, H, kvh, hd, P, [3, 45], 37, seed=80 + kv_type)
+
+
+def test_prefill_q4_llama8b_chunks(gi, oracle, dev):
+    """Q4_0 KV, Llama-3-8B shape, 256-token chunks: the last chunk of a
+    768-token prefill, batch 2, inputs with 1 % outliers."""
+    prefill_case(gi, oracle, dev, 3, 32, 8, 128, 16, [512, 256], 256, seed=75)
 
 
 def test_prefill_q8_llama8b_chunks(gi, oracle, dev):
