@@ -25,6 +25,8 @@ Prints one JSON line (see --help).  --config selects other shapes:
   llama8b_b256_8k_q4  the headline step over Q4_0 pages (blocks of 32 4-bit
                       values + fp16 scale, kvcache.go's KVTypeQ4_0): append
                       with on-the-fly quantisation + paged attention
+  llama8b_b64_8k_f32  the headline shape over f32 pages (kvcache.go's KVTypeF32)
+                      at batch 64, so that the pool fits one GPU
   llama8b_b256_8k_driver the headline step driven by the continuous-batching
                       decoder (gi_batch): Step() reserves one token per sequence
                       and updates the device tables in place, then per layer
@@ -75,6 +77,10 @@ CONFIGS = {
                                         "paged attention", layers=32, q_heads=32, kv_heads=8,
                                head_dim=128, page_tokens=16, batch=256, context="8192",
                                frag=True, kv_dtype="q8_0"),
+    "llama8b_b64_8k_f32": dict(workload="llama3-8b-shape decode step over f32 pages: append + "
+                                        "paged attention", layers=32, q_heads=32, kv_heads=8,
+                               head_dim=128, page_tokens=16, batch=64, context="8192",
+                               frag=True, kv_dtype="f32"),
     "llama8b_b256_8k_driver": dict(workload="llama3-8b-shape decode step through the batch driver: "
                                             "token reservation + RoPE + append + paged attention",
                                    layers=32, q_heads=32, kv_heads=8, head_dim=128, page_tokens=16,

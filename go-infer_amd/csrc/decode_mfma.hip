@@ -298,6 +298,230 @@ __device__ __forceinline__ void read_q(const QStage<KT, HD> &S, int j, int g, QB
         B.vs[db] = *reinterpret_cast<const u4 *>(&S.vs[128 * (g >> 1) + 32 * db + 16 * (g & 1)]);
 }
 
+// One wave's staging area for a block of an f32 page, filled by 16-byte
+// direct global->LDS loads.  With x(j) = (j >> 1) & 7:
+//   k: slot ((kk*2 + t)*16 + j)*8 + (c ^ x(j)) holds token row tk_t(j),
+//      dimensions 32*kk + 4*c .. + 3;
+//   v: slot (nb*16 + j)*8 + (c ^ x(j)) holds dimension 16*nb + j, block
+//      tokens 4*c .. 4*c + 3.
+// A quarter-wave of a load fetches two whole 128-byte K rows (V: two
+// dimensions' 64-byte runs of both pages), and the swizzle spreads the
+// 16-byte operand reads of 16 lanes over all banks.
+template <int HD>
+struct F32Stage {
+    static constexpr int BYTES = 32 * HD * 4, NLOAD = BYTES / 1024;
+    uint8_t k[BYTES];
+    uint8_t v[BYTES];
+};
+
+template <int HD>
+__device__ __forceinline__ void issue_f32(const DecodeArgs &a, int64_t pA, int64_t pB, int sA, int sB,
+                                          int64_t koff, int64_t voff, int lane, F32Stage<HD> &S)
+{
+    const PoolLayout &L = a.L;
+    const int P = L.page_tokens;
+    const uint8_t *gA = a.base + pA * L.page_bytes, *gB = a.base + pB * L.page_bytes;
+#pragma unroll
+    for (int q = 0; q < F32Stage<HD>::NLOAD; q++) {
+        const int sl = 64 * q + lane;
+        const int kt = sl >> 7, jj = (sl >> 3) & 15, c = (sl & 7) ^ ((jj >> 1) & 7);
+        const int kk = kt >> 1, tk = 8 * (jj >> 2) + (jj & 3) + 4 * (kt & 1);
+        const uint8_t *src = (tk < 16 ? gA + (int64_t)(sA + tk) * HD * 4 : gB + (int64_t)(sB + tk - 16) * HD * 4) +
+                             koff + (32 * kk + 4 * c) * 4;
+        __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.k[1024 * q], 16, 0, GI_DECODE_LDS_AUX);
+    }
+#pragma unroll
+    for (int q = 0; q < F32Stage<HD>::NLOAD; q++) {
+        const int sl = 64 * q + lane;
+        const int nb = sl >> 7, jj = (sl >> 3) & 15, c = (sl & 7) ^ ((jj >> 1) & 7);
+        const uint8_t *src = (c < 4 ? gA + (int64_t)(sA + 4 * c) * 4 : gB + (int64_t)(sB + 4 * c - 16) * 4) + voff +
+                             (int64_t)(16 * nb + jj) * P * 4;
+        __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.v[1024 * q], 16, 0, GI_DECODE_LDS_AUX);
+    }
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+
+// Maximum of a non-negative value over the wave, wave-uniform: DPP within
+// each 16-lane row, then the four row results (non-negative floats order
+// like their bit patterns).
+__device__ __forceinline__ float wave_max_nonneg(float x)
+{
+    x = fmaxf(x, dpp_f<0xB1>(x));  // quad_perm [1,0,3,2]
+    x = fmaxf(x, dpp_f<0x4E>(x));  // quad_perm [2,3,0,1]
+    x = fmaxf(x, dpp_f<0x141>(x)); // row_half_mirror
+    x = fmaxf(x, dpp_f<0x140>(x)); // row_mirror
+    const uint32_t b = __builtin_bit_cast(uint32_t, x);
+    const uint32_t m = max(max(__builtin_amdgcn_readlane(b, 0), __builtin_amdgcn_readlane(b, 16)),
+                           max(__builtin_amdgcn_readlane(b, 32), __builtin_amdgcn_readlane(b, 48)));
+    return __builtin_bit_cast(float, m);
+}
+
+// Power-of-two operand scale of one block with largest magnitude m: the
+// running scale `run` is kept while m*run lies in [2^-2, 2^15) (fp16 hi
+// halves below 65504, lo halves normal down to 2^-22 of the maximum);
+// otherwise the scale puts m in [2^14, 2^15).  The first block (run == 0)
+// keeps 1 when it may, so that ordinary data needs no multiply.
+__device__ __forceinline__ float block_scale(float m, float run)
+{
+    const float r = run == 0.0f ? 1.0f : run;
+    const float ms = m * r;
+    if (m == 0.0f || (ms >= 0.25f && ms < 32768.0f))
+        return r;
+    int k = 14 - ((int)((__builtin_bit_cast(uint32_t, m) >> 23) & 0xFF) - 127);
+    k = min(max(k, -126), 127);
+    return __builtin_bit_cast(float, (uint32_t)(k + 127) << 23);
+}
+
+// 1 / x for a power of two x in [2^-126, 2^126]: exact exponent arithmetic.
+__device__ __forceinline__ float pow2_recip(float x)
+{
+    return __builtin_bit_cast(float, 0x7F000000u - __builtin_bit_cast(uint32_t, x));
+}
+
+// x (already scaled into fp16 range) as hi + lo halves: hi = x cut to 11
+// significant bits (what the round-toward-zero conversion gives), lo the
+// exact remainder rounded to nearest, so hi + lo is x to 2^-23 relative.
+__device__ __forceinline__ void split_pair(float x0, float x1, uint32_t &hi, uint32_t &lo)
+{
+    const float t0 = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, x0) & 0xFFFFE000u);
+    const float t1 = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, x1) & 0xFFFFE000u);
+    hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x0, x1));
+    const h2 l = {(_Float16)(x0 - t0), (_Float16)(x1 - t1)};
+    lo = __builtin_bit_cast(uint32_t, l);
+}
+
+// Reads one f32 block from the staging area and turns it into hi/lo fp16
+// operands.  Tokens past t1 (or the whole block on a rejected page) are
+// zeroed first, so that stale slots take no part in the scales.  K is scaled
+// by ksc and V by vsc (running powers of two, updated here); when vsc changes
+// the accumulators are rescaled to the new one.
+template <int HD>
+__device__ __forceinline__ void read_f32(const F32Stage<HD> &Sf, int j, int g, int base, bool ok, int t1,
+                                         h8 *kh0, h8 *kh1, h8 *kl0, h8 *kl1, h8 *vh, h8 *vl, float &ksc,
+                                         float &vsc, State<HD> &S)
+{
+    constexpr int KK = HD / 32, NB = HD / 16;
+    const int x = (j >> 1) & 7;
+    float kf[2][KK][8], vf[NB][8];
+#pragma unroll
+    for (int kk = 0; kk < KK; kk++)
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const float4 w = *reinterpret_cast<const float4 *>(
+                    &Sf.k[((((kk * 2 + t) * 16 + j) * 8) + ((2 * g + h) ^ x)) * 16]);
+                kf[t][kk][4 * h] = w.x;
+                kf[t][kk][4 * h + 1] = w.y;
+                kf[t][kk][4 * h + 2] = w.z;
+                kf[t][kk][4 * h + 3] = w.w;
+            }
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const float4 w =
+                *reinterpret_cast<const float4 *>(&Sf.v[(((nb * 16 + j) * 8) + ((2 * g + h) ^ x)) * 16]);
+            vf[nb][4 * h] = w.x;
+            vf[nb][4 * h + 1] = w.y;
+            vf[nb][4 * h + 2] = w.z;
+            vf[nb][4 * h + 3] = w.w;
+        }
+    if (base + 32 > t1 || !ok) {
+        const int tk0 = 8 * (j >> 2) + (j & 3);
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const bool live = ok && base + tk0 + 4 * t < t1;
+#pragma unroll
+            for (int kk = 0; kk < KK; kk++)
+#pragma unroll
+                for (int i = 0; i < 8; i++)
+                    kf[t][kk][i] = live ? kf[t][kk][i] : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const bool live = ok && base + 8 * g + i < t1;
+#pragma unroll
+            for (int nb = 0; nb < NB; nb++)
+                vf[nb][i] = live ? vf[nb][i] : 0.0f;
+        }
+    }
+    float mk = 0.0f, mv = 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < KK; kk++)
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            mk = fmaxf(mk, fmaxf(fabsf(kf[0][kk][i]), fabsf(kf[1][kk][i])));
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++)
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            mv = fmaxf(mv, fabsf(vf[nb][i]));
+    mk = wave_max_nonneg(mk);
+    mv = wave_max_nonneg(mv);
+    ksc = block_scale(mk, ksc);
+    const float vnew = block_scale(mv, vsc);
+    if (vsc != 0.0f && vnew != vsc) {
+        const float f = vnew * pow2_recip(vsc);
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++)
+            S.o[nb] *= f;
+    }
+    vsc = vnew;
+    if (ksc != 1.0f) {
+#pragma unroll
+        for (int kk = 0; kk < KK; kk++)
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                kf[0][kk][i] *= ksc;
+                kf[1][kk][i] *= ksc;
+            }
+    }
+    if (vsc != 1.0f) {
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++)
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                vf[nb][i] *= vsc;
+    }
+#pragma unroll
+    for (int kk = 0; kk < KK; kk++) {
+        u4 h0, l0, h1, l1;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            uint32_t a0, b0, a1, b1;
+            split_pair(kf[0][kk][2 * k], kf[0][kk][2 * k + 1], a0, b0);
+            split_pair(kf[1][kk][2 * k], kf[1][kk][2 * k + 1], a1, b1);
+            h0[k] = a0;
+            l0[k] = b0;
+            h1[k] = a1;
+            l1[k] = b1;
+        }
+        kh0[kk] = __builtin_bit_cast(h8, h0);
+        kl0[kk] = __builtin_bit_cast(h8, l0);
+        kh1[kk] = __builtin_bit_cast(h8, h1);
+        kl1[kk] = __builtin_bit_cast(h8, l1);
+    }
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++) {
+        u4 hh, ll;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            uint32_t a0, b0;
+            split_pair(vf[nb][2 * k], vf[nb][2 * k + 1], a0, b0);
+            hh[k] = a0;
+            ll[k] = b0;
+        }
+        vh[nb] = __builtin_bit_cast(h8, hh);
+        vl[nb] = __builtin_bit_cast(h8, ll);
+    }
+}
+
 // Scores of one block from quantised K: per k-step a fresh product of the
 // codes, scaled by the K block scale of its row's token, then the packed
 // hi/lo columns are completed with the lane mirror.
@@ -357,9 +581,9 @@ __device__ __forceinline__ void qk(const h8 *k0, const h8 *k1, const h8 *qh, con
 // j < G carries p_hi of head j and row 2G-1-j p_lo of head j (the lane of
 // that column already holds the head's full score), one product; the two
 // output rows of a head are added in the final merge.
-template <int HD, int GP>
+template <int HD, int GP, bool VLO = false>
 __device__ __forceinline__ void softmax_pv(f4 s0, f4 s1, h8 *v, int base, bool ok, int t1, int j,
-                                           int g, float c, State<HD> &S)
+                                           int g, float c, State<HD> &S, h8 *vl = nullptr)
 {
     constexpr int NB = HD / 16;
     float sc[8];
@@ -377,8 +601,11 @@ __device__ __forceinline__ void softmax_pv(f4 s0, f4 s1, h8 *v, int base, bool o
             if (!(base + 8 * g + i < t1 && ok)) {
                 sc[i] = -INFINITY;
 #pragma unroll
-                for (int nb = 0; nb < NB; nb++)
+                for (int nb = 0; nb < NB; nb++) {
                     v[nb][i] = (_Float16)0.0f;
+                    if (VLO)
+                        vl[nb][i] = (_Float16)0.0f;
+                }
             }
         }
     }
@@ -427,6 +654,8 @@ __device__ __forceinline__ void softmax_pv(f4 s0, f4 s1, h8 *v, int base, bool o
         S.o[nb] = mfma(ph, v[nb], S.o[nb]);
         if (GP == 0)
             S.o[nb] = mfma(pl, v[nb], S.o[nb]);
+        if (VLO)
+            S.o[nb] = mfma(ph, vl[nb], S.o[nb]);
     }
 }
 
@@ -552,8 +781,9 @@ template <int KT, int HD, int GP, bool NT, bool PREFETCH>
 __device__ __forceinline__ void decode_body(const DecodeArgs &a)
 {
     constexpr int KK = HD / 32, NB = HD / 16;
-    constexpr bool QUANT = KT != KV_F16;
-    static_assert(!QUANT || GP != 0, "quantised pages use the packed hi/lo form");
+    constexpr bool QUANT = KT == KV_Q8_0 || KT == KV_Q4_0;
+    constexpr bool F32 = KT == KV_F32;
+    static_assert(!(QUANT || F32) || GP != 0, "quantised and f32 pages use the packed hi/lo form");
     const PoolLayout &L = a.L;
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -574,7 +804,8 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
     // after it, the cross-wave merge share one LDS allocation.  (fp16 pages
     // load straight into registers: staging them through LDS measured
     // slower.)
-    constexpr int STAGE_BYTES = QUANT ? 4 * (int)sizeof(QStage<KT == KV_F16 ? KV_Q8_0 : KT, HD>) : 0;
+    constexpr int STAGE_BYTES = QUANT ? 4 * (int)sizeof(QStage<QUANT ? KT : KV_Q8_0, HD>)
+                                : F32 ? 4 * (int)sizeof(F32Stage<HD>) : 0;
     constexpr int MERGE_BYTES = 4 * 16 * HD * (int)sizeof(float);
     __shared__ __align__(16) uint8_t s_stage[STAGE_BYTES > MERGE_BYTES ? STAGE_BYTES : MERGE_BYTES];
     float(*s_o)[16][HD] = reinterpret_cast<float(*)[16][HD]>(s_stage);
@@ -640,10 +871,11 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
 #pragma unroll
     for (int nb = 0; nb < NB; nb++)
         S.o[nb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    float ksc = 0.0f, vsc = 0.0f; // f32 pages: running K / V operand scales
     float vnorm = 0.0f; // quantised pages: running power-of-two cap of the V scales
 
     // bytes per stored element: fp16 2, q8_0 1, q4_0 1/2
-    constexpr int EB_NUM = KT == KV_F16 ? 2 : 1, EB_DEN = KT == KV_Q4_0 ? 2 : 1;
+    constexpr int EB_NUM = F32 ? 4 : KT == KV_F16 ? 2 : 1, EB_DEN = KT == KV_Q4_0 ? 2 : 1;
     const int64_t koff = L.k_off + (int64_t)kvh * P * HD * EB_NUM / EB_DEN;
     const int64_t voff = L.v_off + (int64_t)kvh * HD * P * EB_NUM / EB_DEN;
     const int32_t *bt = a.block_tables + (int64_t)b * a.max_blocks;
@@ -686,6 +918,54 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
                 f4 s0, s1;
                 qk_q<KT, HD, GP>(B, qh, g, s0, s1);
                 softmax_pv_q<KT, HD, GP>(s0, s1, B, base, ok, t1, j, g, c, S, vnorm);
+                if (!more)
+                    break;
+                pA = nA;
+                pB = nB;
+                sA = nsA;
+                sB = nsB;
+                ok = nok;
+                base = next;
+            }
+        }
+    } else if constexpr (F32) {
+        if (base < t1) {
+            F32Stage<HD> &Sf = reinterpret_cast<F32Stage<HD> *>(s_stage)[w];
+            int64_t pA, pB;
+            int sA, sB;
+            bool ok;
+            block_pages(a, bt, base, t1, pA, pB, sA, sB, ok);
+            issue_f32<HD>(a, pA, pB, sA, sB, koff, voff, lane, Sf);
+            for (;;) {
+                h8 kh0[KK], kh1[KK], kl0[KK], kl1[KK], vh[NB], vl[NB];
+                // the only vector loads in flight are this block's
+                __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0)
+                read_f32<HD>(Sf, j, g, base, ok, t1, kh0, kh1, kl0, kl1, vh, vl, ksc, vsc, S);
+                const int next = base + stride;
+                const bool more = next < t1;
+                int64_t nA = pA, nB = pB;
+                int nsA = sA, nsB = sB;
+                bool nok = ok;
+                if (more) {
+                    block_pages(a, bt, next, t1, nA, nB, nsA, nsB, nok);
+                    __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0): this block's reads returned
+                    issue_f32<HD>(a, nA, nB, nsA, nsB, koff, voff, lane, Sf);
+                }
+                // S = (kh + kl) . (q_hi | q_lo): two products per k-step
+                f4 s0 = f4{0.0f, 0.0f, 0.0f, 0.0f}, s1 = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int kk = 0; kk < KK; kk++) {
+                    s0 = mfma(kh0[kk], qh[kk], s0);
+                    s1 = mfma(kh1[kk], qh[kk], s1);
+                    s0 = mfma(kl0[kk], qh[kk], s0);
+                    s1 = mfma(kl1[kk], qh[kk], s1);
+                }
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    s0[r] += mirror<GP>(s0[r]);
+                    s1[r] += mirror<GP>(s1[r]);
+                }
+                softmax_pv<HD, GP, true>(s0, s1, vh, base, ok, t1, j, g, c * pow2_recip(ksc), S, vl);
                 if (!more)
                     break;
                 pA = nA;
@@ -752,6 +1032,11 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
                 const int row = 4 * g + r;
                 o *= vnorm * (row >= G && row < 2 * G ? 1.0f / 2048.0f : 1.0f);
             }
+            if constexpr (F32) {
+                // the accumulators hold O times the wave's V scale
+                if (vsc != 0.0f)
+                    o *= pow2_recip(vsc);
+            }
             s_o[w][4 * g + r][16 * nb + j] = o;
         }
     __syncthreads();
@@ -796,6 +1081,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
     decode_body<KV_F16, HD, GP, NT, PREFETCH>(a);
 }
 
+// f32 pages, packed form (GP = G in {1, 2, 4, 8}).
+template <int HD, int GP, bool NT, bool PREFETCH, int OCC>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void attn_mfma_f32(DecodeArgs a)
+{
+    decode_body<KV_F32, HD, GP, NT, PREFETCH>(a);
+}
+
 // q8_0 / q4_0 pages, packed form (GP = G in {1, 2, 4, 8}).
 template <int KT, int HD, int GP, bool NT, bool PREFETCH, int OCC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void attn_mfma_q(DecodeArgs a)
@@ -816,7 +1108,7 @@ bool mfma_decode_supported(const PoolLayout &L, int num_heads)
     const int G = num_heads / L.num_kv_heads;
     if (L.kv_type == KV_F16)
         return G >= 1 && G <= 16;
-    if (L.kv_type == KV_Q8_0 || L.kv_type == KV_Q4_0)
+    if (L.kv_type == KV_Q8_0 || L.kv_type == KV_Q4_0 || L.kv_type == KV_F32)
         return G == 1 || G == 2 || G == 4 || G == 8;
     return false;
 }
@@ -859,6 +1151,22 @@ static void launch_mfma_q(const DecodeArgs &a, dim3 grid, hipStream_t st)
 }
 
 template <int HD>
+static void launch_mfma_f32(const DecodeArgs &a, dim3 grid, hipStream_t st)
+{
+#define GI_F(GPv)                                                                                 \
+    hipLaunchKernelGGL((mfma_decode::attn_mfma_f32<HD, GPv, GI_MFMA_DECODE_NT, GI_MFMA_DECODE_PREFETCH, \
+                                                   GI_MFMA_DECODE_OCC>),                         \
+                       grid, dim3(256), 0, st, a)
+    switch (a.num_heads / a.L.num_kv_heads) {
+    case 1: GI_F(1); break;
+    case 2: GI_F(2); break;
+    case 4: GI_F(4); break;
+    default: GI_F(8); break;
+    }
+#undef GI_F
+}
+
+template <int HD>
 static void launch_mfma_g(const DecodeArgs &a, dim3 grid, hipStream_t st)
 {
     switch (a.num_heads / a.L.num_kv_heads) {
@@ -886,6 +1194,12 @@ hipError_t launch_decode_mfma(const DecodeArgs &a, hipStream_t st)
             launch_mfma_q<KV_Q4_0, 128>(a, grid, st);
         else
             launch_mfma_q<KV_Q4_0, 64>(a, grid, st);
+        break;
+    case KV_F32:
+        if (h128)
+            launch_mfma_f32<128>(a, grid, st);
+        else
+            launch_mfma_f32<64>(a, grid, st);
         break;
     default:
         if (h128)

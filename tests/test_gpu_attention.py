@@ -31,8 +31,9 @@ def oracle_decode(oracle, pop, layer, q, H, lens, scale):
 
 def kernels_for(pool, H):
     """Every decode kernel that can serve this pool: the vector-ALU one
-    always, the matrix-core one where supported (fp16, q8_0 and q4_0 pages
-    of 16-token multiples; quantised pages with groups of 1, 2, 4 or 8)."""
+    always, the matrix-core one where supported (pages of 16-token
+    multiples, head_dim 64 or 128; f32 and quantised pages with groups of 1,
+    2, 4 or 8)."""
     pool.set_decode_kernel(1)
     ks = [0, 1] if pool.decode_kernel(H) == 1 else [0]
     pool.set_decode_kernel(-1)
@@ -150,7 +151,7 @@ def test_decode_empty_and_short(gi, oracle, dev):
         assert rel_err_rows(o[2], want[2], 32, 128).max() <= 1e-3
 
 
-@pytest.mark.parametrize("kv_type", [1, 2, 3], ids=["f16", "q8_0", "q4_0"])
+@pytest.mark.parametrize("kv_type", [0, 1, 2, 3], ids=["f32", "f16", "q8_0", "q4_0"])
 def test_decode_stale_nan_beyond_length_is_ignored(gi, oracle, dev, kv_type):
     """Slots past a sequence's length may hold anything (a freed page's old
     contents): NaN there (for quantised pages, values of 1e30 whose fp16
@@ -163,7 +164,7 @@ def test_decode_stale_nan_beyond_length_is_ignored(gi, oracle, dev, kv_type):
     t = pop.table(0)
     ids = torch.from_numpy(np.repeat(t, P)[20:40].copy()).to(dev)
     slots = torch.from_numpy((np.arange(20, 40) % P).astype(np.int32)).to(dev)
-    bad = float("nan") if kv_type == 1 else 1e30
+    bad = float("nan") if kv_type in (0, 1) else 1e30
     nan = torch.full((20, kvh * hd), bad, device=dev)
     pop.pool.Write(0, ids, slots, nan, nan)
     bt = pop.block_tables()
@@ -214,6 +215,56 @@ def test_prefill_stale_nan_beyond_context_is_ignored(gi, oracle, dev, kv_type):
         assert np.isfinite(o).all(), kern
         assert rel_err_rows(o, want, H, hd).max() <= 1e-3, kern
     pop.pool.set_decode_kernel(-1)
+
+
+@pytest.mark.parametrize("H,kvh,hd", [(32, 8, 128), (32, 4, 64), (8, 8, 128)])
+def test_decode_f32_wide_range(gi, oracle, dev, H, kvh, hd):
+    """f32 pages whose magnitude changes by up to 10^10 from one 32-token
+    block to the next (K from 1e-4 to 1e3, V from 1e-5 to 1e5, beyond fp16's
+    range both ways): the matrix-core kernel's per-block power-of-two operand
+    scales must keep the 1e-5 bound of the f32 path."""
+    import torch
+    P, lens = 16, [300, 77, 33]
+    kv_dim = kvh * hd
+    pages = sum((n + P - 1) // P for n in lens) + 2
+    mgr = gi.PagedKVManager(1, kv_dim, pages, P)
+    mgr.SetFreeList(np.random.default_rng(5).permutation(pages).astype(np.int32))
+    pool = gi.PagedKVCache(1, kvh, hd, P, pages, gi.KV_F32)
+    kf = np.array([1e-4, 1.0, 30.0, 1e-2, 1e3, 0.5, 3e-3], np.float32)
+    vf = np.array([1.0, 1e5, 1e-5, 3e3, 1e-3, 7.0, 2e4], np.float32)
+    ks, vs, tabs = [], [], []
+    for i, n in enumerate(lens):
+        sid = mgr.AllocateSequence()
+        ids, slots = mgr.AppendTokens(sid, n)
+        blk = (np.arange(n) // 32 + i) % len(kf)
+        k = (oracle.normal(300 + i, (n, kv_dim)) * kf[blk][:, None]).astype(np.float32)
+        v = (oracle.normal(400 + i, (n, kv_dim)) * vf[blk][:, None]).astype(np.float32)
+        pool.Write(0, torch.from_numpy(ids).to(dev), torch.from_numpy(slots).to(dev),
+                   torch.from_numpy(k).to(dev), torch.from_numpy(v).to(dev))
+        ks.append(k)
+        vs.append(v)
+        tabs.append(mgr.Tables[sid].BlockIDs)
+    mb = max(len(t) for t in tabs)
+    bt = torch.tensor([t + [0] * (mb - len(t)) for t in tabs], dtype=torch.int32, device=dev)
+    sl = torch.tensor(lens, dtype=torch.int32, device=dev)
+    q = (oracle.normal(500, (len(lens), H * hd)) * 0.05).astype(np.float32)
+    qd = torch.from_numpy(q).to(dev)
+    scale = oracle.attn_scale(hd)
+    kinds = kernels_for(pool, H)
+    assert kinds == [0, 1], "f32 pages should have the matrix-core kernel"
+    worst = {}
+    for kern in kinds:
+        pool.set_decode_kernel(kern)
+        out = torch.full_like(qd, float("nan"))
+        pool.AttentionGQA(out, qd, 0, bt, sl, H, scale)
+        pool.synchronize()
+        o = out.cpu().numpy()
+        for i, n in enumerate(lens):
+            want = oracle.attention_decode(q[i], ks[i], vs[i], H, kvh, hd, n, scale)
+            worst[kern] = max(worst.get(kern, 0.0), float(rel_err_rows(o[i], want, H, hd).max()))
+    pool.set_decode_kernel(-1)
+    print("f32 wide-range decode max rel err by kernel:", worst)
+    assert max(worst.values()) <= 1e-5, worst
 
 
 def prefill_case(gi, oracle, dev, kv_type, H, kvh, hd, P, starts, chunk, seed):
