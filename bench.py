@@ -1020,8 +1020,8 @@ def main():
 
     kind = pool.decode_kernel(H)
     if kind == 1:
-        kname = ("attn_mfma_f16<%d>" % hd) if kv_dtype == "f16" else \
-            ("attn_mfma_q<%d,%d>" % (kv_type_of(gi, kv_dtype), hd))
+        kname = {"f16": "attn_mfma_f16<%d>" % hd, "f32": "attn_mfma_f32<%d>" % hd}.get(
+            kv_dtype, "attn_mfma_q<%d,%d>" % (kv_type_of(gi, kv_dtype), hd))
     else:
         kname = "attn_valu<%d,%d,%d>" % (kv_type_of(gi, kv_dtype), hd, H // kvh)
     traffic = profiled_traffic(kname, args.config)
