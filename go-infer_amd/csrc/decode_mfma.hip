@@ -692,13 +692,17 @@ __device__ __forceinline__ void softmax_pv_q(f4 s0, f4 s1, QBlock<KT, HD> &B, in
     }
     // cap: the largest V scale of the block.  Scales are non-negative
     // halves, whose bit patterns order like the values.
+    // (each word is copied out before the bit cast: hipcc's __builtin_bit_cast
+    // of an ext_vector element reads element 0 whatever the index)
     uint32_t mw = 0;
 #pragma unroll
     for (int db = 0; db < KK; db++)
 #pragma unroll
-        for (int k = 0; k < 4; k++)
+        for (int k = 0; k < 4; k++) {
+            const uint32_t e = B.vs[db][k];
             mw = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(us2, mw),
-                                                                         __builtin_bit_cast(us2, B.vs[db][k])));
+                                                                         __builtin_bit_cast(us2, e)));
+        }
     uint32_t mh = max(mw & 0xFFFFu, mw >> 16);
     mh = max(mh, (uint32_t)__shfl_xor((int)mh, 16));
     mh = max(mh, (uint32_t)__shfl_xor((int)mh, 32));

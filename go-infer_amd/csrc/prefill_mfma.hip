@@ -428,19 +428,20 @@ constexpr float kPExp = 6.0f, kLazy = 8.0f;
 
 template <int HD, int KT>
 struct StageRegs {
-    // 16-byte chunks per thread and block: fp16 K rows / V columns of 8
-    // elements, int8 K rows / V columns of 16 elements, or q4_0 K rows of 32
+    // 16-byte chunks per thread and block: f32 K rows / V columns of 4
+    // elements, fp16 of 8, int8 K rows / V columns of 16 elements, or q4_0 K rows of 32
     // nibbles (one quantisation block) / V byte rows of 16 tokens (two
     // dimensions each).
-    static constexpr bool QUANT = KT != KV_F16;
-    static constexpr int NC = KT == KV_F16 ? HD / 32 : KT == KV_Q8_0 ? HD / 64 : HD / 128;
+    static constexpr bool QUANT = KT == KV_Q8_0 || KT == KV_Q4_0;
+    static constexpr int NC = KT == KV_F32 ? HD / 16 : KT == KV_F16 ? HD / 32 : KT == KV_Q8_0 ? HD / 64 : HD / 128;
     static_assert(NC >= 1, "q4_0 staging needs head_dim 128");
     u4 k[NC], v[NC];
     int64_t kpage[QUANT ? NC : 1]; // quantised pages: page of each chunk (wave-uniform)
     int64_t vpage[QUANT ? NC : 1];
 };
 
-// Quantised K and V are stored dequantised as exact hi + lo fp16 pairs.
+// Quantised and f32 K and V are stored as hi + lo fp16 pairs (exact for
+// quantised pages, 2^-23 relative for f32 ones).
 template <int HD, int KT, int NBUF>
 struct Lds {
     static constexpr bool Q8 = KT != KV_F16;
@@ -451,14 +452,14 @@ struct Lds {
 };
 
 // Chunk -> (token, column) of K and (page segment, code row, token group)
-// of V inside one block.  K chunks hold EK dimensions of one token (fp16 8,
-// q8_0 16, q4_0 32); V chunks EV tokens of one code row (fp16 8, quantised
-// 16), a code row being a dimension (fp16, q8_0) or the byte row of
+// of V inside one block.  K chunks hold EK dimensions of one token (f32 4,
+// fp16 8, q8_0 16, q4_0 32); V chunks EV tokens of one code row (f32 4,
+// fp16 8, quantised 16), a code row being a dimension (f32, fp16, q8_0) or the byte row of
 // dimensions 32r' + r'' and 32r' + 16 + r'' (q4_0 row 16r' + r'').
 template <int HD, int KT, int P>
 struct ChunkMap {
-    static constexpr int EK = KT == KV_F16 ? 8 : KT == KV_Q8_0 ? 16 : 32;
-    static constexpr int EV = KT == KV_F16 ? 8 : 16;
+    static constexpr int EK = KT == KV_F32 ? 4 : KT == KV_F16 ? 8 : KT == KV_Q8_0 ? 16 : 32;
+    static constexpr int EV = KT == KV_F32 ? 4 : KT == KV_F16 ? 8 : 16;
     static constexpr int VROWS = KT == KV_Q4_0 ? HD / 2 : HD;
     static constexpr int KPR = HD / EK;  // K chunks per token row
     static constexpr int VPD = P / EV;   // V chunks per code row and page
@@ -496,7 +497,10 @@ __device__ __forceinline__ void stage_load(const PrefillArgs &a, int kvh, int ti
         const int tk = M::k_tok(ch);
         const uint8_t *vp = a.base + page(M::v_seg(ch0) * P) * L.page_bytes;
         const int d = M::v_dim(ch), tv = M::v_tok(ch);
-        if (KT == KV_F16) {
+        if (KT == KV_F32) {
+            R.k[c] = *reinterpret_cast<const u4 *>(kp + (((int64_t)kvh * P + tk % P) * HD + M::k_col(ch)) * 4);
+            R.v[c] = *reinterpret_cast<const u4 *>(vp + L.v_off + (((int64_t)kvh * HD + d) * P + tv) * 4);
+        } else if (KT == KV_F16) {
             R.k[c] = *reinterpret_cast<const u4 *>(kp + (((int64_t)kvh * P + tk % P) * HD + M::k_col(ch)) * 2);
             R.v[c] = *reinterpret_cast<const u4 *>(vp + L.v_off + (((int64_t)kvh * HD + d) * P + tv) * 2);
         } else if (KT == KV_Q8_0) {
@@ -522,22 +526,100 @@ __device__ __forceinline__ void dequant_pair(h8 q, h8 s, h8 &hi, h8 &lo)
     lo = __builtin_elementwise_fma(q, s, -hi);
 }
 
+// x (already scaled into fp16 range) as hi + lo halves: hi = x cut to 11
+// significant bits (what the round-toward-zero conversion gives), lo the
+// exact remainder rounded to nearest, so hi + lo is x to 2^-23 relative.
+__device__ __forceinline__ void split_pair(float x0, float x1, uint32_t &hi, uint32_t &lo)
+{
+    const float t0 = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, x0) & 0xFFFFE000u);
+    const float t1 = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, x1) & 0xFFFFE000u);
+    hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x0, x1));
+    const h2 l = {(_Float16)(x0 - t0), (_Float16)(x1 - t1)};
+    lo = __builtin_bit_cast(uint32_t, l);
+}
+
+// Largest |K| and |V| of this thread's f32 chunks of a staged block, over the
+// live tokens only (stale slots may hold anything).
+template <int HD, int P>
+__device__ __forceinline__ void f32_chunk_max(const StageRegs<HD, KV_F32> &R, int tid, uint64_t vmask, float &mk,
+                                              float &mv)
+{
+    using M = ChunkMap<HD, KV_F32, P>;
+    mk = 0.0f;
+    mv = 0.0f;
+#pragma unroll
+    for (int c = 0; c < R.NC; c++) {
+        const int ch = tid + 256 * c;
+        const bool klive = (vmask >> M::k_tok(ch)) & 1u;
+        const int t0 = M::v_seg(ch) * P + M::v_tok(ch);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            // words copied out first: hipcc's __builtin_bit_cast of an
+            // ext_vector element reads element 0 whatever the index
+            const uint32_t kw = R.k[c][i], vw = R.v[c][i];
+            if (klive)
+                mk = fmaxf(mk, fabsf(__builtin_bit_cast(float, kw)));
+            if ((vmask >> (t0 + i)) & 1u)
+                mv = fmaxf(mv, fabsf(__builtin_bit_cast(float, vw)));
+        }
+    }
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+
+// Maximum of a non-negative value over the wave, wave-uniform.
+__device__ __forceinline__ float wave_max_nonneg(float x)
+{
+    x = fmaxf(x, dpp_f<0xB1>(x));  // quad_perm [1,0,3,2]
+    x = fmaxf(x, dpp_f<0x4E>(x));  // quad_perm [2,3,0,1]
+    x = fmaxf(x, dpp_f<0x141>(x)); // row_half_mirror
+    x = fmaxf(x, dpp_f<0x140>(x)); // row_mirror
+    const uint32_t b = __builtin_bit_cast(uint32_t, x);
+    const uint32_t m = max(max(__builtin_amdgcn_readlane(b, 0), __builtin_amdgcn_readlane(b, 16)),
+                           max(__builtin_amdgcn_readlane(b, 32), __builtin_amdgcn_readlane(b, 48)));
+    return __builtin_bit_cast(float, m);
+}
+
+// Power-of-two operand scale of a block with largest magnitude m: the
+// running scale `run` (0: none yet) is kept while m*run lies in [2^-2,
+// 2^15), otherwise m is moved to [2^14, 2^15).
+__device__ __forceinline__ float block_scale(float m, float run)
+{
+    const float r = run == 0.0f ? 1.0f : run;
+    const float ms = m * r;
+    if (m == 0.0f || (ms >= 0.25f && ms < 32768.0f))
+        return r;
+    int k = 14 - ((int)((__builtin_bit_cast(uint32_t, m) >> 23) & 0xFF) - 127);
+    k = min(max(k, -126), 127);
+    return __builtin_bit_cast(float, (uint32_t)(k + 127) << 23);
+}
+
+// 1 / x for a power of two x in [2^-126, 2^126].
+__device__ __forceinline__ float pow2_recip(float x)
+{
+    return __builtin_bit_cast(float, 0x7F000000u - __builtin_bit_cast(uint32_t, x));
+}
+
 // Converts and stores a staged block.  `vmask` bit l: block token l is cached
 // and on a valid page; V of other tokens is stored as zero (their scores are
 // masked, and stale values must not reach O through 0 * NaN).
 template <int HD, int KT, int P, int NBUF>
 __device__ __forceinline__ void stage_store(const PrefillArgs &a, int kvh, int tid, int w, int buf,
                                             uint64_t vmask, const StageRegs<HD, KT> &R,
-                                            Lds<HD, KT, NBUF> &S)
+                                            Lds<HD, KT, NBUF> &S, float ksc = 1.0f, float vsc = 1.0f)
 {
     using M = ChunkMap<HD, KT, P>;
     // q8_0 block scales: one per K chunk, 16 per V chunk.  Loaded here rather
     // than with the chunk so that they hold no registers through the block's
     // compute (they are shared by many chunks and come from the caches).
-    constexpr int NCS = KT != KV_F16 ? StageRegs<HD, KT>::NC : 1;
+    constexpr int NCS = StageRegs<HD, KT>::QUANT ? StageRegs<HD, KT>::NC : 1;
     u4 vs[2 * NCS];
     _Float16 ks[NCS];
-    if (KT != KV_F16) {
+    if (StageRegs<HD, KT>::QUANT) {
 #pragma unroll
         for (int c = 0; c < R.NC; c++) {
             const int ch = tid + 256 * c;
@@ -556,7 +638,37 @@ __device__ __forceinline__ void stage_store(const PrefillArgs &a, int kvh, int t
         const int tk = M::k_tok(ch), col = M::k_col(ch);
         const int d = M::v_dim(ch), t0 = M::v_seg(ch) * P + M::v_tok(ch); // block-local token
         const uint32_t live = (uint32_t)(vmask >> t0) & ((1u << M::EV) - 1u);
-        if (KT == KV_F16) {
+        if (KT == KV_F32) {
+            // K: 4 dimensions of token tk; V: tokens t0 .. t0+3 of dimension
+            // d, dead tokens zeroed (their weights are 0)
+            float kx[4], vx[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t kw = R.k[c][i], vw = R.v[c][i]; // (see f32_chunk_max)
+                kx[i] = __builtin_bit_cast(float, kw);
+                vx[i] = ((live >> i) & 1u) ? __builtin_bit_cast(float, vw) : 0.0f;
+            }
+            // the scales are workgroup-uniform and 1 for ordinary data
+            if (ksc != 1.0f) {
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    kx[i] *= ksc;
+            }
+            if (vsc != 1.0f) {
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    vx[i] *= vsc;
+            }
+            uint32_t kh[2], kl[2], vh[2], vl[2];
+            split_pair(kx[0], kx[1], kh[0], kl[0]);
+            split_pair(kx[2], kx[3], kh[1], kl[1]);
+            split_pair(vx[0], vx[1], vh[0], vl[0]);
+            split_pair(vx[2], vx[3], vh[1], vl[1]);
+            *reinterpret_cast<u2 *>(&S.k[buf][tk][col]) = u2{kh[0], kh[1]};
+            *reinterpret_cast<u2 *>(&S.kl[buf][tk][col]) = u2{kl[0], kl[1]};
+            *reinterpret_cast<u2 *>(&S.v[buf][d][t0]) = u2{vh[0], vh[1]};
+            *reinterpret_cast<u2 *>(&S.vl[buf][d][t0]) = u2{vl[0], vl[1]};
+        } else if (KT == KV_F16) {
             *reinterpret_cast<u4 *>(&S.k[buf][tk][col]) = R.k[c];
             u4 vv = R.v[c];
             if (live != 0xFFu) {
@@ -717,6 +829,7 @@ struct WaveAttn {
     static constexpr int KK = HD / 32, NB = HD / 16;
     h8 qh[NCG][KK], ql[NCG][KK];
     float c2s[NCG], m2[NCG], lsum[NCG];
+    float kinv = 1.0f; // f32 pages: 1 / the current block's K operand scale
     f4 o[NCG][NB];
     int qlen[NCG];
 
@@ -796,7 +909,7 @@ struct WaveAttn {
             mx = fmaxf(mx, sv[i]);
         mx = fmaxf(mx, __shfl_xor(mx, 16));
         mx = fmaxf(mx, __shfl_xor(mx, 32));
-        mx *= c2s[cg];
+        mx *= c2s[cg] * kinv;
         const bool grow = mx > m2[cg] + kLazy;
         const float mref = grow ? mx : m2[cg];
         alpha = grow ? __builtin_amdgcn_exp2f(m2[cg] - mref) : 1.0f;
@@ -806,7 +919,7 @@ struct WaveAttn {
         float ps = 0.0f;
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            p[i] = __builtin_amdgcn_exp2f(fmaf(sv[i], c2s[cg], -msub));
+            p[i] = __builtin_amdgcn_exp2f(fmaf(sv[i], c2s[cg] * kinv, -msub));
             ps += p[i];
         }
         lsum[cg] = lsum[cg] * alpha + ps;
@@ -906,6 +1019,16 @@ struct WaveAttn {
         }
     }
 
+    // O of every column times f (an exact power of two).
+    __device__ __forceinline__ void scale_o(float f)
+    {
+#pragma unroll
+        for (int cg = 0; cg < NCG; cg++)
+#pragma unroll
+            for (int nb = 0; nb < NB; nb++)
+                o[cg][nb] *= f;
+    }
+
     __device__ __forceinline__ void finish(const PrefillArgs &a, int b, int kvh, int col0, int j, int g)
     {
         const int H = a.num_heads, G = H / a.L.num_kv_heads, chunk = a.chunk_len;
@@ -987,17 +1110,45 @@ struct PrefillWork {
 template <int HD, int KT, int P, int NBUF, int NCG>
 __global__ __launch_bounds__(256) void attn_prefill_lds(PrefillArgs a)
 {
+    constexpr bool F32 = KT == KV_F32;
+    static_assert(!F32 || NBUF == 1, "f32 pages exchange block maxima at the single-buffer barrier");
     const PrefillWork<P, NCG> W(a);
     __shared__ Lds<HD, KT, NBUF> S;
+    __shared__ float s_bmax[4][2]; // f32 pages: per-wave |K|, |V| maxima of the block being staged
     WaveAttn<HD, KT, NCG> A;
     A.init(a, W.b, W.kvh, W.col0, W.start, W.mapped, W.wave_active, W.j, W.g);
 
     StageRegs<HD, KT> R;
+    // f32 pages: power-of-two operand scales of the staged block (running,
+    // workgroup-uniform), of the block in LDS, and the scale O is held in
+    float ksc_run = 0.0f, vsc_run = 0.0f, ksc_cur = 1.0f, vsc_cur = 1.0f, vsc_o = 0.0f;
+    // all threads: the staged block's maxima over the workgroup (one
+    // barrier), then its scales
+    auto f32_scales = [&](uint64_t vmask) {
+        if constexpr (F32) {
+            float mk, mv;
+            f32_chunk_max<HD, P>(R, W.tid, vmask, mk, mv);
+            mk = wave_max_nonneg(mk);
+            mv = wave_max_nonneg(mv);
+            if (W.lane == 0) {
+                s_bmax[W.w][0] = mk;
+                s_bmax[W.w][1] = mv;
+            }
+            __syncthreads();
+            mk = fmaxf(fmaxf(s_bmax[0][0], s_bmax[1][0]), fmaxf(s_bmax[2][0], s_bmax[3][0]));
+            mv = fmaxf(fmaxf(s_bmax[0][1], s_bmax[1][1]), fmaxf(s_bmax[2][1], s_bmax[3][1]));
+            ksc_run = block_scale(mk, ksc_run);
+            vsc_run = block_scale(mv, vsc_run);
+        }
+    };
     int tb = W.table(0);
     uint64_t mask_c = W.valid_mask(a, tb, 0);
     stage_load<HD, KT, P>(a, W.kvh, W.tid, W.w, tb, R);
     tb = W.table(kTB);
-    stage_store<HD, KT, P, NBUF>(a, W.kvh, W.tid, W.w, 0, mask_c, R, S);
+    f32_scales(mask_c);
+    stage_store<HD, KT, P, NBUF>(a, W.kvh, W.tid, W.w, 0, mask_c, R, S, ksc_run, vsc_run);
+    ksc_cur = ksc_run;
+    vsc_cur = vsc_run;
     __syncthreads();
 
     // One staged block; FULL: no column of the workgroup needs masking.
@@ -1012,14 +1163,27 @@ __global__ __launch_bounds__(256) void attn_prefill_lds(PrefillArgs a)
             stage_load<HD, KT, P>(a, W.kvh, W.tid, W.w, tb, R);
             tb = W.table(base + 2 * kTB);
         }
+        if constexpr (F32) {
+            // scores of this block carry its K scale; O moves to its V
+            // scale (exact powers of two)
+            A.kinv = pow2_recip(ksc_cur);
+            if (vsc_o != 0.0f && vsc_o != vsc_cur)
+                A.scale_o(vsc_cur * pow2_recip(vsc_o));
+            vsc_o = vsc_cur;
+        }
         if (W.wave_active && base < W.wave_len)
             A.template block<FULL>(S, buf, base, mask_c, W.j, W.g);
         if (more) {
-            if (NBUF == 1)
+            if (F32)
+                f32_scales(mask_n); // its barrier also frees the single buffer
+            else if (NBUF == 1)
                 __syncthreads();
-            stage_store<HD, KT, P, NBUF>(a, W.kvh, W.tid, W.w, NBUF == 2 ? (buf ^ 1) : 0, mask_n, R, S);
+            stage_store<HD, KT, P, NBUF>(a, W.kvh, W.tid, W.w, NBUF == 2 ? (buf ^ 1) : 0, mask_n, R, S,
+                                         ksc_run, vsc_run);
         }
         mask_c = mask_n;
+        ksc_cur = ksc_run;
+        vsc_cur = vsc_run;
         __syncthreads();
         base += kTB;
         it++;
@@ -1031,8 +1195,11 @@ __global__ __launch_bounds__(256) void attn_prefill_lds(PrefillArgs a)
         step(std::true_type{});
     while (base < W.wg_len)
         step(std::false_type{});
-    if (W.wave_active)
+    if (W.wave_active) {
+        if (F32 && vsc_o != 0.0f)
+            A.scale_o(pow2_recip(vsc_o));
         A.finish(a, W.b, W.kvh, W.col0, W.j, W.g);
+    }
 }
 
 // Issues the direct global->LDS loads of one fp16 block into buffer `buf`.
@@ -1156,11 +1323,12 @@ __global__ __launch_bounds__(256) void attn_prefill_dlds(PrefillArgs a)
 
 bool mfma_prefill_supported(const PoolLayout &L, int num_heads)
 {
-    // q4_0: the staged kernel, head_dim 128, pages of 16/32/64 tokens
-    if (L.kv_type == KV_Q4_0 &&
-        (L.head_dim != 128 || (L.page_tokens != 16 && L.page_tokens != 32 && L.page_tokens != 64)))
+    // q4_0 and f32: the staged kernel only (pages of 16/32/64 tokens; q4_0
+    // with head_dim 128)
+    const bool staged = L.page_tokens == 16 || L.page_tokens == 32 || L.page_tokens == 64;
+    if (L.kv_type == KV_Q4_0 && (L.head_dim != 128 || !staged))
         return false;
-    if (L.kv_type != KV_F16 && L.kv_type != KV_Q8_0 && L.kv_type != KV_Q4_0)
+    if (L.kv_type == KV_F32 && !staged)
         return false;
     if (L.page_tokens % 16 != 0 || (L.head_dim != 64 && L.head_dim != 128))
         return false;
@@ -1188,16 +1356,19 @@ constexpr int prefill_ncg()
 #ifndef GI_PREFILL_NBUF_Q8
 #define GI_PREFILL_NBUF_Q8 1
 #endif
+// f32 pages: one buffer (their block maxima are exchanged at its barrier).
 
 // Column groups per wave: two halve the LDS reads per matrix-core product;
-// taken where the kernel then still fits two waves per SIMD (256 VGPRs).
+// taken where the kernel then still fits two waves per SIMD (256 VGPRs), and
+// always for f32 pages, whose 64 staging registers leave one wave per SIMD
+// either way (two groups amortise the staging over twice the products).
 template <int HD, int KT, int P>
 constexpr int prefill_lds_ncg()
 {
 #ifdef GI_PREFILL_NCG
     return GI_PREFILL_NCG;
 #else
-    return (HD == 64 || P == 16 || (KT != KV_F16 && P == 32)) ? 2 : 1;
+    return KT == KV_F32 ? 2 : (HD == 64 || P == 16 || (KT != KV_F16 && P == 32)) ? 2 : 1;
 #endif
 }
 
@@ -1214,7 +1385,7 @@ template <int HD, int KT>
 static void launch_lds(const PrefillArgs &a, hipStream_t st)
 {
     using namespace mfma_prefill;
-    constexpr int NBUF = KT == KV_F16 ? GI_PREFILL_NBUF_F16 : GI_PREFILL_NBUF_Q8;
+    constexpr int NBUF = KT == KV_F32 ? 1 : KT == KV_F16 ? GI_PREFILL_NBUF_F16 : GI_PREFILL_NBUF_Q8;
     const int G = a.num_heads / a.L.num_kv_heads;
     const int64_t cols = (int64_t)a.chunk_len * G;
     auto grid = [&](int ncg) {
@@ -1265,11 +1436,15 @@ hipError_t launch_prefill_mfma(const PrefillArgs &a, hipStream_t st)
                 launch_lds<128, KV_F16>(a, st);
             else if (a.L.kv_type == KV_Q4_0)
                 launch_lds<128, KV_Q4_0>(a, st);
+            else if (a.L.kv_type == KV_F32)
+                launch_lds<128, KV_F32>(a, st);
             else
                 launch_lds<128, KV_Q8_0>(a, st);
         } else {
             if (a.L.kv_type == KV_F16)
                 launch_lds<64, KV_F16>(a, st);
+            else if (a.L.kv_type == KV_F32)
+                launch_lds<64, KV_F32>(a, st);
             else
                 launch_lds<64, KV_Q8_0>(a, st);
         }

@@ -184,7 +184,7 @@ def test_decode_stale_nan_beyond_length_is_ignored(gi, oracle, dev, kv_type):
         assert rel_err_rows(o[0], want, H, hd).max() <= 1e-3
 
 
-@pytest.mark.parametrize("kv_type", [1, 2, 3], ids=["f16", "q8_0", "q4_0"])
+@pytest.mark.parametrize("kv_type", [0, 1, 2, 3], ids=["f32", "f16", "q8_0", "q4_0"])
 def test_prefill_stale_nan_beyond_context_is_ignored(gi, oracle, dev, kv_type):
     """Prefill of 12 queries at start 16 reads 28 tokens; slots 28..39 hold
     NaN (fp16) or 1e30 (quantised: Inf block scales), inside the last read
@@ -196,7 +196,7 @@ def test_prefill_stale_nan_beyond_context_is_ignored(gi, oracle, dev, kv_type):
     t = pop.table(0)
     ids = torch.from_numpy(np.repeat(t, P)[28:40].copy()).to(dev)
     slots = torch.from_numpy((np.arange(28, 40) % P).astype(np.int32)).to(dev)
-    bad = float("nan") if kv_type == 1 else 1e30
+    bad = float("nan") if kv_type in (0, 1) else 1e30
     poison = torch.full((12, kvh * hd), bad, device=dev)
     pop.pool.Write(0, ids, slots, poison, poison)
     bt = pop.block_tables()
@@ -206,6 +206,7 @@ def test_prefill_stale_nan_beyond_context_is_ignored(gi, oracle, dev, kv_type):
     ks, vs = pop.stored(0, 0)
     kw, vw = oracle.widen(kv_type, kvh * hd, ks[:28]), oracle.widen(kv_type, kvh * hd, vs[:28])
     want = oracle.attention_prefill(q[0], kw, vw, H, kvh, hd, 16, 12, 1 << 30, scale)
+    tol = 1e-5 if kv_type == 0 else 1e-3
     for kern in (0, 1):
         pop.pool.set_decode_kernel(kern)
         out = torch.full_like(qd, float("nan"))
@@ -213,14 +214,62 @@ def test_prefill_stale_nan_beyond_context_is_ignored(gi, oracle, dev, kv_type):
         pop.pool.synchronize()
         o = out.cpu().numpy()[0]
         assert np.isfinite(o).all(), kern
-        assert rel_err_rows(o, want, H, hd).max() <= 1e-3, kern
+        assert rel_err_rows(o, want, H, hd).max() <= tol, kern
     pop.pool.set_decode_kernel(-1)
+
+
+@pytest.mark.parametrize("kv_type", [2, 3], ids=["q8_0", "q4_0"])
+def test_decode_quant_scale_spread(gi, oracle, dev, kv_type):
+    """One token of every 32 (slot 29 of the block, deep inside a lane's
+    8-token group) has values 200x the others, so its V block scales are
+    far above the rest of the block's.  The matrix-core kernel's running
+    cap must cover them: a cap taken from a subset of the scales lets that
+    token's weights overflow fp16."""
+    import torch
+    H, kvh, hd, P, lens = 32, 8, 128, 16, [200, 64]
+    kv_dim = kvh * hd
+    pages = sum((n + P - 1) // P for n in lens) + 2
+    mgr = gi.PagedKVManager(1, kv_dim, pages, P)
+    mgr.SetFreeList(np.random.default_rng(13).permutation(pages).astype(np.int32))
+    pool = gi.PagedKVCache(1, kvh, hd, P, pages, kv_type)
+    tabs, ks, vs = [], [], []
+    for i, n in enumerate(lens):
+        sid = mgr.AllocateSequence()
+        ids, slots = mgr.AppendTokens(sid, n)
+        f = np.where(np.arange(n) % 32 == 29, 200.0, 1.0).astype(np.float32)[:, None]
+        k = (oracle.normal(900 + i, (n, kv_dim)) * 0.2).astype(np.float32)
+        v = (oracle.normal(950 + i, (n, kv_dim)) * f).astype(np.float32)
+        pool.Write(0, torch.from_numpy(ids).to(dev), torch.from_numpy(slots).to(dev),
+                   torch.from_numpy(k).to(dev), torch.from_numpy(v).to(dev))
+        ks.append(oracle.widen(kv_type, kv_dim, oracle.store_vectors(kv_type, k)))
+        vs.append(oracle.widen(kv_type, kv_dim, oracle.store_vectors(kv_type, v)))
+        tabs.append(mgr.Tables[sid].BlockIDs)
+    mb = max(len(t) for t in tabs)
+    bt = torch.tensor([t + [0] * (mb - len(t)) for t in tabs], dtype=torch.int32, device=dev)
+    sl = torch.tensor(lens, dtype=torch.int32, device=dev)
+    q = oracle.normal(990, (len(lens), H * hd)).astype(np.float32)
+    qd = torch.from_numpy(q).to(dev)
+    scale = oracle.attn_scale(hd)
+    worst = {}
+    for kern in kernels_for(pool, H):
+        pool.set_decode_kernel(kern)
+        out = torch.full_like(qd, float("nan"))
+        pool.AttentionGQA(out, qd, 0, bt, sl, H, scale)
+        pool.synchronize()
+        o = out.cpu().numpy()
+        assert np.isfinite(o).all(), kern
+        for i, n in enumerate(lens):
+            want = oracle.attention_decode(q[i], ks[i], vs[i], H, kvh, hd, n, scale)
+            worst[kern] = max(worst.get(kern, 0.0), float(rel_err_rows(o[i], want, H, hd).max()))
+    pool.set_decode_kernel(-1)
+    print("quantised scale-spread decode max rel err by kernel:", worst)
+    assert max(worst.values()) <= 1e-3, worst
 
 
 @pytest.mark.parametrize("H,kvh,hd", [(32, 8, 128), (32, 4, 64), (8, 8, 128)])
 def test_decode_f32_wide_range(gi, oracle, dev, H, kvh, hd):
-    """f32 pages whose magnitude changes by up to 10^10 from one 32-token
-    block to the next (K from 1e-4 to 1e3, V from 1e-5 to 1e5, beyond fp16's
+    """f32 pages whose magnitude changes by up to 10^9 from one 32-token
+    block to the next (K from 1e-4 to 1e5, V from 1e-5 to 1e5, beyond fp16's
     range both ways): the matrix-core kernel's per-block power-of-two operand
     scales must keep the 1e-5 bound of the f32 path."""
     import torch
@@ -230,7 +279,8 @@ def test_decode_f32_wide_range(gi, oracle, dev, H, kvh, hd):
     mgr = gi.PagedKVManager(1, kv_dim, pages, P)
     mgr.SetFreeList(np.random.default_rng(5).permutation(pages).astype(np.int32))
     pool = gi.PagedKVCache(1, kvh, hd, P, pages, gi.KV_F32)
-    kf = np.array([1e-4, 1.0, 30.0, 1e-2, 1e3, 0.5, 3e-3], np.float32)
+    # K reaches 4e5 (beyond fp16) with q at 1e-5, so scores stay moderate
+    kf = np.array([1e-4, 1.0, 3e4, 1e-2, 1e5, 0.5, 3e-3], np.float32)
     vf = np.array([1.0, 1e5, 1e-5, 3e3, 1e-3, 7.0, 2e4], np.float32)
     ks, vs, tabs = [], [], []
     for i, n in enumerate(lens):
@@ -247,7 +297,7 @@ def test_decode_f32_wide_range(gi, oracle, dev, H, kvh, hd):
     mb = max(len(t) for t in tabs)
     bt = torch.tensor([t + [0] * (mb - len(t)) for t in tabs], dtype=torch.int32, device=dev)
     sl = torch.tensor(lens, dtype=torch.int32, device=dev)
-    q = (oracle.normal(500, (len(lens), H * hd)) * 0.05).astype(np.float32)
+    q = (oracle.normal(500, (len(lens), H * hd)) * 1e-5).astype(np.float32)
     qd = torch.from_numpy(q).to(dev)
     scale = oracle.attn_scale(hd)
     kinds = kernels_for(pool, H)
@@ -282,10 +332,10 @@ def prefill_case(gi, oracle, dev, kv_type, H, kvh, hd, P, starts, chunk, seed):
         kw = oracle.widen(kv_type, pop.kv_dim, ks)
         vw = oracle.widen(kv_type, pop.kv_dim, vs)
         wants.append(oracle.attention_prefill(q[i], kw, vw, H, kvh, hd, s, chunk, 1 << 30, scale))
-    # both attention kernels: vector ALU (0) and, for fp16 / q8_0 / q4_0
-    # pages, the matrix-core prefill (1; q4_0 with head_dim 128 only, other
-    # shapes fall back to the vector kernel)
-    kinds = [0, 1] if kv_type in (1, 2, 3) else [0]
+    # both attention kernels: vector ALU (0) and the matrix-core prefill (1;
+    # f32 and q4_0 pages on the staged kernel only, q4_0 with head_dim 128:
+    # other shapes fall back to the vector kernel)
+    kinds = [0, 1]
     worst = {}
     for kern in kinds:
         pop.pool.set_decode_kernel(kern)
@@ -306,7 +356,7 @@ def test_prefill_chunk(gi, oracle, dev, kv_type):
     prefill_case(gi, oracle, dev, kv_type, 32, 8, 128, 16, [0, 100, 509], 64, seed=60 + kv_type)
 
 
-@pytest.mark.parametrize("kv_type", [1, 2, 3], ids=["f16", "q8_0", "q4_0"])
+@pytest.mark.parametrize("kv_type", [0, 1, 2, 3], ids=["f32", "f16", "q8_0", "q4_0"])
 @pytest.mark.parametrize("H,kvh,hd,P", [(8, 8, 64, 16), (16, 8, 64, 32), (64, 8, 128, 32),
                                         (32, 2, 128, 16), (16, 4, 128, 64)])
 def test_prefill_shapes(gi, oracle, dev, kv_type, H, kvh, hd, P):
@@ -314,6 +364,56 @@ def test_prefill_shapes(gi, oracle, dev, kv_type, H, kvh, hd, P):
     the matrix-core prefill; ragged chunk (37 queries) and start positions
     off the page grid."""
     prefill_case(gi, oracle, dev, kv_type, H, kvh, hd, P, [3, 45], 37, seed=80 + kv_type)
+
+
+@pytest.mark.parametrize("hd,P", [(128, 16), (64, 32)])
+def test_prefill_f32_wide_range(gi, oracle, dev, hd, P):
+    """f32 pages whose magnitude moves by up to 10^9 between 64-token
+    blocks (K 1e-4 .. 1e5 with q at 1e-5, V 1e-5 .. 1e5): the staged kernel's workgroup
+    block scales must keep the 1e-5 bound of the f32 path.  A 200-query
+    chunk at start 300, batch 2."""
+    import torch
+    H, kvh = 16, 4
+    kv_dim = kvh * hd
+    starts, chunk = [300, 129], 200
+    lens = [s + chunk for s in starts]
+    pages = sum((n + P - 1) // P for n in lens) + 2
+    mgr = gi.PagedKVManager(1, kv_dim, pages, P)
+    mgr.SetFreeList(np.random.default_rng(9).permutation(pages).astype(np.int32))
+    pool = gi.PagedKVCache(1, kvh, hd, P, pages, gi.KV_F32)
+    kf = np.array([1e-4, 1.0, 3e4, 1e-2, 1e5, 0.5, 3e-3], np.float32)
+    vf = np.array([1.0, 1e5, 1e-5, 3e3, 1e-3, 7.0, 2e4], np.float32)
+    ks, vs, tabs = [], [], []
+    for i, n in enumerate(lens):
+        sid = mgr.AllocateSequence()
+        ids, slots = mgr.AppendTokens(sid, n)
+        blk = (np.arange(n) // 64 + i) % len(kf)
+        k = (oracle.normal(600 + i, (n, kv_dim)) * kf[blk][:, None]).astype(np.float32)
+        v = (oracle.normal(700 + i, (n, kv_dim)) * vf[blk][:, None]).astype(np.float32)
+        pool.Write(0, torch.from_numpy(ids).to(dev), torch.from_numpy(slots).to(dev),
+                   torch.from_numpy(k).to(dev), torch.from_numpy(v).to(dev))
+        ks.append(k)
+        vs.append(v)
+        tabs.append(mgr.Tables[sid].BlockIDs)
+    mb = max(len(t) for t in tabs)
+    bt = torch.tensor([t + [0] * (mb - len(t)) for t in tabs], dtype=torch.int32, device=dev)
+    sp = torch.tensor(starts, dtype=torch.int32, device=dev)
+    q = (oracle.normal(800, (len(starts), chunk, H * hd)) * 1e-5).astype(np.float32)
+    qd = torch.from_numpy(q).to(dev)
+    scale = oracle.attn_scale(hd)
+    worst = {}
+    for kern in (0, 1):
+        pool.set_decode_kernel(kern)
+        out = torch.full_like(qd, float("nan"))
+        pool.AttentionGQABatch(out, qd, 0, bt, sp, H, scale, chunk)
+        pool.synchronize()
+        o = out.cpu().numpy()
+        for i, s0 in enumerate(starts):
+            want = oracle.attention_prefill(q[i], ks[i], vs[i], H, kvh, hd, s0, chunk, 1 << 30, scale)
+            worst[kern] = max(worst.get(kern, 0.0), float(rel_err_rows(o[i], want, H, hd).max()))
+    pool.set_decode_kernel(-1)
+    print("f32 wide-range prefill max rel err by kernel:", worst)
+    assert max(worst.values()) <= 1e-5, worst
 
 
 def test_prefill_q4_llama8b_chunks(gi, oracle, dev):
