@@ -843,32 +843,46 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
     // halves stay normal -- the matrix cores read fp16 denormals as zero --
     // and the scores are scaled back through c.  The hi and lo columns of a
     // head see the same values, so they pick the same qe.
+    // (Loaded by load_q once the wave's first block is in flight, so that the
+    // two memory round trips overlap.)
     h8 qh[KK], ql[KK];
-    float qv[KK][8];
-    float mq = 0.0f;
+    float c = 0.0f;
+    auto load_q = [&]() {
+        float qv[KK][8];
+        float mq = 0.0f;
+        const float *qp = a.q + (qrow + qhead) * HD + 8 * g;
 #pragma unroll
-    for (int kk = 0; kk < KK; kk++)
+        for (int kk = 0; kk < KK; kk++) {
+            const float4 x0 = qvalid ? *reinterpret_cast<const float4 *>(qp + 32 * kk) : float4{};
+            const float4 x1 = qvalid ? *reinterpret_cast<const float4 *>(qp + 32 * kk + 4) : float4{};
+            qv[kk][0] = x0.x;
+            qv[kk][1] = x0.y;
+            qv[kk][2] = x0.z;
+            qv[kk][3] = x0.w;
+            qv[kk][4] = x1.x;
+            qv[kk][5] = x1.y;
+            qv[kk][6] = x1.z;
+            qv[kk][7] = x1.w;
 #pragma unroll
-        for (int v = 0; v < 8; v++) {
-            qv[kk][v] = qvalid ? a.q[(qrow + qhead) * HD + 32 * kk + 8 * g + v] : 0.0f;
-            mq = fmaxf(mq, fabsf(qv[kk][v]));
+            for (int v = 0; v < 8; v++)
+                mq = fmaxf(mq, fabsf(qv[kk][v]));
         }
-    mq = fmaxf(mq, __shfl_xor(mq, 16));
-    mq = fmaxf(mq, __shfl_xor(mq, 32));
-    const int qe = pow2_exponent_for(mq);
-    const float up = ldexpf(1.0f, qe);
+        mq = fmaxf(mq, __shfl_xor(mq, 16));
+        mq = fmaxf(mq, __shfl_xor(mq, 32));
+        const int qe = pow2_exponent_for(mq);
+        const float up = ldexpf(1.0f, qe);
 #pragma unroll
-    for (int kk = 0; kk < KK; kk++)
+        for (int kk = 0; kk < KK; kk++)
 #pragma unroll
-        for (int v = 0; v < 8; v++) {
-            const float x = qv[kk][v] * up;
-            _Float16 hi = (_Float16)x;
-            _Float16 lo = (_Float16)(x - (float)hi);
-            qh[kk][v] = qlo ? lo : hi;
-            ql[kk][v] = lo;
-        }
-
-    const float c = a.scale * kLog2e * ldexpf(1.0f, -qe);
+            for (int v = 0; v < 8; v++) {
+                const float x = qv[kk][v] * up;
+                _Float16 hi = (_Float16)x;
+                _Float16 lo = (_Float16)(x - (float)hi);
+                qh[kk][v] = qlo ? lo : hi;
+                ql[kk][v] = lo;
+            }
+        c = a.scale * kLog2e * ldexpf(1.0f, -qe);
+    };
     State<HD> S;
     S.m2 = -INFINITY;
     S.lsum = 0.0f;
@@ -902,6 +916,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
             bool ok;
             block_pages(a, bt, base, t1, pA, pB, sA, sB, ok);
             issue_q<KT, HD>(a, pA, pB, sA, sB, koff, ksoff, voff, vsoff, lane, Sq);
+            load_q();
             for (;;) {
                 QBlock<KT, HD> B;
                 // the only vector loads in flight are this block's
@@ -940,6 +955,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
             bool ok;
             block_pages(a, bt, base, t1, pA, pB, sA, sB, ok);
             issue_f32<HD>(a, pA, pB, sA, sB, koff, voff, lane, Sf);
+            load_q();
             for (;;) {
                 h8 kh0[KK], kh1[KK], kl0[KK], kl1[KK], vh[NB], vl[NB];
                 // the only vector loads in flight are this block's
@@ -988,6 +1004,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
         block_pages(a, bt, base, t1, pA, pB, sA, sB, ok);
         load_k<HD, NT>(a, pA, pB, sA, sB, koff, j, g, k0, k1);
         load_v<HD, NT>(a, pA, pB, sA, sB, voff, j, g, v);
+        load_q();
         f4 s0, s1;
         for (;;) {
             qk<HD, GP>(k0, k1, qh, ql, s0, s1);
