@@ -440,15 +440,36 @@ struct StageRegs {
     int64_t vpage[QUANT ? NC : 1];
 };
 
+// Swizzled geometry of one staged block in LDS, shared by both staged
+// kernels.  K: segments of 512/HD token rows (1 KiB, rows unpadded inside),
+// each followed by 4096/HD bytes of padding, the low two bits of a row's
+// 16-byte chunk index XORed with row % 4; V: [dimension][kTB] halves with the
+// 16-byte chunk index XORed with dimension % 8.  The MFMA operand reads of a
+// quarter-wave then fall on distinct banks.
+template <int HD>
+struct SwzGeom {
+    static constexpr int KROWS = 512 / HD;             // K rows per segment
+    static constexpr int KSEGB = 1024 + 4096 / HD;     // bytes per K segment, padded
+    static constexpr int KBYTES = kTB / KROWS * KSEGB; // bytes of one K plane
+    static constexpr int VBYTES = HD * kTB * 2;        // bytes of one V plane
+    // byte offsets of chunk c (8 halves) of K row `row` / of V dimension `dim`
+    __device__ static int koff(int row, int c) { return row / KROWS * KSEGB + row % KROWS * HD * 2 + 16 * (c ^ (row & 3)); }
+    __device__ static int voff(int dim, int c) { return (dim * kTB + 8 * (c ^ (dim & 7))) * 2; }
+    // byte offsets of element `col` of K row `row` / token `t` of V dimension `dim`
+    __device__ static int kel(int row, int col) { return koff(row, col >> 3) + (col & 7) * 2; }
+    __device__ static int vel(int dim, int t) { return voff(dim, t >> 3) + (t & 7) * 2; }
+};
+
 // Quantised and f32 K and V are stored as hi + lo fp16 pairs (exact for
-// quantised pages, 2^-23 relative for f32 ones).
+// quantised pages, 2^-23 relative for f32 ones), in the swizzled geometry.
 template <int HD, int KT, int NBUF>
 struct Lds {
     static constexpr bool Q8 = KT != KV_F16;
-    __attribute__((aligned(16))) _Float16 k[NBUF][kTB][HD + 8];  // token-major K, rows padded
-    __attribute__((aligned(16))) _Float16 v[NBUF][HD][kTB + 8];  // dimension-major V
-    __attribute__((aligned(16))) _Float16 kl[Q8 ? NBUF : 1][Q8 ? kTB : 1][HD + 8]; // q8_0: K lo
-    __attribute__((aligned(16))) _Float16 vl[Q8 ? NBUF : 1][Q8 ? HD : 1][kTB + 8]; // q8_0: V lo
+    using G = SwzGeom<HD>;
+    __attribute__((aligned(16))) uint8_t k[NBUF][G::KBYTES];
+    __attribute__((aligned(16))) uint8_t v[NBUF][G::VBYTES];
+    __attribute__((aligned(16))) uint8_t kl[Q8 ? NBUF : 1][Q8 ? G::KBYTES : 1]; // K lo
+    __attribute__((aligned(16))) uint8_t vl[Q8 ? NBUF : 1][Q8 ? G::VBYTES : 1]; // V lo
 };
 
 // Chunk -> (token, column) of K and (page segment, code row, token group)
@@ -613,6 +634,7 @@ __device__ __forceinline__ void stage_store(const PrefillArgs &a, int kvh, int t
                                             Lds<HD, KT, NBUF> &S, float ksc = 1.0f, float vsc = 1.0f)
 {
     using M = ChunkMap<HD, KT, P>;
+    using G = SwzGeom<HD>;
     // q8_0 block scales: one per K chunk, 16 per V chunk.  Loaded here rather
     // than with the chunk so that they hold no registers through the block's
     // compute (they are shared by many chunks and come from the caches).
@@ -664,12 +686,12 @@ __device__ __forceinline__ void stage_store(const PrefillArgs &a, int kvh, int t
             split_pair(kx[2], kx[3], kh[1], kl[1]);
             split_pair(vx[0], vx[1], vh[0], vl[0]);
             split_pair(vx[2], vx[3], vh[1], vl[1]);
-            *reinterpret_cast<u2 *>(&S.k[buf][tk][col]) = u2{kh[0], kh[1]};
-            *reinterpret_cast<u2 *>(&S.kl[buf][tk][col]) = u2{kl[0], kl[1]};
-            *reinterpret_cast<u2 *>(&S.v[buf][d][t0]) = u2{vh[0], vh[1]};
-            *reinterpret_cast<u2 *>(&S.vl[buf][d][t0]) = u2{vl[0], vl[1]};
+            *reinterpret_cast<u2 *>(&S.k[buf][G::kel(tk, col)]) = u2{kh[0], kh[1]};
+            *reinterpret_cast<u2 *>(&S.kl[buf][G::kel(tk, col)]) = u2{kl[0], kl[1]};
+            *reinterpret_cast<u2 *>(&S.v[buf][G::vel(d, t0)]) = u2{vh[0], vh[1]};
+            *reinterpret_cast<u2 *>(&S.vl[buf][G::vel(d, t0)]) = u2{vl[0], vl[1]};
         } else if (KT == KV_F16) {
-            *reinterpret_cast<u4 *>(&S.k[buf][tk][col]) = R.k[c];
+            *reinterpret_cast<u4 *>(&S.k[buf][G::kel(tk, col)]) = R.k[c];
             u4 vv = R.v[c];
             if (live != 0xFFu) {
 #pragma unroll
@@ -677,7 +699,7 @@ __device__ __forceinline__ void stage_store(const PrefillArgs &a, int kvh, int t
                     if (!((live >> i) & 1u))
                         vv[i / 2] &= (i & 1) ? 0x0000FFFFu : 0xFFFF0000u;
             }
-            *reinterpret_cast<u4 *>(&S.v[buf][d][t0]) = vv;
+            *reinterpret_cast<u4 *>(&S.v[buf][G::vel(d, t0)]) = vv;
         } else if (KT == KV_Q4_0) {
             // K: the chunk is one block; low nibbles are dimensions col ..
             // col + 15, high nibbles col + 16 .. col + 31
@@ -687,8 +709,8 @@ __device__ __forceinline__ void stage_store(const PrefillArgs &a, int kvh, int t
                 h8 hi, lo;
                 const u2 w = u2{R.k[c][2 * (m & 1)], R.k[c][2 * (m & 1) + 1]};
                 dequant_pair(u4x8_to_h8(w, 4 * (m >> 1)), ksp, hi, lo);
-                *reinterpret_cast<h8 *>(&S.k[buf][tk][col + 8 * m]) = hi;
-                *reinterpret_cast<h8 *>(&S.kl[buf][tk][col + 8 * m]) = lo;
+                *reinterpret_cast<h8 *>(&S.k[buf][G::kel(tk, col + 8 * m)]) = hi;
+                *reinterpret_cast<h8 *>(&S.kl[buf][G::kel(tk, col + 8 * m)]) = lo;
             }
             // V: byte row d = 16 db + r holds dimension 32 db + r (low
             // nibble) and 32 db + 16 + r (high nibble) of 16 tokens
@@ -709,8 +731,8 @@ __device__ __forceinline__ void stage_store(const PrefillArgs &a, int kvh, int t
                                 lo[i] = (_Float16)0.0f;
                             }
                     }
-                    *reinterpret_cast<h8 *>(&S.v[buf][dl + 16 * nib][t0 + 8 * half]) = hi;
-                    *reinterpret_cast<h8 *>(&S.vl[buf][dl + 16 * nib][t0 + 8 * half]) = lo;
+                    *reinterpret_cast<h8 *>(&S.v[buf][G::vel(dl + 16 * nib, t0 + 8 * half)]) = hi;
+                    *reinterpret_cast<h8 *>(&S.vl[buf][G::vel(dl + 16 * nib, t0 + 8 * half)]) = lo;
                 }
             }
         } else {
@@ -719,8 +741,8 @@ __device__ __forceinline__ void stage_store(const PrefillArgs &a, int kvh, int t
             for (int half = 0; half < 2; half++) {
                 h8 hi, lo;
                 dequant_pair(i8x8_to_h8(u2{R.k[c][2 * half], R.k[c][2 * half + 1]}), ksp, hi, lo);
-                *reinterpret_cast<h8 *>(&S.k[buf][tk][col + 8 * half]) = hi;
-                *reinterpret_cast<h8 *>(&S.kl[buf][tk][col + 8 * half]) = lo;
+                *reinterpret_cast<h8 *>(&S.k[buf][G::kel(tk, col + 8 * half)]) = hi;
+                *reinterpret_cast<h8 *>(&S.kl[buf][G::kel(tk, col + 8 * half)]) = lo;
             }
 #pragma unroll
             for (int half = 0; half < 2; half++) {
@@ -736,8 +758,8 @@ __device__ __forceinline__ void stage_store(const PrefillArgs &a, int kvh, int t
                             lo[i] = (_Float16)0.0f;
                         }
                 }
-                *reinterpret_cast<h8 *>(&S.v[buf][d][t0 + 8 * half]) = hi;
-                *reinterpret_cast<h8 *>(&S.vl[buf][d][t0 + 8 * half]) = lo;
+                *reinterpret_cast<h8 *>(&S.v[buf][G::vel(d, t0 + 8 * half)]) = hi;
+                *reinterpret_cast<h8 *>(&S.vl[buf][G::vel(d, t0 + 8 * half)]) = lo;
             }
         }
     }
@@ -749,48 +771,43 @@ __device__ __forceinline__ void stage_store(const PrefillArgs &a, int kvh, int t
 // layout splits these addresses into a per-lane base, computed once per
 // block, and a compile-time offset, so that the reads use immediate offsets.
 
-// Register-staged layout (rows padded by 16 bytes).
+// Register-staged layout: the swizzled geometry (SwzGeom), hi and lo planes.
 template <int HD, int KT, int NBUF>
 __device__ __forceinline__ const uint8_t *k_lane(const Lds<HD, KT, NBUF> &S, int buf, int j, int g, bool lo)
 {
-    return reinterpret_cast<const uint8_t *>(lo ? &S.kl[buf][8 * (j >> 2) + (j & 3)][8 * g]
-                                                : &S.k[buf][8 * (j >> 2) + (j & 3)][8 * g]);
+    // row 8(j/4) + j%4 (+ 32h + 4t): segment and row inside it
+    using G = SwzGeom<HD>;
+    constexpr int KR = G::KROWS;
+    const int seg = KR == 4 ? 2 * (j >> 2) : (j >> 2);
+    return (lo ? S.kl[buf] : S.k[buf]) + seg * G::KSEGB + (j & 3) * HD * 2 + 16 * (g ^ (j & 3));
 }
 template <int HD, int KT, int NBUF>
 __device__ __forceinline__ const uint8_t *v_lane(const Lds<HD, KT, NBUF> &S, int buf, int h, int j, int g,
                                                  bool lo)
 {
-    return reinterpret_cast<const uint8_t *>(lo ? &S.vl[buf][j][32 * h + 8 * g] : &S.v[buf][j][32 * h + 8 * g]);
+    return (lo ? S.vl[buf] : S.v[buf]) + (j * kTB + 8 * ((4 * h + g) ^ (j & 7))) * 2;
 }
 template <int HD, int KT, int NBUF>
 __device__ constexpr int k_const(const Lds<HD, KT, NBUF> *, int h, int t, int kk)
 {
-    return ((32 * h + 4 * t) * (HD + 8) + 32 * kk) * 2;
+    constexpr int KR = SwzGeom<HD>::KROWS, SB = SwzGeom<HD>::KSEGB;
+    return (KR == 4 ? (8 * h + t) * SB : 4 * h * SB + 4 * t * HD * 2) + 64 * kk;
 }
 template <int HD, int KT, int NBUF>
 __device__ constexpr int v_const(const Lds<HD, KT, NBUF> *, int nb)
 {
-    return 16 * nb * (kTB + 8) * 2;
+    return 16 * nb * kTB * 2;
 }
 
-// Layout written by direct global->LDS loads (fp16 pages).  One load
-// instruction fills a 1 KiB segment of LDS with its lanes' 16 bytes in lane
-// order, so rows inside a segment are unpadded.  K: segments of 512/HD token
-// rows, each followed by 4096/HD bytes of padding, and the low two bits of a
-// row's 16-byte chunk index XORed with row % 4; V: segments of 8 dimensions,
-// chunk index XORed with dim % 8.  The MFMA operand reads of 8 consecutive
-// lanes then fall on distinct banks.
+// Layout written by direct global->LDS loads (fp16 pages): the swizzled
+// geometry (SwzGeom), whose K segments are exactly what one 1 KiB load
+// instruction fills in lane order.
 template <int HD>
 struct LdsDirect {
-    static constexpr int KROWS = 512 / HD;             // K rows per segment
-    static constexpr int KSEGB = 1024 + 4096 / HD;     // bytes per K segment, padded
-    static constexpr int KBYTES = kTB / KROWS * KSEGB; // bytes of one K buffer
+    static constexpr int KROWS = SwzGeom<HD>::KROWS, KSEGB = SwzGeom<HD>::KSEGB, KBYTES = SwzGeom<HD>::KBYTES;
     __attribute__((aligned(16))) uint8_t k[2][KBYTES];
     __attribute__((aligned(16))) _Float16 v[2][HD * kTB]; // [dim][kTB], chunk c at c ^ (dim & 7)
-    __device__ static int koff(int row, int c)
-    {
-        return row / KROWS * KSEGB + row % KROWS * HD * 2 + 16 * (c ^ (row & 3));
-    }
+    __device__ static int koff(int row, int c) { return SwzGeom<HD>::koff(row, c); }
 };
 template <int HD>
 __device__ __forceinline__ const uint8_t *k_lane(const LdsDirect<HD> &S, int buf, int j, int g, bool)
