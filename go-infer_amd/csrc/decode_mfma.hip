@@ -256,16 +256,23 @@ __device__ __forceinline__ void issue_q(const DecodeArgs &a, int64_t pA, int64_t
         const uint8_t *src = (h ? gB + sB : gA + sA) + voff + (int64_t)(16 * r + jj) * P;
         __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.v[1024 * q], 16, 0, GI_DECODE_LDS_AUX);
     }
+    // Both scale planes in one 16-byte load of 32 lanes: lane c < 16 fills
+    // ks bytes 16c .. 16c+15, lane 16 + c fills vs bytes 16c .. 16c+15.  The
+    // texture unit spends about as long on a load of 4-byte lanes as on one
+    // of 16-byte lanes, so one wide load replaces two narrow ones.
     {
-        // 16 tokens x KK halves = 8*KK words per half; spare lanes repeat
-        const int h = lane >> 5, wd = min(lane & 31, 8 * KK - 1);
-        const uint8_t *src = (h ? gB + (int64_t)sB * KK * 2 : gA + (int64_t)sA * KK * 2) + ksoff + 4 * wd;
-        __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.ks[0], 4, 0, GI_DECODE_LDS_AUX);
-    }
-    {
-        const int h = lane >> 5, db = min((lane >> 3) & 3, KK - 1), wd = lane & 7;
-        const uint8_t *src = (h ? gB : gA) + vsoff + ((int64_t)db * P + (h ? sB : sA)) * 2 + 4 * wd;
-        __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.vs[0], 4, 0, GI_DECODE_LDS_AUX);
+        const int c = lane & 15, h = c >> 3;
+        const uint8_t *pg = h ? gB : gA;
+        const int slot = h ? sB : sA;
+        // K: 16 tokens x KK halves = 32*KK bytes per half; V: block db of a
+        // half is 16 tokens = 32 bytes, two lanes
+        const int o = 16 * (c & 7), db = (c >> 1) & 3, part = c & 1;
+        const int64_t koffs = ksoff + (int64_t)slot * KK * 2 + o;
+        const int64_t voffs = vsoff + ((int64_t)db * P + slot + 8 * part) * 2;
+        const uint8_t *src = pg + (lane < 16 ? koffs : voffs);
+        const bool use = lane < 16 ? o < 32 * KK : db < KK;
+        if (lane < 32 && use)
+            __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.ks[0], 16, 0, GI_DECODE_LDS_AUX);
     }
 }
 
@@ -616,16 +623,19 @@ __device__ __forceinline__ void softmax_pv(f4 s0, f4 s1, h8 *v, int base, bool o
     mx = fmaxf(mx, __shfl_xor(mx, 16));
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     const float mnew = fmaxf(S.m2, mx);
-    const float alpha = exp2f(S.m2 - mnew);
+    // the bare exponential instruction: results below 2^-126 (flushed to
+    // zero) weigh nothing beside the block maximum's 2^14
+    const float alpha = __builtin_amdgcn_exp2f(S.m2 - mnew);
     S.m2 = mnew;
     // p carries a factor 2^14 (its lo half stays a normal fp16); the running
     // sum carries the same factor, which cancels in the final division.
+    const float msub = mnew - 14.0f;
     float ps = 0.0f;
     h8 ph, pl;
     const bool lo_row = GP != 0 && j >= GP;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-        const float p = exp2f(sc[i] - mnew + 14.0f);
+        const float p = __builtin_amdgcn_exp2f(sc[i] - msub);
         ps += p;
         const _Float16 hi = (_Float16)p;
         const _Float16 lo = (_Float16)(p - (float)hi);
@@ -713,12 +723,13 @@ __device__ __forceinline__ void softmax_pv_q(f4 s0, f4 s1, QBlock<KT, HD> &B, in
     mx = fmaxf(mx, __shfl_xor(mx, 16));
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     const float mnew = fmaxf(S.m2, mx);
-    const float alpha = exp2f(S.m2 - mnew);
+    const float alpha = __builtin_amdgcn_exp2f(S.m2 - mnew);
     S.m2 = mnew;
+    const float msub = mnew - 14.0f;
     float p[8], ps = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-        p[i] = exp2f(sc[i] - mnew + 14.0f);
+        p[i] = __builtin_amdgcn_exp2f(sc[i] - msub);
         ps += p[i];
     }
     S.lsum = S.lsum * alpha + ps;
@@ -1143,6 +1154,9 @@ bool mfma_decode_supported(const PoolLayout &L, int num_heads)
 #ifndef GI_MFMA_DECODE_OCC
 #define GI_MFMA_DECODE_OCC 1
 #endif
+#ifndef GI_MFMA_DECODE_OCC_Q
+#define GI_MFMA_DECODE_OCC_Q GI_MFMA_DECODE_OCC
+#endif
 #ifndef GI_MFMA_DECODE_PACK
 #define GI_MFMA_DECODE_PACK true
 #endif
@@ -1160,7 +1174,7 @@ static void launch_mfma_q(const DecodeArgs &a, dim3 grid, hipStream_t st)
 {
 #define GI_Q(GPv)                                                                                        \
     hipLaunchKernelGGL((mfma_decode::attn_mfma_q<KT, HD, GPv, GI_MFMA_DECODE_NT, GI_MFMA_DECODE_PREFETCH, \
-                                                 GI_MFMA_DECODE_OCC>),                                  \
+                                                 GI_MFMA_DECODE_OCC_Q>),                                \
                        grid, dim3(256), 0, st, a)
     switch (a.num_heads / a.L.num_kv_heads) {
     case 1: GI_Q(1); break;

@@ -319,14 +319,15 @@ __global__ __launch_bounds__(256) void attn_prefill(PrefillArgs a)
             const float mnew = fmaxf(m2[cg], mx);
             // A column whose tokens all lie ahead (possible only for a block
             // past its own limit, which it never reaches first) keeps -inf.
-            const float alpha = mnew == -INFINITY ? 1.0f : exp2f(m2[cg] - mnew);
+            const float alpha = mnew == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m2[cg] - mnew);
             m2[cg] = mnew;
             // p carries a factor 2^14 (so its lo half stays a normal fp16);
             // the running sum carries the same factor and it cancels at the end.
+            const float msub = mnew - 14.0f;
             float p[8], ps = 0.0f;
 #pragma unroll
             for (int i = 0; i < 8; i++) {
-                p[i] = mnew == -INFINITY ? 0.0f : exp2f(sc[i] - mnew + 14.0f);
+                p[i] = mnew == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sc[i] - msub);
                 ps += p[i];
             }
             lsum[cg] = lsum[cg] * alpha + ps;
