@@ -49,7 +49,7 @@ using mfma_ops::f4;
 using mfma_ops::u2;
 using mfma_ops::u4;
 using mfma_ops::i8x8_to_h8;
-using mfma_ops::u4x8_to_h8;
+using mfma_ops::u4x8_masked_to_h8;
 typedef uint16_t us2 __attribute__((ext_vector_type(2)));
 
 // Cache policy of the direct global->LDS loads (2: non-temporal, which
@@ -164,9 +164,12 @@ __device__ __forceinline__ float mirror(float x)
 {
     // DPP within 16-lane rows: quad_perm [1,0,3,2] (^1), quad_perm [3,2,1,0]
     // (^3), row_half_mirror (^7 within 8 lanes), row_mirror (^15).
+    // Every lane reads a lane of its own row, so the bound control never
+    // applies; written as an update of 0 the move folds into the add that
+    // uses it (one v_add_f32_dpp).
     constexpr int ctrl = GP == 1 ? 0xB1 : GP == 2 ? 0x1B : GP == 4 ? 0x141 : 0x140;
-    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), ctrl,
-                                                               0xF, 0xF, false));
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), ctrl,
+                                                                  0xF, 0xF, true));
 }
 
 // Half i of a run of uint32 words, widened to float by the hardware
@@ -350,7 +353,8 @@ __device__ __forceinline__ void issue_f32(const DecodeArgs &a, int64_t pA, int64
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float x)
 {
-    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+    // (an update of 0 with in-row patterns: folds into the instruction using it)
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
 }
 
 // Maximum of a non-negative value over the wave, wave-uniform: DPP within
@@ -538,11 +542,15 @@ __device__ __forceinline__ void qk_q(const QBlock<KT, HD> &B, const h8 *qh, int 
     constexpr int KK = HD / 32;
     s0 = f4{0.0f, 0.0f, 0.0f, 0.0f};
     s1 = f4{0.0f, 0.0f, 0.0f, 0.0f};
-    const int sh = (g & 2) ? 4 : 0;
+    // q4_0: lanes g >= 2 take the high nibbles in place (16 (n - 8)); their
+    // query elements carry 1/16
+    const bool hi_nib = (g & 2) != 0;
+    const uint32_t km = hi_nib ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
+    const h2 kb = hi_nib ? h2{(_Float16)1152.0f, (_Float16)1152.0f} : h2{(_Float16)1032.0f, (_Float16)1032.0f};
 #pragma unroll
     for (int kk = 0; kk < KK; kk++) {
-        const h8 a0 = KT == KV_Q4_0 ? u4x8_to_h8(B.k0[kk], sh) : i8x8_to_h8(B.k0[kk]);
-        const h8 a1 = KT == KV_Q4_0 ? u4x8_to_h8(B.k1[kk], sh) : i8x8_to_h8(B.k1[kk]);
+        const h8 a0 = KT == KV_Q4_0 ? u4x8_masked_to_h8(B.k0[kk], km, kb) : i8x8_to_h8(B.k0[kk]);
+        const h8 a1 = KT == KV_Q4_0 ? u4x8_masked_to_h8(B.k1[kk], km, kb) : i8x8_to_h8(B.k1[kk]);
         const f4 z0 = mfma(a0, qh[kk], f4{0.0f, 0.0f, 0.0f, 0.0f});
         const f4 z1 = mfma(a1, qh[kk], f4{0.0f, 0.0f, 0.0f, 0.0f});
 #pragma unroll
@@ -784,7 +792,11 @@ __device__ __forceinline__ void softmax_pv_q(f4 s0, f4 s1, QBlock<KT, HD> &B, in
         const h8 pw8 = __builtin_bit_cast(h8, u4{pk[0], pk[1], pk[2], pk[3]});
 #pragma unroll
         for (int h = 0; h < 2; h++) {
-            const h8 vv = KT == KV_Q4_0 ? u4x8_to_h8(B.v[db], 4 * h) : i8x8_to_h8(B.v[2 * db + h]);
+            // q4_0: the high nibbles in place, so tile 2db+1 accumulates 16 O
+            const h8 vv = KT == KV_Q4_0 ? u4x8_masked_to_h8(B.v[db], h ? 0xF0F0F0F0u : 0x0F0F0F0Fu,
+                                                            h ? h2{(_Float16)1152.0f, (_Float16)1152.0f}
+                                                              : h2{(_Float16)1032.0f, (_Float16)1032.0f})
+                                        : i8x8_to_h8(B.v[2 * db + h]);
             S.o[2 * db + h] = mfma(pw8, vv, S.o[2 * db + h]);
         }
     }
@@ -851,9 +863,8 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
     const bool qvalid = GP == 0 ? j < G : j < 2 * G;
     const bool qlo = GP != 0 && j >= G;
     // Each head's query is scaled by 2^qe (from its largest |q|) so both fp16
-    // halves stay normal -- the matrix cores read fp16 denormals as zero --
-    // and the scores are scaled back through c.  The hi and lo columns of a
-    // head see the same values, so they pick the same qe.
+    // halves stay normal, and the scores are scaled back through c.  The hi
+    // and lo columns of a head see the same values, so they pick the same qe.
     // (Loaded by load_q once the wave's first block is in flight, so that the
     // two memory round trips overlap.)
     h8 qh[KK], ql[KK];
@@ -881,7 +892,9 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
         mq = fmaxf(mq, __shfl_xor(mq, 16));
         mq = fmaxf(mq, __shfl_xor(mq, 32));
         const int qe = pow2_exponent_for(mq);
-        const float up = ldexpf(1.0f, qe);
+        // q4_0 pages: dimensions 16..31 of each block (lanes g >= 2) meet
+        // high nibbles that carry 16
+        const float up = ldexpf(KT == KV_Q4_0 && (g & 2) ? 0.0625f : 1.0f, qe);
 #pragma unroll
         for (int kk = 0; kk < KK; kk++)
 #pragma unroll
@@ -1062,7 +1075,8 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
                 // rows G .. 2G-1 hold lo halves carrying 2^11; every row
                 // holds O / vnorm of its dimension block
                 const int row = 4 * g + r;
-                o *= vnorm * (row >= G && row < 2 * G ? 1.0f / 2048.0f : 1.0f);
+                o *= vnorm * (row >= G && row < 2 * G ? 1.0f / 2048.0f : 1.0f) *
+                     (KT == KV_Q4_0 && (nb & 1) ? 0.0625f : 1.0f);
             }
             if constexpr (F32) {
                 // the accumulators hold O times the wave's V scale

@@ -60,5 +60,27 @@ __device__ __forceinline__ h8 u4x8_to_h8(u2 w, int sh)
     return r;
 }
 
+// Eight Q4_0 nibbles left in place -> eight exact fp16 values: the bytes of
+// w masked by m (0x0F0F0F0F keeps the low nibbles n, 0xF0F0F0F0 the high
+// ones as 16n) under 0x64 make the halves 1024 + n or 1024 + 16n, and the
+// bias (1032 or 1152) leaves n - 8 or 16(n - 8).  A high-nibble operand so
+// carries a factor 16 that the caller takes out of the other operand or of
+// the accumulator, and needs no shift.
+__device__ __forceinline__ h8 u4x8_masked_to_h8(u2 w, uint32_t m, h2 bias)
+{
+    const uint32_t x0 = w.x & m, x1 = w.y & m;
+    const uint32_t c = 0x64646464u;
+    const uint32_t u[4] = {__builtin_amdgcn_perm(c, x0, 0x04010400u), __builtin_amdgcn_perm(c, x0, 0x04030402u),
+                           __builtin_amdgcn_perm(c, x1, 0x04010400u), __builtin_amdgcn_perm(c, x1, 0x04030402u)};
+    h8 r;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const h2 t = __builtin_bit_cast(h2, u[i]) - bias;
+        r[2 * i] = t[0];
+        r[2 * i + 1] = t[1];
+    }
+    return r;
+}
+
 } // namespace mfma_ops
 } // namespace gi

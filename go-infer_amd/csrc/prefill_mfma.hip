@@ -590,7 +590,8 @@ __device__ __forceinline__ void f32_chunk_max(const StageRegs<HD, KV_F32> &R, in
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float x)
 {
-    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+    // (an update of 0 with in-row patterns: folds into the instruction using it)
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
 }
 
 // Maximum of a non-negative value over the wave, wave-uniform.
