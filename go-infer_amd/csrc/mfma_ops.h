@@ -20,6 +20,36 @@ __device__ __forceinline__ f4 mfma16(h8 a, h8 b, f4 c)
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// Maximum of x and its value in lane l ^ 16 (l ^ 32): one permlane swap
+// (a VALU instruction, with no trip through LDS) hands each lane the other
+// row's (half's) value in one of its two results.
+__device__ __forceinline__ float max_xor16(float x)
+{
+    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+                                                    false, false);
+    // (elements copied out before the bit cast: hipcc's __builtin_bit_cast
+    // of a vector element reads element 0 whatever the index)
+    const uint32_t r0 = r[0], r1 = r[1];
+    return fmaxf(__builtin_bit_cast(float, r0), __builtin_bit_cast(float, r1));
+}
+__device__ __forceinline__ float max_xor32(float x)
+{
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+                                                    false, false);
+    const uint32_t r0 = r[0], r1 = r[1];
+    return fmaxf(__builtin_bit_cast(float, r0), __builtin_bit_cast(float, r1));
+}
+
+// -1.0f in a register the optimiser cannot see through, so that x - hi
+// (hi a half) is selected as one mixed-precision multiply-add reading the
+// half in place, not as a conversion and a subtraction.
+__device__ __forceinline__ float opaque_neg1()
+{
+    float v;
+    asm volatile("" : "=s"(v) : "0"(-1.0f));
+    return v;
+}
+
 // Eight int8 codes -> eight exact fp16 values: (x ^ 0x80) is x + 128 as an
 // unsigned byte, 0x64 above it makes the half 1024 + x + 128, and the bias
 // 1152 is subtracted.

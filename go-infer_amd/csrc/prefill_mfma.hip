@@ -60,15 +60,17 @@ __device__ __forceinline__ void split_hilo(float x, _Float16 &hi, _Float16 &lo)
 // the very value lo was computed against (with floating-point contraction a
 // plain (_Float16)x can be evaluated twice with different roundings when x is
 // a product, and the halves then no longer sum to x).
-__device__ __forceinline__ void split8(const float *x, h8 &hi, h8 &lo)
+// neg1 is -1 (mfma_ops::opaque_neg1), so that each remainder x - hi is one
+// mixed-precision multiply-add reading hi in place.
+__device__ __forceinline__ void split8(const float *x, h8 &hi, h8 &lo, float neg1)
 {
 #pragma unroll
     for (int k = 0; k < 4; k++) {
         const h2 h = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(x[2 * k], x[2 * k + 1]));
         hi[2 * k] = h[0];
         hi[2 * k + 1] = h[1];
-        lo[2 * k] = (_Float16)(x[2 * k] - (float)h[0]);
-        lo[2 * k + 1] = (_Float16)(x[2 * k + 1] - (float)h[1]);
+        lo[2 * k] = (_Float16)fmaf((float)h[0], neg1, x[2 * k]);
+        lo[2 * k + 1] = (_Float16)fmaf((float)h[1], neg1, x[2 * k + 1]);
     }
 }
 
@@ -363,7 +365,7 @@ __global__ __launch_bounds__(256) void attn_prefill(PrefillArgs a)
                     for (int i = 0; i < 8; i++)
                         x[i] = p[i] * vsc[db][i];
                     h8 ph, pl;
-                    split8(x, ph, pl);
+                    split8(x, ph, pl, mfma_ops::opaque_neg1());
 #pragma unroll
                     for (int h = 0; h < 2; h++) {
                         o[cg][2 * db + h] = mfma(ph, vv[2 * db + h], o[cg][2 * db + h]);
@@ -849,6 +851,7 @@ struct WaveAttn {
     h8 qh[NCG][KK], ql[NCG][KK];
     float c2s[NCG], m2[NCG], lsum[NCG];
     float kinv = 1.0f; // f32 pages: 1 / the current block's K operand scale
+    float neg1;        // -1, opaque to the optimiser (split8)
     f4 o[NCG][NB];
     int qlen[NCG];
 
@@ -858,6 +861,7 @@ struct WaveAttn {
                                          int mapped, bool active, int j, int g)
     {
         const int H = a.num_heads, G = H / a.L.num_kv_heads, chunk = a.chunk_len;
+        neg1 = mfma_ops::opaque_neg1();
 #pragma unroll
         for (int cg = 0; cg < NCG; cg++) {
             const int c = col0 + 16 * cg + j;
@@ -890,7 +894,7 @@ struct WaveAttn {
                     x[v] = x0[v] * up;
                     x[4 + v] = x1[v] * up;
                 }
-                split8(x, qh[cg][kk], ql[cg][kk]);
+                split8(x, qh[cg][kk], ql[cg][kk], neg1);
             }
             m2[cg] = -INFINITY;
             lsum[cg] = 0.0f;
@@ -926,8 +930,7 @@ struct WaveAttn {
 #pragma unroll
         for (int i = 1; i < 16; i++)
             mx = fmaxf(mx, sv[i]);
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        mx = mfma_ops::max_xor32(mfma_ops::max_xor16(mx));
         mx *= c2s[cg] * kinv;
         const bool grow = mx > m2[cg] + kLazy;
         const float mref = grow ? mx : m2[cg];
@@ -942,8 +945,8 @@ struct WaveAttn {
             ps += p[i];
         }
         lsum[cg] = lsum[cg] * alpha + ps;
-        split8(&p[0], ph0, pl0);
-        split8(&p[8], ph1, pl1);
+        split8(&p[0], ph0, pl0, neg1);
+        split8(&p[8], ph1, pl1, neg1);
         return __any(grow);
     }
 
