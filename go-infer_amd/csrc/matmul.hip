@@ -7,14 +7,23 @@
 //                                            pkg/metal/metal_darwin.go:849-880)
 //
 // Weights are converted once (gi_weights_upload) from their GGUF layout into
-// one laid out for 16-byte operand loads:
-//   F16   fp16 [rows][cols] as stored;
-//   F32   two fp16 arrays, hi and lo, of W * 2^e[r] (e[r] from the row's
-//         largest |w|, so both halves stay normal), and 2^-e[r] per row;
-//   Q8_0  int8 codes [rows][cols] and fp16 block scales [cols/32][rows];
-//   Q4_0  the 16 nibble bytes of each block [rows][cols/32][16] (byte j holds
-//         elements j and j+16, quant.go:504) and the scales as Q8_0.
-// (GGUF's 34- and 18-byte blocks are not 16-byte aligned.)
+// operand order, and activations are split into it on every call, so that
+// each 16-byte operand load of a wave reads one contiguous 1 KiB run (a
+// row-major load would send every quarter-wave to 16 rows, and the L1 tag
+// rate -- one line per lane -- bounds that form):
+//   16-bit matrices (F16 weights, the F32 weight halves, the activation
+//   halves): the 16 x 32 tile (rows 16t.., columns 32kk..) is 512 elements
+//   in lane order, lane 16 * ((c / 8) % 4) + r % 16 holding columns
+//   8 ((c / 8) % 4) .. +7 of its row (op_index);
+//   Q8_0  int8 codes in the same order (512 bytes per tile), fp16 block
+//         scales [cols/32][rows64];
+//   Q4_0  per tile and block, the 16 nibble bytes of each of the 16 rows
+//         (byte j holds elements j and j+16, quant.go:504), 256 bytes;
+//         scales as Q8_0;
+//   F32   two fp16 halves, hi and lo, of W * 2^e[r] (e[r] from the row's
+//         largest |w|, so both halves stay normal), and 2^-e[r] per row.
+// Rows of weights and activations are padded with zeros to multiples of 64,
+// the output tile, so the product loop needs no bounds checks.
 //
 // Activations are split per batch row into fp16 hi + lo of x * 2^e[b], so the
 // products keep float32 accuracy.  The matrix cores then compute W * x^T on
@@ -26,8 +35,8 @@
 //
 // A workgroup owns a 64 x 64 (rows x batch) output tile.  Its four waves take
 // every fourth k-step each; waves 1-3 leave their partial tiles in LDS and
-// wave 0 adds them to its own, so one launch of (batch/64) x (rows/64)
-// workgroups covers the product with no global reduction.
+// wave 0 adds them to its own, so one launch covers the product with no
+// global reduction.
 #include "../../include/goinfer_paged.h"
 #include "gi_common.h"
 #include "gi_host.h"
@@ -51,34 +60,78 @@ using mfma_ops::u4x8_to_h8;
 
 enum : int { W_F32 = 0, W_F16 = 1, W_Q4_0 = 2, W_Q8_0 = 8 }; // GGML type ids
 
+__host__ __device__ __forceinline__ int64_t round64(int64_t n) { return (n + 63) / 64 * 64; }
+
+// Element (r, c) of a 16-bit matrix (or an int8 code matrix) with KS
+// k-steps of 32 columns, in operand order.
+__host__ __device__ __forceinline__ int64_t op_index(int64_t r, int c, int KS)
+{
+    return (((r >> 4) * KS + (c >> 5)) * 64 + 16 * ((c >> 3) & 3) + (r & 15)) * 8 + (c & 7);
+}
+
+// Byte i of row r's Q4_0 block kk.
+__host__ __device__ __forceinline__ int64_t q4_index(int64_t r, int kk, int i, int KS)
+{
+    return (((r >> 4) * KS + kk) * 16 + (r & 15)) * 16 + i;
+}
+
 // ---- conversion of GGUF weights into the operand layout ------------------
 
-// Q8_0 / Q4_0: one thread per (row, block); raw blocks are byte-addressed.
+// Q8_0 / Q4_0: one thread per (row, block) of the padded rows; raw blocks
+// are byte-addressed.
 __global__ __launch_bounds__(256) void convert_quant(const uint8_t *__restrict__ raw, int type, int rows,
-                                                    int cols, uint8_t *__restrict__ codes,
+                                                    int rows64, int cols, uint8_t *__restrict__ codes,
                                                     uint16_t *__restrict__ scales)
 {
     const int nb = cols / 32;
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= (int64_t)rows * nb)
+    if (i >= (int64_t)rows64 * nb)
         return;
     const int r = (int)(i / nb), kb = (int)(i - (int64_t)r * nb);
+    const bool live = r < rows;
     const int bb = type == W_Q8_0 ? 34 : 18;
-    const uint8_t *blk = raw + i * bb;
-    scales[(int64_t)kb * rows + r] = (uint16_t)(blk[0] | (blk[1] << 8));
-    const int n = type == W_Q8_0 ? 32 : 16;
-    uint8_t *dst = codes + i * n; // [rows][cols] int8, or [rows][nb][16]
-    for (int j = 0; j < n; j++)
-        dst[j] = blk[2 + j];
+    const uint8_t *blk = raw + (live ? i : 0) * bb;
+    scales[(int64_t)kb * rows64 + r] = live ? (uint16_t)(blk[0] | (blk[1] << 8)) : 0;
+    if (type == W_Q8_0) {
+        for (int j = 0; j < 32; j++)
+            codes[op_index(r, 32 * kb + j, nb)] = live ? blk[2 + j] : 0;
+    } else {
+        for (int j = 0; j < 16; j++)
+            codes[q4_index(r, kb, j, nb)] = live ? blk[2 + j] : 0x88; // padded rows: codes 8 (zero)
+    }
 }
 
-// F32: one workgroup per row; W * 2^e split into hi + lo fp16.
-__global__ __launch_bounds__(256) void convert_f32(const float *__restrict__ raw, int cols,
+// F16: one thread per 8 consecutive elements of the padded rows.
+__global__ __launch_bounds__(256) void convert_f16(const uint16_t *__restrict__ raw, int rows, int rows64, int cols,
+                                                  uint16_t *__restrict__ dst)
+{
+    const int per = cols / 8;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)rows64 * per)
+        return;
+    const int r = (int)(i / per), c = 8 * (int)(i - (int64_t)r * per);
+    uint4 v = {0u, 0u, 0u, 0u};
+    if (r < rows)
+        v = *reinterpret_cast<const uint4 *>(raw + (int64_t)r * cols + c);
+    *reinterpret_cast<uint4 *>(dst + op_index(r, c, cols / 32)) = v;
+}
+
+// F32: one workgroup per padded row; W * 2^e split into hi + lo fp16.
+__global__ __launch_bounds__(256) void convert_f32(const float *__restrict__ raw, int rows, int cols,
                                                   _Float16 *__restrict__ hi, _Float16 *__restrict__ lo,
                                                   float *__restrict__ row_scale)
 {
     __shared__ float s_max[256];
-    const int r = blockIdx.x;
+    const int r = blockIdx.x, KS = cols / 32;
+    if (r >= rows) {
+        for (int c = threadIdx.x; c < cols; c += 256) {
+            hi[op_index(r, c, KS)] = (_Float16)0.0f;
+            lo[op_index(r, c, KS)] = (_Float16)0.0f;
+        }
+        if (threadIdx.x == 0)
+            row_scale[r] = 0.0f;
+        return;
+    }
     const float *w = raw + (int64_t)r * cols;
     float m = 0.0f;
     for (int c = threadIdx.x; c < cols; c += 256)
@@ -95,8 +148,8 @@ __global__ __launch_bounds__(256) void convert_f32(const float *__restrict__ raw
     for (int c = threadIdx.x; c < cols; c += 256) {
         const float x = w[c] * up; // exact: a power of two
         const _Float16 h = (_Float16)x;
-        hi[(int64_t)r * cols + c] = h;
-        lo[(int64_t)r * cols + c] = (_Float16)(x - (float)h);
+        hi[op_index(r, c, KS)] = h;
+        lo[op_index(r, c, KS)] = (_Float16)(x - (float)h);
     }
     if (threadIdx.x == 0)
         row_scale[r] = ldexpf(1.0f, -e);
@@ -104,11 +157,20 @@ __global__ __launch_bounds__(256) void convert_f32(const float *__restrict__ raw
 
 // ---- activations: x * 2^e split into hi + lo per batch row ---------------
 
-__global__ __launch_bounds__(256) void split_rows(const float *__restrict__ x, int cols, _Float16 *__restrict__ xh,
-                                                 _Float16 *__restrict__ xl, float *__restrict__ xscale)
+// One workgroup per padded batch row (rows past the batch are zeros).
+__global__ __launch_bounds__(256) void split_rows(const float *__restrict__ x, int batch, int cols,
+                                                 _Float16 *__restrict__ xh, _Float16 *__restrict__ xl,
+                                                 float *__restrict__ xscale)
 {
     __shared__ float s_max[256];
-    const int b = blockIdx.x;
+    const int b = blockIdx.x, KS = cols / 32;
+    if (b >= batch) {
+        for (int c = threadIdx.x; c < cols; c += 256) {
+            xh[op_index(b, c, KS)] = (_Float16)0.0f;
+            xl[op_index(b, c, KS)] = (_Float16)0.0f;
+        }
+        return;
+    }
     const float *xr = x + (int64_t)b * cols;
     float m = 0.0f;
     for (int c = threadIdx.x; c < cols; c += 256)
@@ -125,8 +187,8 @@ __global__ __launch_bounds__(256) void split_rows(const float *__restrict__ x, i
     for (int c = threadIdx.x; c < cols; c += 256) {
         const float v = xr[c] * up; // exact: a power of two
         const _Float16 h = (_Float16)v;
-        xh[(int64_t)b * cols + c] = h;
-        xl[(int64_t)b * cols + c] = (_Float16)(v - (float)h);
+        xh[op_index(b, c, KS)] = h;
+        xl[op_index(b, c, KS)] = (_Float16)(v - (float)h);
     }
     if (threadIdx.x == 0)
         xscale[b] = ldexpf(1.0f, -e);
@@ -137,6 +199,7 @@ __global__ __launch_bounds__(256) void split_rows(const float *__restrict__ x, i
 struct MatArgs {
     int type;
     int rows, cols, batch;
+    int rows64;             // rows padded to the output tile
     const uint8_t *a;      // F16 / F32-hi / Q8 codes / Q4 nibble bytes
     const uint8_t *a_lo;   // F32 lo
     const uint16_t *scales; // Q8 / Q4 block scales [cols/32][rows]
@@ -156,7 +219,8 @@ __device__ __forceinline__ h8 ld_h8(const void *p)
 
 // Workgroup: 4 waves, output tile rows [r0, r0+64) x batch [b0, b0+64).
 // Wave w takes k-steps w, w+4, ...; lane (j, g) of row tile rs holds output
-// rows 16*rs + 4g + i (i < 4), batch column 16*bs + j.
+// rows 16*rs + 4g + i (i < 4), batch column 16*bs + j.  Every operand load
+// is one 1 KiB run of the operand-order layouts.
 template <int WT>
 __global__ __launch_bounds__(256) void matmul_tile(MatArgs a)
 {
@@ -171,71 +235,79 @@ __global__ __launch_bounds__(256) void matmul_tile(MatArgs a)
 #pragma unroll
         for (int bs = 0; bs < 4; bs++)
             acc[rs][bs] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-    // A rows of this lane (clamped: rows past the end are computed and not stored)
-    int64_t arow[4];
-#pragma unroll
-    for (int rs = 0; rs < 4; rs++)
-        arow[rs] = min(r0 + 16 * rs + j, R - 1);
-    // B columns: batch rows (past the end: zero operands)
-    bool bvalid[4];
-    int64_t brow[4];
-#pragma unroll
-    for (int bs = 0; bs < 4; bs++) {
-        const int b = b0 + 16 * bs + j;
-        bvalid[bs] = b < a.batch;
-        brow[bs] = bvalid[bs] ? b : 0;
-    }
-    const h8 zero8 = {};
-    for (int kk = w; kk < KS; kk += 4) {
-        const int c0 = 32 * kk + 8 * g;
+    // 16-row tiles of this workgroup's weight rows and batch rows
+    const int64_t rt0 = r0 / 16, bt0 = b0 / 16;
+    // One k-step's operands; the next k-step's are loaded while this one's
+    // products run (the last iteration reloads an in-range step, unused).
+    struct Step {
         h8 bh[4], bl[4];
+        h8 ah[4], al[4]; // F16 / F32
+        u2 aq[4], sc[4]; // Q8_0 / Q4_0 codes and the scales of rows 16rs + 4g .. + 3
+    };
+    auto load = [&](int kk, Step &S) {
 #pragma unroll
         for (int bs = 0; bs < 4; bs++) {
-            bh[bs] = bvalid[bs] ? ld_h8<false>(a.xh + brow[bs] * C + c0) : zero8;
-            bl[bs] = bvalid[bs] ? ld_h8<false>(a.xl + brow[bs] * C + c0) : zero8;
+            const int64_t o = (((bt0 + bs) * KS + kk) * 64 + lane) * 8;
+            S.bh[bs] = ld_h8<false>(a.xh + o);
+            S.bl[bs] = ld_h8<false>(a.xl + o);
         }
 #pragma unroll
         for (int rs = 0; rs < 4; rs++) {
+            const int64_t t = (rt0 + rs) * KS + kk; // the (row tile, k-step) tile
             if (WT == W_F16 || WT == W_F32) {
-                const h8 ah = ld_h8<true>(a.a + (arow[rs] * C + c0) * 2);
-                h8 al = {};
+                S.ah[rs] = ld_h8<true>(a.a + (t * 64 + lane) * 16);
                 if (WT == W_F32)
-                    al = ld_h8<true>(a.a_lo + (arow[rs] * C + c0) * 2);
+                    S.al[rs] = ld_h8<true>(a.a_lo + (t * 64 + lane) * 16);
+            } else {
+                // Q4_0: dims 8g..8g+7 of the block are the low (g < 2) or
+                // high nibbles of bytes 8*(g%2) .. +7
+                S.aq[rs] = WT == W_Q8_0 ? *reinterpret_cast<const u2 *>(a.a + (t * 64 + lane) * 8)
+                                        : *reinterpret_cast<const u2 *>(a.a + (t * 16 + j) * 16 + 8 * (g & 1));
+                S.sc[rs] = *reinterpret_cast<const u2 *>(a.scales + (int64_t)kk * a.rows64 + r0 + 16 * rs + 4 * g);
+            }
+        }
+    };
+    auto compute = [&](const Step &S) {
+#pragma unroll
+        for (int rs = 0; rs < 4; rs++) {
+            if (WT == W_F16 || WT == W_F32) {
 #pragma unroll
                 for (int bs = 0; bs < 4; bs++) {
-                    acc[rs][bs] = mfma16(ah, bh[bs], acc[rs][bs]);
-                    acc[rs][bs] = mfma16(ah, bl[bs], acc[rs][bs]);
+                    acc[rs][bs] = mfma16(S.ah[rs], S.bh[bs], acc[rs][bs]);
+                    acc[rs][bs] = mfma16(S.ah[rs], S.bl[bs], acc[rs][bs]);
                     if (WT == W_F32)
-                        acc[rs][bs] = mfma16(al, bh[bs], acc[rs][bs]);
+                        acc[rs][bs] = mfma16(S.al[rs], S.bh[bs], acc[rs][bs]);
                 }
             } else {
-                h8 aq;
-                if (WT == W_Q8_0) {
-                    aq = i8x8_to_h8(*reinterpret_cast<const u2 *>(a.a + arow[rs] * C + c0));
-                } else {
-                    // dims 8g..8g+7 of the block: low (g < 2) or high nibbles
-                    // of bytes 8*(g%2) .. +7
-                    const u2 wq = *reinterpret_cast<const u2 *>(a.a + (arow[rs] * KS + kk) * 16 + 8 * (g & 1));
-                    aq = u4x8_to_h8(wq, (g & 2) ? 4 : 0);
-                }
-                // scales of output rows 16rs + 4g + i, i < 4 (rows past the
-                // end read row R-1's)
+                const h8 aq = WT == W_Q8_0 ? i8x8_to_h8(S.aq[rs]) : u4x8_to_h8(S.aq[rs], (g & 2) ? 4 : 0);
+                // (words copied out before the bit casts)
+                const uint32_t s01 = S.sc[rs].x, s23 = S.sc[rs].y;
                 float d[4];
-                const int rb = r0 + 16 * rs + 4 * g;
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const uint16_t hb = a.scales[(int64_t)kk * R + min(rb + i, R - 1)];
-                    d[i] = (float)__builtin_bit_cast(_Float16, hb);
-                }
+                d[0] = (float)__builtin_bit_cast(_Float16, (uint16_t)(s01 & 0xFFFFu));
+                d[1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(s01 >> 16));
+                d[2] = (float)__builtin_bit_cast(_Float16, (uint16_t)(s23 & 0xFFFFu));
+                d[3] = (float)__builtin_bit_cast(_Float16, (uint16_t)(s23 >> 16));
 #pragma unroll
                 for (int bs = 0; bs < 4; bs++) {
-                    f4 z = mfma16(aq, bh[bs], f4{0.0f, 0.0f, 0.0f, 0.0f});
-                    z = mfma16(aq, bl[bs], z);
+                    f4 z = mfma16(aq, S.bh[bs], f4{0.0f, 0.0f, 0.0f, 0.0f});
+                    z = mfma16(aq, S.bl[bs], z);
 #pragma unroll
                     for (int i = 0; i < 4; i++)
                         acc[rs][bs][i] = fmaf(z[i], d[i], acc[rs][bs][i]);
                 }
             }
+        }
+    };
+    if (w < KS) {
+        Step cur, nxt;
+        load(w, cur);
+        for (int kk = w; kk < KS; kk += 4) {
+            load(min(kk + 4, KS - 1), nxt);
+            // keeps the scheduler from sinking those loads to their use in
+            // the next iteration
+            __builtin_amdgcn_sched_barrier(0);
+            compute(cur);
+            cur = nxt;
         }
     }
     if (w > 0) {
@@ -326,43 +398,47 @@ int gi_weights_upload(gi_paged *h, int ggml_type, int rows, int cols, const void
         if (rc == GI_OK)
             rc = gi_dev_alloc(h, n, dst);
     };
-    if (ggml_type == W_F16) {
-        alloc((size_t)raw_bytes, &p);
-        wt->a = (uint8_t *)p;
-        if (rc == GI_OK)
-            rc = gi_memcpy_h2d(h, wt->a, raw, (size_t)raw_bytes);
-    } else {
+    const int64_t rows64 = round64(rows);
+    {
         alloc((size_t)raw_bytes, &tmp);
         if (rc == GI_OK)
             rc = gi_memcpy_h2d(h, tmp, raw, (size_t)raw_bytes);
-        if (ggml_type == W_F32) {
-            alloc((size_t)rows * cols * 2, &p);
+        hipError_t e = hipSuccess;
+        if (ggml_type == W_F16) {
+            alloc((size_t)rows64 * cols * 2, &p);
             wt->a = (uint8_t *)p;
-            alloc((size_t)rows * cols * 2, &p);
+            if (rc == GI_OK) {
+                const int64_t n = rows64 * (cols / 8);
+                hipLaunchKernelGGL(convert_f16, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                                   (const uint16_t *)tmp, rows, (int)rows64, cols, (uint16_t *)wt->a);
+                e = hipGetLastError();
+            }
+        } else if (ggml_type == W_F32) {
+            alloc((size_t)rows64 * cols * 2, &p);
+            wt->a = (uint8_t *)p;
+            alloc((size_t)rows64 * cols * 2, &p);
             wt->a_lo = (uint8_t *)p;
-            alloc((size_t)rows * 4, &p);
+            alloc((size_t)rows64 * 4, &p);
             wt->row_scale = (float *)p;
             if (rc == GI_OK) {
-                hipLaunchKernelGGL(convert_f32, dim3((unsigned)rows), dim3(256), 0, st, (const float *)tmp, cols,
-                                   (_Float16 *)wt->a, (_Float16 *)wt->a_lo, wt->row_scale);
-                hipError_t e = hipGetLastError();
-                if (e != hipSuccess)
-                    rc = hip_fail(e, "gi_weights_upload");
+                hipLaunchKernelGGL(convert_f32, dim3((unsigned)rows64), dim3(256), 0, st, (const float *)tmp, rows,
+                                   cols, (_Float16 *)wt->a, (_Float16 *)wt->a_lo, wt->row_scale);
+                e = hipGetLastError();
             }
         } else {
-            alloc((size_t)rows * (ggml_type == W_Q8_0 ? cols : cols / 2), &p);
+            alloc((size_t)rows64 * (ggml_type == W_Q8_0 ? cols : cols / 2), &p);
             wt->a = (uint8_t *)p;
-            alloc((size_t)rows * nb * 2, &p);
+            alloc((size_t)rows64 * nb * 2, &p);
             wt->scales = (uint16_t *)p;
             if (rc == GI_OK) {
-                const int64_t n = (int64_t)rows * nb;
+                const int64_t n = rows64 * nb;
                 hipLaunchKernelGGL(convert_quant, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
-                                   (const uint8_t *)tmp, ggml_type, rows, cols, wt->a, wt->scales);
-                hipError_t e = hipGetLastError();
-                if (e != hipSuccess)
-                    rc = hip_fail(e, "gi_weights_upload");
+                                   (const uint8_t *)tmp, ggml_type, rows, (int)rows64, cols, wt->a, wt->scales);
+                e = hipGetLastError();
             }
         }
+        if (e != hipSuccess && rc == GI_OK)
+            rc = hip_fail(e, "gi_weights_upload");
         if (tmp) {
             const int rc2 = gi_dev_free(h, tmp); // waits for the conversion
             if (rc == GI_OK)
@@ -402,7 +478,8 @@ int gi_matmul_batch(gi_weights *w, int batch, const float *x, float *y)
     if (batch == 0)
         return GI_OK;
     gi_paged *h = w->h;
-    if (batch > w->x_cap) {
+    const int batch64 = (int)round64(batch); // activation rows, zero-padded to the output tile
+    if (batch64 > w->x_cap) {
         for (void *p : {(void *)w->xh, (void *)w->xl, (void *)w->xscale})
             if (p)
                 (void)gi_dev_free(h, p); // waits for queued work that reads them
@@ -410,22 +487,24 @@ int gi_matmul_batch(gi_weights *w, int batch, const float *x, float *y)
         w->xscale = nullptr;
         w->x_cap = 0;
         void *p = nullptr;
-        const size_t nx = (size_t)batch * w->cols * 2;
+        const size_t nx = (size_t)batch64 * w->cols * 2;
         int rc = gi_dev_alloc(h, nx, &p);
         w->xh = (_Float16 *)p;
         if (rc == GI_OK && (rc = gi_dev_alloc(h, nx, &p)) == GI_OK)
             w->xl = (_Float16 *)p;
-        if (rc == GI_OK && (rc = gi_dev_alloc(h, (size_t)batch * 4, &p)) == GI_OK)
+        if (rc == GI_OK && (rc = gi_dev_alloc(h, (size_t)batch64 * 4, &p)) == GI_OK)
             w->xscale = (float *)p;
         if (rc != GI_OK)
             return rc;
-        w->x_cap = batch;
+        w->x_cap = batch64;
     }
     hipStream_t st = (hipStream_t)gi_paged_stream(h);
-    hipLaunchKernelGGL(split_rows, dim3((unsigned)batch), dim3(256), 0, st, x, w->cols, w->xh, w->xl, w->xscale);
+    hipLaunchKernelGGL(split_rows, dim3((unsigned)batch64), dim3(256), 0, st, x, batch, w->cols, w->xh, w->xl,
+                       w->xscale);
     MatArgs a{};
     a.type = w->type;
     a.rows = w->rows;
+    a.rows64 = (int)round64(w->rows);
     a.cols = w->cols;
     a.batch = batch;
     a.a = w->a;
@@ -436,7 +515,7 @@ int gi_matmul_batch(gi_weights *w, int batch, const float *x, float *y)
     a.xl = w->xl;
     a.xscale = w->xscale;
     a.y = y;
-    dim3 grid((unsigned)((batch + 63) / 64), (unsigned)((w->rows + 63) / 64));
+    dim3 grid((unsigned)(batch64 / 64), (unsigned)(a.rows64 / 64));
     switch (w->type) {
     case W_F32: hipLaunchKernelGGL(matmul_tile<W_F32>, grid, dim3(256), 0, st, a); break;
     case W_F16: hipLaunchKernelGGL(matmul_tile<W_F16>, grid, dim3(256), 0, st, a); break;
