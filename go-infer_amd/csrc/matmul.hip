@@ -34,9 +34,11 @@
 // lo*hi).
 //
 // A workgroup owns a 64 x 64 (rows x batch) output tile.  Its four waves take
-// every fourth k-step each; waves 1-3 leave their partial tiles in LDS and
-// wave 0 adds them to its own, so one launch covers the product with no
-// global reduction.
+// every fourth k-step each, and each wave streams its k-steps through its own
+// LDS stages by direct global->LDS loads, two steps ahead (one for F32,
+// whose stages are twice as large).  Waves 1-3 then leave their partial tiles
+// in LDS and wave 0 adds them to its own, so one launch covers the product
+// with no global reduction.
 #include "../../include/goinfer_paged.h"
 #include "gi_common.h"
 #include "gi_host.h"
@@ -59,6 +61,7 @@ using mfma_ops::u2;
 using mfma_ops::u4x8_to_h8;
 
 enum : int { W_F32 = 0, W_F16 = 1, W_Q4_0 = 2, W_Q8_0 = 8 }; // GGML type ids
+
 
 __host__ __device__ __forceinline__ int64_t round64(int64_t n) { return (n + 63) / 64 * 64; }
 
@@ -202,114 +205,140 @@ struct MatArgs {
     int rows64;             // rows padded to the output tile
     const uint8_t *a;      // F16 / F32-hi / Q8 codes / Q4 nibble bytes
     const uint8_t *a_lo;   // F32 lo
-    const uint16_t *scales; // Q8 / Q4 block scales [cols/32][rows]
+    const uint16_t *scales; // Q8 / Q4 block scales [cols/32][rows64]
     const float *row_scale; // F32
     const _Float16 *xh, *xl;
     const float *xscale;
     float *y;
 };
 
-template <bool NT>
-__device__ __forceinline__ h8 ld_h8(const void *p)
-{
-    if (NT)
-        return __builtin_nontemporal_load(reinterpret_cast<const h8 *>(p));
-    return *reinterpret_cast<const h8 *>(p);
-}
-
-// Workgroup: 4 waves, output tile rows [r0, r0+64) x batch [b0, b0+64).
-// Wave w takes k-steps w, w+4, ...; lane (j, g) of row tile rs holds output
-// rows 16*rs + 4g + i (i < 4), batch column 16*bs + j.  Every operand load
-// is one 1 KiB run of the operand-order layouts.
+// One wave's operands of one k-step, as the direct loads lay them down: the
+// four batch tiles' hi and lo halves (1 KiB each), the four weight tiles
+// (F16 1 KiB, F32 hi then lo, Q8_0 512 B, Q4_0 256 B), and for Q8_0 / Q4_0
+// the 64 rows' block scales.
 template <int WT>
-__global__ __launch_bounds__(256) void matmul_tile(MatArgs a)
+struct MStage {
+    static constexpr int XB = 8 * 1024;
+    static constexpr int WB = WT == W_F32 ? 8192 : WT == W_F16 ? 4096 : WT == W_Q8_0 ? 2048 : 1024;
+    static constexpr int SB = (WT == W_Q8_0 || WT == W_Q4_0) ? 128 : 0;
+    static constexpr int BYTES = XB + WB + SB;
+    // direct loads per k-step: 8 activation tiles, the weight tiles, the scales
+    static constexpr int NL = 8 + (WT == W_F32 ? 8 : 4) + (SB ? 1 : 0);
+};
+
+typedef __attribute__((address_space(3))) void *lds_void;
+
+template <int WT, int NST>
+__global__ __launch_bounds__(256) void matmul_lds(MatArgs a)
 {
-    __shared__ float s_acc[3][64][65]; // waves 1..3; wave 0 folds them in
+    typedef MStage<WT> M;
+    constexpr int STAGE_ALL = 4 * NST * M::BYTES, ACC = 3 * 64 * 65 * 4;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[STAGE_ALL > ACC ? STAGE_ALL : ACC];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int j = lane & 15, g = lane >> 4;
     const int b0 = blockIdx.x * 64, r0 = blockIdx.y * 64;
     const int C = a.cols, R = a.rows, KS = C / 32;
+    const int64_t rt0 = r0 / 16, bt0 = b0 / 16;
     f4 acc[4][4];
 #pragma unroll
     for (int rs = 0; rs < 4; rs++)
 #pragma unroll
         for (int bs = 0; bs < 4; bs++)
             acc[rs][bs] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-    // 16-row tiles of this workgroup's weight rows and batch rows
-    const int64_t rt0 = r0 / 16, bt0 = b0 / 16;
-    // One k-step's operands; the next k-step's are loaded while this one's
-    // products run (the last iteration reloads an in-range step, unused).
-    struct Step {
-        h8 bh[4], bl[4];
-        h8 ah[4], al[4]; // F16 / F32
-        u2 aq[4], sc[4]; // Q8_0 / Q4_0 codes and the scales of rows 16rs + 4g .. + 3
-    };
-    auto load = [&](int kk, Step &S) {
+    uint8_t *mine = smem + w * NST * M::BYTES;
+    // This wave's k-steps are w, w + 4, ...: nk of them.
+    const int nk = w < KS ? (KS - w + 3) / 4 : 0;
+    // The NL direct loads of this wave's i-th k-step (clamped to its last,
+    // so every call issues the same number of loads) into stage st.
+    auto issue = [&](int i, int st) {
+        const int kk = w + 4 * min(i, nk - 1);
+        uint8_t *d = mine + st * M::BYTES;
 #pragma unroll
         for (int bs = 0; bs < 4; bs++) {
             const int64_t o = (((bt0 + bs) * KS + kk) * 64 + lane) * 8;
-            S.bh[bs] = ld_h8<false>(a.xh + o);
-            S.bl[bs] = ld_h8<false>(a.xl + o);
+            __builtin_amdgcn_global_load_lds(a.xh + o, (lds_void)(d + 2048 * bs), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(a.xl + o, (lds_void)(d + 2048 * bs + 1024), 16, 0, 0);
         }
+        d += M::XB;
 #pragma unroll
         for (int rs = 0; rs < 4; rs++) {
-            const int64_t t = (rt0 + rs) * KS + kk; // the (row tile, k-step) tile
+            const int64_t t = (rt0 + rs) * KS + kk;
             if (WT == W_F16 || WT == W_F32) {
-                S.ah[rs] = ld_h8<true>(a.a + (t * 64 + lane) * 16);
+                __builtin_amdgcn_global_load_lds(a.a + t * 1024 + 16 * lane, (lds_void)(d + 1024 * rs), 16, 0, 0);
                 if (WT == W_F32)
-                    S.al[rs] = ld_h8<true>(a.a_lo + (t * 64 + lane) * 16);
+                    __builtin_amdgcn_global_load_lds(a.a_lo + t * 1024 + 16 * lane, (lds_void)(d + 4096 + 1024 * rs),
+                                                     16, 0, 0);
             } else {
-                // Q4_0: dims 8g..8g+7 of the block are the low (g < 2) or
-                // high nibbles of bytes 8*(g%2) .. +7
-                S.aq[rs] = WT == W_Q8_0 ? *reinterpret_cast<const u2 *>(a.a + (t * 64 + lane) * 8)
-                                        : *reinterpret_cast<const u2 *>(a.a + (t * 16 + j) * 16 + 8 * (g & 1));
-                S.sc[rs] = *reinterpret_cast<const u2 *>(a.scales + (int64_t)kk * a.rows64 + r0 + 16 * rs + 4 * g);
+                constexpr int TB = WT == W_Q8_0 ? 512 : 256; // bytes of one weight tile
+                if (lane < TB / 16)
+                    __builtin_amdgcn_global_load_lds(a.a + t * TB + 16 * lane, (lds_void)(d + TB * rs), 16, 0, 0);
             }
         }
+        if (M::SB && lane < 8)
+            __builtin_amdgcn_global_load_lds(a.scales + (int64_t)kk * a.rows64 + r0 + 8 * lane,
+                                             (lds_void)(d + M::WB), 16, 0, 0);
     };
-    auto compute = [&](const Step &S) {
+    if (nk > 0) {
 #pragma unroll
-        for (int rs = 0; rs < 4; rs++) {
-            if (WT == W_F16 || WT == W_F32) {
+        for (int i = 0; i < NST - 1; i++)
+            issue(i, i);
+        for (int i = 0; i < nk; i++) {
+            issue(i + NST - 1, (i + NST - 1) % NST);
+            // this k-step's loads are done once no more than the later
+            // stages' remain in flight
+            constexpr int VM = (NST - 1) * M::NL;
+            __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | (7 << 4) | (15 << 8));
+            const uint8_t *sp = mine + (i % NST) * M::BYTES;
+            h8 bh[4], bl[4];
 #pragma unroll
-                for (int bs = 0; bs < 4; bs++) {
-                    acc[rs][bs] = mfma16(S.ah[rs], S.bh[bs], acc[rs][bs]);
-                    acc[rs][bs] = mfma16(S.ah[rs], S.bl[bs], acc[rs][bs]);
+            for (int bs = 0; bs < 4; bs++) {
+                bh[bs] = *reinterpret_cast<const h8 *>(sp + 2048 * bs + 16 * lane);
+                bl[bs] = *reinterpret_cast<const h8 *>(sp + 2048 * bs + 1024 + 16 * lane);
+            }
+            const uint8_t *wp = sp + M::XB;
+#pragma unroll
+            for (int rs = 0; rs < 4; rs++) {
+                if (WT == W_F16 || WT == W_F32) {
+                    const h8 ah = *reinterpret_cast<const h8 *>(wp + 1024 * rs + 16 * lane);
+                    h8 al = {};
                     if (WT == W_F32)
-                        acc[rs][bs] = mfma16(S.al[rs], S.bh[bs], acc[rs][bs]);
-                }
-            } else {
-                const h8 aq = WT == W_Q8_0 ? i8x8_to_h8(S.aq[rs]) : u4x8_to_h8(S.aq[rs], (g & 2) ? 4 : 0);
-                // (words copied out before the bit casts)
-                const uint32_t s01 = S.sc[rs].x, s23 = S.sc[rs].y;
-                float d[4];
-                d[0] = (float)__builtin_bit_cast(_Float16, (uint16_t)(s01 & 0xFFFFu));
-                d[1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(s01 >> 16));
-                d[2] = (float)__builtin_bit_cast(_Float16, (uint16_t)(s23 & 0xFFFFu));
-                d[3] = (float)__builtin_bit_cast(_Float16, (uint16_t)(s23 >> 16));
+                        al = *reinterpret_cast<const h8 *>(wp + 4096 + 1024 * rs + 16 * lane);
 #pragma unroll
-                for (int bs = 0; bs < 4; bs++) {
-                    f4 z = mfma16(aq, S.bh[bs], f4{0.0f, 0.0f, 0.0f, 0.0f});
-                    z = mfma16(aq, S.bl[bs], z);
+                    for (int bs = 0; bs < 4; bs++) {
+                        acc[rs][bs] = mfma16(ah, bh[bs], acc[rs][bs]);
+                        acc[rs][bs] = mfma16(ah, bl[bs], acc[rs][bs]);
+                        if (WT == W_F32)
+                            acc[rs][bs] = mfma16(al, bh[bs], acc[rs][bs]);
+                    }
+                } else {
+                    const h8 aq = WT == W_Q8_0
+                                      ? i8x8_to_h8(*reinterpret_cast<const u2 *>(wp + 512 * rs + 8 * lane))
+                                      : u4x8_to_h8(*reinterpret_cast<const u2 *>(wp + 256 * rs + 16 * j + 8 * (g & 1)),
+                                                   (g & 2) ? 4 : 0);
+                    const u2 sw = *reinterpret_cast<const u2 *>(wp + M::WB + (16 * rs + 4 * g) * 2);
+                    const uint32_t s01 = sw.x, s23 = sw.y;
+                    float d[4];
+                    d[0] = (float)__builtin_bit_cast(_Float16, (uint16_t)(s01 & 0xFFFFu));
+                    d[1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(s01 >> 16));
+                    d[2] = (float)__builtin_bit_cast(_Float16, (uint16_t)(s23 & 0xFFFFu));
+                    d[3] = (float)__builtin_bit_cast(_Float16, (uint16_t)(s23 >> 16));
 #pragma unroll
-                    for (int i = 0; i < 4; i++)
-                        acc[rs][bs][i] = fmaf(z[i], d[i], acc[rs][bs][i]);
+                    for (int bs = 0; bs < 4; bs++) {
+                        f4 z = mfma16(aq, bh[bs], f4{0.0f, 0.0f, 0.0f, 0.0f});
+                        z = mfma16(aq, bl[bs], z);
+#pragma unroll
+                        for (int r = 0; r < 4; r++)
+                            acc[rs][bs][r] = fmaf(z[r], d[r], acc[rs][bs][r]);
+                    }
                 }
             }
-        }
-    };
-    if (w < KS) {
-        Step cur, nxt;
-        load(w, cur);
-        for (int kk = w; kk < KS; kk += 4) {
-            load(min(kk + 4, KS - 1), nxt);
-            // keeps the scheduler from sinking those loads to their use in
-            // the next iteration
-            __builtin_amdgcn_sched_barrier(0);
-            compute(cur);
-            cur = nxt;
         }
     }
+    // the trailing (unused) loads land before the staging area becomes the
+    // reduction buffer
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+    float(*s_acc)[64][65] = reinterpret_cast<float(*)[64][65]>(smem);
     if (w > 0) {
 #pragma unroll
         for (int rs = 0; rs < 4; rs++)
@@ -517,10 +546,10 @@ int gi_matmul_batch(gi_weights *w, int batch, const float *x, float *y)
     a.y = y;
     dim3 grid((unsigned)(batch64 / 64), (unsigned)(a.rows64 / 64));
     switch (w->type) {
-    case W_F32: hipLaunchKernelGGL(matmul_tile<W_F32>, grid, dim3(256), 0, st, a); break;
-    case W_F16: hipLaunchKernelGGL(matmul_tile<W_F16>, grid, dim3(256), 0, st, a); break;
-    case W_Q8_0: hipLaunchKernelGGL(matmul_tile<W_Q8_0>, grid, dim3(256), 0, st, a); break;
-    default: hipLaunchKernelGGL(matmul_tile<W_Q4_0>, grid, dim3(256), 0, st, a); break;
+    case W_F32: hipLaunchKernelGGL((matmul_lds<W_F32, 2>), grid, dim3(256), 0, st, a); break;
+    case W_F16: hipLaunchKernelGGL((matmul_lds<W_F16, 3>), grid, dim3(256), 0, st, a); break;
+    case W_Q8_0: hipLaunchKernelGGL((matmul_lds<W_Q8_0, 3>), grid, dim3(256), 0, st, a); break;
+    default: hipLaunchKernelGGL((matmul_lds<W_Q4_0, 3>), grid, dim3(256), 0, st, a); break;
     }
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? GI_OK : hip_fail(e, "gi_matmul_batch");
