@@ -11,19 +11,21 @@
 // each 16-byte operand load of a wave reads one contiguous 1 KiB run (a
 // row-major load would send every quarter-wave to 16 rows, and the L1 tag
 // rate -- one line per lane -- bounds that form):
-//   16-bit matrices (F16 weights, the F32 weight halves, the activation
-//   halves): the 16 x 32 tile (rows 16t.., columns 32kk..) is 512 elements
-//   in lane order, lane 16 * ((c / 8) % 4) + r % 16 holding columns
-//   8 ((c / 8) % 4) .. +7 of its row (op_index);
+//   16-bit weight matrices (F16, the F32 halves): the 16 x 32 tile (rows
+//   16t.., columns 32kk..) is 512 elements in lane order, lane
+//   16 * ((c / 8) % 4) + r % 16 holding columns 8 ((c / 8) % 4) .. +7 of its
+//   row (op_index);
+//   activation halves: the same tiles, each row-major (x_index), which the
+//   direct loads permute into lane order;
 //   Q8_0  int8 codes in the same order (512 bytes per tile), fp16 block
-//         scales [cols/32][rows64];
+//         scales [cols/32][rows_pad];
 //   Q4_0  per tile and block, the 16 nibble bytes of each of the 16 rows
 //         (byte j holds elements j and j+16, quant.go:504), 256 bytes;
 //         scales as Q8_0;
 //   F32   two fp16 halves, hi and lo, of W * 2^e[r] (e[r] from the row's
 //         largest |w|, so both halves stay normal), and 2^-e[r] per row.
 // Rows of weights and activations are padded with zeros to multiples of 64,
-// the output tile, so the product loop needs no bounds checks.
+// so the product loop needs no bounds checks.
 //
 // Activations are split per batch row into fp16 hi + lo of x * 2^e[b], so the
 // products keep float32 accuracy.  The matrix cores then compute W * x^T on
@@ -63,13 +65,25 @@ using mfma_ops::u4x8_to_h8;
 enum : int { W_F32 = 0, W_F16 = 1, W_Q4_0 = 2, W_Q8_0 = 8 }; // GGML type ids
 
 
-__host__ __device__ __forceinline__ int64_t round64(int64_t n) { return (n + 63) / 64 * 64; }
+
+// Rows of weights and activations are padded to multiples of 64, the output
+// tile.
+__host__ __device__ __forceinline__ int64_t round_pad(int64_t n) { return (n + 63) / 64 * 64; }
 
 // Element (r, c) of a 16-bit matrix (or an int8 code matrix) with KS
 // k-steps of 32 columns, in operand order.
 __host__ __device__ __forceinline__ int64_t op_index(int64_t r, int c, int KS)
 {
     return (((r >> 4) * KS + (c >> 5)) * 64 + 16 * ((c >> 3) & 3) + (r & 15)) * 8 + (c & 7);
+}
+
+// Element (b, c) of the activation halves: each 16 x 32 tile row-major
+// (16 rows of 64 bytes), so that one batch row's k-step is one 64-byte run
+// when it is written.  The direct loads read a tile's 1 KiB whole and permute
+// it into lane order (operand order) on the way into LDS.
+__host__ __device__ __forceinline__ int64_t x_index(int64_t b, int c, int KS)
+{
+    return (((b >> 4) * KS + (c >> 5)) * 16 + (b & 15)) * 32 + (c & 31);
 }
 
 // Byte i of row r's Q4_0 block kk.
@@ -83,18 +97,18 @@ __host__ __device__ __forceinline__ int64_t q4_index(int64_t r, int kk, int i, i
 // Q8_0 / Q4_0: one thread per (row, block) of the padded rows; raw blocks
 // are byte-addressed.
 __global__ __launch_bounds__(256) void convert_quant(const uint8_t *__restrict__ raw, int type, int rows,
-                                                    int rows64, int cols, uint8_t *__restrict__ codes,
+                                                    int rows_pad, int cols, uint8_t *__restrict__ codes,
                                                     uint16_t *__restrict__ scales)
 {
     const int nb = cols / 32;
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= (int64_t)rows64 * nb)
+    if (i >= (int64_t)rows_pad * nb)
         return;
     const int r = (int)(i / nb), kb = (int)(i - (int64_t)r * nb);
     const bool live = r < rows;
     const int bb = type == W_Q8_0 ? 34 : 18;
     const uint8_t *blk = raw + (live ? i : 0) * bb;
-    scales[(int64_t)kb * rows64 + r] = live ? (uint16_t)(blk[0] | (blk[1] << 8)) : 0;
+    scales[(int64_t)kb * rows_pad + r] = live ? (uint16_t)(blk[0] | (blk[1] << 8)) : 0;
     if (type == W_Q8_0) {
         for (int j = 0; j < 32; j++)
             codes[op_index(r, 32 * kb + j, nb)] = live ? blk[2 + j] : 0;
@@ -105,12 +119,12 @@ __global__ __launch_bounds__(256) void convert_quant(const uint8_t *__restrict__
 }
 
 // F16: one thread per 8 consecutive elements of the padded rows.
-__global__ __launch_bounds__(256) void convert_f16(const uint16_t *__restrict__ raw, int rows, int rows64, int cols,
+__global__ __launch_bounds__(256) void convert_f16(const uint16_t *__restrict__ raw, int rows, int rows_pad, int cols,
                                                   uint16_t *__restrict__ dst)
 {
     const int per = cols / 8;
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= (int64_t)rows64 * per)
+    if (i >= (int64_t)rows_pad * per)
         return;
     const int r = (int)(i / per), c = 8 * (int)(i - (int64_t)r * per);
     uint4 v = {0u, 0u, 0u, 0u};
@@ -160,39 +174,75 @@ __global__ __launch_bounds__(256) void convert_f32(const float *__restrict__ raw
 
 // ---- activations: x * 2^e split into hi + lo per batch row ---------------
 
-// One workgroup per padded batch row (rows past the batch are zeros).
+// One workgroup per padded batch row (rows past the batch are zeros); each
+// thread takes runs of 8 columns, so the halves go out as 16-byte stores,
+// four of them one 64-byte run of a tile (x_index).
 __global__ __launch_bounds__(256) void split_rows(const float *__restrict__ x, int batch, int cols,
                                                  _Float16 *__restrict__ xh, _Float16 *__restrict__ xl,
                                                  float *__restrict__ xscale)
 {
-    __shared__ float s_max[256];
-    const int b = blockIdx.x, KS = cols / 32;
+    __shared__ float s_max[4];
+    const int b = blockIdx.x, KS = cols / 32, runs = cols / 8;
     if (b >= batch) {
-        for (int c = threadIdx.x; c < cols; c += 256) {
-            xh[op_index(b, c, KS)] = (_Float16)0.0f;
-            xl[op_index(b, c, KS)] = (_Float16)0.0f;
+        for (int q = threadIdx.x; q < runs; q += 256) {
+            *reinterpret_cast<uint4 *>(xh + x_index(b, 8 * q, KS)) = uint4{0u, 0u, 0u, 0u};
+            *reinterpret_cast<uint4 *>(xl + x_index(b, 8 * q, KS)) = uint4{0u, 0u, 0u, 0u};
         }
         return;
     }
     const float *xr = x + (int64_t)b * cols;
+    // a thread's first KEEP runs stay in registers between the two passes
+    // (all of them for rows up to 8192 columns)
+    constexpr int KEEP = 4;
+    f4 ku[KEEP], kv[KEEP];
     float m = 0.0f;
-    for (int c = threadIdx.x; c < cols; c += 256)
-        m = fmaxf(m, fabsf(xr[c]));
-    s_max[threadIdx.x] = m;
+#pragma unroll
+    for (int k = 0; k < KEEP; k++) {
+        const int q = threadIdx.x + 256 * k;
+        ku[k] = kv[k] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (q < runs) {
+            ku[k] = *reinterpret_cast<const f4 *>(xr + 8 * q);
+            kv[k] = *reinterpret_cast<const f4 *>(xr + 8 * q + 4);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            m = fmaxf(m, fmaxf(fabsf(ku[k][i]), fabsf(kv[k][i])));
+    }
+    for (int q = threadIdx.x + 256 * KEEP; q < runs; q += 256) {
+        const f4 u = *reinterpret_cast<const f4 *>(xr + 8 * q), v = *reinterpret_cast<const f4 *>(xr + 8 * q + 4);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            m = fmaxf(m, fmaxf(fabsf(u[i]), fabsf(v[i])));
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1)
+        m = fmaxf(m, __shfl_xor(m, o));
+    if ((threadIdx.x & 63) == 0)
+        s_max[threadIdx.x >> 6] = m;
     __syncthreads();
-    for (int s = 128; s > 0; s >>= 1) {
-        if ((int)threadIdx.x < s)
-            s_max[threadIdx.x] = fmaxf(s_max[threadIdx.x], s_max[threadIdx.x + s]);
-        __syncthreads();
-    }
-    const int e = pow2_exponent_for(s_max[0]);
+    m = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
+    const int e = pow2_exponent_for(m);
     const float up = ldexpf(1.0f, e);
-    for (int c = threadIdx.x; c < cols; c += 256) {
-        const float v = xr[c] * up; // exact: a power of two
-        const _Float16 h = (_Float16)v;
-        xh[op_index(b, c, KS)] = h;
-        xl[op_index(b, c, KS)] = (_Float16)(v - (float)h);
+    auto emit = [&](int q, const f4 &u, const f4 &v) {
+        h8 hi, lo;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const float t = (k < 4 ? u[k] : v[k - 4]) * up; // exact: a power of two
+            const _Float16 h = (_Float16)t;
+            hi[k] = h;
+            lo[k] = (_Float16)(t - (float)h);
+        }
+        *reinterpret_cast<h8 *>(xh + x_index(b, 8 * q, KS)) = hi;
+        *reinterpret_cast<h8 *>(xl + x_index(b, 8 * q, KS)) = lo;
+    };
+#pragma unroll
+    for (int k = 0; k < KEEP; k++) {
+        const int q = threadIdx.x + 256 * k;
+        if (q < runs)
+            emit(q, ku[k], kv[k]);
     }
+    for (int q = threadIdx.x + 256 * KEEP; q < runs; q += 256)
+        emit(q, *reinterpret_cast<const f4 *>(xr + 8 * q), *reinterpret_cast<const f4 *>(xr + 8 * q + 4));
     if (threadIdx.x == 0)
         xscale[b] = ldexpf(1.0f, -e);
 }
@@ -202,10 +252,10 @@ __global__ __launch_bounds__(256) void split_rows(const float *__restrict__ x, i
 struct MatArgs {
     int type;
     int rows, cols, batch;
-    int rows64;             // rows padded to the output tile
+    int rows_pad;           // rows padded to a multiple of 64
     const uint8_t *a;      // F16 / F32-hi / Q8 codes / Q4 nibble bytes
     const uint8_t *a_lo;   // F32 lo
-    const uint16_t *scales; // Q8 / Q4 block scales [cols/32][rows64]
+    const uint16_t *scales; // Q8 / Q4 block scales [cols/32][rows_pad]
     const float *row_scale; // F32
     const _Float16 *xh, *xl;
     const float *xscale;
@@ -255,7 +305,8 @@ __global__ __launch_bounds__(256) void matmul_lds(MatArgs a)
         uint8_t *d = mine + st * M::BYTES;
 #pragma unroll
         for (int bs = 0; bs < 4; bs++) {
-            const int64_t o = (((bt0 + bs) * KS + kk) * 64 + lane) * 8;
+            // lane (j, g) fetches row j's k-elements 8g .. 8g+7 of the tile
+            const int64_t o = ((bt0 + bs) * KS + kk) * 512 + 32 * j + 8 * g;
             __builtin_amdgcn_global_load_lds(a.xh + o, (lds_void)(d + 2048 * bs), 16, 0, 0);
             __builtin_amdgcn_global_load_lds(a.xl + o, (lds_void)(d + 2048 * bs + 1024), 16, 0, 0);
         }
@@ -275,7 +326,7 @@ __global__ __launch_bounds__(256) void matmul_lds(MatArgs a)
             }
         }
         if (M::SB && lane < 8)
-            __builtin_amdgcn_global_load_lds(a.scales + (int64_t)kk * a.rows64 + r0 + 8 * lane,
+            __builtin_amdgcn_global_load_lds(a.scales + (int64_t)kk * a.rows_pad + r0 + 8 * lane,
                                              (lds_void)(d + M::WB), 16, 0, 0);
     };
     if (nk > 0) {
@@ -427,42 +478,42 @@ int gi_weights_upload(gi_paged *h, int ggml_type, int rows, int cols, const void
         if (rc == GI_OK)
             rc = gi_dev_alloc(h, n, dst);
     };
-    const int64_t rows64 = round64(rows);
+    const int64_t rows_pad = round_pad(rows);
     {
         alloc((size_t)raw_bytes, &tmp);
         if (rc == GI_OK)
             rc = gi_memcpy_h2d(h, tmp, raw, (size_t)raw_bytes);
         hipError_t e = hipSuccess;
         if (ggml_type == W_F16) {
-            alloc((size_t)rows64 * cols * 2, &p);
+            alloc((size_t)rows_pad * cols * 2, &p);
             wt->a = (uint8_t *)p;
             if (rc == GI_OK) {
-                const int64_t n = rows64 * (cols / 8);
+                const int64_t n = rows_pad * (cols / 8);
                 hipLaunchKernelGGL(convert_f16, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
-                                   (const uint16_t *)tmp, rows, (int)rows64, cols, (uint16_t *)wt->a);
+                                   (const uint16_t *)tmp, rows, (int)rows_pad, cols, (uint16_t *)wt->a);
                 e = hipGetLastError();
             }
         } else if (ggml_type == W_F32) {
-            alloc((size_t)rows64 * cols * 2, &p);
+            alloc((size_t)rows_pad * cols * 2, &p);
             wt->a = (uint8_t *)p;
-            alloc((size_t)rows64 * cols * 2, &p);
+            alloc((size_t)rows_pad * cols * 2, &p);
             wt->a_lo = (uint8_t *)p;
-            alloc((size_t)rows64 * 4, &p);
+            alloc((size_t)rows_pad * 4, &p);
             wt->row_scale = (float *)p;
             if (rc == GI_OK) {
-                hipLaunchKernelGGL(convert_f32, dim3((unsigned)rows64), dim3(256), 0, st, (const float *)tmp, rows,
+                hipLaunchKernelGGL(convert_f32, dim3((unsigned)rows_pad), dim3(256), 0, st, (const float *)tmp, rows,
                                    cols, (_Float16 *)wt->a, (_Float16 *)wt->a_lo, wt->row_scale);
                 e = hipGetLastError();
             }
         } else {
-            alloc((size_t)rows64 * (ggml_type == W_Q8_0 ? cols : cols / 2), &p);
+            alloc((size_t)rows_pad * (ggml_type == W_Q8_0 ? cols : cols / 2), &p);
             wt->a = (uint8_t *)p;
-            alloc((size_t)rows64 * nb * 2, &p);
+            alloc((size_t)rows_pad * nb * 2, &p);
             wt->scales = (uint16_t *)p;
             if (rc == GI_OK) {
-                const int64_t n = rows64 * nb;
+                const int64_t n = rows_pad * nb;
                 hipLaunchKernelGGL(convert_quant, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
-                                   (const uint8_t *)tmp, ggml_type, rows, (int)rows64, cols, wt->a, wt->scales);
+                                   (const uint8_t *)tmp, ggml_type, rows, (int)rows_pad, cols, wt->a, wt->scales);
                 e = hipGetLastError();
             }
         }
@@ -507,8 +558,8 @@ int gi_matmul_batch(gi_weights *w, int batch, const float *x, float *y)
     if (batch == 0)
         return GI_OK;
     gi_paged *h = w->h;
-    const int batch64 = (int)round64(batch); // activation rows, zero-padded to the output tile
-    if (batch64 > w->x_cap) {
+    const int batch_pad = (int)round_pad(batch); // activation rows, zero-padded
+    if (batch_pad > w->x_cap) {
         for (void *p : {(void *)w->xh, (void *)w->xl, (void *)w->xscale})
             if (p)
                 (void)gi_dev_free(h, p); // waits for queued work that reads them
@@ -516,24 +567,24 @@ int gi_matmul_batch(gi_weights *w, int batch, const float *x, float *y)
         w->xscale = nullptr;
         w->x_cap = 0;
         void *p = nullptr;
-        const size_t nx = (size_t)batch64 * w->cols * 2;
+        const size_t nx = (size_t)batch_pad * w->cols * 2;
         int rc = gi_dev_alloc(h, nx, &p);
         w->xh = (_Float16 *)p;
         if (rc == GI_OK && (rc = gi_dev_alloc(h, nx, &p)) == GI_OK)
             w->xl = (_Float16 *)p;
-        if (rc == GI_OK && (rc = gi_dev_alloc(h, (size_t)batch64 * 4, &p)) == GI_OK)
+        if (rc == GI_OK && (rc = gi_dev_alloc(h, (size_t)batch_pad * 4, &p)) == GI_OK)
             w->xscale = (float *)p;
         if (rc != GI_OK)
             return rc;
-        w->x_cap = batch64;
+        w->x_cap = batch_pad;
     }
     hipStream_t st = (hipStream_t)gi_paged_stream(h);
-    hipLaunchKernelGGL(split_rows, dim3((unsigned)batch64), dim3(256), 0, st, x, batch, w->cols, w->xh, w->xl,
+    hipLaunchKernelGGL(split_rows, dim3((unsigned)batch_pad), dim3(256), 0, st, x, batch, w->cols, w->xh, w->xl,
                        w->xscale);
     MatArgs a{};
     a.type = w->type;
     a.rows = w->rows;
-    a.rows64 = (int)round64(w->rows);
+    a.rows_pad = (int)round_pad(w->rows);
     a.cols = w->cols;
     a.batch = batch;
     a.a = w->a;
@@ -544,7 +595,7 @@ int gi_matmul_batch(gi_weights *w, int batch, const float *x, float *y)
     a.xl = w->xl;
     a.xscale = w->xscale;
     a.y = y;
-    dim3 grid((unsigned)(batch64 / 64), (unsigned)(a.rows64 / 64));
+    dim3 grid((unsigned)(batch_pad / 64), (unsigned)(a.rows_pad / 64));
     switch (w->type) {
     case W_F32: hipLaunchKernelGGL((matmul_lds<W_F32, 2>), grid, dim3(256), 0, st, a); break;
     case W_F16: hipLaunchKernelGGL((matmul_lds<W_F16, 3>), grid, dim3(256), 0, st, a); break;
