@@ -50,6 +50,7 @@ using mfma_ops::u2;
 using mfma_ops::u4;
 using mfma_ops::i8x8_to_h8;
 using mfma_ops::u4x8_masked_to_h8;
+using mfma_ops::split_pair;
 typedef uint16_t us2 __attribute__((ext_vector_type(2)));
 
 // Cache policy of the direct global->LDS loads (2: non-temporal, which
@@ -324,28 +325,54 @@ struct F32Stage {
     uint8_t v[BYTES];
 };
 
+// Per-lane parts of the f32 staging addresses, fixed for the kernel.  Load q
+// of K reads page (q & 1) only (rows of tokens 16 (q & 1) ..); each V lane
+// keeps to one page per parity of q.  So a load is a per-block base, the
+// lane's offset and a constant.
+struct F32Lanes {
+    uint32_t k[2], v[2]; // byte offsets for even / odd loads
+    bool vb[2];          // V lane on page B
+};
+
+template <int HD>
+__device__ __forceinline__ F32Lanes f32_lanes(int lane, int P)
+{
+    F32Lanes n;
+    const int jl = lane >> 3;
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+        const int c = (lane & 7) ^ ((4 * p + (lane >> 4)) & 7);
+        n.k[p] = (uint32_t)((8 * (jl >> 2) + (jl & 3)) * HD * 4 + 16 * c);
+        n.v[p] = (uint32_t)(16 * c + jl * P * 4);
+        n.vb[p] = c >= 4;
+    }
+    return n;
+}
+
 template <int HD>
 __device__ __forceinline__ void issue_f32(const DecodeArgs &a, int64_t pA, int64_t pB, int sA, int sB,
-                                          int64_t koff, int64_t voff, int lane, F32Stage<HD> &S)
+                                          int64_t koff, int64_t voff, const F32Lanes &ln, F32Stage<HD> &S)
 {
     const PoolLayout &L = a.L;
     const int P = L.page_tokens;
     const uint8_t *gA = a.base + pA * L.page_bytes, *gB = a.base + pB * L.page_bytes;
+    // K: slot 64q + lane holds token row 16 (q & 1) + 8 (jl >> 2) + (jl & 3)
+    // + 4 ((q >> 1) & 1), dimensions 32 (q >> 2) + 4c .. + 3
+    const uint8_t *kA = gA + (int64_t)sA * HD * 4 + koff, *kB = gB + (int64_t)sB * HD * 4 + koff;
 #pragma unroll
     for (int q = 0; q < F32Stage<HD>::NLOAD; q++) {
-        const int sl = 64 * q + lane;
-        const int kt = sl >> 7, jj = (sl >> 3) & 15, c = (sl & 7) ^ ((jj >> 1) & 7);
-        const int kk = kt >> 1, tk = 8 * (jj >> 2) + (jj & 3) + 4 * (kt & 1);
-        const uint8_t *src = (tk < 16 ? gA + (int64_t)(sA + tk) * HD * 4 : gB + (int64_t)(sB + tk - 16) * HD * 4) +
-                             koff + (32 * kk + 4 * c) * 4;
+        const int p = q & 1;
+        const uint8_t *src = (p ? kB : kA) + ln.k[p] + (4 * ((q >> 1) & 1) * HD * 4 + 128 * (q >> 2));
         __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.k[1024 * q], 16, 0, GI_DECODE_LDS_AUX);
     }
+    // V: slot 64q + lane holds dimension 16 (q >> 1) + 8 (q & 1) + jl, block
+    // tokens 4c .. 4c + 3 (page A for c < 4)
+    const uint8_t *vA = gA + voff + (int64_t)sA * 4, *vB = gB + voff + (int64_t)(sB - 16) * 4;
+    const uint8_t *vbase[2] = {ln.vb[0] ? vB : vA, ln.vb[1] ? vB : vA};
 #pragma unroll
     for (int q = 0; q < F32Stage<HD>::NLOAD; q++) {
-        const int sl = 64 * q + lane;
-        const int nb = sl >> 7, jj = (sl >> 3) & 15, c = (sl & 7) ^ ((jj >> 1) & 7);
-        const uint8_t *src = (c < 4 ? gA + (int64_t)(sA + 4 * c) * 4 : gB + (int64_t)(sB + 4 * c - 16) * 4) + voff +
-                             (int64_t)(16 * nb + jj) * P * 4;
+        const int p = q & 1;
+        const uint8_t *src = vbase[p] + ln.v[p] + (int64_t)(16 * (q >> 1) + 8 * p) * P * 4;
         __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.v[1024 * q], 16, 0, GI_DECODE_LDS_AUX);
     }
 }
@@ -394,18 +421,6 @@ __device__ __forceinline__ float pow2_recip(float x)
     return __builtin_bit_cast(float, 0x7F000000u - __builtin_bit_cast(uint32_t, x));
 }
 
-// x (already scaled into fp16 range) as hi + lo halves: hi = x cut to 11
-// significant bits (what the round-toward-zero conversion gives), lo the
-// exact remainder rounded to nearest, so hi + lo is x to 2^-23 relative.
-__device__ __forceinline__ void split_pair(float x0, float x1, uint32_t &hi, uint32_t &lo)
-{
-    const float t0 = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, x0) & 0xFFFFE000u);
-    const float t1 = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, x1) & 0xFFFFE000u);
-    hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x0, x1));
-    const h2 l = {(_Float16)(x0 - t0), (_Float16)(x1 - t1)};
-    lo = __builtin_bit_cast(uint32_t, l);
-}
-
 // Reads one f32 block from the staging area and turns it into hi/lo fp16
 // operands.  Tokens past t1 (or the whole block on a rejected page) are
 // zeroed first, so that stale slots take no part in the scales.  K is scaled
@@ -414,7 +429,7 @@ __device__ __forceinline__ void split_pair(float x0, float x1, uint32_t &hi, uin
 template <int HD>
 __device__ __forceinline__ void read_f32(const F32Stage<HD> &Sf, int j, int g, int base, bool ok, int t1,
                                          h8 *kh0, h8 *kh1, h8 *kl0, h8 *kl1, h8 *vh, h8 *vl, float &ksc,
-                                         float &vsc, State<HD> &S)
+                                         float &vsc, State<HD> &S, float neg1)
 {
     constexpr int KK = HD / 32, NB = HD / 16;
     const int x = (j >> 1) & 7;
@@ -506,8 +521,8 @@ __device__ __forceinline__ void read_f32(const F32Stage<HD> &Sf, int j, int g, i
 #pragma unroll
         for (int k = 0; k < 4; k++) {
             uint32_t a0, b0, a1, b1;
-            split_pair(kf[0][kk][2 * k], kf[0][kk][2 * k + 1], a0, b0);
-            split_pair(kf[1][kk][2 * k], kf[1][kk][2 * k + 1], a1, b1);
+            split_pair(kf[0][kk][2 * k], kf[0][kk][2 * k + 1], a0, b0, neg1);
+            split_pair(kf[1][kk][2 * k], kf[1][kk][2 * k + 1], a1, b1, neg1);
             h0[k] = a0;
             l0[k] = b0;
             h1[k] = a1;
@@ -524,7 +539,7 @@ __device__ __forceinline__ void read_f32(const F32Stage<HD> &Sf, int j, int g, i
 #pragma unroll
         for (int k = 0; k < 4; k++) {
             uint32_t a0, b0;
-            split_pair(vf[nb][2 * k], vf[nb][2 * k + 1], a0, b0);
+            split_pair(vf[nb][2 * k], vf[nb][2 * k + 1], a0, b0, neg1);
             hh[k] = a0;
             ll[k] = b0;
         }
@@ -914,6 +929,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
     for (int nb = 0; nb < NB; nb++)
         S.o[nb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     float ksc = 0.0f, vsc = 0.0f; // f32 pages: running K / V operand scales
+    const float neg1 = mfma_ops::opaque_neg1(); // f32 pages: for split_pair
     float vnorm = 0.0f; // quantised pages: running power-of-two cap of the V scales
 
     // bytes per stored element: fp16 2, q8_0 1, q4_0 1/2
@@ -974,17 +990,18 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
     } else if constexpr (F32) {
         if (base < t1) {
             F32Stage<HD> &Sf = reinterpret_cast<F32Stage<HD> *>(s_stage)[w];
+            const F32Lanes fl = f32_lanes<HD>(lane, P);
             int64_t pA, pB;
             int sA, sB;
             bool ok;
             block_pages(a, bt, base, t1, pA, pB, sA, sB, ok);
-            issue_f32<HD>(a, pA, pB, sA, sB, koff, voff, lane, Sf);
+            issue_f32<HD>(a, pA, pB, sA, sB, koff, voff, fl, Sf);
             load_q();
             for (;;) {
                 h8 kh0[KK], kh1[KK], kl0[KK], kl1[KK], vh[NB], vl[NB];
                 // the only vector loads in flight are this block's
                 __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0)
-                read_f32<HD>(Sf, j, g, base, ok, t1, kh0, kh1, kl0, kl1, vh, vl, ksc, vsc, S);
+                read_f32<HD>(Sf, j, g, base, ok, t1, kh0, kh1, kl0, kl1, vh, vl, ksc, vsc, S, neg1);
                 const int next = base + stride;
                 const bool more = next < t1;
                 int64_t nA = pA, nB = pB;
@@ -993,7 +1010,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
                 if (more) {
                     block_pages(a, bt, next, t1, nA, nB, nsA, nsB, nok);
                     __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0): this block's reads returned
-                    issue_f32<HD>(a, nA, nB, nsA, nsB, koff, voff, lane, Sf);
+                    issue_f32<HD>(a, nA, nB, nsA, nsB, koff, voff, fl, Sf);
                 }
                 // S = (kh + kl) . (q_hi | q_lo): two products per k-step
                 f4 s0 = f4{0.0f, 0.0f, 0.0f, 0.0f}, s1 = f4{0.0f, 0.0f, 0.0f, 0.0f};

@@ -50,6 +50,19 @@ __device__ __forceinline__ float opaque_neg1()
     return v;
 }
 
+// x0, x1 (already scaled into fp16 range) as packed hi + lo halves: hi = x
+// cut to 11 significant bits by the round-toward-zero conversion, lo = x - hi
+// (one mixed-precision multiply-add reading hi in place, exact in float32)
+// rounded to nearest, so hi + lo is x to 2^-23 relative.  neg1 is -1
+// (opaque_neg1).
+__device__ __forceinline__ void split_pair(float x0, float x1, uint32_t &hi, uint32_t &lo, float neg1)
+{
+    const h2 h = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(x0, x1));
+    hi = __builtin_bit_cast(uint32_t, h);
+    const h2 l = {(_Float16)fmaf((float)h[0], neg1, x0), (_Float16)fmaf((float)h[1], neg1, x1)};
+    lo = __builtin_bit_cast(uint32_t, l);
+}
+
 // Eight int8 codes -> eight exact fp16 values: (x ^ 0x80) is x + 128 as an
 // unsigned byte, 0x64 above it makes the half 1024 + x + 128, and the bias
 // 1152 is subtracted.

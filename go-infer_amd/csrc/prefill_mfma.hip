@@ -35,6 +35,7 @@ using mfma_ops::h8;
 using mfma_ops::i8x8_to_h8;
 using mfma_ops::u2;
 using mfma_ops::u4;
+using mfma_ops::split_pair;
 using mfma_ops::u4x8_to_h8;
 
 constexpr float kLog2e = 1.4426950408889634f;
@@ -550,18 +551,6 @@ __device__ __forceinline__ void dequant_pair(h8 q, h8 s, h8 &hi, h8 &lo)
     lo = __builtin_elementwise_fma(q, s, -hi);
 }
 
-// x (already scaled into fp16 range) as hi + lo halves: hi = x cut to 11
-// significant bits (what the round-toward-zero conversion gives), lo the
-// exact remainder rounded to nearest, so hi + lo is x to 2^-23 relative.
-__device__ __forceinline__ void split_pair(float x0, float x1, uint32_t &hi, uint32_t &lo)
-{
-    const float t0 = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, x0) & 0xFFFFE000u);
-    const float t1 = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, x1) & 0xFFFFE000u);
-    hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x0, x1));
-    const h2 l = {(_Float16)(x0 - t0), (_Float16)(x1 - t1)};
-    lo = __builtin_bit_cast(uint32_t, l);
-}
-
 // Largest |K| and |V| of this thread's f32 chunks of a staged block, over the
 // live tokens only (stale slots may hold anything).
 template <int HD, int P>
@@ -635,7 +624,7 @@ __device__ __forceinline__ float pow2_recip(float x)
 template <int HD, int KT, int P, int NBUF>
 __device__ __forceinline__ void stage_store(const PrefillArgs &a, int kvh, int tid, int w, int buf,
                                             uint64_t vmask, const StageRegs<HD, KT> &R,
-                                            Lds<HD, KT, NBUF> &S, float ksc = 1.0f, float vsc = 1.0f)
+                                            Lds<HD, KT, NBUF> &S, float ksc = 1.0f, float vsc = 1.0f, float neg1 = -1.0f)
 {
     using M = ChunkMap<HD, KT, P>;
     using G = SwzGeom<HD>;
@@ -686,10 +675,10 @@ __device__ __forceinline__ void stage_store(const PrefillArgs &a, int kvh, int t
                     vx[i] *= vsc;
             }
             uint32_t kh[2], kl[2], vh[2], vl[2];
-            split_pair(kx[0], kx[1], kh[0], kl[0]);
-            split_pair(kx[2], kx[3], kh[1], kl[1]);
-            split_pair(vx[0], vx[1], vh[0], vl[0]);
-            split_pair(vx[2], vx[3], vh[1], vl[1]);
+            split_pair(kx[0], kx[1], kh[0], kl[0], neg1);
+            split_pair(kx[2], kx[3], kh[1], kl[1], neg1);
+            split_pair(vx[0], vx[1], vh[0], vl[0], neg1);
+            split_pair(vx[2], vx[3], vh[1], vl[1], neg1);
             *reinterpret_cast<u2 *>(&S.k[buf][G::kel(tk, col)]) = u2{kh[0], kh[1]};
             *reinterpret_cast<u2 *>(&S.kl[buf][G::kel(tk, col)]) = u2{kl[0], kl[1]};
             *reinterpret_cast<u2 *>(&S.v[buf][G::vel(d, t0)]) = u2{vh[0], vh[1]};
@@ -1168,7 +1157,7 @@ __global__ __launch_bounds__(256) void attn_prefill_lds(PrefillArgs a)
     stage_load<HD, KT, P>(a, W.kvh, W.tid, W.w, tb, R);
     tb = W.table(kTB);
     f32_scales(mask_c);
-    stage_store<HD, KT, P, NBUF>(a, W.kvh, W.tid, W.w, 0, mask_c, R, S, ksc_run, vsc_run);
+    stage_store<HD, KT, P, NBUF>(a, W.kvh, W.tid, W.w, 0, mask_c, R, S, ksc_run, vsc_run, A.neg1);
     ksc_cur = ksc_run;
     vsc_cur = vsc_run;
     __syncthreads();
@@ -1201,7 +1190,7 @@ __global__ __launch_bounds__(256) void attn_prefill_lds(PrefillArgs a)
             else if (NBUF == 1)
                 __syncthreads();
             stage_store<HD, KT, P, NBUF>(a, W.kvh, W.tid, W.w, NBUF == 2 ? (buf ^ 1) : 0, mask_n, R, S,
-                                         ksc_run, vsc_run);
+                                         ksc_run, vsc_run, A.neg1);
         }
         mask_c = mask_n;
         ksc_cur = ksc_run;
