@@ -48,7 +48,7 @@ def _run(gi, dev, t, rows, cols, raw, x):
 
 @pytest.mark.parametrize("t", [0, 1, 2, 8], ids=["f32", "f16", "q4_0", "q8_0"])
 @pytest.mark.parametrize("rows,cols,batch", [(64, 64, 1), (80, 96, 5), (1024, 4096, 64),
-                                             (2048, 512, 130), (4096, 1024, 256), (200, 256, 100)])
+                                             (2048, 512, 130), (4096, 1024, 256), (200, 256, 100), (5, 96, 3)])
 def test_matmul_batch(gi, oracle, dev, t, rows, cols, batch):
     W = oracle.normal_with_outliers(7 + t + rows, (rows, cols))
     W[1] *= 1e-3
