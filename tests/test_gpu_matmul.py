@@ -86,6 +86,33 @@ def test_matmul_well_conditioned(gi, oracle, dev, t):
     assert e_or <= 1e-5 and e_ex <= 1e-5, (e_or, e_ex)
 
 
+@pytest.mark.parametrize("t", [1, 8], ids=["f16", "q8_0"])
+def test_matmul_batch_sizes_on_one_weight_set(gi, oracle, dev, t):
+    """One weight set called with a growing, then shrinking, batch: the
+    activation buffers grow, and the zero padding past each batch is rewritten
+    on every call (a smaller batch after a larger one must not see its rows)."""
+    import torch
+    rows, cols = 192, 256
+    W = oracle.normal(81 + t, (rows, cols))
+    raw = oracle.quantize_weights(t, W)
+    wd = dequant(oracle, t, raw, rows, cols).astype(np.float64)
+    pool = gi.PagedKVCache(1, 1, 32, 16, 1, gi.KV_F16)
+    wt = gi.Weights(pool, t, rows, cols, raw)
+    try:
+        for i, batch in enumerate((5, 130, 3, 64, 65)):
+            x = oracle.normal(90 + i, (batch, cols))
+            yd = torch.full((batch, rows), float("nan"), device=dev)
+            wt.MatMulBatch(yd, torch.from_numpy(x).to(dev))
+            pool.synchronize()
+            got = yd.cpu().numpy()
+            exact = x.astype(np.float64) @ wd.T
+            err = float((np.abs(got - exact).max(axis=1) / np.abs(exact).max(axis=1)).max())
+            assert err <= 1e-5, (batch, err)
+    finally:
+        wt.close()
+        pool.close()
+
+
 def test_matmul_errors(gi, dev):
     pool = gi.PagedKVCache(1, 1, 32, 16, 1, gi.KV_F16)
     raw = np.zeros((4, 40), np.uint8)
