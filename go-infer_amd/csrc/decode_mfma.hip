@@ -692,6 +692,134 @@ __device__ __forceinline__ void softmax_pv(f4 s0, f4 s1, h8 *v, int base, bool o
     }
 }
 
+// Lane j ^ 8 of the same 16-lane row (an update of 0: folds into its user).
+__device__ __forceinline__ float xor8(float x)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x128, 0xF, 0xF, true));
+}
+__device__ __forceinline__ uint32_t xor8u(uint32_t x)
+{
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x128, 0xF, 0xF, true);
+}
+
+// softmax_pv_q for four heads per kv head (packed columns 0-3 hi, 4-7 lo,
+// 8-15 unused).  The unused lanes take half the work: lane j + 8 holds
+// tokens 8g+4 .. 8g+7 of column j, lane j < 8 keeps tokens 8g .. 8g+3, so
+// the softmax and the V-scale fold run on 4 tokens per lane instead of 8.
+// The folded P pairs then go back to the lanes of their operand rows
+// (lanes 8-15 feed P rows 8-15, whose output rows are never read).  A
+// column's running sum is split over lanes j and j + 8; the merge adds them.
+template <int KT, int HD>
+__device__ __forceinline__ void softmax_pv_q4(f4 s0, f4 s1, QBlock<KT, HD> &B, int base, bool ok, int t1, int j,
+                                              int g, float c, State<HD> &S, float &vnorm)
+{
+    constexpr int KK = HD / 32, GP = 4;
+    const bool upper = j >= 8;
+    const int t_0 = 8 * g + (upper ? 4 : 0); // block-local token of sc[0]
+    float sc[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const float moved = xor8(s1[r] * c);
+        sc[r] = upper ? moved : s0[r] * c;
+    }
+    if (base + 32 > t1 || !ok) {
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+            if (!(base + t_0 + r < t1 && ok))
+                sc[r] = -INFINITY;
+        // scales of dead tokens (all 8 of this lane's group) to 0, as in
+        // softmax_pv_q
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            if (!(base + 8 * g + i < t1 && ok)) {
+                const uint32_t keep = (i & 1) ? 0x0000FFFFu : 0xFFFF0000u;
+#pragma unroll
+                for (int db = 0; db < KK; db++)
+                    B.vs[db][i >> 1] &= keep;
+            }
+        }
+    }
+    uint32_t mw = 0;
+#pragma unroll
+    for (int db = 0; db < KK; db++)
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t e = B.vs[db][k];
+            mw = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(us2, mw),
+                                                                         __builtin_bit_cast(us2, e)));
+        }
+    uint32_t mh = max(mw & 0xFFFFu, mw >> 16);
+    mh = max(mh, (uint32_t)__shfl_xor((int)mh, 16));
+    mh = max(mh, (uint32_t)__shfl_xor((int)mh, 32));
+    float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+    mx = fmaxf(mx, xor8(mx));
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float mnew = fmaxf(S.m2, mx);
+    const float alpha = __builtin_amdgcn_exp2f(S.m2 - mnew);
+    S.m2 = mnew;
+    const float msub = mnew - 14.0f;
+    float p[4], ps = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        p[r] = __builtin_amdgcn_exp2f(sc[r] - msub);
+        ps += p[r];
+    }
+    S.lsum = S.lsum * alpha + ps;
+    uint32_t bits = __builtin_bit_cast(uint32_t, (float)__builtin_bit_cast(_Float16, (uint16_t)mh));
+    if (bits & 0x7FFFFFu)
+        bits = (bits & 0xFF800000u) + 0x800000u;
+    const float pw = __builtin_bit_cast(float, bits);
+    const bool grow = pw > vnorm;
+    const float f = grow ? vnorm * __builtin_bit_cast(float, 0x7F000000u - bits) : 1.0f;
+    if (grow)
+        vnorm = pw;
+    if (__any(alpha != 1.0f) || grow) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float ar = __shfl(alpha, 4 * g + r) * f;
+#pragma unroll
+            for (int nb = 0; nb < 2 * KK; nb++)
+                S.o[nb][r] *= ar;
+        }
+    }
+    // the column this lane works for is j & 7: lo rows are 4..7
+    const bool lo_row = (j & 7) >= GP;
+    const float inv = vnorm > 0.0f ? __builtin_bit_cast(float, 0x7F000000u - __builtin_bit_cast(uint32_t, vnorm)) *
+                                         (lo_row ? 2048.0f : 1.0f)
+                                   : 0.0f;
+    const uint32_t cut = lo_row ? 0xFFFFE000u : 0u;
+    float pp[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+        pp[r] = p[r] * inv;
+#pragma unroll
+    for (int db = 0; db < KK; db++) {
+        // the scale words of this lane's 4 tokens (copied out before the
+        // bit casts)
+        const uint32_t w0 = upper ? B.vs[db][2] : B.vs[db][0], w1 = upper ? B.vs[db][3] : B.vs[db][1];
+        const h2 v01 = __builtin_bit_cast(h2, w0), v23 = __builtin_bit_cast(h2, w1);
+        const float x0 = fmaf(pp[0], (float)v01[0], 0.0f), x1 = fmaf(pp[1], (float)v01[1], 0.0f);
+        const float x2 = fmaf(pp[2], (float)v23[0], 0.0f), x3 = fmaf(pp[3], (float)v23[1], 0.0f);
+        const float y0 = x0 - __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, x0) & cut);
+        const float y1 = x1 - __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, x1) & cut);
+        const float y2 = x2 - __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, x2) & cut);
+        const float y3 = x3 - __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, x3) & cut);
+        const uint32_t pa = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(y0, y1));
+        const uint32_t pb = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(y2, y3));
+        // lanes j < 8: own tokens 0-3, then lane j+8's tokens 4-7
+        const h8 pw8 = __builtin_bit_cast(h8, u4{pa, pb, xor8u(pa), xor8u(pb)});
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const h8 vv = KT == KV_Q4_0 ? u4x8_masked_to_h8(B.v[db], h ? 0xF0F0F0F0u : 0x0F0F0F0Fu,
+                                                            h ? h2{(_Float16)1152.0f, (_Float16)1152.0f}
+                                                              : h2{(_Float16)1032.0f, (_Float16)1032.0f})
+                                        : i8x8_to_h8(B.v[2 * db + h]);
+            S.o[2 * db + h] = mfma(pw8, vv, S.o[2 * db + h]);
+        }
+    }
+}
+
 // Online softmax and P*V for one block of a quantised page.  Rows of P are
 // packed as in softmax_pv (row j < G: hi half of head j, row 2G-1-j: lo half
 // times 2^11).  For V block db the rows carry w = p * vscale / vnorm, vnorm
@@ -705,6 +833,10 @@ __device__ __forceinline__ void softmax_pv_q(f4 s0, f4 s1, QBlock<KT, HD> &B, in
                                              int g, float c, State<HD> &S, float &vnorm)
 {
     constexpr int KK = HD / 32;
+    if constexpr (GP == 4) {
+        softmax_pv_q4<KT, HD>(s0, s1, B, base, ok, t1, j, g, c, S, vnorm);
+        return;
+    }
     float sc[8];
 #pragma unroll
     for (int r = 0; r < 4; r++) {
@@ -1077,6 +1209,8 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
     __syncthreads();
     // wave totals -> LDS
     float lt = S.lsum;
+    if constexpr (QUANT && GP == 4)
+        lt += xor8(lt); // the compact softmax splits a column over lanes j, j + 8
     lt += __shfl_xor(lt, 16);
     lt += __shfl_xor(lt, 32);
     if (g == 0) {
