@@ -812,7 +812,37 @@ def run_tinyllama(args, gi, torch, dev, cfg):
     torch.cuda.synchronize()
     wall = (time.perf_counter() - w0) / args.steps
     pool.synchronize()
-    ms_step = s0.elapsed_time(s1) / args.steps
+    ms_eager = s0.elapsed_time(s1) / args.steps
+    ms_step, launch = ms_eager, "eager (one DecodeStep call per layer and token)"
+    if not args.no_graph:
+        # The step is 22 x 128 tiny launches, so host time bounds it.  The
+        # entry points allocate nothing once the workspace is sized and never
+        # synchronise, so the whole step can be captured as one HIP graph on
+        # the pool's stream and replayed; every replay must reproduce the
+        # eager outputs bit for bit.
+        ref = out.clone()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            run()
+        for _ in range(3):
+            out.zero_()
+            graph.replay()
+            torch.cuda.synchronize()
+            if not torch.equal(out, ref):
+                raise RuntimeError("tinyllama: a graph replay differs from the eager step")
+        pool.synchronize()
+        g0 = torch.cuda.Event(enable_timing=True)
+        g1 = torch.cuda.Event(enable_timing=True)
+        w0 = time.perf_counter()
+        g0.record(stream)
+        for _ in range(args.steps):
+            graph.replay()
+        g1.record(stream)
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - w0) / args.steps
+        pool.synchronize()
+        ms_step = g0.elapsed_time(g1) / args.steps
+        launch = "one HIP graph of the whole step (its %d launches captured once)" % (layers + ND * layers * 2)
     tok_s = ND / (ms_step * 1e-3)
     # algorithmic bytes of one step: the prompt's append, then per decode
     # token and layer K+V over n tokens, q/out, the appended K/V
@@ -823,7 +853,8 @@ def run_tinyllama(args, gi, torch, dev, cfg):
         byt += layers * (2 * n * kv_dim * e + ((n + P - 1) // P) * 4 + 2 * H * hd * 4
                          + 2 * kv_dim * (4 + e))
     gbs = byt / (ms_step * 1e-3) / 1e9
-    log("tinyllama step %.3f ms (wall %.3f ms): %.0f decode tokens/s" % (ms_step, wall * 1e3, tok_s))
+    log("tinyllama step %.3f ms (wall %.3f ms): %.0f decode tokens/s; eager %.3f ms (%.0f tokens/s)" %
+        (ms_step, wall * 1e3, tok_s, ms_eager, ND / (ms_eager * 1e-3)))
     parity = None
     if not args.no_parity:
         Kh, Vh, Qh, Oh = K.cpu().numpy(), V.cpu().numpy(), Q.cpu().numpy(), out.cpu().numpy()
@@ -868,6 +899,8 @@ def run_tinyllama(args, gi, torch, dev, cfg):
                    "prompt": T0, "decode": ND},
         "tokens_per_s": round(tok_s, 1),
         "us_per_token": round(ms_step * 1e3 / ND, 2),
+        "launch": launch,
+        "eager_tokens_per_s": round(ND / (ms_eager * 1e-3), 1),
         "hbm_frac_of_peak": round(gbs / HBM_PEAK_GBS, 5),
         "roofline": None,
         "cpu_baseline": cpu,
@@ -886,6 +919,8 @@ def main():
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="tinyllama_b1: time the eager calls instead of one HIP graph of the step")
     ap.add_argument("--decode-kernel", type=int, default=-1, choices=[-1, 0, 1],
                     help="-1 automatic, 0 vector ALU, 1 matrix core")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
