@@ -252,12 +252,26 @@ def profiled_traffic(kernel, workload):
     return None
 
 
-def cpu_baseline(oracle, cfg, budget_s=12.0):
+def _timed_units(fn, budget_s, max_units):
+    units, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        units += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or units >= max_units:
+            return units, el
+
+
+def cpu_baseline(oracle, cfg, budget_s=10.0, mt_budget_s=6.0):
     """The oracle's decode (widen the stored vectors -> f32, then the
-    reference loop of forward.go:242-267) on one host core for a bounded sample of the same
-    workload: whole (sequence, layer) units at the configured context,
-    repeated until about budget_s of CPU work; extrapolated to the full
-    step by the number of units."""
+    reference loop of forward.go:242-267) timed on the host for a bounded
+    sample of the same workload: whole (sequence, layer) units at the
+    configured context, repeated until about budget_s of work, extrapolated to
+    the full step by the number of units.  Two figures: one thread (the
+    reference's decode attention is single-threaded, forward.go:247-267) and
+    every host core the process may use (at most 16), with each unit's q-heads
+    split over the threads as forward.go:1342-1378 splits heads over
+    goroutines; the threaded rows are bit-identical to the one-thread ones."""
     H, kvh, hd = cfg["q_heads"], cfg["kv_heads"], cfg["head_dim"]
     kv_dim = kvh * hd
     lens = seq_lengths(cfg, 11)
@@ -267,31 +281,41 @@ def cpu_baseline(oracle, cfg, budget_s=12.0):
     v = oracle.store_vectors(kt, oracle.normal(2, (L, kv_dim)))
     q = oracle.normal(3, (1, H * hd))
     sc = oracle.attn_scale(hd)
-    units, t0 = 0, time.perf_counter()
-    while True:
-        oracle.decode_batch(kt, q, k, v, np.zeros(1, np.int64), np.array([L], np.int32), H, kvh,
-                            hd, sc)
-        units += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s or units >= 256:
-            break
-    per_unit = el / units
+    off, ln = np.zeros(1, np.int64), np.array([L], np.int32)
     full_units = float(np.sum(lens)) / L * cfg["layers"]
-    step_s = per_unit * full_units
-    return {"value": round(cfg["batch"] / step_s, 4), "unit": "tokens/s", "cores": 1,
-            "kind": "port",
-            "sample": "%d (sequence, layer) decode units at L=%d on 1 thread, %.1f s; "
-                      "extrapolated x%.0f to the full step" % (units, L, el, full_units / units),
-            "ms_per_step": round(step_s * 1e3, 1)}
+
+    def figure(units, el, cores):
+        step_s = el / units * full_units
+        return {"value": round(cfg["batch"] / step_s, 4), "unit": "tokens/s", "cores": cores,
+                "kind": "port",
+                "sample": "%d (sequence, layer) decode units at L=%d on %d thread%s, %.1f s; "
+                          "extrapolated x%.0f to the full step"
+                          % (units, L, cores, "" if cores == 1 else "s", el, full_units / units),
+                "ms_per_step": round(step_s * 1e3, 1)}
+
+    u1, e1 = _timed_units(lambda: oracle.decode_batch(kt, q, k, v, off, ln, H, kvh, hd, sc),
+                          budget_s, 256)
+    one = figure(u1, e1, 1)
+    n = oracle.host_threads()
+    ran = [1]
+
+    def mt():
+        ran[0] = oracle.decode_batch(kt, q, k, v, off, ln, H, kvh, hd, sc, threads=n)[1]
+
+    un, en = _timed_units(mt, mt_budget_s, 4096)
+    res = figure(un, en, ran[0])
+    res["one_thread"] = one
+    return res
 
 
-def cpu_baseline_prefill(oracle, cfg, budget_s=10.0):
+def cpu_baseline_prefill(oracle, cfg, budget_s=8.0, mt_budget_s=6.0):
     """The oracle's chunked-prefill attention (forward.go:547-577, over
     f32 K/V: quantised pages dequantised first, a pass over the context that is
-    under 0.1 % of the work and left out) on one host core for a bounded
-    sample: 16 queries at the end of the last chunk (context 4096), repeated
-    until about budget_s of CPU work.  Reported as TFLOP/s of the same
-    algorithmic flop count as the GPU figure."""
+    under 0.1 % of the work and left out) on the host for a bounded sample: 16
+    queries at the end of the last chunk (context 4096), repeated until about
+    budget_s of work, on one thread and on every host core the process may
+    use (at most 16; rows split over threads).  Reported as TFLOP/s of the
+    same algorithmic flop count as the GPU figure."""
     H, kvh, hd = cfg["q_heads"], cfg["kv_heads"], cfg["head_dim"]
     Ltot = int(cfg["context"])
     nq, start = 16, Ltot - 16
@@ -300,19 +324,25 @@ def cpu_baseline_prefill(oracle, cfg, budget_s=10.0):
     q = oracle.normal(13, (nq, H * hd))
     sc = oracle.attn_scale(hd)
     flops = 4 * hd * H * sum(start + i + 1 for i in range(nq))
-    units, t0 = 0, time.perf_counter()
-    while True:
-        oracle.attention_prefill(q, k, v, H, kvh, hd, start, nq, 1 << 30, sc)
-        units += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s or units >= 64:
-            break
-    tflops = flops * units / el / 1e12
-    full_s = prefill_flops(cfg) / (tflops * 1e12)
-    return {"value": round(tflops, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
-            "sample": "%d units of 16 queries at positions %d..%d over f32 K/V (%.2f GFLOP each) "
-                      "on 1 thread, %.1f s; the whole prefill would take %.0f s"
-                      % (units, start, Ltot - 1, flops / 1e9, el, full_s)}
+
+    def figure(units, el, cores):
+        tflops = flops * units / el / 1e12
+        full_s = prefill_flops(cfg) / (tflops * 1e12)
+        return {"value": round(tflops, 6), "unit": "TFLOP/s", "cores": cores, "kind": "port",
+                "sample": "%d units of 16 queries at positions %d..%d over f32 K/V (%.2f GFLOP "
+                          "each) on %d thread%s, %.1f s; the whole prefill would take %.0f s"
+                          % (units, start, Ltot - 1, flops / 1e9, cores,
+                             "" if cores == 1 else "s", el, full_s)}
+
+    u1, e1 = _timed_units(
+        lambda: oracle.attention_prefill(q, k, v, H, kvh, hd, start, nq, 1 << 30, sc), budget_s, 64)
+    n = oracle.host_threads()
+    un, en = _timed_units(
+        lambda: oracle.attention_prefill(q, k, v, H, kvh, hd, start, nq, 1 << 30, sc, threads=n),
+        mt_budget_s, 1024)
+    res = figure(un, en, n)
+    res["one_thread"] = figure(u1, e1, 1)
+    return res
 
 
 def prefill_flops(cfg):
@@ -870,17 +900,27 @@ def run_tinyllama(args, gi, torch, dev, cfg):
                   "pass": bool(worst <= 1e-5)}
     cpu = None
     if not args.no_cpu_baseline:
-        # the whole case on one core: the reference's store and decode loop
+        # the whole case: the reference's decode loop on one core, then with
+        # the q-heads split over every host core the process may use
         Kh, Vh, Qh = K.cpu().numpy(), V.cpu().numpy(), Q.cpu().numpy()
-        t0 = time.perf_counter()
-        for i in range(ND):
-            n = T0 + i + 1
-            for l in range(layers):
-                oracle.attention_decode(Qh[i, l], Kh[l, :n], Vh[l, :n], H, kvh, hd, n, scale)
-        el = time.perf_counter() - t0
-        cpu = {"value": round(ND / el, 2), "unit": "tokens/s", "cores": 1, "kind": "port",
-               "sample": "the whole case (128 decode tokens x 22 layers, 129..256 tokens of "
-                         "context) on 1 thread: %.2f s" % el}
+
+        def whole(threads):
+            t0 = time.perf_counter()
+            for i in range(ND):
+                n = T0 + i + 1
+                for l in range(layers):
+                    oracle.attention_decode(Qh[i, l], Kh[l, :n], Vh[l, :n], H, kvh, hd, n, scale,
+                                            threads=threads)
+            el = time.perf_counter() - t0
+            return {"value": round(ND / el, 2), "unit": "tokens/s", "cores": threads,
+                    "kind": "port",
+                    "sample": "the whole case (128 decode tokens x 22 layers, 129..256 tokens of "
+                              "context) on %d thread%s: %.2f s"
+                              % (threads, "" if threads == 1 else "s", el)}
+
+        one = whole(1)
+        cpu = whole(oracle.host_threads())
+        cpu["one_thread"] = one
     res = {
         "metric": METRIC,
         "value": round(gbs, 2),

@@ -57,6 +57,12 @@ def lib():
                                             ctypes.c_float, _f32p]),
             "ref_attention_prefill": (None, [_f32p, _f32p, _f32p, _f32p, _int, _int, _int, _int,
                                              _int, _int, ctypes.c_float, _f32p]),
+            "ref_attention_decode_mt": (_int, [_f32p, _f32p, _f32p, _f32p, _int, _int, _int, _int,
+                                               ctypes.c_float, _int]),
+            "ref_attention_prefill_mt": (_int, [_f32p, _f32p, _f32p, _f32p, _int, _int, _int, _int,
+                                                _int, _int, ctypes.c_float, _int]),
+            "ref_decode_batch_mt": (_int, [_int, _f32p, _u8p, _u8p, _i64p, _i32p, _int, _f32p,
+                                           _int, _int, _int, ctypes.c_float, _f32p, _f32p, _int]),
             "ref_bytes_per_vec": (_i64, [_int, _int]),
             "ref_kv_write": (None, [_int, _int, _int, _u8p, _u8p, _int, _f32p, _f32p]),
             "ref_kv_widen": (None, [_int, _int, _u8p, _i64, _f32p]),
@@ -270,25 +276,51 @@ def widen(kv_type, kv_dim, stored):
 
 # ---- attention (pkg/engine/forward.go) --------------------------------------
 
-def attention_decode(q, kc, vc, H, KVH, hd, L, scale):
+def host_threads():
+    """Host threads for the multi-threaded oracle: the CPUs this process may
+    run on, at most 16 (the host share of one GPU on the MI355X boxes)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def attention_decode(q, kc, vc, H, KVH, hd, L, scale, threads=1):
     """Decode GQA attention of forward.go:242-267 over float32 caches kc/vc
-    [>=L, KVH*hd]; q [H*hd] -> out [H*hd]."""
+    [>=L, KVH*hd]; q [H*hd] -> out [H*hd].  threads > 1 splits the q-heads
+    over host threads; the result is bit-identical."""
     q = _c(q, np.float32)
     kc = _c(kc, np.float32)
     vc = _c(vc, np.float32)
     out = np.empty(H * hd, np.float32)
+    if threads > 1:
+        rc = lib().ref_attention_decode_mt(_p(q, _f32p), _p(kc, _f32p), _p(vc, _f32p),
+                                           _p(out, _f32p), H, KVH, hd, L, float(scale), threads)
+        if rc != 0:
+            raise MemoryError("ref_attention_decode_mt failed")
+        return out
     scores = np.empty(max(L, 1), np.float32)
     lib().ref_attention_decode(_p(q, _f32p), _p(kc, _f32p), _p(vc, _f32p), _p(out, _f32p),
                                H, KVH, hd, L, float(scale), _p(scores, _f32p))
     return out
 
 
-def attention_prefill(q, kc, vc, H, KVH, hd, start_pos, chunk, max_seq, scale):
-    """Chunked-prefill causal attention of forward.go:547-577; q [chunk, H*hd]."""
+def attention_prefill(q, kc, vc, H, KVH, hd, start_pos, chunk, max_seq, scale, threads=1):
+    """Chunked-prefill causal attention of forward.go:547-577; q [chunk, H*hd].
+    threads > 1 splits the (query, q-head) rows over host threads; the result
+    is bit-identical."""
     q = _c(q, np.float32)
     kc = _c(kc, np.float32)
     vc = _c(vc, np.float32)
     out = np.empty((chunk, H * hd), np.float32)
+    if threads > 1:
+        rc = lib().ref_attention_prefill_mt(_p(q, _f32p), _p(kc, _f32p), _p(vc, _f32p),
+                                            _p(out, _f32p), H, KVH, hd, start_pos, chunk, max_seq,
+                                            float(scale), threads)
+        if rc != 0:
+            raise MemoryError("ref_attention_prefill_mt failed")
+        return out
     scores = np.empty(max(min(start_pos + chunk, max_seq), 1), np.float32)
     lib().ref_attention_prefill(_p(q, _f32p), _p(kc, _f32p), _p(vc, _f32p), _p(out, _f32p),
                                 H, KVH, hd, start_pos, chunk, max_seq, float(scale),
@@ -296,8 +328,11 @@ def attention_prefill(q, kc, vc, H, KVH, hd, start_pos, chunk, max_seq, scale):
     return out
 
 
-def decode_batch(kv_type, q, kcat, vcat, tok_off, seq_lens, H, KVH, hd, scale):
-    """Decode attention for a batch from stored-format caches (CPU baseline)."""
+def decode_batch(kv_type, q, kcat, vcat, tok_off, seq_lens, H, KVH, hd, scale, threads=1):
+    """Decode attention for a batch from stored-format caches (CPU baseline).
+    threads > 1 widens each sequence and splits its q-heads over host
+    threads; the result is bit-identical.  Returns out, or (out, threads
+    that ran) when threads > 1."""
     q = _c(q, np.float32)
     kcat = _c(kcat, np.uint8)
     vcat = _c(vcat, np.uint8)
@@ -305,9 +340,17 @@ def decode_batch(kv_type, q, kcat, vcat, tok_off, seq_lens, H, KVH, hd, scale):
     seq_lens = _c(seq_lens, np.int32)
     batch = seq_lens.size
     out = np.empty((batch, H * hd), np.float32)
-    Lmax = int(seq_lens.max()) if batch else 1
+    Lmax = max(int(seq_lens.max()) if batch else 1, 1)
     wk = np.empty(Lmax * KVH * hd, np.float32)
     wv = np.empty(Lmax * KVH * hd, np.float32)
+    if threads > 1:
+        ran = lib().ref_decode_batch_mt(kv_type, _p(q, _f32p), _p(kcat, _u8p), _p(vcat, _u8p),
+                                        _p(tok_off, _i64p), _p(seq_lens, _i32p), batch,
+                                        _p(out, _f32p), H, KVH, hd, float(scale), _p(wk, _f32p),
+                                        _p(wv, _f32p), threads)
+        if ran < 1:
+            raise MemoryError("ref_decode_batch_mt failed")
+        return out, ran
     sc = np.empty(Lmax, np.float32)
     lib().ref_decode_batch(kv_type, _p(q, _f32p), _p(kcat, _u8p), _p(vcat, _u8p),
                            _p(tok_off, _i64p), _p(seq_lens, _i32p), batch, _p(out, _f32p),

@@ -19,7 +19,7 @@ OUT = os.path.join(HERE, "libcpuref.so")
 
 def build(verbose=False):
     cmd = ["gcc", "-std=c11", "-O2", "-ffp-contract=off", "-fno-fast-math",
-           "-fPIC", "-shared", "-Wall", "-Wextra", "-o", OUT + ".tmp", SRC, "-lm"]
+           "-fPIC", "-shared", "-pthread", "-Wall", "-Wextra", "-o", OUT + ".tmp", SRC, "-lm"]
     if verbose:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)

@@ -34,7 +34,9 @@
  *       the rotation of (1, 0) lands at angle +pos*freq (sign and pairing);
  *       pair norms and the relative-position property of q.k.
  */
+#define _POSIX_C_SOURCE 200809L /* pthread barriers under -std=c11 */
 #include <math.h>
+#include <pthread.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
@@ -340,28 +342,35 @@ float ref_attn_scale(int head_dim)
  * indexed by kv.Key[l][t*kvDim + kvHead*headDim]; q/out are [H][hd].
  * q-head h reads kv head h / (H/KVH) (forward.go:249, config.go:59-64).
  * scores must hold L floats. */
+/* One q-head of forward.go:243-266: out zeroed (243-245), scores over the
+ * first L tokens of kv head kvh (252-255), Softmax, then the weighted V sum
+ * in token order (259-266). */
+static void attend_head(const float *qh, const float *kc, const float *vc,
+                        float *oh, int kvh, int kv_dim, int hd, int L,
+                        float scale, float *scores)
+{
+    for (int d = 0; d < hd; d++)
+        oh[d] = 0.0f;
+    for (int t = 0; t < L; t++)
+        scores[t] = ref_dot_vec_f32(qh, kc + (int64_t)t * kv_dim + kvh * hd, hd) * scale;
+    ref_softmax(scores, L);
+    for (int t = 0; t < L; t++) {
+        const float *vt = vc + (int64_t)t * kv_dim + kvh * hd;
+        float wgt = scores[t];
+        for (int d = 0; d < hd; d++)
+            oh[d] += wgt * vt[d];
+    }
+}
+
 void ref_attention_decode(const float *q, const float *kc, const float *vc,
                           float *out, int H, int KVH, int hd, int L,
                           float scale, float *scores)
 {
     int kv_dim = KVH * hd;
     int kv_mul = H / KVH;
-    for (int i = 0; i < H * hd; i++)
-        out[i] = 0.0f;
-    for (int h = 0; h < H; h++) {
-        const float *qh = q + (int64_t)h * hd;
-        int kvh = h / kv_mul;
-        for (int t = 0; t < L; t++)
-            scores[t] = ref_dot_vec_f32(qh, kc + (int64_t)t * kv_dim + kvh * hd, hd) * scale;
-        ref_softmax(scores, L);
-        float *oh = out + (int64_t)h * hd;
-        for (int t = 0; t < L; t++) {
-            const float *vt = vc + (int64_t)t * kv_dim + kvh * hd;
-            float wgt = scores[t];
-            for (int d = 0; d < hd; d++)
-                oh[d] += wgt * vt[d];
-        }
-    }
+    for (int h = 0; h < H; h++)
+        attend_head(q + (int64_t)h * hd, kc, vc, out + (int64_t)h * hd, h / kv_mul,
+                    kv_dim, hd, L, scale, scores);
 }
 
 /* pkg/engine/forward.go:547-577 (chunked prefill, causal).  The chunk's own
@@ -502,6 +511,204 @@ void ref_decode_batch(int kv_type, const float *q, const uint8_t *kcat,
                              out + (int64_t)b * H * hd, H, KVH, hd, L, scale,
                              scores);
     }
+}
+
+/* ---- the same loops on several host threads ------------------------------ */
+
+/* Work is split by (query, q-head) row, the split the reference's threaded
+ * attention uses (pkg/engine/forward.go:1342-1378 hands heads to
+ * goroutines).  Every row is computed by attend_head exactly as in the
+ * one-thread functions above, so the results are bit-identical to theirs;
+ * only the order in which rows finish differs.  Return 0, or -1 when a
+ * thread or a buffer cannot be had. */
+
+struct mt_job {
+    const float *q, *kc, *vc;
+    float *out;
+    int H, KVH, hd, start, chunk, max_seq;
+    float scale;
+    int next; /* next row, taken with an atomic add */
+    int failed;
+};
+
+static void *mt_prefill_worker(void *arg)
+{
+    struct mt_job *j = (struct mt_job *)arg;
+    int kv_dim = j->KVH * j->hd, kv_mul = j->H / j->KVH;
+    int cap = j->start + j->chunk < j->max_seq ? j->start + j->chunk : j->max_seq;
+    float *scores = (float *)malloc(sizeof(float) * (size_t)(cap > 0 ? cap : 1));
+    if (!scores) {
+        __atomic_store_n(&j->failed, 1, __ATOMIC_RELAXED);
+        return NULL;
+    }
+    const int rows = j->chunk * j->H;
+    for (;;) {
+        int r = __atomic_fetch_add(&j->next, 1, __ATOMIC_RELAXED);
+        if (r >= rows)
+            break;
+        int b = r / j->H, h = r % j->H;
+        int active = j->start + b + 1;
+        if (active > j->max_seq)
+            active = j->max_seq;
+        int64_t off = ((int64_t)b * j->H + h) * j->hd;
+        attend_head(j->q + off, j->kc, j->vc, j->out + off, h / kv_mul, kv_dim, j->hd, active,
+                    j->scale, scores);
+    }
+    free(scores);
+    return NULL;
+}
+
+static int run_threads(void *(*fn)(void *), void *arg, int nthreads)
+{
+    if (nthreads < 1)
+        nthreads = 1;
+    pthread_t *t = (pthread_t *)malloc(sizeof(pthread_t) * (size_t)nthreads);
+    if (!t)
+        return -1;
+    int started = 0, rc = 0;
+    for (; started < nthreads - 1; started++)
+        if (pthread_create(&t[started], NULL, fn, arg) != 0) {
+            rc = -1;
+            break;
+        }
+    fn(arg); /* the calling thread works too */
+    for (int i = 0; i < started; i++)
+        pthread_join(t[i], NULL);
+    free(t);
+    return rc;
+}
+
+/* ref_attention_prefill on nthreads threads (rows taken dynamically, since
+ * causal rows differ in length). */
+int ref_attention_prefill_mt(const float *q, const float *kc, const float *vc,
+                             float *out, int H, int KVH, int hd, int start_pos,
+                             int chunk, int max_seq, float scale, int nthreads)
+{
+    struct mt_job j = {q, kc, vc, out, H, KVH, hd, start_pos, chunk, max_seq, scale, 0, 0};
+    int rc = run_threads(mt_prefill_worker, &j, nthreads);
+    return rc || j.failed ? -1 : 0;
+}
+
+/* ref_attention_decode on nthreads threads: one query at position L-1. */
+int ref_attention_decode_mt(const float *q, const float *kc, const float *vc,
+                            float *out, int H, int KVH, int hd, int L,
+                            float scale, int nthreads)
+{
+    return ref_attention_prefill_mt(q, kc, vc, out, H, KVH, hd, L - 1, 1, L, scale, nthreads);
+}
+
+struct mt_batch {
+    int kv_type, batch, H, KVH, hd, nthreads;
+    const float *q;
+    const uint8_t *kcat, *vcat;
+    const int64_t *tok_off;
+    const int32_t *seq_lens;
+    float *out, *wk, *wv, scale;
+    pthread_mutex_t mu;
+    pthread_cond_t go;
+    int ready; /* set once every thread that will run has started */
+    pthread_barrier_t bar;
+    int next_tid;
+    int failed;
+};
+
+static void *mt_batch_worker(void *arg)
+{
+    struct mt_batch *j = (struct mt_batch *)arg;
+    pthread_mutex_lock(&j->mu);
+    while (!j->ready)
+        pthread_cond_wait(&j->go, &j->mu);
+    pthread_mutex_unlock(&j->mu);
+    const int tid = __atomic_fetch_add(&j->next_tid, 1, __ATOMIC_RELAXED);
+    const int n = j->nthreads, kv_dim = j->KVH * j->hd, kv_mul = j->H / j->KVH;
+    const int64_t bpv = ref_bytes_per_vec(j->kv_type, kv_dim);
+    int lmax = 1;
+    for (int b = 0; b < j->batch; b++)
+        if (j->seq_lens[b] > lmax)
+            lmax = j->seq_lens[b];
+    float *scores = (float *)malloc(sizeof(float) * (size_t)lmax);
+    if (!scores)
+        __atomic_store_n(&j->failed, 1, __ATOMIC_RELAXED);
+    for (int b = 0; b < j->batch; b++) {
+        const int L = j->seq_lens[b];
+        /* widen this thread's share of the sequence's tokens */
+        const int64_t t0 = (int64_t)L * tid / n, t1 = (int64_t)L * (tid + 1) / n;
+        ref_kv_widen(j->kv_type, kv_dim, j->kcat + (j->tok_off[b] + t0) * bpv, t1 - t0,
+                     j->wk + t0 * kv_dim);
+        ref_kv_widen(j->kv_type, kv_dim, j->vcat + (j->tok_off[b] + t0) * bpv, t1 - t0,
+                     j->wv + t0 * kv_dim);
+        pthread_barrier_wait(&j->bar);
+        for (int h = tid; scores && h < j->H; h += n) {
+            int64_t off = ((int64_t)b * j->H + h) * j->hd;
+            attend_head(j->q + off, j->wk, j->wv, j->out + off, h / kv_mul, kv_dim, j->hd, L,
+                        j->scale, scores);
+        }
+        /* every row of this sequence is done before its buffers are reused */
+        pthread_barrier_wait(&j->bar);
+    }
+    free(scores);
+    return NULL;
+}
+
+/* ref_decode_batch on up to nthreads threads: each sequence is widened by
+ * all threads (a share of its tokens each), then its q-heads are split over
+ * them.  wk/wv must hold max(L)*kv_dim floats.  Returns the number of
+ * threads that ran (fewer than asked if some could not be started), or -1. */
+int ref_decode_batch_mt(int kv_type, const float *q, const uint8_t *kcat,
+                        const uint8_t *vcat, const int64_t *tok_off,
+                        const int32_t *seq_lens, int batch, float *out, int H,
+                        int KVH, int hd, float scale, float *wk, float *wv,
+                        int nthreads)
+{
+    if (nthreads < 1)
+        nthreads = 1;
+    struct mt_batch j;
+    memset(&j, 0, sizeof j);
+    j.kv_type = kv_type;
+    j.batch = batch;
+    j.H = H;
+    j.KVH = KVH;
+    j.hd = hd;
+    j.q = q;
+    j.kcat = kcat;
+    j.vcat = vcat;
+    j.tok_off = tok_off;
+    j.seq_lens = seq_lens;
+    j.out = out;
+    j.wk = wk;
+    j.wv = wv;
+    j.scale = scale;
+    pthread_t *t = (pthread_t *)malloc(sizeof(pthread_t) * (size_t)nthreads);
+    if (!t)
+        return -1;
+    pthread_mutex_init(&j.mu, NULL);
+    pthread_cond_init(&j.go, NULL);
+    /* threads wait at the gate until the barrier is sized for those that
+     * actually started */
+    int started = 0;
+    for (; started < nthreads - 1; started++)
+        if (pthread_create(&t[started], NULL, mt_batch_worker, &j) != 0)
+            break;
+    j.nthreads = started + 1;
+    int rc = pthread_barrier_init(&j.bar, NULL, (unsigned)j.nthreads) == 0 ? 0 : -1;
+    if (rc) {
+        /* the workers still pass the gate; with no sequences they only
+         * allocate and exit */
+        j.batch = 0;
+    }
+    pthread_mutex_lock(&j.mu);
+    j.ready = 1;
+    pthread_cond_broadcast(&j.go);
+    pthread_mutex_unlock(&j.mu);
+    mt_batch_worker(&j);
+    for (int k = 0; k < started; k++)
+        pthread_join(t[k], NULL);
+    free(t);
+    if (rc == 0)
+        pthread_barrier_destroy(&j.bar);
+    pthread_cond_destroy(&j.go);
+    pthread_mutex_destroy(&j.mu);
+    return rc || j.failed ? -1 : j.nthreads;
 }
 
 /* ---- rotary position embedding ------------------------------------------- */

@@ -295,6 +295,40 @@ def test_prefill_equals_decode_per_token(oracle):
     assert np.array_equal(capped[10], oracle.attention_decode(q[10], kc, vc, H, KVH, hd, 25, sc))
 
 
+@pytest.mark.parametrize("threads", [2, 3, 8])
+def test_threaded_oracle_is_bit_identical(oracle, threads):
+    """The multi-threaded forms split (query, q-head) rows over threads
+    (forward.go:1342-1378 splits heads over goroutines); each row is the
+    one-thread computation, so every output bit must match, including the
+    empty context and the ring cap."""
+    H, KVH, hd = 16, 4, 64
+    kc = oracle.normal(31, (300, KVH * hd))
+    vc = oracle.normal(32, (300, KVH * hd))
+    q = oracle.normal(33, (40, H * hd))
+    sc = oracle.attn_scale(hd)
+    for L in (0, 1, 17, 300):
+        one = oracle.attention_decode(q[0], kc, vc, H, KVH, hd, L, sc)
+        assert np.array_equal(one, oracle.attention_decode(q[0], kc, vc, H, KVH, hd, L, sc,
+                                                           threads=threads))
+    for start, chunk, cap in ((0, 40, 8192), (200, 40, 8192), (250, 40, 270)):
+        one = oracle.attention_prefill(q, kc, vc, H, KVH, hd, start, chunk, cap, sc)
+        mt = oracle.attention_prefill(q, kc, vc, H, KVH, hd, start, chunk, cap, sc,
+                                      threads=threads)
+        assert np.array_equal(one, mt)
+    # batch decode from stored fp16 / q8_0 vectors, ragged lengths
+    lens = np.array([300, 0, 5, 123], np.int32)
+    off = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int64)
+    for kt in (1, 2):
+        ks = oracle.store_vectors(kt, oracle.normal(34, (int(lens.sum()), KVH * hd)))
+        vs = oracle.store_vectors(kt, oracle.normal(35, (int(lens.sum()), KVH * hd)))
+        qb = q[:lens.size]
+        one = oracle.decode_batch(kt, qb, ks, vs, off, lens, H, KVH, hd, sc)
+        mt, ran = oracle.decode_batch(kt, qb, ks, vs, off, lens, H, KVH, hd, sc, threads=threads)
+        assert ran == threads
+        assert np.array_equal(one, mt)
+        assert not one[1].any()
+
+
 # ---- KV store / paged pool -----------------------------------------------------
 
 def test_kv_context_wrap(oracle):
