@@ -357,6 +357,26 @@ def _ptr(t, dtype=None, what="tensor"):
     return _vp(t.data_ptr())
 
 
+def _need(ok, msg):
+    """Shape check of a wrapper: a mismatch would send the kernels past the
+    ends of the buffers, so it is refused here as GI_ERR_BAD_ARG."""
+    if not ok:
+        raise GIError(-3, msg)
+
+
+def _numel(t):
+    return 0 if t is None else int(t.numel())
+
+
+def _tables(block_tables, batch, what="block_tables"):
+    """max_blocks of a [batch, max_blocks] table (0 for an empty batch)."""
+    if batch == 0:
+        return 0
+    _need(block_tables is not None and block_tables.dim() == 2 and int(block_tables.shape[0]) == batch,
+          "%s must be [batch=%d, max_blocks]" % (what, batch))
+    return int(block_tables.shape[1])
+
+
 class PagedKVCache:
     """Device page pool for num_layers layers (one page id covers every
     layer, like KVBlock in paged_kv.go:13-38).  kv_type: KV_F32, KV_F16,
@@ -431,6 +451,9 @@ class PagedKVCache:
         slots[i]) of one layer (KVCache.Write, kvcache.go:146-180)."""
         import torch
         n = int(block_ids.numel())
+        _need(_numel(slots) == n, "Write: slots must hold %d entries" % n)
+        _need(_numel(k) == n * self.kv_dim and _numel(v) == n * self.kv_dim,
+              "Write: k and v must be [%d, %d]" % (n, self.kv_dim))
         _check(lib().gi_paged_append(self._h, layer, n, _ptr(block_ids, torch.int32, "block_ids"),
                                      _ptr(slots, torch.int32, "slots"),
                                      _ptr(k, torch.float32, "k"), _ptr(v, torch.float32, "v")))
@@ -438,9 +461,12 @@ class PagedKVCache:
     def WriteAtLen(self, layer, block_tables, seq_lens, k, v):
         import torch
         batch = int(seq_lens.numel())
+        mb = _tables(block_tables, batch)
+        _need(_numel(k) == batch * self.kv_dim and _numel(v) == batch * self.kv_dim,
+              "WriteAtLen: k and v must be [%d, %d]" % (batch, self.kv_dim))
         _check(lib().gi_paged_append_at_len(
             self._h, layer, batch, _ptr(block_tables, torch.int32, "block_tables"),
-            int(block_tables.shape[1]) if batch else 0, _ptr(seq_lens, torch.int32, "seq_lens"),
+            mb, _ptr(seq_lens, torch.int32, "seq_lens"),
             _ptr(k, torch.float32, "k"), _ptr(v, torch.float32, "v")))
 
     def Get(self, layer, block_table, n_tok, widen=False):
@@ -449,6 +475,8 @@ class PagedKVCache:
         widen=True: float32 [n_tok, kv_dim]."""
         import torch
         dev = block_table.device
+        _need(n_tok >= 0 and _numel(block_table) * self.page_tokens >= n_tok,
+              "Get: block_table maps fewer than %d tokens" % n_tok)
         if widen:
             ko = torch.empty((n_tok, self.kv_dim), dtype=torch.float32, device=dev)
         else:
@@ -475,12 +503,16 @@ class PagedKVCache:
         [batch, num_heads*head_dim] float32."""
         import torch
         batch = int(seq_lens.numel())
+        mb = _tables(block_tables, batch)
+        qn = batch * num_heads * self.head_dim
+        _need(_numel(q) == qn and _numel(out) == qn,
+              "AttentionGQA: q and out must be [%d, %d]" % (batch, num_heads * self.head_dim))
         if max_seq_len is None:
-            max_seq_len = int(seq_lens.max().item()) if batch else 0
+            max_seq_len = 0   # the kernels read the lengths on the device
         _check(lib().gi_paged_decode_attention(
             self._h, layer, batch, num_heads, _ptr(q, torch.float32, "q"),
             _ptr(out, torch.float32, "out"), _ptr(block_tables, torch.int32, "block_tables"),
-            int(block_tables.shape[1]) if batch else 0, _ptr(seq_lens, torch.int32, "seq_lens"),
+            mb, _ptr(seq_lens, torch.int32, "seq_lens"),
             int(max_seq_len), float(attn_scale)))
 
     def DecodeStep(self, out, q, k, v, layer, block_tables, seq_lens, num_heads, attn_scale,
@@ -489,13 +521,19 @@ class PagedKVCache:
         attention over seq_lens[b] tokens (forward.go:236-267)."""
         import torch
         batch = int(seq_lens.numel())
+        mb = _tables(block_tables, batch)
+        qn = batch * num_heads * self.head_dim
+        _need(_numel(q) == qn and _numel(out) == qn,
+              "DecodeStep: q and out must be [%d, %d]" % (batch, num_heads * self.head_dim))
+        _need(_numel(k) == batch * self.kv_dim and _numel(v) == batch * self.kv_dim,
+              "DecodeStep: k and v must be [%d, %d]" % (batch, self.kv_dim))
         if max_seq_len is None:
-            max_seq_len = int(seq_lens.max().item()) if batch else 0
+            max_seq_len = 0
         _check(lib().gi_paged_decode_step(
             self._h, layer, batch, num_heads, _ptr(q, torch.float32, "q"),
             _ptr(k, torch.float32, "k"), _ptr(v, torch.float32, "v"),
             _ptr(out, torch.float32, "out"), _ptr(block_tables, torch.int32, "block_tables"),
-            int(block_tables.shape[1]) if batch else 0, _ptr(seq_lens, torch.int32, "seq_lens"),
+            mb, _ptr(seq_lens, torch.int32, "seq_lens"),
             int(max_seq_len), float(attn_scale)))
 
     # -- RoPE fused with the append (forward.go:228-240, 527-545) ------------
@@ -514,6 +552,12 @@ class PagedKVCache:
             num_heads = int(q.shape[-1]) // self.head_dim
             if q_out is None:
                 q_out = q
+            _need(_numel(q) == n * num_heads * self.head_dim and _numel(q_out) == _numel(q),
+                  "RoPEWrite: q and q_out must be [%d, num_heads * %d]" % (n, self.head_dim))
+        _need(_numel(slots) == n and _numel(positions) == n, "RoPEWrite: positions and slots "
+              "must hold %d entries" % n)
+        _need(_numel(k) == n * self.kv_dim and _numel(v) == n * self.kv_dim,
+              "RoPEWrite: k and v must be [%d, %d]" % (n, self.kv_dim))
         _check(lib().gi_paged_rope_append(
             self._h, layer, n, num_heads, _ptr(positions, torch.int32, "positions"),
             _ptr(block_ids, torch.int32, "block_ids"), _ptr(slots, torch.int32, "slots"),
@@ -524,14 +568,19 @@ class PagedKVCache:
         """Decode form: token b at position seq_lens[b]-1 of sequence b."""
         import torch
         batch = int(seq_lens.numel())
+        mb = _tables(block_tables, batch)
         num_heads = 0
         if q is not None:
             num_heads = int(q.shape[-1]) // self.head_dim
             if q_out is None:
                 q_out = q
+            _need(_numel(q) == batch * num_heads * self.head_dim and _numel(q_out) == _numel(q),
+                  "RoPEWriteAtLen: q and q_out must be [%d, num_heads * %d]" % (batch, self.head_dim))
+        _need(_numel(k) == batch * self.kv_dim and _numel(v) == batch * self.kv_dim,
+              "RoPEWriteAtLen: k and v must be [%d, %d]" % (batch, self.kv_dim))
         _check(lib().gi_paged_rope_append_at_len(
             self._h, layer, batch, num_heads, _ptr(block_tables, torch.int32, "block_tables"),
-            int(block_tables.shape[1]) if batch else 0, _ptr(seq_lens, torch.int32, "seq_lens"),
+            mb, _ptr(seq_lens, torch.int32, "seq_lens"),
             _ptr(q, torch.float32, "q"), _ptr(q_out, torch.float32, "q_out"),
             _ptr(k, torch.float32, "k"), _ptr(v, torch.float32, "v")))
 
@@ -541,13 +590,19 @@ class PagedKVCache:
         at position seq_lens[b]-1, k/v appended, then decode attention."""
         import torch
         batch = int(seq_lens.numel())
+        mb = _tables(block_tables, batch)
+        qn = batch * num_heads * self.head_dim
+        _need(_numel(q) == qn and _numel(out) == qn,
+              "RoPEDecodeStep: q and out must be [%d, %d]" % (batch, num_heads * self.head_dim))
+        _need(_numel(k) == batch * self.kv_dim and _numel(v) == batch * self.kv_dim,
+              "RoPEDecodeStep: k and v must be [%d, %d]" % (batch, self.kv_dim))
         if max_seq_len is None:
-            max_seq_len = int(seq_lens.max().item()) if batch else 0
+            max_seq_len = 0
         _check(lib().gi_paged_rope_decode_step(
             self._h, layer, batch, num_heads, _ptr(q, torch.float32, "q"),
             _ptr(k, torch.float32, "k"), _ptr(v, torch.float32, "v"),
             _ptr(out, torch.float32, "out"), _ptr(block_tables, torch.int32, "block_tables"),
-            int(block_tables.shape[1]) if batch else 0, _ptr(seq_lens, torch.int32, "seq_lens"),
+            mb, _ptr(seq_lens, torch.int32, "seq_lens"),
             int(max_seq_len), float(attn_scale)))
 
     def AttentionGQABatch(self, out, q, layer, block_tables, start_pos, num_heads, attn_scale,
@@ -556,10 +611,15 @@ class PagedKVCache:
         [batch, chunk_len, num_heads*head_dim] float32."""
         import torch
         batch = int(start_pos.numel())
+        mb = _tables(block_tables, batch)
+        qn = batch * chunk_len * num_heads * self.head_dim
+        _need(_numel(q) == qn and _numel(out) == qn,
+              "AttentionGQABatch: q and out must be [%d, %d, %d]"
+              % (batch, chunk_len, num_heads * self.head_dim))
         _check(lib().gi_paged_prefill_attention(
             self._h, layer, batch, chunk_len, num_heads, _ptr(q, torch.float32, "q"),
             _ptr(out, torch.float32, "out"), _ptr(block_tables, torch.int32, "block_tables"),
-            int(block_tables.shape[1]) if batch else 0, _ptr(start_pos, torch.int32, "start_pos"),
+            mb, _ptr(start_pos, torch.int32, "start_pos"),
             float(attn_scale)))
 
 

@@ -29,8 +29,6 @@ HIP_FLAGS = [
     "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-I" + CSRC, "-I" + INC,
 ]
-# Extra hipcc arguments (for example tuning macros such as -DGI_PREFILL_NCG=1).
-HIP_FLAGS += os.environ.get("GI_EXTRA_HIPFLAGS", "").split()
 CXX_FLAGS = ["-O2", "-fPIC", "-std=c++17", "-Wall", "-Wextra", "-I" + CSRC, "-I" + INC]
 
 

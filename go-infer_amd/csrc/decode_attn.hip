@@ -11,6 +11,7 @@
 // from HBM once per decode step.
 #include "gi_common.h"
 #include "gi_kernels.h"
+#include "split_plan.h"
 
 #include <math.h>
 
@@ -103,21 +104,36 @@ __global__ __launch_bounds__(NT) void attn_valu(DecodeArgs a)
     static_assert(TOK % NG == 0, "tile tokens split evenly over P*V groups");
 
     const PoolLayout &L = a.L;
-    const int split = blockIdx.x, kvh = blockIdx.y, qrow = blockIdx.z;
-    const int b = qrow / a.n_q, qi = qrow - b * a.n_q;
+    const int kvh = blockIdx.y;
     const int tid = threadIdx.x;
     const int H = a.num_heads;
     const int h0 = kvh * G;
     const int P = L.page_tokens;
-    int len = a.start_pos ? a.start_pos[b] + qi + 1 : a.seq_lens[b];
-    if (len > a.max_blocks * P) {
-        // More tokens than the block table maps: read what it maps.
-        if (tid == 0 && split == 0 && a.status)
-            atomicOr(a.status, FLAG_BAD_SLOT);
-        len = a.max_blocks * P;
+    // decode: this workgroup's item of the split plan; prefill: query row
+    // blockIdx.z whole, one workgroup per (query, kv head)
+    PlanItem it{};
+    int b, qi, t0, t1;
+    if (a.plan_target > 0) {
+        if (!plan_item<NT>(a, blockIdx.x, it))
+            return;
+        b = it.b;
+        qi = 0;
+        t0 = it.t0;
+        t1 = it.t1;
+    } else {
+        b = blockIdx.z / a.n_q;
+        qi = blockIdx.z - b * a.n_q;
+        int len = a.start_pos ? a.start_pos[b] + qi + 1 : a.seq_lens[b];
+        if (len > a.max_blocks * P) {
+            // More tokens than the block table maps: read what it maps.
+            if (tid == 0 && a.status)
+                atomicOr(a.status, FLAG_BAD_SLOT);
+            len = a.max_blocks * P;
+        }
+        t0 = 0;
+        t1 = len;
     }
-    const int t0 = split * a.split_tokens;
-    const int t1 = min(len, t0 + a.split_tokens);
+    const int qrow = b * a.n_q + qi;
     const int32_t *bt = a.block_tables + (int64_t)b * a.max_blocks;
     const int64_t qbase = (int64_t)qrow * H;
 
@@ -126,12 +142,11 @@ __global__ __launch_bounds__(NT) void attn_valu(DecodeArgs a)
     __shared__ float s_m[G], s_l[G];
     __shared__ float s_acc[NG][G][HD];
 
-    float *wsp = nullptr;
-    if (a.num_splits > 1)
-        wsp = a.ws + (((int64_t)qrow * L.num_kv_heads + kvh) * a.num_splits + split) * (G * (HD + 2));
+    // partial slot when the sequence is split over several items
+    float *wsp = a.plan_target > 0 && it.nsplit > 1 ? plan_slot(a, blockIdx.x, kvh, G, HD) : nullptr;
 
     if (t0 >= t1) {
-        // Empty split: partial with m = -inf, l = 0 (or zero output when the
+        // Empty range: partial with m = -inf, l = 0 (or zero output when the
         // whole sequence is empty).
         for (int e = tid; e < G * HD; e += NT) {
             if (wsp)
@@ -143,6 +158,8 @@ __global__ __launch_bounds__(NT) void attn_valu(DecodeArgs a)
             wsp[G * HD + 2 * tid] = -INFINITY;
             wsp[G * HD + 2 * tid + 1] = 0.0f;
         }
+        if (wsp)
+            merge_if_last<NT>(a, it, blockIdx.x, kvh, G, HD);
         return;
     }
 
@@ -267,37 +284,8 @@ __global__ __launch_bounds__(NT) void attn_valu(DecodeArgs a)
             wsp[G * HD + 2 * tid + 1] = s_l[tid];
         }
     }
-}
-
-// Merges split partials: out = sum_s acc_s e^(m_s - M) / sum_s l_s e^(m_s - M).
-// One workgroup per (query row, head), one thread per output dimension.
-__global__ __launch_bounds__(256) void merge_splits(float *__restrict__ out,
-                                                    const float *__restrict__ ws, int H, int KVH,
-                                                    int HD, int splits)
-{
-    const int h = blockIdx.x, qrow = blockIdx.y;
-    const int G = H / KVH;
-    const int kvh = h / G, g = h - kvh * G;
-    const int64_t stride = (int64_t)G * (HD + 2);
-    const float *w0 = ws + ((int64_t)qrow * KVH + kvh) * splits * stride;
-    float M = -INFINITY;
-    for (int s = 0; s < splits; s++)
-        M = fmaxf(M, w0[s * stride + G * HD + 2 * g]);
-    for (int d = threadIdx.x; d < HD; d += blockDim.x) {
-        float num = 0.0f, den = 0.0f;
-        if (M != -INFINITY) {
-            for (int s = 0; s < splits; s++) {
-                const float *w = w0 + s * stride;
-                const float m = w[G * HD + 2 * g];
-                if (m == -INFINITY)
-                    continue;
-                const float f = expf(m - M);
-                num = fmaf(w[g * HD + d], f, num);
-                den = fmaf(w[G * HD + 2 * g + 1], f, den);
-            }
-        }
-        out[((int64_t)qrow * H + h) * HD + d] = den > 0.0f ? num / den : 0.0f;
-    }
+    if (wsp)
+        merge_if_last<NT>(a, it, blockIdx.x, kvh, G, HD);
 }
 
 template <int KT>
@@ -318,50 +306,31 @@ hipError_t launch_valu_kt(const DecodeArgs &a, dim3 grid, hipStream_t st)
 
 } // namespace
 
-size_t decode_workspace_bytes(const PoolLayout &L, int batch, int num_heads, int num_splits)
+void decode_plan(const PoolLayout &L, int num_cus, DecodeArgs &a)
 {
-    if (num_splits <= 1)
-        return 0;
-    const int G = num_heads / L.num_kv_heads;
-    return (size_t)batch * L.num_kv_heads * num_splits * G * (L.head_dim + 2) * sizeof(float);
-}
-
-// Split-K planning: enough (split, kv head, sequence) workgroups for about
-// GI_DECODE_WG_PER_CU per CU, each split at least GI_DECODE_MIN_SPLIT tokens.
-// Measured on MI355X: 2 and 1024 beat finer splits (4/512, 8/256, 16/128) on
-// both 32 ragged sequences of 512-4096 tokens and 8 sequences of 32768, since
-// every workgroup pays a fixed cost (query load, cross-wave merge, partials).
-#ifndef GI_DECODE_WG_PER_CU
-#define GI_DECODE_WG_PER_CU 2
-#endif
-#ifndef GI_DECODE_MIN_SPLIT
-#define GI_DECODE_MIN_SPLIT 1024
-#endif
-
-void decode_plan(const PoolLayout &L, int batch, int num_heads, int max_len, int num_cus,
-                 int *split_tokens, int *num_splits)
-{
-    (void)num_heads;
-    // Split unit: whole page pairs and a multiple of 64 tokens.
+    // Split unit: whole page pairs and a multiple of 64 tokens (the matrix-core
+    // kernel's waves take 32-token blocks four at a time).
     int unit = 2 * L.page_tokens;
     while (unit % 64)
         unit += 2 * L.page_tokens;
-    if (max_len < 1)
-        max_len = 1;
-    const int64_t pairs = (int64_t)batch * L.num_kv_heads;
-    const int64_t target = (int64_t)GI_DECODE_WG_PER_CU * (num_cus > 0 ? num_cus : 256);
-    int splits = (int)((target + pairs - 1) / pairs);
-    // A minimum of tokens per split keeps the merge negligible.
-    int max_splits = (max_len + GI_DECODE_MIN_SPLIT - 1) / GI_DECODE_MIN_SPLIT;
-    if (splits > max_splits)
-        splits = max_splits;
-    if (splits < 1)
-        splits = 1;
-    int per = (max_len + splits - 1) / splits;
-    per = (per + unit - 1) / unit * unit;
-    splits = (max_len + per - 1) / per;
-    *split_tokens = per;
-    *num_splits = splits;
+    const int wg = kDecodeWgPerCu * (num_cus > 0 ? num_cus : 256);
+    a.plan_target = max(1, (wg + L.num_kv_heads - 1) / L.num_kv_heads);
+    a.plan_min = (kDecodeMinSplit + unit - 1) / unit * unit;
+    a.plan_unit = unit;
+}
+
+int decode_grid_items(const DecodeArgs &a) { return a.batch + a.plan_target; }
+
+size_t decode_counter_bytes(const PoolLayout &L, int batch)
+{
+    return ((size_t)batch * L.num_kv_heads * sizeof(int) + 255) / 256 * 256;
+}
+
+size_t decode_workspace_bytes(const PoolLayout &L, int batch, int num_heads, int grid_items)
+{
+    const int G = num_heads / L.num_kv_heads;
+    return decode_counter_bytes(L, batch) +
+           (size_t)grid_items * L.num_kv_heads * G * (L.head_dim + 2) * sizeof(float);
 }
 
 int decode_kernel_kind(const PoolLayout &L, int num_heads, int requested)
@@ -378,23 +347,16 @@ hipError_t launch_decode(const DecodeArgs &a, hipStream_t st)
     if (a.num_heads % L.num_kv_heads)
         return hipErrorInvalidValue;
     const int n_q = a.n_q > 0 ? a.n_q : 1;
-    hipError_t e;
-    if (n_q == 1 && !a.start_pos && decode_kernel_kind(L, a.num_heads, a.kernel) == 1) {
-        e = launch_decode_mfma(a, st);
-    } else {
-        dim3 grid(a.num_splits, L.num_kv_heads, a.batch * n_q);
-        switch (L.kv_type) {
-        case KV_F32: e = launch_valu_kt<KV_F32>(a, grid, st); break;
-        case KV_F16: e = launch_valu_kt<KV_F16>(a, grid, st); break;
-        case KV_Q4_0: e = launch_valu_kt<KV_Q4_0>(a, grid, st); break;
-        default: e = launch_valu_kt<KV_Q8_0>(a, grid, st); break;
-        }
+    if (a.plan_target > 0 && n_q == 1 && !a.start_pos && decode_kernel_kind(L, a.num_heads, a.kernel) == 1)
+        return launch_decode_mfma(a, st);
+    dim3 grid = a.plan_target > 0 ? dim3(decode_grid_items(a), L.num_kv_heads, 1)
+                                  : dim3(1, L.num_kv_heads, a.batch * n_q);
+    switch (L.kv_type) {
+    case KV_F32: return launch_valu_kt<KV_F32>(a, grid, st);
+    case KV_F16: return launch_valu_kt<KV_F16>(a, grid, st);
+    case KV_Q4_0: return launch_valu_kt<KV_Q4_0>(a, grid, st);
+    default: return launch_valu_kt<KV_Q8_0>(a, grid, st);
     }
-    if (e != hipSuccess || a.num_splits <= 1)
-        return e;
-    hipLaunchKernelGGL(merge_splits, dim3(a.num_heads, a.batch * n_q), dim3(min(L.head_dim, 256)),
-                       0, st, a.out, a.ws, a.num_heads, L.num_kv_heads, L.head_dim, a.num_splits);
-    return hipGetLastError();
 }
 
 hipError_t launch_prefill(const PrefillArgs &p, hipStream_t st)
@@ -416,13 +378,11 @@ hipError_t launch_prefill(const PrefillArgs &p, hipStream_t st)
     a.start_pos = p.start_pos;
     a.num_heads = p.num_heads;
     a.scale = p.scale;
-    a.split_tokens = 1 << 30;
-    a.num_splits = 1;
+    a.plan_target = 0; // one workgroup per (query, kv head), no split
     a.ws = nullptr;
+    a.plan_cnt = nullptr;
     a.status = p.status;
     a.kernel = 0;
-    if (p.chunk_len <= 0 || p.batch <= 0)
-        return hipSuccess;
     return launch_decode(a, st);
 }
 

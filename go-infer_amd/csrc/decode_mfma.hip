@@ -38,6 +38,7 @@
 #include "gi_common.h"
 #include "gi_kernels.h"
 #include "mfma_ops.h"
+#include "split_plan.h"
 
 #include <math.h>
 
@@ -55,9 +56,7 @@ typedef uint16_t us2 __attribute__((ext_vector_type(2)));
 
 // Cache policy of the direct global->LDS loads (2: non-temporal, which
 // measured slower for q8_0 pages and within noise for q4_0).
-#ifndef GI_DECODE_LDS_AUX
-#define GI_DECODE_LDS_AUX 0
-#endif
+constexpr int kDecodeLdsAux = 0;
 
 namespace mfma_decode {
 
@@ -88,7 +87,7 @@ __device__ __forceinline__ h8 ld16(const uint8_t *p)
 // (Plain scalars rather than a struct: a struct carried across the loop is
 // not promoted to registers by the compiler.)
 __device__ __forceinline__ void block_pages(const DecodeArgs &a, const int32_t *bt, int base, int t1,
-                                            int64_t &pA, int64_t &pB, int &sA, int &sB, bool &ok)
+                                            int64_t &pA, int64_t &pB, int &sA, int &sB, int &ok)
 {
     typedef const __attribute__((address_space(4))) int32_t *const_i32;
     const PoolLayout &L = a.L;
@@ -102,8 +101,10 @@ __device__ __forceinline__ void block_pages(const DecodeArgs &a, const int32_t *
     pB = base + 16 < t1 ? (int64_t)cb[ib] : pA;
     const bool okA = pA >= 0 && pA < L.num_pages;
     const bool okB = pB >= 0 && pB < L.num_pages;
-    ok = okA && okB;
-    if (!ok) {
+    // bit 0: tokens 0-15 of the block are on a page of the pool, bit 1:
+    // tokens 16-31; the tokens of a rejected page are skipped
+    ok = (okA ? 1 : 0) | (okB ? 2 : 0);
+    if (ok != 3) {
         if ((threadIdx.x & 63) == 0 && a.status)
             atomicOr(a.status, FLAG_BAD_PAGE);
         if (!okA)
@@ -250,7 +251,7 @@ __device__ __forceinline__ void issue_q(const DecodeArgs &a, int64_t pA, int64_t
         const int kk = kt >> 1, tk = 8 * (jj >> 2) + (jj & 3) + 4 * (kt & 1);
         const uint8_t *src = (tk < 16 ? gA + (int64_t)(sA + tk) * RB : gB + (int64_t)(sB + tk - 16) * RB) +
                              koff + kk * CB + 16 * gp;
-        __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.k[1024 * q], 16, 0, GI_DECODE_LDS_AUX);
+        __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.k[1024 * q], 16, 0, kDecodeLdsAux);
     }
 #pragma unroll
     for (int q = 0; q < Q::NLOAD; q++) {
@@ -258,7 +259,7 @@ __device__ __forceinline__ void issue_q(const DecodeArgs &a, int64_t pA, int64_t
         const int jj = (sl >> 1) & 15, r = sl >> 5;
         const int h = (sl & 1) ^ ((jj >> 3) & 1);
         const uint8_t *src = (h ? gB + sB : gA + sA) + voff + (int64_t)(16 * r + jj) * P;
-        __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.v[1024 * q], 16, 0, GI_DECODE_LDS_AUX);
+        __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.v[1024 * q], 16, 0, kDecodeLdsAux);
     }
     // Both scale planes in one 16-byte load of 32 lanes: lane c < 16 fills
     // ks bytes 16c .. 16c+15, lane 16 + c fills vs bytes 16c .. 16c+15.  The
@@ -276,7 +277,7 @@ __device__ __forceinline__ void issue_q(const DecodeArgs &a, int64_t pA, int64_t
         const uint8_t *src = pg + (lane < 16 ? koffs : voffs);
         const bool use = lane < 16 ? o < 32 * KK : db < KK;
         if (lane < 32 && use)
-            __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.ks[0], 16, 0, GI_DECODE_LDS_AUX);
+            __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.ks[0], 16, 0, kDecodeLdsAux);
     }
 }
 
@@ -363,7 +364,7 @@ __device__ __forceinline__ void issue_f32(const DecodeArgs &a, int64_t pA, int64
     for (int q = 0; q < F32Stage<HD>::NLOAD; q++) {
         const int p = q & 1;
         const uint8_t *src = (p ? kB : kA) + ln.k[p] + (4 * ((q >> 1) & 1) * HD * 4 + 128 * (q >> 2));
-        __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.k[1024 * q], 16, 0, GI_DECODE_LDS_AUX);
+        __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.k[1024 * q], 16, 0, kDecodeLdsAux);
     }
     // V: slot 64q + lane holds dimension 16 (q >> 1) + 8 (q & 1) + jl, block
     // tokens 4c .. 4c + 3 (page A for c < 4)
@@ -373,7 +374,7 @@ __device__ __forceinline__ void issue_f32(const DecodeArgs &a, int64_t pA, int64
     for (int q = 0; q < F32Stage<HD>::NLOAD; q++) {
         const int p = q & 1;
         const uint8_t *src = vbase[p] + ln.v[p] + (int64_t)(16 * (q >> 1) + 8 * p) * P * 4;
-        __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.v[1024 * q], 16, 0, GI_DECODE_LDS_AUX);
+        __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.v[1024 * q], 16, 0, kDecodeLdsAux);
     }
 }
 
@@ -427,7 +428,7 @@ __device__ __forceinline__ float pow2_recip(float x)
 // by ksc and V by vsc (running powers of two, updated here); when vsc changes
 // the accumulators are rescaled to the new one.
 template <int HD>
-__device__ __forceinline__ void read_f32(const F32Stage<HD> &Sf, int j, int g, int base, bool ok, int t1,
+__device__ __forceinline__ void read_f32(const F32Stage<HD> &Sf, int j, int g, int base, int ok, int t1,
                                          h8 *kh0, h8 *kh1, h8 *kl0, h8 *kl1, h8 *vh, h8 *vl, float &ksc,
                                          float &vsc, State<HD> &S, float neg1)
 {
@@ -458,11 +459,13 @@ __device__ __forceinline__ void read_f32(const F32Stage<HD> &Sf, int j, int g, i
             vf[nb][4 * h + 2] = w.z;
             vf[nb][4 * h + 3] = w.w;
         }
-    if (base + 32 > t1 || !ok) {
+    if (base + 32 > t1 || ok != 3) {
         const int tk0 = 8 * (j >> 2) + (j & 3);
+        const bool okk = (ok >> (j >> 3)) & 1; // K rows: tokens 16-31 in lanes j >= 8
+        const bool okv = (ok >> (g >> 1)) & 1; // V rows: tokens 8g .. 8g+7
 #pragma unroll
         for (int t = 0; t < 2; t++) {
-            const bool live = ok && base + tk0 + 4 * t < t1;
+            const bool live = okk && base + tk0 + 4 * t < t1;
 #pragma unroll
             for (int kk = 0; kk < KK; kk++)
 #pragma unroll
@@ -471,7 +474,7 @@ __device__ __forceinline__ void read_f32(const F32Stage<HD> &Sf, int j, int g, i
         }
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            const bool live = ok && base + 8 * g + i < t1;
+            const bool live = okv && base + 8 * g + i < t1;
 #pragma unroll
             for (int nb = 0; nb < NB; nb++)
                 vf[nb][i] = live ? vf[nb][i] : 0.0f;
@@ -612,7 +615,7 @@ __device__ __forceinline__ void qk(const h8 *k0, const h8 *k1, const h8 *qh, con
 // that column already holds the head's full score), one product; the two
 // output rows of a head are added in the final merge.
 template <int HD, int GP, bool VLO = false>
-__device__ __forceinline__ void softmax_pv(f4 s0, f4 s1, h8 *v, int base, bool ok, int t1, int j,
+__device__ __forceinline__ void softmax_pv(f4 s0, f4 s1, h8 *v, int base, int ok, int t1, int j,
                                            int g, float c, State<HD> &S, h8 *vl = nullptr)
 {
     constexpr int NB = HD / 16;
@@ -622,13 +625,14 @@ __device__ __forceinline__ void softmax_pv(f4 s0, f4 s1, h8 *v, int base, bool o
         sc[r] = s0[r] * c;
         sc[4 + r] = s1[r] * c;
     }
-    if (base + 32 > t1 || !ok) {
+    if (base + 32 > t1 || ok != 3) {
         // Tokens past the end (or on a rejected page) get weight 0, and
         // their V values -- whatever the slot holds -- are zeroed so they
         // cannot turn 0 * V into NaN.
+        const bool okg = (ok >> (g >> 1)) & 1; // this lane's tokens 8g .. 8g+7
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            if (!(base + 8 * g + i < t1 && ok)) {
+            if (!(base + 8 * g + i < t1 && okg)) {
                 sc[i] = -INFINITY;
 #pragma unroll
                 for (int nb = 0; nb < NB; nb++) {
@@ -646,13 +650,16 @@ __device__ __forceinline__ void softmax_pv(f4 s0, f4 s1, h8 *v, int base, bool o
     mx = fmaxf(mx, __shfl_xor(mx, 16));
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     const float mnew = fmaxf(S.m2, mx);
+    // every score so far masked (a rejected first page): a finite reference
+    // keeps alpha and p at 0 instead of exp2(-inf + inf)
+    const float mref = mnew == -INFINITY ? 0.0f : mnew;
     // the bare exponential instruction: results below 2^-126 (flushed to
     // zero) weigh nothing beside the block maximum's 2^14
-    const float alpha = __builtin_amdgcn_exp2f(S.m2 - mnew);
+    const float alpha = __builtin_amdgcn_exp2f(S.m2 - mref);
     S.m2 = mnew;
     // p carries a factor 2^14 (its lo half stays a normal fp16); the running
     // sum carries the same factor, which cancels in the final division.
-    const float msub = mnew - 14.0f;
+    const float msub = mref - 14.0f;
     float ps = 0.0f;
     h8 ph, pl;
     const bool lo_row = GP != 0 && j >= GP;
@@ -710,7 +717,7 @@ __device__ __forceinline__ uint32_t xor8u(uint32_t x)
 // (lanes 8-15 feed P rows 8-15, whose output rows are never read).  A
 // column's running sum is split over lanes j and j + 8; the merge adds them.
 template <int KT, int HD>
-__device__ __forceinline__ void softmax_pv_q4(f4 s0, f4 s1, QBlock<KT, HD> &B, int base, bool ok, int t1, int j,
+__device__ __forceinline__ void softmax_pv_q4(f4 s0, f4 s1, QBlock<KT, HD> &B, int base, int ok, int t1, int j,
                                               int g, float c, State<HD> &S, float &vnorm)
 {
     constexpr int KK = HD / 32, GP = 4;
@@ -722,16 +729,17 @@ __device__ __forceinline__ void softmax_pv_q4(f4 s0, f4 s1, QBlock<KT, HD> &B, i
         const float moved = xor8(s1[r] * c);
         sc[r] = upper ? moved : s0[r] * c;
     }
-    if (base + 32 > t1 || !ok) {
+    if (base + 32 > t1 || ok != 3) {
+        const bool okg = (ok >> (g >> 1)) & 1; // tokens 8g .. 8g+7
 #pragma unroll
         for (int r = 0; r < 4; r++)
-            if (!(base + t_0 + r < t1 && ok))
+            if (!(base + t_0 + r < t1 && okg))
                 sc[r] = -INFINITY;
         // scales of dead tokens (all 8 of this lane's group) to 0, as in
         // softmax_pv_q
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            if (!(base + 8 * g + i < t1 && ok)) {
+            if (!(base + 8 * g + i < t1 && okg)) {
                 const uint32_t keep = (i & 1) ? 0x0000FFFFu : 0xFFFF0000u;
 #pragma unroll
                 for (int db = 0; db < KK; db++)
@@ -756,9 +764,10 @@ __device__ __forceinline__ void softmax_pv_q4(f4 s0, f4 s1, QBlock<KT, HD> &B, i
     mx = fmaxf(mx, __shfl_xor(mx, 16));
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     const float mnew = fmaxf(S.m2, mx);
-    const float alpha = __builtin_amdgcn_exp2f(S.m2 - mnew);
+    const float mref = mnew == -INFINITY ? 0.0f : mnew; // as in softmax_pv
+    const float alpha = __builtin_amdgcn_exp2f(S.m2 - mref);
     S.m2 = mnew;
-    const float msub = mnew - 14.0f;
+    const float msub = mref - 14.0f;
     float p[4], ps = 0.0f;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
@@ -829,7 +838,7 @@ __device__ __forceinline__ void softmax_pv_q4(f4 s0, f4 s1, QBlock<KT, HD> &B, i
 // rejected page get score -inf and scale 0, so whatever their slots hold
 // takes no part in w or in the cap.
 template <int KT, int HD, int GP>
-__device__ __forceinline__ void softmax_pv_q(f4 s0, f4 s1, QBlock<KT, HD> &B, int base, bool ok, int t1, int j,
+__device__ __forceinline__ void softmax_pv_q(f4 s0, f4 s1, QBlock<KT, HD> &B, int base, int ok, int t1, int j,
                                              int g, float c, State<HD> &S, float &vnorm)
 {
     constexpr int KK = HD / 32;
@@ -843,10 +852,11 @@ __device__ __forceinline__ void softmax_pv_q(f4 s0, f4 s1, QBlock<KT, HD> &B, in
         sc[r] = s0[r] * c;
         sc[4 + r] = s1[r] * c;
     }
-    if (base + 32 > t1 || !ok) {
+    if (base + 32 > t1 || ok != 3) {
+        const bool okg = (ok >> (g >> 1)) & 1; // tokens 8g .. 8g+7
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            if (!(base + 8 * g + i < t1 && ok)) {
+            if (!(base + 8 * g + i < t1 && okg)) {
                 sc[i] = -INFINITY;
                 const uint32_t keep = (i & 1) ? 0x0000FFFFu : 0xFFFF0000u;
 #pragma unroll
@@ -878,9 +888,10 @@ __device__ __forceinline__ void softmax_pv_q(f4 s0, f4 s1, QBlock<KT, HD> &B, in
     mx = fmaxf(mx, __shfl_xor(mx, 16));
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     const float mnew = fmaxf(S.m2, mx);
-    const float alpha = __builtin_amdgcn_exp2f(S.m2 - mnew);
+    const float mref = mnew == -INFINITY ? 0.0f : mnew; // as in softmax_pv
+    const float alpha = __builtin_amdgcn_exp2f(S.m2 - mref);
     S.m2 = mnew;
-    const float msub = mnew - 14.0f;
+    const float msub = mref - 14.0f;
     float p[8], ps = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
@@ -959,19 +970,17 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
     constexpr bool F32 = KT == KV_F32;
     static_assert(!(QUANT || F32) || GP != 0, "quantised and f32 pages use the packed hi/lo form");
     const PoolLayout &L = a.L;
-    const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    const int kvh = blockIdx.y;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int j = lane & 15, g = lane >> 4;
-    const int H = a.num_heads, KVH = L.num_kv_heads, G = H / KVH, P = L.page_tokens;
+    const int H = a.num_heads, G = H / L.num_kv_heads, P = L.page_tokens;
     const int h0 = kvh * G;
-    int len = a.seq_lens[b];
-    if (len > a.max_blocks * P) {
-        if (threadIdx.x == 0 && split == 0 && a.status)
-            atomicOr(a.status, FLAG_BAD_SLOT);
-        len = a.max_blocks * P;
-    }
-    const int t0 = split * a.split_tokens;
-    const int t1 = min(len, t0 + a.split_tokens);
+    // this workgroup's tokens [t0, t1) of sequence b (split_plan.h)
+    PlanItem it;
+    if (!plan_item<256>(a, blockIdx.x, it))
+        return;
+    const int b = it.b;
+    const int t0 = it.t0, t1 = it.t1;
     const int64_t qrow = (int64_t)b * H + h0;
 
     // The per-wave staging areas of the block loop (quantised pages) and,
@@ -985,9 +994,8 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
     float(*s_o)[16][HD] = reinterpret_cast<float(*)[16][HD]>(s_stage);
     __shared__ float s_m[4][16], s_l[4][16];
 
-    float *wsp = nullptr;
-    if (a.num_splits > 1)
-        wsp = a.ws + (((int64_t)b * KVH + kvh) * a.num_splits + split) * (G * (HD + 2));
+    // partial slot when the sequence is split over several items
+    float *wsp = it.nsplit > 1 ? plan_slot(a, blockIdx.x, kvh, G, HD) : nullptr;
 
     if (t0 >= t1) {
         for (int e = threadIdx.x; e < G * HD; e += 256) {
@@ -1000,6 +1008,8 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
             wsp[G * HD + 2 * threadIdx.x] = -INFINITY;
             wsp[G * HD + 2 * threadIdx.x + 1] = 0.0f;
         }
+        if (wsp)
+            merge_if_last<256>(a, it, blockIdx.x, kvh, G, HD);
         return;
     }
 
@@ -1085,7 +1095,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
             QStage<KT, HD> &Sq = reinterpret_cast<QStage<KT, HD> *>(s_stage)[w];
             int64_t pA, pB;
             int sA, sB;
-            bool ok;
+            int ok;
             block_pages(a, bt, base, t1, pA, pB, sA, sB, ok);
             issue_q<KT, HD>(a, pA, pB, sA, sB, koff, ksoff, voff, vsoff, lane, Sq);
             load_q();
@@ -1098,7 +1108,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
                 const bool more = next < t1;
                 int64_t nA = pA, nB = pB;
                 int nsA = sA, nsB = sB;
-                bool nok = ok;
+                int nok = ok;
                 if (more) {
                     block_pages(a, bt, next, t1, nA, nB, nsA, nsB, nok);
                     // every read of this block has returned before its
@@ -1125,7 +1135,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
             const F32Lanes fl = f32_lanes<HD>(lane, P);
             int64_t pA, pB;
             int sA, sB;
-            bool ok;
+            int ok;
             block_pages(a, bt, base, t1, pA, pB, sA, sB, ok);
             issue_f32<HD>(a, pA, pB, sA, sB, koff, voff, fl, Sf);
             load_q();
@@ -1138,7 +1148,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
                 const bool more = next < t1;
                 int64_t nA = pA, nB = pB;
                 int nsA = sA, nsB = sB;
-                bool nok = ok;
+                int nok = ok;
                 if (more) {
                     block_pages(a, bt, next, t1, nA, nB, nsA, nsB, nok);
                     __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0): this block's reads returned
@@ -1173,7 +1183,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
         h8 k0[KK], k1[KK], v[NB];
         int64_t pA, pB;
         int sA, sB;
-        bool ok;
+        int ok;
         block_pages(a, bt, base, t1, pA, pB, sA, sB, ok);
         load_k<HD, NT>(a, pA, pB, sA, sB, koff, j, g, k0, k1);
         load_v<HD, NT>(a, pA, pB, sA, sB, voff, j, g, v);
@@ -1186,7 +1196,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
                 break;
             int64_t nA, nB;
             int nsA, nsB;
-            bool nok;
+            int nok;
             block_pages(a, bt, next, t1, nA, nB, nsA, nsB, nok);
             if (PREFETCH)
                 load_k<HD, NT>(a, nA, nB, nsA, nsB, koff, j, g, k0, k1);
@@ -1265,6 +1275,8 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
             a.out[(qrow + hh) * HD + d] = den > 0.0f ? num / den : 0.0f;
         }
     }
+    if (wsp)
+        merge_if_last<256>(a, it, blockIdx.x, kvh, G, HD);
 }
 
 // GP: 0 for any group size up to 16 (hi/lo halves in separate products),
@@ -1310,27 +1322,20 @@ bool mfma_decode_supported(const PoolLayout &L, int num_heads)
     return false;
 }
 
-#ifndef GI_MFMA_DECODE_NT
-#define GI_MFMA_DECODE_NT true
-#endif
-#ifndef GI_MFMA_DECODE_PREFETCH
-#define GI_MFMA_DECODE_PREFETCH true
-#endif
-#ifndef GI_MFMA_DECODE_OCC
-#define GI_MFMA_DECODE_OCC 1
-#endif
-#ifndef GI_MFMA_DECODE_OCC_Q
-#define GI_MFMA_DECODE_OCC_Q GI_MFMA_DECODE_OCC
-#endif
-#ifndef GI_MFMA_DECODE_PACK
-#define GI_MFMA_DECODE_PACK true
-#endif
+// Launch choices of the decode kernels, as measured best on MI355X:
+// non-temporal K/V loads (read once), the next block's loads issued as soon as
+// registers free up, at least one wave per SIMD asked of the register
+// allocator, and the packed hi/lo query layout for groups of up to 8 heads.
+constexpr bool kDecodeNt = true;
+constexpr bool kDecodePrefetch = true;
+constexpr int kDecodeOcc = 1;
+constexpr bool kDecodePack = true;
 
 template <int HD, int GP>
 static void launch_mfma_hd(const DecodeArgs &a, dim3 grid, hipStream_t st)
 {
-    hipLaunchKernelGGL((mfma_decode::attn_mfma_f16<HD, GP, GI_MFMA_DECODE_NT, GI_MFMA_DECODE_PREFETCH,
-                                                   GI_MFMA_DECODE_OCC>),
+    hipLaunchKernelGGL((mfma_decode::attn_mfma_f16<HD, GP, kDecodeNt, kDecodePrefetch,
+                                                   kDecodeOcc>),
                        grid, dim3(256), 0, st, a);
 }
 
@@ -1338,8 +1343,8 @@ template <int KT, int HD>
 static void launch_mfma_q(const DecodeArgs &a, dim3 grid, hipStream_t st)
 {
 #define GI_Q(GPv)                                                                                        \
-    hipLaunchKernelGGL((mfma_decode::attn_mfma_q<KT, HD, GPv, GI_MFMA_DECODE_NT, GI_MFMA_DECODE_PREFETCH, \
-                                                 GI_MFMA_DECODE_OCC_Q>),                                \
+    hipLaunchKernelGGL((mfma_decode::attn_mfma_q<KT, HD, GPv, kDecodeNt, kDecodePrefetch, \
+                                                 kDecodeOcc>),                                \
                        grid, dim3(256), 0, st, a)
     switch (a.num_heads / a.L.num_kv_heads) {
     case 1: GI_Q(1); break;
@@ -1354,8 +1359,8 @@ template <int HD>
 static void launch_mfma_f32(const DecodeArgs &a, dim3 grid, hipStream_t st)
 {
 #define GI_F(GPv)                                                                                 \
-    hipLaunchKernelGGL((mfma_decode::attn_mfma_f32<HD, GPv, GI_MFMA_DECODE_NT, GI_MFMA_DECODE_PREFETCH, \
-                                                   GI_MFMA_DECODE_OCC>),                         \
+    hipLaunchKernelGGL((mfma_decode::attn_mfma_f32<HD, GPv, kDecodeNt, kDecodePrefetch, \
+                                                   kDecodeOcc>),                         \
                        grid, dim3(256), 0, st, a)
     switch (a.num_heads / a.L.num_kv_heads) {
     case 1: GI_F(1); break;
@@ -1370,17 +1375,17 @@ template <int HD>
 static void launch_mfma_g(const DecodeArgs &a, dim3 grid, hipStream_t st)
 {
     switch (a.num_heads / a.L.num_kv_heads) {
-    case 1: launch_mfma_hd<HD, GI_MFMA_DECODE_PACK ? 1 : 0>(a, grid, st); break;
-    case 2: launch_mfma_hd<HD, GI_MFMA_DECODE_PACK ? 2 : 0>(a, grid, st); break;
-    case 4: launch_mfma_hd<HD, GI_MFMA_DECODE_PACK ? 4 : 0>(a, grid, st); break;
-    case 8: launch_mfma_hd<HD, GI_MFMA_DECODE_PACK ? 8 : 0>(a, grid, st); break;
+    case 1: launch_mfma_hd<HD, kDecodePack ? 1 : 0>(a, grid, st); break;
+    case 2: launch_mfma_hd<HD, kDecodePack ? 2 : 0>(a, grid, st); break;
+    case 4: launch_mfma_hd<HD, kDecodePack ? 4 : 0>(a, grid, st); break;
+    case 8: launch_mfma_hd<HD, kDecodePack ? 8 : 0>(a, grid, st); break;
     default: launch_mfma_hd<HD, 0>(a, grid, st); break;
     }
 }
 
 hipError_t launch_decode_mfma(const DecodeArgs &a, hipStream_t st)
 {
-    dim3 grid(a.num_splits, a.L.num_kv_heads, a.batch);
+    dim3 grid(decode_grid_items(a), a.L.num_kv_heads, 1);
     const bool h128 = a.L.head_dim == 128;
     switch (a.L.kv_type) {
     case KV_Q8_0:

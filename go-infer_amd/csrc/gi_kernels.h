@@ -46,9 +46,11 @@ hipError_t launch_copy_pages(const PoolLayout &L, uint8_t *const *layer_base, in
 
 // Attention over paged context.  Decode: q/out are [batch][num_heads][head_dim]
 // float32, block_tables is [batch][max_blocks], sequence b attends its first
-// seq_lens[b] tokens.  The same kernels serve chunked prefill on the vector
-// path: n_q queries per sequence, query i of sequence b attends
-// start_pos[b] + i + 1 tokens, q/out are [batch][n_q][num_heads][head_dim].
+// seq_lens[b] tokens; the launch is cut into work items by the split plan
+// (split_plan.h), grid (decode_grid_items, kv heads).  The vector kernel also
+// serves chunked prefill (plan_target 0): n_q queries per sequence, query i of
+// sequence b attends start_pos[b] + i + 1 tokens, q/out are
+// [batch][n_q][num_heads][head_dim], grid (1, kv heads, batch * n_q).
 struct DecodeArgs {
     PoolLayout L;
     const uint8_t *base;
@@ -62,20 +64,29 @@ struct DecodeArgs {
     const int32_t *start_pos; // prefill only: tokens cached before the chunk
     int num_heads;
     float scale;
-    int split_tokens; // tokens per split, a multiple of the page size
-    int num_splits;
-    float *ws; // partials when num_splits > 1
+    // split plan (decode): work items per kv head aimed at, the shortest
+    // split and the split granularity in tokens; 0 targets: no plan
+    int plan_target;
+    int plan_min;
+    int plan_unit;
+    float *ws;     // partials of split sequences, decode_grid_items x kv heads slots
+    int *plan_cnt; // [batch][kv heads] arrival counters, zero between launches
     int *status;
     int kernel; // -1 automatic, 0 vector ALU, 1 matrix core
 };
 
-// Bytes of split-K workspace needed for a decode launch.
-size_t decode_workspace_bytes(const PoolLayout &L, int batch, int num_heads, int num_splits);
+// Split-plan parameters of a decode launch on a device with num_cus CUs
+// (fills plan_target, plan_min, plan_unit).
+void decode_plan(const PoolLayout &L, int num_cus, DecodeArgs &a);
 
-// Picks (split_tokens, num_splits) for a batch whose longest sequence has
-// max_len tokens, so the grid fills the device.
-void decode_plan(const PoolLayout &L, int batch, int num_heads, int max_len, int num_cus,
-                 int *split_tokens, int *num_splits);
+// Grid width (work items per kv head) of a decode launch: an upper bound of
+// the plan's item count, batch + plan_target.
+int decode_grid_items(const DecodeArgs &a);
+
+// Bytes of decode workspace: the arrival counters (first, rounded to 256 B)
+// then the partial slots.
+size_t decode_counter_bytes(const PoolLayout &L, int batch);
+size_t decode_workspace_bytes(const PoolLayout &L, int batch, int num_heads, int grid_items);
 
 // Returns hipErrorInvalidValue for shapes without a kernel instance.
 hipError_t launch_decode(const DecodeArgs &a, hipStream_t st);

@@ -455,8 +455,17 @@ int gi_prefix_store(gi_prefix *pc, const int32_t *tokens, int n, int seq_id)
         return GI_OK;
     std::lock_guard<std::mutex> g(pc->mu);
     std::lock_guard<std::mutex> gm(pc->m->mu);
-    if (pc->m->tables.find(seq_id) == pc->m->tables.end())
+    auto st = pc->m->tables.find(seq_id);
+    if (st == pc->m->tables.end())
         return gi::set_error(GI_ERR_UNKNOWN_SEQ, "sequence " + std::to_string(seq_id) + " not found");
+    // The entry is keyed on all n tokens, so the sequence must hold them: a
+    // shorter one would make a later hit report more cached tokens than the
+    // fork has.  (cloneKVCachePrefix, prefix_cache.go:122-150, copies
+    // prefixLen slots whatever the cache holds; refusing is the safe form.)
+    if (n > st->second.num_tokens)
+        return gi::set_error(GI_ERR_BAD_ARG, "gi_prefix_store: " + std::to_string(n) + " tokens but sequence " +
+                                                 std::to_string(seq_id) + " holds " +
+                                                 std::to_string(st->second.num_tokens));
     // prefix_cache.go:106-112: a full cache drops one entry first
     if ((int)pc->entries.size() >= pc->max_size && !pc->order.empty()) {
         const std::string victim = pc->order.front();

@@ -43,7 +43,7 @@
 // with no global reduction.
 #include "../../include/goinfer_paged.h"
 #include "gi_common.h"
-#include "gi_host.h"
+#include "devbuf.h"
 #include "mfma_ops.h"
 
 #include <hip/hip_runtime.h>
@@ -440,10 +440,8 @@ struct gi_weights {
     uint8_t *a = nullptr, *a_lo = nullptr;
     uint16_t *scales = nullptr;
     float *row_scale = nullptr;
-    // activation split, grown on demand
-    _Float16 *xh = nullptr, *xl = nullptr;
-    float *xscale = nullptr;
-    int x_cap = 0; // batch rows the split buffers hold
+    // activation split (hi, lo halves, row scales), grown on demand
+    gi::DevBuffer xsplit;
 };
 
 extern "C" {
@@ -543,10 +541,10 @@ void gi_weights_destroy(gi_weights *w)
     // the device's queued work (which may still read these buffers) first.
     if (hipSetDevice(w->device) == hipSuccess)
         (void)hipDeviceSynchronize();
-    for (void *p : {(void *)w->a, (void *)w->a_lo, (void *)w->scales, (void *)w->row_scale, (void *)w->xh,
-                    (void *)w->xl, (void *)w->xscale})
+    for (void *p : {(void *)w->a, (void *)w->a_lo, (void *)w->scales, (void *)w->row_scale})
         if (p)
             (void)hipFree(p);
+    gi::devbuf_release(w->xsplit);
     delete w;
 }
 
@@ -559,28 +557,19 @@ int gi_matmul_batch(gi_weights *w, int batch, const float *x, float *y)
         return GI_OK;
     gi_paged *h = w->h;
     const int batch_pad = (int)round_pad(batch); // activation rows, zero-padded
-    if (batch_pad > w->x_cap) {
-        for (void *p : {(void *)w->xh, (void *)w->xl, (void *)w->xscale})
-            if (p)
-                (void)gi_dev_free(h, p); // waits for queued work that reads them
-        w->xh = w->xl = nullptr;
-        w->xscale = nullptr;
-        w->x_cap = 0;
-        void *p = nullptr;
-        const size_t nx = (size_t)batch_pad * w->cols * 2;
-        int rc = gi_dev_alloc(h, nx, &p);
-        w->xh = (_Float16 *)p;
-        if (rc == GI_OK && (rc = gi_dev_alloc(h, nx, &p)) == GI_OK)
-            w->xl = (_Float16 *)p;
-        if (rc == GI_OK && (rc = gi_dev_alloc(h, (size_t)batch_pad * 4, &p)) == GI_OK)
-            w->xscale = (float *)p;
-        if (rc != GI_OK)
-            return rc;
-        w->x_cap = batch_pad;
-    }
     hipStream_t st = (hipStream_t)gi_paged_stream(h);
-    hipLaunchKernelGGL(split_rows, dim3((unsigned)batch_pad), dim3(256), 0, st, x, batch, w->cols, w->xh, w->xl,
-                       w->xscale);
+    // hi and lo halves [batch_pad][cols], then the row scales
+    const size_t nx = (size_t)batch_pad * w->cols * 2;
+    hipError_t e = hipSetDevice(w->device);
+    if (e != hipSuccess)
+        return hip_fail(e, "gi_matmul_batch");
+    const int rc = devbuf_reserve(w->xsplit, 2 * nx + (size_t)batch_pad * 4, false, st, "gi_matmul_batch");
+    if (rc != GI_OK)
+        return rc;
+    _Float16 *xh = (_Float16 *)w->xsplit.ptr;
+    _Float16 *xl = (_Float16 *)((uint8_t *)w->xsplit.ptr + nx);
+    float *xscale = (float *)((uint8_t *)w->xsplit.ptr + 2 * nx);
+    hipLaunchKernelGGL(split_rows, dim3((unsigned)batch_pad), dim3(256), 0, st, x, batch, w->cols, xh, xl, xscale);
     MatArgs a{};
     a.type = w->type;
     a.rows = w->rows;
@@ -591,9 +580,9 @@ int gi_matmul_batch(gi_weights *w, int batch, const float *x, float *y)
     a.a_lo = w->a_lo;
     a.scales = w->scales;
     a.row_scale = w->row_scale;
-    a.xh = w->xh;
-    a.xl = w->xl;
-    a.xscale = w->xscale;
+    a.xh = xh;
+    a.xl = xl;
+    a.xscale = xscale;
     a.y = y;
     dim3 grid((unsigned)(batch_pad / 64), (unsigned)(a.rows_pad / 64));
     switch (w->type) {
@@ -602,7 +591,7 @@ int gi_matmul_batch(gi_weights *w, int batch, const float *x, float *y)
     case W_Q8_0: hipLaunchKernelGGL((matmul_lds<W_Q8_0, 3>), grid, dim3(256), 0, st, a); break;
     default: hipLaunchKernelGGL((matmul_lds<W_Q4_0, 3>), grid, dim3(256), 0, st, a); break;
     }
-    hipError_t e = hipGetLastError();
+    e = hipGetLastError();
     return e == hipSuccess ? GI_OK : hip_fail(e, "gi_matmul_batch");
 }
 

@@ -3,7 +3,7 @@
 // reference interfaces each entry point replaces are in
 // include/goinfer_paged.h.
 #include "../../include/goinfer_paged.h"
-#include "gi_host.h"
+#include "devbuf.h"
 #include "gi_kernels.h"
 
 #include <hip/hip_runtime.h>
@@ -28,6 +28,61 @@ int set_error(int code, const std::string &msg)
 
 void clear_error() { g_last_error.clear(); }
 
+int devbuf_reserve(DevBuffer &b, size_t need, bool zero, hipStream_t st, const char *what)
+{
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    hipError_t e = hipStreamIsCapturing(st, &cs);
+    if (e != hipSuccess)
+        return set_error(GI_ERR_HIP, std::string(what) + ": hipStreamIsCapturing: " + hipGetErrorString(e));
+    const bool capturing = cs != hipStreamCaptureStatusNone;
+    if (capturing)
+        b.captured = true;
+    if (need <= b.bytes)
+        return GI_OK;
+    if (capturing)
+        return set_error(GI_ERR_BAD_ARG,
+                         std::string(what) + ": needs " + std::to_string(need) + " bytes of workspace (holds " +
+                             std::to_string(b.bytes) +
+                             ") while the stream is capturing a graph; make one eager call of this shape "
+                             "(or a larger batch) before capturing");
+    if (b.ptr) {
+        if (b.captured) {
+            // a captured graph may still address it: keep it until release
+            b.retired.push_back(b.ptr);
+        } else {
+            // work already queued may still read it
+            e = hipStreamSynchronize(st);
+            if (e != hipSuccess)
+                return set_error(GI_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+            (void)hipFree(b.ptr);
+        }
+        b.ptr = nullptr;
+        b.bytes = 0;
+    }
+    const size_t want = need + need / 4;
+    void *p = nullptr;
+    if (hipMalloc(&p, want) != hipSuccess)
+        return set_error(GI_ERR_OOM, std::string(what) + ": hipMalloc(" + std::to_string(want) + ") failed");
+    if (zero && (e = hipMemsetAsync(p, 0, want, st)) != hipSuccess) {
+        (void)hipFree(p);
+        return set_error(GI_ERR_HIP, std::string(what) + ": clear: " + hipGetErrorString(e));
+    }
+    b.ptr = p;
+    b.bytes = want;
+    return GI_OK;
+}
+
+void devbuf_release(DevBuffer &b)
+{
+    if (b.ptr)
+        (void)hipFree(b.ptr);
+    for (void *p : b.retired)
+        (void)hipFree(p);
+    b.retired.clear();
+    b.ptr = nullptr;
+    b.bytes = 0;
+}
+
 } // namespace gi
 
 struct gi_paged {
@@ -40,8 +95,8 @@ struct gi_paged {
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
     int *d_status = nullptr;
-    void *ws = nullptr;
-    size_t ws_bytes = 0;
+    gi::DevBuffer plan_cnt; // decode: arrival counters of split sequences
+    gi::DevBuffer plan_ws;  // decode: partials of split sequences
     int decode_kernel = -1; // -1 automatic, 0 vector ALU, 1 matrix core
     float2 *d_rope = nullptr; // (cos, sin) [rope_max_pos][rope_half]
     int rope_half = 0;
@@ -71,30 +126,6 @@ int check_layer(const gi_paged *h, int layer, const char *what)
     if (layer < 0 || layer >= h->L.num_layers)
         return gi::set_error(GI_ERR_BAD_ARG, std::string(what) + ": layer " + std::to_string(layer) +
                                                  " out of range");
-    return GI_OK;
-}
-
-// Grows the split-K workspace.  Work already queued may still read the old
-// buffer, so the stream is drained before it is released.
-int ensure_ws(gi_paged *h, size_t bytes)
-{
-    if (bytes <= h->ws_bytes)
-        return GI_OK;
-    if (h->ws) {
-        hipError_t e = hipStreamSynchronize(h->stream);
-        if (e != hipSuccess)
-            return hip_fail(e, "workspace resize");
-        (void)hipFree(h->ws);
-        h->ws = nullptr;
-        h->ws_bytes = 0;
-    }
-    size_t want = bytes + bytes / 4;
-    hipError_t e = hipMalloc(&h->ws, want);
-    if (e != hipSuccess) {
-        h->ws = nullptr;
-        return gi::set_error(GI_ERR_OOM, "decode workspace: hipMalloc failed");
-    }
-    h->ws_bytes = want;
     return GI_OK;
 }
 
@@ -225,8 +256,8 @@ void gi_paged_destroy(gi_paged *h)
         (void)hipFree(h->d_status);
     if (h->d_layer_base)
         (void)hipFree(h->d_layer_base);
-    if (h->ws)
-        (void)hipFree(h->ws);
+    gi::devbuf_release(h->plan_cnt);
+    gi::devbuf_release(h->plan_ws);
     if (h->d_rope)
         (void)hipFree(h->d_rope);
     if (h->own_stream)
@@ -521,7 +552,7 @@ int gi_paged_gather(gi_paged *h, int layer, const int32_t *block_table, int n_to
 
 static int decode_locked(gi_paged *h, int layer, int batch, int num_heads, const float *q,
                          float *out, const int32_t *block_tables, int max_blocks,
-                         const int32_t *seq_lens, int max_seq_len, float scale)
+                         const int32_t *seq_lens, float scale)
 {
     gi::DecodeArgs a{};
     a.L = h->L;
@@ -538,14 +569,18 @@ static int decode_locked(gi_paged *h, int layer, int batch, int num_heads, const
     a.scale = scale;
     a.status = h->d_status;
     a.kernel = h->decode_kernel;
-    int max_len = max_seq_len;
-    if ((int64_t)max_len > (int64_t)max_blocks * h->L.page_tokens)
-        max_len = max_blocks * h->L.page_tokens;
-    gi::decode_plan(h->L, batch, num_heads, max_len, h->num_cus, &a.split_tokens, &a.num_splits);
-    int rc = ensure_ws(h, gi::decode_workspace_bytes(h->L, batch, num_heads, a.num_splits));
+    gi::decode_plan(h->L, h->num_cus, a);
+    int rc = gi::devbuf_reserve(h->plan_cnt, gi::decode_counter_bytes(h->L, batch), true, h->stream,
+                                "decode attention");
+    if (rc == GI_OK)
+        rc = gi::devbuf_reserve(h->plan_ws,
+                                gi::decode_workspace_bytes(h->L, batch, num_heads, gi::decode_grid_items(a)) -
+                                    gi::decode_counter_bytes(h->L, batch),
+                                false, h->stream, "decode attention");
     if (rc)
         return rc;
-    a.ws = (float *)h->ws;
+    a.plan_cnt = (int *)h->plan_cnt.ptr;
+    a.ws = (float *)h->plan_ws.ptr;
     hipError_t e = gi::launch_decode(a, h->stream);
     return e == hipSuccess ? GI_OK : hip_fail(e, "decode attention");
 }
@@ -581,8 +616,7 @@ int gi_paged_decode_attention(gi_paged *h, int layer, int batch, int num_heads, 
     if (batch == 0)
         return GI_OK;
     std::lock_guard<std::mutex> g(h->mu);
-    return decode_locked(h, layer, batch, num_heads, q, out, block_tables, max_blocks, seq_lens,
-                         max_seq_len, scale);
+    return decode_locked(h, layer, batch, num_heads, q, out, block_tables, max_blocks, seq_lens, scale);
 }
 
 int gi_paged_decode_step(gi_paged *h, int layer, int batch, int num_heads, const float *q,
@@ -602,8 +636,7 @@ int gi_paged_decode_step(gi_paged *h, int layer, int batch, int num_heads, const
                                             max_blocks, seq_lens, k, v, h->d_status, h->stream);
     if (e != hipSuccess)
         return hip_fail(e, "gi_paged_decode_step: append");
-    return decode_locked(h, layer, batch, num_heads, q, out, block_tables, max_blocks, seq_lens,
-                         max_seq_len, scale);
+    return decode_locked(h, layer, batch, num_heads, q, out, block_tables, max_blocks, seq_lens, scale);
 }
 
 int gi_paged_rope_decode_step(gi_paged *h, int layer, int batch, int num_heads, float *q, const float *k,
@@ -624,8 +657,7 @@ int gi_paged_rope_decode_step(gi_paged *h, int layer, int batch, int num_heads, 
                                           h->stream);
     if (e != hipSuccess)
         return hip_fail(e, "gi_paged_rope_decode_step: rope + append");
-    return decode_locked(h, layer, batch, num_heads, q, out, block_tables, max_blocks, seq_lens,
-                         max_seq_len, scale);
+    return decode_locked(h, layer, batch, num_heads, q, out, block_tables, max_blocks, seq_lens, scale);
 }
 
 int gi_paged_prefill_attention(gi_paged *h, int layer, int batch, int chunk_len, int num_heads,

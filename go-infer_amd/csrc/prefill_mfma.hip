@@ -1373,12 +1373,8 @@ constexpr int prefill_ncg()
 // LDS buffers of the staged kernel: two (one barrier per block) for fp16
 // pages; one for q8_0, whose V hi/lo planes would otherwise leave room for a
 // single workgroup per CU.
-#ifndef GI_PREFILL_NBUF_F16
-#define GI_PREFILL_NBUF_F16 2
-#endif
-#ifndef GI_PREFILL_NBUF_Q8
-#define GI_PREFILL_NBUF_Q8 1
-#endif
+constexpr int kPrefillNbufF16 = 2;
+constexpr int kPrefillNbufQ8 = 1;
 // f32 pages: one buffer (their block maxima are exchanged at its barrier).
 
 // Column groups per wave: two halve the LDS reads per matrix-core product;
@@ -1388,35 +1384,26 @@ constexpr int prefill_ncg()
 template <int HD, int KT, int P>
 constexpr int prefill_lds_ncg()
 {
-#ifdef GI_PREFILL_NCG
-    return GI_PREFILL_NCG;
-#else
     return KT == KV_F32 ? 2 : (HD == 64 || P == 16 || (KT != KV_F16 && P == 32)) ? 2 : 1;
-#endif
 }
 
 // fp16 pages use the direct global->LDS kernel (no staging registers, so
 // two column groups always fit).
-#ifndef GI_PREFILL_DIRECT
-#define GI_PREFILL_DIRECT 1
-#endif
-#ifndef GI_PREFILL_DIRECT_NCG
-#define GI_PREFILL_DIRECT_NCG 2
-#endif
+constexpr int kPrefillDirectNcg = 2;
 
 template <int HD, int KT>
 static void launch_lds(const PrefillArgs &a, hipStream_t st)
 {
     using namespace mfma_prefill;
-    constexpr int NBUF = KT == KV_F32 ? 1 : KT == KV_F16 ? GI_PREFILL_NBUF_F16 : GI_PREFILL_NBUF_Q8;
+    constexpr int NBUF = KT == KV_F32 ? 1 : KT == KV_F16 ? kPrefillNbufF16 : kPrefillNbufQ8;
     const int G = a.num_heads / a.L.num_kv_heads;
     const int64_t cols = (int64_t)a.chunk_len * G;
     auto grid = [&](int ncg) {
         const int64_t per_wg = 4 * 16 * ncg;
         return dim3((unsigned)((cols + per_wg - 1) / per_wg), a.L.num_kv_heads, a.batch);
     };
-    if (KT == KV_F16 && GI_PREFILL_DIRECT) {
-        constexpr int NCG = GI_PREFILL_DIRECT_NCG;
+    if (KT == KV_F16) {
+        constexpr int NCG = kPrefillDirectNcg;
         switch (a.L.page_tokens) {
         case 16:
             hipLaunchKernelGGL((attn_prefill_dlds<HD, 16, NCG>), grid(NCG), dim3(256), 0, st, a);

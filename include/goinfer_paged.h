@@ -252,9 +252,20 @@ int gi_paged_gather(gi_paged *h, int layer, const int32_t *block_table, int n_to
 
 /* Decode attention (forward.go:242-267) of one layer for a batch read
  * directly from pages: q, out [batch][num_heads][head_dim] float32; sequence
- * b attends its first seq_lens[b] tokens; max_seq_len bounds seq_lens and
- * sizes the context split.  q-head h reads kv head h / (num_heads /
- * num_kv_heads) (forward.go:249). */
+ * b attends its first seq_lens[b] tokens.  q-head h reads kv head h /
+ * (num_heads / num_kv_heads) (forward.go:249).
+ *
+ * The kernels split the batch's context into about equal work items from the
+ * lengths in device memory, so every seq_lens[b] token is attended whatever
+ * max_seq_len says (it is only checked to be >= 0; 0 is fine); a length below
+ * zero or beyond max_blocks * page_tokens is clamped and reported by
+ * gi_synchronize as GI_ERR_BAD_PAGE.
+ *
+ * Workspace: the handle keeps split partials and arrival counters sized by
+ * batch.  A call that needs them to grow while the handle's stream is
+ * capturing a graph fails with GI_ERR_BAD_ARG (make one eager call with the
+ * largest batch first); once any call has been captured, growth keeps the old
+ * buffers alive until gi_paged_destroy, so captured graphs stay valid. */
 int gi_paged_decode_attention(gi_paged *h, int layer, int batch, int num_heads, const float *q,
                               float *out, const int32_t *block_tables, int max_blocks,
                               const int32_t *seq_lens, int max_seq_len, float scale);

@@ -140,3 +140,44 @@ def test_no_device_paths_fail_cleanly(gi):
 def test_attn_scale_matches_reference_bits(gi):
     assert np.float32(gi.attn_scale(64)).view(np.uint32) == 0x3E000000
     assert np.float32(gi.attn_scale(128)).view(np.uint32) == 0x3DB504F3
+
+
+def test_wrapper_shape_checks_refuse_before_the_kernels(gi):
+    """A q/out, k/v or block-table size that does not match batch, heads and
+    kv_dim would send the kernels past the ends of the buffers: the wrappers
+    refuse it (GI_ERR_BAD_ARG) before any call reaches the library."""
+    import torch
+    p = object.__new__(gi.PagedKVCache)
+    p._h = None
+    p.num_layers, p.num_kv_heads, p.head_dim, p.page_tokens = 1, 8, 128, 16
+    p.num_pages, p.kv_type, p.kv_dim = 4, gi.KV_F16, 1024
+
+    def i32(*s):
+        return torch.zeros(s, dtype=torch.int32)
+
+    def f32(*s):
+        return torch.zeros(s, dtype=torch.float32)
+
+    cases = [
+        lambda: p.Write(0, i32(3), i32(2), f32(3, 1024), f32(3, 1024)),
+        lambda: p.Write(0, i32(3), i32(3), f32(2, 1024), f32(3, 1024)),
+        lambda: p.WriteAtLen(0, i32(2, 4), i32(3), f32(3, 1024), f32(3, 1024)),
+        lambda: p.WriteAtLen(0, i32(3, 4), i32(3), f32(3, 1000), f32(3, 1024)),
+        lambda: p.Get(0, i32(2), 33),
+        lambda: p.AttentionGQA(f32(2, 4096), f32(2, 4096), 0, i32(3, 4), i32(2), 32, 0.1),
+        lambda: p.AttentionGQA(f32(2, 4096), f32(2, 4000), 0, i32(2, 4), i32(2), 32, 0.1),
+        lambda: p.AttentionGQA(f32(2, 4096), f32(2, 4096), 0, i32(8), i32(2), 32, 0.1),
+        lambda: p.DecodeStep(f32(2, 4096), f32(2, 4096), f32(2, 1000), f32(2, 1024), 0, i32(2, 4),
+                             i32(2), 32, 0.1),
+        lambda: p.RoPEDecodeStep(f32(2, 4096), f32(2, 4096), f32(2, 1024), f32(1, 1024), 0, i32(2, 4),
+                                 i32(2), 32, 0.1),
+        lambda: p.RoPEWrite(0, i32(2), i32(2), i32(2), f32(2, 4000), f32(2, 1024), f32(2, 1024)),
+        lambda: p.RoPEWriteAtLen(0, i32(2, 4), i32(2), f32(2, 4096), f32(2, 1024), f32(3, 1024)),
+        lambda: p.AttentionGQABatch(f32(2, 5, 4096), f32(2, 4, 4096), 0, i32(2, 4), i32(2), 32, 0.1, 5),
+    ]
+    for i, c in enumerate(cases):
+        with pytest.raises(gi.GIError) as e:
+            c()
+        assert e.value.code == -3, i
+        msg = str(e.value)
+        assert "must be [" in msg or "must hold" in msg or "maps fewer" in msg, (i, msg)

@@ -427,3 +427,97 @@ def test_prefill_q8_llama8b_chunks(gi, oracle, dev):
     quantisation, N(0,1) inputs with 1 % outliers at +-8 sigma: the last
     chunk of a 1536-token prefill, batch 2."""
     prefill_case(gi, oracle, dev, 2, 32, 8, 128, 16, [1024, 512], 512, seed=70)
+
+
+def test_decode_plan_ignores_a_short_max_seq_len(gi, oracle, dev):
+    """The split plan is derived on the device from seq_lens, so a
+    max_seq_len below the real lengths (0, or one frozen at graph capture
+    while lengths grew) still attends every token of every sequence.  A
+    ragged batch whose longest sequence spans several work items."""
+    import torch
+    H, kvh, hd, P = 32, 8, 128, 16
+    lens = [1, 5000, 700, 2049, 64, 3333]
+    pop = Populated(gi, dev, 1, 1, kvh, hd, P, lens, seed=21)
+    bt = pop.block_tables()
+    sl = torch.tensor(lens, dtype=torch.int32, device=dev)
+    qd, q = seeded((len(lens), H * hd), 22, dev)
+    scale = oracle.attn_scale(hd)
+    want = oracle_decode(oracle, pop, 0, q, H, lens, scale)
+    for kern in kernels_for(pop.pool, H):
+        pop.pool.set_decode_kernel(kern)
+        for msl in (0, 1, 64):
+            out = torch.full_like(qd, float("nan"))
+            pop.pool.AttentionGQA(out, qd, 0, bt, sl, H, scale, msl)
+            pop.pool.synchronize()
+            err = float(rel_err_rows(out.cpu().numpy(), want, H, hd).max())
+            assert err <= 1e-3, (kern, msl, err)
+    pop.pool.set_decode_kernel(-1)
+
+
+def test_decode_bad_lengths_are_clamped_and_reported(gi, oracle, dev):
+    """A length beyond what the block table maps is clamped to the mapped
+    tokens, a negative one to 0 (zero output); both are reported by
+    gi_synchronize, and the other sequences are unaffected."""
+    import torch
+    H, kvh, hd, P = 32, 8, 128, 16
+    lens = [100, 300, 50]
+    pop = Populated(gi, dev, 1, 1, kvh, hd, P, lens, seed=23)
+    bt = pop.block_tables()            # max_blocks = 19 pages = 304 tokens
+    mapped = bt.shape[1] * P
+    qd, q = seeded((len(lens), H * hd), 24, dev)
+    scale = oracle.attn_scale(hd)
+    want = oracle_decode(oracle, pop, 0, q, H, lens, scale)
+    for kern in kernels_for(pop.pool, H):
+        pop.pool.set_decode_kernel(kern)
+        sl = torch.tensor([100, mapped + 500, -7], dtype=torch.int32, device=dev)
+        out = torch.full_like(qd, float("nan"))
+        pop.pool.AttentionGQA(out, qd, 0, bt, sl, H, scale)
+        with pytest.raises(gi.GIError) as e:
+            pop.pool.synchronize()
+        assert e.value.code == -7, kern
+        o = out.cpu().numpy()
+        assert rel_err_rows(o[0], want[0], H, hd).max() <= 1e-3
+        # sequence 1: every mapped token; its slots past 300 hold zeros
+        ks, vs = pop.stored(0, 1)
+        kw = np.zeros((mapped, kvh * hd), np.float32)
+        vw = np.zeros((mapped, kvh * hd), np.float32)
+        kw[:300] = oracle.widen(1, kvh * hd, ks)
+        vw[:300] = oracle.widen(1, kvh * hd, vs)
+        w1 = oracle.attention_decode(q[1], kw, vw, H, kvh, hd, mapped, scale)
+        assert rel_err_rows(o[1], w1, H, hd).max() <= 1e-3
+        assert not o[2].any()
+    pop.pool.set_decode_kernel(-1)
+
+
+@pytest.mark.parametrize("kv_type", [0, 1, 2, 3], ids=["f32", "f16", "q8_0", "q4_0"])
+def test_decode_bad_first_page_is_skipped(gi, oracle, dev, kv_type):
+    """A block table whose first entry is outside the pool: that page's
+    tokens are skipped (the wave that meets it first sees only masked
+    scores, which must not turn into NaN), the sequence attends the rest,
+    gi_synchronize reports the id, and the other sequence is unaffected."""
+    import torch
+    H, kvh, hd, P = 32, 8, 128, 16
+    lens = [600, 300]
+    pop = Populated(gi, dev, kv_type, 1, kvh, hd, P, lens, seed=25)
+    bt = pop.block_tables()
+    bt[0, 0] = pop.pool.num_pages + 5
+    sl = torch.tensor(lens, dtype=torch.int32, device=dev)
+    qd, q = seeded((len(lens), H * hd), 26, dev)
+    scale = oracle.attn_scale(hd)
+    ks, vs = pop.stored(0, 0)
+    kw = oracle.widen(kv_type, kvh * hd, ks)[P:]
+    vw = oracle.widen(kv_type, kvh * hd, vs)[P:]
+    want0 = oracle.attention_decode(q[0], kw, vw, H, kvh, hd, lens[0] - P, scale)
+    want1 = oracle_decode(oracle, pop, 0, q, H, lens, scale)[1]
+    for kern in kernels_for(pop.pool, H):
+        pop.pool.set_decode_kernel(kern)
+        out = torch.full_like(qd, float("nan"))
+        pop.pool.AttentionGQA(out, qd, 0, bt, sl, H, scale)
+        with pytest.raises(gi.GIError) as e:
+            pop.pool.synchronize()
+        assert e.value.code == -7, kern
+        o = out.cpu().numpy()
+        assert np.isfinite(o).all(), kern
+        assert rel_err_rows(o[0], want0, H, hd).max() <= TOL[kv_type], kern
+        assert rel_err_rows(o[1], want1, H, hd).max() <= TOL[kv_type], kern
+    pop.pool.set_decode_kernel(-1)

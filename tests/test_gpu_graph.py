@@ -22,7 +22,8 @@ TOL = {0: 1e-5, 1: 1e-3, 2: 1e-3, 3: 1e-3}
 def test_decode_and_prefill_graph_replays(gi, oracle, dev, kv_type):
     import torch
     H, kvh, hd, P, C = 32, 8, 128, 16, 64
-    # 1100 tokens take two splits and the merge kernel; 70 is a ragged tail.
+    # 1100 tokens take two work items, merged by the last to finish; 70 is a
+    # ragged tail.
     lens = [300, 70, 1100]
     pop = Populated(gi, dev, kv_type, 2, kvh, hd, P, lens, seed=11 + kv_type)
     stream = torch.cuda.Stream(dev)
@@ -82,3 +83,79 @@ def test_decode_and_prefill_graph_replays(gi, oracle, dev, kv_type):
             pop.pool.AttentionGQA(other, qd * 0.5, 0, bt, sl, H, scale, max(lens))
             other.mul_(2.0).add_(1.0)
         torch.cuda.synchronize()
+
+
+def test_workspace_growth_keeps_captured_graphs_valid(gi, oracle, dev):
+    """The decode workspace (split partials and arrival counters) grows with
+    the batch.  A graph captured at batch 3 must keep replaying bit for bit
+    after an eager call with a larger batch grew it (the buffers the graph
+    holds stay alive), and a call that would need it to grow while the
+    stream captures is refused (GI_ERR_BAD_ARG) without synchronising or
+    freeing anything; the first graph still replays afterwards."""
+    import torch
+    H, kvh, hd, P = 32, 8, 128, 16
+    lens = [300, 70, 1100]
+    pop = Populated(gi, dev, 1, 1, kvh, hd, P, lens, seed=31)
+    stream = torch.cuda.Stream(dev)
+    pop.pool.set_stream(stream.cuda_stream)
+    bt = pop.block_tables()
+    sl = torch.tensor(lens, dtype=torch.int32, device=dev)
+    qd, q = seeded((3, H * hd), 32, dev)
+    od = torch.empty((3, H * hd), device=dev)
+    scale = oracle.attn_scale(hd)
+
+    def step():
+        pop.pool.AttentionGQA(od, qd, 0, bt, sl, H, scale)
+
+    with torch.cuda.stream(stream):
+        step()
+    torch.cuda.synchronize()
+    ref = od.clone()
+    want = np.zeros((3, H * hd), np.float32)
+    for i, n in enumerate(lens):
+        ks, vs = pop.stored(0, i)
+        want[i] = oracle.attention_decode(q[i], oracle.widen(1, kvh * hd, ks),
+                                          oracle.widen(1, kvh * hd, vs), H, kvh, hd, n, scale)
+    assert float(rel_err_rows(ref.cpu().numpy(), want, H, hd).max()) <= 1e-3
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        step()
+
+    def replay_matches(tag):
+        od.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(od, ref), tag
+
+    replay_matches("first replay")
+    # eager call with 60 rows: the counters and partials grow
+    big = 60
+    bt_big = bt[torch.arange(big, device=dev) % 3].contiguous()
+    sl_big = sl[torch.arange(big, device=dev) % 3].contiguous()
+    q_big = qd[torch.arange(big, device=dev) % 3].contiguous()
+    o_big = torch.empty((big, H * hd), device=dev)
+    with torch.cuda.stream(stream):
+        pop.pool.AttentionGQA(o_big, q_big, 0, bt_big, sl_big, H, scale)
+    torch.cuda.synchronize()
+    pop.pool.synchronize()
+    got = o_big.cpu().numpy()
+    for r in range(big):
+        assert float(rel_err_rows(got[r], want[r % 3], H, hd).max()) <= 1e-3, r
+    replay_matches("replay after growth")
+    # growth while capturing is refused
+    huge = 200
+    bt_h = bt[torch.arange(huge, device=dev) % 3].contiguous()
+    sl_h = sl[torch.arange(huge, device=dev) % 3].contiguous()
+    q_h = qd[torch.arange(huge, device=dev) % 3].contiguous()
+    o_h = torch.empty((huge, H * hd), device=dev)
+    g2 = torch.cuda.CUDAGraph()
+    with pytest.raises(gi.GIError) as e:
+        with torch.cuda.graph(g2, stream=stream):
+            o_h.fill_(0.0)
+            pop.pool.AttentionGQA(o_h, q_h, 0, bt_h, sl_h, H, scale)
+    assert e.value.code == -3
+    assert "capturing" in str(e.value)
+    torch.cuda.synchronize()
+    replay_matches("replay after the refused capture")

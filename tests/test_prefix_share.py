@@ -221,6 +221,12 @@ def test_reference_prefix_cache(gi, oracle):
     assert k0.shape[0] == 5 and np.array_equal(k0, ka[:5])
     assert pc.FindLongestPrefix([999, 888, 777]) == (0, None)
     assert len(pc) == 1
+    # an entry keyed on more tokens than the sequence holds is refused: a hit
+    # on it would report 12 cached tokens for a 10-token fork
+    with pytest.raises(gi.GIError) as e:
+        pc.Store(list(range(12)), a)
+    assert e.value.code == -3
+    assert len(pc) == 1 and pc.FindLongestPrefix(list(range(12)) + [0]) == (0, None)
     pc.close()
 
 
