@@ -158,8 +158,6 @@ __global__ __launch_bounds__(NT) void attn_valu(DecodeArgs a)
             wsp[G * HD + 2 * tid] = -INFINITY;
             wsp[G * HD + 2 * tid + 1] = 0.0f;
         }
-        if (wsp)
-            merge_if_last<NT>(a, it, blockIdx.x, kvh, G, HD);
         return;
     }
 
@@ -284,8 +282,97 @@ __global__ __launch_bounds__(NT) void attn_valu(DecodeArgs a)
             wsp[G * HD + 2 * tid + 1] = s_l[tid];
         }
     }
-    if (wsp)
-        merge_if_last<NT>(a, it, blockIdx.x, kvh, G, HD);
+}
+
+// Combines the partials of split sequences (split_plan.h):
+//   out = sum_s acc_s e^(m_s - M) / sum_s l_s e^(m_s - M),  M = max_s m_s,
+// summed in split order (so the result does not depend on scheduling).
+// One workgroup per (kv head, sequence); sequences left whole exit at once.
+// Thread g first takes head g's maximum and denominator; the per-split
+// factors then go through LDS, so that every thread issues all of its
+// partial loads of a pass together.
+constexpr int kMergePass = 32; // splits per pass
+__global__ __launch_bounds__(256) void merge_splits(DecodeArgs a)
+{
+    const int kvh = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+    int first, n;
+    plan_seq<256>(a, b, first, n);
+    if (n <= 1)
+        return;
+    const int HD = a.L.head_dim, G = a.num_heads / a.L.num_kv_heads;
+    const int64_t step = (int64_t)a.L.num_kv_heads * G * (HD + 2);
+    const float *w0 = plan_slot(a, first, kvh, G, HD);
+    __shared__ float s_f[kMergePass][16]; // e^(m_s - M) of head g
+    __shared__ float s_M[16], s_den[16];
+    if (tid < G) {
+        const float *ml = w0 + G * HD + 2 * tid;
+        float M = -INFINITY;
+        for (int s0 = 0; s0 < n; s0 += 8) {
+            float m[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                m[i] = s0 + i < n ? ml[(s0 + i) * step] : -INFINITY;
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                M = fmaxf(M, m[i]);
+        }
+        float den = 0.0f;
+        if (M != -INFINITY) {
+            for (int s0 = 0; s0 < n; s0 += 8) {
+                float m[8], l[8];
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    m[i] = s0 + i < n ? ml[(s0 + i) * step] : -INFINITY;
+                    l[i] = s0 + i < n ? ml[(s0 + i) * step + 1] : 0.0f;
+                }
+#pragma unroll
+                for (int i = 0; i < 8; i++)
+                    if (m[i] != -INFINITY)
+                        den = fmaf(l[i], expf(m[i] - M), den);
+            }
+        }
+        s_M[tid] = M;
+        s_den[tid] = den;
+    }
+    // outputs of this thread: e = tid + 256 i < G * HD (G * HD <= 2048)
+    float num[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s0 = 0; s0 < n; s0 += kMergePass) {
+        const int ns = min(kMergePass, n - s0);
+        __syncthreads(); // s_M is set, and s_f is free again
+        for (int e = tid; e < ns * G; e += 256) {
+            const int s = e / G, g = e - s * G;
+            const float M = s_M[g], m = w0[(s0 + s) * step + G * HD + 2 * g];
+            s_f[s][g] = (M == -INFINITY || m == -INFINITY) ? 0.0f : expf(m - M);
+        }
+        __syncthreads();
+        for (int s1 = 0; s1 < ns; s1 += 8) {
+            float v[8][8];
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const int e = tid + 256 * i;
+                    v[k][i] = s1 + k < ns && e < G * HD ? w0[(s0 + s1 + k) * step + e] : 0.0f;
+                }
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const int e = tid + 256 * i;
+                    if (s1 + k < ns && e < G * HD)
+                        num[i] = fmaf(v[k][i], s_f[s1 + k][e / HD], num[i]);
+                }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int e = tid + 256 * i;
+        if (e < G * HD) {
+            const int g = e / HD, d = e - g * HD;
+            const float den = s_den[g];
+            a.out[((int64_t)b * a.num_heads + kvh * G + g) * HD + d] = den > 0.0f ? num[i] / den : 0.0f;
+        }
+    }
 }
 
 template <int KT>
@@ -321,16 +408,10 @@ void decode_plan(const PoolLayout &L, int num_cus, DecodeArgs &a)
 
 int decode_grid_items(const DecodeArgs &a) { return a.batch + a.plan_target; }
 
-size_t decode_counter_bytes(const PoolLayout &L, int batch)
-{
-    return ((size_t)batch * L.num_kv_heads * sizeof(int) + 255) / 256 * 256;
-}
-
-size_t decode_workspace_bytes(const PoolLayout &L, int batch, int num_heads, int grid_items)
+size_t decode_workspace_bytes(const PoolLayout &L, int num_heads, int grid_items)
 {
     const int G = num_heads / L.num_kv_heads;
-    return decode_counter_bytes(L, batch) +
-           (size_t)grid_items * L.num_kv_heads * G * (L.head_dim + 2) * sizeof(float);
+    return (size_t)grid_items * L.num_kv_heads * G * (L.head_dim + 2) * sizeof(float);
 }
 
 int decode_kernel_kind(const PoolLayout &L, int num_heads, int requested)
@@ -347,16 +428,23 @@ hipError_t launch_decode(const DecodeArgs &a, hipStream_t st)
     if (a.num_heads % L.num_kv_heads)
         return hipErrorInvalidValue;
     const int n_q = a.n_q > 0 ? a.n_q : 1;
-    if (a.plan_target > 0 && n_q == 1 && !a.start_pos && decode_kernel_kind(L, a.num_heads, a.kernel) == 1)
-        return launch_decode_mfma(a, st);
-    dim3 grid = a.plan_target > 0 ? dim3(decode_grid_items(a), L.num_kv_heads, 1)
-                                  : dim3(1, L.num_kv_heads, a.batch * n_q);
-    switch (L.kv_type) {
-    case KV_F32: return launch_valu_kt<KV_F32>(a, grid, st);
-    case KV_F16: return launch_valu_kt<KV_F16>(a, grid, st);
-    case KV_Q4_0: return launch_valu_kt<KV_Q4_0>(a, grid, st);
-    default: return launch_valu_kt<KV_Q8_0>(a, grid, st);
+    hipError_t e;
+    if (a.plan_target > 0 && n_q == 1 && !a.start_pos && decode_kernel_kind(L, a.num_heads, a.kernel) == 1) {
+        e = launch_decode_mfma(a, st);
+    } else {
+        dim3 grid = a.plan_target > 0 ? dim3(decode_grid_items(a), L.num_kv_heads, 1)
+                                      : dim3(1, L.num_kv_heads, a.batch * n_q);
+        switch (L.kv_type) {
+        case KV_F32: e = launch_valu_kt<KV_F32>(a, grid, st); break;
+        case KV_F16: e = launch_valu_kt<KV_F16>(a, grid, st); break;
+        case KV_Q4_0: e = launch_valu_kt<KV_Q4_0>(a, grid, st); break;
+        default: e = launch_valu_kt<KV_Q8_0>(a, grid, st); break;
+        }
     }
+    if (e != hipSuccess || a.plan_target <= 0)
+        return e;
+    hipLaunchKernelGGL(merge_splits, dim3(L.num_kv_heads, a.batch), dim3(256), 0, st, a);
+    return hipGetLastError();
 }
 
 hipError_t launch_prefill(const PrefillArgs &p, hipStream_t st)
@@ -380,7 +468,6 @@ hipError_t launch_prefill(const PrefillArgs &p, hipStream_t st)
     a.scale = p.scale;
     a.plan_target = 0; // one workgroup per (query, kv head), no split
     a.ws = nullptr;
-    a.plan_cnt = nullptr;
     a.status = p.status;
     a.kernel = 0;
     return launch_decode(a, st);

@@ -1008,8 +1008,6 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
             wsp[G * HD + 2 * threadIdx.x] = -INFINITY;
             wsp[G * HD + 2 * threadIdx.x + 1] = 0.0f;
         }
-        if (wsp)
-            merge_if_last<256>(a, it, blockIdx.x, kvh, G, HD);
         return;
     }
 
@@ -1275,8 +1273,6 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
             a.out[(qrow + hh) * HD + d] = den > 0.0f ? num / den : 0.0f;
         }
     }
-    if (wsp)
-        merge_if_last<256>(a, it, blockIdx.x, kvh, G, HD);
 }
 
 // GP: 0 for any group size up to 16 (hi/lo halves in separate products),

@@ -9,8 +9,7 @@
 
 namespace gi {
 
-// A device buffer that grows on demand (split-K partials, arrival counters,
-// activation splits).
+// A device buffer that grows on demand (split-K partials, activation splits).
 //
 // Growth needs a synchronisation and an allocation, which a stream that is
 // capturing a graph cannot take, so devbuf_reserve refuses to grow while the
@@ -26,10 +25,9 @@ struct DevBuffer {
 };
 
 // Makes b hold at least `need` bytes on the current device (allocating a
-// quarter more), noting whether `st` is capturing.  A new allocation is
-// cleared on st when `zero` is set.  Returns GI_OK or an error code with the
-// reason set; `what` names the caller in the message.
-int devbuf_reserve(DevBuffer &b, size_t need, bool zero, hipStream_t st, const char *what);
+// quarter more), noting whether `st` is capturing.  Returns GI_OK or an error
+// code with the reason set; `what` names the caller in the message.
+int devbuf_reserve(DevBuffer &b, size_t need, hipStream_t st, const char *what);
 
 // Frees b and every allocation it retired (the caller has drained the
 // streams that use them).

@@ -69,8 +69,7 @@ struct DecodeArgs {
     int plan_target;
     int plan_min;
     int plan_unit;
-    float *ws;     // partials of split sequences, decode_grid_items x kv heads slots
-    int *plan_cnt; // [batch][kv heads] arrival counters, zero between launches
+    float *ws; // partials of split sequences, decode_grid_items x kv heads slots
     int *status;
     int kernel; // -1 automatic, 0 vector ALU, 1 matrix core
 };
@@ -83,12 +82,11 @@ void decode_plan(const PoolLayout &L, int num_cus, DecodeArgs &a);
 // the plan's item count, batch + plan_target.
 int decode_grid_items(const DecodeArgs &a);
 
-// Bytes of decode workspace: the arrival counters (first, rounded to 256 B)
-// then the partial slots.
-size_t decode_counter_bytes(const PoolLayout &L, int batch);
-size_t decode_workspace_bytes(const PoolLayout &L, int batch, int num_heads, int grid_items);
+// Bytes of decode workspace: the partial slots of grid_items work items.
+size_t decode_workspace_bytes(const PoolLayout &L, int num_heads, int grid_items);
 
-// Returns hipErrorInvalidValue for shapes without a kernel instance.
+// The decode kernel, then (decode) the merge of split sequences.  Returns
+// hipErrorInvalidValue for shapes without a kernel instance.
 hipError_t launch_decode(const DecodeArgs &a, hipStream_t st);
 
 // Which kernel launch_decode uses for a layout/head count and a requested

@@ -563,7 +563,7 @@ int gi_matmul_batch(gi_weights *w, int batch, const float *x, float *y)
     hipError_t e = hipSetDevice(w->device);
     if (e != hipSuccess)
         return hip_fail(e, "gi_matmul_batch");
-    const int rc = devbuf_reserve(w->xsplit, 2 * nx + (size_t)batch_pad * 4, false, st, "gi_matmul_batch");
+    const int rc = devbuf_reserve(w->xsplit, 2 * nx + (size_t)batch_pad * 4, st, "gi_matmul_batch");
     if (rc != GI_OK)
         return rc;
     _Float16 *xh = (_Float16 *)w->xsplit.ptr;

@@ -28,7 +28,7 @@ int set_error(int code, const std::string &msg)
 
 void clear_error() { g_last_error.clear(); }
 
-int devbuf_reserve(DevBuffer &b, size_t need, bool zero, hipStream_t st, const char *what)
+int devbuf_reserve(DevBuffer &b, size_t need, hipStream_t st, const char *what)
 {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     hipError_t e = hipStreamIsCapturing(st, &cs);
@@ -63,10 +63,6 @@ int devbuf_reserve(DevBuffer &b, size_t need, bool zero, hipStream_t st, const c
     void *p = nullptr;
     if (hipMalloc(&p, want) != hipSuccess)
         return set_error(GI_ERR_OOM, std::string(what) + ": hipMalloc(" + std::to_string(want) + ") failed");
-    if (zero && (e = hipMemsetAsync(p, 0, want, st)) != hipSuccess) {
-        (void)hipFree(p);
-        return set_error(GI_ERR_HIP, std::string(what) + ": clear: " + hipGetErrorString(e));
-    }
     b.ptr = p;
     b.bytes = want;
     return GI_OK;
@@ -95,8 +91,7 @@ struct gi_paged {
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
     int *d_status = nullptr;
-    gi::DevBuffer plan_cnt; // decode: arrival counters of split sequences
-    gi::DevBuffer plan_ws;  // decode: partials of split sequences
+    gi::DevBuffer plan_ws; // decode: partials of split sequences
     int decode_kernel = -1; // -1 automatic, 0 vector ALU, 1 matrix core
     float2 *d_rope = nullptr; // (cos, sin) [rope_max_pos][rope_half]
     int rope_half = 0;
@@ -256,7 +251,6 @@ void gi_paged_destroy(gi_paged *h)
         (void)hipFree(h->d_status);
     if (h->d_layer_base)
         (void)hipFree(h->d_layer_base);
-    gi::devbuf_release(h->plan_cnt);
     gi::devbuf_release(h->plan_ws);
     if (h->d_rope)
         (void)hipFree(h->d_rope);
@@ -570,16 +564,10 @@ static int decode_locked(gi_paged *h, int layer, int batch, int num_heads, const
     a.status = h->d_status;
     a.kernel = h->decode_kernel;
     gi::decode_plan(h->L, h->num_cus, a);
-    int rc = gi::devbuf_reserve(h->plan_cnt, gi::decode_counter_bytes(h->L, batch), true, h->stream,
-                                "decode attention");
-    if (rc == GI_OK)
-        rc = gi::devbuf_reserve(h->plan_ws,
-                                gi::decode_workspace_bytes(h->L, batch, num_heads, gi::decode_grid_items(a)) -
-                                    gi::decode_counter_bytes(h->L, batch),
-                                false, h->stream, "decode attention");
+    const size_t need = gi::decode_workspace_bytes(h->L, num_heads, gi::decode_grid_items(a));
+    const int rc = gi::devbuf_reserve(h->plan_ws, need, h->stream, "decode attention");
     if (rc)
         return rc;
-    a.plan_cnt = (int *)h->plan_cnt.ptr;
     a.ws = (float *)h->plan_ws.ptr;
     hipError_t e = gi::launch_decode(a, h->stream);
     return e == hipSuccess ? GI_OK : hip_fail(e, "decode attention");

@@ -16,8 +16,10 @@
 //
 // A sequence with n_b > 1 leaves one partial per item (G rows of HD
 // unnormalised accumulators, then (m, l) per row, m in natural-log units);
-// the last of its n_b workgroups to finish merges them into out (so no
-// second launch is needed) and re-arms the sequence's arrival counter.
+// merge_splits, launched next on the same stream, combines them.  (Merging
+// in the decode launch by its last-arriving workgroup needs a device-scope
+// release by every split workgroup, which writes back its XCD's L2: that
+// measured 2.4x slower on ragged batches.)
 #pragma once
 
 #include "gi_kernels.h"
@@ -46,16 +48,14 @@ __device__ __forceinline__ int plan_len(const DecodeArgs &a, int b, int64_t cap,
     return len;
 }
 
-// Workgroup-wide (NT threads, every thread calls it): the plan entry of work
-// item `item`; false for items past the end of the list.  Lengths below zero
-// or beyond what the block table maps are clamped and raise FLAG_BAD_SLOT.
+// Workgroup-wide (NT threads, every thread calls it): the plan's chunk
+// length.  Lengths below zero or beyond what the block table maps are clamped
+// (and raise FLAG_BAD_SLOT when `flag` is set).
 template <int NT>
-__device__ bool plan_item(const DecodeArgs &a, int item, PlanItem &it)
+__device__ int plan_chunk(const DecodeArgs &a, bool flag)
 {
     constexpr int NW = NT / 64;
     __shared__ int64_t s_tot[NW];
-    __shared__ int s_cnt[NW];
-    __shared__ int s_hit[4];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int64_t cap = (int64_t)a.max_blocks * a.L.page_tokens;
     bool bad = false;
@@ -67,9 +67,7 @@ __device__ bool plan_item(const DecodeArgs &a, int item, PlanItem &it)
         sum += __shfl_xor(sum, o);
     if (lane == 0)
         s_tot[w] = sum;
-    if (tid == 0)
-        s_hit[0] = -1;
-    if (bad && blockIdx.x == 0 && blockIdx.y == 0 && a.status)
+    if (bad && flag && a.status)
         atomicOr(a.status, FLAG_BAD_SLOT);
     __syncthreads();
     int64_t total = 0;
@@ -78,14 +76,31 @@ __device__ bool plan_item(const DecodeArgs &a, int item, PlanItem &it)
         total += s_tot[i];
     int64_t per = (total + a.plan_target - 1) / a.plan_target;
     per = (per + a.plan_unit - 1) / a.plan_unit * a.plan_unit;
-    const int chunk = (int)(per > a.plan_min ? (per < (1 << 30) ? per : (1 << 30)) : a.plan_min);
+    return (int)(per > a.plan_min ? (per < (1 << 30) ? per : (1 << 30)) : a.plan_min);
+}
 
+__device__ __forceinline__ int plan_items(int len, int chunk) { return max(1, (len + chunk - 1) / chunk); }
+
+// Workgroup-wide: the plan entry of work item `item`; false for items past
+// the end of the list.
+template <int NT>
+__device__ bool plan_item(const DecodeArgs &a, int item, PlanItem &it)
+{
+    constexpr int NW = NT / 64;
+    __shared__ int s_cnt[NW];
+    __shared__ int s_hit[4];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int64_t cap = (int64_t)a.max_blocks * a.L.page_tokens;
+    if (tid == 0)
+        s_hit[0] = -1;
+    // (the barrier inside plan_chunk orders that store before the scan)
+    const int chunk = plan_chunk<NT>(a, blockIdx.x == 0 && blockIdx.y == 0);
     int carry = 0;
     for (int base = 0; base < a.batch; base += NT) {
         const int b = base + tid;
         bool unused = false;
         const int len = b < a.batch ? plan_len(a, b, cap, unused) : 0;
-        const int n = b < a.batch ? max(1, (len + chunk - 1) / chunk) : 0;
+        const int n = b < a.batch ? plan_items(len, chunk) : 0;
         int x = n; // inclusive scan over the wave
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
@@ -126,57 +141,36 @@ __device__ bool plan_item(const DecodeArgs &a, int item, PlanItem &it)
     return true;
 }
 
+// Workgroup-wide: the first item of sequence b and its item count.
+template <int NT>
+__device__ void plan_seq(const DecodeArgs &a, int b, int &first, int &n)
+{
+    constexpr int NW = NT / 64;
+    __shared__ int s_first[NW];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int64_t cap = (int64_t)a.max_blocks * a.L.page_tokens;
+    const int chunk = plan_chunk<NT>(a, false);
+    bool unused = false;
+    int sum = 0;
+    for (int c = tid; c < b; c += NT)
+        sum += plan_items(plan_len(a, c, cap, unused), chunk);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1)
+        sum += __shfl_xor(sum, o);
+    if (lane == 0)
+        s_first[w] = sum;
+    __syncthreads();
+    first = 0;
+#pragma unroll
+    for (int i = 0; i < NW; i++)
+        first += s_first[i];
+    n = plan_items(plan_len(a, b, cap, unused), chunk);
+}
+
 // Partial slot of work item `item` for kv head kvh (G * (HD + 2) floats).
 __device__ __forceinline__ float *plan_slot(const DecodeArgs &a, int item, int kvh, int G, int HD)
 {
     return a.ws + ((int64_t)item * a.L.num_kv_heads + kvh) * ((int64_t)G * (HD + 2));
-}
-
-// Workgroup-wide, after this workgroup has written its partial to its slot:
-// the last of the sequence's items to arrive merges every slot,
-//   out = sum_s acc_s e^(m_s - M) / sum_s l_s e^(m_s - M),  M = max_s m_s,
-// into out rows (b, kvh*G + g).
-template <int NT>
-__device__ void merge_if_last(const DecodeArgs &a, const PlanItem &it, int item, int kvh, int G, int HD)
-{
-    __shared__ int s_last;
-    // this workgroup's partial is visible device-wide before it is counted
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        int *cnt = a.plan_cnt + (int64_t)it.b * a.L.num_kv_heads + kvh;
-        const int last = atomicAdd(cnt, 1) == it.nsplit - 1;
-        if (last)
-            atomicExch(cnt, 0); // every item has arrived: ready for the next launch
-        s_last = last;
-    }
-    __syncthreads();
-    if (!s_last)
-        return;
-    // the other items' partials are read after their counts were seen
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    const int KVH = a.L.num_kv_heads;
-    const int64_t stride = (int64_t)G * (HD + 2), step = (int64_t)KVH * stride;
-    const float *w0 = plan_slot(a, item - it.split, kvh, G, HD);
-    for (int e = threadIdx.x; e < G * HD; e += NT) {
-        const int g = e / HD, d = e - g * HD;
-        float M = -INFINITY;
-        for (int s = 0; s < it.nsplit; s++)
-            M = fmaxf(M, w0[s * step + G * HD + 2 * g]);
-        float num = 0.0f, den = 0.0f;
-        if (M != -INFINITY) {
-            for (int s = 0; s < it.nsplit; s++) {
-                const float *w = w0 + s * step;
-                const float m = w[G * HD + 2 * g];
-                if (m == -INFINITY)
-                    continue;
-                const float f = expf(m - M);
-                num = fmaf(w[g * HD + d], f, num);
-                den = fmaf(w[G * HD + 2 * g + 1], f, den);
-            }
-        }
-        a.out[((int64_t)it.b * a.num_heads + kvh * G + g) * HD + d] = den > 0.0f ? num / den : 0.0f;
-    }
 }
 
 } // namespace gi

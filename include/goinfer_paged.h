@@ -261,7 +261,7 @@ int gi_paged_gather(gi_paged *h, int layer, const int32_t *block_table, int n_to
  * zero or beyond max_blocks * page_tokens is clamped and reported by
  * gi_synchronize as GI_ERR_BAD_PAGE.
  *
- * Workspace: the handle keeps split partials and arrival counters sized by
+ * Workspace: the handle keeps the partials of split sequences, sized by
  * batch.  A call that needs them to grow while the handle's stream is
  * capturing a graph fails with GI_ERR_BAD_ARG (make one eager call with the
  * largest batch first); once any call has been captured, growth keeps the old

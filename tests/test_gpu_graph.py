@@ -22,8 +22,8 @@ TOL = {0: 1e-5, 1: 1e-3, 2: 1e-3, 3: 1e-3}
 def test_decode_and_prefill_graph_replays(gi, oracle, dev, kv_type):
     import torch
     H, kvh, hd, P, C = 32, 8, 128, 16, 64
-    # 1100 tokens take two work items, merged by the last to finish; 70 is a
-    # ragged tail.
+    # 1100 tokens take two work items and the merge kernel; 70 is a ragged
+    # tail.
     lens = [300, 70, 1100]
     pop = Populated(gi, dev, kv_type, 2, kvh, hd, P, lens, seed=11 + kv_type)
     stream = torch.cuda.Stream(dev)
@@ -86,8 +86,8 @@ def test_decode_and_prefill_graph_replays(gi, oracle, dev, kv_type):
 
 
 def test_workspace_growth_keeps_captured_graphs_valid(gi, oracle, dev):
-    """The decode workspace (split partials and arrival counters) grows with
-    the batch.  A graph captured at batch 3 must keep replaying bit for bit
+    """The decode workspace (partials of split sequences) grows with the
+    batch.  A graph captured at batch 3 must keep replaying bit for bit
     after an eager call with a larger batch grew it (the buffers the graph
     holds stay alive), and a call that would need it to grow while the
     stream captures is refused (GI_ERR_BAD_ARG) without synchronising or
@@ -130,7 +130,7 @@ def test_workspace_growth_keeps_captured_graphs_valid(gi, oracle, dev):
         assert torch.equal(od, ref), tag
 
     replay_matches("first replay")
-    # eager call with 60 rows: the counters and partials grow
+    # eager call with 60 rows: the partials grow
     big = 60
     bt_big = bt[torch.arange(big, device=dev) % 3].contiguous()
     sl_big = sl[torch.arange(big, device=dev) % 3].contiguous()
