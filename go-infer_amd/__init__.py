@@ -94,6 +94,8 @@ EXPORTS = {
     "gi_paged_gather": (_c_int, [_vp, _c_int, _vp, _c_int, _vp, _vp, _c_int]),
     "gi_paged_decode_attention": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _c_int,
                                            _vp, _c_int, ctypes.c_float]),
+    "gi_paged_decode_attention_noalloc": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp, _vp,
+                                                   _c_int, _vp, _c_int, ctypes.c_float]),
     "gi_paged_decode_step": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp,
                                       _c_int, _vp, _c_int, ctypes.c_float]),
     "gi_paged_prefill_attention": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp,
@@ -514,6 +516,21 @@ class PagedKVCache:
             _ptr(out, torch.float32, "out"), _ptr(block_tables, torch.int32, "block_tables"),
             mb, _ptr(seq_lens, torch.int32, "seq_lens"),
             int(max_seq_len), float(attn_scale)))
+
+    def AttentionGQANoAlloc(self, out, q, layer, block_tables, seq_lens, num_heads, attn_scale,
+                            max_seq_len=None):
+        """AttentionGQA through the entry point that allocates nothing (its
+        split partials in the library's fixed per-device scratch)."""
+        import torch
+        batch = int(seq_lens.numel())
+        mb = _tables(block_tables, batch)
+        qn = batch * num_heads * self.head_dim
+        _need(_numel(q) == qn and _numel(out) == qn,
+              "AttentionGQANoAlloc: q and out must be [%d, %d]" % (batch, num_heads * self.head_dim))
+        _check(lib().gi_paged_decode_attention_noalloc(
+            self._h, layer, batch, num_heads, _ptr(q, torch.float32, "q"),
+            _ptr(out, torch.float32, "out"), _ptr(block_tables, torch.int32, "block_tables"),
+            mb, _ptr(seq_lens, torch.int32, "seq_lens"), int(max_seq_len or 0), float(attn_scale)))
 
     def DecodeStep(self, out, q, k, v, layer, block_tables, seq_lens, num_heads, attn_scale,
                    max_seq_len=None):

@@ -92,6 +92,7 @@ struct gi_paged {
     hipStream_t stream = nullptr;
     int *d_status = nullptr;
     gi::DevBuffer plan_ws; // decode: partials of split sequences
+    void *scratch = nullptr; // this device's address of `scratch` (allocate-nothing decode)
     int decode_kernel = -1; // -1 automatic, 0 vector ALU, 1 matrix core
     float2 *d_rope = nullptr; // (cos, sin) [rope_max_pos][rope_half]
     int rope_half = 0;
@@ -121,6 +122,37 @@ int check_layer(const gi_paged *h, int layer, const char *what)
     if (layer < 0 || layer >= h->L.num_layers)
         return gi::set_error(GI_ERR_BAD_ARG, std::string(what) + ": layer " + std::to_string(layer) +
                                                  " out of range");
+    return GI_OK;
+}
+
+// Scratch of gi_paged_decode_attention_noalloc: the split partials live in
+// this fixed array of the code object (one per device, held until the
+// process ends) instead of the handle's growable workspace.  Its name is a
+// host-side stand-in for the array, not a device address: host code uses the
+// address hipGetSymbolAddress gives on each device (scratch_address).
+constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
+__device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+std::mutex g_scratch_mu;
+std::vector<void *> g_scratch_addr; // by device id
+
+// With `device` current: the device address of `scratch` there, looked up
+// once per device.
+int scratch_address(int device, void **addr)
+{
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    if ((size_t)device < g_scratch_addr.size() && g_scratch_addr[(size_t)device]) {
+        *addr = g_scratch_addr[(size_t)device];
+        return GI_OK;
+    }
+    void *p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+        return hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol, "scratch: hipGetSymbolAddress");
+    if (g_scratch_addr.size() <= (size_t)device)
+        g_scratch_addr.resize((size_t)device + 1, nullptr);
+    g_scratch_addr[(size_t)device] = p;
+    *addr = p;
     return GI_OK;
 }
 
@@ -192,8 +224,8 @@ int gi_paged_create(int num_layers, int num_kv_heads, int head_dim, int page_tok
         return rc;
     }
     h->stream = h->own_stream;
-    int rc = GI_OK;
-    if (hipMalloc((void **)&h->d_status, sizeof(int)) != hipSuccess) {
+    int rc = scratch_address(h->device, &h->scratch);
+    if (rc == GI_OK && hipMalloc((void **)&h->d_status, sizeof(int)) != hipSuccess) {
         h->d_status = nullptr;
         rc = gi::set_error(GI_ERR_OOM, "gi_paged_create: status word");
     }
@@ -544,9 +576,12 @@ int gi_paged_gather(gi_paged *h, int layer, const int32_t *block_table, int n_to
     return e == hipSuccess ? GI_OK : hip_fail(e, "gi_paged_gather");
 }
 
+// fixed_ws: the allocate-nothing form's scratch (fixed_cap bytes) in place
+// of the handle's growable workspace.
 static int decode_locked(gi_paged *h, int layer, int batch, int num_heads, const float *q,
                          float *out, const int32_t *block_tables, int max_blocks,
-                         const int32_t *seq_lens, float scale)
+                         const int32_t *seq_lens, float scale, void *fixed_ws = nullptr,
+                         size_t fixed_cap = 0)
 {
     gi::DecodeArgs a{};
     a.L = h->L;
@@ -565,10 +600,19 @@ static int decode_locked(gi_paged *h, int layer, int batch, int num_heads, const
     a.kernel = h->decode_kernel;
     gi::decode_plan(h->L, h->num_cus, a);
     const size_t need = gi::decode_workspace_bytes(h->L, num_heads, gi::decode_grid_items(a));
-    const int rc = gi::devbuf_reserve(h->plan_ws, need, h->stream, "decode attention");
-    if (rc)
-        return rc;
-    a.ws = (float *)h->plan_ws.ptr;
+    if (fixed_ws) {
+        if (need > fixed_cap)
+            return gi::set_error(GI_ERR_BAD_ARG,
+                                 "gi_paged_decode_attention_noalloc: this batch needs " + std::to_string(need) +
+                                     " bytes of scratch; the fixed maximum is " + std::to_string(fixed_cap) +
+                                     " (use gi_paged_decode_attention)");
+        a.ws = (float *)fixed_ws;
+    } else {
+        const int rc = gi::devbuf_reserve(h->plan_ws, need, h->stream, "decode attention");
+        if (rc)
+            return rc;
+        a.ws = (float *)h->plan_ws.ptr;
+    }
     hipError_t e = gi::launch_decode(a, h->stream);
     return e == hipSuccess ? GI_OK : hip_fail(e, "decode attention");
 }
@@ -605,6 +649,21 @@ int gi_paged_decode_attention(gi_paged *h, int layer, int batch, int num_heads, 
         return GI_OK;
     std::lock_guard<std::mutex> g(h->mu);
     return decode_locked(h, layer, batch, num_heads, q, out, block_tables, max_blocks, seq_lens, scale);
+}
+
+int gi_paged_decode_attention_noalloc(gi_paged *h, int layer, int batch, int num_heads, const float *q,
+                                      float *out, const int32_t *block_tables, int max_blocks,
+                                      const int32_t *seq_lens, int max_seq_len, float scale)
+{
+    int rc = enter(h, "gi_paged_decode_attention_noalloc");
+    if (rc || (rc = check_decode_args(h, layer, batch, num_heads, q, out, block_tables, max_blocks, seq_lens,
+                                      max_seq_len, scale, "gi_paged_decode_attention_noalloc")))
+        return rc;
+    if (batch == 0)
+        return GI_OK;
+    std::lock_guard<std::mutex> g(h->mu);
+    return decode_locked(h, layer, batch, num_heads, q, out, block_tables, max_blocks, seq_lens, scale, h->scratch,
+                         kNoAllocScratchBytes);
 }
 
 int gi_paged_decode_step(gi_paged *h, int layer, int batch, int num_heads, const float *q,

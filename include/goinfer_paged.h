@@ -270,6 +270,20 @@ int gi_paged_decode_attention(gi_paged *h, int layer, int batch, int num_heads, 
                               float *out, const int32_t *block_tables, int max_blocks,
                               const int32_t *seq_lens, int max_seq_len, float scale);
 
+/* gi_paged_decode_attention that allocates nothing.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, hosts that forbid it).  The
+ * split partials live in a fixed 32 MiB scratch array that the library holds
+ * on each device it runs on until the process ends, instead of the handle's
+ * growable workspace; a batch that would need more (about 2,000 sequences of
+ * Llama-3-8B shape) fails with GI_ERR_BAD_ARG.  Every call on one device
+ * shares that array, so calls that overlap on one device (other handles or
+ * streams) race: serialise them.  Same arguments and results as
+ * gi_paged_decode_attention. */
+int gi_paged_decode_attention_noalloc(gi_paged *h, int layer, int batch, int num_heads, const float *q,
+                                      float *out, const int32_t *block_tables, int max_blocks,
+                                      const int32_t *seq_lens, int max_seq_len, float scale);
+
 /* One decode step of one layer: gi_paged_append_at_len of k/v, then
  * gi_paged_decode_attention over seq_lens[b] tokens (the new token
  * included), as Forward stores then attends (forward.go:236-267). */

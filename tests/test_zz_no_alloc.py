@@ -1,0 +1,59 @@
+"""The decode entry point that allocates nothing
+(gi_paged_decode_attention_noalloc): its split partials live in the
+library's fixed per-device scratch array instead of the handle's workspace.
+Called through the C ABI, its output must equal gi_paged_decode_attention's
+bit for bit (same kernels, same split plan, same merge order) on two calls in
+a row, the second with a smaller batch and shorter contexts (the scratch keeps
+the first call's contents), and both must match the oracle (forward.go:
+242-267) within the fp16 tolerance 1e-3.  A batch whose partials would not fit
+the fixed maximum is refused."""
+import numpy as np
+import pytest
+
+from gpu_util import Populated, rel_err_rows, seeded
+
+pytestmark = pytest.mark.gpu
+
+
+def test_noalloc_decode_matches_the_allocating_entry_point(gi, oracle, dev):
+    import torch
+    H, kvh, hd, P = 32, 8, 128, 16
+    lens = [5000, 300, 2048, 1, 4100, 777]
+    pop = Populated(gi, dev, 1, 1, kvh, hd, P, lens, seed=41)
+    bt = pop.block_tables()
+    scale = oracle.attn_scale(hd)
+    qd, q = seeded((len(lens), H * hd), 42, dev)
+    # second call: fewer sequences and shorter contexts
+    small = [0, 5, 1]
+    lens2 = [1500, 777, 64]
+    for rows, ls in ((list(range(len(lens))), lens), (small, lens2)):
+        idx = torch.tensor(rows, device=dev)
+        btr = bt[idx].contiguous()
+        sl = torch.tensor(ls, dtype=torch.int32, device=dev)
+        qr = qd[idx].contiguous()
+        want = torch.full_like(qr, float("nan"))
+        got = torch.full_like(qr, float("nan"))
+        pop.pool.AttentionGQA(want, qr, 0, btr, sl, H, scale)
+        pop.pool.AttentionGQANoAlloc(got, qr, 0, btr, sl, H, scale)
+        pop.pool.synchronize()
+        assert torch.equal(got, want), rows
+        o = got.cpu().numpy()
+        for r, (i, n) in enumerate(zip(rows, ls)):
+            ks, vs = pop.stored(0, i)
+            w = oracle.attention_decode(q[i], oracle.widen(1, kvh * hd, ks[:n]),
+                                        oracle.widen(1, kvh * hd, vs[:n]), H, kvh, hd, n, scale)
+            assert float(rel_err_rows(o[r], w, H, hd).max()) <= 1e-3, (i, n)
+
+
+def test_noalloc_decode_refuses_a_batch_beyond_its_scratch(gi, oracle, dev):
+    import torch
+    H, kvh, hd, P = 32, 8, 128, 16
+    pop = Populated(gi, dev, 1, 1, kvh, hd, P, [40], seed=43)
+    B = 4096
+    bt = pop.block_tables()[torch.zeros(B, dtype=torch.long, device=dev)].contiguous()
+    sl = torch.full((B,), 40, dtype=torch.int32, device=dev)
+    q = torch.zeros((B, H * hd), device=dev)
+    out = torch.zeros_like(q)
+    with pytest.raises(gi.GIError) as e:
+        pop.pool.AttentionGQANoAlloc(out, q, 0, bt, sl, H, oracle.attn_scale(hd))
+    assert e.value.code == -3 and "scratch" in str(e.value)
