@@ -48,7 +48,7 @@ hipError_t launch_copy_pages(const PoolLayout &L, uint8_t *const *layer_base, in
 // float32, block_tables is [batch][max_blocks], sequence b attends its first
 // seq_lens[b] tokens; the launch is cut into work items by the split plan
 // (split_plan.h), grid (decode_grid_items, kv heads).  The vector kernel also
-// serves chunked prefill (plan_target 0): n_q queries per sequence, query i of
+// serves chunked prefill (plan_units 0): n_q queries per sequence, query i of
 // sequence b attends start_pos[b] + i + 1 tokens, q/out are
 // [batch][n_q][num_heads][head_dim], grid (1, kv heads, batch * n_q).
 struct DecodeArgs {
@@ -64,26 +64,26 @@ struct DecodeArgs {
     const int32_t *start_pos; // prefill only: tokens cached before the chunk
     int num_heads;
     float scale;
-    // split plan (decode): work items per kv head aimed at, the shortest
-    // split and the split granularity in tokens; 0 targets: no plan
-    int plan_target;
-    int plan_min;
-    int plan_unit;
-    float *ws; // partials of split sequences, decode_grid_items x kv heads slots
+    // decode work plan (split_plan.h): work units per kv head (0: no plan)
+    int plan_units;
+    float *ws;      // partials of split sequences: 2 slots per unit and kv head
+    int *plan_desc; // merge descriptors: 2 ints per unit (after the slots)
     int *status;
     int kernel; // -1 automatic, 0 vector ALU, 1 matrix core
 };
 
-// Split-plan parameters of a decode launch on a device with num_cus CUs
-// (fills plan_target, plan_min, plan_unit).
-void decode_plan(const PoolLayout &L, int num_cus, DecodeArgs &a);
+// Work units of a decode launch on a device with num_cus CUs (fills
+// plan_units; a.batch, a.num_heads and a.kernel must be set).  max_len: the
+// longest sequence if the caller knows it, else 0.
+void decode_plan(const PoolLayout &L, int num_cus, int max_len, DecodeArgs &a);
 
-// Grid width (work items per kv head) of a decode launch: an upper bound of
-// the plan's item count, batch + plan_target.
+// Grid width (workgroups per kv head) of a decode launch.
 int decode_grid_items(const DecodeArgs &a);
 
-// Bytes of decode workspace: the partial slots of grid_items work items.
-size_t decode_workspace_bytes(const PoolLayout &L, int num_heads, int grid_items);
+// Bytes of decode workspace: two partial slots per unit and kv head, then
+// the units' merge descriptors (at decode_desc_offset).
+size_t decode_desc_offset(const PoolLayout &L, int num_heads, int plan_units);
+size_t decode_workspace_bytes(const PoolLayout &L, int num_heads, int plan_units);
 
 // The decode kernel, then (decode) the merge of split sequences.  Returns
 // hipErrorInvalidValue for shapes without a kernel instance.

@@ -130,7 +130,7 @@ int check_layer(const gi_paged *h, int layer, const char *what)
 // process ends) instead of the handle's growable workspace.  Its name is a
 // host-side stand-in for the array, not a device address: host code uses the
 // address hipGetSymbolAddress gives on each device (scratch_address).
-constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
+constexpr size_t kNoAllocScratchBytes = (size_t)8 << 20;
 __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 
 std::mutex g_scratch_mu;
@@ -580,7 +580,7 @@ int gi_paged_gather(gi_paged *h, int layer, const int32_t *block_table, int n_to
 // of the handle's growable workspace.
 static int decode_locked(gi_paged *h, int layer, int batch, int num_heads, const float *q,
                          float *out, const int32_t *block_tables, int max_blocks,
-                         const int32_t *seq_lens, float scale, void *fixed_ws = nullptr,
+                         const int32_t *seq_lens, int max_seq_len, float scale, void *fixed_ws = nullptr,
                          size_t fixed_cap = 0)
 {
     gi::DecodeArgs a{};
@@ -598,12 +598,15 @@ static int decode_locked(gi_paged *h, int layer, int batch, int num_heads, const
     a.scale = scale;
     a.status = h->d_status;
     a.kernel = h->decode_kernel;
-    gi::decode_plan(h->L, h->num_cus, a);
-    const size_t need = gi::decode_workspace_bytes(h->L, num_heads, gi::decode_grid_items(a));
+    // max_seq_len only sizes the grid of small launches (a hint, see
+    // decode_plan); the kernels read the lengths on the device
+    const int64_t mapped = (int64_t)max_blocks * h->L.page_tokens;
+    gi::decode_plan(h->L, h->num_cus, (int)(max_seq_len < mapped ? max_seq_len : mapped), a);
+    const size_t need = gi::decode_workspace_bytes(h->L, num_heads, a.plan_units);
     if (fixed_ws) {
         if (need > fixed_cap)
             return gi::set_error(GI_ERR_BAD_ARG,
-                                 "gi_paged_decode_attention_noalloc: this batch needs " + std::to_string(need) +
+                                 "gi_paged_decode_attention_noalloc: this shape needs " + std::to_string(need) +
                                      " bytes of scratch; the fixed maximum is " + std::to_string(fixed_cap) +
                                      " (use gi_paged_decode_attention)");
         a.ws = (float *)fixed_ws;
@@ -613,6 +616,7 @@ static int decode_locked(gi_paged *h, int layer, int batch, int num_heads, const
             return rc;
         a.ws = (float *)h->plan_ws.ptr;
     }
+    a.plan_desc = (int *)((uint8_t *)a.ws + gi::decode_desc_offset(h->L, num_heads, a.plan_units));
     hipError_t e = gi::launch_decode(a, h->stream);
     return e == hipSuccess ? GI_OK : hip_fail(e, "decode attention");
 }
@@ -648,7 +652,7 @@ int gi_paged_decode_attention(gi_paged *h, int layer, int batch, int num_heads, 
     if (batch == 0)
         return GI_OK;
     std::lock_guard<std::mutex> g(h->mu);
-    return decode_locked(h, layer, batch, num_heads, q, out, block_tables, max_blocks, seq_lens, scale);
+    return decode_locked(h, layer, batch, num_heads, q, out, block_tables, max_blocks, seq_lens, max_seq_len, scale);
 }
 
 int gi_paged_decode_attention_noalloc(gi_paged *h, int layer, int batch, int num_heads, const float *q,
@@ -662,8 +666,8 @@ int gi_paged_decode_attention_noalloc(gi_paged *h, int layer, int batch, int num
     if (batch == 0)
         return GI_OK;
     std::lock_guard<std::mutex> g(h->mu);
-    return decode_locked(h, layer, batch, num_heads, q, out, block_tables, max_blocks, seq_lens, scale, h->scratch,
-                         kNoAllocScratchBytes);
+    return decode_locked(h, layer, batch, num_heads, q, out, block_tables, max_blocks, seq_lens, max_seq_len, scale,
+                         h->scratch, kNoAllocScratchBytes);
 }
 
 int gi_paged_decode_step(gi_paged *h, int layer, int batch, int num_heads, const float *q,
@@ -683,7 +687,7 @@ int gi_paged_decode_step(gi_paged *h, int layer, int batch, int num_heads, const
                                             max_blocks, seq_lens, k, v, h->d_status, h->stream);
     if (e != hipSuccess)
         return hip_fail(e, "gi_paged_decode_step: append");
-    return decode_locked(h, layer, batch, num_heads, q, out, block_tables, max_blocks, seq_lens, scale);
+    return decode_locked(h, layer, batch, num_heads, q, out, block_tables, max_blocks, seq_lens, max_seq_len, scale);
 }
 
 int gi_paged_rope_decode_step(gi_paged *h, int layer, int batch, int num_heads, float *q, const float *k,
@@ -704,7 +708,7 @@ int gi_paged_rope_decode_step(gi_paged *h, int layer, int batch, int num_heads, 
                                           h->stream);
     if (e != hipSuccess)
         return hip_fail(e, "gi_paged_rope_decode_step: rope + append");
-    return decode_locked(h, layer, batch, num_heads, q, out, block_tables, max_blocks, seq_lens, scale);
+    return decode_locked(h, layer, batch, num_heads, q, out, block_tables, max_blocks, seq_lens, max_seq_len, scale);
 }
 
 int gi_paged_prefill_attention(gi_paged *h, int layer, int batch, int chunk_len, int num_heads,

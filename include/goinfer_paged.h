@@ -255,14 +255,16 @@ int gi_paged_gather(gi_paged *h, int layer, const int32_t *block_table, int n_to
  * b attends its first seq_lens[b] tokens.  q-head h reads kv head h /
  * (num_heads / num_kv_heads) (forward.go:249).
  *
- * The kernels split the batch's context into about equal work items from the
+ * The kernels cut the batch's context into equal work ranges from the
  * lengths in device memory, so every seq_lens[b] token is attended whatever
- * max_seq_len says (it is only checked to be >= 0; 0 is fine); a length below
- * zero or beyond max_blocks * page_tokens is clamped and reported by
- * gi_synchronize as GI_ERR_BAD_PAGE.
+ * max_seq_len says.  max_seq_len (>= 0; 0 means unknown) is a hint that only
+ * shrinks the grid of small launches.  A length below zero or beyond
+ * max_blocks * page_tokens is clamped and reported by gi_synchronize as
+ * GI_ERR_BAD_PAGE.
  *
- * Workspace: the handle keeps the partials of split sequences, sized by
- * batch.  A call that needs them to grow while the handle's stream is
+ * Workspace: the handle keeps the partials of split sequences, two slots per
+ * work unit (sized by the device's CUs and, for a small stream, by
+ * max_seq_len).  A call that needs them to grow while the handle's stream is
  * capturing a graph fails with GI_ERR_BAD_ARG (make one eager call with the
  * largest batch first); once any call has been captured, growth keeps the old
  * buffers alive until gi_paged_destroy, so captured graphs stay valid. */
@@ -273,10 +275,11 @@ int gi_paged_decode_attention(gi_paged *h, int layer, int batch, int num_heads, 
 /* gi_paged_decode_attention that allocates nothing.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, hosts that forbid it).  The
- * split partials live in a fixed 32 MiB scratch array that the library holds
+ * split partials live in a fixed 8 MiB scratch array that the library holds
  * on each device it runs on until the process ends, instead of the handle's
- * growable workspace; a batch that would need more (about 2,000 sequences of
- * Llama-3-8B shape) fails with GI_ERR_BAD_ARG.  Every call on one device
+ * growable workspace.  The partials do not grow with the batch: every batch
+ * fits up to 8 query heads per kv head at head_dim 128 (more heads per kv
+ * head fail with GI_ERR_BAD_ARG).  Every call on one device
  * shares that array, so calls that overlap on one device (other handles or
  * streams) race: serialise them.  Same arguments and results as
  * gi_paged_decode_attention. */

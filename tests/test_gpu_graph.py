@@ -86,12 +86,14 @@ def test_decode_and_prefill_graph_replays(gi, oracle, dev, kv_type):
 
 
 def test_workspace_growth_keeps_captured_graphs_valid(gi, oracle, dev):
-    """The decode workspace (partials of split sequences) grows with the
-    batch.  A graph captured at batch 3 must keep replaying bit for bit
-    after an eager call with a larger batch grew it (the buffers the graph
-    holds stay alive), and a call that would need it to grow while the
-    stream captures is refused (GI_ERR_BAD_ARG) without synchronising or
-    freeing anything; the first graph still replays afterwards."""
+    """The decode workspace (two partial slots per work unit) grows with the
+    number of units and with the query heads per kv head.  A graph captured
+    with a small stream (max_seq_len 1100: a few units) must keep replaying
+    bit for bit after an eager call with more units grew it (the buffers the
+    graph holds stay alive), and a call that would need it to grow while the
+    stream captures (twice the heads per kv head) is refused
+    (GI_ERR_BAD_ARG) without synchronising or freeing anything; the first
+    graph still replays afterwards."""
     import torch
     H, kvh, hd, P = 32, 8, 128, 16
     lens = [300, 70, 1100]
@@ -105,7 +107,7 @@ def test_workspace_growth_keeps_captured_graphs_valid(gi, oracle, dev):
     scale = oracle.attn_scale(hd)
 
     def step():
-        pop.pool.AttentionGQA(od, qd, 0, bt, sl, H, scale)
+        pop.pool.AttentionGQA(od, qd, 0, bt, sl, H, scale, max(lens))
 
     with torch.cuda.stream(stream):
         step()
@@ -130,31 +132,30 @@ def test_workspace_growth_keeps_captured_graphs_valid(gi, oracle, dev):
         assert torch.equal(od, ref), tag
 
     replay_matches("first replay")
-    # eager call with 60 rows: the partials grow
+    # eager call with 60 rows and no length hint: a unit per wave of two
+    # workgroups per CU, so the partials grow
     big = 60
     bt_big = bt[torch.arange(big, device=dev) % 3].contiguous()
     sl_big = sl[torch.arange(big, device=dev) % 3].contiguous()
     q_big = qd[torch.arange(big, device=dev) % 3].contiguous()
     o_big = torch.empty((big, H * hd), device=dev)
     with torch.cuda.stream(stream):
-        pop.pool.AttentionGQA(o_big, q_big, 0, bt_big, sl_big, H, scale)
+        pop.pool.AttentionGQA(o_big, q_big, 0, bt_big, sl_big, H, scale, 0)
     torch.cuda.synchronize()
     pop.pool.synchronize()
     got = o_big.cpu().numpy()
     for r in range(big):
         assert float(rel_err_rows(got[r], want[r % 3], H, hd).max()) <= 1e-3, r
     replay_matches("replay after growth")
-    # growth while capturing is refused
-    huge = 200
-    bt_h = bt[torch.arange(huge, device=dev) % 3].contiguous()
-    sl_h = sl[torch.arange(huge, device=dev) % 3].contiguous()
-    q_h = qd[torch.arange(huge, device=dev) % 3].contiguous()
-    o_h = torch.empty((huge, H * hd), device=dev)
+    # growth while capturing is refused: 64 query heads (8 per kv head)
+    # double the partial slots
+    q64 = torch.zeros((3, 2 * H * hd), device=dev)
+    o64 = torch.empty_like(q64)
     g2 = torch.cuda.CUDAGraph()
     with pytest.raises(gi.GIError) as e:
         with torch.cuda.graph(g2, stream=stream):
-            o_h.fill_(0.0)
-            pop.pool.AttentionGQA(o_h, q_h, 0, bt_h, sl_h, H, scale)
+            o64.fill_(0.0)
+            pop.pool.AttentionGQA(o64, q64, 0, bt, sl, 2 * H, scale, 0)
     assert e.value.code == -3
     assert "capturing" in str(e.value)
     torch.cuda.synchronize()

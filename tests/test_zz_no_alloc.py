@@ -5,8 +5,8 @@ Called through the C ABI, its output must equal gi_paged_decode_attention's
 bit for bit (same kernels, same split plan, same merge order) on two calls in
 a row, the second with a smaller batch and shorter contexts (the scratch keeps
 the first call's contents), and both must match the oracle (forward.go:
-242-267) within the fp16 tolerance 1e-3.  A batch whose partials would not fit
-the fixed maximum is refused."""
+242-267) within the fp16 tolerance 1e-3.  A shape whose partials would not
+fit the fixed maximum is refused."""
 import numpy as np
 import pytest
 
@@ -45,14 +45,17 @@ def test_noalloc_decode_matches_the_allocating_entry_point(gi, oracle, dev):
             assert float(rel_err_rows(o[r], w, H, hd).max()) <= 1e-3, (i, n)
 
 
-def test_noalloc_decode_refuses_a_batch_beyond_its_scratch(gi, oracle, dev):
+def test_noalloc_decode_refuses_a_shape_beyond_its_scratch(gi, oracle, dev):
+    """The partials take two slots per work unit (two workgroups per CU) of
+    G * (head_dim + 2) floats per kv head: with 16 query heads per kv head at
+    head_dim 128 that is 8.5 MB, beyond the fixed 8 MiB scratch, and the call
+    is refused before any launch."""
     import torch
-    H, kvh, hd, P = 32, 8, 128, 16
-    pop = Populated(gi, dev, 1, 1, kvh, hd, P, [40], seed=43)
-    B = 4096
-    bt = pop.block_tables()[torch.zeros(B, dtype=torch.long, device=dev)].contiguous()
-    sl = torch.full((B,), 40, dtype=torch.int32, device=dev)
-    q = torch.zeros((B, H * hd), device=dev)
+    H, kvh, hd, P = 128, 8, 128, 16
+    pop = Populated(gi, dev, 1, 1, kvh, hd, P, [40, 3000], seed=43)
+    bt = pop.block_tables()
+    sl = torch.tensor([40, 3000], dtype=torch.int32, device=dev)
+    q = torch.zeros((2, H * hd), device=dev)
     out = torch.zeros_like(q)
     with pytest.raises(gi.GIError) as e:
         pop.pool.AttentionGQANoAlloc(out, q, 0, bt, sl, H, oracle.attn_scale(hd))
