@@ -11,7 +11,6 @@
 // from HBM once per decode step.
 #include "gi_common.h"
 #include "gi_kernels.h"
-#include "split_plan.h"
 
 #include <math.h>
 
@@ -104,283 +103,203 @@ __global__ __launch_bounds__(NT) void attn_valu(DecodeArgs a)
     static_assert(TOK % NG == 0, "tile tokens split evenly over P*V groups");
 
     const PoolLayout &L = a.L;
-    const int kvh = blockIdx.y;
+    const int split = blockIdx.x, kvh = blockIdx.y, qrow = blockIdx.z;
+    const int b = qrow / a.n_q, qi = qrow - b * a.n_q;
     const int tid = threadIdx.x;
     const int H = a.num_heads;
     const int h0 = kvh * G;
     const int P = L.page_tokens;
+    int len = a.start_pos ? a.start_pos[b] + qi + 1 : a.seq_lens[b];
+    if (len > a.max_blocks * P || len < 0) {
+        // More tokens than the block table maps (read what it maps), or a
+        // negative length (nothing to read).
+        if (tid == 0 && split == 0 && a.status)
+            atomicOr(a.status, FLAG_BAD_SLOT);
+        len = len < 0 ? 0 : a.max_blocks * P;
+    }
+    // the last split runs to the end of the sequence, so that a length
+    // beyond the one the plan was sized for is still attended in full
+    const int t0 = split * a.split_tokens;
+    const int t1 = split == a.num_splits - 1 ? len : min(len, t0 + a.split_tokens);
+    const int32_t *bt = a.block_tables + (int64_t)b * a.max_blocks;
+    const int64_t qbase = (int64_t)qrow * H;
 
     __shared__ float s_p[G][TOK];
     __shared__ float s_alpha[G];
     __shared__ float s_m[G], s_l[G];
     __shared__ float s_acc[NG][G][HD];
 
-    // decode: the workgroup is a work unit of the plan (split_plan.h) and
-    // walks the segments of its block range; prefill: query row blockIdx.z
-    // whole, one workgroup per (query, kv head)
-    const bool planned = a.plan_units > 0;
-    UnitCursor cur{};
-    if (planned && !plan_unit<NT>(a, blockIdx.x, kvh, blockIdx.x == 0 && blockIdx.y == 0, cur))
-        return;
-    for (;;) {
-        int b, qi, t0, t1, len;
-        Segment seg{};
-        if (planned) {
-            bool unused = false;
-            b = cur.b;
-            qi = 0;
-            len = plan_len(a, b, (int64_t)a.max_blocks * P, unused);
-            seg = plan_segment(cur, len);
-            t0 = seg.t0;
-            t1 = seg.t1;
-        } else {
-            b = blockIdx.z / a.n_q;
-            qi = blockIdx.z - b * a.n_q;
-            len = a.start_pos ? a.start_pos[b] + qi + 1 : a.seq_lens[b];
-            if (len > a.max_blocks * P) {
-                // More tokens than the block table maps: read what it maps.
-                if (tid == 0 && a.status)
-                    atomicOr(a.status, FLAG_BAD_SLOT);
-                len = a.max_blocks * P;
-            }
-            t0 = 0;
-            t1 = len;
-        }
-        const int qrow = b * a.n_q + qi;
-        const int32_t *bt = a.block_tables + (int64_t)b * a.max_blocks;
-        const int64_t qbase = (int64_t)qrow * H;
+    float *wsp = nullptr;
+    if (a.num_splits > 1)
+        wsp = a.ws + (((int64_t)qrow * L.num_kv_heads + kvh) * a.num_splits + split) * (G * (HD + 2));
 
-        // partial slot when the sequence continues outside this unit's range
-        float *wsp = planned && seg.split ? plan_slot(a, cur.unit, seg.slot, kvh, G, HD) : nullptr;
-
-        if (t0 >= t1) {
-            // Empty range (an empty prefill context): zero output.
-            for (int e = tid; e < G * HD; e += NT)
+    if (t0 >= t1) {
+        // Empty split: partial with m = -inf, l = 0 (or zero output when the
+        // whole sequence is empty).
+        for (int e = tid; e < G * HD; e += NT) {
+            if (wsp)
+                wsp[e] = 0.0f;
+            else
                 a.out[(qbase + h0 + e / HD) * HD + e % HD] = 0.0f;
-            break;
         }
+        if (wsp && tid < G) {
+            wsp[G * HD + 2 * tid] = -INFINITY;
+            wsp[G * HD + 2 * tid + 1] = 0.0f;
+        }
+        return;
+    }
 
-        const int part = tid % TPT, tok = tid / TPT, d0 = part * 8;
-        float qr[G][8];
-    #pragma unroll
+    const int part = tid % TPT, tok = tid / TPT, d0 = part * 8;
+    float qr[G][8];
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            qr[g][j] = a.q[(qbase + h0 + g) * HD + d0 + j];
+    if (tid < G) {
+        s_m[tid] = -INFINITY;
+        s_l[tid] = 0.0f;
+    }
+    const int pd = tid % HD, pgp = tid / HD;
+    float acc[G];
+#pragma unroll
+    for (int g = 0; g < G; g++)
+        acc[g] = 0.0f;
+    __syncthreads();
+
+    for (int tb = t0; tb < t1; tb += TOK) {
+        // ---- scores ----
+        const int t = tb + tok;
+        bool valid = t < t1;
+        float ps[G];
+#pragma unroll
         for (int g = 0; g < G; g++)
-    #pragma unroll
-            for (int j = 0; j < 8; j++)
-                qr[g][j] = a.q[(qbase + h0 + g) * HD + d0 + j];
-        if (tid < G) {
-            s_m[tid] = -INFINITY;
-            s_l[tid] = 0.0f;
+            ps[g] = 0.0f;
+        if (valid) {
+            int64_t page = bt[t / P];
+            if (page < 0 || page >= L.num_pages) {
+                if (part == 0 && a.status)
+                    atomicOr(a.status, FLAG_BAD_PAGE);
+                valid = false;
+            } else {
+                float kf[8];
+                load8_k<KT, HD>(a.base + page * L.page_bytes, L, kvh, t % P, d0, kf);
+#pragma unroll
+                for (int g = 0; g < G; g++)
+#pragma unroll
+                    for (int j = 0; j < 8; j++)
+                        ps[g] = fmaf(qr[g][j], kf[j], ps[g]);
+            }
         }
-        const int pd = tid % HD, pgp = tid / HD;
-        float acc[G];
-    #pragma unroll
+#pragma unroll
         for (int g = 0; g < G; g++)
-            acc[g] = 0.0f;
+#pragma unroll
+            for (int m = TPT / 2; m >= 1; m >>= 1)
+                ps[g] += __shfl_xor(ps[g], m, TPT);
+#pragma unroll
+        for (int g = 0; g < G; g++)
+            if (part == g)
+                s_p[g][tok] = valid ? ps[g] * a.scale : -INFINITY;
         __syncthreads();
 
-        for (int tb = t0; tb < t1; tb += TOK) {
-            // ---- scores ----
-            const int t = tb + tok;
-            bool valid = t < t1;
-            float ps[G];
-    #pragma unroll
-            for (int g = 0; g < G; g++)
-                ps[g] = 0.0f;
-            if (valid) {
-                int64_t page = bt[t / P];
-                if (page < 0 || page >= L.num_pages) {
-                    if (part == 0 && a.status)
-                        atomicOr(a.status, FLAG_BAD_PAGE);
-                    valid = false;
-                } else {
-                    float kf[8];
-                    load8_k<KT, HD>(a.base + page * L.page_bytes, L, kvh, t % P, d0, kf);
-    #pragma unroll
+        // ---- online softmax, one thread per (head, token) ----
+        if (tid < G * TOK) {
+            const int g = tid / TOK, tt = tid % TOK;
+            const float sv = s_p[g][tt];
+            float mx = sv;
+#pragma unroll
+            for (int m = TOK / 2; m >= 1; m >>= 1)
+                mx = fmaxf(mx, __shfl_xor(mx, m, TOK));
+            const float m_old = s_m[g];
+            const float m_new = fmaxf(m_old, mx);
+            const float p = sv == -INFINITY ? 0.0f : expf(sv - m_new);
+            float sum = p;
+#pragma unroll
+            for (int m = TOK / 2; m >= 1; m >>= 1)
+                sum += __shfl_xor(sum, m, TOK);
+            s_p[g][tt] = p;
+            if (tt == 0) {
+                const float al = m_old == -INFINITY ? 0.0f : expf(m_old - m_new);
+                s_alpha[g] = al;
+                s_m[g] = m_new;
+                s_l[g] = s_l[g] * al + sum;
+            }
+        }
+        __syncthreads();
+
+        // ---- P * V ----
+#pragma unroll
+        for (int g = 0; g < G; g++)
+            acc[g] *= s_alpha[g];
+        for (int i = 0; i < TPG; i++) {
+            const int tt = pgp * TPG + i;
+            const int t2 = tb + tt;
+            if (t2 < t1) {
+                int64_t page = bt[t2 / P];
+                if (page >= 0 && page < L.num_pages) {
+                    float vv = load_v<KT, HD>(a.base + page * L.page_bytes, L, kvh, pd, t2 % P);
+#pragma unroll
                     for (int g = 0; g < G; g++)
-    #pragma unroll
-                        for (int j = 0; j < 8; j++)
-                            ps[g] = fmaf(qr[g][j], kf[j], ps[g]);
+                        acc[g] = fmaf(s_p[g][tt], vv, acc[g]);
                 }
             }
-    #pragma unroll
-            for (int g = 0; g < G; g++)
-    #pragma unroll
-                for (int m = TPT / 2; m >= 1; m >>= 1)
-                    ps[g] += __shfl_xor(ps[g], m, TPT);
-    #pragma unroll
-            for (int g = 0; g < G; g++)
-                if (part == g)
-                    s_p[g][tok] = valid ? ps[g] * a.scale : -INFINITY;
-            __syncthreads();
-
-            // ---- online softmax, one thread per (head, token) ----
-            if (tid < G * TOK) {
-                const int g = tid / TOK, tt = tid % TOK;
-                const float sv = s_p[g][tt];
-                float mx = sv;
-    #pragma unroll
-                for (int m = TOK / 2; m >= 1; m >>= 1)
-                    mx = fmaxf(mx, __shfl_xor(mx, m, TOK));
-                const float m_old = s_m[g];
-                const float m_new = fmaxf(m_old, mx);
-                const float p = sv == -INFINITY ? 0.0f : expf(sv - m_new);
-                float sum = p;
-    #pragma unroll
-                for (int m = TOK / 2; m >= 1; m >>= 1)
-                    sum += __shfl_xor(sum, m, TOK);
-                s_p[g][tt] = p;
-                if (tt == 0) {
-                    const float al = m_old == -INFINITY ? 0.0f : expf(m_old - m_new);
-                    s_alpha[g] = al;
-                    s_m[g] = m_new;
-                    s_l[g] = s_l[g] * al + sum;
-                }
-            }
-            __syncthreads();
-
-            // ---- P * V ----
-    #pragma unroll
-            for (int g = 0; g < G; g++)
-                acc[g] *= s_alpha[g];
-            for (int i = 0; i < TPG; i++) {
-                const int tt = pgp * TPG + i;
-                const int t2 = tb + tt;
-                if (t2 < t1) {
-                    int64_t page = bt[t2 / P];
-                    if (page >= 0 && page < L.num_pages) {
-                        float vv = load_v<KT, HD>(a.base + page * L.page_bytes, L, kvh, pd, t2 % P);
-    #pragma unroll
-                        for (int g = 0; g < G; g++)
-                            acc[g] = fmaf(s_p[g][tt], vv, acc[g]);
-                    }
-                }
-            }
-            __syncthreads();
         }
-
-    #pragma unroll
-        for (int g = 0; g < G; g++)
-            s_acc[pgp][g][pd] = acc[g];
         __syncthreads();
-        if (tid < HD) {
-    #pragma unroll
-            for (int g = 0; g < G; g++) {
-                float s = 0.0f;
-    #pragma unroll
-                for (int grp = 0; grp < NG; grp++)
-                    s += s_acc[grp][g][pd];
-                if (wsp) {
-                    wsp[g * HD + pd] = s;
-                } else {
-                    const float l = s_l[g];
-                    a.out[(qbase + h0 + g) * HD + pd] = l > 0.0f ? s / l : 0.0f;
-                }
-            }
-            if (wsp && tid < G) {
-                wsp[G * HD + 2 * tid] = s_m[tid];
-                wsp[G * HD + 2 * tid + 1] = s_l[tid];
+    }
+
+#pragma unroll
+    for (int g = 0; g < G; g++)
+        s_acc[pgp][g][pd] = acc[g];
+    __syncthreads();
+    if (tid < HD) {
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            float s = 0.0f;
+#pragma unroll
+            for (int grp = 0; grp < NG; grp++)
+                s += s_acc[grp][g][pd];
+            if (wsp) {
+                wsp[g * HD + pd] = s;
+            } else {
+                const float l = s_l[g];
+                a.out[(qbase + h0 + g) * HD + pd] = l > 0.0f ? s / l : 0.0f;
             }
         }
-        if (planned && seg.split && seg.slot == 1 && kvh == 0 && tid == 0) {
-            // b starts here and continues: merge_splits combines its units
-            plan_desc(a, cur.unit)[0] = b;
-            plan_desc(a, cur.unit)[1] = (cur.sblk + plan_nblk(len) - 1) / cur.cb - cur.unit + 1;
+        if (wsp && tid < G) {
+            wsp[G * HD + 2 * tid] = s_m[tid];
+            wsp[G * HD + 2 * tid + 1] = s_l[tid];
         }
-        if (!planned || !plan_next(a, cur, plan_nblk(len)))
-            break;
-        __syncthreads(); // the shared arrays are free for the next segment
     }
 }
 
-// Combines the partials of split sequences (split_plan.h):
-//   out = sum_s acc_s e^(m_s - M) / sum_s l_s e^(m_s - M),  M = max_s m_s,
-// summed in unit order (so the result does not depend on scheduling).  One
-// workgroup per (kv head, unit): unit u's descriptor names the sequence that
-// starts in its range and continues (its partials: slot 1 of unit u, then
-// slot 0 of the next n - 1 units); other workgroups exit at once.  Thread g
-// first takes head g's maximum and denominator; the per-split factors then
-// go through LDS, so that every thread issues its partial loads together.
-constexpr int kMergePass = 32; // splits per pass
-__global__ __launch_bounds__(256) void merge_splits(DecodeArgs a)
+// Merges split partials: out = sum_s acc_s e^(m_s - M) / sum_s l_s e^(m_s - M).
+// One workgroup per (query row, head), one thread per output dimension.
+__global__ __launch_bounds__(256) void merge_splits(float *__restrict__ out,
+                                                    const float *__restrict__ ws, int H, int KVH,
+                                                    int HD, int splits)
 {
-    const int kvh = blockIdx.x, u0 = blockIdx.y, tid = threadIdx.x;
-    const int b = plan_desc(a, u0)[0], n = plan_desc(a, u0)[1];
-    if (b < 0 || n <= 1)
-        return;
-    const int HD = a.L.head_dim, G = a.num_heads / a.L.num_kv_heads;
-    float *out = a.out + ((int64_t)b * a.num_heads + kvh * G) * HD;
-    // partial s: slot 1 of unit u0, then slot 0 of units u0 + 1 ..
-    auto part = [&](int s) -> const float * {
-        return s == 0 ? plan_slot(a, u0, 1, kvh, G, HD) : plan_slot(a, u0 + s, 0, kvh, G, HD);
-    };
-    __shared__ float s_f[kMergePass][16]; // e^(m_s - M) of head g
-    __shared__ float s_M[16], s_den[16];
-    if (tid < G) {
-        float M = -INFINITY;
-        for (int s0 = 0; s0 < n; s0 += 8) {
-            float m[8];
-#pragma unroll
-            for (int i = 0; i < 8; i++)
-                m[i] = s0 + i < n ? part(s0 + i)[G * HD + 2 * tid] : -INFINITY;
-#pragma unroll
-            for (int i = 0; i < 8; i++)
-                M = fmaxf(M, m[i]);
-        }
-        float den = 0.0f;
+    const int h = blockIdx.x, qrow = blockIdx.y;
+    const int G = H / KVH;
+    const int kvh = h / G, g = h - kvh * G;
+    const int64_t stride = (int64_t)G * (HD + 2);
+    const float *w0 = ws + ((int64_t)qrow * KVH + kvh) * splits * stride;
+    float M = -INFINITY;
+    for (int s = 0; s < splits; s++)
+        M = fmaxf(M, w0[s * stride + G * HD + 2 * g]);
+    for (int d = threadIdx.x; d < HD; d += blockDim.x) {
+        float num = 0.0f, den = 0.0f;
         if (M != -INFINITY) {
-            for (int s0 = 0; s0 < n; s0 += 8) {
-                float m[8], l[8];
-#pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    m[i] = s0 + i < n ? part(s0 + i)[G * HD + 2 * tid] : -INFINITY;
-                    l[i] = s0 + i < n ? part(s0 + i)[G * HD + 2 * tid + 1] : 0.0f;
-                }
-#pragma unroll
-                for (int i = 0; i < 8; i++)
-                    if (m[i] != -INFINITY)
-                        den = fmaf(l[i], expf(m[i] - M), den);
+            for (int s = 0; s < splits; s++) {
+                const float *w = w0 + s * stride;
+                const float m = w[G * HD + 2 * g];
+                if (m == -INFINITY)
+                    continue;
+                const float f = expf(m - M);
+                num = fmaf(w[g * HD + d], f, num);
+                den = fmaf(w[G * HD + 2 * g + 1], f, den);
             }
         }
-        s_M[tid] = M;
-        s_den[tid] = den;
-    }
-    // outputs of this thread: e = tid + 256 i < G * HD (G * HD <= 2048)
-    float num[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-    for (int s0 = 0; s0 < n; s0 += kMergePass) {
-        const int ns = min(kMergePass, n - s0);
-        __syncthreads(); // s_M is set, and s_f is free again
-        for (int e = tid; e < ns * G; e += 256) {
-            const int s = e / G, g = e - s * G;
-            const float M = s_M[g], m = part(s0 + s)[G * HD + 2 * g];
-            s_f[s][g] = (M == -INFINITY || m == -INFINITY) ? 0.0f : expf(m - M);
-        }
-        __syncthreads();
-        for (int s1 = 0; s1 < ns; s1 += 8) {
-            float v[8][8];
-#pragma unroll
-            for (int k = 0; k < 8; k++)
-#pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    const int e = tid + 256 * i;
-                    v[k][i] = s1 + k < ns && e < G * HD ? part(s0 + s1 + k)[e] : 0.0f;
-                }
-#pragma unroll
-            for (int k = 0; k < 8; k++)
-#pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    const int e = tid + 256 * i;
-                    if (s1 + k < ns && e < G * HD)
-                        num[i] = fmaf(v[k][i], s_f[s1 + k][e / HD], num[i]);
-                }
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const int e = tid + 256 * i;
-        if (e < G * HD) {
-            const float den = s_den[e / HD];
-            out[e] = den > 0.0f ? num[i] / den : 0.0f;
-        }
+        out[((int64_t)qrow * H + h) * HD + d] = den > 0.0f ? num / den : 0.0f;
     }
 }
 
@@ -402,34 +321,50 @@ hipError_t launch_valu_kt(const DecodeArgs &a, dim3 grid, hipStream_t st)
 
 } // namespace
 
-void decode_plan(const PoolLayout &L, int num_cus, int max_len, DecodeArgs &a)
+size_t decode_workspace_bytes(const PoolLayout &L, int batch, int num_heads, int num_splits)
 {
-    // work units (workgroups) per kv head: kDecodeWgPerCu per CU over the kv
-    // heads, fewer when max_len (a hint: 0 when unknown) shows a smaller
-    // stream, so that no unit is planned below kMinUnitBlocks blocks.  A
-    // wrong hint only changes the balance: the kernels size their ranges from
-    // the lengths in device memory.
-    int wg = (kDecodeWgPerCu * (num_cus > 0 ? num_cus : 256) + L.num_kv_heads - 1) / L.num_kv_heads;
-    if (max_len > 0) {
-        const int64_t blocks = (int64_t)a.batch * ((max_len + kPlanBlock - 1) / kPlanBlock);
-        const int64_t need = (blocks + kMinUnitBlocks - 1) / kMinUnitBlocks;
-        if (need < wg)
-            wg = (int)(need > 0 ? need : 1);
-    }
-    a.plan_units = wg;
-}
-
-int decode_grid_items(const DecodeArgs &a) { return a.plan_units; }
-
-size_t decode_desc_offset(const PoolLayout &L, int num_heads, int plan_units)
-{
+    if (num_splits <= 1)
+        return 0;
     const int G = num_heads / L.num_kv_heads;
-    return ((size_t)2 * plan_units * L.num_kv_heads * G * (L.head_dim + 2) * sizeof(float) + 255) / 256 * 256;
+    return (size_t)batch * L.num_kv_heads * num_splits * G * (L.head_dim + 2) * sizeof(float);
 }
 
-size_t decode_workspace_bytes(const PoolLayout &L, int num_heads, int plan_units)
+// Split-K planning: enough (split, kv head, sequence) workgroups for about
+// kDecodeWgPerCu per CU, each split at least kDecodeMinSplit tokens.
+// Measured on MI355X: 2 and 1024 beat finer splits (4/512, 8/256, 16/128) on
+// both 32 ragged sequences of 512-4096 tokens and 8 sequences of 32768, since
+// every workgroup pays a fixed cost (query load, cross-wave merge, partials).
+// A plan that balances equal token ranges over all workgroups regardless of
+// sequence boundaries (with partial slots per range and a merge per
+// sequence) measured 2-10% slower on long and uniform batches and only 5%
+// faster on ragged ones.
+constexpr int kDecodeWgPerCu = 2;
+constexpr int kDecodeMinSplit = 1024;
+
+void decode_plan(const PoolLayout &L, int batch, int num_heads, int max_len, int num_cus,
+                 int *split_tokens, int *num_splits)
 {
-    return decode_desc_offset(L, num_heads, plan_units) + (size_t)2 * plan_units * sizeof(int);
+    (void)num_heads;
+    // Split unit: whole page pairs and a multiple of 64 tokens.
+    int unit = 2 * L.page_tokens;
+    while (unit % 64)
+        unit += 2 * L.page_tokens;
+    if (max_len < 1)
+        max_len = 1;
+    const int64_t pairs = (int64_t)batch * L.num_kv_heads;
+    const int64_t target = (int64_t)kDecodeWgPerCu * (num_cus > 0 ? num_cus : 256);
+    int splits = (int)((target + pairs - 1) / pairs);
+    // A minimum of tokens per split keeps the merge negligible.
+    int max_splits = (max_len + kDecodeMinSplit - 1) / kDecodeMinSplit;
+    if (splits > max_splits)
+        splits = max_splits;
+    if (splits < 1)
+        splits = 1;
+    int per = (max_len + splits - 1) / splits;
+    per = (per + unit - 1) / unit * unit;
+    splits = (max_len + per - 1) / per;
+    *split_tokens = per;
+    *num_splits = splits;
 }
 
 int decode_kernel_kind(const PoolLayout &L, int num_heads, int requested)
@@ -447,11 +382,10 @@ hipError_t launch_decode(const DecodeArgs &a, hipStream_t st)
         return hipErrorInvalidValue;
     const int n_q = a.n_q > 0 ? a.n_q : 1;
     hipError_t e;
-    if (a.plan_units > 0 && n_q == 1 && !a.start_pos && decode_kernel_kind(L, a.num_heads, a.kernel) == 1) {
+    if (n_q == 1 && !a.start_pos && decode_kernel_kind(L, a.num_heads, a.kernel) == 1) {
         e = launch_decode_mfma(a, st);
     } else {
-        dim3 grid = a.plan_units > 0 ? dim3(decode_grid_items(a), L.num_kv_heads, 1)
-                                     : dim3(1, L.num_kv_heads, a.batch * n_q);
+        dim3 grid(a.num_splits, L.num_kv_heads, a.batch * n_q);
         switch (L.kv_type) {
         case KV_F32: e = launch_valu_kt<KV_F32>(a, grid, st); break;
         case KV_F16: e = launch_valu_kt<KV_F16>(a, grid, st); break;
@@ -459,10 +393,10 @@ hipError_t launch_decode(const DecodeArgs &a, hipStream_t st)
         default: e = launch_valu_kt<KV_Q8_0>(a, grid, st); break;
         }
     }
-    // one unit per kv head covers the whole stream: nothing is split
-    if (e != hipSuccess || a.plan_units <= 1)
+    if (e != hipSuccess || a.num_splits <= 1)
         return e;
-    hipLaunchKernelGGL(merge_splits, dim3(L.num_kv_heads, a.plan_units), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(merge_splits, dim3(a.num_heads, a.batch * n_q), dim3(min(L.head_dim, 256)),
+                       0, st, a.out, a.ws, a.num_heads, L.num_kv_heads, L.head_dim, a.num_splits);
     return hipGetLastError();
 }
 
@@ -485,11 +419,13 @@ hipError_t launch_prefill(const PrefillArgs &p, hipStream_t st)
     a.start_pos = p.start_pos;
     a.num_heads = p.num_heads;
     a.scale = p.scale;
-    a.plan_units = 0; // one workgroup per (query, kv head), no split
+    a.split_tokens = 1 << 30;
+    a.num_splits = 1;
     a.ws = nullptr;
-    a.plan_desc = nullptr;
     a.status = p.status;
     a.kernel = 0;
+    if (p.chunk_len <= 0 || p.batch <= 0)
+        return hipSuccess;
     return launch_decode(a, st);
 }
 

@@ -38,7 +38,6 @@
 #include "gi_common.h"
 #include "gi_kernels.h"
 #include "mfma_ops.h"
-#include "split_plan.h"
 
 #include <math.h>
 
@@ -57,11 +56,6 @@ typedef uint16_t us2 __attribute__((ext_vector_type(2)));
 // Cache policy of the direct global->LDS loads (2: non-temporal, which
 // measured slower for q8_0 pages and within noise for q4_0).
 constexpr int kDecodeLdsAux = 0;
-
-// Grid order of the decode launch: (units, kv heads), so that consecutive
-// workgroups (dealt round-robin to the 8 XCDs) take consecutive ranges of one
-// kv head.
-constexpr bool kDecodeGridKvFirst = false;
 
 namespace mfma_decode {
 
@@ -965,11 +959,8 @@ __device__ __forceinline__ void softmax_pv_q(f4 s0, f4 s1, QBlock<KT, HD> &B, in
     }
 }
 
-// Body of the decode kernels.  KT: KV_F16, or KV_Q8_0 / KV_Q4_0 / KV_F32
-// (packed GP only).  The workgroup is a work unit of the plan (split_plan.h):
-// it walks the segments of its block range one sequence at a time, its four
-// waves taking every fourth 32-token block of a segment, and finishes each
-// segment by merging the waves' states through LDS.
+// Body of the decode kernels.  KT: KV_F16, or KV_Q8_0 / KV_Q4_0 (packed GP
+// only).
 template <int KT, int HD, int GP, bool NT, bool PREFETCH>
 __device__ __forceinline__ void decode_body(const DecodeArgs &a)
 {
@@ -978,12 +969,25 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
     constexpr bool F32 = KT == KV_F32;
     static_assert(!(QUANT || F32) || GP != 0, "quantised and f32 pages use the packed hi/lo form");
     const PoolLayout &L = a.L;
-    const int kvh = kDecodeGridKvFirst ? blockIdx.x : blockIdx.y;
-    const int unit = kDecodeGridKvFirst ? blockIdx.y : blockIdx.x;
+    const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int j = lane & 15, g = lane >> 4;
-    const int H = a.num_heads, G = H / L.num_kv_heads, P = L.page_tokens;
+    const int H = a.num_heads, KVH = L.num_kv_heads, G = H / KVH, P = L.page_tokens;
     const int h0 = kvh * G;
+    int len = a.seq_lens[b];
+    if (len > a.max_blocks * P || len < 0) {
+        // more tokens than the block table maps (read what it maps), or a
+        // negative length (nothing to read)
+        if (threadIdx.x == 0 && split == 0 && a.status)
+            atomicOr(a.status, FLAG_BAD_SLOT);
+        len = len < 0 ? 0 : a.max_blocks * P;
+    }
+    // the last split runs to the end of the sequence, so that a length
+    // beyond the one the plan was sized for is still attended in full
+    const int t0 = split * a.split_tokens;
+    const int t1 = split == a.num_splits - 1 ? len : min(len, t0 + a.split_tokens);
+    const int64_t qrow = (int64_t)b * H + h0;
+
     // The per-wave staging areas of the block loop (quantised pages) and,
     // after it, the cross-wave merge share one LDS allocation.  (fp16 pages
     // load straight into registers: staging them through LDS measured
@@ -995,9 +999,23 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
     float(*s_o)[16][HD] = reinterpret_cast<float(*)[16][HD]>(s_stage);
     __shared__ float s_m[4][16], s_l[4][16];
 
-    UnitCursor cur;
-    if (!plan_unit<256>(a, unit, kvh, blockIdx.x == 0 && blockIdx.y == 0, cur))
-        return; // this workgroup's range is past the end of the stream
+    float *wsp = nullptr;
+    if (a.num_splits > 1)
+        wsp = a.ws + (((int64_t)b * KVH + kvh) * a.num_splits + split) * (G * (HD + 2));
+
+    if (t0 >= t1) {
+        for (int e = threadIdx.x; e < G * HD; e += 256) {
+            if (wsp)
+                wsp[e] = 0.0f;
+            else
+                a.out[qrow * HD + e] = 0.0f;
+        }
+        if (wsp && threadIdx.x < G) {
+            wsp[G * HD + 2 * threadIdx.x] = -INFINITY;
+            wsp[G * HD + 2 * threadIdx.x + 1] = 0.0f;
+        }
+        return;
+    }
 
     // Q^T operand: column j = head h0 + j (zero beyond the group), k-slot
     // (g, v) of step kk = dimension 32*kk + 8*g + v.
@@ -1008,11 +1026,11 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
     // Each head's query is scaled by 2^qe (from its largest |q|) so both fp16
     // halves stay normal, and the scores are scaled back through c.  The hi
     // and lo columns of a head see the same values, so they pick the same qe.
-    // (Loaded by load_q once the wave's first block of a segment is in
-    // flight, so that the two memory round trips overlap.)
+    // (Loaded by load_q once the wave's first block is in flight, so that the
+    // two memory round trips overlap.)
     h8 qh[KK], ql[KK];
     float c = 0.0f;
-    auto load_q = [&](int64_t qrow) {
+    auto load_q = [&]() {
         float qv[KK][8];
         float mq = 0.0f;
         const float *qp = a.q + (qrow + qhead) * HD + 8 * g;
@@ -1050,157 +1068,63 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
             }
         c = a.scale * kLog2e * ldexpf(1.0f, -qe);
     };
+    State<HD> S;
+    S.m2 = -INFINITY;
+    S.lsum = 0.0f;
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++)
+        S.o[nb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    float ksc = 0.0f, vsc = 0.0f; // f32 pages: running K / V operand scales
     const float neg1 = mfma_ops::opaque_neg1(); // f32 pages: for split_pair
+    float vnorm = 0.0f; // quantised pages: running power-of-two cap of the V scales
 
     // bytes per stored element: fp16 2, q8_0 1, q4_0 1/2
     constexpr int EB_NUM = F32 ? 4 : KT == KV_F16 ? 2 : 1, EB_DEN = KT == KV_Q4_0 ? 2 : 1;
     const int64_t koff = L.k_off + (int64_t)kvh * P * HD * EB_NUM / EB_DEN;
     const int64_t voff = L.v_off + (int64_t)kvh * HD * P * EB_NUM / EB_DEN;
-    const int64_t cap = (int64_t)a.max_blocks * P;
-    for (;;) {
-        bool unused = false;
-        const int b = __builtin_amdgcn_readfirstlane(cur.b); // scalar: see plan_uniform
-        const int len = plan_len(a, b, cap, unused);
-        const Segment seg = plan_segment(cur, len);
-        const int t1 = seg.t1;
-        const int64_t qrow = (int64_t)b * H + h0;
-        const int32_t *bt = a.block_tables + (int64_t)b * a.max_blocks;
-        // partial slot when the sequence continues outside this unit's range
-        float *wsp = seg.split ? plan_slot(a, cur.unit, seg.slot, kvh, G, HD) : nullptr;
-        State<HD> S;
-        S.m2 = -INFINITY;
-        S.lsum = 0.0f;
-#pragma unroll
-        for (int nb = 0; nb < NB; nb++)
-            S.o[nb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-        float ksc = 0.0f, vsc = 0.0f; // f32 pages: running K / V operand scales
-        float vnorm = 0.0f;           // quantised pages: running power-of-two cap of the V scales
+    const int32_t *bt = a.block_tables + (int64_t)b * a.max_blocks;
+    const int stride = 32 * 4;
 
-        const int stride = 32 * 4;
-        // Block starts are wave-uniform (scalar registers), so the loop test is a
-        // scalar branch.  Every block but the last runs inside the loop, where
-        // the next block's loads are issued unconditionally (K once this block's
-        // scores exist, V once its P*V has consumed the V registers): the wait
-        // counters then see one pattern of loads in flight on every path, and a
-        // wait for this block's V never waits for the next block's K.
-        int base = __builtin_amdgcn_readfirstlane(seg.t0 + 32 * w);
-        if constexpr (QUANT) {
-            const int64_t ksoff = L.ks_off + (int64_t)kvh * P * KK * 2;
-            const int64_t vsoff = L.vs_off + (int64_t)kvh * KK * P * 2;
-            if (base < t1) {
-                QStage<KT, HD> &Sq = reinterpret_cast<QStage<KT, HD> *>(s_stage)[w];
-                int64_t pA, pB;
-                int sA, sB;
-                int ok;
-                block_pages(a, bt, base, t1, pA, pB, sA, sB, ok);
-                issue_q<KT, HD>(a, pA, pB, sA, sB, koff, ksoff, voff, vsoff, lane, Sq);
-                load_q(qrow);
-                for (;;) {
-                    QBlock<KT, HD> B;
-                    // the only vector loads in flight are this block's
-                    __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0)
-                    read_q<KT, HD>(Sq, j, g, B);
-                    const int next = base + stride;
-                    const bool more = next < t1;
-                    int64_t nA = pA, nB = pB;
-                    int nsA = sA, nsB = sB;
-                    int nok = ok;
-                    if (more) {
-                        block_pages(a, bt, next, t1, nA, nB, nsA, nsB, nok);
-                        // every read of this block has returned before its
-                        // slots are refilled
-                        __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0)
-                        issue_q<KT, HD>(a, nA, nB, nsA, nsB, koff, ksoff, voff, vsoff, lane, Sq);
-                    }
-                    f4 s0, s1;
-                    qk_q<KT, HD, GP>(B, qh, g, s0, s1);
-                    softmax_pv_q<KT, HD, GP>(s0, s1, B, base, ok, t1, j, g, c, S, vnorm);
-                    if (!more)
-                        break;
-                    pA = nA;
-                    pB = nB;
-                    sA = nsA;
-                    sB = nsB;
-                    ok = nok;
-                    base = next;
-                }
-            }
-        } else if constexpr (F32) {
-            if (base < t1) {
-                F32Stage<HD> &Sf = reinterpret_cast<F32Stage<HD> *>(s_stage)[w];
-                const F32Lanes fl = f32_lanes<HD>(lane, P);
-                int64_t pA, pB;
-                int sA, sB;
-                int ok;
-                block_pages(a, bt, base, t1, pA, pB, sA, sB, ok);
-                issue_f32<HD>(a, pA, pB, sA, sB, koff, voff, fl, Sf);
-                load_q(qrow);
-                for (;;) {
-                    h8 kh0[KK], kh1[KK], kl0[KK], kl1[KK], vh[NB], vl[NB];
-                    // the only vector loads in flight are this block's
-                    __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0)
-                    read_f32<HD>(Sf, j, g, base, ok, t1, kh0, kh1, kl0, kl1, vh, vl, ksc, vsc, S, neg1);
-                    const int next = base + stride;
-                    const bool more = next < t1;
-                    int64_t nA = pA, nB = pB;
-                    int nsA = sA, nsB = sB;
-                    int nok = ok;
-                    if (more) {
-                        block_pages(a, bt, next, t1, nA, nB, nsA, nsB, nok);
-                        __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0): this block's reads returned
-                        issue_f32<HD>(a, nA, nB, nsA, nsB, koff, voff, fl, Sf);
-                    }
-                    // S = (kh + kl) . (q_hi | q_lo): two products per k-step
-                    f4 s0 = f4{0.0f, 0.0f, 0.0f, 0.0f}, s1 = f4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                    for (int kk = 0; kk < KK; kk++) {
-                        s0 = mfma(kh0[kk], qh[kk], s0);
-                        s1 = mfma(kh1[kk], qh[kk], s1);
-                        s0 = mfma(kl0[kk], qh[kk], s0);
-                        s1 = mfma(kl1[kk], qh[kk], s1);
-                    }
-#pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        s0[r] += mirror<GP>(s0[r]);
-                        s1[r] += mirror<GP>(s1[r]);
-                    }
-                    softmax_pv<HD, GP, true>(s0, s1, vh, base, ok, t1, j, g, c * pow2_recip(ksc), S, vl);
-                    if (!more)
-                        break;
-                    pA = nA;
-                    pB = nB;
-                    sA = nsA;
-                    sB = nsB;
-                    ok = nok;
-                    base = next;
-                }
-            }
-        } else if (base < t1) {
-            h8 k0[KK], k1[KK], v[NB];
+    // Block starts are wave-uniform (scalar registers), so the loop test is a
+    // scalar branch.  Every block but the last runs inside the loop, where
+    // the next block's loads are issued unconditionally (K once this block's
+    // scores exist, V once its P*V has consumed the V registers): the wait
+    // counters then see one pattern of loads in flight on every path, and a
+    // wait for this block's V never waits for the next block's K.
+    int base = __builtin_amdgcn_readfirstlane(t0 + 32 * w);
+    if constexpr (QUANT) {
+        const int64_t ksoff = L.ks_off + (int64_t)kvh * P * KK * 2;
+        const int64_t vsoff = L.vs_off + (int64_t)kvh * KK * P * 2;
+        if (base < t1) {
+            QStage<KT, HD> &Sq = reinterpret_cast<QStage<KT, HD> *>(s_stage)[w];
             int64_t pA, pB;
             int sA, sB;
             int ok;
             block_pages(a, bt, base, t1, pA, pB, sA, sB, ok);
-            load_k<HD, NT>(a, pA, pB, sA, sB, koff, j, g, k0, k1);
-            load_v<HD, NT>(a, pA, pB, sA, sB, voff, j, g, v);
-            load_q(qrow);
-            f4 s0, s1;
+            issue_q<KT, HD>(a, pA, pB, sA, sB, koff, ksoff, voff, vsoff, lane, Sq);
+            load_q();
             for (;;) {
-                qk<HD, GP>(k0, k1, qh, ql, s0, s1);
+                QBlock<KT, HD> B;
+                // the only vector loads in flight are this block's
+                __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0)
+                read_q<KT, HD>(Sq, j, g, B);
                 const int next = base + stride;
-                if (next >= t1)
+                const bool more = next < t1;
+                int64_t nA = pA, nB = pB;
+                int nsA = sA, nsB = sB;
+                int nok = ok;
+                if (more) {
+                    block_pages(a, bt, next, t1, nA, nB, nsA, nsB, nok);
+                    // every read of this block has returned before its
+                    // slots are refilled
+                    __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0)
+                    issue_q<KT, HD>(a, nA, nB, nsA, nsB, koff, ksoff, voff, vsoff, lane, Sq);
+                }
+                f4 s0, s1;
+                qk_q<KT, HD, GP>(B, qh, g, s0, s1);
+                softmax_pv_q<KT, HD, GP>(s0, s1, B, base, ok, t1, j, g, c, S, vnorm);
+                if (!more)
                     break;
-                int64_t nA, nB;
-                int nsA, nsB;
-                int nok;
-                block_pages(a, bt, next, t1, nA, nB, nsA, nsB, nok);
-                if (PREFETCH)
-                    load_k<HD, NT>(a, nA, nB, nsA, nsB, koff, j, g, k0, k1);
-                softmax_pv<HD, GP>(s0, s1, v, base, ok, t1, j, g, c, S);
-                if (!PREFETCH)
-                    load_k<HD, NT>(a, nA, nB, nsA, nsB, koff, j, g, k0, k1);
-                __builtin_amdgcn_sched_barrier(0);
-                load_v<HD, NT>(a, nA, nB, nsA, nsB, voff, j, g, v);
                 pA = nA;
                 pB = nB;
                 sA = nsA;
@@ -1208,77 +1132,152 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
                 ok = nok;
                 base = next;
             }
+        }
+    } else if constexpr (F32) {
+        if (base < t1) {
+            F32Stage<HD> &Sf = reinterpret_cast<F32Stage<HD> *>(s_stage)[w];
+            const F32Lanes fl = f32_lanes<HD>(lane, P);
+            int64_t pA, pB;
+            int sA, sB;
+            int ok;
+            block_pages(a, bt, base, t1, pA, pB, sA, sB, ok);
+            issue_f32<HD>(a, pA, pB, sA, sB, koff, voff, fl, Sf);
+            load_q();
+            for (;;) {
+                h8 kh0[KK], kh1[KK], kl0[KK], kl1[KK], vh[NB], vl[NB];
+                // the only vector loads in flight are this block's
+                __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0)
+                read_f32<HD>(Sf, j, g, base, ok, t1, kh0, kh1, kl0, kl1, vh, vl, ksc, vsc, S, neg1);
+                const int next = base + stride;
+                const bool more = next < t1;
+                int64_t nA = pA, nB = pB;
+                int nsA = sA, nsB = sB;
+                int nok = ok;
+                if (more) {
+                    block_pages(a, bt, next, t1, nA, nB, nsA, nsB, nok);
+                    __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0): this block's reads returned
+                    issue_f32<HD>(a, nA, nB, nsA, nsB, koff, voff, fl, Sf);
+                }
+                // S = (kh + kl) . (q_hi | q_lo): two products per k-step
+                f4 s0 = f4{0.0f, 0.0f, 0.0f, 0.0f}, s1 = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int kk = 0; kk < KK; kk++) {
+                    s0 = mfma(kh0[kk], qh[kk], s0);
+                    s1 = mfma(kh1[kk], qh[kk], s1);
+                    s0 = mfma(kl0[kk], qh[kk], s0);
+                    s1 = mfma(kl1[kk], qh[kk], s1);
+                }
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    s0[r] += mirror<GP>(s0[r]);
+                    s1[r] += mirror<GP>(s1[r]);
+                }
+                softmax_pv<HD, GP, true>(s0, s1, vh, base, ok, t1, j, g, c * pow2_recip(ksc), S, vl);
+                if (!more)
+                    break;
+                pA = nA;
+                pB = nB;
+                sA = nsA;
+                sB = nsB;
+                ok = nok;
+                base = next;
+            }
+        }
+    } else if (base < t1) {
+        h8 k0[KK], k1[KK], v[NB];
+        int64_t pA, pB;
+        int sA, sB;
+        int ok;
+        block_pages(a, bt, base, t1, pA, pB, sA, sB, ok);
+        load_k<HD, NT>(a, pA, pB, sA, sB, koff, j, g, k0, k1);
+        load_v<HD, NT>(a, pA, pB, sA, sB, voff, j, g, v);
+        load_q();
+        f4 s0, s1;
+        for (;;) {
+            qk<HD, GP>(k0, k1, qh, ql, s0, s1);
+            const int next = base + stride;
+            if (next >= t1)
+                break;
+            int64_t nA, nB;
+            int nsA, nsB;
+            int nok;
+            block_pages(a, bt, next, t1, nA, nB, nsA, nsB, nok);
+            if (PREFETCH)
+                load_k<HD, NT>(a, nA, nB, nsA, nsB, koff, j, g, k0, k1);
             softmax_pv<HD, GP>(s0, s1, v, base, ok, t1, j, g, c, S);
+            if (!PREFETCH)
+                load_k<HD, NT>(a, nA, nB, nsA, nsB, koff, j, g, k0, k1);
+            __builtin_amdgcn_sched_barrier(0);
+            load_v<HD, NT>(a, nA, nB, nsA, nsB, voff, j, g, v);
+            pA = nA;
+            pB = nB;
+            sA = nsA;
+            sB = nsB;
+            ok = nok;
+            base = next;
         }
+        softmax_pv<HD, GP>(s0, s1, v, base, ok, t1, j, g, c, S);
+    }
 
-        // every wave is done with its staging area before the merge reuses it
-        __syncthreads();
-        // wave totals -> LDS
-        float lt = S.lsum;
-        if constexpr (QUANT && GP == 4)
-            lt += xor8(lt); // the compact softmax splits a column over lanes j, j + 8
-        lt += __shfl_xor(lt, 16);
-        lt += __shfl_xor(lt, 32);
-        if (g == 0) {
-            s_m[w][j] = S.m2;
-            s_l[w][j] = lt;
-        }
+    // every wave is done with its staging area before the merge reuses it
+    __syncthreads();
+    // wave totals -> LDS
+    float lt = S.lsum;
+    if constexpr (QUANT && GP == 4)
+        lt += xor8(lt); // the compact softmax splits a column over lanes j, j + 8
+    lt += __shfl_xor(lt, 16);
+    lt += __shfl_xor(lt, 32);
+    if (g == 0) {
+        s_m[w][j] = S.m2;
+        s_l[w][j] = lt;
+    }
 #pragma unroll
-        for (int nb = 0; nb < NB; nb++)
+    for (int nb = 0; nb < NB; nb++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                float o = S.o[nb][r];
-                if constexpr (QUANT) {
-                    // rows G .. 2G-1 hold lo halves carrying 2^11; every row
-                    // holds O / vnorm of its dimension block
-                    const int row = 4 * g + r;
-                    o *= vnorm * (row >= G && row < 2 * G ? 1.0f / 2048.0f : 1.0f) *
-                         (KT == KV_Q4_0 && (nb & 1) ? 0.0625f : 1.0f);
-                }
-                if constexpr (F32) {
-                    // the accumulators hold O times the wave's V scale
-                    if (vsc != 0.0f)
-                        o *= pow2_recip(vsc);
-                }
-                s_o[w][4 * g + r][16 * nb + j] = o;
+        for (int r = 0; r < 4; r++) {
+            float o = S.o[nb][r];
+            if constexpr (QUANT) {
+                // rows G .. 2G-1 hold lo halves carrying 2^11; every row
+                // holds O / vnorm of its dimension block
+                const int row = 4 * g + r;
+                o *= vnorm * (row >= G && row < 2 * G ? 1.0f / 2048.0f : 1.0f) *
+                     (KT == KV_Q4_0 && (nb & 1) ? 0.0625f : 1.0f);
             }
-        __syncthreads();
+            if constexpr (F32) {
+                // the accumulators hold O times the wave's V scale
+                if (vsc != 0.0f)
+                    o *= pow2_recip(vsc);
+            }
+            s_o[w][4 * g + r][16 * nb + j] = o;
+        }
+    __syncthreads();
 
-        for (int e = threadIdx.x; e < G * HD; e += 256) {
-            const int hh = e / HD, d = e - hh * HD;
-            float M = s_m[0][hh];
+    for (int e = threadIdx.x; e < G * HD; e += 256) {
+        const int hh = e / HD, d = e - hh * HD;
+        float M = s_m[0][hh];
 #pragma unroll
-            for (int x = 1; x < 4; x++)
-                M = fmaxf(M, s_m[x][hh]);
-            float num = 0.0f, den = 0.0f;
+        for (int x = 1; x < 4; x++)
+            M = fmaxf(M, s_m[x][hh]);
+        float num = 0.0f, den = 0.0f;
 #pragma unroll
-            for (int x = 0; x < 4; x++) {
-                const float mx2 = s_m[x][hh];
-                const float f = mx2 == -INFINITY ? 0.0f : exp2f(mx2 - M);
-                float o = s_o[x][hh][d];
-                if (GP != 0)
-                    o += s_o[x][2 * G - 1 - hh][d];
-                num = fmaf(o, f, num);
-                den = fmaf(s_l[x][hh], f, den);
-            }
-            if (wsp) {
-                wsp[hh * HD + d] = num;
-                if (d == 0) {
-                    wsp[G * HD + 2 * hh] = M * (1.0f / kLog2e);
-                    wsp[G * HD + 2 * hh + 1] = den;
-                }
-            } else {
-                a.out[(qrow + hh) * HD + d] = den > 0.0f ? num / den : 0.0f;
-            }
+        for (int x = 0; x < 4; x++) {
+            const float mx2 = s_m[x][hh];
+            const float f = mx2 == -INFINITY ? 0.0f : exp2f(mx2 - M);
+            float o = s_o[x][hh][d];
+            if (GP != 0)
+                o += s_o[x][2 * G - 1 - hh][d];
+            num = fmaf(o, f, num);
+            den = fmaf(s_l[x][hh], f, den);
         }
-        if (seg.split && seg.slot == 1 && kvh == 0 && threadIdx.x == 0) {
-            // b starts here and continues: merge_splits combines its units
-            plan_desc(a, cur.unit)[0] = b;
-            plan_desc(a, cur.unit)[1] = (cur.sblk + plan_nblk(len) - 1) / cur.cb - cur.unit + 1;
+        if (wsp) {
+            wsp[hh * HD + d] = num;
+            if (d == 0) {
+                wsp[G * HD + 2 * hh] = M * (1.0f / kLog2e);
+                wsp[G * HD + 2 * hh + 1] = den;
+            }
+        } else {
+            a.out[(qrow + hh) * HD + d] = den > 0.0f ? num / den : 0.0f;
         }
-        if (!plan_next(a, cur, plan_nblk(len)))
-            break;
-        __syncthreads(); // the merge rows are read before the next segment's staging
     }
 }
 
@@ -1388,9 +1387,7 @@ static void launch_mfma_g(const DecodeArgs &a, dim3 grid, hipStream_t st)
 
 hipError_t launch_decode_mfma(const DecodeArgs &a, hipStream_t st)
 {
-    // one workgroup per (kv head, unit)
-    const dim3 grid = kDecodeGridKvFirst ? dim3(a.L.num_kv_heads, decode_grid_items(a), 1)
-                                         : dim3(decode_grid_items(a), a.L.num_kv_heads, 1);
+    dim3 grid(a.num_splits, a.L.num_kv_heads, a.batch);
     const bool h128 = a.L.head_dim == 128;
     switch (a.L.kv_type) {
     case KV_Q8_0:

@@ -46,11 +46,9 @@ hipError_t launch_copy_pages(const PoolLayout &L, uint8_t *const *layer_base, in
 
 // Attention over paged context.  Decode: q/out are [batch][num_heads][head_dim]
 // float32, block_tables is [batch][max_blocks], sequence b attends its first
-// seq_lens[b] tokens; the launch is cut into work items by the split plan
-// (split_plan.h), grid (decode_grid_items, kv heads).  The vector kernel also
-// serves chunked prefill (plan_units 0): n_q queries per sequence, query i of
-// sequence b attends start_pos[b] + i + 1 tokens, q/out are
-// [batch][n_q][num_heads][head_dim], grid (1, kv heads, batch * n_q).
+// seq_lens[b] tokens.  The same kernels serve chunked prefill on the vector
+// path: n_q queries per sequence, query i of sequence b attends
+// start_pos[b] + i + 1 tokens, q/out are [batch][n_q][num_heads][head_dim].
 struct DecodeArgs {
     PoolLayout L;
     const uint8_t *base;
@@ -64,29 +62,22 @@ struct DecodeArgs {
     const int32_t *start_pos; // prefill only: tokens cached before the chunk
     int num_heads;
     float scale;
-    // decode work plan (split_plan.h): work units per kv head (0: no plan)
-    int plan_units;
-    float *ws;      // partials of split sequences: 2 slots per unit and kv head
-    int *plan_desc; // merge descriptors: 2 ints per unit (after the slots)
+    int split_tokens; // tokens per split, a multiple of the page size
+    int num_splits;
+    float *ws; // partials when num_splits > 1
     int *status;
     int kernel; // -1 automatic, 0 vector ALU, 1 matrix core
 };
 
-// Work units of a decode launch on a device with num_cus CUs (fills
-// plan_units; a.batch, a.num_heads and a.kernel must be set).  max_len: the
-// longest sequence if the caller knows it, else 0.
-void decode_plan(const PoolLayout &L, int num_cus, int max_len, DecodeArgs &a);
+// Bytes of split-K workspace needed for a decode launch.
+size_t decode_workspace_bytes(const PoolLayout &L, int batch, int num_heads, int num_splits);
 
-// Grid width (workgroups per kv head) of a decode launch.
-int decode_grid_items(const DecodeArgs &a);
+// Picks (split_tokens, num_splits) for a batch whose longest sequence has
+// max_len tokens, so the grid fills the device.
+void decode_plan(const PoolLayout &L, int batch, int num_heads, int max_len, int num_cus,
+                 int *split_tokens, int *num_splits);
 
-// Bytes of decode workspace: two partial slots per unit and kv head, then
-// the units' merge descriptors (at decode_desc_offset).
-size_t decode_desc_offset(const PoolLayout &L, int num_heads, int plan_units);
-size_t decode_workspace_bytes(const PoolLayout &L, int num_heads, int plan_units);
-
-// The decode kernel, then (decode) the merge of split sequences.  Returns
-// hipErrorInvalidValue for shapes without a kernel instance.
+// Returns hipErrorInvalidValue for shapes without a kernel instance.
 hipError_t launch_decode(const DecodeArgs &a, hipStream_t st);
 
 // Which kernel launch_decode uses for a layout/head count and a requested

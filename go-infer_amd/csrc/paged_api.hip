@@ -598,11 +598,14 @@ static int decode_locked(gi_paged *h, int layer, int batch, int num_heads, const
     a.scale = scale;
     a.status = h->d_status;
     a.kernel = h->decode_kernel;
-    // max_seq_len only sizes the grid of small launches (a hint, see
-    // decode_plan); the kernels read the lengths on the device
+    // max_seq_len sizes the split plan only (0: the longest sequence the
+    // block tables map); the kernels read the lengths on the device and the
+    // last split of each sequence runs to its end
     const int64_t mapped = (int64_t)max_blocks * h->L.page_tokens;
-    gi::decode_plan(h->L, h->num_cus, (int)(max_seq_len < mapped ? max_seq_len : mapped), a);
-    const size_t need = gi::decode_workspace_bytes(h->L, num_heads, a.plan_units);
+    const int max_len = (int)(max_seq_len > 0 && max_seq_len < mapped ? max_seq_len
+                              : mapped < INT32_MAX ? mapped : INT32_MAX);
+    gi::decode_plan(h->L, batch, num_heads, max_len, h->num_cus, &a.split_tokens, &a.num_splits);
+    const size_t need = gi::decode_workspace_bytes(h->L, batch, num_heads, a.num_splits);
     if (fixed_ws) {
         if (need > fixed_cap)
             return gi::set_error(GI_ERR_BAD_ARG,
@@ -616,7 +619,6 @@ static int decode_locked(gi_paged *h, int layer, int batch, int num_heads, const
             return rc;
         a.ws = (float *)h->plan_ws.ptr;
     }
-    a.plan_desc = (int *)((uint8_t *)a.ws + gi::decode_desc_offset(h->L, num_heads, a.plan_units));
     hipError_t e = gi::launch_decode(a, h->stream);
     return e == hipSuccess ? GI_OK : hip_fail(e, "decode attention");
 }

@@ -255,19 +255,21 @@ int gi_paged_gather(gi_paged *h, int layer, const int32_t *block_table, int n_to
  * b attends its first seq_lens[b] tokens.  q-head h reads kv head h /
  * (num_heads / num_kv_heads) (forward.go:249).
  *
- * The kernels cut the batch's context into equal work ranges from the
- * lengths in device memory, so every seq_lens[b] token is attended whatever
- * max_seq_len says.  max_seq_len (>= 0; 0 means unknown) is a hint that only
- * shrinks the grid of small launches.  A length below zero or beyond
- * max_blocks * page_tokens is clamped and reported by gi_synchronize as
- * GI_ERR_BAD_PAGE.
+ * Long sequences are cut into splits of equal token ranges, attended by
+ * separate workgroups and merged by a second launch.  max_seq_len (>= 0; 0
+ * means unknown: the longest sequence max_blocks maps) sizes that split
+ * plan only: the last split of every sequence runs to its end, so every
+ * seq_lens[b] token is attended whatever max_seq_len says (a short hint
+ * costs balance, never tokens).  A length below zero or beyond max_blocks *
+ * page_tokens is clamped and reported by gi_synchronize as GI_ERR_BAD_PAGE.
  *
- * Workspace: the handle keeps the partials of split sequences, two slots per
- * work unit (sized by the device's CUs and, for a small stream, by
- * max_seq_len).  A call that needs them to grow while the handle's stream is
- * capturing a graph fails with GI_ERR_BAD_ARG (make one eager call with the
- * largest batch first); once any call has been captured, growth keeps the old
- * buffers alive until gi_paged_destroy, so captured graphs stay valid. */
+ * Workspace: the handle keeps the partials of split sequences, batch *
+ * num_kv_heads * splits slots of (num_heads / num_kv_heads) * (head_dim + 2)
+ * floats, where splits falls as batch * num_kv_heads grows (about two
+ * workgroups per CU).  A call that needs it to grow while the handle's stream
+ * is capturing a graph fails with GI_ERR_BAD_ARG (make one eager call with
+ * the same shape first); once any call has been captured, growth keeps the
+ * old buffers alive until gi_paged_destroy, so captured graphs stay valid. */
 int gi_paged_decode_attention(gi_paged *h, int layer, int batch, int num_heads, const float *q,
                               float *out, const int32_t *block_tables, int max_blocks,
                               const int32_t *seq_lens, int max_seq_len, float scale);
@@ -277,12 +279,13 @@ int gi_paged_decode_attention(gi_paged *h, int layer, int batch, int num_heads, 
  * under HIP graph capture, tight serving loops, hosts that forbid it).  The
  * split partials live in a fixed 8 MiB scratch array that the library holds
  * on each device it runs on until the process ends, instead of the handle's
- * growable workspace.  The partials do not grow with the batch: every batch
- * fits up to 8 query heads per kv head at head_dim 128 (more heads per kv
- * head fail with GI_ERR_BAD_ARG).  Every call on one device
- * shares that array, so calls that overlap on one device (other handles or
- * streams) race: serialise them.  Same arguments and results as
- * gi_paged_decode_attention. */
+ * growable workspace.  On a 256-CU device every shape with up to 8 query
+ * heads per kv head fits (at most about 1000 partial slots of 4 KiB); with 16
+ * per kv head a few batches (batch * num_kv_heads of 505 to 511) would need
+ * up to 8.5 MB and fail with GI_ERR_BAD_ARG before any launch.  Every call
+ * on one device shares that array, so calls that overlap on one device
+ * (other handles or streams) race: serialise them.  Same arguments and
+ * results as gi_paged_decode_attention. */
 int gi_paged_decode_attention_noalloc(gi_paged *h, int layer, int batch, int num_heads, const float *q,
                                       float *out, const int32_t *block_tables, int max_blocks,
                                       const int32_t *seq_lens, int max_seq_len, float scale);

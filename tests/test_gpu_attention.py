@@ -429,11 +429,13 @@ def test_prefill_q8_llama8b_chunks(gi, oracle, dev):
     prefill_case(gi, oracle, dev, 2, 32, 8, 128, 16, [1024, 512], 512, seed=70)
 
 
-def test_decode_plan_ignores_a_short_max_seq_len(gi, oracle, dev):
-    """The split plan is derived on the device from seq_lens, so a
-    max_seq_len below the real lengths (0, or one frozen at graph capture
-    while lengths grew) still attends every token of every sequence.  A
-    ragged batch whose longest sequence spans several work items."""
+def test_decode_short_max_seq_len_attends_every_token(gi, oracle, dev):
+    """max_seq_len sizes the split plan only: the last split of a sequence
+    runs to its end, so a hint below the real lengths (one frozen at graph
+    capture while lengths grew) still attends every token of every sequence,
+    and 0 plans for the longest sequence the block tables map.  A ragged
+    batch: hints 1 and 64 give one split per sequence, 2048 two splits of
+    1024 tokens whose second runs on to 5000, 3000 three."""
     import torch
     H, kvh, hd, P = 32, 8, 128, 16
     lens = [1, 5000, 700, 2049, 64, 3333]
@@ -445,7 +447,7 @@ def test_decode_plan_ignores_a_short_max_seq_len(gi, oracle, dev):
     want = oracle_decode(oracle, pop, 0, q, H, lens, scale)
     for kern in kernels_for(pop.pool, H):
         pop.pool.set_decode_kernel(kern)
-        for msl in (0, 1, 64):
+        for msl in (0, 1, 64, 2048, 3000):
             out = torch.full_like(qd, float("nan"))
             pop.pool.AttentionGQA(out, qd, 0, bt, sl, H, scale, msl)
             pop.pool.synchronize()

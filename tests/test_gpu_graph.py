@@ -22,7 +22,7 @@ TOL = {0: 1e-5, 1: 1e-3, 2: 1e-3, 3: 1e-3}
 def test_decode_and_prefill_graph_replays(gi, oracle, dev, kv_type):
     import torch
     H, kvh, hd, P, C = 32, 8, 128, 16, 64
-    # 1100 tokens take two work items and the merge kernel; 70 is a ragged
+    # 1100 tokens take two splits and the merge kernel; 70 is a ragged
     # tail.
     lens = [300, 70, 1100]
     pop = Populated(gi, dev, kv_type, 2, kvh, hd, P, lens, seed=11 + kv_type)
@@ -86,14 +86,14 @@ def test_decode_and_prefill_graph_replays(gi, oracle, dev, kv_type):
 
 
 def test_workspace_growth_keeps_captured_graphs_valid(gi, oracle, dev):
-    """The decode workspace (two partial slots per work unit) grows with the
-    number of units and with the query heads per kv head.  A graph captured
-    with a small stream (max_seq_len 1100: a few units) must keep replaying
-    bit for bit after an eager call with more units grew it (the buffers the
-    graph holds stay alive), and a call that would need it to grow while the
-    stream captures (twice the heads per kv head) is refused
-    (GI_ERR_BAD_ARG) without synchronising or freeing anything; the first
-    graph still replays afterwards."""
+    """The decode workspace (the partials of split sequences) grows with the
+    batch and with the query heads per kv head.  A graph captured with 3
+    sequences must keep replaying bit for bit after an eager call with 60
+    sequences grew it (the buffers the graph holds stay alive), and a call
+    that would need it to grow while the stream captures (60 sequences with
+    twice the heads per kv head) is refused (GI_ERR_BAD_ARG) without
+    synchronising or freeing anything; the first graph still replays
+    afterwards."""
     import torch
     H, kvh, hd, P = 32, 8, 128, 16
     lens = [300, 70, 1100]
@@ -132,8 +132,8 @@ def test_workspace_growth_keeps_captured_graphs_valid(gi, oracle, dev):
         assert torch.equal(od, ref), tag
 
     replay_matches("first replay")
-    # eager call with 60 rows and no length hint: a unit per wave of two
-    # workgroups per CU, so the partials grow
+    # eager call with 60 rows and no length hint: 2 splits of 60 x 8
+    # (sequence, kv head) pairs, 20x the partials of the captured call
     big = 60
     bt_big = bt[torch.arange(big, device=dev) % 3].contiguous()
     sl_big = sl[torch.arange(big, device=dev) % 3].contiguous()
@@ -148,14 +148,14 @@ def test_workspace_growth_keeps_captured_graphs_valid(gi, oracle, dev):
         assert float(rel_err_rows(got[r], want[r % 3], H, hd).max()) <= 1e-3, r
     replay_matches("replay after growth")
     # growth while capturing is refused: 64 query heads (8 per kv head)
-    # double the partial slots
-    q64 = torch.zeros((3, 2 * H * hd), device=dev)
+    # double the partials of the 60-row call
+    q64 = torch.zeros((big, 2 * H * hd), device=dev)
     o64 = torch.empty_like(q64)
     g2 = torch.cuda.CUDAGraph()
     with pytest.raises(gi.GIError) as e:
         with torch.cuda.graph(g2, stream=stream):
             o64.fill_(0.0)
-            pop.pool.AttentionGQA(o64, q64, 0, bt, sl, 2 * H, scale, 0)
+            pop.pool.AttentionGQA(o64, q64, 0, bt_big, sl_big, 2 * H, scale, 0)
     assert e.value.code == -3
     assert "capturing" in str(e.value)
     torch.cuda.synchronize()
