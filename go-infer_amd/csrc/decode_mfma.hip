@@ -48,8 +48,10 @@ using mfma_ops::h8;
 using mfma_ops::f4;
 using mfma_ops::u2;
 using mfma_ops::u4;
+using mfma_ops::i8x8_sub_to_h8;
 using mfma_ops::i8x8_to_h8;
 using mfma_ops::u4x8_masked_to_h8;
+using mfma_ops::u4x8_sub_to_h8;
 using mfma_ops::split_pair;
 typedef uint16_t us2 __attribute__((ext_vector_type(2)));
 
@@ -232,15 +234,14 @@ struct QStage {
 
 typedef __attribute__((address_space(3))) void *lds_ptr;
 
+// K codes of a block into the staging area.
 template <int KT, int HD>
-__device__ __forceinline__ void issue_q(const DecodeArgs &a, int64_t pA, int64_t pB, int sA, int sB,
-                                        int64_t koff, int64_t ksoff, int64_t voff, int64_t vsoff, int lane,
-                                        QStage<KT, HD> &S)
+__device__ __forceinline__ void issue_qk(const DecodeArgs &a, int64_t pA, int64_t pB, int sA, int sB,
+                                         int64_t koff, int lane, QStage<KT, HD> &S)
 {
     typedef QStage<KT, HD> Q;
-    constexpr int KK = Q::KK, RB = Q::RB, CB = Q::CB, NS = Q::NS;
+    constexpr int RB = Q::RB, CB = Q::CB, NS = Q::NS;
     const PoolLayout &L = a.L;
-    const int P = L.page_tokens;
     const uint8_t *gA = a.base + pA * L.page_bytes, *gB = a.base + pB * L.page_bytes;
 #pragma unroll
     for (int q = 0; q < Q::NLOAD; q++) {
@@ -252,18 +253,25 @@ __device__ __forceinline__ void issue_q(const DecodeArgs &a, int64_t pA, int64_t
                              koff + kk * CB + 16 * gp;
         __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.k[1024 * q], 16, 0, kDecodeLdsAux);
     }
-#pragma unroll
-    for (int q = 0; q < Q::NLOAD; q++) {
-        const int sl = 64 * q + lane;
-        const int jj = (sl >> 1) & 15, r = sl >> 5;
-        const int h = (sl & 1) ^ ((jj >> 3) & 1);
-        const uint8_t *src = (h ? gB + sB : gA + sA) + voff + (int64_t)(16 * r + jj) * P;
-        __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.v[1024 * q], 16, 0, kDecodeLdsAux);
-    }
+}
+
+// Both scale planes, then the V codes of a block, into the staging area (in
+// this order: a wait for all but the last NLOAD loads covers the scales).
+template <int KT, int HD>
+__device__ __forceinline__ void issue_qv(const DecodeArgs &a, int64_t pA, int64_t pB, int sA, int sB,
+                                         int64_t ksoff, int64_t voff, int64_t vsoff, int lane,
+                                         QStage<KT, HD> &S)
+{
+    typedef QStage<KT, HD> Q;
+    constexpr int KK = Q::KK;
+    const PoolLayout &L = a.L;
+    const int P = L.page_tokens;
+    const uint8_t *gA = a.base + pA * L.page_bytes, *gB = a.base + pB * L.page_bytes;
     // Both scale planes in one 16-byte load of 32 lanes: lane c < 16 fills
     // ks bytes 16c .. 16c+15, lane 16 + c fills vs bytes 16c .. 16c+15.  The
     // texture unit spends about as long on a load of 4-byte lanes as on one
-    // of 16-byte lanes, so one wide load replaces two narrow ones.
+    // of 16-byte lanes, so one wide load replaces two narrow ones.  (Some
+    // lane of the first 16 always takes part, so the wave always issues it.)
     {
         const int c = lane & 15, h = c >> 3;
         const uint8_t *pg = h ? gB : gA;
@@ -278,10 +286,25 @@ __device__ __forceinline__ void issue_q(const DecodeArgs &a, int64_t pA, int64_t
         if (lane < 32 && use)
             __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.ks[0], 16, 0, kDecodeLdsAux);
     }
+#pragma unroll
+    for (int q = 0; q < Q::NLOAD; q++) {
+        const int sl = 64 * q + lane;
+        const int jj = (sl >> 1) & 15, r = sl >> 5;
+        const int h = (sl & 1) ^ ((jj >> 3) & 1);
+        const uint8_t *src = (h ? gB + sB : gA + sA) + voff + (int64_t)(16 * r + jj) * P;
+        __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.v[1024 * q], 16, 0, kDecodeLdsAux);
+    }
 }
 
+// s_waitcnt immediate for vmcnt(n), the other counters left alone.
+constexpr int vmcnt_imm(int n)
+{
+    return 0x0F70 | (n & 15) | ((n >> 4) << 14);
+}
+
+// K codes and K scales of the staged block into operand registers.
 template <int KT, int HD>
-__device__ __forceinline__ void read_q(const QStage<KT, HD> &S, int j, int g, QBlock<KT, HD> &B)
+__device__ __forceinline__ void read_qk(const QStage<KT, HD> &S, int j, int g, QBlock<KT, HD> &B)
 {
     typedef QStage<KT, HD> Q;
     constexpr int KK = Q::KK, CB = Q::CB, NS = Q::NS;
@@ -299,11 +322,19 @@ __device__ __forceinline__ void read_q(const QStage<KT, HD> &S, int j, int g, QB
                 B.k0[kk] = c;
         }
 #pragma unroll
-    for (int r = 0; r < (KT == KV_Q4_0 ? KK : 2 * KK); r++)
-        B.v[r] = *reinterpret_cast<const u2 *>(&S.v[((r * 16 + j) * 2 + ((g >> 1) ^ x)) * 16 + 8 * (g & 1)]);
-#pragma unroll
     for (int i = 0; i < KK; i++)
         B.ks[i] = *reinterpret_cast<const u4 *>(&S.ks[128 * (g >> 1) + 16 * KK * (g & 1) + 16 * i]);
+}
+
+// V codes and V scales of the staged block into operand registers.
+template <int KT, int HD>
+__device__ __forceinline__ void read_qv(const QStage<KT, HD> &S, int j, int g, QBlock<KT, HD> &B)
+{
+    constexpr int KK = QStage<KT, HD>::KK;
+    const int x = (j >> 3) & 1;
+#pragma unroll
+    for (int r = 0; r < (KT == KV_Q4_0 ? KK : 2 * KK); r++)
+        B.v[r] = *reinterpret_cast<const u2 *>(&S.v[((r * 16 + j) * 2 + ((g >> 1) ^ x)) * 16 + 8 * (g & 1)]);
 #pragma unroll
     for (int db = 0; db < KK; db++)
         B.vs[db] = *reinterpret_cast<const u4 *>(&S.vs[128 * (g >> 1) + 32 * db + 16 * (g & 1)]);
@@ -552,24 +583,27 @@ __device__ __forceinline__ void read_f32(const F32Stage<HD> &Sf, int j, int g, i
 
 // Scores of one block from quantised K: per k-step a fresh product of the
 // codes, scaled by the K block scale of its row's token, then the packed
-// hi/lo columns are completed with the lane mirror.
+// hi/lo columns are completed with the lane mirror.  The codes enter as fp16
+// subnormals (code + offset) * 2^-24 (q4_0: n = code + 8, its high nibbles
+// in place as 16n; q8_0: code + 128); each product starts from qz[kk], minus
+// the offset times 2^-24 times its column's query sum over the k-step, so it
+// ends at 2^-24 times the product of the codes themselves (the 2^24 is in
+// the scores' factor).
 template <int KT, int HD, int GP>
-__device__ __forceinline__ void qk_q(const QBlock<KT, HD> &B, const h8 *qh, int g, f4 &s0, f4 &s1)
+__device__ __forceinline__ void qk_q(const QBlock<KT, HD> &B, const h8 *qh, const f4 *qz, int g, f4 &s0, f4 &s1)
 {
     constexpr int KK = HD / 32;
     s0 = f4{0.0f, 0.0f, 0.0f, 0.0f};
     s1 = f4{0.0f, 0.0f, 0.0f, 0.0f};
-    // q4_0: lanes g >= 2 take the high nibbles in place (16 (n - 8)); their
-    // query elements carry 1/16
-    const bool hi_nib = (g & 2) != 0;
-    const uint32_t km = hi_nib ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
-    const h2 kb = hi_nib ? h2{(_Float16)1152.0f, (_Float16)1152.0f} : h2{(_Float16)1032.0f, (_Float16)1032.0f};
+    // q4_0: lanes g >= 2 take the high nibbles in place (16n); their query
+    // elements carry 1/16
+    const uint32_t km = (g & 2) ? 0x00F000F0u : 0x000F000Fu;
 #pragma unroll
     for (int kk = 0; kk < KK; kk++) {
-        const h8 a0 = KT == KV_Q4_0 ? u4x8_masked_to_h8(B.k0[kk], km, kb) : i8x8_to_h8(B.k0[kk]);
-        const h8 a1 = KT == KV_Q4_0 ? u4x8_masked_to_h8(B.k1[kk], km, kb) : i8x8_to_h8(B.k1[kk]);
-        const f4 z0 = mfma(a0, qh[kk], f4{0.0f, 0.0f, 0.0f, 0.0f});
-        const f4 z1 = mfma(a1, qh[kk], f4{0.0f, 0.0f, 0.0f, 0.0f});
+        const h8 a0 = KT == KV_Q4_0 ? u4x8_sub_to_h8(B.k0[kk], km) : i8x8_sub_to_h8(B.k0[kk]);
+        const h8 a1 = KT == KV_Q4_0 ? u4x8_sub_to_h8(B.k1[kk], km) : i8x8_sub_to_h8(B.k1[kk]);
+        const f4 z0 = mfma(a0, qh[kk], qz[kk]);
+        const f4 z1 = mfma(a1, qh[kk], qz[kk]);
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             // output row 4g + r of tile 0 is token 8g + r, of tile 1 8g + 4 + r
@@ -698,6 +732,22 @@ __device__ __forceinline__ void softmax_pv(f4 s0, f4 s1, h8 *v, int base, int ok
     }
 }
 
+// P*V of one output tile from quantised V.  The codes enter as exact fp16
+// values code - offset (q4_0: n - 8 of dimension tile h of the byte row,
+// the high nibbles in place as 16 (n - 8), so tile 2db+1 accumulates 16 O).
+// (Codes taken as subnormals with the offset taken out by a second product
+// lose accuracy: the two sums cancel when the output is small beside the
+// weights, 9e-5 against 6e-6 relative at batch 256 x 8192.)
+template <int KT>
+__device__ __forceinline__ void pv_q(const h8 &pw8, u2 codes, int h, f4 &o)
+{
+    const h8 vv = KT == KV_Q4_0 ? u4x8_masked_to_h8(codes, h ? 0xF0F0F0F0u : 0x0F0F0F0Fu,
+                                                    h ? h2{(_Float16)1152.0f, (_Float16)1152.0f}
+                                                      : h2{(_Float16)1032.0f, (_Float16)1032.0f})
+                                : i8x8_to_h8(codes);
+    o = mfma(pw8, vv, o);
+}
+
 // Lane j ^ 8 of the same 16-lane row (an update of 0: folds into its user).
 __device__ __forceinline__ float xor8(float x)
 {
@@ -818,13 +868,8 @@ __device__ __forceinline__ void softmax_pv_q4(f4 s0, f4 s1, QBlock<KT, HD> &B, i
         // lanes j < 8: own tokens 0-3, then lane j+8's tokens 4-7
         const h8 pw8 = __builtin_bit_cast(h8, u4{pa, pb, xor8u(pa), xor8u(pb)});
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const h8 vv = KT == KV_Q4_0 ? u4x8_masked_to_h8(B.v[db], h ? 0xF0F0F0F0u : 0x0F0F0F0Fu,
-                                                            h ? h2{(_Float16)1152.0f, (_Float16)1152.0f}
-                                                              : h2{(_Float16)1032.0f, (_Float16)1032.0f})
-                                        : i8x8_to_h8(B.v[2 * db + h]);
-            S.o[2 * db + h] = mfma(pw8, vv, S.o[2 * db + h]);
-        }
+        for (int h = 0; h < 2; h++)
+            pv_q<KT>(pw8, B.v[KT == KV_Q4_0 ? db : 2 * db + h], h, S.o[2 * db + h]);
     }
 }
 
@@ -934,28 +979,23 @@ __device__ __forceinline__ void softmax_pv_q(f4 s0, f4 s1, QBlock<KT, HD> &B, in
 #pragma unroll
     for (int db = 0; db < KK; db++) {
         const h8 vh = __builtin_bit_cast(h8, B.vs[db]);
-        uint32_t pk[4];
+        float y[8];
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
+        for (int i = 0; i < 8; i++) {
             // x = p / vnorm * vscale (times 2^11 on lo rows), the scale read
             // as a half by the mixed-precision multiply-add (exact widening)
-            const float x0 = fmaf(pp[2 * k], (float)vh[2 * k], 0.0f);
-            const float x1 = fmaf(pp[2 * k + 1], (float)vh[2 * k + 1], 0.0f);
+            const float x = fmaf(pp[i], (float)vh[i], 0.0f);
             // hi rows: x itself; lo rows: x - trunc11(x)
-            const float y0 = x0 - __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, x0) & cut);
-            const float y1 = x1 - __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, x1) & cut);
-            pk[k] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(y0, y1));
+            y[i] = x - __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, x) & cut);
         }
+        uint32_t pk[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            pk[k] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(y[2 * k], y[2 * k + 1]));
         const h8 pw8 = __builtin_bit_cast(h8, u4{pk[0], pk[1], pk[2], pk[3]});
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            // q4_0: the high nibbles in place, so tile 2db+1 accumulates 16 O
-            const h8 vv = KT == KV_Q4_0 ? u4x8_masked_to_h8(B.v[db], h ? 0xF0F0F0F0u : 0x0F0F0F0Fu,
-                                                            h ? h2{(_Float16)1152.0f, (_Float16)1152.0f}
-                                                              : h2{(_Float16)1032.0f, (_Float16)1032.0f})
-                                        : i8x8_to_h8(B.v[2 * db + h]);
-            S.o[2 * db + h] = mfma(pw8, vv, S.o[2 * db + h]);
-        }
+        for (int h = 0; h < 2; h++)
+            pv_q<KT>(pw8, B.v[KT == KV_Q4_0 ? db : 2 * db + h], h, S.o[2 * db + h]);
     }
 }
 
@@ -1029,6 +1069,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
     // (Loaded by load_q once the wave's first block is in flight, so that the
     // two memory round trips overlap.)
     h8 qh[KK], ql[KK];
+    f4 qz[KK]; // quantised pages: the initial value of each k-step's product
     float c = 0.0f;
     auto load_q = [&]() {
         float qv[KK][8];
@@ -1060,13 +1101,37 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
         for (int kk = 0; kk < KK; kk++)
 #pragma unroll
             for (int v = 0; v < 8; v++) {
-                const float x = qv[kk][v] * up;
+                // q4_0 pages: operand slot v holds dimension 8g + sv, in the
+                // order the nibble conversion yields (0, 2, 1, 3, 4, 6, 5, 7)
+                const int sv = KT == KV_Q4_0 ? (v & 4) | ((v & 1) << 1) | ((v >> 1) & 1) : v;
+                const float x = qv[kk][sv] * up;
                 _Float16 hi = (_Float16)x;
                 _Float16 lo = (_Float16)(x - (float)hi);
                 qh[kk][v] = qlo ? lo : hi;
                 ql[kk][v] = lo;
             }
         c = a.scale * kLog2e * ldexpf(1.0f, -qe);
+        if constexpr (QUANT) {
+            // codes enter the products as (code + off) * 2^-24: start each
+            // product at -off * 2^-24 times its column's query sum (the
+            // values of the operand itself; q4_0 high-nibble slots count 16
+            // times), and take 2^24 out through c
+            const float off = KT == KV_Q4_0 ? 8.0f : 128.0f;
+            const float fac = KT == KV_Q4_0 && (g & 2) ? 16.0f : 1.0f;
+#pragma unroll
+            for (int kk = 0; kk < KK; kk++) {
+                float t = 0.0f;
+#pragma unroll
+                for (int v = 0; v < 8; v++)
+                    t += (float)qh[kk][v];
+                t *= fac;
+                t += __shfl_xor(t, 16);
+                t += __shfl_xor(t, 32);
+                const float z = t * (-off * 0x1p-24f);
+                qz[kk] = f4{z, z, z, z};
+            }
+            c *= 0x1p24f;
+        }
     };
     State<HD> S;
     S.m2 = -INFINITY;
@@ -1101,13 +1166,21 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
             int sA, sB;
             int ok;
             block_pages(a, bt, base, t1, pA, pB, sA, sB, ok);
-            issue_q<KT, HD>(a, pA, pB, sA, sB, koff, ksoff, voff, vsoff, lane, Sq);
+            issue_qk<KT, HD>(a, pA, pB, sA, sB, koff, lane, Sq);
+            issue_qv<KT, HD>(a, pA, pB, sA, sB, ksoff, voff, vsoff, lane, Sq);
             load_q();
+            // Loads go out in the order K codes, scales, V codes of one
+            // block, K codes of the next, ...: the K half of a block is read
+            // (and the next block's K refills its slots) before the scores,
+            // the V half after them, so neither half's registers live
+            // through the other's work.
+            constexpr int NL = QStage<KT, HD>::NLOAD;
             for (;;) {
                 QBlock<KT, HD> B;
-                // the only vector loads in flight are this block's
-                __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0)
-                read_q<KT, HD>(Sq, j, g, B);
+                // this block's K codes and scales have arrived (its V codes,
+                // the last NL loads issued, may still be in flight)
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm(NL));
+                read_qk<KT, HD>(Sq, j, g, B);
                 const int next = base + stride;
                 const bool more = next < t1;
                 int64_t nA = pA, nB = pB;
@@ -1115,13 +1188,24 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
                 int nok = ok;
                 if (more) {
                     block_pages(a, bt, next, t1, nA, nB, nsA, nsB, nok);
-                    // every read of this block has returned before its
-                    // slots are refilled
+                    // every read of this block's K half has returned before
+                    // its slots are refilled
                     __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0)
-                    issue_q<KT, HD>(a, nA, nB, nsA, nsB, koff, ksoff, voff, vsoff, lane, Sq);
+                    issue_qk<KT, HD>(a, nA, nB, nsA, nsB, koff, lane, Sq);
                 }
                 f4 s0, s1;
-                qk_q<KT, HD, GP>(B, qh, g, s0, s1);
+                qk_q<KT, HD, GP>(B, qh, qz, g, s0, s1);
+                // this block's V codes have arrived (the next block's K
+                // codes, issued after them, may still be in flight)
+                if (more)
+                    __builtin_amdgcn_s_waitcnt(vmcnt_imm(NL));
+                else
+                    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+                read_qv<KT, HD>(Sq, j, g, B);
+                if (more) {
+                    __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0)
+                    issue_qv<KT, HD>(a, nA, nB, nsA, nsB, ksoff, voff, vsoff, lane, Sq);
+                }
                 softmax_pv_q<KT, HD, GP>(s0, s1, B, base, ok, t1, j, g, c, S, vnorm);
                 if (!more)
                     break;
@@ -1341,12 +1425,19 @@ static void launch_mfma_hd(const DecodeArgs &a, dim3 grid, hipStream_t st)
                        grid, dim3(256), 0, st, a);
 }
 
+// q4_0 pages are bound by the vector ALU: three waves per SIMD (the
+// register allocator then keeps the kernel at 168 VGPRs, unspilled) measured
+// 0.487 against 0.522 ms per launch at batch 256 x 8192.  q8_0 pages are
+// bound by the texture path, where a third wave costs (0.855 against 0.78).
+template <int KT>
+constexpr int kDecodeOccQ = KT == KV_Q4_0 ? 3 : kDecodeOcc;
+
 template <int KT, int HD>
 static void launch_mfma_q(const DecodeArgs &a, dim3 grid, hipStream_t st)
 {
 #define GI_Q(GPv)                                                                                        \
     hipLaunchKernelGGL((mfma_decode::attn_mfma_q<KT, HD, GPv, kDecodeNt, kDecodePrefetch, \
-                                                 kDecodeOcc>),                                \
+                                                 kDecodeOccQ<KT>>),                           \
                        grid, dim3(256), 0, st, a)
     switch (a.num_heads / a.L.num_kv_heads) {
     case 1: GI_Q(1); break;

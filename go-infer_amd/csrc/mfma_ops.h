@@ -125,5 +125,30 @@ __device__ __forceinline__ h8 u4x8_masked_to_h8(u2 w, uint32_t m, h2 bias)
     return r;
 }
 
+// Eight Q4_0 nibbles -> eight fp16 subnormals n * 2^-24, exact: the mask m
+// (0x000F000F: low nibbles n; 0x00F000F0: high nibbles in place, 16n) keeps
+// one nibble of bytes 0 and 2 of a word in the low bits of its two halves,
+// and the word shifted right by 8 gives bytes 1 and 3.  The operand order is
+// bytes 0, 2, 1, 3, 4, 6, 5, 7 (the other operand of the product must follow
+// it); the code offset 8 is left to the caller.  One AND per two halves, and
+// one shift per four, against a permute and a packed subtract per two
+// halves for the normal 1024 + n form.
+__device__ __forceinline__ h8 u4x8_sub_to_h8(u2 w, uint32_t m)
+{
+    const u4 r = {w.x & m, (w.x >> 8) & m, w.y & m, (w.y >> 8) & m};
+    return __builtin_bit_cast(h8, r);
+}
+
+// Eight int8 codes x -> eight fp16 subnormals (x + 128) * 2^-24, exact and in
+// order: (x ^ 0x80) is x + 128 as an unsigned byte, placed in the low byte of
+// a half whose high byte is 0.  The offset 128 is left to the caller.
+__device__ __forceinline__ h8 i8x8_sub_to_h8(u2 w)
+{
+    const uint32_t x0 = w.x ^ 0x80808080u, x1 = w.y ^ 0x80808080u;
+    const u4 r = {__builtin_amdgcn_perm(0u, x0, 0x0C010C00u), __builtin_amdgcn_perm(0u, x0, 0x0C030C02u),
+                  __builtin_amdgcn_perm(0u, x1, 0x0C010C00u), __builtin_amdgcn_perm(0u, x1, 0x0C030C02u)};
+    return __builtin_bit_cast(h8, r);
+}
+
 } // namespace mfma_ops
 } // namespace gi
