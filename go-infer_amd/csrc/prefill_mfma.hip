@@ -1402,7 +1402,7 @@ static void launch_lds(const PrefillArgs &a, hipStream_t st)
         const int64_t per_wg = 4 * 16 * ncg;
         return dim3((unsigned)((cols + per_wg - 1) / per_wg), a.L.num_kv_heads, a.batch);
     };
-    if (KT == KV_F16) {
+    if constexpr (KT == KV_F16) {
         constexpr int NCG = kPrefillDirectNcg;
         switch (a.L.page_tokens) {
         case 16:
@@ -1415,8 +1415,7 @@ static void launch_lds(const PrefillArgs &a, hipStream_t st)
             hipLaunchKernelGGL((attn_prefill_dlds<HD, 64, NCG>), grid(NCG), dim3(256), 0, st, a);
             break;
         }
-        return;
-    }
+    } else {
 #define GI_PFL(PT)                                                                           \
     hipLaunchKernelGGL((attn_prefill_lds<HD, KT, PT, NBUF, prefill_lds_ncg<HD, KT, PT>()>), \
                        grid(prefill_lds_ncg<HD, KT, PT>()), dim3(256), 0, st, a)
@@ -1432,6 +1431,7 @@ static void launch_lds(const PrefillArgs &a, hipStream_t st)
         break;
     }
 #undef GI_PFL
+    }
 }
 
 hipError_t launch_prefill_mfma(const PrefillArgs &a, hipStream_t st)
