@@ -430,15 +430,15 @@ constexpr int kTB = 64; // tokens per staged block
 // lagging the true one by at most kLazy, so p <= 2^14 stays well inside fp16.
 constexpr float kPExp = 6.0f, kLazy = 8.0f;
 
-template <int HD, int KT>
+template <int HD, int KT, int NW = 4>
 struct StageRegs {
-    // 16-byte chunks per thread and block: f32 K rows / V columns of 4
-    // elements, fp16 of 8, int8 K rows / V columns of 16 elements, or q4_0 K rows of 32
-    // nibbles (one quantisation block) / V byte rows of 16 tokens (two
-    // dimensions each).
+    // 16-byte chunks per thread and block (NW waves stage it): f32 K rows /
+    // V columns of 4 elements, fp16 of 8, int8 K rows / V columns of 16
+    // elements, or q4_0 K rows of 32 nibbles (one quantisation block) / V
+    // byte rows of 16 tokens (two dimensions each).
     static constexpr bool QUANT = KT == KV_Q8_0 || KT == KV_Q4_0;
-    static constexpr int NC = KT == KV_F32 ? HD / 16 : KT == KV_F16 ? HD / 32 : KT == KV_Q8_0 ? HD / 64 : HD / 128;
-    static_assert(NC >= 1, "q4_0 staging needs head_dim 128");
+    static constexpr int NC = (KT == KV_F32 ? HD / 16 : KT == KV_F16 ? HD / 32 : KT == KV_Q8_0 ? HD / 64 : HD / 128) * 4 / NW;
+    static_assert(NC >= 1, "too few chunks per thread (q4_0 staging needs head_dim 128 and 4 waves)");
     u4 k[NC], v[NC];
     int64_t kpage[QUANT ? NC : 1]; // quantised pages: page of each chunk (wave-uniform)
     int64_t vpage[QUANT ? NC : 1];
@@ -504,10 +504,11 @@ __device__ __forceinline__ int table_entry(const int32_t *bt, int t, int wg_len)
     return t < wg_len ? bt[t / P] : -1;
 }
 
-template <int HD, int KT, int P>
+template <int HD, int KT, int P, int NW>
 __device__ __forceinline__ void stage_load(const PrefillArgs &a, int kvh, int tid, int w, int tb,
-                                           StageRegs<HD, KT> &R)
+                                           StageRegs<HD, KT, NW> &R)
 {
+    constexpr int NT = 64 * NW;
     using M = ChunkMap<HD, KT, P>;
     const PoolLayout &L = a.L;
     const int64_t np = L.num_pages;
@@ -517,7 +518,7 @@ __device__ __forceinline__ void stage_load(const PrefillArgs &a, int kvh, int ti
     };
 #pragma unroll
     for (int c = 0; c < R.NC; c++) {
-        const int ch = tid + 256 * c, ch0 = 64 * w + 256 * c;
+        const int ch = tid + NT * c, ch0 = 64 * w + NT * c;
         const uint8_t *kp = a.base + page(M::k_tok(ch0)) * L.page_bytes + L.k_off;
         const int tk = M::k_tok(ch);
         const uint8_t *vp = a.base + page(M::v_seg(ch0) * P) * L.page_bytes;
@@ -621,9 +622,9 @@ __device__ __forceinline__ float pow2_recip(float x)
 // Converts and stores a staged block.  `vmask` bit l: block token l is cached
 // and on a valid page; V of other tokens is stored as zero (their scores are
 // masked, and stale values must not reach O through 0 * NaN).
-template <int HD, int KT, int P, int NBUF>
+template <int HD, int KT, int P, int NBUF, int NW>
 __device__ __forceinline__ void stage_store(const PrefillArgs &a, int kvh, int tid, int w, int buf,
-                                            uint64_t vmask, const StageRegs<HD, KT> &R,
+                                            uint64_t vmask, const StageRegs<HD, KT, NW> &R,
                                             Lds<HD, KT, NBUF> &S, float ksc = 1.0f, float vsc = 1.0f, float neg1 = -1.0f)
 {
     using M = ChunkMap<HD, KT, P>;
@@ -631,13 +632,15 @@ __device__ __forceinline__ void stage_store(const PrefillArgs &a, int kvh, int t
     // q8_0 block scales: one per K chunk, 16 per V chunk.  Loaded here rather
     // than with the chunk so that they hold no registers through the block's
     // compute (they are shared by many chunks and come from the caches).
-    constexpr int NCS = StageRegs<HD, KT>::QUANT ? StageRegs<HD, KT>::NC : 1;
+    typedef StageRegs<HD, KT, NW> SR;
+    constexpr int NT = 64 * NW;
+    constexpr int NCS = SR::QUANT ? SR::NC : 1;
     u4 vs[2 * NCS];
     _Float16 ks[NCS];
-    if (StageRegs<HD, KT>::QUANT) {
+    if (SR::QUANT) {
 #pragma unroll
         for (int c = 0; c < R.NC; c++) {
-            const int ch = tid + 256 * c;
+            const int ch = tid + NT * c;
             const u4 *sp = reinterpret_cast<const u4 *>(
                 a.base + R.vpage[c] * a.L.page_bytes + a.L.vs_off +
                 (((int64_t)kvh * (HD / 32) + M::v_dim(ch) / (KT == KV_Q4_0 ? 16 : 32)) * P + M::v_tok(ch)) * 2);
@@ -649,7 +652,7 @@ __device__ __forceinline__ void stage_store(const PrefillArgs &a, int kvh, int t
     }
 #pragma unroll
     for (int c = 0; c < R.NC; c++) {
-        const int ch = tid + 256 * c;
+        const int ch = tid + NT * c;
         const int tk = M::k_tok(ch), col = M::k_col(ch);
         const int d = M::v_dim(ch), t0 = M::v_seg(ch) * P + M::v_tok(ch); // block-local token
         const uint32_t live = (uint32_t)(vmask >> t0) & ((1u << M::EV) - 1u);
@@ -1079,7 +1082,7 @@ struct WaveAttn {
 
 // Work split shared by both staged kernels: the workgroup's columns, the
 // context each wave and the workgroup must cover, and the block-table reads.
-template <int P, int NCG>
+template <int P, int NCG, int NW = 4>
 struct PrefillWork {
     int wx, kvh, b, tid, lane, w, j, g, start, mapped, col0, wave_len, wg_full, wg_len;
     bool wave_active;
@@ -1100,10 +1103,10 @@ struct PrefillWork {
         start = a.start_pos[b];
         bt = a.block_tables + (int64_t)b * a.max_blocks;
         mapped = a.max_blocks * P;
-        col0 = (wx * 4 + w) * WCOLS;
+        col0 = (wx * NW + w) * WCOLS;
         wave_len = min(start + min((col0 + WCOLS - 1) / G, chunk - 1) + 1, mapped);
-        wg_full = min(start + wx * 4 * WCOLS / G + 1, mapped); // shortest column of the workgroup
-        wg_len = min(start + min((wx * 4 * WCOLS + 4 * WCOLS - 1) / G, chunk - 1) + 1, mapped);
+        wg_full = min(start + wx * NW * WCOLS / G + 1, mapped); // shortest column of the workgroup
+        wg_len = min(start + min((wx * NW * WCOLS + NW * WCOLS - 1) / G, chunk - 1) + 1, mapped);
         wave_active = col0 / G < chunk;
         if (start + chunk > mapped && tid == 0 && a.status)
             atomicOr(a.status, FLAG_BAD_SLOT);
@@ -1130,18 +1133,20 @@ struct PrefillWork {
     }
 };
 
-template <int HD, int KT, int P, int NBUF, int NCG>
-__global__ __launch_bounds__(256) void attn_prefill_lds(PrefillArgs a)
+// NW waves per workgroup share its staging: 4, or 8 (two per SIMD in one
+// workgroup, so that one workgroup per CU holds two staging buffers).
+template <int HD, int KT, int P, int NBUF, int NCG, int NW>
+__global__ __launch_bounds__(64 * NW) void attn_prefill_lds(PrefillArgs a)
 {
     constexpr bool F32 = KT == KV_F32;
-    static_assert(!F32 || NBUF == 1, "f32 pages exchange block maxima at the single-buffer barrier");
-    const PrefillWork<P, NCG> W(a);
+    static_assert(!F32 || (NBUF == 1 && NW == 4), "f32 pages exchange block maxima at the single-buffer barrier");
+    const PrefillWork<P, NCG, NW> W(a);
     __shared__ Lds<HD, KT, NBUF> S;
     __shared__ float s_bmax[4][2]; // f32 pages: per-wave |K|, |V| maxima of the block being staged
     WaveAttn<HD, KT, NCG> A;
     A.init(a, W.b, W.kvh, W.col0, W.start, W.mapped, W.wave_active, W.j, W.g);
 
-    StageRegs<HD, KT> R;
+    StageRegs<HD, KT, NW> R;
     // f32 pages: power-of-two operand scales of the staged block (running,
     // workgroup-uniform), of the block in LDS, and the scale O is held in
     float ksc_run = 0.0f, vsc_run = 0.0f, ksc_cur = 1.0f, vsc_cur = 1.0f, vsc_o = 0.0f;
@@ -1166,10 +1171,10 @@ __global__ __launch_bounds__(256) void attn_prefill_lds(PrefillArgs a)
     };
     int tb = W.table(0);
     uint64_t mask_c = W.valid_mask(a, tb, 0);
-    stage_load<HD, KT, P>(a, W.kvh, W.tid, W.w, tb, R);
+    stage_load<HD, KT, P, NW>(a, W.kvh, W.tid, W.w, tb, R);
     tb = W.table(kTB);
     f32_scales(mask_c);
-    stage_store<HD, KT, P, NBUF>(a, W.kvh, W.tid, W.w, 0, mask_c, R, S, ksc_run, vsc_run, A.neg1);
+    stage_store<HD, KT, P, NBUF, NW>(a, W.kvh, W.tid, W.w, 0, mask_c, R, S, ksc_run, vsc_run, A.neg1);
     ksc_cur = ksc_run;
     vsc_cur = vsc_run;
     __syncthreads();
@@ -1183,7 +1188,7 @@ __global__ __launch_bounds__(256) void attn_prefill_lds(PrefillArgs a)
         uint64_t mask_n = 0;
         if (more) {
             mask_n = W.valid_mask(a, tb, base + kTB);
-            stage_load<HD, KT, P>(a, W.kvh, W.tid, W.w, tb, R);
+            stage_load<HD, KT, P, NW>(a, W.kvh, W.tid, W.w, tb, R);
             tb = W.table(base + 2 * kTB);
         }
         if constexpr (F32) {
@@ -1201,7 +1206,7 @@ __global__ __launch_bounds__(256) void attn_prefill_lds(PrefillArgs a)
                 f32_scales(mask_n); // its barrier also frees the single buffer
             else if (NBUF == 1)
                 __syncthreads();
-            stage_store<HD, KT, P, NBUF>(a, W.kvh, W.tid, W.w, NBUF == 2 ? (buf ^ 1) : 0, mask_n, R, S,
+            stage_store<HD, KT, P, NBUF, NW>(a, W.kvh, W.tid, W.w, NBUF == 2 ? (buf ^ 1) : 0, mask_n, R, S,
                                          ksc_run, vsc_run, A.neg1);
         }
         mask_c = mask_n;
@@ -1371,10 +1376,15 @@ constexpr int prefill_ncg()
 }
 
 // LDS buffers of the staged kernel: two (one barrier per block) for fp16
-// pages; one for q8_0, whose V hi/lo planes would otherwise leave room for a
-// single workgroup per CU.
+// pages.  Quantised pages stage K and V as hi/lo planes (64 KiB a block at
+// head_dim 128): q8_0 at head_dim 128 runs one workgroup of 8 waves per CU
+// over two buffers (128 KiB); the other quantised shapes (fewer 16-byte
+// chunks per block than 512 threads) one 4-wave workgroup over one buffer.
 constexpr int kPrefillNbufF16 = 2;
-constexpr int kPrefillNbufQ8 = 1;
+template <int HD, int KT>
+constexpr int kPrefillWaves = KT == KV_Q8_0 && HD == 128 ? 8 : 4;
+template <int HD, int KT>
+constexpr int kPrefillNbufQ = kPrefillWaves<HD, KT> == 8 ? 2 : 1;
 // f32 pages: one buffer (their block maxima are exchanged at its barrier).
 
 // Column groups per wave: two halve the LDS reads per matrix-core product;
@@ -1395,30 +1405,31 @@ template <int HD, int KT>
 static void launch_lds(const PrefillArgs &a, hipStream_t st)
 {
     using namespace mfma_prefill;
-    constexpr int NBUF = KT == KV_F32 ? 1 : KT == KV_F16 ? kPrefillNbufF16 : kPrefillNbufQ8;
+    constexpr int NBUF = KT == KV_F32 ? 1 : KT == KV_F16 ? kPrefillNbufF16 : kPrefillNbufQ<HD, KT>;
+    constexpr int NW = KT == KV_F32 || KT == KV_F16 ? 4 : kPrefillWaves<HD, KT>;
     const int G = a.num_heads / a.L.num_kv_heads;
     const int64_t cols = (int64_t)a.chunk_len * G;
-    auto grid = [&](int ncg) {
-        const int64_t per_wg = 4 * 16 * ncg;
+    auto grid = [&](int ncg, int nw) {
+        const int64_t per_wg = nw * 16 * ncg;
         return dim3((unsigned)((cols + per_wg - 1) / per_wg), a.L.num_kv_heads, a.batch);
     };
     if constexpr (KT == KV_F16) {
         constexpr int NCG = kPrefillDirectNcg;
         switch (a.L.page_tokens) {
         case 16:
-            hipLaunchKernelGGL((attn_prefill_dlds<HD, 16, NCG>), grid(NCG), dim3(256), 0, st, a);
+            hipLaunchKernelGGL((attn_prefill_dlds<HD, 16, NCG>), grid(NCG, 4), dim3(256), 0, st, a);
             break;
         case 32:
-            hipLaunchKernelGGL((attn_prefill_dlds<HD, 32, NCG>), grid(NCG), dim3(256), 0, st, a);
+            hipLaunchKernelGGL((attn_prefill_dlds<HD, 32, NCG>), grid(NCG, 4), dim3(256), 0, st, a);
             break;
         default:
-            hipLaunchKernelGGL((attn_prefill_dlds<HD, 64, NCG>), grid(NCG), dim3(256), 0, st, a);
+            hipLaunchKernelGGL((attn_prefill_dlds<HD, 64, NCG>), grid(NCG, 4), dim3(256), 0, st, a);
             break;
         }
     } else {
 #define GI_PFL(PT)                                                                           \
-    hipLaunchKernelGGL((attn_prefill_lds<HD, KT, PT, NBUF, prefill_lds_ncg<HD, KT, PT>()>), \
-                       grid(prefill_lds_ncg<HD, KT, PT>()), dim3(256), 0, st, a)
+    hipLaunchKernelGGL((attn_prefill_lds<HD, KT, PT, NBUF, prefill_lds_ncg<HD, KT, PT>(), NW>), \
+                       grid(prefill_lds_ncg<HD, KT, PT>(), NW), dim3(64 * NW), 0, st, a)
     switch (a.L.page_tokens) {
     case 16:
         GI_PFL(16);
