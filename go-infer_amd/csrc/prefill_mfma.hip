@@ -436,9 +436,13 @@ struct StageRegs {
     // V columns of 4 elements, fp16 of 8, int8 K rows / V columns of 16
     // elements, or q4_0 K rows of 32 nibbles (one quantisation block) / V
     // byte rows of 16 tokens (two dimensions each).
+    // The chunks of K (and as many of V) are spread over ST threads, the
+    // first ST of the workgroup; the others stage nothing.
     static constexpr bool QUANT = KT == KV_Q8_0 || KT == KV_Q4_0;
-    static constexpr int NC = (KT == KV_F32 ? HD / 16 : KT == KV_F16 ? HD / 32 : KT == KV_Q8_0 ? HD / 64 : HD / 128) * 4 / NW;
-    static_assert(NC >= 1, "too few chunks per thread (q4_0 staging needs head_dim 128 and 4 waves)");
+    static constexpr int CH = kTB * HD / (KT == KV_F32 ? 4 : KT == KV_F16 ? 8 : KT == KV_Q8_0 ? 16 : 32);
+    static constexpr int ST = CH < 64 * NW ? CH : 64 * NW;
+    static constexpr int NC = CH / ST;
+    static_assert(ST % 64 == 0 && NC * ST == CH, "whole waves stage whole blocks");
     u4 k[NC], v[NC];
     int64_t kpage[QUANT ? NC : 1]; // quantised pages: page of each chunk (wave-uniform)
     int64_t vpage[QUANT ? NC : 1];
@@ -508,7 +512,9 @@ template <int HD, int KT, int P, int NW>
 __device__ __forceinline__ void stage_load(const PrefillArgs &a, int kvh, int tid, int w, int tb,
                                            StageRegs<HD, KT, NW> &R)
 {
-    constexpr int NT = 64 * NW;
+    constexpr int NT = StageRegs<HD, KT, NW>::ST;
+    if (NT < 64 * NW && tid >= NT) // wave-uniform
+        return;
     using M = ChunkMap<HD, KT, P>;
     const PoolLayout &L = a.L;
     const int64_t np = L.num_pages;
@@ -633,7 +639,9 @@ __device__ __forceinline__ void stage_store(const PrefillArgs &a, int kvh, int t
     // than with the chunk so that they hold no registers through the block's
     // compute (they are shared by many chunks and come from the caches).
     typedef StageRegs<HD, KT, NW> SR;
-    constexpr int NT = 64 * NW;
+    constexpr int NT = SR::ST;
+    if (NT < 64 * NW && tid >= NT) // wave-uniform
+        return;
     constexpr int NCS = SR::QUANT ? SR::NC : 1;
     u4 vs[2 * NCS];
     _Float16 ks[NCS];
@@ -1377,12 +1385,12 @@ constexpr int prefill_ncg()
 
 // LDS buffers of the staged kernel: two (one barrier per block) for fp16
 // pages.  Quantised pages stage K and V as hi/lo planes (64 KiB a block at
-// head_dim 128): q8_0 at head_dim 128 runs one workgroup of 8 waves per CU
-// over two buffers (128 KiB); the other quantised shapes (fewer 16-byte
-// chunks per block than 512 threads) one 4-wave workgroup over one buffer.
+// head_dim 128): there one workgroup of 8 waves per CU runs over two buffers
+// (130 KiB; q4_0 blocks have 256 chunks, so only 4 of the waves stage);
+// head_dim 64 keeps 4-wave workgroups over one buffer.
 constexpr int kPrefillNbufF16 = 2;
 template <int HD, int KT>
-constexpr int kPrefillWaves = KT == KV_Q8_0 && HD == 128 ? 8 : 4;
+constexpr int kPrefillWaves = (KT == KV_Q8_0 || KT == KV_Q4_0) && HD == 128 ? 8 : 4;
 template <int HD, int KT>
 constexpr int kPrefillNbufQ = kPrefillWaves<HD, KT> == 8 ? 2 : 1;
 // f32 pages: one buffer (their block maxima are exchanged at its barrier).
