@@ -437,10 +437,13 @@ struct StageRegs {
     // elements, or q4_0 K rows of 32 nibbles (one quantisation block) / V
     // byte rows of 16 tokens (two dimensions each).
     // The chunks of K (and as many of V) are spread over ST threads, the
-    // first ST of the workgroup; the others stage nothing.
+    // first ST of the workgroup (at most four waves); the others stage
+    // nothing.  With 8 waves, four staging q8_0 blocks at two chunks each
+    // measured 381 against 369 TFLOP/s for all eight at one (two staging
+    // waves at four chunks each spill).
     static constexpr bool QUANT = KT == KV_Q8_0 || KT == KV_Q4_0;
     static constexpr int CH = kTB * HD / (KT == KV_F32 ? 4 : KT == KV_F16 ? 8 : KT == KV_Q8_0 ? 16 : 32);
-    static constexpr int ST = CH < 64 * NW ? CH : 64 * NW;
+    static constexpr int ST = CH < 256 ? CH : 256;
     static constexpr int NC = CH / ST;
     static_assert(ST % 64 == 0 && NC * ST == CH, "whole waves stage whole blocks");
     u4 k[NC], v[NC];
@@ -1386,8 +1389,8 @@ constexpr int prefill_ncg()
 // LDS buffers of the staged kernel: two (one barrier per block) for fp16
 // pages.  Quantised pages stage K and V as hi/lo planes (64 KiB a block at
 // head_dim 128): there one workgroup of 8 waves per CU runs over two buffers
-// (130 KiB; q4_0 blocks have 256 chunks, so only 4 of the waves stage);
-// head_dim 64 keeps 4-wave workgroups over one buffer.
+// (130 KiB), four of the waves staging; head_dim 64 keeps 4-wave workgroups
+// over one buffer.
 constexpr int kPrefillNbufF16 = 2;
 template <int HD, int KT>
 constexpr int kPrefillWaves = (KT == KV_Q8_0 || KT == KV_Q4_0) && HD == 128 ? 8 : 4;
