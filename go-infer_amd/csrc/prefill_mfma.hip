@@ -437,13 +437,14 @@ struct StageRegs {
     // elements, or q4_0 K rows of 32 nibbles (one quantisation block) / V
     // byte rows of 16 tokens (two dimensions each).
     // The chunks of K (and as many of V) are spread over ST threads, the
-    // first ST of the workgroup (at most four waves); the others stage
-    // nothing.  With 8 waves, four staging q8_0 blocks at two chunks each
+    // first ST of the workgroup (at most four waves, f32 pages every wave);
+    // the others stage nothing.  With 8 waves, four staging q8_0 blocks at two chunks each
     // measured 381 against 369 TFLOP/s for all eight at one (two staging
     // waves at four chunks each spill).
     static constexpr bool QUANT = KT == KV_Q8_0 || KT == KV_Q4_0;
     static constexpr int CH = kTB * HD / (KT == KV_F32 ? 4 : KT == KV_F16 ? 8 : KT == KV_Q8_0 ? 16 : 32);
-    static constexpr int ST = CH < 256 ? CH : 256;
+    static constexpr int SMAX = KT == KV_F32 ? 64 * NW : 256;
+    static constexpr int ST = CH < SMAX ? CH : SMAX;
     static constexpr int NC = CH / ST;
     static_assert(ST % 64 == 0 && NC * ST == CH, "whole waves stage whole blocks");
     u4 k[NC], v[NC];
@@ -563,16 +564,19 @@ __device__ __forceinline__ void dequant_pair(h8 q, h8 s, h8 &hi, h8 &lo)
 
 // Largest |K| and |V| of this thread's f32 chunks of a staged block, over the
 // live tokens only (stale slots may hold anything).
-template <int HD, int P>
-__device__ __forceinline__ void f32_chunk_max(const StageRegs<HD, KV_F32> &R, int tid, uint64_t vmask, float &mk,
+template <int HD, int P, int NW>
+__device__ __forceinline__ void f32_chunk_max(const StageRegs<HD, KV_F32, NW> &R, int tid, uint64_t vmask, float &mk,
                                               float &mv)
 {
     using M = ChunkMap<HD, KV_F32, P>;
+    constexpr int ST = StageRegs<HD, KV_F32, NW>::ST;
     mk = 0.0f;
     mv = 0.0f;
+    if (ST < 64 * NW && tid >= ST)
+        return;
 #pragma unroll
     for (int c = 0; c < R.NC; c++) {
-        const int ch = tid + 256 * c;
+        const int ch = tid + ST * c;
         const bool klive = (vmask >> M::k_tok(ch)) & 1u;
         const int t0 = M::v_seg(ch) * P + M::v_tok(ch);
 #pragma unroll
@@ -1150,10 +1154,10 @@ template <int HD, int KT, int P, int NBUF, int NCG, int NW>
 __global__ __launch_bounds__(64 * NW) void attn_prefill_lds(PrefillArgs a)
 {
     constexpr bool F32 = KT == KV_F32;
-    static_assert(!F32 || (NBUF == 1 && NW == 4), "f32 pages exchange block maxima at the single-buffer barrier");
+    static_assert(!F32 || NBUF == 1, "f32 pages exchange block maxima at the single-buffer barrier");
     const PrefillWork<P, NCG, NW> W(a);
     __shared__ Lds<HD, KT, NBUF> S;
-    __shared__ float s_bmax[4][2]; // f32 pages: per-wave |K|, |V| maxima of the block being staged
+    __shared__ float s_bmax[NW][2]; // f32 pages: per-wave |K|, |V| maxima of the block being staged
     WaveAttn<HD, KT, NCG> A;
     A.init(a, W.b, W.kvh, W.col0, W.start, W.mapped, W.wave_active, W.j, W.g);
 
@@ -1166,7 +1170,7 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_lds(PrefillArgs a)
     auto f32_scales = [&](uint64_t vmask) {
         if constexpr (F32) {
             float mk, mv;
-            f32_chunk_max<HD, P>(R, W.tid, vmask, mk, mv);
+            f32_chunk_max<HD, P, NW>(R, W.tid, vmask, mk, mv);
             mk = wave_max_nonneg(mk);
             mv = wave_max_nonneg(mv);
             if (W.lane == 0) {
@@ -1174,8 +1178,13 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_lds(PrefillArgs a)
                 s_bmax[W.w][1] = mv;
             }
             __syncthreads();
-            mk = fmaxf(fmaxf(s_bmax[0][0], s_bmax[1][0]), fmaxf(s_bmax[2][0], s_bmax[3][0]));
-            mv = fmaxf(fmaxf(s_bmax[0][1], s_bmax[1][1]), fmaxf(s_bmax[2][1], s_bmax[3][1]));
+            mk = s_bmax[0][0];
+            mv = s_bmax[0][1];
+#pragma unroll
+            for (int x = 1; x < NW; x++) {
+                mk = fmaxf(mk, s_bmax[x][0]);
+                mv = fmaxf(mv, s_bmax[x][1]);
+            }
             ksc_run = block_scale(mk, ksc_run);
             vsc_run = block_scale(mv, vsc_run);
         }
@@ -1390,7 +1399,8 @@ constexpr int prefill_ncg()
 // pages.  Quantised pages stage K and V as hi/lo planes (64 KiB a block at
 // head_dim 128): there one workgroup of 8 waves per CU runs over two buffers
 // (130 KiB), four of the waves staging; head_dim 64 keeps 4-wave workgroups
-// over one buffer.
+// over one buffer.  f32 pages run 8-wave workgroups over one buffer (their
+// block maxima are exchanged at its barrier), every wave staging.
 constexpr int kPrefillNbufF16 = 2;
 template <int HD, int KT>
 constexpr int kPrefillWaves = (KT == KV_Q8_0 || KT == KV_Q4_0) && HD == 128 ? 8 : 4;
@@ -1399,13 +1409,15 @@ constexpr int kPrefillNbufQ = kPrefillWaves<HD, KT> == 8 ? 2 : 1;
 // f32 pages: one buffer (their block maxima are exchanged at its barrier).
 
 // Column groups per wave: two halve the LDS reads per matrix-core product;
-// taken where the kernel then still fits two waves per SIMD (256 VGPRs), and
-// always for f32 pages, whose 64 staging registers leave one wave per SIMD
-// either way (two groups amortise the staging over twice the products).
+// taken where the kernel then still fits two waves per SIMD (256 VGPRs).
+// f32 pages take one: with their staging spread over 8 waves (four 16-byte
+// chunks per thread) the kernel then fits two waves per SIMD (234 VGPRs),
+// where two groups over 4 waves held one (397 VGPRs): 203 against 153
+// TFLOP/s on the Llama-3-8B 4096-token prefill.
 template <int HD, int KT, int P>
 constexpr int prefill_lds_ncg()
 {
-    return KT == KV_F32 ? 2 : (HD == 64 || P == 16 || (KT != KV_F16 && P == 32)) ? 2 : 1;
+    return KT == KV_F32 ? 1 : (HD == 64 || P == 16 || (KT != KV_F16 && P == 32)) ? 2 : 1;
 }
 
 // fp16 pages use the direct global->LDS kernel (no staging registers, so
@@ -1417,7 +1429,7 @@ static void launch_lds(const PrefillArgs &a, hipStream_t st)
 {
     using namespace mfma_prefill;
     constexpr int NBUF = KT == KV_F32 ? 1 : KT == KV_F16 ? kPrefillNbufF16 : kPrefillNbufQ<HD, KT>;
-    constexpr int NW = KT == KV_F32 || KT == KV_F16 ? 4 : kPrefillWaves<HD, KT>;
+    constexpr int NW = KT == KV_F16 ? 4 : KT == KV_F32 ? 8 : kPrefillWaves<HD, KT>;
     const int G = a.num_heads / a.L.num_kv_heads;
     const int64_t cols = (int64_t)a.chunk_len * G;
     auto grid = [&](int ncg, int nw) {
