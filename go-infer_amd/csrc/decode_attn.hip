@@ -383,8 +383,14 @@ hipError_t launch_decode(const DecodeArgs &a, hipStream_t st)
     const int n_q = a.n_q > 0 ? a.n_q : 1;
     hipError_t e;
     if (n_q == 1 && !a.start_pos && decode_kernel_kind(L, a.num_heads, a.kernel) == 1) {
-        e = launch_decode_mfma(a, st);
+        e = launch_decode_mfma(a, st); // stores a decode step's token itself
     } else {
+        if (a.new_k) {
+            e = launch_append_at_len(L, a.append_base, a.batch, a.block_tables, a.max_blocks, a.seq_lens,
+                                     a.new_k, a.new_v, a.status, st);
+            if (e != hipSuccess)
+                return e;
+        }
         dim3 grid(a.num_splits, L.num_kv_heads, a.batch * n_q);
         switch (L.kv_type) {
         case KV_F32: e = launch_valu_kt<KV_F32>(a, grid, st); break;

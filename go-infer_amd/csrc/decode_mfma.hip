@@ -38,6 +38,7 @@
 #include "gi_common.h"
 #include "gi_kernels.h"
 #include "mfma_ops.h"
+#include "token_store.h"
 
 #include <math.h>
 
@@ -1027,6 +1028,32 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
     const int t0 = split * a.split_tokens;
     const int t1 = split == a.num_splits - 1 ? len : min(len, t0 + a.split_tokens);
     const int64_t qrow = (int64_t)b * H + h0;
+
+    // Decode step (gi_paged_decode_step): the workgroup whose token range
+    // holds the new token (position seq_lens[b] - 1) first stores its kv
+    // head's slice of it, as Forward stores before it attends
+    // (forward.go:236-267).  The barrier's workgroup-scope fence makes the
+    // stores visible to every wave's loads; no other workgroup reads that
+    // token (other kv heads are other bytes, and split ranges are whole
+    // pages).  A length the tables cannot hold is flagged, as the separate
+    // append does, and nothing is stored.
+    if (a.new_k) {
+        const int raw = a.seq_lens[b], pos = raw - 1;
+        if (pos < 0 && threadIdx.x == 0 && split == 0 && a.status)
+            atomicOr(a.status, FLAG_BAD_SLOT);
+        if (raw == len && t0 <= pos && pos < t1) {
+            const int64_t pg = a.block_tables[(int64_t)b * a.max_blocks + pos / P];
+            const bool okp = pg >= 0 && pg < L.num_pages;
+            if (!okp && threadIdx.x == 0 && a.status)
+                atomicOr(a.status, FLAG_BAD_PAGE);
+            if (okp && threadIdx.x < HD) {
+                const int64_t e = ((int64_t)b * L.num_kv_heads + kvh) * HD + threadIdx.x;
+                store_token_elem<KT>(L, a.append_base + pg * L.page_bytes, pos % P, kvh, threadIdx.x,
+                                     a.new_k[e], a.new_v[e], true);
+            }
+            __syncthreads();
+        }
+    }
 
     // The per-wave staging areas of the block loop (quantised pages) and,
     // after it, the cross-wave merge share one LDS allocation.  (fp16 pages

@@ -67,6 +67,11 @@ struct DecodeArgs {
     float *ws; // partials when num_splits > 1
     int *status;
     int kernel; // -1 automatic, 0 vector ALU, 1 matrix core
+    // Decode step: the new token's K and V ([batch][kv_dim] float32) to store
+    // at position seq_lens[b] - 1 before attending, as gi_paged_append_at_len
+    // does; null for attention alone.  append_base is base, writable.
+    const float *new_k, *new_v;
+    uint8_t *append_base;
 };
 
 // Bytes of split-K workspace needed for a decode launch.

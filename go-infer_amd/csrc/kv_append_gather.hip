@@ -16,6 +16,7 @@
 // (block_table[t / page_tokens], t % page_tokens) (paged_kv.go:107-131).
 #include "gi_common.h"
 #include "gi_kernels.h"
+#include "token_store.h"
 
 #include <algorithm>
 
@@ -96,31 +97,9 @@ __global__ __launch_bounds__(kThreads) void append_plain(PoolLayout L, uint8_t *
         int *st = j == 0 ? status : nullptr;
         if (!resolve(D, L, i, &page, &s, st))
             continue;
-        int kvh = j / hd;
-        int d = j - kvh * hd;
-        uint8_t *pg = base + page * L.page_bytes;
-        int64_t ki = ((int64_t)kvh * L.page_tokens + s) * hd + d;
-        int64_t vi = ((int64_t)kvh * hd + d) * L.page_tokens + s;
-        float kx = k[e], vx = v[e];
-        if (KT == KV_F32) {
-            reinterpret_cast<float *>(pg + L.k_off)[ki] = kx;
-            reinterpret_cast<float *>(pg + L.v_off)[vi] = vx;
-        } else {
-            reinterpret_cast<uint16_t *>(pg + L.k_off)[ki] = (uint16_t)float_to_half_bits_rtz(kx);
-            reinterpret_cast<uint16_t *>(pg + L.v_off)[vi] = (uint16_t)float_to_half_bits_rtz(vx);
-        }
+        const int kvh = j / hd;
+        store_token_elem<KT>(L, base + page * L.page_bytes, s, kvh, j - kvh * hd, k[e], v[e], true);
     }
-}
-
-// 32-lane maximum of an unsigned key (lanes of one Q8_0 block).
-__device__ __forceinline__ uint32_t max32(uint32_t x)
-{
-#pragma unroll
-    for (int m = 16; m >= 1; m >>= 1) {
-        uint32_t y = (uint32_t)__shfl_xor((int)x, m, 32);
-        x = x > y ? x : y;
-    }
-    return x;
 }
 
 // q8_0 append: 32 consecutive threads quantise one block of 32 elements.
@@ -130,7 +109,6 @@ __global__ __launch_bounds__(kThreads) void append_q8(PoolLayout L, uint8_t *bas
                                                       const float *__restrict__ v, int *status)
 {
     const int hd = L.head_dim;
-    const int nb = hd / 32;
     const int kv_dim = L.num_kv_heads * hd;
     const int64_t total = (int64_t)n_tok * kv_dim; // multiple of 32
     for (int64_t e0 = (int64_t)blockIdx.x * kThreads; e0 < total;
@@ -143,57 +121,12 @@ __global__ __launch_bounds__(kThreads) void append_q8(PoolLayout L, uint8_t *bas
             break;
         int i = (int)(e / kv_dim);
         int j = (int)(e - (int64_t)i * kv_dim);
-        int64_t page;
-        int s;
+        int64_t page = 0;
+        int s = 0;
         int *st = j == 0 ? status : nullptr;
-        bool ok = resolve(D, L, i, &page, &s, st);
-        float kx = k[e], vx = v[e];
-        float kinv, vinv;
-        uint32_t kd = q8_scale(__builtin_bit_cast(float, max32(abs_key(kx))), &kinv);
-        uint32_t vd = q8_scale(__builtin_bit_cast(float, max32(abs_key(vx))), &vinv);
-        if (!ok)
-            continue;
-        int kvh = j / hd;
-        int d = j - kvh * hd;
-        int blk = d >> 5;
-        uint8_t *pg = base + page * L.page_bytes;
-        int64_t ki = ((int64_t)kvh * L.page_tokens + s) * hd + d;
-        int64_t vi = ((int64_t)kvh * hd + d) * L.page_tokens + s;
-        reinterpret_cast<int8_t *>(pg + L.k_off)[ki] = (int8_t)q8_quant(kx, kinv);
-        reinterpret_cast<int8_t *>(pg + L.v_off)[vi] = (int8_t)q8_quant(vx, vinv);
-        if ((d & 31) == 0) {
-            reinterpret_cast<uint16_t *>(pg + L.ks_off)[((int64_t)kvh * L.page_tokens + s) * nb + blk] =
-                (uint16_t)kd;
-            reinterpret_cast<uint16_t *>(pg + L.vs_off)[((int64_t)kvh * nb + blk) * L.page_tokens + s] =
-                (uint16_t)vd;
-        }
-    }
-}
-
-// Q4_0 quantise-and-store of element e of one token vector (slot s of page
-// pg), called by all 32 lanes of the block's lane group: lane j < 16 writes
-// byte j of the K and of the V block (element j low, element j + 16 high,
-// quant.go:504), lane 0 the two fp16 scales.  ok == false only joins the
-// shuffles.
-__device__ __forceinline__ void quant_store_q4(const PoolLayout &L, uint8_t *pg, int s, int e, float kx,
-                                               float vx, bool ok)
-{
-    const int hd = L.head_dim, nb = hd / 32, P = L.page_tokens;
-    float kinv, vinv;
-    uint32_t kd = q4_scale(__builtin_bit_cast(float, max32(abs_key(kx))), &kinv);
-    uint32_t vd = q4_scale(__builtin_bit_cast(float, max32(abs_key(vx))), &vinv);
-    const int kq = q4_quant(kx, kinv), vq = q4_quant(vx, vinv);
-    const int kq_hi = __shfl_down(kq, 16, 32), vq_hi = __shfl_down(vq, 16, 32);
-    if (!ok)
-        return;
-    const int kvh = e / hd, d = e - kvh * hd, blk = d >> 5, j = d & 31;
-    if (j < 16) {
-        pg[L.k_off + (((int64_t)kvh * P + s) * nb + blk) * 16 + j] = (uint8_t)(kq | (kq_hi << 4));
-        pg[L.v_off + (((int64_t)kvh * nb + blk) * 16 + j) * P + s] = (uint8_t)(vq | (vq_hi << 4));
-    }
-    if (j == 0) {
-        reinterpret_cast<uint16_t *>(pg + L.ks_off)[((int64_t)kvh * P + s) * nb + blk] = (uint16_t)kd;
-        reinterpret_cast<uint16_t *>(pg + L.vs_off)[((int64_t)kvh * nb + blk) * P + s] = (uint16_t)vd;
+        const bool ok = resolve(D, L, i, &page, &s, st);
+        const int kvh = j / hd;
+        store_token_elem<KV_Q8_0>(L, base + page * L.page_bytes, s, kvh, j - kvh * hd, k[e], v[e], ok);
     }
 }
 

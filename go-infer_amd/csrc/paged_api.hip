@@ -581,7 +581,7 @@ int gi_paged_gather(gi_paged *h, int layer, const int32_t *block_table, int n_to
 static int decode_locked(gi_paged *h, int layer, int batch, int num_heads, const float *q,
                          float *out, const int32_t *block_tables, int max_blocks,
                          const int32_t *seq_lens, int max_seq_len, float scale, void *fixed_ws = nullptr,
-                         size_t fixed_cap = 0)
+                         size_t fixed_cap = 0, const float *new_k = nullptr, const float *new_v = nullptr)
 {
     gi::DecodeArgs a{};
     a.L = h->L;
@@ -598,6 +598,9 @@ static int decode_locked(gi_paged *h, int layer, int batch, int num_heads, const
     a.scale = scale;
     a.status = h->d_status;
     a.kernel = h->decode_kernel;
+    a.new_k = new_k;
+    a.new_v = new_v;
+    a.append_base = h->layer_base[(size_t)layer];
     // max_seq_len sizes the split plan only (0: the longest sequence the
     // block tables map); the kernels read the lengths on the device and the
     // last split of each sequence runs to its end
@@ -685,11 +688,10 @@ int gi_paged_decode_step(gi_paged *h, int layer, int batch, int num_heads, const
     if (!k || !v)
         return gi::set_error(GI_ERR_BAD_ARG, "gi_paged_decode_step: NULL k or v");
     std::lock_guard<std::mutex> g(h->mu);
-    hipError_t e = gi::launch_append_at_len(h->L, h->layer_base[(size_t)layer], batch, block_tables,
-                                            max_blocks, seq_lens, k, v, h->d_status, h->stream);
-    if (e != hipSuccess)
-        return hip_fail(e, "gi_paged_decode_step: append");
-    return decode_locked(h, layer, batch, num_heads, q, out, block_tables, max_blocks, seq_lens, max_seq_len, scale);
+    // one launch: the matrix-core decode kernels store the token themselves
+    // (the vector path appends first)
+    return decode_locked(h, layer, batch, num_heads, q, out, block_tables, max_blocks, seq_lens, max_seq_len, scale,
+                         nullptr, 0, k, v);
 }
 
 int gi_paged_rope_decode_step(gi_paged *h, int layer, int batch, int num_heads, float *q, const float *k,
