@@ -367,6 +367,20 @@ void decode_plan(const PoolLayout &L, int batch, int num_heads, int max_len, int
     *num_splits = splits;
 }
 
+// Whether a decode step stores its token inside the matrix-core decode
+// launch (DecodeArgs.new_k) rather than in an append launch before it:
+// when the grid is one round of the plan's workgroups per CU.  Measured
+// same-box: batch 32 x U[512, 4096] 2.84 against 2.93 ms per step, 8 x
+// 32768 (page 32) 14.64-14.69 against 14.93-14.97, batch 1 (TinyLlama,
+// one graph) 5,245 against 4,315 tokens/s; but batch 256 x 8192 (four
+// rounds) 42.63-42.96 against 42.09-42.42 ms, the fused launch slower by
+// more than the append launch it saves.
+bool decode_fuses_append(const PoolLayout &L, int batch, int num_splits, int num_cus)
+{
+    const int64_t wgs = (int64_t)batch * L.num_kv_heads * (num_splits > 0 ? num_splits : 1);
+    return wgs <= (int64_t)kDecodeWgPerCu * (num_cus > 0 ? num_cus : 256);
+}
+
 int decode_kernel_kind(const PoolLayout &L, int num_heads, int requested)
 {
     const bool mfma = mfma_decode_supported(L, num_heads);
@@ -385,7 +399,7 @@ hipError_t launch_decode(const DecodeArgs &a, hipStream_t st)
     if (n_q == 1 && !a.start_pos && decode_kernel_kind(L, a.num_heads, a.kernel) == 1) {
         e = launch_decode_mfma(a, st); // stores a decode step's token itself
     } else {
-        if (a.new_k) {
+        if (a.new_k) { // the vector path appends in a launch of its own
             e = launch_append_at_len(L, a.append_base, a.batch, a.block_tables, a.max_blocks, a.seq_lens,
                                      a.new_k, a.new_v, a.status, st);
             if (e != hipSuccess)

@@ -1029,14 +1029,24 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
     const int t1 = split == a.num_splits - 1 ? len : min(len, t0 + a.split_tokens);
     const int64_t qrow = (int64_t)b * H + h0;
 
-    // Decode step (gi_paged_decode_step): the workgroup whose token range
-    // holds the new token (position seq_lens[b] - 1) first stores its kv
-    // head's slice of it, as Forward stores before it attends
-    // (forward.go:236-267).  The barrier's workgroup-scope fence makes the
-    // stores visible to every wave's loads; no other workgroup reads that
-    // token (other kv heads are other bytes, and split ranges are whole
-    // pages).  A length the tables cannot hold is flagged, as the separate
-    // append does, and nothing is stored.
+    // Decode step (gi_paged_decode_step): the new token (position
+    // seq_lens[b] - 1) is stored before it is attended, as Forward stores
+    // before it attends (forward.go:236-267), by the workgroup whose token
+    // range holds it, for its own kv head.  With pages of up to 32 tokens
+    // every cache line of a page belongs to one 32-token block, which one
+    // wave reads (wave w reads blocks t0 + 32w + 128i): that wave stores the
+    // token, after issuing its first block's loads unless that is the
+    // token's block (the stores wait for the loads of the token's values,
+    // which should not hold up the block's loads), and waits for the stores
+    // to complete only before it issues the token's block.  The other waves
+    // never wait.  Wider pages share lines between the blocks of two waves,
+    // so there every thread joins the store and a barrier follows.  No other
+    // workgroup reads that token's bytes (other kv heads are other bytes,
+    // split ranges are whole pages).  A length the tables cannot hold is
+    // flagged, as the separate append does, and nothing is stored.
+    int sblk = -1;          // the token's block, in the wave that stores it
+    int64_t st_page = 0;    // and where the token goes
+    int st_slot = 0;
     if (a.new_k) {
         const int raw = a.seq_lens[b], pos = raw - 1;
         if (pos < 0 && threadIdx.x == 0 && split == 0 && a.status)
@@ -1046,14 +1056,28 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
             const bool okp = pg >= 0 && pg < L.num_pages;
             if (!okp && threadIdx.x == 0 && a.status)
                 atomicOr(a.status, FLAG_BAD_PAGE);
-            if (okp && threadIdx.x < HD) {
+            if (P <= 32) {
+                if (okp && w == ((pos - t0) >> 5) % 4) {
+                    sblk = __builtin_amdgcn_readfirstlane(t0 + ((pos - t0) & ~31));
+                    st_page = pg;
+                    st_slot = pos % P;
+                }
+            } else {
                 const int64_t e = ((int64_t)b * L.num_kv_heads + kvh) * HD + threadIdx.x;
-                store_token_elem<KT>(L, a.append_base + pg * L.page_bytes, pos % P, kvh, threadIdx.x,
-                                     a.new_k[e], a.new_v[e], true);
+                if (okp && threadIdx.x < HD)
+                    store_token_elem<KT>(L, a.append_base + pg * L.page_bytes, pos % P, kvh, threadIdx.x,
+                                         a.new_k[e], a.new_v[e], true);
+                __syncthreads();
             }
-            __syncthreads();
         }
     }
+    auto store_token = [&]() {
+        const int64_t e0 = ((int64_t)b * L.num_kv_heads + kvh) * HD;
+#pragma unroll
+        for (int d = lane; d < HD; d += 64)
+            store_token_elem<KT>(L, a.append_base + st_page * L.page_bytes, st_slot, kvh, d, a.new_k[e0 + d],
+                                 a.new_v[e0 + d], true);
+    };
 
     // The per-wave staging areas of the block loop (quantised pages) and,
     // after it, the cross-wave merge share one LDS allocation.  (fp16 pages
@@ -1184,6 +1208,18 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
     // counters then see one pattern of loads in flight on every path, and a
     // wait for this block's V never waits for the next block's K.
     int base = __builtin_amdgcn_readfirstlane(t0 + 32 * w);
+    // before the loads of block x are issued: the decode step's token stores
+    // of this wave have completed if x holds the token (the memory clobber
+    // keeps the compiler from moving loads or stores across the wait)
+    auto store_done = [&](int x) {
+        if (x == sblk)
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    };
+    // the token's stores: before the first block's loads if that block holds
+    // it, otherwise right after them (store_late)
+    const bool store_late = sblk >= 0 && sblk != base;
+    if (sblk >= 0 && !store_late)
+        store_token();
     if constexpr (QUANT) {
         const int64_t ksoff = L.ks_off + (int64_t)kvh * P * KK * 2;
         const int64_t vsoff = L.vs_off + (int64_t)kvh * KK * P * 2;
@@ -1192,10 +1228,13 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
             int64_t pA, pB;
             int sA, sB;
             int ok;
+            store_done(base);
             block_pages(a, bt, base, t1, pA, pB, sA, sB, ok);
             issue_qk<KT, HD>(a, pA, pB, sA, sB, koff, lane, Sq);
             issue_qv<KT, HD>(a, pA, pB, sA, sB, ksoff, voff, vsoff, lane, Sq);
             load_q();
+            if (store_late)
+                store_token();
             // Loads go out in the order K codes, scales, V codes of one
             // block, K codes of the next, ...: the K half of a block is read
             // (and the next block's K refills its slots) before the scores,
@@ -1214,6 +1253,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
                 int nsA = sA, nsB = sB;
                 int nok = ok;
                 if (more) {
+                    store_done(next);
                     block_pages(a, bt, next, t1, nA, nB, nsA, nsB, nok);
                     // every read of this block's K half has returned before
                     // its slots are refilled
@@ -1251,9 +1291,12 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
             int64_t pA, pB;
             int sA, sB;
             int ok;
+            store_done(base);
             block_pages(a, bt, base, t1, pA, pB, sA, sB, ok);
             issue_f32<HD>(a, pA, pB, sA, sB, koff, voff, fl, Sf);
             load_q();
+            if (store_late)
+                store_token();
             for (;;) {
                 h8 kh0[KK], kh1[KK], kl0[KK], kl1[KK], vh[NB], vl[NB];
                 // the only vector loads in flight are this block's
@@ -1265,6 +1308,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
                 int nsA = sA, nsB = sB;
                 int nok = ok;
                 if (more) {
+                    store_done(next);
                     block_pages(a, bt, next, t1, nA, nB, nsA, nsB, nok);
                     __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0): this block's reads returned
                     issue_f32<HD>(a, nA, nB, nsA, nsB, koff, voff, fl, Sf);
@@ -1299,10 +1343,13 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
         int64_t pA, pB;
         int sA, sB;
         int ok;
+        store_done(base);
         block_pages(a, bt, base, t1, pA, pB, sA, sB, ok);
         load_k<HD, NT>(a, pA, pB, sA, sB, koff, j, g, k0, k1);
         load_v<HD, NT>(a, pA, pB, sA, sB, voff, j, g, v);
         load_q();
+        if (store_late)
+            store_token();
         f4 s0, s1;
         for (;;) {
             qk<HD, GP>(k0, k1, qh, ql, s0, s1);
@@ -1312,6 +1359,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
             int64_t nA, nB;
             int nsA, nsB;
             int nok;
+            store_done(next);
             block_pages(a, bt, next, t1, nA, nB, nsA, nsB, nok);
             if (PREFETCH)
                 load_k<HD, NT>(a, nA, nB, nsA, nsB, koff, j, g, k0, k1);

@@ -77,6 +77,10 @@ struct DecodeArgs {
 // Bytes of split-K workspace needed for a decode launch.
 size_t decode_workspace_bytes(const PoolLayout &L, int batch, int num_heads, int num_splits);
 
+// Whether a decode step's token store goes into the matrix-core decode
+// launch (DecodeArgs.new_k) for this grid, rather than an append launch.
+bool decode_fuses_append(const PoolLayout &L, int batch, int num_splits, int num_cus);
+
 // Picks (split_tokens, num_splits) for a batch whose longest sequence has
 // max_len tokens, so the grid fills the device.
 void decode_plan(const PoolLayout &L, int batch, int num_heads, int max_len, int num_cus,

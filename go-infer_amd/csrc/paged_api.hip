@@ -598,8 +598,6 @@ static int decode_locked(gi_paged *h, int layer, int batch, int num_heads, const
     a.scale = scale;
     a.status = h->d_status;
     a.kernel = h->decode_kernel;
-    a.new_k = new_k;
-    a.new_v = new_v;
     a.append_base = h->layer_base[(size_t)layer];
     // max_seq_len sizes the split plan only (0: the longest sequence the
     // block tables map); the kernels read the lengths on the device and the
@@ -608,6 +606,19 @@ static int decode_locked(gi_paged *h, int layer, int batch, int num_heads, const
     const int max_len = (int)(max_seq_len > 0 && max_seq_len < mapped ? max_seq_len
                               : mapped < INT32_MAX ? mapped : INT32_MAX);
     gi::decode_plan(h->L, batch, num_heads, max_len, h->num_cus, &a.split_tokens, &a.num_splits);
+    if (new_k) {
+        // a decode step: the token goes into the decode launch where that
+        // pays (one round of workgroups), else into an append launch first
+        if (gi::decode_fuses_append(h->L, batch, a.num_splits, h->num_cus)) {
+            a.new_k = new_k;
+            a.new_v = new_v;
+        } else {
+            const hipError_t e = gi::launch_append_at_len(h->L, a.append_base, batch, block_tables, max_blocks,
+                                                          seq_lens, new_k, new_v, h->d_status, h->stream);
+            if (e != hipSuccess)
+                return hip_fail(e, "decode step: append");
+        }
+    }
     const size_t need = gi::decode_workspace_bytes(h->L, batch, num_heads, a.num_splits);
     if (fixed_ws) {
         if (need > fixed_cap)
@@ -688,8 +699,8 @@ int gi_paged_decode_step(gi_paged *h, int layer, int batch, int num_heads, const
     if (!k || !v)
         return gi::set_error(GI_ERR_BAD_ARG, "gi_paged_decode_step: NULL k or v");
     std::lock_guard<std::mutex> g(h->mu);
-    // one launch: the matrix-core decode kernels store the token themselves
-    // (the vector path appends first)
+    // the token is stored inside the decode launch, or by an append launch
+    // before it (decode_fuses_append)
     return decode_locked(h, layer, batch, num_heads, q, out, block_tables, max_blocks, seq_lens, max_seq_len, scale,
                          nullptr, 0, k, v);
 }

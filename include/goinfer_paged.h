@@ -292,7 +292,10 @@ int gi_paged_decode_attention_noalloc(gi_paged *h, int layer, int batch, int num
 
 /* One decode step of one layer: gi_paged_append_at_len of k/v, then
  * gi_paged_decode_attention over seq_lens[b] tokens (the new token
- * included), as Forward stores then attends (forward.go:236-267). */
+ * included), as Forward stores then attends (forward.go:236-267).  Where the
+ * decode grid is one round of workgroups (small batches), the matrix-core
+ * kernels store the token themselves in the same launch; the stored bytes
+ * and the outputs are those of the two calls. */
 int gi_paged_decode_step(gi_paged *h, int layer, int batch, int num_heads, const float *q,
                          const float *k, const float *v, float *out, const int32_t *block_tables,
                          int max_blocks, const int32_t *seq_lens, int max_seq_len, float scale);
