@@ -40,6 +40,25 @@ using mfma_ops::u4x8_to_h8;
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+__device__ __forceinline__ float maxnum(float a, float b) { return __builtin_elementwise_maximumnum(a, b); }
+__device__ __forceinline__ float maxnum3(float a, float b, float c) { return maxnum(maxnum(a, b), c); }
+// Maximum over lanes l, l ^ 16 and l ^ 32 partners, as mfma_ops::max_xor16 /
+// max_xor32, with maximumNumber.
+__device__ __forceinline__ float max_xor16n(float x)
+{
+    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+                                                    false, false);
+    const uint32_t r0 = r[0], r1 = r[1];
+    return maxnum(__builtin_bit_cast(float, r0), __builtin_bit_cast(float, r1));
+}
+__device__ __forceinline__ float max_xor32n(float x)
+{
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+                                                    false, false);
+    const uint32_t r0 = r[0], r1 = r[1];
+    return maxnum(__builtin_bit_cast(float, r0), __builtin_bit_cast(float, r1));
+}
+
 __device__ __forceinline__ f4 mfma(h8 a, h8 b, f4 c)
 {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
@@ -776,6 +795,123 @@ __device__ __forceinline__ void stage_store(const PrefillArgs &a, int kvh, int t
     }
 }
 
+// One plane (K or V) of a quantised block staged by the NT = 256 threads of
+// one wave group: its chunks (ChunkMap; q8_0 two per thread, q4_0 one) and
+// their pages (wave-uniform: a wave's chunks share one page).
+template <int HD, int KT>
+struct PlaneRegs {
+    static constexpr int NT = 256;
+    static constexpr int CH = kTB * HD / (KT == KV_Q8_0 ? 16 : 32);
+    static constexpr int NC = CH / NT;
+    static_assert(NC * NT == CH, "whole chunks per thread");
+    u4 x[NC];
+    int64_t page[NC];
+};
+
+// Loads the K (PLANE 0) or V (PLANE 1) chunks of thread st (0..255) of the
+// block whose page ids are in tb (lane l: token l).
+template <int PLANE, int HD, int KT, int P>
+__device__ __forceinline__ void plane_load(const PrefillArgs &a, int kvh, int st, int tb, PlaneRegs<HD, KT> &R)
+{
+    using M = ChunkMap<HD, KT, P>;
+    constexpr int NT = PlaneRegs<HD, KT>::NT;
+    const PoolLayout &L = a.L;
+    const int64_t np = L.num_pages;
+    auto page = [&](int tok) -> int64_t { // wave-uniform
+        const int pg = __builtin_amdgcn_readlane(tb, tok);
+        return (pg >= 0 && pg < np) ? pg : 0;
+    };
+    constexpr int RB = KT == KV_Q4_0 ? HD / 2 : HD; // bytes of a K row / V code rows of a head
+#pragma unroll
+    for (int c = 0; c < R.NC; c++) {
+        const int ch = st + NT * c, ch0 = 64 * (st >> 6) + NT * c;
+        if (PLANE == 0) {
+            R.page[c] = page(M::k_tok(ch0));
+            const uint8_t *kp = a.base + R.page[c] * L.page_bytes + L.k_off;
+            R.x[c] = *reinterpret_cast<const u4 *>(kp + ((int64_t)kvh * P + M::k_tok(ch) % P) * RB +
+                                                   M::k_col(ch) / (KT == KV_Q4_0 ? 2 : 1));
+        } else {
+            R.page[c] = page(M::v_seg(ch0) * P);
+            const uint8_t *vp = a.base + R.page[c] * L.page_bytes + L.v_off;
+            R.x[c] = *reinterpret_cast<const u4 *>(vp + ((int64_t)kvh * (KT == KV_Q4_0 ? HD / 2 : HD) + M::v_dim(ch)) * P +
+                                                   M::v_tok(ch));
+        }
+    }
+}
+
+// Dequantises the chunks of plane_load into exact hi + lo fp16 planes of
+// buffer `buf` (the layout stage_store writes); V of tokens whose `vmask`
+// bit is clear is stored as zero.
+template <int PLANE, int HD, int KT, int P, int NBUF>
+__device__ __forceinline__ void plane_store(const PrefillArgs &a, int kvh, int st, int buf, uint64_t vmask,
+                                            const PlaneRegs<HD, KT> &R, Lds<HD, KT, NBUF> &S)
+{
+    using M = ChunkMap<HD, KT, P>;
+    using G = SwzGeom<HD>;
+    constexpr int NT = PlaneRegs<HD, KT>::NT;
+    const PoolLayout &L = a.L;
+#pragma unroll
+    for (int c = 0; c < R.NC; c++) {
+        const int ch = st + NT * c;
+        if (PLANE == 0) {
+            const int tk = M::k_tok(ch), col = M::k_col(ch);
+            const h8 ksp = reinterpret_cast<const _Float16 *>(a.base + R.page[c] * L.page_bytes + L.ks_off)
+                [((int64_t)kvh * P + tk % P) * (HD / 32) + col / 32]; // splat
+            if (KT == KV_Q4_0) {
+                // the chunk is one block: low nibbles are dimensions col ..
+                // col + 15, high nibbles col + 16 .. col + 31
+#pragma unroll
+                for (int m = 0; m < 4; m++) {
+                    h8 hi, lo;
+                    const u2 w = u2{R.x[c][2 * (m & 1)], R.x[c][2 * (m & 1) + 1]};
+                    dequant_pair(u4x8_to_h8(w, 4 * (m >> 1)), ksp, hi, lo);
+                    *reinterpret_cast<h8 *>(&S.k[buf][G::kel(tk, col + 8 * m)]) = hi;
+                    *reinterpret_cast<h8 *>(&S.kl[buf][G::kel(tk, col + 8 * m)]) = lo;
+                }
+            } else {
+#pragma unroll
+                for (int half = 0; half < 2; half++) {
+                    h8 hi, lo;
+                    dequant_pair(i8x8_to_h8(u2{R.x[c][2 * half], R.x[c][2 * half + 1]}), ksp, hi, lo);
+                    *reinterpret_cast<h8 *>(&S.k[buf][G::kel(tk, col + 8 * half)]) = hi;
+                    *reinterpret_cast<h8 *>(&S.kl[buf][G::kel(tk, col + 8 * half)]) = lo;
+                }
+            }
+        } else {
+            const int d = M::v_dim(ch), t0 = M::v_seg(ch) * P + M::v_tok(ch); // block-local token
+            const uint32_t live = (uint32_t)(vmask >> t0) & 0xFFFFu;
+            const u4 *sp = reinterpret_cast<const u4 *>(
+                a.base + R.page[c] * L.page_bytes + L.vs_off +
+                (((int64_t)kvh * (HD / 32) + d / (KT == KV_Q4_0 ? 16 : 32)) * P + M::v_tok(ch)) * 2);
+            const u4 vs[2] = {sp[0], sp[1]};
+            // q4_0: byte row d = 16 db + r holds dimension 32 db + r (low
+            // nibble) and 32 db + 16 + r (high nibble) of 16 tokens
+            const int dl = KT == KV_Q4_0 ? 32 * (d >> 4) + (d & 15) : d;
+#pragma unroll
+            for (int half = 0; half < 2; half++) {
+                const u2 w = u2{R.x[c][2 * half], R.x[c][2 * half + 1]};
+                const uint32_t lv = live >> (8 * half);
+#pragma unroll
+                for (int nib = 0; nib < (KT == KV_Q4_0 ? 2 : 1); nib++) {
+                    h8 hi, lo;
+                    dequant_pair(KT == KV_Q4_0 ? u4x8_to_h8(w, 4 * nib) : i8x8_to_h8(w),
+                                 __builtin_bit_cast(h8, vs[half]), hi, lo);
+                    if ((lv & 0xFFu) != 0xFFu) {
+#pragma unroll
+                        for (int i = 0; i < 8; i++)
+                            if (!((lv >> i) & 1u)) {
+                                hi[i] = (_Float16)0.0f;
+                                lo[i] = (_Float16)0.0f;
+                            }
+                    }
+                    *reinterpret_cast<h8 *>(&S.v[buf][G::vel(dl + 16 * nib, t0 + 8 * half)]) = hi;
+                    *reinterpret_cast<h8 *>(&S.vl[buf][G::vel(dl + 16 * nib, t0 + 8 * half)]) = lo;
+                }
+            }
+        }
+    }
+}
+
 // MFMA operand addresses.  A lane's K operand of tile (h, t) and k-step kk
 // is row 32h + 8(j/4) + j%4 + 4t, 16-byte chunk 4kk + g; its V operand of
 // half h and output tile nb is dimension 16nb + j, chunk 4h + g.  Each
@@ -848,6 +984,23 @@ __device__ constexpr int v_const(const LdsDirect<HD> *, int nb)
 __device__ __forceinline__ h8 ld_frag(const uint8_t *p, int off)
 {
     return *reinterpret_cast<const h8 *>(p + off);
+}
+
+// Schedule of a run of NF operand steps, each R reads from LDS feeding M
+// products: the reads of the first RA steps, then for each step the reads RA
+// steps ahead followed by its products, so that a read has RA steps of
+// products to land (the scheduler would otherwise sink every read next to
+// its products and wait out the LDS latency each time).
+template <int NF, int M, int R, int RA>
+__device__ __forceinline__ void read_ahead_order()
+{
+    __builtin_amdgcn_sched_group_barrier(0x100, RA * R, 0);
+#pragma unroll
+    for (int f = 0; f < NF; f++) {
+        if (f + RA < NF)
+            __builtin_amdgcn_sched_group_barrier(0x100, R, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, M, 0);
+    }
 }
 
 // Per-wave attention state over NCG column groups of 16 (query, head)
@@ -933,11 +1086,14 @@ struct WaveAttn {
                     sv[i] = -INFINITY;
             }
         }
-        float mx = sv[0];
+        // maximumNumber (IEEE 754-2019) compiles to v_max3_f32 with no
+        // canonicalising moves of the product results that fmaxf needs
+        float m3[5];
 #pragma unroll
-        for (int i = 1; i < 16; i++)
-            mx = fmaxf(mx, sv[i]);
-        mx = mfma_ops::max_xor32(mfma_ops::max_xor16(mx));
+        for (int i = 0; i < 5; i++)
+            m3[i] = maxnum3(sv[3 * i], sv[3 * i + 1], sv[3 * i + 2]);
+        float mx = maxnum3(maxnum3(m3[0], m3[1], m3[2]), maxnum3(m3[3], m3[4], sv[15]), sv[15]);
+        mx = max_xor32n(max_xor16n(mx));
         mx *= c2s[cg] * kinv;
         const bool grow = mx > m2[cg] + kLazy;
         const float mref = grow ? mx : m2[cg];
@@ -1058,6 +1214,121 @@ struct WaveAttn {
         }
         if (PRIO)
             __builtin_amdgcn_s_setprio(0);
+    }
+
+    // ---- the three stages of block(), for the ping-pong kernels ----
+    // The operand fragments are read from LDS RA steps ahead of their
+    // products, so that the products of one group of waves run back to back
+    // while the other group is on the vector ALU.  fp16 pages take two
+    // products per operand pair, staged quantised pages three (hi x hi,
+    // lo x hi, hi x lo).
+    static constexpr bool LOP = KT != KV_F16;      // lo planes of K and V
+    static constexpr int NPR = LOP ? 3 : 2;        // products per pair
+    static constexpr int NRD = LOP ? 2 : 1;        // fragment reads per step
+    static constexpr int RA = LOP ? 1 : 2;         // steps read ahead
+
+    // Score tiles of the block in K buffer kb.
+    template <class LDS>
+    __device__ __forceinline__ void qk_block(const LDS &S, int kb, f4 (&s)[NCG][2][2], int j, int g) const
+    {
+        const uint8_t *kp = k_lane(S, kb, j, g, false);
+        const uint8_t *klp = LOP ? k_lane(S, kb, j, g, true) : kp;
+        constexpr int NF = 4 * KK; // steps: (h, t, kk), kk fastest
+        auto off = [&](int f) { return k_const(&S, f / (2 * KK), (f / KK) % 2, f % KK); };
+        h8 kh[RA + 1], kl[RA + 1];
+#pragma unroll
+        for (int f = 0; f < RA; f++) {
+            kh[f] = ld_frag(kp, off(f));
+            if (LOP)
+                kl[f] = ld_frag(klp, off(f));
+        }
+#pragma unroll
+        for (int f = 0; f < NF; f++) {
+            const int h = f / (2 * KK), t = (f / KK) % 2, kk = f % KK;
+            if (f + RA < NF) {
+                kh[(f + RA) % (RA + 1)] = ld_frag(kp, off(f + RA));
+                if (LOP)
+                    kl[(f + RA) % (RA + 1)] = ld_frag(klp, off(f + RA));
+            }
+            const h8 ka = kh[f % (RA + 1)];
+            if (kk == 0)
+#pragma unroll
+                for (int cg = 0; cg < NCG; cg++)
+                    s[cg][h][t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int cg = 0; cg < NCG; cg++) {
+                s[cg][h][t] = mfma(ka, qh[cg][kk], s[cg][h][t]);
+                s[cg][h][t] = mfma(ka, ql[cg][kk], s[cg][h][t]);
+                if (LOP)
+                    s[cg][h][t] = mfma(kl[f % (RA + 1)], qh[cg][kk], s[cg][h][t]);
+            }
+        }
+        read_ahead_order<NF, NPR * NCG, NRD, RA>();
+    }
+
+    // Online softmax of the block at `base`: the scores in st are replaced by
+    // P in place (st[cg][h][0] holds the hi halves of P half h, st[cg][h][1]
+    // the lo halves), so that one register array carries a block between
+    // the stages; O is rescaled where a column's reference maximum grew.
+    template <bool FULL>
+    __device__ __forceinline__ void softmax_block(f4 (&st)[NCG][2][2], int base, uint64_t mask, int g)
+    {
+        float alpha[NCG];
+        bool grow = false;
+#pragma unroll
+        for (int cg = 0; cg < NCG; cg++) {
+            float sv[16];
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+#pragma unroll
+                for (int t = 0; t < 2; t++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        sv[8 * h + 4 * t + r] = st[cg][h][t][r];
+            h8 ph0, pl0, ph1, pl1;
+            grow |= softmax16<FULL>(cg, sv, base, mask, ph0, pl0, ph1, pl1, alpha[cg], g);
+            st[cg][0][0] = __builtin_bit_cast(f4, ph0);
+            st[cg][0][1] = __builtin_bit_cast(f4, pl0);
+            st[cg][1][0] = __builtin_bit_cast(f4, ph1);
+            st[cg][1][1] = __builtin_bit_cast(f4, pl1);
+        }
+        if (grow)
+            rescale(alpha, g);
+    }
+
+    // O += P V over the block in V buffer vb, P as softmax_block left it.
+    template <class LDS>
+    __device__ __forceinline__ void pv_block(const LDS &S, int vb, const f4 (&st)[NCG][2][2], int j, int g)
+    {
+        const uint8_t *vp[2] = {v_lane(S, vb, 0, j, g, false), v_lane(S, vb, 1, j, g, false)};
+        const uint8_t *vlp[2] = {LOP ? v_lane(S, vb, 0, j, g, true) : vp[0], LOP ? v_lane(S, vb, 1, j, g, true) : vp[1]};
+        constexpr int NF = 2 * NB; // steps: (h, nb), nb fastest
+        h8 vh[RA + 1], vl[RA + 1];
+#pragma unroll
+        for (int f = 0; f < RA; f++) {
+            vh[f] = ld_frag(vp[f / NB], v_const(&S, f % NB));
+            if (LOP)
+                vl[f] = ld_frag(vlp[f / NB], v_const(&S, f % NB));
+        }
+#pragma unroll
+        for (int f = 0; f < NF; f++) {
+            const int h = f / NB, nb = f % NB;
+            if (f + RA < NF) {
+                vh[(f + RA) % (RA + 1)] = ld_frag(vp[(f + RA) / NB], v_const(&S, (f + RA) % NB));
+                if (LOP)
+                    vl[(f + RA) % (RA + 1)] = ld_frag(vlp[(f + RA) / NB], v_const(&S, (f + RA) % NB));
+            }
+            const h8 vv = vh[f % (RA + 1)];
+#pragma unroll
+            for (int cg = 0; cg < NCG; cg++) {
+                const h8 phh = __builtin_bit_cast(h8, st[cg][h][0]);
+                o[cg][nb] = mfma(phh, vv, o[cg][nb]);
+                o[cg][nb] = mfma(__builtin_bit_cast(h8, st[cg][h][1]), vv, o[cg][nb]);
+                if (LOP)
+                    o[cg][nb] = mfma(phh, vl[f % (RA + 1)], o[cg][nb]);
+            }
+        }
+        read_ahead_order<NF, NPR * NCG, NRD, RA>();
     }
 
     // O of every column times f (an exact power of two).
@@ -1254,16 +1525,19 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_lds(PrefillArgs a)
 // K: 1 KiB segments of 512/HD tokens (one page each); V: segments of 8
 // dimensions x 64 tokens, where lane l always fetches logical chunk
 // (l & 7) ^ ((l >> 3) & 7), i.e. the same 8 tokens of every segment.
-template <int HD, int P>
-__device__ __forceinline__ void issue_direct(const PrefillArgs &a, int kvh, int w, int lane, int tb,
-                                             LdsDirect<HD> &S, int buf)
+// issue_k and issue_v are its two halves; NW waves share them (HD / (8 NW)
+// loads per wave each).
+template <int HD, int P, int NW = 4>
+__device__ __forceinline__ void issue_k(const PrefillArgs &a, int kvh, int w, int lane, int tb, LdsDirect<HD> &S,
+                                        int buf)
 {
     const PoolLayout &L = a.L;
     const int64_t np = L.num_pages;
-    constexpr int KROWS = LdsDirect<HD>::KROWS, KSEG = kTB / KROWS, VSEG = HD / 8;
+    constexpr int KROWS = LdsDirect<HD>::KROWS, KSEG = kTB / KROWS;
+    static_assert(KSEG % NW == 0, "whole K segments per wave");
 #pragma unroll
-    for (int q = 0; q < KSEG / 4; q++) {
-        const int seg = 4 * q + w;
+    for (int q = 0; q < KSEG / NW; q++) {
+        const int seg = NW * q + w;
         const int row = seg * KROWS + lane / (HD / 8);
         const int c = (lane % (HD / 8)) ^ (row & 3);
         const int pr = __builtin_amdgcn_readlane(tb, seg * KROWS);
@@ -1273,13 +1547,23 @@ __device__ __forceinline__ void issue_direct(const PrefillArgs &a, int kvh, int 
         __builtin_amdgcn_global_load_lds(
             src, (__attribute__((address_space(3))) void *)&S.k[buf][seg * LdsDirect<HD>::KSEGB], 16, 0, 0);
     }
+}
+
+template <int HD, int P, int NW = 4>
+__device__ __forceinline__ void issue_v(const PrefillArgs &a, int kvh, int w, int lane, int tb, LdsDirect<HD> &S,
+                                        int buf)
+{
+    const PoolLayout &L = a.L;
+    const int64_t np = L.num_pages;
+    constexpr int VSEG = HD / 8;
+    static_assert(VSEG % NW == 0, "whole V segments per wave");
     const int vtok = 8 * ((lane & 7) ^ ((lane >> 3) & 7));
     const int vr = __shfl(tb, vtok);
     const int64_t vpg = (vr >= 0 && vr < np) ? vr : 0;
     const uint8_t *vsrc = a.base + vpg * L.page_bytes + L.v_off + (int64_t)(vtok % P) * 2;
 #pragma unroll
-    for (int q = 0; q < VSEG / 4; q++) {
-        const int seg = 4 * q + w;
+    for (int q = 0; q < VSEG / NW; q++) {
+        const int seg = NW * q + w;
         const int d = 8 * seg + (lane >> 3);
         __builtin_amdgcn_global_load_lds(vsrc + ((int64_t)kvh * HD + d) * P * 2,
                                          (__attribute__((address_space(3))) void *)&S.v[buf][seg * 8 * kTB],
@@ -1287,13 +1571,21 @@ __device__ __forceinline__ void issue_direct(const PrefillArgs &a, int kvh, int 
     }
 }
 
+template <int HD, int P>
+__device__ __forceinline__ void issue_direct(const PrefillArgs &a, int kvh, int w, int lane, int tb,
+                                             LdsDirect<HD> &S, int buf)
+{
+    issue_k<HD, P>(a, kvh, w, lane, tb, S, buf);
+    issue_v<HD, P>(a, kvh, w, lane, tb, S, buf);
+}
+
 // Zeroes V of the tokens whose `vmask` bit is clear (past the cached range or
 // on an invalid page) after a direct load; their scores are masked, and stale
 // values must not reach O through 0 * NaN.
-template <int HD>
+template <int HD, int NT = 256>
 __device__ __forceinline__ void zero_dead_v(LdsDirect<HD> &S, int buf, uint64_t vmask, int tid)
 {
-    for (int e = tid; e < HD * (kTB / 8); e += 256) {
+    for (int e = tid; e < HD * (kTB / 8); e += NT) {
         const int d = e / (kTB / 8), c = e % (kTB / 8);
         const uint32_t live = (uint32_t)(vmask >> (8 * c)) & 0xFFu;
         if (live == 0xFFu)
@@ -1363,6 +1655,238 @@ __global__ __launch_bounds__(256) void attn_prefill_dlds(PrefillArgs a)
         step(std::true_type{});
     while (base < W.wg_len)
         step(std::false_type{});
+    if (W.wave_active)
+        A.finish(a, W.b, W.kvh, W.col0, W.j, W.g);
+}
+
+// fp16 pages, two waves per SIMD in ping-pong.  The workgroup's 8 waves form
+// two groups, A (waves 0-3) and B (waves 4-7), one wave of each per SIMD,
+// offset by half a block: while one group issues its matrix-core products
+// (P V of one block and Q K^T of the next, back to back, at raised wave
+// priority) the other runs the online softmax between them on the vector
+// ALU, and the roles swap at each barrier.  Per block n:
+//   phase 1: A: P V (n - 1), scores (n)      B: softmax (n)
+//   phase 2: A: softmax (n)                  B: P V (n), scores (n + 1)
+// K and V have two LDS buffers each, filled by direct global->LDS loads that
+// all 8 waves issue at the start of phase 2 (K of block n + 2, V of block
+// n + 1) and wait for at the end of the next phase 1.  Each group runs its
+// own copy of the loop (pp_loop<GB>), so that neither carries the other's
+// live values; both pass the same barriers.
+template <int HD, int P, int NCG>
+struct PingPong {
+    static constexpr int NW = 8;
+    const PrefillArgs &a;
+    const PrefillWork<P, NCG, NW> &W;
+    LdsDirect<HD> &S;
+    WaveAttn<HD, KV_F16, NCG> &A;
+
+    // whether this wave computes on the block at `base`
+    __device__ __forceinline__ bool live(int base) const { return W.wave_active && base < W.wave_len; }
+
+    template <bool GB>
+    __device__ __forceinline__ void run(int tbv, int tbk, uint64_t mask_c, uint64_t mask_n, int nblk)
+    {
+        f4 s[NCG][2][2]; // a block's scores, then its P (softmax_block)
+        if (GB && live(0))
+            A.qk_block(S, 0, s, W.j, W.g);
+        int n = 0;
+        auto step = [&](auto full) {
+            constexpr bool FULL = decltype(full)::value;
+            const int base = n * kTB, cur = n & 1;
+            // phase 1
+            if (!GB) {
+                __builtin_amdgcn_s_setprio(1);
+                if (n > 0 && live(base - kTB))
+                    A.pv_block(S, cur ^ 1, s, W.j, W.g);
+                if (live(base))
+                    A.qk_block(S, cur, s, W.j, W.g);
+                __builtin_amdgcn_s_setprio(0);
+            } else if (live(base)) {
+                A.template softmax_block<FULL>(s, base, mask_c, W.g);
+            }
+            wait_direct_loads(); // K of block n + 1 and V of block n
+            __syncthreads();
+            if (mask_c != ~0ull) { // V of block n has tokens to zero
+                zero_dead_v<HD, 64 * NW>(S, cur, mask_c, W.tid);
+                __syncthreads();
+            }
+            // phase 2
+            issue_k<HD, P, NW>(a, W.kvh, W.w, W.lane, tbk, S, cur);     // block n + 2
+            issue_v<HD, P, NW>(a, W.kvh, W.w, W.lane, tbv, S, cur ^ 1); // block n + 1
+            const uint64_t mask_nn = W.valid_mask(a, tbk, base + 2 * kTB);
+            tbv = tbk;
+            tbk = W.table(base + 3 * kTB);
+            if (!GB) {
+                if (live(base))
+                    A.template softmax_block<FULL>(s, base, mask_c, W.g);
+            } else {
+                __builtin_amdgcn_s_setprio(1);
+                if (live(base))
+                    A.pv_block(S, cur, s, W.j, W.g);
+                if (live(base + kTB))
+                    A.qk_block(S, cur ^ 1, s, W.j, W.g);
+                __builtin_amdgcn_s_setprio(0);
+            }
+            __syncthreads();
+            mask_c = mask_n;
+            mask_n = mask_nn;
+            n++;
+        };
+        while (n < nblk && W.block_full(n * kTB, mask_c))
+            step(std::true_type{});
+        while (n < nblk)
+            step(std::false_type{});
+        if (!GB && nblk > 0 && live((nblk - 1) * kTB))
+            A.pv_block(S, (nblk - 1) & 1, s, W.j, W.g);
+    }
+};
+
+template <int HD, int P, int NCG>
+__global__ __launch_bounds__(512) void attn_prefill_pp(PrefillArgs a)
+{
+    constexpr int NW = PingPong<HD, P, NCG>::NW;
+    const PrefillWork<P, NCG, NW> W(a);
+    __shared__ LdsDirect<HD> S;
+    WaveAttn<HD, KV_F16, NCG> A;
+    A.init(a, W.b, W.kvh, W.col0, W.start, W.mapped, W.wave_active, W.j, W.g);
+    const int nblk = (W.wg_len + kTB - 1) / kTB;
+
+    // prologue: K and V of block 0, K of block 1
+    const int tb = W.table(0);
+    const uint64_t mask_c = W.valid_mask(a, tb, 0);
+    issue_k<HD, P, NW>(a, W.kvh, W.w, W.lane, tb, S, 0);
+    issue_v<HD, P, NW>(a, W.kvh, W.w, W.lane, tb, S, 0);
+    const int tbv = W.table(kTB); // block whose V is issued next
+    const uint64_t mask_n = W.valid_mask(a, tbv, kTB);
+    issue_k<HD, P, NW>(a, W.kvh, W.w, W.lane, tbv, S, 1);
+    const int tbk = W.table(2 * kTB); // block whose K is issued next
+    wait_direct_loads();
+    __syncthreads();
+    if (mask_c != ~0ull) {
+        zero_dead_v<HD, 64 * NW>(S, 0, mask_c, W.tid);
+        __syncthreads();
+    }
+    PingPong<HD, P, NCG> pp{a, W, S, A};
+    if (W.w >= NW / 2)
+        pp.template run<true>(tbv, tbk, mask_c, mask_n, nblk);
+    else
+        pp.template run<false>(tbv, tbk, mask_c, mask_n, nblk);
+    wait_direct_loads(); // loads issued past the end, before the workgroup's LDS is released
+    if (W.wave_active)
+        A.finish(a, W.b, W.kvh, W.col0, W.j, W.g);
+}
+
+// Quantised pages (q8_0, q4_0; head_dim 128), two waves per SIMD in
+// ping-pong as attn_prefill_pp, with the blocks staged through registers
+// into exact hi + lo fp16 planes (two LDS buffers each for K and V).  Each
+// group stages one plane in its vector-ALU phase: B the K plane of block
+// n + 1 in phase 1 of block n, A the V plane of block n + 1 in phase 2; the
+// global loads of a plane go out one block before its conversion.  Per
+// block n:
+//   phase 1: A: P V (n - 1), scores (n)      B: softmax (n), K (n + 1) staged
+//   phase 2: A: softmax (n), V (n + 1) staged B: P V (n), scores (n + 1)
+template <int HD, int KT, int P, int NCG>
+struct PingPongQ {
+    static constexpr int NW = 8;
+    const PrefillArgs &a;
+    const PrefillWork<P, NCG, NW> &W;
+    Lds<HD, KT, 2> &S;
+    WaveAttn<HD, KT, NCG> &A;
+
+    __device__ __forceinline__ bool live(int base) const { return W.wave_active && base < W.wave_len; }
+
+    // GB: group B (stages K), else group A (stages V).  R holds this
+    // group's plane of block 1; tb2 the page ids of block 2.
+    template <bool GB>
+    __device__ __forceinline__ void run(PlaneRegs<HD, KT> &R, int tb2, uint64_t mask_c, uint64_t mask_n, int nblk)
+    {
+        const int st = W.tid & 255;
+        f4 s[NCG][2][2]; // a block's scores, then its P (softmax_block)
+        if (GB && live(0))
+            A.qk_block(S, 0, s, W.j, W.g);
+        int n = 0;
+        auto step = [&](auto full) {
+            constexpr bool FULL = decltype(full)::value;
+            const int base = n * kTB, cur = n & 1;
+            // phase 1
+            if (!GB) {
+                __builtin_amdgcn_s_setprio(1);
+                if (n > 0 && live(base - kTB))
+                    A.pv_block(S, cur ^ 1, s, W.j, W.g);
+                if (live(base))
+                    A.qk_block(S, cur, s, W.j, W.g);
+                __builtin_amdgcn_s_setprio(0);
+            } else {
+                if (live(base))
+                    A.template softmax_block<FULL>(s, base, mask_c, W.g);
+                plane_store<0, HD, KT, P, 2>(a, W.kvh, st, cur ^ 1, 0, R, S); // K of block n + 1
+                plane_load<0, HD, KT, P>(a, W.kvh, st, tb2, R);                // K of block n + 2
+            }
+            __syncthreads();
+            // phase 2
+            if (!GB) {
+                if (live(base))
+                    A.template softmax_block<FULL>(s, base, mask_c, W.g);
+                plane_store<1, HD, KT, P, 2>(a, W.kvh, st, cur ^ 1, mask_n, R, S); // V of block n + 1
+                plane_load<1, HD, KT, P>(a, W.kvh, st, tb2, R);                     // V of block n + 2
+            } else {
+                __builtin_amdgcn_s_setprio(1);
+                if (live(base))
+                    A.pv_block(S, cur, s, W.j, W.g);
+                if (live(base + kTB))
+                    A.qk_block(S, cur ^ 1, s, W.j, W.g);
+                __builtin_amdgcn_s_setprio(0);
+            }
+            const uint64_t mask_nn = W.valid_mask(a, tb2, base + 2 * kTB);
+            tb2 = W.table(base + 3 * kTB);
+            __syncthreads();
+            mask_c = mask_n;
+            mask_n = mask_nn;
+            n++;
+        };
+        while (n < nblk && W.block_full(n * kTB, mask_c))
+            step(std::true_type{});
+        while (n < nblk)
+            step(std::false_type{});
+        if (!GB && nblk > 0 && live((nblk - 1) * kTB))
+            A.pv_block(S, (nblk - 1) & 1, s, W.j, W.g);
+    }
+};
+
+template <int HD, int KT, int P, int NCG>
+__global__ __launch_bounds__(512) void attn_prefill_ppq(PrefillArgs a)
+{
+    constexpr int NW = PingPongQ<HD, KT, P, NCG>::NW;
+    const PrefillWork<P, NCG, NW> W(a);
+    __shared__ Lds<HD, KT, 2> S;
+    WaveAttn<HD, KT, NCG> A;
+    A.init(a, W.b, W.kvh, W.col0, W.start, W.mapped, W.wave_active, W.j, W.g);
+    const int nblk = (W.wg_len + kTB - 1) / kTB;
+    const bool gb = W.w >= NW / 2;
+    const int st = W.tid & 255;
+
+    // prologue: both planes of block 0 staged (B: K, A: V), and each group's
+    // plane of block 1 loaded
+    const int tb0 = W.table(0), tb1 = W.table(kTB);
+    const uint64_t mask_c = W.valid_mask(a, tb0, 0);
+    const uint64_t mask_n = W.valid_mask(a, tb1, kTB);
+    PlaneRegs<HD, KT> R;
+    if (gb) {
+        plane_load<0, HD, KT, P>(a, W.kvh, st, tb0, R);
+        plane_store<0, HD, KT, P, 2>(a, W.kvh, st, 0, 0, R, S);
+        plane_load<0, HD, KT, P>(a, W.kvh, st, tb1, R);
+    } else {
+        plane_load<1, HD, KT, P>(a, W.kvh, st, tb0, R);
+        plane_store<1, HD, KT, P, 2>(a, W.kvh, st, 0, mask_c, R, S);
+        plane_load<1, HD, KT, P>(a, W.kvh, st, tb1, R);
+    }
+    const int tb2 = W.table(2 * kTB);
+    __syncthreads();
+    PingPongQ<HD, KT, P, NCG> pp{a, W, S, A};
+    if (gb)
+        pp.template run<true>(R, tb2, mask_c, mask_n, nblk);
+    else
+        pp.template run<false>(R, tb2, mask_c, mask_n, nblk);
     if (W.wave_active)
         A.finish(a, W.b, W.kvh, W.col0, W.j, W.g);
 }
@@ -1440,13 +1964,26 @@ static void launch_lds(const PrefillArgs &a, hipStream_t st)
         constexpr int NCG = kPrefillDirectNcg;
         switch (a.L.page_tokens) {
         case 16:
-            hipLaunchKernelGGL((attn_prefill_dlds<HD, 16, NCG>), grid(NCG, 4), dim3(256), 0, st, a);
+            hipLaunchKernelGGL((attn_prefill_pp<HD, 16, NCG>), grid(NCG, 8), dim3(512), 0, st, a);
             break;
         case 32:
-            hipLaunchKernelGGL((attn_prefill_dlds<HD, 32, NCG>), grid(NCG, 4), dim3(256), 0, st, a);
+            hipLaunchKernelGGL((attn_prefill_pp<HD, 32, NCG>), grid(NCG, 8), dim3(512), 0, st, a);
             break;
         default:
-            hipLaunchKernelGGL((attn_prefill_dlds<HD, 64, NCG>), grid(NCG, 4), dim3(256), 0, st, a);
+            hipLaunchKernelGGL((attn_prefill_pp<HD, 64, NCG>), grid(NCG, 8), dim3(512), 0, st, a);
+            break;
+        }
+    } else if constexpr ((KT == KV_Q8_0 || KT == KV_Q4_0) && HD == 128) {
+        constexpr int NCG = 2;
+        switch (a.L.page_tokens) {
+        case 16:
+            hipLaunchKernelGGL((attn_prefill_ppq<HD, KT, 16, NCG>), grid(NCG, 8), dim3(512), 0, st, a);
+            break;
+        case 32:
+            hipLaunchKernelGGL((attn_prefill_ppq<HD, KT, 32, NCG>), grid(NCG, 8), dim3(512), 0, st, a);
+            break;
+        default:
+            hipLaunchKernelGGL((attn_prefill_ppq<HD, KT, 64, NCG>), grid(NCG, 8), dim3(512), 0, st, a);
             break;
         }
     } else {
