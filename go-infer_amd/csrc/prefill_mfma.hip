@@ -1,4 +1,4 @@
-// Chunked-prefill causal attention on the matrix cores (fp16 and q8_0 pages).
+// Chunked-prefill causal attention on the matrix cores (fp16, q8_0, q4_0 and f32 pages).
 //
 // Semantics: pkg/engine/forward.go:547-577 -- the chunk's K/V are already in
 // the pages; query i of sequence b sits at position start_pos[b] + i and
@@ -11,7 +11,10 @@
 // wave owns its columns for the whole context (no cross-wave merge); the four
 // waves of a workgroup take consecutive column groups, so they stream the same
 // K/V blocks and share them through the caches.  Query and P are split into
-// fp16 hi + lo halves, so results keep float32 accuracy.
+// fp16 hi + lo halves, so results keep float32 accuracy.  The LDS-staged
+// kernels share one block of K and V among the waves of a workgroup; the
+// ping-pong kernels (attn_prefill_pp, attn_prefill_ppq) put two waves on
+// every SIMD that alternate between products and softmax.
 //
 // q8_0 pages stay exact: int8 values are exact in fp16 (converted with a
 // byte permute: 0x64XX is 1024 + XX).  The LDS-staged kernel turns value x
@@ -1131,18 +1134,12 @@ struct WaveAttn {
     // is cached and on a valid page.  FULL: every token of the block is valid
     // for every column of the wave (a separate instantiation, with no masking
     // code).
-    // PRIO: raise the wave's priority while it issues products, so that the
-    // other wave on the SIMD fills the gaps with its softmax (measured +1.8 %
-    // for fp16 pages, but a loss for the register-staged kernels, whose
-    // staging competes for the same issue slots).
-    template <bool FULL, bool PRIO = false, class LDS>
+    template <bool FULL, class LDS>
     __device__ __forceinline__ void block(const LDS &S, int buf, int base, uint64_t mask, int j, int g)
     {
         // ---- scores: tiles (h, t), row j = token 32h + 8(j/4) + j%4 + 4t ----
         const uint8_t *kp = k_lane(S, buf, j, g, false);
         const uint8_t *klp = KT != KV_F16 ? k_lane(S, buf, j, g, true) : kp;
-        if (PRIO)
-            __builtin_amdgcn_s_setprio(1);
         f4 s[NCG][2][2];
 #pragma unroll
         for (int h = 0; h < 2; h++)
@@ -1168,8 +1165,6 @@ struct WaveAttn {
                 }
             }
 
-        if (PRIO)
-            __builtin_amdgcn_s_setprio(0);
         // ---- online softmax of each column over this lane's 16 tokens ----
         h8 ph[2][NCG], pl[2][NCG];
         float alpha[NCG];
@@ -1191,8 +1186,6 @@ struct WaveAttn {
             rescale(alpha, g);
 
         // ---- P V, V operand: dimension 16nb + j, tokens 32h + 8g .. +7 ----
-        if (PRIO)
-            __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             const uint8_t *vp = v_lane(S, buf, h, j, g, false);
@@ -1212,8 +1205,6 @@ struct WaveAttn {
                 }
             }
         }
-        if (PRIO)
-            __builtin_amdgcn_s_setprio(0);
     }
 
     // ---- the three stages of block(), for the ping-pong kernels ----
@@ -1521,12 +1512,12 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_lds(PrefillArgs a)
     }
 }
 
-// Issues the direct global->LDS loads of one fp16 block into buffer `buf`.
-// K: 1 KiB segments of 512/HD tokens (one page each); V: segments of 8
-// dimensions x 64 tokens, where lane l always fetches logical chunk
-// (l & 7) ^ ((l >> 3) & 7), i.e. the same 8 tokens of every segment.
-// issue_k and issue_v are its two halves; NW waves share them (HD / (8 NW)
-// loads per wave each).
+// Direct global->LDS loads of one fp16 block: issue_k the K plane into K
+// buffer `buf`, issue_v the V plane into V buffer `buf`; NW waves share each
+// (HD / (8 NW) loads per wave).  K: 1 KiB segments of 512/HD tokens (one page
+// each); V: segments of 8 dimensions x 64 tokens, where lane l always fetches
+// logical chunk (l & 7) ^ ((l >> 3) & 7), i.e. the same 8 tokens of every
+// segment.
 template <int HD, int P, int NW = 4>
 __device__ __forceinline__ void issue_k(const PrefillArgs &a, int kvh, int w, int lane, int tb, LdsDirect<HD> &S,
                                         int buf)
@@ -1571,14 +1562,6 @@ __device__ __forceinline__ void issue_v(const PrefillArgs &a, int kvh, int w, in
     }
 }
 
-template <int HD, int P>
-__device__ __forceinline__ void issue_direct(const PrefillArgs &a, int kvh, int w, int lane, int tb,
-                                             LdsDirect<HD> &S, int buf)
-{
-    issue_k<HD, P>(a, kvh, w, lane, tb, S, buf);
-    issue_v<HD, P>(a, kvh, w, lane, tb, S, buf);
-}
-
 // Zeroes V of the tokens whose `vmask` bit is clear (past the cached range or
 // on an invalid page) after a direct load; their scores are masked, and stale
 // values must not reach O through 0 * NaN.
@@ -1603,60 +1586,6 @@ __device__ __forceinline__ void zero_dead_v(LdsDirect<HD> &S, int buf, uint64_t 
 __device__ __forceinline__ void wait_direct_loads()
 {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-}
-
-// fp16 pages through direct global->LDS loads: no staging registers and no
-// LDS store instructions; two LDS buffers, one barrier per block (two more on
-// blocks with tokens to zero).
-template <int HD, int P, int NCG>
-__global__ __launch_bounds__(256) void attn_prefill_dlds(PrefillArgs a)
-{
-    const PrefillWork<P, NCG> W(a);
-    __shared__ LdsDirect<HD> S;
-    WaveAttn<HD, KV_F16, NCG> A;
-    A.init(a, W.b, W.kvh, W.col0, W.start, W.mapped, W.wave_active, W.j, W.g);
-
-    int tb = W.table(0);
-    uint64_t mask_c = W.valid_mask(a, tb, 0);
-    issue_direct<HD, P>(a, W.kvh, W.w, W.lane, tb, S, 0);
-    tb = W.table(kTB);
-    wait_direct_loads();
-    __syncthreads();
-    if (mask_c != ~0ull) {
-        zero_dead_v<HD>(S, 0, mask_c, W.tid);
-        __syncthreads();
-    }
-
-    // One block; FULL: no column of the workgroup needs masking.
-    int base = 0, it = 0;
-    auto step = [&](auto full) {
-        constexpr bool FULL = decltype(full)::value;
-        const int buf = it & 1;
-        const bool more = base + kTB < W.wg_len;
-        uint64_t mask_n = 0;
-        if (more) {
-            mask_n = W.valid_mask(a, tb, base + kTB);
-            issue_direct<HD, P>(a, W.kvh, W.w, W.lane, tb, S, buf ^ 1);
-            tb = W.table(base + 2 * kTB);
-        }
-        if (W.wave_active && base < W.wave_len)
-            A.template block<FULL, true>(S, buf, base, mask_c, W.j, W.g);
-        wait_direct_loads();
-        __syncthreads();
-        if (more && mask_n != ~0ull) {
-            zero_dead_v<HD>(S, buf ^ 1, mask_n, W.tid);
-            __syncthreads();
-        }
-        mask_c = mask_n;
-        base += kTB;
-        it++;
-    };
-    while (base < W.wg_len && W.block_full(base, mask_c))
-        step(std::true_type{});
-    while (base < W.wg_len)
-        step(std::false_type{});
-    if (W.wave_active)
-        A.finish(a, W.b, W.kvh, W.col0, W.j, W.g);
 }
 
 // fp16 pages, two waves per SIMD in ping-pong.  The workgroup's 8 waves form
@@ -1919,18 +1848,13 @@ constexpr int prefill_ncg()
     return HD == 64 ? 2 : 1;
 }
 
-// LDS buffers of the staged kernel: two (one barrier per block) for fp16
-// pages.  Quantised pages stage K and V as hi/lo planes (64 KiB a block at
-// head_dim 128): there one workgroup of 8 waves per CU runs over two buffers
-// (130 KiB), four of the waves staging; head_dim 64 keeps 4-wave workgroups
-// over one buffer.  f32 pages run 8-wave workgroups over one buffer (their
-// block maxima are exchanged at its barrier), every wave staging.
-constexpr int kPrefillNbufF16 = 2;
+// The register-staged kernel (attn_prefill_lds) now serves f32 pages (8-wave
+// workgroups over one buffer: their block maxima are exchanged at its
+// barrier, every wave staging) and q8_0 pages at head_dim 64 (4-wave
+// workgroups over one buffer).  fp16 pages and the quantised pages at
+// head_dim 128 run the ping-pong kernels.
 template <int HD, int KT>
-constexpr int kPrefillWaves = (KT == KV_Q8_0 || KT == KV_Q4_0) && HD == 128 ? 8 : 4;
-template <int HD, int KT>
-constexpr int kPrefillNbufQ = kPrefillWaves<HD, KT> == 8 ? 2 : 1;
-// f32 pages: one buffer (their block maxima are exchanged at its barrier).
+constexpr int kPrefillWaves = KT == KV_F32 ? 8 : 4;
 
 // Column groups per wave: two halve the LDS reads per matrix-core product;
 // taken where the kernel then still fits two waves per SIMD (256 VGPRs).
@@ -1944,16 +1868,15 @@ constexpr int prefill_lds_ncg()
     return KT == KV_F32 ? 1 : (HD == 64 || P == 16 || (KT != KV_F16 && P == 32)) ? 2 : 1;
 }
 
-// fp16 pages use the direct global->LDS kernel (no staging registers, so
-// two column groups always fit).
-constexpr int kPrefillDirectNcg = 2;
+// The ping-pong kernels hold two column groups per wave.
+constexpr int kPrefillPingPongNcg = 2;
 
 template <int HD, int KT>
 static void launch_lds(const PrefillArgs &a, hipStream_t st)
 {
     using namespace mfma_prefill;
-    constexpr int NBUF = KT == KV_F32 ? 1 : KT == KV_F16 ? kPrefillNbufF16 : kPrefillNbufQ<HD, KT>;
-    constexpr int NW = KT == KV_F16 ? 4 : KT == KV_F32 ? 8 : kPrefillWaves<HD, KT>;
+    constexpr int NBUF = 1;
+    constexpr int NW = kPrefillWaves<HD, KT>;
     const int G = a.num_heads / a.L.num_kv_heads;
     const int64_t cols = (int64_t)a.chunk_len * G;
     auto grid = [&](int ncg, int nw) {
@@ -1961,7 +1884,7 @@ static void launch_lds(const PrefillArgs &a, hipStream_t st)
         return dim3((unsigned)((cols + per_wg - 1) / per_wg), a.L.num_kv_heads, a.batch);
     };
     if constexpr (KT == KV_F16) {
-        constexpr int NCG = kPrefillDirectNcg;
+        constexpr int NCG = kPrefillPingPongNcg;
         switch (a.L.page_tokens) {
         case 16:
             hipLaunchKernelGGL((attn_prefill_pp<HD, 16, NCG>), grid(NCG, 8), dim3(512), 0, st, a);
@@ -1974,7 +1897,7 @@ static void launch_lds(const PrefillArgs &a, hipStream_t st)
             break;
         }
     } else if constexpr ((KT == KV_Q8_0 || KT == KV_Q4_0) && HD == 128) {
-        constexpr int NCG = 2;
+        constexpr int NCG = kPrefillPingPongNcg;
         switch (a.L.page_tokens) {
         case 16:
             hipLaunchKernelGGL((attn_prefill_ppq<HD, KT, 16, NCG>), grid(NCG, 8), dim3(512), 0, st, a);
