@@ -8,7 +8,11 @@ each of the 32 layers: append the new token's K/V (position 8191, through
 the block table) then paged decode attention over all 8192 tokens.  Inputs
 (q, k, v, block tables, lengths) are resident in HBM before timing.
 
-Prints one JSON line (see --help).  --config selects other shapes:
+Prints one JSON line (see --help).  Without --config it times the workload
+above, then the other configurations of the baseline -- the TinyLlama batch-1
+case (A), the ragged batch 32 (B), the Llama-3-70B batch 8 x 32768 (D) and the
+q8_0 chunked prefill (E) -- each over at most 10 steps with its parity sample,
+and reports them under "other_configs".  --config selects one shape:
   llama8b_b32         Llama-3-8B shape, batch 32, context U[512, 4096]
   llama70b_b8         Llama-3-70B shape (64 q / 8 kv), page 32, batch 8 x 32768
   llama8b_q8_prefill  Llama-3-8B shape, Q8_0 KV: a 4096-token prefill of batch 4
@@ -444,8 +448,8 @@ def run_fork(args, gi, torch, dev, cfg):
         "cpu_baseline": cpu,
         "parity": {"copied_pages_equal": ok, "pass": ok},
     }
-    print(json.dumps(res), flush=True)
     pool.close()
+    return res
 
 
 def run_prefill(args, gi, torch, dev, cfg):
@@ -567,8 +571,8 @@ def run_prefill(args, gi, torch, dev, cfg):
         "cpu_baseline": cpu,
         "parity": parity,
     }
-    print(json.dumps(res), flush=True)
     pool.close()
+    return res
 
 
 def run_driver(args, gi, torch, dev, cfg):
@@ -689,9 +693,9 @@ def run_driver(args, gi, torch, dev, cfg):
         "cpu_baseline": None,
         "roofline": None,
     }
-    print(json.dumps(res), flush=True)
     drv.close()
     pool.close()
+    return res
 
 
 def run_oproj(args, gi, torch, dev, cfg):
@@ -787,10 +791,10 @@ def run_oproj(args, gi, torch, dev, cfg):
         "cpu_baseline": cpu,
         "parity": parity,
     }
-    print(json.dumps(res), flush=True)
     for w in ws:
         w.close()
     pool.close()
+    return res
 
 
 def run_tinyllama(args, gi, torch, dev, cfg):
@@ -946,8 +950,8 @@ def run_tinyllama(args, gi, torch, dev, cfg):
         "cpu_baseline": cpu,
         "parity": parity,
     }
-    print(json.dumps(res), flush=True)
     pool.close()
+    return res
 
 
 def main():
@@ -955,7 +959,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="llama8b_b256_8k", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default=None, choices=sorted(CONFIGS),
+                    help="one configuration (default: llama8b_b256_8k, followed by the other "
+                         "configurations of the baseline, reported under other_configs)")
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
@@ -965,6 +971,8 @@ def main():
                     help="-1 automatic, 0 vector ALU, 1 matrix core")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="also run one device copy of this many MiB (counter calibration)")
+    ap.add_argument("--no-suite", action="store_true",
+                    help="without --config: time llama8b_b256_8k only, not the other configurations")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the paged decode path runs on a single MI355X "
@@ -978,22 +986,70 @@ def main():
     gi.lib()
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
     dev = torch.device("cuda:0")
-    cfg = CONFIGS[args.config]
+    suite = args.config is None and not args.no_suite
+    if args.config is None:
+        args.config = DEFAULT_CONFIG
+    res = run_config(args, gi, torch, dev, args.config)
+    if suite:
+        res["other_configs"] = run_suite(args, gi, torch, dev)
+    print(json.dumps(res), flush=True)
+
+
+# Configurations the default run times after the headline (config C), so that
+# every workload of the baseline is measured by the same invocation: the
+# reference's CPU-runnable case (A), the ragged batch (B), the 70B long-context
+# batch (D) and the q8_0 chunked prefill (E).
+DEFAULT_CONFIG = "llama8b_b256_8k"
+SUITE = (("A", "tinyllama_b1"), ("B", "llama8b_b32"), ("D", "llama70b_b8"), ("E", "llama8b_q8_prefill"))
+
+
+def run_config(args, gi, torch, dev, name):
+    cfg = CONFIGS[name]
     if cfg.get("fork"):
-        run_fork(args, gi, torch, dev, cfg)
-        return
+        return run_fork(args, gi, torch, dev, cfg)
     if cfg.get("driver"):
-        run_driver(args, gi, torch, dev, cfg)
-        return
+        return run_driver(args, gi, torch, dev, cfg)
     if cfg.get("wtype"):
-        run_oproj(args, gi, torch, dev, cfg)
-        return
+        return run_oproj(args, gi, torch, dev, cfg)
     if cfg.get("tiny"):
-        run_tinyllama(args, gi, torch, dev, cfg)
-        return
+        return run_tinyllama(args, gi, torch, dev, cfg)
     if cfg.get("prefill"):
-        run_prefill(args, gi, torch, dev, cfg)
-        return
+        return run_prefill(args, gi, torch, dev, cfg)
+    return run_decode(args, gi, torch, dev, cfg, name)
+
+
+def run_suite(args, gi, torch, dev):
+    """The SUITE configurations, each timed over at most 10 steps after 2
+    warm-ups, with its parity sample and without its CPU baseline; a summary
+    of each result line (or the error it raised)."""
+    out = {}
+    for letter, name in SUITE:
+        sub = argparse.Namespace(**vars(args))
+        sub.config = name
+        sub.steps = min(args.steps, 10)
+        sub.warmup = min(args.warmup, 2)
+        sub.no_cpu_baseline = True
+        torch.cuda.empty_cache()
+        log("-- config %s (%s)" % (letter, name))
+        try:
+            r = run_config(sub, gi, torch, dev, name)
+        except Exception as e:  # one configuration's failure leaves the others' results
+            out[letter] = {"config": name, "error": "%s: %s" % (type(e).__name__, e)}
+            continue
+        roof = r.get("roofline") or {}
+        par = r.get("parity") or {}
+        out[letter] = {
+            "config": name, "workload": r["config"]["workload"], "value": r["value"], "unit": r["unit"],
+            "ms_per_step": r["ms_per_step"], "steps": r["steps"], "warmup": r["warmup"],
+            "tokens_per_s": r.get("tokens_per_s"),
+            "roofline": {k: roof.get(k) for k in ("bound", "achieved", "peak", "unit", "frac", "kernel",
+                                                 "launch_ms") if k in roof} or None,
+            "parity": {k: par.get(k) for k in ("max_rel_err", "tol", "pass") if k in par} or None,
+        }
+    return out
+
+
+def run_decode(args, gi, torch, dev, cfg, name):
     H, kvh, hd, P, layers = (cfg["q_heads"], cfg["kv_heads"], cfg["head_dim"],
                              cfg["page_tokens"], cfg["layers"])
     kv_dim = kvh * hd
@@ -1110,7 +1166,7 @@ def main():
             kv_dtype, "attn_mfma_q<%d,%d>" % (kv_type_of(gi, kv_dtype), hd))
     else:
         kname = "attn_valu<%d,%d,%d>" % (kv_type_of(gi, kv_dtype), hd, H // kvh)
-    traffic = profiled_traffic(kname, args.config)
+    traffic = profiled_traffic(kname, name)
     res = {
         "metric": METRIC,
         "value": round(tot_gbs, 2),
@@ -1144,8 +1200,8 @@ def main():
         "cpu_baseline": cpu,
         "parity": parity,
     }
-    print(json.dumps(res), flush=True)
     pool.close()
+    return res
 
 
 if __name__ == "__main__":
