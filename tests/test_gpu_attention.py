@@ -523,3 +523,44 @@ def test_decode_bad_first_page_is_skipped(gi, oracle, dev, kv_type):
         assert rel_err_rows(o[0], want0, H, hd).max() <= TOL[kv_type], kern
         assert rel_err_rows(o[1], want1, H, hd).max() <= TOL[kv_type], kern
     pop.pool.set_decode_kernel(-1)
+
+
+@pytest.mark.parametrize("kv_type", [0, 1, 2, 3], ids=["f32", "f16", "q8_0", "q4_0"])
+def test_prefill_bad_page_is_skipped(gi, oracle, dev, kv_type):
+    """A 64-query chunk at start 200 whose block table holds an id outside
+    the pool for tokens 48..63 (inside every query's context): both prefill
+    kernels skip that page's tokens -- the block it sits in runs the masked
+    path, and its V is zeroed before the products -- report the id at
+    gi_synchronize, and match the oracle over the context without those 16
+    tokens (forward.go:547-577 with the page removed).  The second sequence
+    of the batch is unaffected."""
+    import torch
+    H, kvh, hd, P = 32, 8, 128, 16
+    starts, chunk = [200, 150], 64
+    lens = [s + chunk for s in starts]
+    pop = Populated(gi, dev, kv_type, 1, kvh, hd, P, lens, seed=31, append_chunk=chunk, outliers=True)
+    bt = pop.block_tables()
+    bt[0, 3] = pop.pool.num_pages + 7
+    sp = torch.tensor(starts, dtype=torch.int32, device=dev)
+    qd, q = seeded((len(starts), chunk, H * hd), 32, dev, outliers=True)
+    scale = oracle.attn_scale(hd)
+    keep = np.r_[0:3 * P, 4 * P:lens[0]]
+    ks, vs = pop.stored(0, 0)
+    kw = oracle.widen(kv_type, kvh * hd, ks)[keep]
+    vw = oracle.widen(kv_type, kvh * hd, vs)[keep]
+    want0 = oracle.attention_prefill(q[0], kw, vw, H, kvh, hd, starts[0] - P, chunk, 1 << 30, scale)
+    ks, vs = pop.stored(0, 1)
+    want1 = oracle.attention_prefill(q[1], oracle.widen(kv_type, kvh * hd, ks), oracle.widen(kv_type, kvh * hd, vs),
+                                     H, kvh, hd, starts[1], chunk, 1 << 30, scale)
+    for kern in (0, 1):
+        pop.pool.set_decode_kernel(kern)
+        out = torch.full_like(qd, float("nan"))
+        pop.pool.AttentionGQABatch(out, qd, 0, bt, sp, H, scale, chunk)
+        with pytest.raises(gi.GIError) as e:
+            pop.pool.synchronize()
+        assert e.value.code == -7, kern
+        o = out.cpu().numpy()
+        assert np.isfinite(o).all(), kern
+        assert rel_err_rows(o[0], want0, H, hd).max() <= TOL[kv_type], kern
+        assert rel_err_rows(o[1], want1, H, hd).max() <= TOL[kv_type], kern
+    pop.pool.set_decode_kernel(-1)
