@@ -16,6 +16,7 @@
 // (block_table[t / page_tokens], t % page_tokens) (paged_kv.go:107-131).
 #include "gi_common.h"
 #include "gi_kernels.h"
+#include "mfma_ops.h"
 #include "token_store.h"
 
 #include <algorithm>
@@ -25,6 +26,9 @@ namespace gi {
 namespace {
 
 constexpr int kThreads = 256;
+using mfma_ops::f4;
+using mfma_ops::u2;
+using mfma_ops::u4;
 
 __device__ __forceinline__ void raise_flag(int *status, int bit)
 {
@@ -154,6 +158,204 @@ __global__ __launch_bounds__(kThreads) void append_q4(PoolLayout L, uint8_t *bas
     }
 }
 
+// Bulk append with explicit destinations (gi_paged_append, a prefill chunk):
+// a workgroup takes kRowTok consecutive tokens of one kv head.  Each thread
+// converts 4 consecutive elements of one token (a 32-element quantisation
+// block is 8 consecutive lanes), writes them into the token's K row, and
+// stages their V form in LDS transposed to [row][token]: V pages are
+// dimension-major, so written element by element each V store would touch
+// its own 32-byte sector.  Then each thread writes 8 tokens of one V row (or
+// of one V-scale row) with one store when they sit on consecutive slots of
+// one page with the store aligned (the usual chunk append), token by token
+// otherwise; neighbouring lanes write the two halves of a 16-token row.
+// Bytes are identical to append_plain / append_q8 / append_q4 (the same
+// conversion and quantisation code).  head_dim is a multiple of 32 and at
+// most kRowMaxHd.
+constexpr int kRowTok = 16, kRowMaxHd = 256;
+
+template <int KT>
+__global__ __launch_bounds__(kThreads) void append_rows(PoolLayout L, uint8_t *base, int n_tok, Dest D,
+                                                        const float *__restrict__ k, const float *__restrict__ v,
+                                                        int *status)
+{
+    const int hd = L.head_dim, P = L.page_tokens, nb = hd / 32;
+    const int kv_dim = L.num_kv_heads * hd;
+    const int h = blockIdx.y, i0 = blockIdx.x * kRowTok, tid = threadIdx.x;
+    const int nt = min(kRowTok, n_tok - i0);
+    const int gpt = hd / 4; // 4-element groups per token
+    const int ngroups = kRowTok * gpt;
+    __shared__ int64_t s_page[kRowTok];
+    __shared__ int s_slot[kRowTok];              // -1: token not stored
+    __shared__ uint32_t s_v[kRowMaxHd * kRowTok]; // V element bits (or codes, q4 bytes) [row][token]
+    __shared__ uint16_t s_vs[kRowMaxHd / 32 * kRowTok]; // V block scales [block][token]
+
+    if (tid < kRowTok) {
+        int64_t pg = 0;
+        int sl = -1;
+        // the kv head 0 workgroup reports each bad token once
+        if (tid < nt && !resolve(D, L, i0 + tid, &pg, &sl, h == 0 ? status : nullptr))
+            sl = -1;
+        s_page[tid] = pg;
+        s_slot[tid] = sl;
+    }
+    __syncthreads();
+
+    // ---- K rows, and V converted into LDS ----
+    for (int g0 = 0; g0 < ngroups; g0 += kThreads) {
+        // whole 8-lane groups (one quantisation block) are in or out of range
+        const int g = g0 + tid;
+        const int t = g / gpt, a4 = g - t * gpt, d0 = 4 * a4, blk = a4 >> 3, a = a4 & 7;
+        const bool in = g < ngroups && t < nt;
+        f4 kx = f4{0.0f, 0.0f, 0.0f, 0.0f}, vx = kx;
+        if (in) {
+            const int64_t e = (int64_t)(i0 + t) * kv_dim + (int64_t)h * hd + d0;
+            kx = *reinterpret_cast<const f4 *>(k + e);
+            vx = *reinterpret_cast<const f4 *>(v + e);
+        }
+        const int sl = g < ngroups ? s_slot[t] : -1;
+        uint8_t *pg = base + (g < ngroups ? s_page[t] : 0) * L.page_bytes;
+        const bool st = in && sl >= 0;
+        const int64_t krow = (int64_t)h * P + sl; // K row of the token
+        uint32_t vb[4];                            // V element bits / codes for s_v
+        if constexpr (KT == KV_F32) {
+            if (st)
+                *reinterpret_cast<f4 *>(pg + L.k_off + (krow * hd + d0) * 4) = kx;
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                // (copied out before the bit cast: hipcc's __builtin_bit_cast
+                // of a vector element reads element 0 whatever the index)
+                const float x = vx[c];
+                vb[c] = __builtin_bit_cast(uint32_t, x);
+            }
+        } else if constexpr (KT == KV_F16) {
+            uint32_t kh[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                kh[c] = float_to_half_bits_rtz(kx[c]);
+                vb[c] = float_to_half_bits_rtz(vx[c]);
+            }
+            if (st)
+                *reinterpret_cast<u2 *>(pg + L.k_off + (krow * hd + d0) * 2) =
+                    u2{kh[0] | (kh[1] << 16), kh[2] | (kh[3] << 16)};
+        } else {
+            uint32_t kk = 0, vk = 0;
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                kk = max(kk, abs_key(kx[c]));
+                vk = max(vk, abs_key(vx[c]));
+            }
+#pragma unroll
+            for (int m = 1; m < 8; m <<= 1) {
+                kk = max(kk, (uint32_t)__shfl_xor((int)kk, m, 8));
+                vk = max(vk, (uint32_t)__shfl_xor((int)vk, m, 8));
+            }
+            float kinv, vinv;
+            const bool q8 = KT == KV_Q8_0;
+            const uint32_t kd = q8 ? q8_scale(__builtin_bit_cast(float, kk), &kinv)
+                                   : q4_scale(__builtin_bit_cast(float, kk), &kinv);
+            const uint32_t vd = q8 ? q8_scale(__builtin_bit_cast(float, vk), &vinv)
+                                   : q4_scale(__builtin_bit_cast(float, vk), &vinv);
+            if (q8) {
+                uint32_t kw = 0;
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    kw |= ((uint32_t)q8_quant(kx[c], kinv) & 0xFFu) << (8 * c);
+                    vb[c] = (uint32_t)q8_quant(vx[c], vinv) & 0xFFu;
+                }
+                if (st)
+                    *reinterpret_cast<uint32_t *>(pg + L.k_off + krow * hd + d0) = kw;
+                if (st && a == 0)
+                    reinterpret_cast<uint16_t *>(pg + L.ks_off)[krow * nb + blk] = (uint16_t)kd;
+            } else {
+                // byte j of a block holds element j (low nibble) and j + 16
+                // (high): lanes a < 4 take the high nibbles of lane a + 4
+                uint32_t kn = 0, vn = 0;
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    kn |= (uint32_t)q4_quant(kx[c], kinv) << (8 * c);
+                    vn |= (uint32_t)q4_quant(vx[c], vinv) << (8 * c);
+                }
+                const uint32_t kh = (uint32_t)__shfl_down((int)kn, 4, 8);
+                const uint32_t vh = (uint32_t)__shfl_down((int)vn, 4, 8);
+                const uint32_t kw = kn | (kh << 4), vw = vn | (vh << 4);
+                if (st && a < 4)
+                    *reinterpret_cast<uint32_t *>(pg + L.k_off + (krow * nb + blk) * 16 + 4 * a) = kw;
+                if (st && a == 0)
+                    reinterpret_cast<uint16_t *>(pg + L.ks_off)[krow * nb + blk] = (uint16_t)kd;
+#pragma unroll
+                for (int c = 0; c < 4; c++)
+                    vb[c] = (vw >> (8 * c)) & 0xFFu;
+            }
+            if (g < ngroups && a == 0)
+                s_vs[blk * kRowTok + t] = (uint16_t)vd;
+        }
+        if (g < ngroups) {
+            if (KT == KV_Q4_0) {
+                if (a < 4) // byte rows 4a .. 4a + 3 of block blk
+#pragma unroll
+                    for (int c = 0; c < 4; c++)
+                        s_v[(blk * 16 + 4 * a + c) * kRowTok + t] = vb[c];
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; c++)
+                    s_v[(d0 + c) * kRowTok + t] = vb[c];
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- V rows and V-scale rows, 8 tokens per task ----
+    constexpr int ESZ = KT == KV_F32 ? 4 : KT == KV_F16 ? 2 : 1;
+    const int vrows = KT == KV_Q4_0 ? hd / 2 : hd;
+    const bool quant = KT == KV_Q8_0 || KT == KV_Q4_0;
+    const int ntask = (vrows + (quant ? nb : 0)) * (kRowTok / 8);
+    for (int task = tid; task < ntask; task += kThreads) {
+        const int row = task / (kRowTok / 8), t0 = 8 * (task % (kRowTok / 8));
+        const bool scale_row = row >= vrows; // quantised pages: V-scale row of block row - vrows
+        const int64_t off = scale_row ? L.vs_off + (((int64_t)h * nb + (row - vrows)) * P) * 2
+                                      : L.v_off + (((int64_t)h * vrows + row) * P) * ESZ;
+        const int esz = scale_row ? 2 : ESZ;
+        // one store when the 8 tokens are consecutive slots of one page
+        const int s0 = s_slot[t0];
+        bool run = s0 >= 0;
+#pragma unroll
+        for (int t = 1; t < 8; t++)
+            run = run && s_slot[t0 + t] == s0 + t && s_page[t0 + t] == s_page[t0];
+        uint8_t *dst0 = base + s_page[t0] * L.page_bytes + off + (int64_t)s0 * esz;
+        run = run && ((uintptr_t)dst0 & (uintptr_t)(8 * esz - 1)) == 0;
+        uint32_t x[8];
+#pragma unroll
+        for (int t = 0; t < 8; t++)
+            x[t] = scale_row ? (uint32_t)s_vs[(row - vrows) * kRowTok + t0 + t] : s_v[row * kRowTok + t0 + t];
+        if (run) {
+            if (esz == 4) {
+                reinterpret_cast<u4 *>(dst0)[0] = u4{x[0], x[1], x[2], x[3]};
+                reinterpret_cast<u4 *>(dst0)[1] = u4{x[4], x[5], x[6], x[7]};
+            } else if (esz == 2) {
+                *reinterpret_cast<u4 *>(dst0) =
+                    u4{x[0] | (x[1] << 16), x[2] | (x[3] << 16), x[4] | (x[5] << 16), x[6] | (x[7] << 16)};
+            } else {
+                *reinterpret_cast<u2 *>(dst0) = u2{x[0] | (x[1] << 8) | (x[2] << 16) | (x[3] << 24),
+                                                   x[4] | (x[5] << 8) | (x[6] << 16) | (x[7] << 24)};
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                const int s = s_slot[t0 + t];
+                if (s < 0)
+                    continue;
+                uint8_t *d = base + s_page[t0 + t] * L.page_bytes + off + (int64_t)s * esz;
+                if (esz == 4)
+                    *reinterpret_cast<uint32_t *>(d) = x[t];
+                else if (esz == 2)
+                    *reinterpret_cast<uint16_t *>(d) = (uint16_t)x[t];
+                else
+                    *d = (uint8_t)x[t];
+            }
+        }
+    }
+}
+
 // Gather one sequence's tokens [0, n_tok) of one layer.
 //   widen == 0: stored format, the reference's bytes per token vector
 //               (f32: 4*kv_dim, f16: 2*kv_dim, q8_0: kv_dim/32 blocks of
@@ -278,9 +480,29 @@ hipError_t append_any(const PoolLayout &L, uint8_t *base, int n_tok, const Dest 
 {
     if (n_tok <= 0)
         return hipSuccess;
+    const bool at_len = D.block_ids == nullptr;
+    if (!at_len && L.head_dim % 32 == 0 && L.head_dim <= kRowMaxHd) {
+        dim3 rgrid((unsigned)((n_tok + kRowTok - 1) / kRowTok), (unsigned)L.num_kv_heads);
+#define GI_ROWS(KT) hipLaunchKernelGGL((append_rows<KT>), rgrid, dim3(kThreads), 0, st, L, base, n_tok, D, k, v, status)
+        switch (L.kv_type) {
+        case KV_F32:
+            GI_ROWS(KV_F32);
+            break;
+        case KV_F16:
+            GI_ROWS(KV_F16);
+            break;
+        case KV_Q4_0:
+            GI_ROWS(KV_Q4_0);
+            break;
+        default:
+            GI_ROWS(KV_Q8_0);
+            break;
+        }
+#undef GI_ROWS
+        return hipGetLastError();
+    }
     int64_t units = (int64_t)n_tok * L.num_kv_heads * L.head_dim;
     dim3 grid(grid_for(units)), block(kThreads);
-    const bool at_len = D.block_ids == nullptr;
 #define GI_APPEND(KERNEL)                                                                    \
     hipLaunchKernelGGL(KERNEL, grid, block, 0, st, L, base, n_tok, D, k, v, status)
     switch (L.kv_type) {

@@ -48,6 +48,27 @@ def test_append_gather_bit_exact(gi, oracle, dev, kv_type, shape):
             assert np.array_equal(rk, ks) and np.array_equal(rv, vs)
 
 
+@pytest.mark.parametrize("kv_type", [0, 1, 2, 3], ids=["f32", "f16", "q8_0", "q4_0"])
+@pytest.mark.parametrize("shape", list(SHAPES))
+def test_bulk_append_bit_exact(gi, oracle, dev, kv_type, shape):
+    """Whole sequences appended in one call each (512 and 300 tokens, the
+    second not a multiple of 16), with NaN / Inf / subnormal / rounding-tie
+    values planted: the bulk append writes runs of 8 tokens of a V row at
+    once where their slots are consecutive on one page, and the stored bytes
+    must equal the oracle's KVCache.Write (kvcache.go:146-180) bit for bit."""
+    import torch
+    kvh, hd, P = SHAPES[shape]
+    lens = [512, 300]
+    pop = Populated(gi, dev, kv_type, 1, kvh, hd, P, lens, seed=41 + kv_type, specials=True)
+    for i, n in enumerate(lens):
+        t = pop.table(i)
+        ko, vo = pop.pool.Get(0, torch.from_numpy(t).to(dev), n)
+        pop.pool.synchronize()
+        ks, vs = pop.stored(0, i)
+        assert np.array_equal(ko.cpu().numpy(), ks), i
+        assert np.array_equal(vo.cpu().numpy(), vs), i
+
+
 def test_reference_kvcache_tests_on_pages(gi, oracle, dev):
     import torch
     # kvcache_test.go:7-71 values i+1 / 2(i+1) and engine_test.go:251-273
