@@ -481,7 +481,10 @@ hipError_t append_any(const PoolLayout &L, uint8_t *base, int n_tok, const Dest 
     if (n_tok <= 0)
         return hipSuccess;
     const bool at_len = D.block_ids == nullptr;
-    if (!at_len && L.head_dim % 32 == 0 && L.head_dim <= kRowMaxHd) {
+    // the row kernel reads K/V 16 bytes at a time: inputs of any other
+    // alignment (a caller's float pointer) take the per-element kernels
+    const bool aligned16 = ((uintptr_t)k % 16 == 0) && ((uintptr_t)v % 16 == 0);
+    if (!at_len && aligned16 && L.head_dim % 32 == 0 && L.head_dim <= kRowMaxHd) {
         dim3 rgrid((unsigned)((n_tok + kRowTok - 1) / kRowTok), (unsigned)L.num_kv_heads);
 #define GI_ROWS(KT) hipLaunchKernelGGL((append_rows<KT>), rgrid, dim3(kThreads), 0, st, L, base, n_tok, D, k, v, status)
         switch (L.kv_type) {

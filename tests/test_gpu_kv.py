@@ -69,6 +69,37 @@ def test_bulk_append_bit_exact(gi, oracle, dev, kv_type, shape):
         assert np.array_equal(vo.cpu().numpy(), vs), i
 
 
+@pytest.mark.parametrize("kv_type", [0, 1, 2, 3], ids=["f32", "f16", "q8_0", "q4_0"])
+def test_append_unaligned_inputs(gi, oracle, dev, kv_type):
+    """K/V inputs that start 4 bytes past a 16-byte boundary (a caller's
+    float pointer) take the per-element append; the stored bytes equal the
+    oracle's KVCache.Write all the same."""
+    import torch
+    kvh, hd, P = SHAPES["llama8b"]
+    kv_dim = kvh * hd
+    n = 100
+    pages = (n + P - 1) // P + 2
+    mgr = gi.PagedKVManager(1, kv_dim, pages, P)
+    pool = gi.PagedKVCache(1, kvh, hd, P, pages, kv_type)
+    sid = mgr.AllocateSequence()
+    ids, slots = mgr.AppendTokens(sid, n)
+    k = oracle.normal(51, (n, kv_dim))
+    v = oracle.normal(52, (n, kv_dim))
+    kb = torch.zeros(n * kv_dim + 1, device=dev)
+    vb = torch.zeros(n * kv_dim + 1, device=dev)
+    kb[1:] = torch.from_numpy(k.reshape(-1)).to(dev)
+    vb[1:] = torch.from_numpy(v.reshape(-1)).to(dev)
+    ku, vu = kb[1:].view(n, kv_dim), vb[1:].view(n, kv_dim)
+    assert ku.data_ptr() % 16 == 4
+    pool.Write(0, torch.from_numpy(ids).to(dev), torch.from_numpy(slots).to(dev), ku, vu)
+    t = torch.tensor(mgr.Tables[sid].BlockIDs, dtype=torch.int32, device=dev)
+    ko, vo = pool.Get(0, t, n)
+    pool.synchronize()
+    assert np.array_equal(ko.cpu().numpy(), oracle.store_vectors(kv_type, k))
+    assert np.array_equal(vo.cpu().numpy(), oracle.store_vectors(kv_type, v))
+    pool.close()
+
+
 def test_reference_kvcache_tests_on_pages(gi, oracle, dev):
     import torch
     # kvcache_test.go:7-71 values i+1 / 2(i+1) and engine_test.go:251-273
