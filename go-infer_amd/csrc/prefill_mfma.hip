@@ -842,12 +842,53 @@ __device__ __forceinline__ void plane_load(const PrefillArgs &a, int kvh, int st
     }
 }
 
-// Dequantises the chunks of plane_load into exact hi + lo fp16 planes of
-// buffer `buf` (the layout stage_store writes); V of tokens whose `vmask`
-// bit is clear is stored as zero.
+// Block scales of the chunks in PlaneRegs: K, one fp16 scale per chunk (the
+// chunk lies in one 32-dimension block of one token); V, the 16 token scales
+// of each chunk's dimension block.  Loaded apart from the codes, so that
+// their latency passes under other work before plane_store needs them.
+template <int HD, int KT>
+struct PlaneScales {
+    static constexpr int NC = PlaneRegs<HD, KT>::NC;
+    // V scales early as well (q8_0: a few registers spill to scratch, 397
+    // against 387 TFLOP/s with its V scales read in plane_store)
+    static constexpr bool EARLY_V = true;
+    uint32_t k[NC];
+    u4 v[2 * NC];
+};
+
+template <int PLANE, int HD, int KT, int P>
+__device__ __forceinline__ void plane_scales(const PrefillArgs &a, int kvh, int st, const PlaneRegs<HD, KT> &R,
+                                             PlaneScales<HD, KT> &C)
+{
+    using M = ChunkMap<HD, KT, P>;
+    constexpr int NT = PlaneRegs<HD, KT>::NT;
+    const PoolLayout &L = a.L;
+#pragma unroll
+    for (int c = 0; c < R.NC; c++) {
+        const int ch = st + NT * c;
+        if (PLANE == 0) {
+            const int tk = M::k_tok(ch), col = M::k_col(ch);
+            C.k[c] = reinterpret_cast<const uint16_t *>(a.base + R.page[c] * L.page_bytes + L.ks_off)
+                [((int64_t)kvh * P + tk % P) * (HD / 32) + col / 32];
+        } else if (C.EARLY_V) {
+            const int d = M::v_dim(ch);
+            const u4 *sp = reinterpret_cast<const u4 *>(
+                a.base + R.page[c] * L.page_bytes + L.vs_off +
+                (((int64_t)kvh * (HD / 32) + d / (KT == KV_Q4_0 ? 16 : 32)) * P + M::v_tok(ch)) * 2);
+            C.v[2 * c] = sp[0];
+            C.v[2 * c + 1] = sp[1];
+        }
+    }
+}
+
+// Dequantises the chunks of plane_load, with the scales plane_scales loaded
+// for them, into exact hi + lo fp16 planes of buffer `buf` (the layout
+// stage_store writes); V of tokens whose `vmask` bit is clear is stored as
+// zero.
 template <int PLANE, int HD, int KT, int P, int NBUF>
 __device__ __forceinline__ void plane_store(const PrefillArgs &a, int kvh, int st, int buf, uint64_t vmask,
-                                            const PlaneRegs<HD, KT> &R, Lds<HD, KT, NBUF> &S)
+                                            const PlaneRegs<HD, KT> &R, const PlaneScales<HD, KT> &C,
+                                            Lds<HD, KT, NBUF> &S)
 {
     using M = ChunkMap<HD, KT, P>;
     using G = SwzGeom<HD>;
@@ -858,8 +899,8 @@ __device__ __forceinline__ void plane_store(const PrefillArgs &a, int kvh, int s
         const int ch = st + NT * c;
         if (PLANE == 0) {
             const int tk = M::k_tok(ch), col = M::k_col(ch);
-            const h8 ksp = reinterpret_cast<const _Float16 *>(a.base + R.page[c] * L.page_bytes + L.ks_off)
-                [((int64_t)kvh * P + tk % P) * (HD / 32) + col / 32]; // splat
+            const _Float16 kscale = __builtin_bit_cast(_Float16, (uint16_t)C.k[c]);
+            const h8 ksp = kscale; // splat
             if (KT == KV_Q4_0) {
                 // the chunk is one block: low nibbles are dimensions col ..
                 // col + 15, high nibbles col + 16 .. col + 31
@@ -883,10 +924,17 @@ __device__ __forceinline__ void plane_store(const PrefillArgs &a, int kvh, int s
         } else {
             const int d = M::v_dim(ch), t0 = M::v_seg(ch) * P + M::v_tok(ch); // block-local token
             const uint32_t live = (uint32_t)(vmask >> t0) & 0xFFFFu;
-            const u4 *sp = reinterpret_cast<const u4 *>(
-                a.base + R.page[c] * L.page_bytes + L.vs_off +
-                (((int64_t)kvh * (HD / 32) + d / (KT == KV_Q4_0 ? 16 : 32)) * P + M::v_tok(ch)) * 2);
-            const u4 vs[2] = {sp[0], sp[1]};
+            u4 vs[2];
+            if (C.EARLY_V) {
+                vs[0] = C.v[2 * c];
+                vs[1] = C.v[2 * c + 1];
+            } else {
+                const u4 *sp = reinterpret_cast<const u4 *>(
+                    a.base + R.page[c] * L.page_bytes + L.vs_off +
+                    (((int64_t)kvh * (HD / 32) + d / (KT == KV_Q4_0 ? 16 : 32)) * P + M::v_tok(ch)) * 2);
+                vs[0] = sp[0];
+                vs[1] = sp[1];
+            }
             // q4_0: byte row d = 16 db + r holds dimension 32 db + r (low
             // nibble) and 32 db + 16 + r (high nibble) of 16 tokens
             const int dl = KT == KV_Q4_0 ? 32 * (d >> 4) + (d & 15) : d;
@@ -1639,9 +1687,12 @@ struct PingPong {
                 zero_dead_v<HD, 64 * NW>(S, cur, mask_c, W.tid);
                 __syncthreads();
             }
-            // phase 2
-            issue_k<HD, P, NW>(a, W.kvh, W.w, W.lane, tbk, S, cur);     // block n + 2
-            issue_v<HD, P, NW>(a, W.kvh, W.w, W.lane, tbv, S, cur ^ 1); // block n + 1
+            // phase 2: group A issues the direct loads before its softmax,
+            // which reads no LDS; B's products read LDS with none in flight
+            if (!GB) {
+                issue_k<HD, P, NW / 2>(a, W.kvh, W.w, W.lane, tbk, S, cur);     // block n + 2
+                issue_v<HD, P, NW / 2>(a, W.kvh, W.w, W.lane, tbv, S, cur ^ 1); // block n + 1
+            }
             const uint64_t mask_nn = W.valid_mask(a, tbk, base + 2 * kTB);
             tbv = tbk;
             tbk = W.table(base + 3 * kTB);
@@ -1746,18 +1797,22 @@ struct PingPongQ {
                     A.qk_block(S, cur, s, W.j, W.g);
                 __builtin_amdgcn_s_setprio(0);
             } else {
+                PlaneScales<HD, KT> C;
+                plane_scales<0, HD, KT, P>(a, W.kvh, st, R, C); // in flight during the softmax
                 if (live(base))
                     A.template softmax_block<FULL>(s, base, mask_c, W.g);
-                plane_store<0, HD, KT, P, 2>(a, W.kvh, st, cur ^ 1, 0, R, S); // K of block n + 1
-                plane_load<0, HD, KT, P>(a, W.kvh, st, tb2, R);                // K of block n + 2
+                plane_store<0, HD, KT, P, 2>(a, W.kvh, st, cur ^ 1, 0, R, C, S); // K of block n + 1
+                plane_load<0, HD, KT, P>(a, W.kvh, st, tb2, R);                   // K of block n + 2
             }
             __syncthreads();
             // phase 2
             if (!GB) {
+                PlaneScales<HD, KT> C;
+                plane_scales<1, HD, KT, P>(a, W.kvh, st, R, C); // in flight during the softmax
                 if (live(base))
                     A.template softmax_block<FULL>(s, base, mask_c, W.g);
-                plane_store<1, HD, KT, P, 2>(a, W.kvh, st, cur ^ 1, mask_n, R, S); // V of block n + 1
-                plane_load<1, HD, KT, P>(a, W.kvh, st, tb2, R);                     // V of block n + 2
+                plane_store<1, HD, KT, P, 2>(a, W.kvh, st, cur ^ 1, mask_n, R, C, S); // V of block n + 1
+                plane_load<1, HD, KT, P>(a, W.kvh, st, tb2, R);                        // V of block n + 2
             } else {
                 __builtin_amdgcn_s_setprio(1);
                 if (live(base))
@@ -1800,13 +1855,16 @@ __global__ __launch_bounds__(512) void attn_prefill_ppq(PrefillArgs a)
     const uint64_t mask_c = W.valid_mask(a, tb0, 0);
     const uint64_t mask_n = W.valid_mask(a, tb1, kTB);
     PlaneRegs<HD, KT> R;
+    PlaneScales<HD, KT> C;
     if (gb) {
         plane_load<0, HD, KT, P>(a, W.kvh, st, tb0, R);
-        plane_store<0, HD, KT, P, 2>(a, W.kvh, st, 0, 0, R, S);
+        plane_scales<0, HD, KT, P>(a, W.kvh, st, R, C);
+        plane_store<0, HD, KT, P, 2>(a, W.kvh, st, 0, 0, R, C, S);
         plane_load<0, HD, KT, P>(a, W.kvh, st, tb1, R);
     } else {
         plane_load<1, HD, KT, P>(a, W.kvh, st, tb0, R);
-        plane_store<1, HD, KT, P, 2>(a, W.kvh, st, 0, mask_c, R, S);
+        plane_scales<1, HD, KT, P>(a, W.kvh, st, R, C);
+        plane_store<1, HD, KT, P, 2>(a, W.kvh, st, 0, mask_c, R, C, S);
         plane_load<1, HD, KT, P>(a, W.kvh, st, tb1, R);
     }
     const int tb2 = W.table(2 * kTB);
