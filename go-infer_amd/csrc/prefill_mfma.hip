@@ -1405,9 +1405,15 @@ struct WaveAttn {
     }
 };
 
-// Work split shared by both staged kernels: the workgroup's columns, the
+// Work split shared by the staged kernels: the workgroup's columns, the
 // context each wave and the workgroup must cover, and the block-table reads.
-template <int P, int NCG, int NW = 4>
+// A tile is the NW * 16 * NCG consecutive columns of one workgroup.  PAIRED
+// (the ping-pong kernels): the first half of the waves take their columns
+// from tile wx and the second half from tile T - 1 - wx (T tiles), so that a
+// short causal range and a long one share each SIMD and every workgroup gets
+// about the same work; each half then decides alone which blocks it sees
+// whole (wg_full is per half).
+template <int P, int NCG, int NW = 4, bool PAIRED = false>
 struct PrefillWork {
     int wx, kvh, b, tid, lane, w, j, g, start, mapped, col0, wave_len, wg_full, wg_len;
     bool wave_active;
@@ -1428,17 +1434,28 @@ struct PrefillWork {
         start = a.start_pos[b];
         bt = a.block_tables + (int64_t)b * a.max_blocks;
         mapped = a.max_blocks * P;
-        col0 = (wx * NW + w) * WCOLS;
-        wave_len = min(start + min((col0 + WCOLS - 1) / G, chunk - 1) + 1, mapped);
-        wg_full = min(start + wx * NW * WCOLS / G + 1, mapped); // shortest column of the workgroup
-        wg_len = min(start + min((wx * NW * WCOLS + NW * WCOLS - 1) / G, chunk - 1) + 1, mapped);
+        auto len = [&](int col) { return min(start + min(col / G, chunk - 1) + 1, mapped); };
+        if (PAIRED) {
+            const int ta = wx, tb = gridDim.x - 1 - wx; // tiles of the two halves
+            const int t = w < NW / 2 ? ta : tb;
+            col0 = (t * NW + w) * WCOLS;
+            // shortest column of this half
+            wg_full = min(start + (t * NW + (w < NW / 2 ? 0 : NW / 2)) * WCOLS / G + 1, mapped);
+            wg_len = max(len((ta * NW + NW / 2) * WCOLS - 1), len((tb * NW + NW) * WCOLS - 1));
+        } else {
+            col0 = (wx * NW + w) * WCOLS;
+            wg_full = min(start + wx * NW * WCOLS / G + 1, mapped); // shortest column of the workgroup
+            wg_len = len(wx * NW * WCOLS + NW * WCOLS - 1);
+        }
+        wave_len = len(col0 + WCOLS - 1);
         wave_active = col0 / G < chunk;
         if (start + chunk > mapped && tid == 0 && a.status)
             atomicOr(a.status, FLAG_BAD_SLOT);
     }
 
-    // Whether the block at `base` is whole for every column of the
-    // workgroup: all its tokens valid and before the shortest column's end.
+    // Whether the block at `base` is whole for every column of the workgroup
+    // (PAIRED: of this wave's half): all its tokens valid and before the
+    // shortest column's end.
     __device__ __forceinline__ bool block_full(int base, uint64_t mask) const
     {
         return mask == ~0ull && base + kTB <= wg_full;
@@ -1653,7 +1670,7 @@ template <int HD, int P, int NCG>
 struct PingPong {
     static constexpr int NW = 8;
     const PrefillArgs &a;
-    const PrefillWork<P, NCG, NW> &W;
+    const PrefillWork<P, NCG, NW, true> &W;
     LdsDirect<HD> &S;
     WaveAttn<HD, KV_F16, NCG> &A;
 
@@ -1725,7 +1742,7 @@ template <int HD, int P, int NCG>
 __global__ __launch_bounds__(512) void attn_prefill_pp(PrefillArgs a)
 {
     constexpr int NW = PingPong<HD, P, NCG>::NW;
-    const PrefillWork<P, NCG, NW> W(a);
+    const PrefillWork<P, NCG, NW, true> W(a);
     __shared__ LdsDirect<HD> S;
     WaveAttn<HD, KV_F16, NCG> A;
     A.init(a, W.b, W.kvh, W.col0, W.start, W.mapped, W.wave_active, W.j, W.g);
@@ -1769,7 +1786,7 @@ template <int HD, int KT, int P, int NCG>
 struct PingPongQ {
     static constexpr int NW = 8;
     const PrefillArgs &a;
-    const PrefillWork<P, NCG, NW> &W;
+    const PrefillWork<P, NCG, NW, true> &W;
     Lds<HD, KT, 2> &S;
     WaveAttn<HD, KT, NCG> &A;
 
@@ -1841,7 +1858,7 @@ template <int HD, int KT, int P, int NCG>
 __global__ __launch_bounds__(512) void attn_prefill_ppq(PrefillArgs a)
 {
     constexpr int NW = PingPongQ<HD, KT, P, NCG>::NW;
-    const PrefillWork<P, NCG, NW> W(a);
+    const PrefillWork<P, NCG, NW, true> W(a);
     __shared__ Lds<HD, KT, 2> S;
     WaveAttn<HD, KT, NCG> A;
     A.init(a, W.b, W.kvh, W.col0, W.start, W.mapped, W.wave_active, W.j, W.g);
