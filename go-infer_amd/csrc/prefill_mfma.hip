@@ -496,14 +496,19 @@ struct SwzGeom {
 
 // Quantised and f32 K and V are stored as hi + lo fp16 pairs (exact for
 // quantised pages, 2^-23 relative for f32 ones), in the swizzled geometry.
-template <int HD, int KT, int NBUF>
+// KC (quantised pages): K is stored as its integer codes instead, exact in
+// fp16, with the block scales beside them ([token][32-dimension block], fp16
+// bits); V keeps its hi + lo planes.
+template <int HD, int KT, int NBUF, bool KC = false>
 struct Lds {
     static constexpr bool Q8 = KT != KV_F16;
+    static constexpr bool KLO = Q8 && !KC;
     using G = SwzGeom<HD>;
     __attribute__((aligned(16))) uint8_t k[NBUF][G::KBYTES];
     __attribute__((aligned(16))) uint8_t v[NBUF][G::VBYTES];
-    __attribute__((aligned(16))) uint8_t kl[Q8 ? NBUF : 1][Q8 ? G::KBYTES : 1]; // K lo
-    __attribute__((aligned(16))) uint8_t vl[Q8 ? NBUF : 1][Q8 ? G::VBYTES : 1]; // V lo
+    __attribute__((aligned(16))) uint8_t kl[KLO ? NBUF : 1][KLO ? G::KBYTES : 1]; // K lo
+    __attribute__((aligned(16))) uint8_t vl[Q8 ? NBUF : 1][Q8 ? G::VBYTES : 1];   // V lo
+    __attribute__((aligned(16))) uint16_t ks[KC ? NBUF : 1][KC ? kTB * (HD / 32) : 1];
 };
 
 // Chunk -> (token, column) of K and (page segment, code row, token group)
@@ -884,11 +889,11 @@ __device__ __forceinline__ void plane_scales(const PrefillArgs &a, int kvh, int 
 // Dequantises the chunks of plane_load, with the scales plane_scales loaded
 // for them, into exact hi + lo fp16 planes of buffer `buf` (the layout
 // stage_store writes); V of tokens whose `vmask` bit is clear is stored as
-// zero.
-template <int PLANE, int HD, int KT, int P, int NBUF>
+// zero.  KC: K is stored as exact fp16 codes, with its scales in S.ks.
+template <int PLANE, int HD, int KT, int P, int NBUF, bool KC>
 __device__ __forceinline__ void plane_store(const PrefillArgs &a, int kvh, int st, int buf, uint64_t vmask,
                                             const PlaneRegs<HD, KT> &R, const PlaneScales<HD, KT> &C,
-                                            Lds<HD, KT, NBUF> &S)
+                                            Lds<HD, KT, NBUF, KC> &S)
 {
     using M = ChunkMap<HD, KT, P>;
     using G = SwzGeom<HD>;
@@ -899,6 +904,24 @@ __device__ __forceinline__ void plane_store(const PrefillArgs &a, int kvh, int s
         const int ch = st + NT * c;
         if (PLANE == 0) {
             const int tk = M::k_tok(ch), col = M::k_col(ch);
+            if (KC) {
+                // the codes, and the scale once per 32-dimension block
+                if (KT == KV_Q4_0) {
+#pragma unroll
+                    for (int m = 0; m < 4; m++) {
+                        const u2 w = u2{R.x[c][2 * (m & 1)], R.x[c][2 * (m & 1) + 1]};
+                        *reinterpret_cast<h8 *>(&S.k[buf][G::kel(tk, col + 8 * m)]) = u4x8_to_h8(w, 4 * (m >> 1));
+                    }
+                } else {
+#pragma unroll
+                    for (int half = 0; half < 2; half++)
+                        *reinterpret_cast<h8 *>(&S.k[buf][G::kel(tk, col + 8 * half)]) =
+                            i8x8_to_h8(u2{R.x[c][2 * half], R.x[c][2 * half + 1]});
+                }
+                if (col % 32 == 0)
+                    S.ks[buf][tk * (HD / 32) + col / 32] = (uint16_t)C.k[c];
+                continue;
+            }
             const _Float16 kscale = __builtin_bit_cast(_Float16, (uint16_t)C.k[c]);
             const h8 ksp = kscale; // splat
             if (KT == KV_Q4_0) {
@@ -970,8 +993,8 @@ __device__ __forceinline__ void plane_store(const PrefillArgs &a, int kvh, int s
 // block, and a compile-time offset, so that the reads use immediate offsets.
 
 // Register-staged layout: the swizzled geometry (SwzGeom), hi and lo planes.
-template <int HD, int KT, int NBUF>
-__device__ __forceinline__ const uint8_t *k_lane(const Lds<HD, KT, NBUF> &S, int buf, int j, int g, bool lo)
+template <int HD, int KT, int NBUF, bool KC>
+__device__ __forceinline__ const uint8_t *k_lane(const Lds<HD, KT, NBUF, KC> &S, int buf, int j, int g, bool lo)
 {
     // row 8(j/4) + j%4 (+ 32h + 4t): segment and row inside it
     using G = SwzGeom<HD>;
@@ -979,20 +1002,20 @@ __device__ __forceinline__ const uint8_t *k_lane(const Lds<HD, KT, NBUF> &S, int
     const int seg = KR == 4 ? 2 * (j >> 2) : (j >> 2);
     return (lo ? S.kl[buf] : S.k[buf]) + seg * G::KSEGB + (j & 3) * HD * 2 + 16 * (g ^ (j & 3));
 }
-template <int HD, int KT, int NBUF>
-__device__ __forceinline__ const uint8_t *v_lane(const Lds<HD, KT, NBUF> &S, int buf, int h, int j, int g,
+template <int HD, int KT, int NBUF, bool KC>
+__device__ __forceinline__ const uint8_t *v_lane(const Lds<HD, KT, NBUF, KC> &S, int buf, int h, int j, int g,
                                                  bool lo)
 {
     return (lo ? S.vl[buf] : S.v[buf]) + (j * kTB + 8 * ((4 * h + g) ^ (j & 7))) * 2;
 }
-template <int HD, int KT, int NBUF>
-__device__ constexpr int k_const(const Lds<HD, KT, NBUF> *, int h, int t, int kk)
+template <int HD, int KT, int NBUF, bool KC>
+__device__ constexpr int k_const(const Lds<HD, KT, NBUF, KC> *, int h, int t, int kk)
 {
     constexpr int KR = SwzGeom<HD>::KROWS, SB = SwzGeom<HD>::KSEGB;
     return (KR == 4 ? (8 * h + t) * SB : 4 * h * SB + 4 * t * HD * 2) + 64 * kk;
 }
-template <int HD, int KT, int NBUF>
-__device__ constexpr int v_const(const Lds<HD, KT, NBUF> *, int nb)
+template <int HD, int KT, int NBUF, bool KC>
+__device__ constexpr int v_const(const Lds<HD, KT, NBUF, KC> *, int nb)
 {
     return 16 * nb * kTB * 2;
 }
@@ -1303,6 +1326,57 @@ struct WaveAttn {
             }
         }
         read_ahead_order<NF, NPR * NCG, NRD, RA>();
+    }
+
+    // Score tiles of the block in K buffer kb from exact K codes (Lds with
+    // KC): per k-step a fresh pair of products (Q hi and lo against the
+    // codes of one 32-dimension block), then one mixed-precision FMA per
+    // score with the block scale of its token, so that QK^T takes two
+    // products per pair instead of three.  A lane's score rows 4g + r of
+    // tile (h, t) are tokens 32h + 8g + 4t + r; their scales are read from
+    // LDS once per tile, a step ahead of its first products.
+    template <class LDS>
+    __device__ __forceinline__ void qk_block_kc(const LDS &S, int kb, f4 (&s)[NCG][2][2], int j, int g) const
+    {
+        const uint8_t *kp = k_lane(S, kb, j, g, false);
+        const uint8_t *sp = reinterpret_cast<const uint8_t *>(&S.ks[kb][8 * g * KK]);
+        constexpr int NF = 4 * KK, RK = 1; // steps: (h, t, kk), kk fastest; read one step ahead
+        auto off = [&](int f) { return k_const(&S, f / (2 * KK), (f / KK) % 2, f % KK); };
+        // tile (h, t) = f / KK: its 4 tokens x KK scales, 8 bytes per token
+        auto soff = [&](int tile) { return (32 * (tile / 2) + 4 * (tile % 2)) * KK * 2; };
+        static_assert(KK == 4, "four scales per token fill 8 bytes");
+        h8 kh[RK + 1];
+        u4 sc[2][2];
+        kh[0] = ld_frag(kp, off(0));
+        sc[0][0] = *reinterpret_cast<const u4 *>(sp + soff(0));
+        sc[0][1] = *reinterpret_cast<const u4 *>(sp + soff(0) + 16);
+        f4 z[NCG];
+#pragma unroll
+        for (int f = 0; f < NF; f++) {
+            const int h = f / (2 * KK), t = (f / KK) % 2, kk = f % KK, tile = f / KK;
+            if (f + RK < NF)
+                kh[(f + RK) % (RK + 1)] = ld_frag(kp, off(f + RK));
+            if (kk == KK - 1 && tile + 1 < 4) {
+                sc[(tile + 1) & 1][0] = *reinterpret_cast<const u4 *>(sp + soff(tile + 1));
+                sc[(tile + 1) & 1][1] = *reinterpret_cast<const u4 *>(sp + soff(tile + 1) + 16);
+            }
+            const h8 ka = kh[f % (RK + 1)];
+#pragma unroll
+            for (int cg = 0; cg < NCG; cg++) {
+                z[cg] = mfma(ka, qh[cg][kk], f4{0.0f, 0.0f, 0.0f, 0.0f});
+                z[cg] = mfma(ka, ql[cg][kk], z[cg]);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                // scale of token row r, block kk: half (r * KK + kk) of the tile's 32 bytes
+                const uint32_t wv = sc[tile & 1][r / 2][(r % 2) * 2 + kk / 2];
+                const h2 hv = __builtin_bit_cast(h2, wv);
+                const float ksc = (float)hv[kk % 2];
+#pragma unroll
+                for (int cg = 0; cg < NCG; cg++)
+                    s[cg][h][t][r] = fmaf(z[cg][r], ksc, kk == 0 ? 0.0f : s[cg][h][t][r]);
+            }
+        }
     }
 
     // Online softmax of the block at `base`: the scores in st are replaced by
@@ -1787,7 +1861,7 @@ struct PingPongQ {
     static constexpr int NW = 8;
     const PrefillArgs &a;
     const PrefillWork<P, NCG, NW, true> &W;
-    Lds<HD, KT, 2> &S;
+    Lds<HD, KT, 2, true> &S;
     WaveAttn<HD, KT, NCG> &A;
 
     __device__ __forceinline__ bool live(int base) const { return W.wave_active && base < W.wave_len; }
@@ -1800,7 +1874,7 @@ struct PingPongQ {
         const int st = W.tid & 255;
         f4 s[NCG][2][2]; // a block's scores, then its P (softmax_block)
         if (GB && live(0))
-            A.qk_block(S, 0, s, W.j, W.g);
+            A.qk_block_kc(S, 0, s, W.j, W.g);
         int n = 0;
         auto step = [&](auto full) {
             constexpr bool FULL = decltype(full)::value;
@@ -1811,7 +1885,7 @@ struct PingPongQ {
                 if (n > 0 && live(base - kTB))
                     A.pv_block(S, cur ^ 1, s, W.j, W.g);
                 if (live(base))
-                    A.qk_block(S, cur, s, W.j, W.g);
+                    A.qk_block_kc(S, cur, s, W.j, W.g);
                 __builtin_amdgcn_s_setprio(0);
             } else {
                 PlaneScales<HD, KT> C;
@@ -1835,7 +1909,7 @@ struct PingPongQ {
                 if (live(base))
                     A.pv_block(S, cur, s, W.j, W.g);
                 if (live(base + kTB))
-                    A.qk_block(S, cur ^ 1, s, W.j, W.g);
+                    A.qk_block_kc(S, cur ^ 1, s, W.j, W.g);
                 __builtin_amdgcn_s_setprio(0);
             }
             const uint64_t mask_nn = W.valid_mask(a, tb2, base + 2 * kTB);
@@ -1859,7 +1933,7 @@ __global__ __launch_bounds__(512) void attn_prefill_ppq(PrefillArgs a)
 {
     constexpr int NW = PingPongQ<HD, KT, P, NCG>::NW;
     const PrefillWork<P, NCG, NW, true> W(a);
-    __shared__ Lds<HD, KT, 2> S;
+    __shared__ Lds<HD, KT, 2, true> S;
     WaveAttn<HD, KT, NCG> A;
     A.init(a, W.b, W.kvh, W.col0, W.start, W.mapped, W.wave_active, W.j, W.g);
     const int nblk = (W.wg_len + kTB - 1) / kTB;
