@@ -211,10 +211,13 @@ struct QBlock {
 // global load fetch long contiguous runs -- the K operand otherwise makes each
 // quarter-wave touch 16 token rows per load -- and the next block's loads
 // need no registers, so they are issued a whole block ahead.
-//   k:  16-byte slot ((kk*2 + t)*16 + j)*NS + (gp ^ x(j)) holds token row
-//       tk_t(j) bytes kk*CB + 16*gp .. + 16 (CB = bytes of 32 codes, NS =
-//       CB / 16, x(j) = (j >> 3) & 1 when NS == 2, else 0: the swizzle keeps
-//       the 8-byte operand reads of j and j + 8 on different banks);
+//   k:  token rows in order, RB bytes each, as the pages hold them; the
+//       16-byte piece p of token t sits at position p ^ m(t) of its row,
+//       m(t) = (t >> 3) & 3 (q4_0) or 2 * ((t >> 3) & 3) (q8_0), cut to the
+//       row's pieces (head_dim 64 has fewer), so that the
+//       operand reads of the 16 token rows of a tile spread over the banks
+//       while every quarter-wave of a load still fetches whole rows (4 rows
+//       of q4_0, 2 of q8_0: two 128-byte lines);
 //   v:  slot (r*16 + j)*2 + (h ^ x(j)) holds the 16 tokens of half h of code
 //       row 16r + j (q8_0: dimension 16r + j; q4_0: the byte row of
 //       dimensions 32r + j and 32r + 16 + j);
@@ -235,23 +238,30 @@ struct QStage {
 
 typedef __attribute__((address_space(3))) void *lds_ptr;
 
-// K codes of a block into the staging area.
+// Swizzle of the 16-byte pieces of K token row t in the staging area (NP
+// pieces per row; a power of two).
+template <int KT, int NP>
+__device__ __forceinline__ int qk_swz(int t)
+{
+    return ((KT == KV_Q4_0 ? 1 : 2) * ((t >> 3) & 3)) & (NP - 1);
+}
+
+// K codes of a block into the staging area: slot sl (16 bytes, lane order)
+// is piece (sl % NP) ^ swizzle of token row sl / NP.
 template <int KT, int HD>
 __device__ __forceinline__ void issue_qk(const DecodeArgs &a, int64_t pA, int64_t pB, int sA, int sB,
                                          int64_t koff, int lane, QStage<KT, HD> &S)
 {
     typedef QStage<KT, HD> Q;
-    constexpr int RB = Q::RB, CB = Q::CB, NS = Q::NS;
+    constexpr int RB = Q::RB, NP = RB / 16;
     const PoolLayout &L = a.L;
     const uint8_t *gA = a.base + pA * L.page_bytes, *gB = a.base + pB * L.page_bytes;
 #pragma unroll
     for (int q = 0; q < Q::NLOAD; q++) {
         const int sl = 64 * q + lane;
-        const int jj = (sl / NS) & 15, kt = sl / (NS * 16);
-        const int gp = NS == 2 ? (sl & 1) ^ ((jj >> 3) & 1) : 0;
-        const int kk = kt >> 1, tk = 8 * (jj >> 2) + (jj & 3) + 4 * (kt & 1);
+        const int tk = sl / NP, pc = (sl % NP) ^ qk_swz<KT, NP>(tk);
         const uint8_t *src = (tk < 16 ? gA + (int64_t)(sA + tk) * RB : gB + (int64_t)(sB + tk - 16) * RB) +
-                             koff + kk * CB + 16 * gp;
+                             koff + 16 * pc;
         __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.k[1024 * q], 16, 0, kDecodeLdsAux);
     }
 }
@@ -308,14 +318,17 @@ template <int KT, int HD>
 __device__ __forceinline__ void read_qk(const QStage<KT, HD> &S, int j, int g, QBlock<KT, HD> &B)
 {
     typedef QStage<KT, HD> Q;
-    constexpr int KK = Q::KK, CB = Q::CB, NS = Q::NS;
-    const int x = (j >> 3) & 1;
+    constexpr int KK = Q::KK, RB = Q::RB;
 #pragma unroll
     for (int kk = 0; kk < KK; kk++)
 #pragma unroll
         for (int t = 0; t < 2; t++) {
-            const int row = (kk * 2 + t) * 16 + j;
-            const int off = NS == 2 ? (row * 2 + ((g >> 1) ^ x)) * 16 + 8 * (g & 1) : row * CB + 8 * (g & 1);
+            // token row of tile t, lane j; the 8 codes of k-step kk for lane
+            // group g: q4_0 piece kk (g >= 2 take its high nibbles), q8_0
+            // piece 2kk + g/2
+            const int tk = 8 * (j >> 2) + (j & 3) + 4 * t;
+            const int pc = KT == KV_Q4_0 ? kk : 2 * kk + (g >> 1);
+            const int off = tk * RB + 16 * (pc ^ qk_swz<KT, RB / 16>(tk)) + 8 * (g & 1);
             const u2 c = *reinterpret_cast<const u2 *>(&S.k[off]);
             if (t)
                 B.k1[kk] = c;
