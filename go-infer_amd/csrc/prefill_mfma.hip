@@ -854,9 +854,6 @@ __device__ __forceinline__ void plane_load(const PrefillArgs &a, int kvh, int st
 template <int HD, int KT>
 struct PlaneScales {
     static constexpr int NC = PlaneRegs<HD, KT>::NC;
-    // V scales early as well (q8_0: a few registers spill to scratch, 397
-    // against 387 TFLOP/s with its V scales read in plane_store)
-    static constexpr bool EARLY_V = true;
     uint32_t k[NC];
     u4 v[2 * NC];
 };
@@ -875,7 +872,7 @@ __device__ __forceinline__ void plane_scales(const PrefillArgs &a, int kvh, int 
             const int tk = M::k_tok(ch), col = M::k_col(ch);
             C.k[c] = reinterpret_cast<const uint16_t *>(a.base + R.page[c] * L.page_bytes + L.ks_off)
                 [((int64_t)kvh * P + tk % P) * (HD / 32) + col / 32];
-        } else if (C.EARLY_V) {
+        } else {
             const int d = M::v_dim(ch);
             const u4 *sp = reinterpret_cast<const u4 *>(
                 a.base + R.page[c] * L.page_bytes + L.vs_off +
@@ -947,17 +944,7 @@ __device__ __forceinline__ void plane_store(const PrefillArgs &a, int kvh, int s
         } else {
             const int d = M::v_dim(ch), t0 = M::v_seg(ch) * P + M::v_tok(ch); // block-local token
             const uint32_t live = (uint32_t)(vmask >> t0) & 0xFFFFu;
-            u4 vs[2];
-            if (C.EARLY_V) {
-                vs[0] = C.v[2 * c];
-                vs[1] = C.v[2 * c + 1];
-            } else {
-                const u4 *sp = reinterpret_cast<const u4 *>(
-                    a.base + R.page[c] * L.page_bytes + L.vs_off +
-                    (((int64_t)kvh * (HD / 32) + d / (KT == KV_Q4_0 ? 16 : 32)) * P + M::v_tok(ch)) * 2);
-                vs[0] = sp[0];
-                vs[1] = sp[1];
-            }
+            const u4 vs[2] = {C.v[2 * c], C.v[2 * c + 1]};
             // q4_0: byte row d = 16 db + r holds dimension 32 db + r (low
             // nibble) and 32 db + 16 + r (high nibble) of 16 tokens
             const int dl = KT == KV_Q4_0 ? 32 * (d >> 4) + (d & 15) : d;
@@ -1282,36 +1269,31 @@ struct WaveAttn {
     // The operand fragments are read from LDS RA steps ahead of their
     // products, so that the products of one group of waves run back to back
     // while the other group is on the vector ALU.  fp16 pages take two
-    // products per operand pair, staged quantised pages three (hi x hi,
-    // lo x hi, hi x lo).
-    static constexpr bool LOP = KT != KV_F16;      // lo planes of K and V
-    static constexpr int NPR = LOP ? 3 : 2;        // products per pair
-    static constexpr int NRD = LOP ? 2 : 1;        // fragment reads per step
+    // products per operand pair; P V on staged quantised pages three (hi x
+    // hi, lo x hi, hi x lo), their scores two (qk_block_kc).
+    static constexpr bool LOP = KT != KV_F16;      // lo plane of V
+    static constexpr int NPR = LOP ? 3 : 2;        // P V products per pair
+    static constexpr int NRD = LOP ? 2 : 1;        // V fragment reads per step
     static constexpr int RA = LOP ? 1 : 2;         // steps read ahead
 
-    // Score tiles of the block in K buffer kb.
+    // Score tiles of the block in K buffer kb (fp16 pages; quantised pages
+    // use qk_block_kc).
     template <class LDS>
     __device__ __forceinline__ void qk_block(const LDS &S, int kb, f4 (&s)[NCG][2][2], int j, int g) const
     {
+        static_assert(KT == KV_F16, "fp16 K operands");
         const uint8_t *kp = k_lane(S, kb, j, g, false);
-        const uint8_t *klp = LOP ? k_lane(S, kb, j, g, true) : kp;
         constexpr int NF = 4 * KK; // steps: (h, t, kk), kk fastest
         auto off = [&](int f) { return k_const(&S, f / (2 * KK), (f / KK) % 2, f % KK); };
-        h8 kh[RA + 1], kl[RA + 1];
+        h8 kh[RA + 1];
 #pragma unroll
-        for (int f = 0; f < RA; f++) {
+        for (int f = 0; f < RA; f++)
             kh[f] = ld_frag(kp, off(f));
-            if (LOP)
-                kl[f] = ld_frag(klp, off(f));
-        }
 #pragma unroll
         for (int f = 0; f < NF; f++) {
             const int h = f / (2 * KK), t = (f / KK) % 2, kk = f % KK;
-            if (f + RA < NF) {
+            if (f + RA < NF)
                 kh[(f + RA) % (RA + 1)] = ld_frag(kp, off(f + RA));
-                if (LOP)
-                    kl[(f + RA) % (RA + 1)] = ld_frag(klp, off(f + RA));
-            }
             const h8 ka = kh[f % (RA + 1)];
             if (kk == 0)
 #pragma unroll
@@ -1321,11 +1303,9 @@ struct WaveAttn {
             for (int cg = 0; cg < NCG; cg++) {
                 s[cg][h][t] = mfma(ka, qh[cg][kk], s[cg][h][t]);
                 s[cg][h][t] = mfma(ka, ql[cg][kk], s[cg][h][t]);
-                if (LOP)
-                    s[cg][h][t] = mfma(kl[f % (RA + 1)], qh[cg][kk], s[cg][h][t]);
             }
         }
-        read_ahead_order<NF, NPR * NCG, NRD, RA>();
+        read_ahead_order<NF, 2 * NCG, 1, RA>();
     }
 
     // Score tiles of the block in K buffer kb from exact K codes (Lds with
