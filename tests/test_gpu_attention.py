@@ -429,6 +429,60 @@ def test_prefill_q8_llama8b_chunks(gi, oracle, dev):
     prefill_case(gi, oracle, dev, 2, 32, 8, 128, 16, [1024, 512], 512, seed=70)
 
 
+@pytest.mark.parametrize("kv_type", [2, 3], ids=["q8_0", "q4_0"])
+def test_prefill_quant_scale_spread(gi, oracle, dev, kv_type):
+    """Quantised pages whose block scales move by up to 3e5 from token to
+    token: K magnitudes cycle through 1e-3 .. 300 with period 5 and V
+    through 1e-2 .. 200 with period 7, so every 32-dimension block of K
+    and every V block row mixes tiny and huge scales.  The matrix-core
+    prefill scales each k-step's product of K codes by its token's block
+    scale and keeps V as exact hi + lo planes; both must hold the 1e-3
+    bound.  Two sequences, 128-query chunks at starts 200 and 64."""
+    import torch
+    H, kvh, hd, P = 32, 8, 128, 16
+    kv_dim = kvh * hd
+    starts, chunk = [200, 64], 128
+    lens = [s + chunk for s in starts]
+    pages = sum((n + P - 1) // P for n in lens) + 2
+    mgr = gi.PagedKVManager(1, kv_dim, pages, P)
+    mgr.SetFreeList(np.random.default_rng(17).permutation(pages).astype(np.int32))
+    pool = gi.PagedKVCache(1, kvh, hd, P, pages, kv_type)
+    kf = np.array([1e-3, 1.0, 300.0, 0.05, 30.0], np.float32)
+    vf = np.array([1.0, 200.0, 1e-2, 3.0, 0.2, 50.0, 0.7], np.float32)
+    tabs, ks, vs = [], [], []
+    for i, n in enumerate(lens):
+        sid = mgr.AllocateSequence()
+        ids, slots = mgr.AppendTokens(sid, n)
+        t = np.arange(n)
+        k = (oracle.normal(1100 + i, (n, kv_dim)) * kf[t % kf.size][:, None]).astype(np.float32)
+        v = (oracle.normal(1150 + i, (n, kv_dim)) * vf[t % vf.size][:, None]).astype(np.float32)
+        pool.Write(0, torch.from_numpy(ids).to(dev), torch.from_numpy(slots).to(dev),
+                   torch.from_numpy(k).to(dev), torch.from_numpy(v).to(dev))
+        ks.append(oracle.widen(kv_type, kv_dim, oracle.store_vectors(kv_type, k)))
+        vs.append(oracle.widen(kv_type, kv_dim, oracle.store_vectors(kv_type, v)))
+        tabs.append(mgr.Tables[sid].BlockIDs)
+    mb = max(len(t) for t in tabs)
+    bt = torch.tensor([t + [0] * (mb - len(t)) for t in tabs], dtype=torch.int32, device=dev)
+    sp = torch.tensor(starts, dtype=torch.int32, device=dev)
+    q = (oracle.normal(1190, (len(starts), chunk, H * hd)) * 0.1).astype(np.float32)
+    qd = torch.from_numpy(q).to(dev)
+    scale = oracle.attn_scale(hd)
+    worst = {}
+    for kern in (0, 1):
+        pool.set_decode_kernel(kern)
+        out = torch.full_like(qd, float("nan"))
+        pool.AttentionGQABatch(out, qd, 0, bt, sp, H, scale, chunk)
+        pool.synchronize()
+        o = out.cpu().numpy()
+        assert np.isfinite(o).all(), kern
+        for i, s0 in enumerate(starts):
+            want = oracle.attention_prefill(q[i], ks[i], vs[i], H, kvh, hd, s0, chunk, 1 << 30, scale)
+            worst[kern] = max(worst.get(kern, 0.0), float(rel_err_rows(o[i], want, H, hd).max()))
+    pool.set_decode_kernel(-1)
+    print("quantised scale-spread prefill max rel err by kernel:", worst)
+    assert max(worst.values()) <= 1e-3, worst
+
+
 def test_decode_short_max_seq_len_attends_every_token(gi, oracle, dev):
     """max_seq_len sizes the split plan only: the last split of a sequence
     runs to its end, so a hint below the real lengths (one frozen at graph
