@@ -1077,12 +1077,62 @@ struct WaveAttn {
     int qlen[NCG];
 
     // Loads Q of columns col0 + 16 cg + j, split into hi + lo halves scaled
-    // per column by 2^qe.
+    // per column by 2^qe.  ONE_PASS: every column group's values are loaded
+    // at once and kept in registers (one memory round trip at the kernel's
+    // start, where every workgroup reads its Q together); otherwise two
+    // passes per group, the second from the caches, so that only 8 values
+    // are live at a time next to the split halves.
+    template <bool ONE_PASS = false>
     __device__ __forceinline__ void init(const PrefillArgs &a, int b, int kvh, int col0, int start,
                                          int mapped, bool active, int j, int g)
     {
         const int H = a.num_heads, G = H / a.L.num_kv_heads, chunk = a.chunk_len;
         neg1 = mfma_ops::opaque_neg1();
+        if (ONE_PASS) {
+            f4 xq[NCG][KK][2];
+#pragma unroll
+            for (int cg = 0; cg < NCG; cg++) {
+                const int c = col0 + 16 * cg + j;
+                const int qi = min(c / G, chunk - 1);
+                qlen[cg] = min(start + qi + 1, mapped);
+                const float *qp = a.q + (((int64_t)b * chunk + qi) * H + kvh * G + c % G) * HD;
+#pragma unroll
+                for (int kk = 0; kk < KK; kk++)
+#pragma unroll
+                    for (int hv = 0; hv < 2; hv++)
+                        xq[cg][kk][hv] = active ? *reinterpret_cast<const f4 *>(qp + 32 * kk + 8 * g + 4 * hv) : f4{};
+            }
+#pragma unroll
+            for (int cg = 0; cg < NCG; cg++) {
+                float mq = 0.0f;
+#pragma unroll
+                for (int kk = 0; kk < KK; kk++)
+#pragma unroll
+                    for (int v = 0; v < 4; v++)
+                        mq = fmaxf(mq, fmaxf(fabsf(xq[cg][kk][0][v]), fabsf(xq[cg][kk][1][v])));
+                mq = fmaxf(mq, __shfl_xor(mq, 16));
+                mq = fmaxf(mq, __shfl_xor(mq, 32));
+                const int qe = pow2_exponent_for(mq);
+                const float up = ldexpf(1.0f, qe);
+                c2s[cg] = a.scale * kLog2e * ldexpf(1.0f, -qe);
+#pragma unroll
+                for (int kk = 0; kk < KK; kk++) {
+                    float x[8];
+#pragma unroll
+                    for (int v = 0; v < 4; v++) {
+                        x[v] = xq[cg][kk][0][v] * up;
+                        x[4 + v] = xq[cg][kk][1][v] * up;
+                    }
+                    split8(x, qh[cg][kk], ql[cg][kk], neg1);
+                }
+                m2[cg] = -INFINITY;
+                lsum[cg] = 0.0f;
+#pragma unroll
+                for (int nb = 0; nb < NB; nb++)
+                    o[cg][nb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+            return;
+        }
 #pragma unroll
         for (int cg = 0; cg < NCG; cg++) {
             const int c = col0 + 16 * cg + j;
@@ -1799,18 +1849,19 @@ __global__ __launch_bounds__(512) void attn_prefill_pp(PrefillArgs a)
     const PrefillWork<P, NCG, NW, true> W(a);
     __shared__ LdsDirect<HD> S;
     WaveAttn<HD, KV_F16, NCG> A;
-    A.init(a, W.b, W.kvh, W.col0, W.start, W.mapped, W.wave_active, W.j, W.g);
     const int nblk = (W.wg_len + kTB - 1) / kTB;
 
-    // prologue: K and V of block 0, K of block 1
+    // prologue: K and V of block 0, K of block 1, in flight while Q is
+    // loaded and split
     const int tb = W.table(0);
-    const uint64_t mask_c = W.valid_mask(a, tb, 0);
+    const int tbv = W.table(kTB); // block whose V is issued next
     issue_k<HD, P, NW>(a, W.kvh, W.w, W.lane, tb, S, 0);
     issue_v<HD, P, NW>(a, W.kvh, W.w, W.lane, tb, S, 0);
-    const int tbv = W.table(kTB); // block whose V is issued next
-    const uint64_t mask_n = W.valid_mask(a, tbv, kTB);
     issue_k<HD, P, NW>(a, W.kvh, W.w, W.lane, tbv, S, 1);
     const int tbk = W.table(2 * kTB); // block whose K is issued next
+    A.template init<true>(a, W.b, W.kvh, W.col0, W.start, W.mapped, W.wave_active, W.j, W.g);
+    const uint64_t mask_c = W.valid_mask(a, tb, 0);
+    const uint64_t mask_n = W.valid_mask(a, tbv, kTB);
     wait_direct_loads();
     __syncthreads();
     if (mask_c != ~0ull) {
@@ -1915,26 +1966,30 @@ __global__ __launch_bounds__(512) void attn_prefill_ppq(PrefillArgs a)
     const PrefillWork<P, NCG, NW, true> W(a);
     __shared__ Lds<HD, KT, 2, true> S;
     WaveAttn<HD, KT, NCG> A;
-    A.init(a, W.b, W.kvh, W.col0, W.start, W.mapped, W.wave_active, W.j, W.g);
     const int nblk = (W.wg_len + kTB - 1) / kTB;
     const bool gb = W.w >= NW / 2;
     const int st = W.tid & 255;
 
     // prologue: both planes of block 0 staged (B: K, A: V), and each group's
-    // plane of block 1 loaded
+    // plane of block 1 loaded; block 0's loads are in flight while Q is
+    // loaded and split
     const int tb0 = W.table(0), tb1 = W.table(kTB);
-    const uint64_t mask_c = W.valid_mask(a, tb0, 0);
-    const uint64_t mask_n = W.valid_mask(a, tb1, kTB);
     PlaneRegs<HD, KT> R;
     PlaneScales<HD, KT> C;
     if (gb) {
         plane_load<0, HD, KT, P>(a, W.kvh, st, tb0, R);
         plane_scales<0, HD, KT, P>(a, W.kvh, st, R, C);
-        plane_store<0, HD, KT, P, 2>(a, W.kvh, st, 0, 0, R, C, S);
-        plane_load<0, HD, KT, P>(a, W.kvh, st, tb1, R);
     } else {
         plane_load<1, HD, KT, P>(a, W.kvh, st, tb0, R);
         plane_scales<1, HD, KT, P>(a, W.kvh, st, R, C);
+    }
+    A.template init<true>(a, W.b, W.kvh, W.col0, W.start, W.mapped, W.wave_active, W.j, W.g);
+    const uint64_t mask_c = W.valid_mask(a, tb0, 0);
+    const uint64_t mask_n = W.valid_mask(a, tb1, kTB);
+    if (gb) {
+        plane_store<0, HD, KT, P, 2>(a, W.kvh, st, 0, 0, R, C, S);
+        plane_load<0, HD, KT, P>(a, W.kvh, st, tb1, R);
+    } else {
         plane_store<1, HD, KT, P, 2>(a, W.kvh, st, 0, mask_c, R, C, S);
         plane_load<1, HD, KT, P>(a, W.kvh, st, tb1, R);
     }
