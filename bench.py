@@ -976,7 +976,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the paged decode path runs on a single MI355X "
-              "(--gpus %d is not supported; sharding is described in DESIGN.md)" % args.gpus,
+              "(--gpus %d is not supported; the kernels shard by sequence or kv head with no "
+              "exchange, which one GPU's share shows)" % args.gpus,
               file=sys.stderr)
         sys.exit(2)
 
