@@ -429,6 +429,17 @@ def test_prefill_q8_llama8b_chunks(gi, oracle, dev):
     prefill_case(gi, oracle, dev, 2, 32, 8, 128, 16, [1024, 512], 512, seed=70)
 
 
+@pytest.mark.parametrize("kv_type", [1, 2, 3], ids=["f16", "q8_0", "q4_0"])
+@pytest.mark.parametrize("P", [32, 64])
+def test_prefill_llama8b_large_pages(gi, oracle, dev, kv_type, P):
+    """Llama-3-8B shape over pages of 32 and 64 tokens with 256-query
+    chunks, so that several tiles of 256 columns pair up in the ping-pong
+    kernels (one per half of a workgroup's waves) and blocks span pages
+    of every size the kernels take; starts 448 and 64, batch 2, inputs
+    with 1 % outliers."""
+    prefill_case(gi, oracle, dev, kv_type, 32, 8, 128, P, [448, 64], 256, seed=90 + kv_type + P)
+
+
 @pytest.mark.parametrize("kv_type", [2, 3], ids=["q8_0", "q4_0"])
 def test_prefill_quant_scale_spread(gi, oracle, dev, kv_type):
     """Quantised pages whose block scales move by up to 3e5 from token to
