@@ -41,6 +41,7 @@
 #include "token_store.h"
 
 #include <math.h>
+#include <type_traits>
 
 namespace gi {
 
@@ -196,13 +197,18 @@ __device__ __forceinline__ float half_at(const u4 *w, int i)
 //              tile nb; q4_0 the byte of dimensions 32*db + j (low nibble,
 //              tile 2*db) and 32*db + 16 + j (high nibble, tile 2*db + 1);
 //   vs[db]:    V scales of block db, tokens 8g .. 8g+7.
-template <int KT, int HD>
+// SPLIT (four heads per kv head): the scores of a block leave the products
+// with tokens 8g .. 8g+3 in lanes j < 8 and 8g+4 .. 8g+7 in lanes j >= 8, and
+// each lane holds the scales of its own four tokens only: ks half t*KK + kk
+// and vs[db] half t for its token t of four.
+template <int KT, int HD, bool SPLIT = false>
 struct QBlock {
     static constexpr int KK = HD / 32;
+    typedef std::conditional_t<SPLIT, u2, u4> VS;
     u2 k0[KK], k1[KK];
-    u4 ks[KK];
+    u4 ks[SPLIT ? KK / 2 : KK];
     u2 v[KT == KV_Q4_0 ? KK : 2 * KK];
-    u4 vs[KK];
+    VS vs[KK];
 };
 
 // One wave's staging area for a block of a quantised page, filled by direct
@@ -314,8 +320,8 @@ constexpr int vmcnt_imm(int n)
 }
 
 // K codes and K scales of the staged block into operand registers.
-template <int KT, int HD>
-__device__ __forceinline__ void read_qk(const QStage<KT, HD> &S, int j, int g, QBlock<KT, HD> &B)
+template <int KT, int HD, bool SPLIT>
+__device__ __forceinline__ void read_qk(const QStage<KT, HD> &S, int j, int g, QBlock<KT, HD, SPLIT> &B)
 {
     typedef QStage<KT, HD> Q;
     constexpr int KK = Q::KK, RB = Q::RB;
@@ -335,23 +341,27 @@ __device__ __forceinline__ void read_qk(const QStage<KT, HD> &S, int j, int g, Q
             else
                 B.k0[kk] = c;
         }
+    // 2*KK bytes per token; SPLIT: lanes j >= 8 start 4 tokens on
+    const int ko = 128 * (g >> 1) + 16 * KK * (g & 1) + (SPLIT && j >= 8 ? 8 * KK : 0);
 #pragma unroll
-    for (int i = 0; i < KK; i++)
-        B.ks[i] = *reinterpret_cast<const u4 *>(&S.ks[128 * (g >> 1) + 16 * KK * (g & 1) + 16 * i]);
+    for (int i = 0; i < (SPLIT ? KK / 2 : KK); i++)
+        B.ks[i] = *reinterpret_cast<const u4 *>(&S.ks[ko + 16 * i]);
 }
 
 // V codes and V scales of the staged block into operand registers.
-template <int KT, int HD>
-__device__ __forceinline__ void read_qv(const QStage<KT, HD> &S, int j, int g, QBlock<KT, HD> &B)
+template <int KT, int HD, bool SPLIT>
+__device__ __forceinline__ void read_qv(const QStage<KT, HD> &S, int j, int g, QBlock<KT, HD, SPLIT> &B)
 {
     constexpr int KK = QStage<KT, HD>::KK;
     const int x = (j >> 3) & 1;
 #pragma unroll
     for (int r = 0; r < (KT == KV_Q4_0 ? KK : 2 * KK); r++)
         B.v[r] = *reinterpret_cast<const u2 *>(&S.v[((r * 16 + j) * 2 + ((g >> 1) ^ x)) * 16 + 8 * (g & 1)]);
+    typedef typename QBlock<KT, HD, SPLIT>::VS VS;
+    const int vo = 128 * (g >> 1) + 16 * (g & 1) + (SPLIT && j >= 8 ? 8 : 0);
 #pragma unroll
     for (int db = 0; db < KK; db++)
-        B.vs[db] = *reinterpret_cast<const u4 *>(&S.vs[128 * (g >> 1) + 32 * db + 16 * (g & 1)]);
+        B.vs[db] = *reinterpret_cast<const VS *>(&S.vs[vo + 32 * db]);
 }
 
 // One wave's staging area for a block of an f32 page, filled by 16-byte
@@ -632,6 +642,36 @@ __device__ __forceinline__ void qk_q(const QBlock<KT, HD> &B, const h8 *qh, cons
     }
 }
 
+// qk_q for four heads per kv head: tile 0 goes through query columns 0-7
+// (qh, zero in 8-15) and tile 1 through columns 8-15 (qh1, the same query
+// moved up 8 columns), into one accumulator per k-step.  Lanes j < 8 then
+// hold tokens 8g .. 8g+3 of column j, lanes j >= 8 tokens 8g+4 .. 8g+7 of
+// column j - 8: every lane's four outputs are scores in use, so the K
+// scales cost four multiply-adds per k-step instead of eight, and the
+// softmax finds its tokens where it needs them.  qz holds each column's
+// start value in both halves.
+template <int KT, int HD>
+__device__ __forceinline__ void qk_q_split(const QBlock<KT, HD, true> &B, const h8 *qh, const h8 *qh1,
+                                           const f4 *qz, int g, f4 &s)
+{
+    constexpr int KK = HD / 32;
+    s = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    const uint32_t km = (g & 2) ? 0x00F000F0u : 0x000F000Fu;
+#pragma unroll
+    for (int kk = 0; kk < KK; kk++) {
+        const h8 a0 = KT == KV_Q4_0 ? u4x8_sub_to_h8(B.k0[kk], km) : i8x8_sub_to_h8(B.k0[kk]);
+        const h8 a1 = KT == KV_Q4_0 ? u4x8_sub_to_h8(B.k1[kk], km) : i8x8_sub_to_h8(B.k1[kk]);
+        f4 z = mfma(a0, qh[kk], qz[kk]);
+        z = mfma(a1, qh1[kk], z);
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+            s[r] = fmaf(z[r], half_at(B.ks, r * KK + kk), s[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+        s[r] += mirror<4>(s[r]);
+}
+
 template <int HD, int GP>
 __device__ __forceinline__ void qk(const h8 *k0, const h8 *k1, const h8 *qh, const h8 *ql, f4 &s0,
                                    f4 &s1)
@@ -772,15 +812,15 @@ __device__ __forceinline__ uint32_t xor8u(uint32_t x)
     return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x128, 0xF, 0xF, true);
 }
 
-// softmax_pv_q for four heads per kv head (packed columns 0-3 hi, 4-7 lo,
-// 8-15 unused).  The unused lanes take half the work: lane j + 8 holds
-// tokens 8g+4 .. 8g+7 of column j, lane j < 8 keeps tokens 8g .. 8g+3, so
-// the softmax and the V-scale fold run on 4 tokens per lane instead of 8.
-// The folded P pairs then go back to the lanes of their operand rows
-// (lanes 8-15 feed P rows 8-15, whose output rows are never read).  A
-// column's running sum is split over lanes j and j + 8; the merge adds them.
+// softmax_pv_q for four heads per kv head (packed columns 0-3 hi, 4-7 lo),
+// on the scores of qk_q_split: lane j < 8 holds tokens 8g .. 8g+3 of column
+// j, lane j + 8 tokens 8g+4 .. 8g+7 of it, so the softmax and the V-scale
+// fold run on 4 tokens per lane instead of 8.  The folded P pairs then go
+// back to the lanes of their operand rows (lanes 8-15 feed P rows 8-15,
+// whose output rows are never read).  A column's running sum is split over
+// lanes j and j + 8; the merge adds them.
 template <int KT, int HD>
-__device__ __forceinline__ void softmax_pv_q4(f4 s0, f4 s1, QBlock<KT, HD> &B, int base, int ok, int t1, int j,
+__device__ __forceinline__ void softmax_pv_q4(f4 s, QBlock<KT, HD, true> &B, int base, int ok, int t1, int j,
                                               int g, float c, State<HD> &S, float &vnorm)
 {
     constexpr int KK = HD / 32, GP = 4;
@@ -788,38 +828,32 @@ __device__ __forceinline__ void softmax_pv_q4(f4 s0, f4 s1, QBlock<KT, HD> &B, i
     const int t_0 = 8 * g + (upper ? 4 : 0); // block-local token of sc[0]
     float sc[4];
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const float moved = xor8(s1[r] * c);
-        sc[r] = upper ? moved : s0[r] * c;
-    }
+    for (int r = 0; r < 4; r++)
+        sc[r] = s[r] * c;
     if (base + 32 > t1 || ok != 3) {
         const bool okg = (ok >> (g >> 1)) & 1; // tokens 8g .. 8g+7
+        // dead tokens: score -inf and V scale 0, as in softmax_pv_q
 #pragma unroll
         for (int r = 0; r < 4; r++)
-            if (!(base + t_0 + r < t1 && okg))
+            if (!(base + t_0 + r < t1 && okg)) {
                 sc[r] = -INFINITY;
-        // scales of dead tokens (all 8 of this lane's group) to 0, as in
-        // softmax_pv_q
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            if (!(base + 8 * g + i < t1 && okg)) {
-                const uint32_t keep = (i & 1) ? 0x0000FFFFu : 0xFFFF0000u;
+                const uint32_t keep = (r & 1) ? 0x0000FFFFu : 0xFFFF0000u;
 #pragma unroll
                 for (int db = 0; db < KK; db++)
-                    B.vs[db][i >> 1] &= keep;
+                    B.vs[db][r >> 1] &= keep;
             }
-        }
     }
     uint32_t mw = 0;
 #pragma unroll
     for (int db = 0; db < KK; db++)
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
+        for (int k = 0; k < 2; k++) {
             const uint32_t e = B.vs[db][k];
             mw = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(us2, mw),
                                                                          __builtin_bit_cast(us2, e)));
         }
     uint32_t mh = max(mw & 0xFFFFu, mw >> 16);
+    mh = max(mh, xor8u(mh));
     mh = max(mh, (uint32_t)__shfl_xor((int)mh, 16));
     mh = max(mh, (uint32_t)__shfl_xor((int)mh, 32));
     float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
@@ -869,7 +903,7 @@ __device__ __forceinline__ void softmax_pv_q4(f4 s0, f4 s1, QBlock<KT, HD> &B, i
     for (int db = 0; db < KK; db++) {
         // the scale words of this lane's 4 tokens (copied out before the
         // bit casts)
-        const uint32_t w0 = upper ? B.vs[db][2] : B.vs[db][0], w1 = upper ? B.vs[db][3] : B.vs[db][1];
+        const uint32_t w0 = B.vs[db][0], w1 = B.vs[db][1];
         const h2 v01 = __builtin_bit_cast(h2, w0), v23 = __builtin_bit_cast(h2, w1);
         const float x0 = fmaf(pp[0], (float)v01[0], 0.0f), x1 = fmaf(pp[1], (float)v01[1], 0.0f);
         const float x2 = fmaf(pp[2], (float)v23[0], 0.0f), x3 = fmaf(pp[3], (float)v23[1], 0.0f);
@@ -900,10 +934,6 @@ __device__ __forceinline__ void softmax_pv_q(f4 s0, f4 s1, QBlock<KT, HD> &B, in
                                              int g, float c, State<HD> &S, float &vnorm)
 {
     constexpr int KK = HD / 32;
-    if constexpr (GP == 4) {
-        softmax_pv_q4<KT, HD>(s0, s1, B, base, ok, t1, j, g, c, S, vnorm);
-        return;
-    }
     float sc[8];
 #pragma unroll
     for (int r = 0; r < 4; r++) {
@@ -1021,6 +1051,9 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
     constexpr int KK = HD / 32, NB = HD / 16;
     constexpr bool QUANT = KT == KV_Q8_0 || KT == KV_Q4_0;
     constexpr bool F32 = KT == KV_F32;
+    // quantised pages, four heads per kv head: the two token tiles of a block
+    // share one score accumulator (qk_q_split)
+    constexpr bool SPLIT = QUANT && GP == 4;
     static_assert(!(QUANT || F32) || GP != 0, "quantised and f32 pages use the packed hi/lo form");
     const PoolLayout &L = a.L;
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
@@ -1124,15 +1157,19 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
     // Q^T operand: column j = head h0 + j (zero beyond the group), k-slot
     // (g, v) of step kk = dimension 32*kk + 8*g + v.
     // Packed: column j < G is q_hi of head j, column 2G-1-j is q_lo of head j.
-    const int qhead = GP == 0 ? j : (j < G ? j : 2 * G - 1 - j);
-    const bool qvalid = GP == 0 ? j < G : j < 2 * G;
-    const bool qlo = GP != 0 && j >= G;
+    // SPLIT: lanes j >= 8 take the query of column j - 8 (qh1, the operand
+    // of the second token tile), so that their scores and scale factor are
+    // those of column j - 8.
+    const int jq = SPLIT ? (j & 7) : j;
+    const int qhead = GP == 0 ? jq : (jq < G ? jq : 2 * G - 1 - jq);
+    const bool qvalid = GP == 0 ? jq < G : jq < 2 * G;
+    const bool qlo = GP != 0 && jq >= G;
     // Each head's query is scaled by 2^qe (from its largest |q|) so both fp16
     // halves stay normal, and the scores are scaled back through c.  The hi
     // and lo columns of a head see the same values, so they pick the same qe.
     // (Loaded by load_q once the wave's first block is in flight, so that the
     // two memory round trips overlap.)
-    h8 qh[KK], ql[KK];
+    h8 qh[KK], ql[KK], qh1[KK];
     f4 qz[KK]; // quantised pages: the initial value of each k-step's product
     float c = 0.0f;
     auto load_q = [&]() {
@@ -1171,7 +1208,9 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
                 const float x = qv[kk][sv] * up;
                 _Float16 hi = (_Float16)x;
                 _Float16 lo = (_Float16)(x - (float)hi);
-                qh[kk][v] = qlo ? lo : hi;
+                const _Float16 q = qlo ? lo : hi;
+                qh[kk][v] = SPLIT && j >= 8 ? (_Float16)0.0f : q;
+                qh1[kk][v] = j >= 8 ? q : (_Float16)0.0f;
                 ql[kk][v] = lo;
             }
         c = a.scale * kLog2e * ldexpf(1.0f, -qe);
@@ -1187,7 +1226,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
                 float t = 0.0f;
 #pragma unroll
                 for (int v = 0; v < 8; v++)
-                    t += (float)qh[kk][v];
+                    t += (float)(SPLIT && j >= 8 ? qh1[kk][v] : qh[kk][v]);
                 t *= fac;
                 t += __shfl_xor(t, 16);
                 t += __shfl_xor(t, 32);
@@ -1255,11 +1294,11 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
             // through the other's work.
             constexpr int NL = QStage<KT, HD>::NLOAD;
             for (;;) {
-                QBlock<KT, HD> B;
+                QBlock<KT, HD, SPLIT> B;
                 // this block's K codes and scales have arrived (its V codes,
                 // the last NL loads issued, may still be in flight)
                 __builtin_amdgcn_s_waitcnt(vmcnt_imm(NL));
-                read_qk<KT, HD>(Sq, j, g, B);
+                read_qk<KT, HD, SPLIT>(Sq, j, g, B);
                 const int next = base + stride;
                 const bool more = next < t1;
                 int64_t nA = pA, nB = pB;
@@ -1274,19 +1313,25 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
                     issue_qk<KT, HD>(a, nA, nB, nsA, nsB, koff, lane, Sq);
                 }
                 f4 s0, s1;
-                qk_q<KT, HD, GP>(B, qh, qz, g, s0, s1);
+                if constexpr (SPLIT)
+                    qk_q_split<KT, HD>(B, qh, qh1, qz, g, s0);
+                else
+                    qk_q<KT, HD, GP>(B, qh, qz, g, s0, s1);
                 // this block's V codes have arrived (the next block's K
                 // codes, issued after them, may still be in flight)
                 if (more)
                     __builtin_amdgcn_s_waitcnt(vmcnt_imm(NL));
                 else
                     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-                read_qv<KT, HD>(Sq, j, g, B);
+                read_qv<KT, HD, SPLIT>(Sq, j, g, B);
                 if (more) {
                     __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0)
                     issue_qv<KT, HD>(a, nA, nB, nsA, nsB, ksoff, voff, vsoff, lane, Sq);
                 }
-                softmax_pv_q<KT, HD, GP>(s0, s1, B, base, ok, t1, j, g, c, S, vnorm);
+                if constexpr (SPLIT)
+                    softmax_pv_q4<KT, HD>(s0, B, base, ok, t1, j, g, c, S, vnorm);
+                else
+                    softmax_pv_q<KT, HD, GP>(s0, s1, B, base, ok, t1, j, g, c, S, vnorm);
                 if (!more)
                     break;
                 pA = nA;
