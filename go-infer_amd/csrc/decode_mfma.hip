@@ -100,10 +100,14 @@ __device__ __forceinline__ void block_pages(const DecodeArgs &a, const int32_t *
     sA = base - ia * P;
     sB = base + 16 - ib * P;
     const const_i32 cb = (const_i32)bt;
-    pA = cb[ia];
-    pB = base + 16 < t1 ? (int64_t)cb[ib] : pA;
-    const bool okA = pA >= 0 && pA < L.num_pages;
-    const bool okB = pB >= 0 && pB < L.num_pages;
+    const int32_t idA = cb[ia], idB = base + 16 < t1 ? cb[ib] : idA;
+    pA = idA;
+    pB = idB;
+    // one unsigned 32-bit compare per id (negative ids wrap above any
+    // limit; a pool of 2^31 pages or more holds every non-negative id)
+    const uint32_t lim = (uint32_t)(L.num_pages < 0x80000000ll ? L.num_pages : 0x80000000ll);
+    const bool okA = (uint32_t)idA < lim;
+    const bool okB = (uint32_t)idB < lim;
     // bit 0: tokens 0-15 of the block are on a page of the pool, bit 1:
     // tokens 16-31; the tokens of a rejected page are skipped
     ok = (okA ? 1 : 0) | (okB ? 2 : 0);
@@ -224,9 +228,10 @@ struct QBlock {
 //       operand reads of the 16 token rows of a tile spread over the banks
 //       while every quarter-wave of a load still fetches whole rows (4 rows
 //       of q4_0, 2 of q8_0: two 128-byte lines);
-//   v:  slot (r*16 + j)*2 + (h ^ x(j)) holds the 16 tokens of half h of code
-//       row 16r + j (q8_0: dimension 16r + j; q4_0: the byte row of
-//       dimensions 32r + j and 32r + 16 + j);
+//   v:  half h (tokens 16h .. 16h+15) in bytes [h, h + 1) * CODE_BYTES / 2,
+//       code row c (q8_0: dimension c; q4_0: the byte row of dimensions
+//       32(c/16) + c%16 and that + 16) at 16c, so that the operand reads
+//       of 32 lanes (16 rows, both 8-byte parts) cover every bank once;
 //   ks: [half][16 tokens][KK halves], 128 bytes per half;
 //   vs: [half][db][16 tokens], 32 bytes per block row, 128 per half.
 template <int KT, int HD>
@@ -253,34 +258,44 @@ __device__ __forceinline__ int qk_swz(int t)
 }
 
 // K codes of a block into the staging area: slot sl (16 bytes, lane order)
-// is piece (sl % NP) ^ swizzle of token row sl / NP.
+// is piece (sl % NP) ^ swizzle of token row sl / NP.  With two or more loads
+// each load reads rows of one page only, so its address is a wave-uniform
+// base (page, slot, kv head) plus a per-lane offset that is the same for
+// every block.
 template <int KT, int HD>
 __device__ __forceinline__ void issue_qk(const DecodeArgs &a, int64_t pA, int64_t pB, int sA, int sB,
                                          int64_t koff, int lane, QStage<KT, HD> &S)
 {
     typedef QStage<KT, HD> Q;
-    constexpr int RB = Q::RB, NP = RB / 16;
+    constexpr int RB = Q::RB, NP = RB / 16, NL = Q::NLOAD;
     const PoolLayout &L = a.L;
-    const uint8_t *gA = a.base + pA * L.page_bytes, *gB = a.base + pB * L.page_bytes;
+    // token 0 of the block, token 16 of the block
+    const uint8_t *gA = a.base + pA * L.page_bytes + koff + (int64_t)sA * RB;
+    const uint8_t *gB = a.base + pB * L.page_bytes + koff + (int64_t)sB * RB;
 #pragma unroll
-    for (int q = 0; q < Q::NLOAD; q++) {
+    for (int q = 0; q < NL; q++) {
         const int sl = 64 * q + lane;
         const int tk = sl / NP, pc = (sl % NP) ^ qk_swz<KT, NP>(tk);
-        const uint8_t *src = (tk < 16 ? gA + (int64_t)(sA + tk) * RB : gB + (int64_t)(sB + tk - 16) * RB) +
-                             koff + 16 * pc;
+        const bool onB = NL >= 2 ? q >= NL / 2 : tk >= 16;
+        const uint32_t off = (uint32_t)((tk - (onB ? 16 : 0)) * RB + 16 * pc);
+        const uint8_t *src = (onB ? gB : gA) + off;
         __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.k[1024 * q], 16, 0, kDecodeLdsAux);
     }
 }
 
 // Both scale planes, then the V codes of a block, into the staging area (in
 // this order: a wait for all but the last NLOAD loads covers the scales).
+// V: half h of the block (tokens 16h .. 16h+15, one page) fills bytes
+// [h * CODE_BYTES / 2, (h + 1) * CODE_BYTES / 2), code row r at 16 r; with two
+// or more loads each load reads one half, so its address is a wave-uniform
+// base plus a per-lane offset.
 template <int KT, int HD>
 __device__ __forceinline__ void issue_qv(const DecodeArgs &a, int64_t pA, int64_t pB, int sA, int sB,
                                          int64_t ksoff, int64_t voff, int64_t vsoff, int lane,
                                          QStage<KT, HD> &S)
 {
     typedef QStage<KT, HD> Q;
-    constexpr int KK = Q::KK;
+    constexpr int KK = Q::KK, NL = Q::NLOAD;
     const PoolLayout &L = a.L;
     const int P = L.page_tokens;
     const uint8_t *gA = a.base + pA * L.page_bytes, *gB = a.base + pB * L.page_bytes;
@@ -294,21 +309,23 @@ __device__ __forceinline__ void issue_qv(const DecodeArgs &a, int64_t pA, int64_
         const uint8_t *pg = h ? gB : gA;
         const int slot = h ? sB : sA;
         // K: 16 tokens x KK halves = 32*KK bytes per half; V: block db of a
-        // half is 16 tokens = 32 bytes, two lanes
+        // half is 16 tokens = 32 bytes, two lanes.  Offsets inside a page
+        // fit 32 bits.
         const int o = 16 * (c & 7), db = (c >> 1) & 3, part = c & 1;
-        const int64_t koffs = ksoff + (int64_t)slot * KK * 2 + o;
-        const int64_t voffs = vsoff + ((int64_t)db * P + slot + 8 * part) * 2;
+        const uint32_t koffs = (uint32_t)ksoff + (uint32_t)(slot * KK * 2 + o);
+        const uint32_t voffs = (uint32_t)vsoff + (uint32_t)((db * P + slot + 8 * part) * 2);
         const uint8_t *src = pg + (lane < 16 ? koffs : voffs);
         const bool use = lane < 16 ? o < 32 * KK : db < KK;
         if (lane < 32 && use)
             __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.ks[0], 16, 0, kDecodeLdsAux);
     }
+    const uint8_t *vA = gA + voff + sA, *vB = gB + voff + sB;
 #pragma unroll
-    for (int q = 0; q < Q::NLOAD; q++) {
-        const int sl = 64 * q + lane;
-        const int jj = (sl >> 1) & 15, r = sl >> 5;
-        const int h = (sl & 1) ^ ((jj >> 3) & 1);
-        const uint8_t *src = (h ? gB + sB : gA + sA) + voff + (int64_t)(16 * r + jj) * P;
+    for (int q = 0; q < NL; q++) {
+        // half h, code row r of it
+        const bool h = NL >= 2 ? q >= NL / 2 : lane >= 32;
+        const int r = NL >= 2 ? 64 * (q % (NL / 2)) + lane : (lane & 31);
+        const uint8_t *src = (h ? vB : vA) + (uint32_t)(r * P);
         __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.v[1024 * q], 16, 0, kDecodeLdsAux);
     }
 }
@@ -352,11 +369,10 @@ __device__ __forceinline__ void read_qk(const QStage<KT, HD> &S, int j, int g, Q
 template <int KT, int HD, bool SPLIT>
 __device__ __forceinline__ void read_qv(const QStage<KT, HD> &S, int j, int g, QBlock<KT, HD, SPLIT> &B)
 {
-    constexpr int KK = QStage<KT, HD>::KK;
-    const int x = (j >> 3) & 1;
+    constexpr int KK = QStage<KT, HD>::KK, HB = QStage<KT, HD>::CODE_BYTES / 2;
 #pragma unroll
     for (int r = 0; r < (KT == KV_Q4_0 ? KK : 2 * KK); r++)
-        B.v[r] = *reinterpret_cast<const u2 *>(&S.v[((r * 16 + j) * 2 + ((g >> 1) ^ x)) * 16 + 8 * (g & 1)]);
+        B.v[r] = *reinterpret_cast<const u2 *>(&S.v[HB * (g >> 1) + 16 * (r * 16 + j) + 8 * (g & 1)]);
     typedef typename QBlock<KT, HD, SPLIT>::VS VS;
     const int vo = 128 * (g >> 1) + 16 * (g & 1) + (SPLIT && j >= 8 ? 8 : 0);
 #pragma unroll
@@ -1057,7 +1073,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
     static_assert(!(QUANT || F32) || GP != 0, "quantised and f32 pages use the packed hi/lo form");
     const PoolLayout &L = a.L;
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int j = lane & 15, g = lane >> 4;
     const int H = a.num_heads, KVH = L.num_kv_heads, G = H / KVH, P = L.page_tokens;
     const int h0 = kvh * G;
