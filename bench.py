@@ -10,9 +10,10 @@ the block table) then paged decode attention over all 8192 tokens.  Inputs
 
 Prints one JSON line (see --help).  Without --config it times the workload
 above, then the other configurations of the baseline -- the TinyLlama batch-1
-case (A), the ragged batch 32 (B), the Llama-3-70B batch 8 x 32768 (D) and the
-q8_0 chunked prefill (E) -- each over at most 10 steps with its parity sample,
-and reports them under "other_configs".  --config selects one shape:
+case (A), the ragged batch 32 (B), the Llama-3-70B batch 8 x 32768 (D), the
+q8_0 chunked prefill (E), and the workload above over Q8_0 and Q4_0 pages
+(C_q8_0, C_q4_0) -- each over at most 10 steps with its parity sample, and
+reports them under "other_configs".  --config selects one shape:
   llama8b_b32         Llama-3-8B shape, batch 32, context U[512, 4096]
   llama70b_b8         Llama-3-70B shape (64 q / 8 kv), page 32, batch 8 x 32768
   llama8b_q8_prefill  Llama-3-8B shape, Q8_0 KV: a 4096-token prefill of batch 4
@@ -1001,7 +1002,8 @@ def main():
 # reference's CPU-runnable case (A), the ragged batch (B), the 70B long-context
 # batch (D) and the q8_0 chunked prefill (E).
 DEFAULT_CONFIG = "llama8b_b256_8k"
-SUITE = (("A", "tinyllama_b1"), ("B", "llama8b_b32"), ("D", "llama70b_b8"), ("E", "llama8b_q8_prefill"))
+SUITE = (("A", "tinyllama_b1"), ("B", "llama8b_b32"), ("D", "llama70b_b8"), ("E", "llama8b_q8_prefill"),
+         ("C_q8_0", "llama8b_b256_8k_q8"), ("C_q4_0", "llama8b_b256_8k_q4"))
 
 
 def run_config(args, gi, torch, dev, name):
