@@ -67,7 +67,7 @@ def run_decode(gi, oracle, dev, kv_type, H, kvh, hd, P, lens, layers=1, seed=1, 
 def test_decode_small_shapes(gi, oracle, dev, kv_type):
     # ragged lengths including 1, page edges and a multi-split sequence
     for (H, kvh, hd, P) in [(32, 4, 64, 16), (32, 8, 128, 16), (64, 8, 128, 32), (8, 8, 128, 16),
-                            (16, 8, 64, 16), (32, 8, 64, 32)]:
+                            (16, 8, 64, 16), (32, 8, 64, 32), (32, 8, 128, 64)]:
         run_decode(gi, oracle, dev, kv_type, H, kvh, hd, P, [1, P, P + 1, 37, 300, 1500],
                    layers=2, seed=3 + kv_type)
 

@@ -26,7 +26,7 @@ def gathered(pop, i):
 
 
 @pytest.mark.parametrize("kv_type", [0, 1, 2, 3], ids=["f32", "f16", "q8_0", "q4_0"])
-@pytest.mark.parametrize("H,kvh,hd,P", [(32, 8, 128, 16), (32, 4, 64, 16), (64, 8, 128, 32)])
+@pytest.mark.parametrize("H,kvh,hd,P", [(32, 8, 128, 16), (32, 4, 64, 16), (64, 8, 128, 32), (32, 8, 128, 64)])
 def test_decode_step_stores_like_the_append(gi, oracle, dev, kv_type, H, kvh, hd, P):
     """Two pools built alike; one takes DecodeStep, the other WriteAtLen then
     AttentionGQA.  Lengths 1, P, P+1, 37, 1500 and 3000 with a 4096-token
