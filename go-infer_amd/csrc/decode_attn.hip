@@ -331,14 +331,16 @@ size_t decode_workspace_bytes(const PoolLayout &L, int batch, int num_heads, int
 
 // Split-K planning: enough (split, kv head, sequence) workgroups for about
 // kDecodeWgPerCu per CU, each split at least kDecodeMinSplit tokens.
-// Measured on MI355X: 2 and 1024 beat finer splits (4/512, 8/256, 16/128) on
-// both 32 ragged sequences of 512-4096 tokens and 8 sequences of 32768, since
-// every workgroup pays a fixed cost (query load, cross-wave merge, partials).
-// A plan that balances equal token ranges over all workgroups regardless of
-// sequence boundaries (with partial slots per range and a merge per
-// sequence) measured 2-10% slower on long and uniform batches and only 5%
-// faster on ragged ones.
-constexpr int kDecodeWgPerCu = 2;
+// Measured on MI355X: 1 and 1024 beat finer splits (2/1024, 4/512, 8/256,
+// 16/128) on 32 ragged sequences of 512-4096 tokens (one workgroup per
+// (sequence, kv head), no merge: 2.79 against 2.93 ms per step) and match
+// 2/1024 on 8 sequences of 32768, since every workgroup pays a fixed cost
+// (query load, cross-wave merge, partials) and a split sequence pays the
+// merge launch.  A plan that balances equal token ranges over all
+// workgroups regardless of sequence boundaries (with partial slots per range
+// and a merge per sequence) measured 2-10% slower on long and uniform
+// batches and only 5% faster on ragged ones.
+constexpr int kDecodeWgPerCu = 1;
 constexpr int kDecodeMinSplit = 1024;
 
 void decode_plan(const PoolLayout &L, int batch, int num_heads, int max_len, int num_cus,

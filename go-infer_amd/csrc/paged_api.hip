@@ -130,7 +130,7 @@ int check_layer(const gi_paged *h, int layer, const char *what)
 // process ends) instead of the handle's growable workspace.  Its name is a
 // host-side stand-in for the array, not a device address: host code uses the
 // address hipGetSymbolAddress gives on each device (scratch_address).
-constexpr size_t kNoAllocScratchBytes = (size_t)8 << 20;
+constexpr size_t kNoAllocScratchBytes = (size_t)4 << 20;
 __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 
 std::mutex g_scratch_mu;

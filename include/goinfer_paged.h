@@ -277,12 +277,14 @@ int gi_paged_decode_attention(gi_paged *h, int layer, int batch, int num_heads, 
 /* gi_paged_decode_attention that allocates nothing.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, hosts that forbid it).  The
- * split partials live in a fixed 8 MiB scratch array that the library holds
+ * split partials live in a fixed 4 MiB scratch array that the library holds
  * on each device it runs on until the process ends, instead of the handle's
  * growable workspace.  On a 256-CU device every shape with up to 8 query
- * heads per kv head fits (at most about 1000 partial slots of 4 KiB); with 16
- * per kv head a few batches (batch * num_kv_heads of 505 to 511) would need
- * up to 8.5 MB and fail with GI_ERR_BAD_ARG before any launch.  Every call
+ * heads per kv head fits (fewer than 512 partial slots of 4 KiB); with 16
+ * per kv head at head_dim 128 the batches with batch * num_kv_heads of 253
+ * to 255 and contexts over 1024 tokens (two splits, 506 to 510 slots of
+ * 8 KiB) would need up to 4.25 MB and fail with GI_ERR_BAD_ARG before any
+ * launch.  Every call
  * on one device shares that array, so calls that overlap on one device
  * (other handles or streams) race: serialise them.  Same arguments and
  * results as gi_paged_decode_attention. */

@@ -88,9 +88,9 @@ def test_decode_and_prefill_graph_replays(gi, oracle, dev, kv_type):
 def test_workspace_growth_keeps_captured_graphs_valid(gi, oracle, dev):
     """The decode workspace (the partials of split sequences) grows with the
     batch and with the query heads per kv head.  A graph captured with 3
-    sequences must keep replaying bit for bit after an eager call with 60
+    sequences must keep replaying bit for bit after an eager call with 24
     sequences grew it (the buffers the graph holds stay alive), and a call
-    that would need it to grow while the stream captures (60 sequences with
+    that would need it to grow while the stream captures (24 sequences with
     twice the heads per kv head) is refused (GI_ERR_BAD_ARG) without
     synchronising or freeing anything; the first graph still replays
     afterwards."""
@@ -132,9 +132,10 @@ def test_workspace_growth_keeps_captured_graphs_valid(gi, oracle, dev):
         assert torch.equal(od, ref), tag
 
     replay_matches("first replay")
-    # eager call with 60 rows and no length hint: 2 splits of 60 x 8
-    # (sequence, kv head) pairs, 20x the partials of the captured call
-    big = 60
+    # eager call with 24 rows and no length hint: 2 splits of 24 x 8
+    # (sequence, kv head) pairs (fewer pairs than CUs), 8x the partials of
+    # the captured call
+    big = 24
     bt_big = bt[torch.arange(big, device=dev) % 3].contiguous()
     sl_big = sl[torch.arange(big, device=dev) % 3].contiguous()
     q_big = qd[torch.arange(big, device=dev) % 3].contiguous()
@@ -148,7 +149,7 @@ def test_workspace_growth_keeps_captured_graphs_valid(gi, oracle, dev):
         assert float(rel_err_rows(got[r], want[r % 3], H, hd).max()) <= 1e-3, r
     replay_matches("replay after growth")
     # growth while capturing is refused: 64 query heads (8 per kv head)
-    # double the partials of the 60-row call
+    # double the partials of the 24-row call
     q64 = torch.zeros((big, 2 * H * hd), device=dev)
     o64 = torch.empty_like(q64)
     g2 = torch.cuda.CUDAGraph()

@@ -46,17 +46,17 @@ def test_noalloc_decode_matches_the_allocating_entry_point(gi, oracle, dev):
 
 
 def test_noalloc_decode_refuses_a_shape_beyond_its_scratch(gi, oracle, dev):
-    """A sequence is cut into splits until there are about two workgroups per
-    CU: with 127 sequences x 4 kv heads that is 2 splits each, 1016 partial
-    slots of 16 heads x (128 + 2) floats, 8.45 MB, beyond the fixed 8 MiB
+    """A sequence is cut into splits until there is about one workgroup per
+    CU: with 253 sequences x 1 kv head that is 2 splits each, 506 partial
+    slots of 16 heads x (128 + 2) floats, 4.21 MB, beyond the fixed 4 MiB
     scratch, and the call is refused before any launch.  (The refusal comes
     before the block tables are read; the rows repeat one sequence.)"""
     import torch
-    H, kvh, hd, P = 64, 4, 128, 16
+    H, kvh, hd, P = 16, 1, 128, 16
     pop = Populated(gi, dev, 1, 1, kvh, hd, P, [1100], seed=43)
     if torch.cuda.get_device_properties(dev).multi_processor_count != 256:
         pytest.skip("the refused shape is worked out for a 256-CU device")
-    B = 127
+    B = 253
     bt = pop.block_tables()[torch.zeros(B, dtype=torch.long, device=dev)].contiguous()
     sl = torch.full((B,), 1100, dtype=torch.int32, device=dev)
     q = torch.zeros((B, H * hd), device=dev)
@@ -64,11 +64,11 @@ def test_noalloc_decode_refuses_a_shape_beyond_its_scratch(gi, oracle, dev):
     with pytest.raises(gi.GIError) as e:
         pop.pool.AttentionGQANoAlloc(out, q, 0, bt, sl, H, oracle.attn_scale(hd))
     assert e.value.code == -3 and "scratch" in str(e.value)
-    # one sequence fewer: 126 x 4 kv heads, 1008 slots, 8.39 MB, fits and
+    # one sequence fewer: 252 x 1 kv head, 504 slots, 4.19 MB, fits and
     # matches the allocating entry point
-    want = torch.full_like(out[:126], float("nan"))
-    got = torch.full_like(out[:126], float("nan"))
-    args = (q[:126].contiguous(), 0, bt[:126].contiguous(), sl[:126].contiguous(), H, oracle.attn_scale(hd))
+    want = torch.full_like(out[:252], float("nan"))
+    got = torch.full_like(out[:252], float("nan"))
+    args = (q[:252].contiguous(), 0, bt[:252].contiguous(), sl[:252].contiguous(), H, oracle.attn_scale(hd))
     pop.pool.AttentionGQA(want, *args)
     pop.pool.AttentionGQANoAlloc(got, *args)
     pop.pool.synchronize()
