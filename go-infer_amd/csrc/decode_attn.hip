@@ -371,7 +371,7 @@ void decode_plan(const PoolLayout &L, int batch, int num_heads, int max_len, int
 
 // Whether a decode step stores its token inside the matrix-core decode
 // launch (DecodeArgs.new_k) rather than in an append launch before it:
-// when the grid is one round of the plan's workgroups per CU.  Measured
+// when the grid fits the CUs at once (two workgroups each).  Measured
 // same-box: batch 32 x U[512, 4096] 2.84 against 2.93 ms per step, 8 x
 // 32768 (page 32) 14.64-14.69 against 14.93-14.97, batch 1 (TinyLlama,
 // one graph) 5,245 against 4,315 tokens/s; but batch 256 x 8192 (four
@@ -379,8 +379,9 @@ void decode_plan(const PoolLayout &L, int batch, int num_heads, int max_len, int
 // more than the append launch it saves.
 bool decode_fuses_append(const PoolLayout &L, int batch, int num_splits, int num_cus)
 {
+    // one round: as many workgroups as the CUs hold at once (two each)
     const int64_t wgs = (int64_t)batch * L.num_kv_heads * (num_splits > 0 ? num_splits : 1);
-    return wgs <= (int64_t)kDecodeWgPerCu * (num_cus > 0 ? num_cus : 256);
+    return wgs <= (int64_t)2 * (num_cus > 0 ? num_cus : 256);
 }
 
 int decode_kernel_kind(const PoolLayout &L, int num_heads, int requested)
