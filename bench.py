@@ -5,8 +5,15 @@ heads, head_dim 128, fp16 KV, 16-token pages, batch 256, every sequence at
 8192 tokens of context, pool fragmented (pages drawn from a shuffled free
 list, then 10 % of the sequences freed and re-allocated).  One step = for
 each of the 32 layers: append the new token's K/V (position 8191, through
-the block table) then paged decode attention over all 8192 tokens.  Inputs
-(q, k, v, block tables, lengths) are resident in HBM before timing.
+the block table) then paged decode attention over all 8192 tokens, through
+the product's decode-step entry point gi_paged_decode_step (which stores the
+token inside the decode launch when the grid fills the CUs once, else in an
+append launch before it).  The same step as two calls (gi_paged_append_at_len
+then gi_paged_decode_attention) is timed beside it ("two_calls"), and once
+more with every launch bracketed by events for the kernels' durations
+(roofline).  The calls are prepared once (PagedKVCache.Prepare), so the host
+time per call is the C ABI's own.  Inputs (q, k, v, block tables, lengths)
+are resident in HBM before timing.
 
 Prints one JSON line (see --help).  Without --config it times the workload
 above, then the other configurations of the baseline -- the TinyLlama batch-1
@@ -1045,10 +1052,13 @@ def run_suite(args, gi, torch, dev):
             "config": name, "workload": r["config"]["workload"], "value": r["value"], "unit": r["unit"],
             "ms_per_step": r["ms_per_step"], "steps": r["steps"], "warmup": r["warmup"],
             "tokens_per_s": r.get("tokens_per_s"),
-            "roofline": {k: roof.get(k) for k in ("bound", "achieved", "peak", "unit", "frac", "kernel",
-                                                 "launch_ms") if k in roof} or None,
+            "roofline": {k: roof.get(k) for k in ("bound", "achieved", "peak", "unit", "frac", "traffic",
+                                                 "traffic_source", "kernel", "launch_ms") if k in roof} or None,
             "parity": {k: par.get(k) for k in ("max_rel_err", "tol", "pass") if k in par} or None,
         }
+        for k in ("step_entry_point", "token_store", "two_calls"):
+            if k in r:
+                out[letter][k] = r[k]
     return out
 
 
@@ -1090,44 +1100,80 @@ def run_decode(args, gi, torch, dev, cfg, name):
     if rope:
         pool.SetRoPE(rope, 0, max_len)
 
-    def step(record=None):
+    # The calls of one step, checked and converted once (Prepare), so that the
+    # host time per call is the C ABI's own, as for a compiled caller:
+    # - the product's decode step per layer (gi_paged_decode_step, or
+    #   gi_paged_rope_decode_step): one launch where the grid fits the CUs
+    #   once, else an append launch and the attention launch;
+    # - the two-call form: the append (gi_paged_append_at_len, with RoPE
+    #   gi_paged_rope_append_at_len), then gi_paged_decode_attention.
+    # q is turned in place at position seq_lens-1 when RoPE is on.
+    prod, app, att = [], [], []
+    for l in range(layers):
+        if rope:
+            prod.append(pool.Prepare("RoPEDecodeStep", out[l], q[l], kn[l], vn[l], l, bt_d, sl_d, H,
+                                     scale, max_len))
+            app.append(pool.Prepare("RoPEWriteAtLen", l, bt_d, sl_d, q[l], kn[l], vn[l]))
+        else:
+            prod.append(pool.Prepare("DecodeStep", out[l], q[l], kn[l], vn[l], l, bt_d, sl_d, H, scale,
+                                     max_len))
+            app.append(pool.Prepare("WriteAtLen", l, bt_d, sl_d, kn[l], vn[l]))
+        att.append(pool.Prepare("AttentionGQA", out[l], q[l], l, bt_d, sl_d, H, scale, max_len))
+
+    def step_product():
+        for f in prod:
+            f()
+
+    def step_two_calls(record=None):
         for l in range(layers):
             if record is not None:
                 eva[record + l].record(stream)
-            if rope:
-                # q turned in place at position seq_lens-1, k turned and stored
-                pool.RoPEWriteAtLen(l, bt_d, sl_d, q[l], kn[l], vn[l])
-            else:
-                pool.WriteAtLen(l, bt_d, sl_d, kn[l], vn[l])
+            app[l]()
             if record is not None:
                 ev0[record + l].record(stream)
-            pool.AttentionGQA(out[l], q[l], l, bt_d, sl_d, H, scale, max_len)
+            att[l]()
             if record is not None:
                 ev1[record + l].record(stream)
 
+    def timed(fn):
+        """ms per step of fn over args.steps steps: events only around the
+        whole run, none between the launches."""
+        pool.synchronize()
+        torch.cuda.synchronize()
+        s0 = torch.cuda.Event(enable_timing=True)
+        s1 = torch.cuda.Event(enable_timing=True)
+        w0 = time.perf_counter()
+        s0.record(stream)
+        for _ in range(args.steps):
+            fn()
+        s1.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - w0
+        pool.synchronize()
+        return s0.elapsed_time(s1) / args.steps, wall * 1e3 / args.steps
+
     for _ in range(args.warmup):
-        step()
+        step_product()
+        step_two_calls()
+    ms_step, wall_step = timed(step_product)
+    ms_two, _ = timed(step_two_calls)
+    # each launch of the two-call form bracketed by events (an instrumented
+    # run of its own, for the kernels' durations)
     pool.synchronize()
     torch.cuda.synchronize()
-    s0 = torch.cuda.Event(enable_timing=True)
-    s1 = torch.cuda.Event(enable_timing=True)
-    w0 = time.perf_counter()
-    s0.record(stream)
     for i in range(args.steps):
-        step(record=i * layers)
-    s1.record(stream)
+        step_two_calls(record=i * layers)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - w0
     pool.synchronize()
-    ms_step = s0.elapsed_time(s1) / args.steps
     attn_ms = float(np.mean([a.elapsed_time(b) for a, b in zip(ev0, ev1)]))
     app_ms = float(np.mean([a.elapsed_time(b) for a, b in zip(eva, ev0)]))
     attn_bytes, app_bytes = step_bytes(cfg, lens)
     tot_gbs = (attn_bytes + app_bytes) / (ms_step * 1e-3) / 1e9
     attn_gbs = (attn_bytes / layers) / (attn_ms * 1e-3) / 1e9
     tok_s = batch / (ms_step * 1e-3)
-    log("step %.3f ms (wall %.3f ms), attention kernel %.3f ms/launch" %
-        (ms_step, wall * 1e3 / args.steps, attn_ms))
+    fused = bool(pool.decode_step_fuses(batch, H, max_len))
+    log("step %.3f ms (wall %.3f ms; token store %s), two calls %.3f ms, attention kernel %.3f ms/launch" %
+        (ms_step, wall_step, "in the decode launch" if fused else "by an append launch", ms_two, attn_ms))
 
     if args.calibrate_copy:
         n = args.calibrate_copy * 2**20 // 4
@@ -1189,6 +1235,13 @@ def run_decode(args, gi, torch, dev, cfg, name):
                    "fragmented_pool": cfg["frag"], "rope_theta": rope},
         "hbm_frac_of_peak": round(tot_gbs / HBM_PEAK_GBS, 4),
         "tokens_per_s": round(tok_s, 1),
+        "step_entry_point": "gi_paged_rope_decode_step" if rope else "gi_paged_decode_step",
+        "token_store": "in the decode launch" if fused else "append launch",
+        "two_calls": {"entry_points": ["gi_paged_rope_append_at_len" if rope else "gi_paged_append_at_len",
+                                       "gi_paged_decode_attention"],
+                      "ms_per_step": round(ms_two, 4),
+                      "value": round((attn_bytes + app_bytes) / (ms_two * 1e-3) / 1e9, 2),
+                      "tokens_per_s": round(batch / (ms_two * 1e-3), 1)},
         "decode_kernel": ["vector-alu", "matrix-core"][kind],
         "append_kernel": append_kernel_name(gi, kv_dtype, rope),
         "append_ms_per_launch": round(app_ms, 4),

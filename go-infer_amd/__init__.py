@@ -22,6 +22,7 @@ import ctypes
 import os
 
 __all__ = ["lib", "GIError", "PagedKVManager", "PagedKVCache", "PrefixCache", "BatchDecoder", "Weights",
+           "AttentionPlan",
            "GGML_F32", "GGML_F16", "GGML_Q4_0", "GGML_Q8_0", "KV_F32", "KV_F16",
            "KV_Q8_0", "KV_Q4_0", "EXPORTS", "LIB_PATH", "attn_scale"]
 
@@ -38,6 +39,15 @@ ERR_NAMES = {-1: "GI_ERR_NO_DEVICE", -2: "GI_ERR_OOM", -3: "GI_ERR_BAD_ARG",
 _c_int, _c_i64, _vp = ctypes.c_int, ctypes.c_int64, ctypes.c_void_p
 _i32p = ctypes.POINTER(ctypes.c_int32)
 _intp = ctypes.POINTER(ctypes.c_int)
+
+
+
+class AttentionPlan(ctypes.Structure):
+    """gi_attention_plan: the launch plan gi_paged_attention_plan reports."""
+    _fields_ = [(n, ctypes.c_int) for n in (
+        "decode_kernel", "decode_fallback", "decode_splits", "decode_split_tokens", "decode_waves",
+        "decode_step_fused", "prefill_kernel", "prefill_fallback")]
+
 
 # Every symbol include/goinfer_paged.h declares, with its ctypes signature.
 EXPORTS = {
@@ -108,6 +118,7 @@ EXPORTS = {
     "gi_paged_rope_decode_step": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp,
                                            _c_int, _vp, _c_int, ctypes.c_float]),
     "gi_paged_decode_kernel": (_c_int, [_vp, _c_int]),
+    "gi_paged_attention_plan": (_c_int, [_vp, _c_int, _c_int, _c_int, ctypes.POINTER(AttentionPlan)]),
     "gi_paged_set_decode_kernel": (_c_int, [_vp, _c_int]),
 }
 
@@ -359,6 +370,12 @@ def _ptr(t, dtype=None, what="tensor"):
     return _vp(t.data_ptr())
 
 
+def _run(call):
+    """Makes a (C function name, arguments) call and raises on failure."""
+    name, args = call
+    _check(getattr(lib(), name)(*args))
+
+
 def _need(ok, msg):
     """Shape check of a wrapper: a mismatch would send the kernels past the
     ends of the buffers, so it is refused here as GI_ERR_BAD_ARG."""
@@ -443,6 +460,20 @@ class PagedKVCache:
         """0: vector-ALU kernel, 1: matrix-core kernel."""
         return lib().gi_paged_decode_kernel(self._h, num_heads)
 
+    def attention_plan(self, batch, num_heads, max_seq_len=0):
+        """gi_paged_attention_plan as a dict: kernel family, split plan,
+        waves per workgroup and whether the decode step's token store is
+        fused, for this pool and shape (nothing is launched)."""
+        p = AttentionPlan()
+        _check(lib().gi_paged_attention_plan(self._h, int(batch), int(num_heads), int(max_seq_len),
+                                             ctypes.byref(p)))
+        return {n: getattr(p, n) for n, _ in AttentionPlan._fields_}
+
+    def decode_step_fuses(self, batch, num_heads, max_seq_len=0):
+        """Whether gi_paged_decode_step stores the token inside the decode
+        launch for this shape (else in an append launch before it)."""
+        return self.attention_plan(batch, num_heads, max_seq_len)["decode_step_fused"] == 1
+
     def set_decode_kernel(self, kind):
         """-1 automatic, 0 vector ALU, 1 matrix core where supported."""
         _check(lib().gi_paged_set_decode_kernel(self._h, kind))
@@ -461,15 +492,18 @@ class PagedKVCache:
                                      _ptr(k, torch.float32, "k"), _ptr(v, torch.float32, "v")))
 
     def WriteAtLen(self, layer, block_tables, seq_lens, k, v):
+        _run(self._write_at_len(layer, block_tables, seq_lens, k, v))
+
+    def _write_at_len(self, layer, block_tables, seq_lens, k, v):
         import torch
         batch = int(seq_lens.numel())
         mb = _tables(block_tables, batch)
         _need(_numel(k) == batch * self.kv_dim and _numel(v) == batch * self.kv_dim,
               "WriteAtLen: k and v must be [%d, %d]" % (batch, self.kv_dim))
-        _check(lib().gi_paged_append_at_len(
-            self._h, layer, batch, _ptr(block_tables, torch.int32, "block_tables"),
-            mb, _ptr(seq_lens, torch.int32, "seq_lens"),
-            _ptr(k, torch.float32, "k"), _ptr(v, torch.float32, "v")))
+        return ("gi_paged_append_at_len",
+                (self._h, layer, batch, _ptr(block_tables, torch.int32, "block_tables"),
+                 mb, _ptr(seq_lens, torch.int32, "seq_lens"),
+                 _ptr(k, torch.float32, "k"), _ptr(v, torch.float32, "v")))
 
     def Get(self, layer, block_table, n_tok, widen=False):
         """Contiguous K, V of tokens [0, n_tok) (KVCache.Get/ForkAt layout).
@@ -503,6 +537,11 @@ class PagedKVCache:
                      max_seq_len=None):
         """Decode attention of forward.go:242-267 for a batch; q/out
         [batch, num_heads*head_dim] float32."""
+        _run(self._attention_gqa(out, q, layer, block_tables, seq_lens, num_heads, attn_scale,
+                                 max_seq_len))
+
+    def _attention_gqa(self, out, q, layer, block_tables, seq_lens, num_heads, attn_scale,
+                       max_seq_len=None):
         import torch
         batch = int(seq_lens.numel())
         mb = _tables(block_tables, batch)
@@ -511,11 +550,11 @@ class PagedKVCache:
               "AttentionGQA: q and out must be [%d, %d]" % (batch, num_heads * self.head_dim))
         if max_seq_len is None:
             max_seq_len = 0   # the kernels read the lengths on the device
-        _check(lib().gi_paged_decode_attention(
-            self._h, layer, batch, num_heads, _ptr(q, torch.float32, "q"),
-            _ptr(out, torch.float32, "out"), _ptr(block_tables, torch.int32, "block_tables"),
-            mb, _ptr(seq_lens, torch.int32, "seq_lens"),
-            int(max_seq_len), float(attn_scale)))
+        return ("gi_paged_decode_attention",
+                (self._h, layer, batch, num_heads, _ptr(q, torch.float32, "q"),
+                 _ptr(out, torch.float32, "out"), _ptr(block_tables, torch.int32, "block_tables"),
+                 mb, _ptr(seq_lens, torch.int32, "seq_lens"),
+                 int(max_seq_len), float(attn_scale)))
 
     def AttentionGQANoAlloc(self, out, q, layer, block_tables, seq_lens, num_heads, attn_scale,
                             max_seq_len=None):
@@ -536,6 +575,11 @@ class PagedKVCache:
                    max_seq_len=None):
         """Append the new token at position seq_lens[b]-1, then decode
         attention over seq_lens[b] tokens (forward.go:236-267)."""
+        _run(self._decode_step(out, q, k, v, layer, block_tables, seq_lens, num_heads, attn_scale,
+                               max_seq_len))
+
+    def _decode_step(self, out, q, k, v, layer, block_tables, seq_lens, num_heads, attn_scale,
+                     max_seq_len=None):
         import torch
         batch = int(seq_lens.numel())
         mb = _tables(block_tables, batch)
@@ -546,12 +590,12 @@ class PagedKVCache:
               "DecodeStep: k and v must be [%d, %d]" % (batch, self.kv_dim))
         if max_seq_len is None:
             max_seq_len = 0
-        _check(lib().gi_paged_decode_step(
-            self._h, layer, batch, num_heads, _ptr(q, torch.float32, "q"),
-            _ptr(k, torch.float32, "k"), _ptr(v, torch.float32, "v"),
-            _ptr(out, torch.float32, "out"), _ptr(block_tables, torch.int32, "block_tables"),
-            mb, _ptr(seq_lens, torch.int32, "seq_lens"),
-            int(max_seq_len), float(attn_scale)))
+        return ("gi_paged_decode_step",
+                (self._h, layer, batch, num_heads, _ptr(q, torch.float32, "q"),
+                 _ptr(k, torch.float32, "k"), _ptr(v, torch.float32, "v"),
+                 _ptr(out, torch.float32, "out"), _ptr(block_tables, torch.int32, "block_tables"),
+                 mb, _ptr(seq_lens, torch.int32, "seq_lens"),
+                 int(max_seq_len), float(attn_scale)))
 
     # -- RoPE fused with the append (forward.go:228-240, 527-545) ------------
     def SetRoPE(self, theta, rope_dim=0, max_positions=8192):
@@ -583,6 +627,9 @@ class PagedKVCache:
 
     def RoPEWriteAtLen(self, layer, block_tables, seq_lens, q, k, v, q_out=None):
         """Decode form: token b at position seq_lens[b]-1 of sequence b."""
+        _run(self._rope_write_at_len(layer, block_tables, seq_lens, q, k, v, q_out))
+
+    def _rope_write_at_len(self, layer, block_tables, seq_lens, q, k, v, q_out=None):
         import torch
         batch = int(seq_lens.numel())
         mb = _tables(block_tables, batch)
@@ -595,16 +642,21 @@ class PagedKVCache:
                   "RoPEWriteAtLen: q and q_out must be [%d, num_heads * %d]" % (batch, self.head_dim))
         _need(_numel(k) == batch * self.kv_dim and _numel(v) == batch * self.kv_dim,
               "RoPEWriteAtLen: k and v must be [%d, %d]" % (batch, self.kv_dim))
-        _check(lib().gi_paged_rope_append_at_len(
-            self._h, layer, batch, num_heads, _ptr(block_tables, torch.int32, "block_tables"),
-            mb, _ptr(seq_lens, torch.int32, "seq_lens"),
-            _ptr(q, torch.float32, "q"), _ptr(q_out, torch.float32, "q_out"),
-            _ptr(k, torch.float32, "k"), _ptr(v, torch.float32, "v")))
+        return ("gi_paged_rope_append_at_len",
+                (self._h, layer, batch, num_heads, _ptr(block_tables, torch.int32, "block_tables"),
+                 mb, _ptr(seq_lens, torch.int32, "seq_lens"),
+                 _ptr(q, torch.float32, "q"), _ptr(q_out, torch.float32, "q_out"),
+                 _ptr(k, torch.float32, "k"), _ptr(v, torch.float32, "v")))
 
     def RoPEDecodeStep(self, out, q, k, v, layer, block_tables, seq_lens, num_heads, attn_scale,
                        max_seq_len=None):
         """forward.go:228-267 for a batch: q (rotated in place) and k turned
         at position seq_lens[b]-1, k/v appended, then decode attention."""
+        _run(self._rope_decode_step(out, q, k, v, layer, block_tables, seq_lens, num_heads,
+                                    attn_scale, max_seq_len))
+
+    def _rope_decode_step(self, out, q, k, v, layer, block_tables, seq_lens, num_heads, attn_scale,
+                          max_seq_len=None):
         import torch
         batch = int(seq_lens.numel())
         mb = _tables(block_tables, batch)
@@ -615,12 +667,36 @@ class PagedKVCache:
               "RoPEDecodeStep: k and v must be [%d, %d]" % (batch, self.kv_dim))
         if max_seq_len is None:
             max_seq_len = 0
-        _check(lib().gi_paged_rope_decode_step(
-            self._h, layer, batch, num_heads, _ptr(q, torch.float32, "q"),
-            _ptr(k, torch.float32, "k"), _ptr(v, torch.float32, "v"),
-            _ptr(out, torch.float32, "out"), _ptr(block_tables, torch.int32, "block_tables"),
-            mb, _ptr(seq_lens, torch.int32, "seq_lens"),
-            int(max_seq_len), float(attn_scale)))
+        return ("gi_paged_rope_decode_step",
+                (self._h, layer, batch, num_heads, _ptr(q, torch.float32, "q"),
+                 _ptr(k, torch.float32, "k"), _ptr(v, torch.float32, "v"),
+                 _ptr(out, torch.float32, "out"), _ptr(block_tables, torch.int32, "block_tables"),
+                 mb, _ptr(seq_lens, torch.int32, "seq_lens"),
+                 int(max_seq_len), float(attn_scale)))
+
+    # -- prepared calls ------------------------------------------------------
+    _PREPARABLE = {"WriteAtLen": "_write_at_len", "AttentionGQA": "_attention_gqa",
+                   "DecodeStep": "_decode_step", "RoPEWriteAtLen": "_rope_write_at_len",
+                   "RoPEDecodeStep": "_rope_decode_step"}
+
+    def Prepare(self, method, *args, **kw):
+        """One of WriteAtLen / AttentionGQA / DecodeStep / RoPEWriteAtLen /
+        RoPEDecodeStep with its arguments checked and converted once: returns
+        a function of no arguments that makes the same C call, as a compiled
+        host repeats a call whose buffers it keeps (each call costs the C
+        ABI's own host time, not the wrapper's checks).  The tensors must
+        stay alive, in place and unchanged in shape while it is used."""
+        if method not in self._PREPARABLE:
+            raise GIError(-3, "Prepare: %s is not one of %s" % (method, sorted(self._PREPARABLE)))
+        name, cargs = getattr(self, self._PREPARABLE[method])(*args, **kw)
+        fn = getattr(lib(), name)
+        conv = tuple(a if isinstance(a, c) else c(a) for c, a in zip(fn.argtypes, cargs))
+
+        def call():
+            rc = fn(*conv)
+            if rc != GI_OK:
+                _check(rc)
+        return call
 
     def AttentionGQABatch(self, out, q, layer, block_tables, start_pos, num_heads, attn_scale,
                           chunk_len):

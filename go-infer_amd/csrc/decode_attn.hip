@@ -384,6 +384,15 @@ bool decode_fuses_append(const PoolLayout &L, int batch, int num_splits, int num
     return wgs <= (int64_t)2 * (num_cus > 0 ? num_cus : 256);
 }
 
+int decode_waves(const PoolLayout &L, int batch, int num_splits, int num_cus)
+{
+    // f32 pages stage 32 KiB per wave in LDS: four waves per workgroup only
+    if (L.kv_type == KV_F32)
+        return 4;
+    const int64_t wgs = (int64_t)batch * L.num_kv_heads * (num_splits > 0 ? num_splits : 1);
+    return wgs <= (num_cus > 0 ? num_cus : 256) ? 8 : 4;
+}
+
 int decode_kernel_kind(const PoolLayout &L, int num_heads, int requested)
 {
     const bool mfma = mfma_decode_supported(L, num_heads);

@@ -20,8 +20,9 @@
 // lanes, and the lane's V operand (dimension 16*nb + j, tokens 8g .. 8g+7) is
 // one contiguous 16-byte run of the dimension-major page.
 //
-// Each of the 4 waves keeps its own running max / sum; the workgroup merges
-// them at the end, and split-K partials are merged by merge_splits.
+// Each of the NW waves of a workgroup (4, or 8 when the grid fills the CUs
+// only once) keeps its own running max / sum; the workgroup merges them at the
+// end, and split-K partials are merged by merge_splits.
 //
 // Quantised pages (q8_0, q4_0) stay exact.  Their integer codes are exact
 // fp16 values (a byte or nibble permute into 0x64XX, then a bias), and one
@@ -1061,7 +1062,7 @@ __device__ __forceinline__ void softmax_pv_q(f4 s0, f4 s1, QBlock<KT, HD> &B, in
 
 // Body of the decode kernels.  KT: KV_F16, or KV_Q8_0 / KV_Q4_0 (packed GP
 // only).
-template <int KT, int HD, int GP, bool NT, bool PREFETCH>
+template <int KT, int HD, int GP, bool NT, bool PREFETCH, int NW>
 __device__ __forceinline__ void decode_body(const DecodeArgs &a)
 {
     constexpr int KK = HD / 32, NB = HD / 16;
@@ -1096,7 +1097,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
     // before it attends (forward.go:236-267), by the workgroup whose token
     // range holds it, for its own kv head.  With pages of up to 32 tokens
     // every cache line of a page belongs to one 32-token block, which one
-    // wave reads (wave w reads blocks t0 + 32w + 128i): that wave stores the
+    // wave reads (wave w reads blocks t0 + 32w + 32*NW*i): that wave stores the
     // token, after issuing its first block's loads unless that is the
     // token's block (the stores wait for the loads of the token's values,
     // which should not hold up the block's loads), and waits for the stores
@@ -1119,7 +1120,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
             if (!okp && threadIdx.x == 0 && a.status)
                 atomicOr(a.status, FLAG_BAD_PAGE);
             if (P <= 32) {
-                if (okp && w == ((pos - t0) >> 5) % 4) {
+                if (okp && w == ((pos - t0) >> 5) % NW) {
                     sblk = __builtin_amdgcn_readfirstlane(t0 + ((pos - t0) & ~31));
                     st_page = pg;
                     st_slot = pos % P;
@@ -1145,19 +1146,19 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
     // after it, the cross-wave merge share one LDS allocation.  (fp16 pages
     // load straight into registers: staging them through LDS measured
     // slower.)
-    constexpr int STAGE_BYTES = QUANT ? 4 * (int)sizeof(QStage<QUANT ? KT : KV_Q8_0, HD>)
-                                : F32 ? 4 * (int)sizeof(F32Stage<HD>) : 0;
-    constexpr int MERGE_BYTES = 4 * 16 * HD * (int)sizeof(float);
+    constexpr int STAGE_BYTES = QUANT ? NW * (int)sizeof(QStage<QUANT ? KT : KV_Q8_0, HD>)
+                                : F32 ? NW * (int)sizeof(F32Stage<HD>) : 0;
+    constexpr int MERGE_BYTES = NW * 16 * HD * (int)sizeof(float);
     __shared__ __align__(16) uint8_t s_stage[STAGE_BYTES > MERGE_BYTES ? STAGE_BYTES : MERGE_BYTES];
     float(*s_o)[16][HD] = reinterpret_cast<float(*)[16][HD]>(s_stage);
-    __shared__ float s_m[4][16], s_l[4][16];
+    __shared__ float s_m[NW][16], s_l[NW][16];
 
     float *wsp = nullptr;
     if (a.num_splits > 1)
         wsp = a.ws + (((int64_t)b * KVH + kvh) * a.num_splits + split) * (G * (HD + 2));
 
     if (t0 >= t1) {
-        for (int e = threadIdx.x; e < G * HD; e += 256) {
+        for (int e = threadIdx.x; e < G * HD; e += 64 * NW) {
             if (wsp)
                 wsp[e] = 0.0f;
             else
@@ -1267,7 +1268,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
     const int64_t koff = L.k_off + (int64_t)kvh * P * HD * EB_NUM / EB_DEN;
     const int64_t voff = L.v_off + (int64_t)kvh * HD * P * EB_NUM / EB_DEN;
     const int32_t *bt = a.block_tables + (int64_t)b * a.max_blocks;
-    const int stride = 32 * 4;
+    const int stride = 32 * NW;
 
     // Block starts are wave-uniform (scalar registers), so the loop test is a
     // scalar branch.  Every block but the last runs inside the loop, where
@@ -1485,15 +1486,15 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
         }
     __syncthreads();
 
-    for (int e = threadIdx.x; e < G * HD; e += 256) {
+    for (int e = threadIdx.x; e < G * HD; e += 64 * NW) {
         const int hh = e / HD, d = e - hh * HD;
         float M = s_m[0][hh];
 #pragma unroll
-        for (int x = 1; x < 4; x++)
+        for (int x = 1; x < NW; x++)
             M = fmaxf(M, s_m[x][hh]);
         float num = 0.0f, den = 0.0f;
 #pragma unroll
-        for (int x = 0; x < 4; x++) {
+        for (int x = 0; x < NW; x++) {
             const float mx2 = s_m[x][hh];
             const float f = mx2 == -INFINITY ? 0.0f : exp2f(mx2 - M);
             float o = s_o[x][hh][d];
@@ -1518,25 +1519,26 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
 // or the group size G in {1, 2, 4, 8} for the packed form.  NT:
 // non-temporal (streaming) loads of K/V.  PREFETCH: the next block's loads
 // are issued as soon as this block's K (then V) registers are consumed.
-// OCC: minimum waves per SIMD requested from the register allocator.
-template <int HD, int GP, bool NT, bool PREFETCH, int OCC>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void attn_mfma_f16(DecodeArgs a)
+// OCC: minimum waves per SIMD requested from the register allocator.  NW:
+// waves per workgroup (DecodeArgs.waves).
+template <int HD, int GP, bool NT, bool PREFETCH, int OCC, int NW = 4>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(OCC))) void attn_mfma_f16(DecodeArgs a)
 {
-    decode_body<KV_F16, HD, GP, NT, PREFETCH>(a);
+    decode_body<KV_F16, HD, GP, NT, PREFETCH, NW>(a);
 }
 
 // f32 pages, packed form (GP = G in {1, 2, 4, 8}).
 template <int HD, int GP, bool NT, bool PREFETCH, int OCC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void attn_mfma_f32(DecodeArgs a)
 {
-    decode_body<KV_F32, HD, GP, NT, PREFETCH>(a);
+    decode_body<KV_F32, HD, GP, NT, PREFETCH, 4>(a);
 }
 
 // q8_0 / q4_0 pages, packed form (GP = G in {1, 2, 4, 8}).
-template <int KT, int HD, int GP, bool NT, bool PREFETCH, int OCC>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void attn_mfma_q(DecodeArgs a)
+template <int KT, int HD, int GP, bool NT, bool PREFETCH, int OCC, int NW = 4>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(OCC))) void attn_mfma_q(DecodeArgs a)
 {
-    decode_body<KT, HD, GP, NT, PREFETCH>(a);
+    decode_body<KT, HD, GP, NT, PREFETCH, NW>(a);
 }
 
 } // namespace mfma_decode
@@ -1569,9 +1571,12 @@ constexpr bool kDecodePack = true;
 template <int HD, int GP>
 static void launch_mfma_hd(const DecodeArgs &a, dim3 grid, hipStream_t st)
 {
-    hipLaunchKernelGGL((mfma_decode::attn_mfma_f16<HD, GP, kDecodeNt, kDecodePrefetch,
-                                                   kDecodeOcc>),
-                       grid, dim3(256), 0, st, a);
+    if (a.waves == 8)
+        hipLaunchKernelGGL((mfma_decode::attn_mfma_f16<HD, GP, kDecodeNt, kDecodePrefetch, kDecodeOcc, 8>),
+                           grid, dim3(512), 0, st, a);
+    else
+        hipLaunchKernelGGL((mfma_decode::attn_mfma_f16<HD, GP, kDecodeNt, kDecodePrefetch, kDecodeOcc, 4>),
+                           grid, dim3(256), 0, st, a);
 }
 
 // q4_0 pages are bound by the vector ALU: three waves per SIMD (the
@@ -1585,9 +1590,14 @@ template <int KT, int HD>
 static void launch_mfma_q(const DecodeArgs &a, dim3 grid, hipStream_t st)
 {
 #define GI_Q(GPv)                                                                                        \
-    hipLaunchKernelGGL((mfma_decode::attn_mfma_q<KT, HD, GPv, kDecodeNt, kDecodePrefetch, \
-                                                 kDecodeOccQ<KT>>),                           \
-                       grid, dim3(256), 0, st, a)
+    if (a.waves == 8)                                                                                    \
+        hipLaunchKernelGGL((mfma_decode::attn_mfma_q<KT, HD, GPv, kDecodeNt, kDecodePrefetch,             \
+                                                     kDecodeOccQ<KT>, 8>),                              \
+                           grid, dim3(512), 0, st, a);                                                  \
+    else                                                                                                 \
+        hipLaunchKernelGGL((mfma_decode::attn_mfma_q<KT, HD, GPv, kDecodeNt, kDecodePrefetch,             \
+                                                     kDecodeOccQ<KT>, 4>),                              \
+                           grid, dim3(256), 0, st, a)
     switch (a.num_heads / a.L.num_kv_heads) {
     case 1: GI_Q(1); break;
     case 2: GI_Q(2); break;

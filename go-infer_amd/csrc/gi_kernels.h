@@ -67,6 +67,7 @@ struct DecodeArgs {
     float *ws; // partials when num_splits > 1
     int *status;
     int kernel; // -1 automatic, 0 vector ALU, 1 matrix core
+    int waves;  // matrix-core decode: waves per workgroup, 4 or 8 (decode_waves)
     // Decode step: the new token's K and V ([batch][kv_dim] float32) to store
     // at position seq_lens[b] - 1 before attending, as gi_paged_append_at_len
     // does; null for attention alone.  append_base is base, writable.
@@ -85,6 +86,11 @@ bool decode_fuses_append(const PoolLayout &L, int batch, int num_splits, int num
 // max_len tokens, so the grid fills the device.
 void decode_plan(const PoolLayout &L, int batch, int num_heads, int max_len, int num_cus,
                  int *split_tokens, int *num_splits);
+
+// Waves per workgroup of the matrix-core decode launch: 8 when the grid of
+// (split, kv head, sequence) workgroups fits the CUs once, so that every
+// SIMD still streams with two waves; 4 otherwise.
+int decode_waves(const PoolLayout &L, int batch, int num_splits, int num_cus);
 
 // Returns hipErrorInvalidValue for shapes without a kernel instance.
 hipError_t launch_decode(const DecodeArgs &a, hipStream_t st);

@@ -11,6 +11,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <memory>
 #include <mutex>
 #include <new>
 #include <string>
@@ -93,6 +94,7 @@ struct gi_paged {
     int *d_status = nullptr;
     gi::DevBuffer plan_ws; // decode: partials of split sequences
     void *scratch = nullptr; // this device's address of `scratch` (allocate-nothing decode)
+    struct ScratchOrder *scratch_order = nullptr; // and the ordering of its users
     int decode_kernel = -1; // -1 automatic, 0 vector ALU, 1 matrix core
     float2 *d_rope = nullptr; // (cos, sin) [rope_max_pos][rope_half]
     int rope_half = 0;
@@ -133,26 +135,52 @@ int check_layer(const gi_paged *h, int layer, const char *what)
 constexpr size_t kNoAllocScratchBytes = (size_t)4 << 20;
 __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 
-std::mutex g_scratch_mu;
-std::vector<void *> g_scratch_addr; // by device id
+} // namespace
 
-// With `device` current: the device address of `scratch` there, looked up
-// once per device.
-int scratch_address(int device, void **addr)
+// Every handle on a device shares that device's array, whatever its stream.
+// Successive users are ordered on the device: each call's launches are
+// followed by a record of `done` on its stream, and a call from another
+// stream first waits for it.  The event is created once per device, with the
+// address; no call allocates.  (A stream that is capturing a graph neither
+// waits nor records: the replays of such a graph are ordered against other
+// users of the array by the caller.)
+struct ScratchOrder {
+    void *addr = nullptr;
+    hipEvent_t done = nullptr;  // recorded after the last eager user's launches
+    hipStream_t last = nullptr; // that user's stream
+    bool recorded = false;
+    std::mutex mu; // held from the wait to the record
+};
+
+namespace {
+
+std::mutex g_scratch_mu;
+std::vector<std::unique_ptr<ScratchOrder>> g_scratch; // by device id
+
+// With `device` current: the device address of `scratch` there and its
+// ordering state, set up once per device.
+int scratch_address(int device, void **addr, ScratchOrder **order)
 {
     std::lock_guard<std::mutex> g(g_scratch_mu);
-    if ((size_t)device < g_scratch_addr.size() && g_scratch_addr[(size_t)device]) {
-        *addr = g_scratch_addr[(size_t)device];
+    if ((size_t)device < g_scratch.size() && g_scratch[(size_t)device]) {
+        *addr = g_scratch[(size_t)device]->addr;
+        *order = g_scratch[(size_t)device].get();
         return GI_OK;
     }
     void *p = nullptr;
     hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || !p)
         return hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol, "scratch: hipGetSymbolAddress");
-    if (g_scratch_addr.size() <= (size_t)device)
-        g_scratch_addr.resize((size_t)device + 1, nullptr);
-    g_scratch_addr[(size_t)device] = p;
+    std::unique_ptr<ScratchOrder> so(new ScratchOrder);
+    so->addr = p;
+    e = hipEventCreateWithFlags(&so->done, hipEventDisableTiming);
+    if (e != hipSuccess)
+        return hip_fail(e, "scratch: hipEventCreateWithFlags");
+    if (g_scratch.size() <= (size_t)device)
+        g_scratch.resize((size_t)device + 1);
     *addr = p;
+    *order = so.get();
+    g_scratch[(size_t)device] = std::move(so);
     return GI_OK;
 }
 
@@ -224,7 +252,7 @@ int gi_paged_create(int num_layers, int num_kv_heads, int head_dim, int page_tok
         return rc;
     }
     h->stream = h->own_stream;
-    int rc = scratch_address(h->device, &h->scratch);
+    int rc = scratch_address(h->device, &h->scratch, &h->scratch_order);
     if (rc == GI_OK && hipMalloc((void **)&h->d_status, sizeof(int)) != hipSuccess) {
         h->d_status = nullptr;
         rc = gi::set_error(GI_ERR_OOM, "gi_paged_create: status word");
@@ -606,6 +634,37 @@ static int decode_locked(gi_paged *h, int layer, int batch, int num_heads, const
     const int max_len = (int)(max_seq_len > 0 && max_seq_len < mapped ? max_seq_len
                               : mapped < INT32_MAX ? mapped : INT32_MAX);
     gi::decode_plan(h->L, batch, num_heads, max_len, h->num_cus, &a.split_tokens, &a.num_splits);
+    a.waves = gi::decode_waves(h->L, batch, a.num_splits, h->num_cus);
+    // the workspace first: a call refused here has queued nothing
+    const size_t need = gi::decode_workspace_bytes(h->L, batch, num_heads, a.num_splits);
+    std::unique_lock<std::mutex> order; // the shared scratch's users, in turn
+    bool eager = false;
+    if (fixed_ws) {
+        if (need > fixed_cap)
+            return gi::set_error(GI_ERR_BAD_ARG,
+                                 "gi_paged_decode_attention_noalloc: this shape needs " + std::to_string(need) +
+                                     " bytes of scratch; the fixed maximum is " + std::to_string(fixed_cap) +
+                                     " (use gi_paged_decode_attention)");
+        a.ws = (float *)fixed_ws;
+        ScratchOrder *so = h->scratch_order;
+        order = std::unique_lock<std::mutex>(so->mu);
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        hipError_t e = hipStreamIsCapturing(h->stream, &cs);
+        if (e != hipSuccess)
+            return hip_fail(e, "gi_paged_decode_attention_noalloc: hipStreamIsCapturing");
+        eager = cs == hipStreamCaptureStatusNone;
+        if (eager && so->recorded && so->last != h->stream) {
+            // the previous user's launches (another stream) finish first
+            e = hipStreamWaitEvent(h->stream, so->done, 0);
+            if (e != hipSuccess)
+                return hip_fail(e, "gi_paged_decode_attention_noalloc: hipStreamWaitEvent");
+        }
+    } else {
+        const int rc = gi::devbuf_reserve(h->plan_ws, need, h->stream, "decode attention");
+        if (rc)
+            return rc;
+        a.ws = (float *)h->plan_ws.ptr;
+    }
     if (new_k) {
         // a decode step: the token goes into the decode launch where that
         // pays (one round of workgroups), else into an append launch first
@@ -619,22 +678,18 @@ static int decode_locked(gi_paged *h, int layer, int batch, int num_heads, const
                 return hip_fail(e, "decode step: append");
         }
     }
-    const size_t need = gi::decode_workspace_bytes(h->L, batch, num_heads, a.num_splits);
-    if (fixed_ws) {
-        if (need > fixed_cap)
-            return gi::set_error(GI_ERR_BAD_ARG,
-                                 "gi_paged_decode_attention_noalloc: this shape needs " + std::to_string(need) +
-                                     " bytes of scratch; the fixed maximum is " + std::to_string(fixed_cap) +
-                                     " (use gi_paged_decode_attention)");
-        a.ws = (float *)fixed_ws;
-    } else {
-        const int rc = gi::devbuf_reserve(h->plan_ws, need, h->stream, "decode attention");
-        if (rc)
-            return rc;
-        a.ws = (float *)h->plan_ws.ptr;
-    }
     hipError_t e = gi::launch_decode(a, h->stream);
-    return e == hipSuccess ? GI_OK : hip_fail(e, "decode attention");
+    if (e != hipSuccess)
+        return hip_fail(e, "decode attention");
+    if (eager) {
+        ScratchOrder *so = h->scratch_order;
+        e = hipEventRecord(so->done, h->stream);
+        if (e != hipSuccess)
+            return hip_fail(e, "gi_paged_decode_attention_noalloc: hipEventRecord");
+        so->last = h->stream;
+        so->recorded = true;
+    }
+    return GI_OK;
 }
 
 static int check_decode_args(gi_paged *h, int layer, int batch, int num_heads, const void *q,
@@ -762,6 +817,27 @@ int gi_paged_decode_kernel(const gi_paged *h, int num_heads)
     if (!h)
         return gi::set_error(GI_ERR_BAD_ARG, "gi_paged_decode_kernel: NULL handle");
     return gi::decode_kernel_kind(h->L, num_heads, h->decode_kernel);
+}
+
+int gi_paged_attention_plan(const gi_paged *h, int batch, int num_heads, int max_seq_len,
+                            gi_attention_plan *plan)
+{
+    if (!h || !plan || batch < 0 || max_seq_len < 0)
+        return gi::set_error(GI_ERR_BAD_ARG, "gi_paged_attention_plan: bad argument");
+    if (!supported_heads(h->L, num_heads))
+        return gi::set_error(GI_ERR_BAD_ARG, "gi_paged_attention_plan: unsupported head layout");
+    gi_attention_plan r{};
+    const bool mfma_req = h->decode_kernel != 0;
+    r.decode_kernel = gi::decode_kernel_kind(h->L, num_heads, h->decode_kernel);
+    r.decode_fallback = mfma_req && r.decode_kernel == 0;
+    gi::decode_plan(h->L, batch, num_heads, max_seq_len > 0 ? max_seq_len : 1, h->num_cus,
+                    &r.decode_split_tokens, &r.decode_splits);
+    r.decode_waves = r.decode_kernel == 1 ? gi::decode_waves(h->L, batch, r.decode_splits, h->num_cus) : 0;
+    r.decode_step_fused = r.decode_kernel == 1 && gi::decode_fuses_append(h->L, batch, r.decode_splits, h->num_cus);
+    r.prefill_kernel = mfma_req && gi::mfma_prefill_supported(h->L, num_heads) ? 1 : 0;
+    r.prefill_fallback = mfma_req && r.prefill_kernel == 0;
+    *plan = r;
+    return GI_OK;
 }
 
 int gi_paged_set_decode_kernel(gi_paged *h, int kind)

@@ -265,8 +265,8 @@ int gi_paged_gather(gi_paged *h, int layer, const int32_t *block_table, int n_to
  *
  * Workspace: the handle keeps the partials of split sequences, batch *
  * num_kv_heads * splits slots of (num_heads / num_kv_heads) * (head_dim + 2)
- * floats, where splits falls as batch * num_kv_heads grows (about two
- * workgroups per CU).  A call that needs it to grow while the handle's stream
+ * floats, where splits falls as batch * num_kv_heads grows (about one
+ * workgroup per CU).  A call that needs it to grow while the handle's stream
  * is capturing a graph fails with GI_ERR_BAD_ARG (make one eager call with
  * the same shape first); once any call has been captured, growth keeps the
  * old buffers alive until gi_paged_destroy, so captured graphs stay valid. */
@@ -284,10 +284,14 @@ int gi_paged_decode_attention(gi_paged *h, int layer, int batch, int num_heads, 
  * per kv head at head_dim 128 the batches with batch * num_kv_heads of 253
  * to 255 and contexts over 1024 tokens (two splits, 506 to 510 slots of
  * 8 KiB) would need up to 4.25 MB and fail with GI_ERR_BAD_ARG before any
- * launch.  Every call
- * on one device shares that array, so calls that overlap on one device
- * (other handles or streams) race: serialise them.  Same arguments and
- * results as gi_paged_decode_attention. */
+ * launch.  Every call on one device shares that array.  The library orders
+ * its eager users on the device: a call whose handle's stream differs from
+ * the previous user's first makes its stream wait for an event recorded
+ * after that user's launches (the event is created once per device, at the
+ * first gi_paged_create there).  A stream that is capturing a graph neither
+ * waits nor records, so replays of captured calls that could overlap other
+ * users of the array on the device (other streams) race: serialise them.
+ * Same arguments and results as gi_paged_decode_attention. */
 int gi_paged_decode_attention_noalloc(gi_paged *h, int layer, int batch, int num_heads, const float *q,
                                       float *out, const int32_t *block_tables, int max_blocks,
                                       const int32_t *seq_lens, int max_seq_len, float scale);
@@ -354,6 +358,30 @@ int gi_paged_prefill_attention(gi_paged *h, int layer, int batch, int chunk_len,
 /* Which decode kernel serves this pool and head count: 0 vector ALU,
  * 1 matrix core (fp16 pages, head_dim 64/128, page_tokens % 16 == 0). */
 int gi_paged_decode_kernel(const gi_paged *h, int num_heads);
+
+/* The launch plan of this pool's attention calls for a batch, head count
+ * and longest context (max_seq_len, as the decode calls take it; 0 counts as
+ * 1), worked out without launching anything.  No counterpart in the
+ * reference (its attention is inline CPU loops); a host checks here whether
+ * its shapes run on the matrix-core kernels, since a shape they do not take
+ * (head_dim other than 64/128, pages not a multiple of 16 tokens, f32 or
+ * quantised pages with 16 query heads per kv head) is served by the
+ * vector-ALU kernels, correct but several times slower (*_fallback). */
+typedef struct gi_attention_plan {
+    int decode_kernel;       /* 0 vector ALU, 1 matrix core */
+    int decode_fallback;     /* 1: matrix core selected but the shape is not
+                                supported, so the vector ALU serves it */
+    int decode_splits;       /* split-K ranges per (sequence, kv head) */
+    int decode_split_tokens; /* tokens per split (the last runs to the end) */
+    int decode_waves;        /* waves per matrix-core workgroup (4 or 8) */
+    int decode_step_fused;   /* gi_paged_decode_step stores the token inside
+                                the decode launch (else an append launch) */
+    int prefill_kernel;      /* 0 vector ALU, 1 matrix core */
+    int prefill_fallback;    /* as decode_fallback, for prefill */
+} gi_attention_plan;
+
+int gi_paged_attention_plan(const gi_paged *h, int batch, int num_heads, int max_seq_len,
+                            gi_attention_plan *plan);
 
 /* Selects the attention kernels (decode and prefill): -1 automatic
  * (default), 0 vector ALU, 1 matrix core where supported.  For

@@ -108,3 +108,72 @@ def test_decode_step_bad_lengths_store_nothing(gi, oracle, dev):
                                        hd, 100, scale)
         assert float(rel_err_rows(out[0].cpu().numpy(), want, H, hd).max()) <= 1e-3, kern
         assert not out[2].cpu().numpy().any(), kern
+
+
+def test_attention_plan_reports_kernels_waves_and_fusion(gi, oracle, dev):
+    """gi_paged_attention_plan on a 256-CU device: the Llama-3-8B shape at
+    batch 32 x 4096 gets one workgroup per (sequence, kv head), 256 of them,
+    so eight waves each and the token store fused; batch 256 x 8192 gets
+    2,048 four-wave workgroups and an append launch; the Llama-3-70B shape
+    at 8 x 32768 (pages of 32) takes 4 splits of 8,192 in eight-wave
+    workgroups.  Pages of 8 tokens are not a matrix-core shape: the plan
+    says the vector ALU serves them as a fallback.  f32 pages keep four
+    waves (32 KiB of LDS staging per wave)."""
+    import torch
+    if torch.cuda.get_device_properties(dev).multi_processor_count != 256:
+        pytest.skip("the plans are worked out for a 256-CU device")
+    f16 = gi.PagedKVCache(1, 8, 128, 16, 64, gi.KV_F16)
+    p = f16.attention_plan(32, 32, 4096)
+    assert (p["decode_kernel"], p["decode_fallback"], p["decode_splits"], p["decode_waves"],
+            p["decode_step_fused"], p["prefill_kernel"]) == (1, 0, 1, 8, 1, 1), p
+    p = f16.attention_plan(256, 32, 8192)
+    assert (p["decode_splits"], p["decode_waves"], p["decode_step_fused"]) == (1, 4, 0), p
+    d70 = gi.PagedKVCache(1, 8, 128, 32, 64, gi.KV_F16)
+    p = d70.attention_plan(8, 64, 32768)
+    assert (p["decode_splits"], p["decode_split_tokens"], p["decode_waves"], p["decode_step_fused"]) == \
+        (4, 8192, 8, 1), p
+    p8 = gi.PagedKVCache(1, 8, 128, 8, 64, gi.KV_F16)
+    p = p8.attention_plan(4, 32, 1000)
+    assert (p["decode_kernel"], p["decode_fallback"], p["decode_waves"], p["prefill_kernel"],
+            p["prefill_fallback"]) == (0, 1, 0, 0, 1), p
+    p8.set_decode_kernel(0)
+    p = p8.attention_plan(4, 32, 1000)
+    assert (p["decode_kernel"], p["decode_fallback"], p["prefill_fallback"]) == (0, 0, 0), p
+    f32 = gi.PagedKVCache(1, 8, 128, 16, 64, gi.KV_F32)
+    assert f32.attention_plan(32, 32, 4096)["decode_waves"] == 4
+    for pool in (f16, d70, p8, f32):
+        pool.close()
+
+
+@pytest.mark.parametrize("kv_type", [1, 2, 3], ids=["f16", "q8_0", "q4_0"])
+def test_decode_four_and_eight_wave_workgroups_match_the_oracle(gi, oracle, dev, kv_type):
+    """33 sequences x 8 kv heads make 264 workgroups, more than the CUs: four
+    waves each.  The first 32 make 256: eight waves each, every wave taking
+    every eighth 32-token block.  Both against the oracle on the stored bits,
+    with lengths that leave each wave a different number of blocks (and some
+    waves none)."""
+    import torch
+    H, kvh, hd, P = 32, 8, 128, 16
+    rng = np.random.default_rng(77 + kv_type)
+    lens = [int(x) for x in rng.integers(1, 700, size=33)]
+    lens[0], lens[1], lens[2] = 1, 32 * 8, 32 * 8 + 1
+    pop = Populated(gi, dev, kv_type, 1, kvh, hd, P, lens, seed=78 + kv_type)
+    bt = pop.block_tables()
+    scale = oracle.attn_scale(hd)
+    qd, q = seeded((len(lens), H * hd), 79 + kv_type, dev)
+    for B in (33, 32):
+        plan = pop.pool.attention_plan(B, H, max(lens[:B]))
+        if torch.cuda.get_device_properties(dev).multi_processor_count == 256:
+            assert plan["decode_waves"] == (4 if B == 33 else 8), plan
+        sl = torch.tensor(lens[:B], dtype=torch.int32, device=dev)
+        out = torch.full_like(qd[:B], float("nan"))
+        pop.pool.AttentionGQA(out, qd[:B].contiguous(), 0, bt[:B].contiguous(), sl, H, scale)
+        pop.pool.synchronize()
+        got = out.cpu().numpy()
+        for i in range(B):
+            ks, vs = pop.stored(0, i)
+            n = lens[i]
+            want = oracle.attention_decode(q[i], oracle.widen(kv_type, kvh * hd, ks[:n]),
+                                           oracle.widen(kv_type, kvh * hd, vs[:n]), H, kvh, hd, n, scale)
+            err = float(rel_err_rows(got[i], want, H, hd).max())
+            assert err <= TOL[kv_type], (B, i, n, err)

@@ -73,3 +73,38 @@ def test_noalloc_decode_refuses_a_shape_beyond_its_scratch(gi, oracle, dev):
     pop.pool.AttentionGQANoAlloc(got, *args)
     pop.pool.synchronize()
     assert torch.equal(got, want)
+
+
+def test_noalloc_decode_orders_two_handles_on_two_streams(gi, oracle, dev):
+    """Two pools on two streams share the device's scratch array.  Calls
+    alternate between them with no host synchronisation in between, each
+    with split sequences (partials in the array), and every output must
+    equal the allocating entry point's bit for bit: the library makes each
+    stream wait for the previous user's launches on the other stream."""
+    import torch
+    H, kvh, hd, P = 32, 8, 128, 16
+    scale = oracle.attn_scale(hd)
+    pops, args, want = [], [], []
+    for t, lens in enumerate(([20000, 9000, 4097], [12000, 3000])):
+        pop = Populated(gi, dev, 1, 1, kvh, hd, P, lens, seed=51 + t)
+        s = torch.cuda.Stream(dev)
+        pop.pool.set_stream(s.cuda_stream)
+        bt = pop.block_tables()
+        sl = torch.tensor(lens, dtype=torch.int32, device=dev)
+        qd, _ = seeded((len(lens), H * hd), 61 + t, dev)
+        w = torch.full_like(qd, float("nan"))
+        torch.cuda.synchronize()
+        pop.pool.AttentionGQA(w, qd, 0, bt, sl, H, scale)
+        pop.pool.synchronize()
+        pops.append(pop)
+        args.append((qd, bt, sl))
+        want.append(w)
+    outs = [(t, torch.full_like(args[t][0], float("nan"))) for _ in range(3) for t in (0, 1)]
+    torch.cuda.synchronize()
+    for t, got in outs:
+        qd, bt, sl = args[t]
+        pops[t].pool.AttentionGQANoAlloc(got, qd, 0, bt, sl, H, scale)
+    for pop in pops:
+        pop.pool.synchronize()
+    for i, (t, got) in enumerate(outs):
+        assert torch.equal(got, want[t]), (i, t)
