@@ -43,13 +43,21 @@ def c_names(src):
 
 
 def exported_api(src):
-    """Exported top-level functions and HIPPagedKV methods with their
-    parameter lists (whitespace-normalised)."""
+    """Exported top-level functions and methods (Type.Method) with their whole
+    signatures, parameters and results (whitespace-normalised)."""
     sigs = {}
-    for m in re.finditer(r"^func (\(p \*HIPPagedKV\) )?([A-Z]\w*)\((.*?)\)", src, flags=re.S | re.M):
-        params = " ".join(m.group(3).split())
-        sigs[("HIPPagedKV." if m.group(1) else "") + m.group(2)] = params
+    for m in re.finditer(r"^func (\(\w+ \*(\w+)\) )?([A-Z]\w*)(\(.*?)\s*\{\}?[ \t]*$", src, flags=re.S | re.M):
+        sig = " ".join(m.group(4).split())
+        sigs[(m.group(2) + "." if m.group(1) else "") + m.group(3)] = sig
     return sigs
+
+
+def exported_types(src):
+    """Exported type names, and the exported fields of AttentionPlan."""
+    types = sorted(set(re.findall(r"^type ([A-Z]\w*) ", src, flags=re.M)))
+    m = re.search(r"^type AttentionPlan struct \{(.*?)^\}", src, flags=re.S | re.M)
+    fields = [ln.split()[0] for ln in m.group(1).splitlines() if ln.strip() and not ln.strip().startswith("//")]
+    return types, fields
 
 
 def compile_and_run(tmp_path, name, source, run=True):
@@ -76,19 +84,75 @@ def test_build_tags_pair():
 
 
 def test_twin_declares_the_same_api():
-    a = exported_api(open(HIP_GO).read())
-    b = exported_api(open(NOHIP_GO).read())
-    assert a == b
+    """Same exported functions, methods (with parameters and results) and
+    types in both builds, covering the pool (forward.go:236-267, 547-577),
+    the copy-on-write manager and prefix cache (kvcache.go:217-284,
+    prefix_cache.go:76-150), the batch driver (engine.go:417) and the
+    O-projection (weights.go:237, forward.go:270)."""
+    hip, nohip = open(HIP_GO).read(), open(NOHIP_GO).read()
+    a = exported_api(hip)
+    b = exported_api(nohip)
+    assert a == b, sorted(set(a.items()) ^ set(b.items()))
+    assert exported_types(hip) == exported_types(nohip)
     for name in ("NewHIPPagedKV", "HIPPagedKV.Write", "HIPPagedKV.Get", "HIPPagedKV.AttentionGQA",
-                 "HIPPagedKV.AttentionGQABatch", "HIPPagedKV.CopyPages", "HIPPagedKV.Close"):
-        assert name in a
+                 "HIPPagedKV.DecodeStep", "HIPPagedKV.SetRoPE", "HIPPagedKV.RoPEDecodeStep",
+                 "HIPPagedKV.AttentionGQABatch", "HIPPagedKV.AttentionPlan", "HIPPagedKV.CopyPages",
+                 "HIPPagedKV.UploadWeights", "HIPPagedKV.Close",
+                 "NewHIPKVManager", "HIPKVManager.AllocateSequence", "HIPKVManager.AppendToken",
+                 "HIPKVManager.AppendBatch", "HIPKVManager.ForkSequence", "HIPKVManager.FreeSequence",
+                 "HIPKVManager.BlockTable", "HIPKVManager.BlockRefs", "HIPKVManager.Close",
+                 "NewHIPPrefixCache", "HIPPrefixCache.Store", "HIPPrefixCache.FindLongestPrefix",
+                 "HIPPrefixCache.Size", "HIPPrefixCache.Close",
+                 "NewHIPBatchDecoder", "HIPBatchDecoder.Add", "HIPBatchDecoder.Remove", "HIPBatchDecoder.Step",
+                 "HIPBatchDecoder.Rows", "HIPBatchDecoder.DecodeLayer", "HIPBatchDecoder.Close",
+                 "HIPWeights.MatMulBatch", "HIPWeights.Close"):
+        assert name in a, name
+
+
+def test_go_sources_are_balanced():
+    """A crude syntax guard in place of the Go compiler, which this image
+    lacks: braces, brackets and parentheses balance outside strings and
+    comments in every Go file of the package."""
+    import glob
+    for path in glob.glob(os.path.join(GO, "*.go")):
+        src = open(path).read()
+        src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+        src = re.sub(r"//[^\n]*", "", src)
+        src = re.sub(r'"(\\.|[^"\\])*"', '""', src)
+        src = re.sub(r"'(\\.|[^'\\])*'", "''", src)
+        depth = {"(": 0, "[": 0, "{": 0}
+        close = {")": "(", "]": "[", "}": "{"}
+        for ch in src:
+            if ch in depth:
+                depth[ch] += 1
+            elif ch in close:
+                depth[close[ch]] -= 1
+                assert depth[close[ch]] >= 0, (path, ch)
+        assert all(v == 0 for v in depth.values()), (path, depth)
+
+
+def test_block_tables_pad_with_an_invalid_id():
+    """flatTables (paged_tables.go, no build tag, so both builds have it) pads
+    rows with -1 and refuses lengths past a row's blocks; its Go test sits
+    beside it (paged_tables_test.go)."""
+    src = open(os.path.join(GO, "paged_tables.go")).read()
+    assert not src.startswith("//go:build")
+    assert "flat[i] = -1" in src and "return nil, 0, fmt.Errorf" in src
+    test = open(os.path.join(GO, "paged_tables_test.go")).read()
+    assert "func TestFlatTablesPadsWithInvalidIDs(t *testing.T)" in test
+    assert "func TestFlatTablesRefusesLengthsPastTheTable(t *testing.T)" in test
 
 
 def test_cgo_preamble_compiles_and_links(gi, tmp_path):
     src = open(HIP_GO).read()
     pre = preamble(src)
     funcs, consts = c_names(src)
-    assert "gi_paged_decode_attention" in funcs and "gi_paged_append" in funcs
+    for f in ("gi_paged_decode_attention", "gi_paged_append", "gi_paged_decode_step",
+              "gi_paged_rope_decode_step", "gi_paged_set_rope", "gi_paged_attention_plan",
+              "gi_kvmgr_fork_sequence", "gi_kvmgr_append_token_cow", "gi_kvmgr_append_batch",
+              "gi_prefix_store", "gi_prefix_find_longest", "gi_batch_step", "gi_batch_decode_layer",
+              "gi_weights_upload", "gi_matmul_batch"):
+        assert f in funcs, f
     # every function cgo would reference must be one the header declares
     from test_abi import declared_functions
     assert set(funcs) <= set(declared_functions())
