@@ -317,7 +317,20 @@ def cpu_baseline(oracle, cfg, budget_s=10.0, mt_budget_s=6.0):
     un, en = _timed_units(mt, mt_budget_s, 4096)
     res = figure(un, en, ran[0])
     res["one_thread"] = one
+    res.update(host_cpus())
     return res
+
+
+def host_cpus():
+    """The host's CPU count as the machine reports it (nproc) and as this
+    process may use it, beside the threads the all-cores figure ran on: the
+    baseline takes at most 16, the host share of one GPU on these boxes."""
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        aff = None
+    return {"nproc": os.cpu_count(), "affinity_cpus": aff,
+            "threads_note": "the all-cores figure uses min(affinity, 16) threads, the host share of one GPU"}
 
 
 def cpu_baseline_prefill(oracle, cfg, budget_s=8.0, mt_budget_s=6.0):
@@ -354,6 +367,7 @@ def cpu_baseline_prefill(oracle, cfg, budget_s=8.0, mt_budget_s=6.0):
         mt_budget_s, 1024)
     res = figure(un, en, n)
     res["one_thread"] = figure(u1, e1, 1)
+    res.update(host_cpus())
     return res
 
 
