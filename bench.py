@@ -1106,10 +1106,6 @@ def run_decode(args, gi, torch, dev, cfg, name):
     vn = torch.randn((layers, batch, kv_dim), generator=gen, device=dev)
     out = torch.empty((layers, batch, H * hd), device=dev)
     scale = gi.attn_scale(hd)
-    n_ev = layers * args.steps
-    ev0 = [torch.cuda.Event(enable_timing=True) for _ in range(n_ev)]
-    ev1 = [torch.cuda.Event(enable_timing=True) for _ in range(n_ev)]
-    eva = [torch.cuda.Event(enable_timing=True) for _ in range(n_ev)]
     rope = cfg.get("rope_theta")
     if rope:
         pool.SetRoPE(rope, 0, max_len)
@@ -1121,7 +1117,10 @@ def run_decode(args, gi, torch, dev, cfg, name):
     #   once, else an append launch and the attention launch;
     # - the two-call form: the append (gi_paged_append_at_len, with RoPE
     #   gi_paged_rope_append_at_len), then gi_paged_decode_attention.
-    # q is turned in place at position seq_lens-1 when RoPE is on.
+    # q is turned in place at position seq_lens-1 when RoPE is on.  The
+    # kernels' durations come from runs of each kind of launch alone, back to
+    # back with events only at the ends (an event pair around every launch
+    # adds its own few microseconds, which short launches would count).
     prod, app, att = [], [], []
     for l in range(layers):
         if rope:
@@ -1138,16 +1137,18 @@ def run_decode(args, gi, torch, dev, cfg, name):
         for f in prod:
             f()
 
-    def step_two_calls(record=None):
+    def step_two_calls():
         for l in range(layers):
-            if record is not None:
-                eva[record + l].record(stream)
             app[l]()
-            if record is not None:
-                ev0[record + l].record(stream)
             att[l]()
-            if record is not None:
-                ev1[record + l].record(stream)
+
+    def attention_only():
+        for f in att:
+            f()
+
+    def append_only():
+        for f in app:
+            f()
 
     def timed(fn):
         """ms per step of fn over args.steps steps: events only around the
@@ -1171,16 +1172,10 @@ def run_decode(args, gi, torch, dev, cfg, name):
         step_two_calls()
     ms_step, wall_step = timed(step_product)
     ms_two, _ = timed(step_two_calls)
-    # each launch of the two-call form bracketed by events (an instrumented
-    # run of its own, for the kernels' durations)
-    pool.synchronize()
-    torch.cuda.synchronize()
-    for i in range(args.steps):
-        step_two_calls(record=i * layers)
-    torch.cuda.synchronize()
-    pool.synchronize()
-    attn_ms = float(np.mean([a.elapsed_time(b) for a, b in zip(ev0, ev1)]))
-    app_ms = float(np.mean([a.elapsed_time(b) for a, b in zip(eva, ev0)]))
+    # appends first: with RoPE each append turns q in place again, and the
+    # outputs the parity sample checks are the last attention run's
+    app_ms = timed(append_only)[0] / layers
+    attn_ms = timed(attention_only)[0] / layers
     attn_bytes, app_bytes = step_bytes(cfg, lens)
     tot_gbs = (attn_bytes + app_bytes) / (ms_step * 1e-3) / 1e9
     attn_gbs = (attn_bytes / layers) / (attn_ms * 1e-3) / 1e9
