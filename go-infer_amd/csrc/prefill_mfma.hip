@@ -1071,7 +1071,12 @@ struct WaveAttn {
     static constexpr int KK = HD / 32, NB = HD / 16;
     h8 qh[NCG][KK], ql[NCG][KK];
     float c2s[NCG], m2[NCG], lsum[NCG];
-    float kinv = 1.0f; // f32 pages: 1 / the current block's K operand scale
+    // f32 pages: 1 / the K operand scale of this lane's tokens of half h of
+    // the current block (tokens 32h + 8g .. 32h + 8g + 7)
+    float kinv[2] = {1.0f, 1.0f};
+    // f32 ping-pong kernel: the power-of-two V operand scale that O tiles
+    // 2q and 2q + 1 (dimensions 32q .. 32q + 31) are held in
+    float vso[4] = {1.0f, 1.0f, 1.0f, 1.0f};
     float neg1;        // -1, opaque to the optimiser (split8)
     f4 o[NCG][NB];
     int qlen[NCG];
@@ -1199,13 +1204,22 @@ struct WaveAttn {
         }
         // maximumNumber (IEEE 754-2019) compiles to v_max3_f32 with no
         // canonicalising moves of the product results that fmaxf needs
-        float m3[5];
+        float mx;
+        if constexpr (KT == KV_F32) {
+            // the two halves may carry different K scales
+            const float a0 = maxnum3(maxnum3(sv[0], sv[1], sv[2]), maxnum3(sv[3], sv[4], sv[5]), maxnum(sv[6], sv[7]));
+            const float a1 =
+                maxnum3(maxnum3(sv[8], sv[9], sv[10]), maxnum3(sv[11], sv[12], sv[13]), maxnum(sv[14], sv[15]));
+            mx = maxnum(a0 * kinv[0], a1 * kinv[1]);
+        } else {
+            float m3[5];
 #pragma unroll
-        for (int i = 0; i < 5; i++)
-            m3[i] = maxnum3(sv[3 * i], sv[3 * i + 1], sv[3 * i + 2]);
-        float mx = maxnum3(maxnum3(m3[0], m3[1], m3[2]), maxnum3(m3[3], m3[4], sv[15]), sv[15]);
+            for (int i = 0; i < 5; i++)
+                m3[i] = maxnum3(sv[3 * i], sv[3 * i + 1], sv[3 * i + 2]);
+            mx = maxnum3(maxnum3(m3[0], m3[1], m3[2]), maxnum3(m3[3], m3[4], sv[15]), sv[15]);
+        }
         mx = max_xor32n(max_xor16n(mx));
-        mx *= c2s[cg] * kinv;
+        mx *= c2s[cg];
         const bool grow = mx > m2[cg] + kLazy;
         const float mref = grow ? mx : m2[cg];
         alpha = grow ? __builtin_amdgcn_exp2f(m2[cg] - mref) : 1.0f;
@@ -1215,7 +1229,7 @@ struct WaveAttn {
         float ps = 0.0f;
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            p[i] = __builtin_amdgcn_exp2f(fmaf(sv[i], c2s[cg] * kinv, -msub));
+            p[i] = __builtin_amdgcn_exp2f(fmaf(sv[i], c2s[cg] * kinv[i / 8], -msub));
             ps += p[i];
         }
         lsum[cg] = lsum[cg] * alpha + ps;
@@ -1326,24 +1340,34 @@ struct WaveAttn {
     static constexpr int NRD = LOP ? 2 : 1;        // V fragment reads per step
     static constexpr int RA = LOP ? 1 : 2;         // steps read ahead
 
-    // Score tiles of the block in K buffer kb (fp16 pages; quantised pages
-    // use qk_block_kc).
+    // Score tiles of the block in K buffer kb: fp16 pages (two products per
+    // pair, Q hi and lo against K), or f32 pages, whose K is staged as hi +
+    // lo planes (three: hi x hi, hi x Q lo, lo x Q hi).  Quantised pages use
+    // qk_block_kc.
     template <class LDS>
     __device__ __forceinline__ void qk_block(const LDS &S, int kb, f4 (&s)[NCG][2][2], int j, int g) const
     {
-        static_assert(KT == KV_F16, "fp16 K operands");
+        static_assert(KT == KV_F16 || KT == KV_F32, "fp16 K operands, or f32 K as hi + lo planes");
+        constexpr bool KLP = KT == KV_F32;
         const uint8_t *kp = k_lane(S, kb, j, g, false);
+        const uint8_t *klp = KLP ? k_lane(S, kb, j, g, true) : kp;
         constexpr int NF = 4 * KK; // steps: (h, t, kk), kk fastest
         auto off = [&](int f) { return k_const(&S, f / (2 * KK), (f / KK) % 2, f % KK); };
-        h8 kh[RA + 1];
+        h8 kh[RA + 1], kl[RA + 1];
 #pragma unroll
-        for (int f = 0; f < RA; f++)
+        for (int f = 0; f < RA; f++) {
             kh[f] = ld_frag(kp, off(f));
+            if (KLP)
+                kl[f] = ld_frag(klp, off(f));
+        }
 #pragma unroll
         for (int f = 0; f < NF; f++) {
             const int h = f / (2 * KK), t = (f / KK) % 2, kk = f % KK;
-            if (f + RA < NF)
+            if (f + RA < NF) {
                 kh[(f + RA) % (RA + 1)] = ld_frag(kp, off(f + RA));
+                if (KLP)
+                    kl[(f + RA) % (RA + 1)] = ld_frag(klp, off(f + RA));
+            }
             const h8 ka = kh[f % (RA + 1)];
             if (kk == 0)
 #pragma unroll
@@ -1353,9 +1377,59 @@ struct WaveAttn {
             for (int cg = 0; cg < NCG; cg++) {
                 s[cg][h][t] = mfma(ka, qh[cg][kk], s[cg][h][t]);
                 s[cg][h][t] = mfma(ka, ql[cg][kk], s[cg][h][t]);
+                if (KLP)
+                    s[cg][h][t] = mfma(kl[f % (RA + 1)], qh[cg][kk], s[cg][h][t]);
             }
         }
-        read_ahead_order<NF, 2 * NCG, 1, RA>();
+        read_ahead_order<NF, (KLP ? 3 : 2) * NCG, KLP ? 2 : 1, RA>();
+    }
+
+    // f32 pages: this lane's K scale factors for the block in buffer kb,
+    // from the per-wave scales of its four 16-token groups (ks: LDS, 4
+    // floats).  Half h of the lane's tokens lies in group 2h + g / 2.
+    __device__ __forceinline__ void k_units(const float *ks, int g)
+    {
+        kinv[0] = pow2_recip(ks[g >> 1]);
+        kinv[1] = pow2_recip(ks[2 + (g >> 1)]);
+    }
+
+    // f32 pages: moves O tiles 2q, 2q + 1 to the V scale of dimension group
+    // q of the block about to be multiplied in (vs: LDS, 4 floats; exact
+    // powers of two).  The scales rarely move, so the check is one uniform
+    // branch per block.
+    __device__ __forceinline__ void v_units(const float *vs)
+    {
+        static_assert(NB == 8, "four dimension groups of two tiles (head_dim 128)");
+        const f4 v4 = *reinterpret_cast<const f4 *>(vs);
+        float v[4];
+        bool moved = false;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            v[q] = v4[q];
+            moved |= v[q] != vso[q];
+        }
+        if (__builtin_amdgcn_readfirstlane((int)moved)) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const float r = v[q] * pow2_recip(vso[q]);
+#pragma unroll
+                for (int cg = 0; cg < NCG; cg++) {
+                    o[cg][2 * q] *= r;
+                    o[cg][2 * q + 1] *= r;
+                }
+                vso[q] = v[q];
+            }
+        }
+    }
+
+    // f32 pages: O back from the V scales it is held in (before finish).
+    __device__ __forceinline__ void v_units_out()
+    {
+#pragma unroll
+        for (int cg = 0; cg < NCG; cg++)
+#pragma unroll
+            for (int nb = 0; nb < NB; nb++)
+                o[cg][nb] *= pow2_recip(vso[nb / 2]);
     }
 
     // Score tiles of the block in K buffer kb from exact K codes (Lds with
@@ -1645,7 +1719,7 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_lds(PrefillArgs a)
         if constexpr (F32) {
             // scores of this block carry its K scale; O moves to its V
             // scale (exact powers of two)
-            A.kinv = pow2_recip(ksc_cur);
+            A.kinv[0] = A.kinv[1] = pow2_recip(ksc_cur);
             if (vsc_o != 0.0f && vsc_o != vsc_cur)
                 A.scale_o(vsc_cur * pow2_recip(vsc_o));
             vsc_o = vsc_cur;
@@ -2004,6 +2078,246 @@ __global__ __launch_bounds__(512) void attn_prefill_ppq(PrefillArgs a)
         A.finish(a, W.b, W.kvh, W.col0, W.j, W.g);
 }
 
+// f32 pages (head_dim 128): one plane of a 64-token block staged by the four
+// waves of one group, eight 16-byte chunks per lane.  Wave ws holds K tokens
+// 16ws .. 16ws + 15 (chunk c: token 16ws + 2c + l/32, dimensions 4(l%32) ..
+// +3, so each load reads 1 KiB of one page), or V dimensions 32ws .. 32ws +
+// 31 (chunk c: dimension 32ws + 4c + l/16, tokens 4(l%16) .. +3).
+struct PlaneF32 {
+    u4 x[8];
+};
+
+template <int PLANE, int P>
+__device__ __forceinline__ void plane_load_f32(const PrefillArgs &a, int kvh, int ws, int lane, int tb, PlaneF32 &R)
+{
+    constexpr int HD = 128;
+    const PoolLayout &L = a.L;
+    const int64_t np = L.num_pages;
+    if (PLANE == 0) {
+        const int pr = __builtin_amdgcn_readlane(tb, 16 * ws);
+        const int64_t pg = (pr >= 0 && pr < np) ? pr : 0;
+        const float *kp = reinterpret_cast<const float *>(a.base + pg * L.page_bytes + L.k_off) +
+                          ((int64_t)kvh * P + (16 * ws) % P) * HD + 4 * lane; // lane l: token l/32, dims 4(l%32)
+#pragma unroll
+        for (int c = 0; c < 8; c++)
+            R.x[c] = *reinterpret_cast<const u4 *>(kp + 2 * c * HD);
+    } else {
+        const int t0 = 4 * (lane & 15);
+        const int pr = __shfl(tb, t0);
+        const int64_t pg = (pr >= 0 && pr < np) ? pr : 0;
+        const float *vp = reinterpret_cast<const float *>(a.base + pg * L.page_bytes + L.v_off) +
+                          ((int64_t)kvh * HD + 32 * ws + (lane >> 4)) * P + t0 % P;
+#pragma unroll
+        for (int c = 0; c < 8; c++)
+            R.x[c] = *reinterpret_cast<const u4 *>(vp + 4 * c * P);
+    }
+}
+
+// Converts a plane of plane_load_f32 into the hi + lo fp16 planes of buffer
+// `buf` (the layout stage_store writes), scaled by this wave's power-of-two
+// operand scale, which it derives from the largest live magnitude with the
+// running rule of block_scale (`run`: this wave's running scale, 0 at the
+// start) and publishes in sc[ws].  `vmask` bit l: block token l is cached and
+// on a valid page; stale slots take no part in the scale, and their V is
+// stored as zero (their scores are masked, and stale values must not reach O
+// through 0 * NaN).
+template <int PLANE, int NBUF>
+__device__ __forceinline__ void plane_store_f32(int ws, int lane, uint64_t vmask, const PlaneF32 &R, float &run,
+                                                float *sc, float neg1, Lds<128, KV_F32, NBUF> &S, int buf)
+{
+    using G = SwzGeom<128>;
+    float x[8][4];
+    float m = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+        // words copied out first: hipcc's __builtin_bit_cast of an
+        // ext_vector element reads element 0 whatever the index
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            w[i] = R.x[c][i];
+        if (PLANE == 0) {
+            const bool live = (vmask >> (16 * ws + 2 * c + (lane >> 5))) & 1u;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                x[c][i] = __builtin_bit_cast(float, w[i]);
+                if (live)
+                    m = fmaxf(m, fabsf(x[c][i]));
+            }
+        } else {
+            const uint32_t live = (uint32_t)(vmask >> (4 * (lane & 15))) & 0xFu;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                x[c][i] = ((live >> i) & 1u) ? __builtin_bit_cast(float, w[i]) : 0.0f;
+                m = fmaxf(m, fabsf(x[c][i]));
+            }
+        }
+    }
+    run = block_scale(wave_max_nonneg(m), run);
+    if (lane == 0)
+        sc[ws] = run;
+    if (run != 1.0f) { // wave-uniform, and 1 for ordinary data
+#pragma unroll
+        for (int c = 0; c < 8; c++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                x[c][i] *= run;
+    }
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+        uint32_t hi[2], lo[2];
+        split_pair(x[c][0], x[c][1], hi[0], lo[0], neg1);
+        split_pair(x[c][2], x[c][3], hi[1], lo[1], neg1);
+        if (PLANE == 0) {
+            const int tk = 16 * ws + 2 * c + (lane >> 5), col = 4 * (lane & 31);
+            *reinterpret_cast<u2 *>(&S.k[buf][G::kel(tk, col)]) = u2{hi[0], hi[1]};
+            *reinterpret_cast<u2 *>(&S.kl[buf][G::kel(tk, col)]) = u2{lo[0], lo[1]};
+        } else {
+            const int d = 32 * ws + 4 * c + (lane >> 4), t0 = 4 * (lane & 15);
+            *reinterpret_cast<u2 *>(&S.v[buf][G::vel(d, t0)]) = u2{hi[0], hi[1]};
+            *reinterpret_cast<u2 *>(&S.vl[buf][G::vel(d, t0)]) = u2{lo[0], lo[1]};
+        }
+    }
+}
+
+// f32 pages (head_dim 128), two waves per SIMD in ping-pong as
+// attn_prefill_ppq, with K and V staged through registers into hi + lo fp16
+// planes (two LDS buffers each): group B stages the K plane of block n + 1
+// in phase 1 of block n, group A the V plane in phase 2, each loading its
+// plane one block ahead.  Every staging wave picks its own power-of-two
+// scale (block_scale), so no barrier is spent on block maxima: a K scale
+// covers 16 tokens (the softmax takes a factor per half of a lane's
+// tokens, k_units), a V scale 32 dimensions (two O tiles, v_units).
+template <int HD, int P, int NCG>
+struct PingPongF {
+    static constexpr int NW = 8;
+    const PrefillArgs &a;
+    const PrefillWork<P, NCG, NW, true> &W;
+    Lds<HD, KV_F32, 2> &S;
+    float (&sc)[2][2][4]; // [plane][buffer][staging wave]
+    WaveAttn<HD, KV_F32, NCG> &A;
+
+    __device__ __forceinline__ bool live(int base) const { return W.wave_active && base < W.wave_len; }
+
+    __device__ __forceinline__ void scores(int kb, f4 (&s)[NCG][2][2]) { A.qk_block(S, kb, s, W.j, W.g); }
+    __device__ __forceinline__ void pv(int vb, const f4 (&s)[NCG][2][2])
+    {
+        A.v_units(sc[1][vb]);
+        A.pv_block(S, vb, s, W.j, W.g);
+    }
+    template <bool FULL>
+    __device__ __forceinline__ void softmax(int kb, f4 (&s)[NCG][2][2], int base, uint64_t mask)
+    {
+        A.k_units(sc[0][kb], W.g);
+        A.template softmax_block<FULL>(s, base, mask, W.g);
+    }
+
+    // GB: group B (stages K), else group A (stages V).  R holds this
+    // group's plane of block 1; tb2 the page ids of block 2; run this
+    // wave's running scale.
+    template <bool GB>
+    __device__ __forceinline__ void run(PlaneF32 &R, float &run, int tb2, uint64_t mask_c, uint64_t mask_n,
+                                        int nblk)
+    {
+        const int ws = W.w & 3;
+        f4 s[NCG][2][2]; // a block's scores, then its P (softmax_block)
+        if (GB && live(0))
+            scores(0, s);
+        int n = 0;
+        auto step = [&](auto full) {
+            constexpr bool FULL = decltype(full)::value;
+            const int base = n * kTB, cur = n & 1;
+            // phase 1
+            if (!GB) {
+                __builtin_amdgcn_s_setprio(1);
+                if (n > 0 && live(base - kTB))
+                    pv(cur ^ 1, s);
+                if (live(base))
+                    scores(cur, s);
+                __builtin_amdgcn_s_setprio(0);
+            } else {
+                if (live(base))
+                    softmax<FULL>(cur, s, base, mask_c);
+                plane_store_f32<0, 2>(ws, W.lane, mask_n, R, run, sc[0][cur ^ 1], A.neg1, S, cur ^ 1); // K (n + 1)
+                plane_load_f32<0, P>(a, W.kvh, ws, W.lane, tb2, R);                                   // K (n + 2)
+            }
+            __syncthreads();
+            // phase 2
+            if (!GB) {
+                if (live(base))
+                    softmax<FULL>(cur, s, base, mask_c);
+                plane_store_f32<1, 2>(ws, W.lane, mask_n, R, run, sc[1][cur ^ 1], A.neg1, S, cur ^ 1); // V (n + 1)
+                plane_load_f32<1, P>(a, W.kvh, ws, W.lane, tb2, R);                                   // V (n + 2)
+            } else {
+                __builtin_amdgcn_s_setprio(1);
+                if (live(base))
+                    pv(cur, s);
+                if (live(base + kTB))
+                    scores(cur ^ 1, s);
+                __builtin_amdgcn_s_setprio(0);
+            }
+            const uint64_t mask_nn = W.valid_mask(a, tb2, base + 2 * kTB);
+            tb2 = W.table(base + 3 * kTB);
+            __syncthreads();
+            mask_c = mask_n;
+            mask_n = mask_nn;
+            n++;
+        };
+        while (n < nblk && W.block_full(n * kTB, mask_c))
+            step(std::true_type{});
+        while (n < nblk)
+            step(std::false_type{});
+        if (!GB && nblk > 0 && live((nblk - 1) * kTB))
+            pv((nblk - 1) & 1, s);
+    }
+};
+
+template <int HD, int P, int NCG>
+__global__ __launch_bounds__(512) void attn_prefill_ppf(PrefillArgs a)
+{
+    static_assert(HD == 128, "f32 ping-pong staging maps head_dim 128");
+    constexpr int NW = PingPongF<HD, P, NCG>::NW;
+    const PrefillWork<P, NCG, NW, true> W(a);
+    __shared__ Lds<HD, KV_F32, 2> S;
+    __shared__ __attribute__((aligned(16))) float sc[2][2][4];
+    WaveAttn<HD, KV_F32, NCG> A;
+    const int nblk = (W.wg_len + kTB - 1) / kTB;
+    const bool gb = W.w >= NW / 2;
+    const int ws = W.w & 3;
+
+    // prologue: both planes of block 0 staged (B: K, A: V), and each group's
+    // plane of block 1 loaded; block 0's loads are in flight while Q is
+    // loaded and split
+    const int tb0 = W.table(0), tb1 = W.table(kTB);
+    PlaneF32 R;
+    float run = 0.0f;
+    if (gb)
+        plane_load_f32<0, P>(a, W.kvh, ws, W.lane, tb0, R);
+    else
+        plane_load_f32<1, P>(a, W.kvh, ws, W.lane, tb0, R);
+    A.template init<true>(a, W.b, W.kvh, W.col0, W.start, W.mapped, W.wave_active, W.j, W.g);
+    const uint64_t mask_c = W.valid_mask(a, tb0, 0);
+    const uint64_t mask_n = W.valid_mask(a, tb1, kTB);
+    if (gb) {
+        plane_store_f32<0, 2>(ws, W.lane, mask_c, R, run, sc[0][0], A.neg1, S, 0);
+        plane_load_f32<0, P>(a, W.kvh, ws, W.lane, tb1, R);
+    } else {
+        plane_store_f32<1, 2>(ws, W.lane, mask_c, R, run, sc[1][0], A.neg1, S, 0);
+        plane_load_f32<1, P>(a, W.kvh, ws, W.lane, tb1, R);
+    }
+    const int tb2 = W.table(2 * kTB);
+    __syncthreads();
+    PingPongF<HD, P, NCG> pp{a, W, S, sc, A};
+    if (gb)
+        pp.template run<true>(R, run, tb2, mask_c, mask_n, nblk);
+    else
+        pp.template run<false>(R, run, tb2, mask_c, mask_n, nblk);
+    if (W.wave_active) {
+        A.v_units_out();
+        A.finish(a, W.b, W.kvh, W.col0, W.j, W.g);
+    }
+}
+
 } // namespace mfma_prefill
 
 bool mfma_prefill_supported(const PoolLayout &L, int num_heads)
@@ -2032,11 +2346,11 @@ constexpr int prefill_ncg()
     return HD == 64 ? 2 : 1;
 }
 
-// The register-staged kernel (attn_prefill_lds) now serves f32 pages (8-wave
-// workgroups over one buffer: their block maxima are exchanged at its
-// barrier, every wave staging) and q8_0 pages at head_dim 64 (4-wave
-// workgroups over one buffer).  fp16 pages and the quantised pages at
-// head_dim 128 run the ping-pong kernels.
+// The register-staged kernel (attn_prefill_lds) now serves f32 pages at
+// head_dim 64 (8-wave workgroups over one buffer: their block maxima are
+// exchanged at its barrier, every wave staging) and q8_0 pages at head_dim
+// 64 (4-wave workgroups over one buffer).  fp16 pages, and f32 and the
+// quantised pages at head_dim 128, run the ping-pong kernels.
 template <int HD, int KT>
 constexpr int kPrefillWaves = KT == KV_F32 ? 8 : 4;
 
@@ -2054,6 +2368,10 @@ constexpr int prefill_lds_ncg()
 
 // The ping-pong kernels hold two column groups per wave.
 constexpr int kPrefillPingPongNcg = 2;
+// The f32 ping-pong kernel holds one column group per wave: its staging
+// keeps a plane's 32 KiB (32 VGPRs per thread) in flight beside each wave's
+// state, 223 VGPRs with one group, and two groups spill 524.
+constexpr int kPrefillF32Ncg = 1;
 
 template <int HD, int KT>
 static void launch_lds(const PrefillArgs &a, hipStream_t st)
@@ -2078,6 +2396,19 @@ static void launch_lds(const PrefillArgs &a, hipStream_t st)
             break;
         default:
             hipLaunchKernelGGL((attn_prefill_pp<HD, 64, NCG>), grid(NCG, 8), dim3(512), 0, st, a);
+            break;
+        }
+    } else if constexpr (KT == KV_F32 && HD == 128) {
+        constexpr int NCG = kPrefillF32Ncg;
+        switch (a.L.page_tokens) {
+        case 16:
+            hipLaunchKernelGGL((attn_prefill_ppf<HD, 16, NCG>), grid(NCG, 8), dim3(512), 0, st, a);
+            break;
+        case 32:
+            hipLaunchKernelGGL((attn_prefill_ppf<HD, 32, NCG>), grid(NCG, 8), dim3(512), 0, st, a);
+            break;
+        default:
+            hipLaunchKernelGGL((attn_prefill_ppf<HD, 64, NCG>), grid(NCG, 8), dim3(512), 0, st, a);
             break;
         }
     } else if constexpr ((KT == KV_Q8_0 || KT == KV_Q4_0) && HD == 128) {

@@ -366,12 +366,17 @@ def test_prefill_shapes(gi, oracle, dev, kv_type, H, kvh, hd, P):
     prefill_case(gi, oracle, dev, kv_type, H, kvh, hd, P, [3, 45], 37, seed=80 + kv_type)
 
 
-@pytest.mark.parametrize("hd,P", [(128, 16), (64, 32)])
-def test_prefill_f32_wide_range(gi, oracle, dev, hd, P):
-    """f32 pages whose magnitude moves by up to 10^9 between 64-token
-    blocks (K 1e-4 .. 1e5 with q at 1e-5, V 1e-5 .. 1e5): the staged kernel's workgroup
-    block scales must keep the 1e-5 bound of the f32 path.  A 200-query
-    chunk at start 300, batch 2."""
+@pytest.mark.parametrize("hd,P,period,vcols", [(128, 16, 64, False), (64, 32, 64, False), (128, 32, 16, True),
+                                                (128, 64, 24, True)],
+                         ids=["hd128-p16-block", "hd64-p32-block", "hd128-p32-16tok-vcols", "hd128-p64-24tok-vcols"])
+def test_prefill_f32_wide_range(gi, oracle, dev, hd, P, period, vcols):
+    """f32 pages whose magnitude moves by up to 10^9 every `period` tokens
+    (K 1e-4 .. 1e5 with q at 1e-5, V 1e-5 .. 1e5), and with vcols V's
+    32-dimension groups also 1, 1e3, 1e-3 and 10 apart.  The kernels' operand
+    scales (per 64-token block and workgroup in the staged kernel, per
+    16-token group of K and 32-dimension group of V in the f32 ping-pong
+    kernel) must keep the 1e-5 bound of the f32 path.  A 200-query chunk at
+    start 300, batch 2."""
     import torch
     H, kvh = 16, 4
     kv_dim = kvh * hd
@@ -387,9 +392,11 @@ def test_prefill_f32_wide_range(gi, oracle, dev, hd, P):
     for i, n in enumerate(lens):
         sid = mgr.AllocateSequence()
         ids, slots = mgr.AppendTokens(sid, n)
-        blk = (np.arange(n) // 64 + i) % len(kf)
+        blk = (np.arange(n) // period + i) % len(kf)
         k = (oracle.normal(600 + i, (n, kv_dim)) * kf[blk][:, None]).astype(np.float32)
         v = (oracle.normal(700 + i, (n, kv_dim)) * vf[blk][:, None]).astype(np.float32)
+        if vcols:
+            v *= np.array([1.0, 1e3, 1e-3, 10.0], np.float32)[(np.arange(kv_dim) % hd) // 32][None, :]
         pool.Write(0, torch.from_numpy(ids).to(dev), torch.from_numpy(slots).to(dev),
                    torch.from_numpy(k).to(dev), torch.from_numpy(v).to(dev))
         ks.append(k)
@@ -429,7 +436,7 @@ def test_prefill_q8_llama8b_chunks(gi, oracle, dev):
     prefill_case(gi, oracle, dev, 2, 32, 8, 128, 16, [1024, 512], 512, seed=70)
 
 
-@pytest.mark.parametrize("kv_type", [1, 2, 3], ids=["f16", "q8_0", "q4_0"])
+@pytest.mark.parametrize("kv_type", [0, 1, 2, 3], ids=["f32", "f16", "q8_0", "q4_0"])
 @pytest.mark.parametrize("P", [32, 64])
 def test_prefill_llama8b_large_pages(gi, oracle, dev, kv_type, P):
     """Llama-3-8B shape over pages of 32 and 64 tokens with 256-query
