@@ -1052,7 +1052,10 @@ __device__ __forceinline__ h8 ld_frag(const uint8_t *p, int off)
 // steps ahead followed by its products, so that a read has RA steps of
 // products to land (the scheduler would otherwise sink every read next to
 // its products and wait out the LDS latency each time).
-template <int NF, int M, int R, int RA>
+// VM > 0: one global load after the products of every VM-th step (from
+// step 0), so that the load instructions, which hold the wave while the
+// address unit takes them, issue between products.
+template <int NF, int M, int R, int RA, int VM = 0>
 __device__ __forceinline__ void read_ahead_order()
 {
     __builtin_amdgcn_sched_group_barrier(0x100, RA * R, 0);
@@ -1061,8 +1064,16 @@ __device__ __forceinline__ void read_ahead_order()
         if (f + RA < NF)
             __builtin_amdgcn_sched_group_barrier(0x100, R, 0);
         __builtin_amdgcn_sched_group_barrier(0x008, M, 0);
+        if (VM > 0 && f % VM == 0)
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
     }
 }
+
+// No extra work between the products of pv_block.
+struct NoLoads {
+    static constexpr int N = 0;
+    __device__ void operator()(int) const {}
+};
 
 // Per-wave attention state over NCG column groups of 16 (query, head)
 // columns: Q^T operands, running maximum and sum, and the O accumulators.
@@ -1514,8 +1525,11 @@ struct WaveAttn {
     }
 
     // O += P V over the block in V buffer vb, P as softmax_block left it.
-    template <class LDS>
-    __device__ __forceinline__ void pv_block(const LDS &S, int vb, const f4 (&st)[NCG][2][2], int j, int g)
+    // `loads` (N > 0): N global loads, load c issued after the products of
+    // step c * (steps / N).
+    template <class LDS, class LD = NoLoads>
+    __device__ __forceinline__ void pv_block(const LDS &S, int vb, const f4 (&st)[NCG][2][2], int j, int g,
+                                             const LD &loads = LD{})
     {
         const uint8_t *vp[2] = {v_lane(S, vb, 0, j, g, false), v_lane(S, vb, 1, j, g, false)};
         const uint8_t *vlp[2] = {LOP ? v_lane(S, vb, 0, j, g, true) : vp[0], LOP ? v_lane(S, vb, 1, j, g, true) : vp[1]};
@@ -1544,8 +1558,11 @@ struct WaveAttn {
                 if (LOP)
                     o[cg][nb] = mfma(phh, vl[f % (RA + 1)], o[cg][nb]);
             }
+            if constexpr (LD::N > 0)
+                if (f % (NF / LD::N) == 0)
+                    loads(f / (NF / LD::N));
         }
-        read_ahead_order<NF, NPR * NCG, NRD, RA>();
+        read_ahead_order<NF, NPR * NCG, NRD, RA, (LD::N > 0 ? NF / LD::N : 0)>();
     }
 
     // O of every column times f (an exact power of two).
@@ -2087,8 +2104,11 @@ struct PlaneF32 {
     u4 x[8];
 };
 
+// This lane's address of chunk 0 of the K (PLANE 0) or V plane of the block
+// whose page ids are in tb (lane l: token l); chunk c lies plane_step(c)
+// floats further.
 template <int PLANE, int P>
-__device__ __forceinline__ void plane_load_f32(const PrefillArgs &a, int kvh, int ws, int lane, int tb, PlaneF32 &R)
+__device__ __forceinline__ const float *plane_ptr_f32(const PrefillArgs &a, int kvh, int ws, int lane, int tb)
 {
     constexpr int HD = 128;
     const PoolLayout &L = a.L;
@@ -2096,21 +2116,42 @@ __device__ __forceinline__ void plane_load_f32(const PrefillArgs &a, int kvh, in
     if (PLANE == 0) {
         const int pr = __builtin_amdgcn_readlane(tb, 16 * ws);
         const int64_t pg = (pr >= 0 && pr < np) ? pr : 0;
-        const float *kp = reinterpret_cast<const float *>(a.base + pg * L.page_bytes + L.k_off) +
-                          ((int64_t)kvh * P + (16 * ws) % P) * HD + 4 * lane; // lane l: token l/32, dims 4(l%32)
-#pragma unroll
-        for (int c = 0; c < 8; c++)
-            R.x[c] = *reinterpret_cast<const u4 *>(kp + 2 * c * HD);
-    } else {
-        const int t0 = 4 * (lane & 15);
-        const int pr = __shfl(tb, t0);
-        const int64_t pg = (pr >= 0 && pr < np) ? pr : 0;
-        const float *vp = reinterpret_cast<const float *>(a.base + pg * L.page_bytes + L.v_off) +
-                          ((int64_t)kvh * HD + 32 * ws + (lane >> 4)) * P + t0 % P;
-#pragma unroll
-        for (int c = 0; c < 8; c++)
-            R.x[c] = *reinterpret_cast<const u4 *>(vp + 4 * c * P);
+        return reinterpret_cast<const float *>(a.base + pg * L.page_bytes + L.k_off) +
+               ((int64_t)kvh * P + (16 * ws) % P) * HD + 4 * lane; // lane l: token l/32, dims 4(l%32)
     }
+    const int t0 = 4 * (lane & 15);
+    const int pr = __shfl(tb, t0);
+    const int64_t pg = (pr >= 0 && pr < np) ? pr : 0;
+    return reinterpret_cast<const float *>(a.base + pg * L.page_bytes + L.v_off) +
+           ((int64_t)kvh * HD + 32 * ws + (lane >> 4)) * P + t0 % P;
+}
+
+template <int PLANE, int P>
+__device__ constexpr int plane_step(int c)
+{
+    return PLANE == 0 ? 2 * c * 128 : 4 * c * P;
+}
+
+// The eight loads of a plane from plane_ptr_f32, one per call (pv_block
+// spreads them between its products).
+template <int PLANE, int P>
+struct PlaneLoads {
+    static constexpr int N = 8;
+    const float *p;
+    PlaneF32 &R;
+    __device__ __forceinline__ void operator()(int c) const
+    {
+        R.x[c] = *reinterpret_cast<const u4 *>(p + plane_step<PLANE, P>(c));
+    }
+};
+
+template <int PLANE, int P>
+__device__ __forceinline__ void plane_load_f32(const PrefillArgs &a, int kvh, int ws, int lane, int tb, PlaneF32 &R)
+{
+    const PlaneLoads<PLANE, P> ld{plane_ptr_f32<PLANE, P>(a, kvh, ws, lane, tb), R};
+#pragma unroll
+    for (int c = 0; c < 8; c++)
+        ld(c);
 }
 
 // Converts a plane of plane_load_f32 into the hi + lo fp16 planes of buffer
@@ -2127,7 +2168,6 @@ __device__ __forceinline__ void plane_store_f32(int ws, int lane, uint64_t vmask
 {
     using G = SwzGeom<128>;
     float x[8][4];
-    float m = 0.0f;
 #pragma unroll
     for (int c = 0; c < 8; c++) {
         // words copied out first: hipcc's __builtin_bit_cast of an
@@ -2136,21 +2176,37 @@ __device__ __forceinline__ void plane_store_f32(int ws, int lane, uint64_t vmask
 #pragma unroll
         for (int i = 0; i < 4; i++)
             w[i] = R.x[c][i];
-        if (PLANE == 0) {
-            const bool live = (vmask >> (16 * ws + 2 * c + (lane >> 5))) & 1u;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                x[c][i] = __builtin_bit_cast(float, w[i]);
-                if (live)
-                    m = fmaxf(m, fabsf(x[c][i]));
-            }
-        } else {
-            const uint32_t live = (uint32_t)(vmask >> (4 * (lane & 15))) & 0xFu;
+        for (int i = 0; i < 4; i++)
+            x[c][i] = __builtin_bit_cast(float, w[i]);
+    }
+    // largest live magnitude: maximumNumber with |x| operands compiles to
+    // v_max3_f32 with abs modifiers (two values per instruction); a block
+    // with every token live (uniform branch) needs no masking
+    float m = 0.0f;
+    if (vmask == ~0ull) {
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                x[c][i] = ((live >> i) & 1u) ? __builtin_bit_cast(float, w[i]) : 0.0f;
-                m = fmaxf(m, fabsf(x[c][i]));
+        for (int c = 0; c < 8; c++)
+#pragma unroll
+            for (int i = 0; i < 4; i += 2)
+                m = maxnum3(m, fabsf(x[c][i]), fabsf(x[c][i + 1]));
+    } else {
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            if (PLANE == 0) {
+                const bool live = (vmask >> (16 * ws + 2 * c + (lane >> 5))) & 1u;
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    x[c][i] = live ? x[c][i] : 0.0f; // K of a dead token: its scores are masked
+            } else {
+                const uint32_t live = (uint32_t)(vmask >> (4 * (lane & 15))) & 0xFu;
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    x[c][i] = ((live >> i) & 1u) ? x[c][i] : 0.0f;
             }
+#pragma unroll
+            for (int i = 0; i < 4; i += 2)
+                m = maxnum3(m, fabsf(x[c][i]), fabsf(x[c][i + 1]));
         }
     }
     run = block_scale(wave_max_nonneg(m), run);
@@ -2182,12 +2238,20 @@ __device__ __forceinline__ void plane_store_f32(int ws, int lane, uint64_t vmask
 
 // f32 pages (head_dim 128), two waves per SIMD in ping-pong as
 // attn_prefill_ppq, with K and V staged through registers into hi + lo fp16
-// planes (two LDS buffers each): group B stages the K plane of block n + 1
-// in phase 1 of block n, group A the V plane in phase 2, each loading its
-// plane one block ahead.  Every staging wave picks its own power-of-two
-// scale (block_scale), so no barrier is spent on block maxima: a K scale
-// covers 16 tokens (the softmax takes a factor per half of a lane's
-// tokens, k_units), a V scale 32 dimensions (two O tiles, v_units).
+// planes (two LDS buffers each): group B converts the K plane of block n + 1
+// at the start of phase 1 of block n, group A the V plane at the start of
+// phase 2.  Each group loads its plane in its product phase before, one
+// load instruction every other step of P V (a load holds the wave while the
+// address unit takes it, about as long as a product), so that the 32
+// staging registers are not live through the softmax.
+// Every staging wave picks its own power-of-two scale (block_scale), so no
+// barrier is spent on block maxima: a K scale covers 16 tokens (the softmax
+// takes a factor per half of a lane's tokens, k_units), a V scale 32
+// dimensions (two O tiles, v_units).  Per block n:
+//   phase 1: A: P V (n - 1) with the loads of V (n + 1), scores (n)
+//            B: convert K (n + 1), softmax (n)
+//   phase 2: A: convert V (n + 1), softmax (n)
+//            B: P V (n) with the loads of K (n + 2), scores (n + 1)
 template <int HD, int P, int NCG>
 struct PingPongF {
     static constexpr int NW = 8;
@@ -2205,6 +2269,21 @@ struct PingPongF {
         A.v_units(sc[1][vb]);
         A.pv_block(S, vb, s, W.j, W.g);
     }
+    // P V with a plane's loads issued between its products (or alone when
+    // this wave has no P V to do)
+    template <int PLANE>
+    __device__ __forceinline__ void pv_loads(bool do_pv, int vb, const f4 (&s)[NCG][2][2], int tb, PlaneF32 &R)
+    {
+        const PlaneLoads<PLANE, P> ld{plane_ptr_f32<PLANE, P>(a, W.kvh, W.w & 3, W.lane, tb), R};
+        if (do_pv) {
+            A.v_units(sc[1][vb]);
+            A.pv_block(S, vb, s, W.j, W.g, ld);
+        } else {
+#pragma unroll
+            for (int c = 0; c < 8; c++)
+                ld(c);
+        }
+    }
     template <bool FULL>
     __device__ __forceinline__ void softmax(int kb, f4 (&s)[NCG][2][2], int base, uint64_t mask)
     {
@@ -2212,11 +2291,12 @@ struct PingPongF {
         A.template softmax_block<FULL>(s, base, mask, W.g);
     }
 
-    // GB: group B (stages K), else group A (stages V).  R holds this
-    // group's plane of block 1; tb2 the page ids of block 2; run this
-    // wave's running scale.
+    // GB: group B (stages K), else group A (stages V).  R: B holds the K
+    // plane of block 1; tbn: the page ids of the block whose plane this
+    // group loads next (B: block 2, A: block 1); run: this wave's running
+    // scale.
     template <bool GB>
-    __device__ __forceinline__ void run(PlaneF32 &R, float &run, int tb2, uint64_t mask_c, uint64_t mask_n,
+    __device__ __forceinline__ void run(PlaneF32 &R, float &run, int tbn, uint64_t mask_c, uint64_t mask_n,
                                         int nblk)
     {
         const int ws = W.w & 3;
@@ -2227,37 +2307,37 @@ struct PingPongF {
         auto step = [&](auto full) {
             constexpr bool FULL = decltype(full)::value;
             const int base = n * kTB, cur = n & 1;
+            int tb2; // page ids of block n + 2
             // phase 1
             if (!GB) {
                 __builtin_amdgcn_s_setprio(1);
-                if (n > 0 && live(base - kTB))
-                    pv(cur ^ 1, s);
+                tb2 = W.table(base + 2 * kTB); // before the plane's loads: the mask below waits for it alone
+                pv_loads<1>(n > 0 && live(base - kTB), cur ^ 1, s, tbn, R); // P V (n - 1), loads of V (n + 1)
+                tbn = tb2;
                 if (live(base))
                     scores(cur, s);
                 __builtin_amdgcn_s_setprio(0);
             } else {
+                plane_store_f32<0, 2>(ws, W.lane, mask_n, R, run, sc[0][cur ^ 1], A.neg1, S, cur ^ 1); // K (n + 1)
                 if (live(base))
                     softmax<FULL>(cur, s, base, mask_c);
-                plane_store_f32<0, 2>(ws, W.lane, mask_n, R, run, sc[0][cur ^ 1], A.neg1, S, cur ^ 1); // K (n + 1)
-                plane_load_f32<0, P>(a, W.kvh, ws, W.lane, tb2, R);                                   // K (n + 2)
             }
             __syncthreads();
             // phase 2
             if (!GB) {
+                plane_store_f32<1, 2>(ws, W.lane, mask_n, R, run, sc[1][cur ^ 1], A.neg1, S, cur ^ 1); // V (n + 1)
                 if (live(base))
                     softmax<FULL>(cur, s, base, mask_c);
-                plane_store_f32<1, 2>(ws, W.lane, mask_n, R, run, sc[1][cur ^ 1], A.neg1, S, cur ^ 1); // V (n + 1)
-                plane_load_f32<1, P>(a, W.kvh, ws, W.lane, tb2, R);                                   // V (n + 2)
             } else {
                 __builtin_amdgcn_s_setprio(1);
-                if (live(base))
-                    pv(cur, s);
+                tb2 = tbn;
+                tbn = W.table(base + 3 * kTB);
+                pv_loads<0>(live(base), cur, s, tb2, R); // P V (n), loads of K (n + 2)
                 if (live(base + kTB))
                     scores(cur ^ 1, s);
                 __builtin_amdgcn_s_setprio(0);
             }
             const uint64_t mask_nn = W.valid_mask(a, tb2, base + 2 * kTB);
-            tb2 = W.table(base + 3 * kTB);
             __syncthreads();
             mask_c = mask_n;
             mask_n = mask_nn;
@@ -2285,10 +2365,10 @@ __global__ __launch_bounds__(512) void attn_prefill_ppf(PrefillArgs a)
     const bool gb = W.w >= NW / 2;
     const int ws = W.w & 3;
 
-    // prologue: both planes of block 0 staged (B: K, A: V), and each group's
-    // plane of block 1 loaded; block 0's loads are in flight while Q is
-    // loaded and split
-    const int tb0 = W.table(0), tb1 = W.table(kTB);
+    // prologue: both planes of block 0 staged (B: K, A: V), and B's plane of
+    // block 1 loaded; block 0's loads are in flight while Q is loaded and
+    // split
+    const int tb0 = W.table(0), tb1 = W.table(kTB), tb2 = W.table(2 * kTB);
     PlaneF32 R;
     float run = 0.0f;
     if (gb)
@@ -2303,15 +2383,13 @@ __global__ __launch_bounds__(512) void attn_prefill_ppf(PrefillArgs a)
         plane_load_f32<0, P>(a, W.kvh, ws, W.lane, tb1, R);
     } else {
         plane_store_f32<1, 2>(ws, W.lane, mask_c, R, run, sc[1][0], A.neg1, S, 0);
-        plane_load_f32<1, P>(a, W.kvh, ws, W.lane, tb1, R);
     }
-    const int tb2 = W.table(2 * kTB);
     __syncthreads();
     PingPongF<HD, P, NCG> pp{a, W, S, sc, A};
     if (gb)
         pp.template run<true>(R, run, tb2, mask_c, mask_n, nblk);
     else
-        pp.template run<false>(R, run, tb2, mask_c, mask_n, nblk);
+        pp.template run<false>(R, run, tb1, mask_c, mask_n, nblk);
     if (W.wave_active) {
         A.v_units_out();
         A.finish(a, W.b, W.kvh, W.col0, W.j, W.g);
