@@ -449,6 +449,52 @@ __device__ __forceinline__ void issue_f32(const DecodeArgs &a, int64_t pA, int64
     }
 }
 
+// fp16 K staged through LDS (one-round grids, head_dim 128).  Loaded
+// straight into operand registers, a K load touches 16 token rows, 64 bytes
+// of each, and one workgroup streams about 31 GB/s however many blocks it
+// keeps in flight; a probe of the same pages streams 35 GB/s with that
+// shape and 60 GB/s when each K load reads 1 KiB in one run (V's register
+// loads, 16 dimensions' rows on each page, are already such runs).  The
+// longest sequences of a ragged one-round batch stream at that rate, so
+// there K goes through LDS: every direct global->LDS load reads four whole
+// 256-byte token rows, and the operands read back are the bytes the
+// register loads would hold.  With sw(r) = ((r >> 1) & 12) | (r & 3), the
+// 16-byte slot 16r + (c ^ sw(r)) holds block token r, bytes 16c .. of its
+// row, so that the operand reads of 16 lanes fall on all 64 banks.
+struct F16KStage {
+    static constexpr int BYTES = 32 * 128 * 2, NLOAD = BYTES / 1024;
+    uint8_t k[BYTES];
+};
+
+__device__ __forceinline__ int f16_kswz(int r) { return ((r >> 1) & 12) | (r & 3); }
+
+__device__ __forceinline__ void issue_k_f16(const DecodeArgs &a, int64_t pA, int64_t pB, int sA, int sB,
+                                            int64_t koff, int lane, F16KStage &S)
+{
+    const PoolLayout &L = a.L;
+    const uint8_t *gA = a.base + pA * L.page_bytes + koff, *gB = a.base + pB * L.page_bytes + koff;
+    // load q reads block rows 4q .. 4q + 3 (tokens 0-15 on page A)
+#pragma unroll
+    for (int q = 0; q < F16KStage::NLOAD; q++) {
+        const int r = 4 * q + (lane >> 4);
+        const uint8_t *row = q < 4 ? gA + (int64_t)(sA + r) * 256 : gB + (int64_t)(sB + r - 16) * 256;
+        __builtin_amdgcn_global_load_lds(row + 16 * ((lane & 15) ^ f16_kswz(r)), (lds_ptr)&S.k[1024 * q], 16, 0,
+                                         kDecodeLdsAux);
+    }
+}
+
+// The operands load_k would hold, from the stage.
+__device__ __forceinline__ void read_k_f16(const F16KStage &S, int j, int g, h8 *k0, h8 *k1)
+{
+    const int tk0 = 8 * (j >> 2) + (j & 3), tk1 = tk0 + 4;
+    const int x0 = f16_kswz(tk0), x1 = f16_kswz(tk1);
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++) {
+        k0[kk] = *reinterpret_cast<const h8 *>(&S.k[(16 * tk0 + ((4 * kk + g) ^ x0)) * 16]);
+        k1[kk] = *reinterpret_cast<const h8 *>(&S.k[(16 * tk1 + ((4 * kk + g) ^ x1)) * 16]);
+    }
+}
+
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float x)
 {
@@ -1061,10 +1107,11 @@ __device__ __forceinline__ void softmax_pv_q(f4 s0, f4 s1, QBlock<KT, HD> &B, in
 }
 
 // Body of the decode kernels.  KT: KV_F16, or KV_Q8_0 / KV_Q4_0 (packed GP
-// only).
-template <int KT, int HD, int GP, bool NT, bool PREFETCH, int NW>
+// only).  STG: fp16 pages with K staged through LDS (F16KStage).
+template <int KT, int HD, int GP, bool NT, bool PREFETCH, int NW, bool STG = false>
 __device__ __forceinline__ void decode_body(const DecodeArgs &a)
 {
+    static_assert(!STG || (KT == KV_F16 && HD == 128), "staged fp16 pages at head_dim 128");
     constexpr int KK = HD / 32, NB = HD / 16;
     constexpr bool QUANT = KT == KV_Q8_0 || KT == KV_Q4_0;
     constexpr bool F32 = KT == KV_F32;
@@ -1142,12 +1189,13 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
                                  a.new_v[e0 + d], true);
     };
 
-    // The per-wave staging areas of the block loop (quantised pages) and,
-    // after it, the cross-wave merge share one LDS allocation.  (fp16 pages
-    // load straight into registers: staging them through LDS measured
-    // slower.)
+    // The per-wave staging areas of the block loop (quantised, f32 and
+    // staged fp16 pages) and, after it, the cross-wave merge share one LDS
+    // allocation.  (fp16 pages otherwise load straight into registers: at
+    // grids of several rounds staging them measured slower.)
     constexpr int STAGE_BYTES = QUANT ? NW * (int)sizeof(QStage<QUANT ? KT : KV_Q8_0, HD>)
-                                : F32 ? NW * (int)sizeof(F32Stage<HD>) : 0;
+                                : F32 ? NW * (int)sizeof(F32Stage<HD>)
+                                : STG ? NW * (int)sizeof(F16KStage) : 0;
     constexpr int MERGE_BYTES = NW * 16 * HD * (int)sizeof(float);
     __shared__ __align__(16) uint8_t s_stage[STAGE_BYTES > MERGE_BYTES ? STAGE_BYTES : MERGE_BYTES];
     float(*s_o)[16][HD] = reinterpret_cast<float(*)[16][HD]>(s_stage);
@@ -1413,6 +1461,58 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
                 base = next;
             }
         }
+    } else if constexpr (STG) {
+        if (base < t1) {
+            // Per block n: wait for K (n) in the stage, read its operands,
+            // issue K (n + 1) into the stage; scores; wait for V (n) (issued
+            // after P V (n - 1), before K (n + 1)); softmax and P V; issue V
+            // (n + 1) into registers.  In flight at the top of block n + 1:
+            // K (n + 1), then V (n + 1), so vmcnt(NLOAD) waits for K alone.
+            F16KStage &Sk = reinterpret_cast<F16KStage *>(s_stage)[w];
+            h8 v[NB];
+            int64_t pA, pB;
+            int sA, sB;
+            int ok;
+            store_done(base);
+            block_pages(a, bt, base, t1, pA, pB, sA, sB, ok);
+            issue_k_f16(a, pA, pB, sA, sB, koff, lane, Sk);
+            load_v<HD, NT>(a, pA, pB, sA, sB, voff, j, g, v);
+            load_q();
+            if (store_late)
+                store_token();
+            // the first block: everything issued so far
+            __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0)
+            for (;;) {
+                h8 k0[KK], k1[KK];
+                read_k_f16(Sk, j, g, k0, k1);
+                const int next = base + stride;
+                const bool more = next < t1;
+                int64_t nA = pA, nB = pB;
+                int nsA = sA, nsB = sB;
+                int nok = ok;
+                if (more) {
+                    store_done(next);
+                    block_pages(a, bt, next, t1, nA, nB, nsA, nsB, nok);
+                    __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0): this block's K reads returned
+                    issue_k_f16(a, nA, nB, nsA, nsB, koff, lane, Sk);
+                }
+                f4 s0, s1;
+                qk<HD, GP>(k0, k1, qh, ql, s0, s1);
+                softmax_pv<HD, GP>(s0, s1, v, base, ok, t1, j, g, c, S);
+                if (!more)
+                    break;
+                __builtin_amdgcn_sched_barrier(0);
+                load_v<HD, NT>(a, nA, nB, nsA, nsB, voff, j, g, v);
+                pA = nA;
+                pB = nB;
+                sA = nsA;
+                sB = nsB;
+                ok = nok;
+                base = next;
+                // K of the next block has arrived (its V, issued after it, may still be in flight)
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm(F16KStage::NLOAD));
+            }
+        }
     } else if (base < t1) {
         h8 k0[KK], k1[KK], v[NB];
         int64_t pA, pB;
@@ -1521,10 +1621,10 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
 // are issued as soon as this block's K (then V) registers are consumed.
 // OCC: minimum waves per SIMD requested from the register allocator.  NW:
 // waves per workgroup (DecodeArgs.waves).
-template <int HD, int GP, bool NT, bool PREFETCH, int OCC, int NW = 4>
+template <int HD, int GP, bool NT, bool PREFETCH, int OCC, int NW = 4, bool STG = false>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(OCC))) void attn_mfma_f16(DecodeArgs a)
 {
-    decode_body<KV_F16, HD, GP, NT, PREFETCH, NW>(a);
+    decode_body<KV_F16, HD, GP, NT, PREFETCH, NW, STG>(a);
 }
 
 // f32 pages, packed form (GP = G in {1, 2, 4, 8}).
@@ -1568,10 +1668,24 @@ constexpr bool kDecodePrefetch = true;
 constexpr int kDecodeOcc = 1;
 constexpr bool kDecodePack = true;
 
+// K staged through LDS (F16KStage) where one workgroup's streaming rate sets
+// the launch's length: grids of one round (eight-wave workgroups) whose
+// splits hold at most kDecodeStgTokens tokens.  Same box, batch 32 x U[512,
+// 4096] (page 16): 0.0638-0.0646 against 0.0723-0.0750 ms per launch; 8 x
+// 32768 in splits of 8192 (page 32), where every CU streams until the end
+// and the aggregate rate rules: 0.1751 against 0.1652, so those keep the
+// register loads.
+constexpr int kDecodeStgTokens = 4096;
+
 template <int HD, int GP>
 static void launch_mfma_hd(const DecodeArgs &a, dim3 grid, hipStream_t st)
 {
-    if (a.waves == 8)
+    const int P = a.L.page_tokens;
+    if (HD == 128 && GP != 0 && a.waves == 8 && (P == 16 || P == 32) && a.split_tokens <= kDecodeStgTokens)
+        hipLaunchKernelGGL((mfma_decode::attn_mfma_f16<HD, GP, kDecodeNt, kDecodePrefetch, kDecodeOcc, 8,
+                                                       HD == 128 && GP != 0>),
+                           grid, dim3(512), 0, st, a);
+    else if (a.waves == 8)
         hipLaunchKernelGGL((mfma_decode::attn_mfma_f16<HD, GP, kDecodeNt, kDecodePrefetch, kDecodeOcc, 8>),
                            grid, dim3(512), 0, st, a);
     else

@@ -145,16 +145,17 @@ def test_attention_plan_reports_kernels_waves_and_fusion(gi, oracle, dev):
         pool.close()
 
 
-@pytest.mark.parametrize("kv_type", [1, 2, 3], ids=["f16", "q8_0", "q4_0"])
-def test_decode_four_and_eight_wave_workgroups_match_the_oracle(gi, oracle, dev, kv_type):
+@pytest.mark.parametrize("kv_type,P", [(1, 16), (1, 32), (2, 16), (3, 16)],
+                         ids=["f16-p16", "f16-p32", "q8_0-p16", "q4_0-p16"])
+def test_decode_four_and_eight_wave_workgroups_match_the_oracle(gi, oracle, dev, kv_type, P):
     """33 sequences x 8 kv heads make 264 workgroups, more than the CUs: four
     waves each.  The first 32 make 256: eight waves each, every wave taking
-    every eighth 32-token block.  Both against the oracle on the stored bits,
-    with lengths that leave each wave a different number of blocks (and some
-    waves none)."""
+    every eighth 32-token block (fp16 pages then stage K through LDS).  Both
+    against the oracle on the stored bits, with lengths that leave each wave
+    a different number of blocks (and some waves none)."""
     import torch
-    H, kvh, hd, P = 32, 8, 128, 16
-    rng = np.random.default_rng(77 + kv_type)
+    H, kvh, hd = 32, 8, 128
+    rng = np.random.default_rng(77 + kv_type + P)
     lens = [int(x) for x in rng.integers(1, 700, size=33)]
     lens[0], lens[1], lens[2] = 1, 32 * 8, 32 * 8 + 1
     pop = Populated(gi, dev, kv_type, 1, kvh, hd, P, lens, seed=78 + kv_type)
