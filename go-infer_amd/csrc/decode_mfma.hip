@@ -1189,10 +1189,10 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
                                  a.new_v[e0 + d], true);
     };
 
-    // The per-wave staging areas of the block loop (quantised, f32 and
-    // staged fp16 pages) and, after it, the cross-wave merge share one LDS
-    // allocation.  (fp16 pages otherwise load straight into registers: at
-    // grids of several rounds staging them measured slower.)
+    // The per-wave staging areas of the block loop (quantised and f32 pages,
+    // and fp16 K) and, after it, the cross-wave merge share one LDS
+    // allocation.  (fp16 V loads straight into registers: staging V as well
+    // measured slower.)
     constexpr int STAGE_BYTES = QUANT ? NW * (int)sizeof(QStage<QUANT ? KT : KV_Q8_0, HD>)
                                 : F32 ? NW * (int)sizeof(F32Stage<HD>)
                                 : STG ? NW * (int)sizeof(F16KStage) : 0;
@@ -1668,12 +1668,14 @@ constexpr bool kDecodePrefetch = true;
 constexpr int kDecodeOcc = 1;
 constexpr bool kDecodePack = true;
 
-// K staged through LDS (F16KStage) where one workgroup's streaming rate sets
-// the launch's length: grids of one round (eight-wave workgroups) whose
-// splits hold at most kDecodeStgTokens tokens.  Same box, batch 32 x U[512,
-// 4096] (page 16): 0.0638-0.0646 against 0.0723-0.0750 ms per launch; 8 x
-// 32768 in splits of 8192 (page 32), where every CU streams until the end
-// and the aggregate rate rules: 0.1751 against 0.1652, so those keep the
+// K staged through LDS (F16KStage) for head_dim 128 and pages of 16 or 32
+// tokens: in four-wave workgroups (grids of several rounds), and in
+// eight-wave ones (one round) whose splits hold at most kDecodeStgTokens
+// tokens, where one workgroup's streaming rate sets the launch's length.
+// Same box: batch 256 x 8192 (page 16) 1.273-1.275 against 1.286 ms per
+// launch; batch 32 x U[512, 4096] (page 16) 0.0638-0.0646 against
+// 0.0723-0.0750; but 8 x 32768 in eight-wave splits of 8192 (page 32), where
+// every CU streams until the end, 0.1751 against 0.1652, so those keep the
 // register loads.
 constexpr int kDecodeStgTokens = 4096;
 
@@ -1681,16 +1683,22 @@ template <int HD, int GP>
 static void launch_mfma_hd(const DecodeArgs &a, dim3 grid, hipStream_t st)
 {
     const int P = a.L.page_tokens;
-    if (HD == 128 && GP != 0 && a.waves == 8 && (P == 16 || P == 32) && a.split_tokens <= kDecodeStgTokens)
-        hipLaunchKernelGGL((mfma_decode::attn_mfma_f16<HD, GP, kDecodeNt, kDecodePrefetch, kDecodeOcc, 8,
-                                                       HD == 128 && GP != 0>),
-                           grid, dim3(512), 0, st, a);
-    else if (a.waves == 8)
-        hipLaunchKernelGGL((mfma_decode::attn_mfma_f16<HD, GP, kDecodeNt, kDecodePrefetch, kDecodeOcc, 8>),
-                           grid, dim3(512), 0, st, a);
-    else
+    const bool stg = HD == 128 && GP != 0 && (P == 16 || P == 32);
+    constexpr bool STG = HD == 128 && GP != 0;
+    if (a.waves == 8) {
+        if (stg && a.split_tokens <= kDecodeStgTokens)
+            hipLaunchKernelGGL((mfma_decode::attn_mfma_f16<HD, GP, kDecodeNt, kDecodePrefetch, kDecodeOcc, 8, STG>),
+                               grid, dim3(512), 0, st, a);
+        else
+            hipLaunchKernelGGL((mfma_decode::attn_mfma_f16<HD, GP, kDecodeNt, kDecodePrefetch, kDecodeOcc, 8>),
+                               grid, dim3(512), 0, st, a);
+    } else if (stg) {
+        hipLaunchKernelGGL((mfma_decode::attn_mfma_f16<HD, GP, kDecodeNt, kDecodePrefetch, kDecodeOcc, 4, STG>),
+                           grid, dim3(256), 0, st, a);
+    } else {
         hipLaunchKernelGGL((mfma_decode::attn_mfma_f16<HD, GP, kDecodeNt, kDecodePrefetch, kDecodeOcc, 4>),
                            grid, dim3(256), 0, st, a);
+    }
 }
 
 // q4_0 pages are bound by the vector ALU: three waves per SIMD (the
