@@ -83,8 +83,14 @@ def check_decode(torch, gi, oracle, pool, bt_d, lens, q, out, kvh, hd, H, scale,
     return worst
 
 
-def test_config_c_full_shape(gi, oracle, dev):
+@pytest.mark.parametrize("kv_name", ["KV_F16", "KV_Q8_0", "KV_Q4_0"], ids=["f16", "q8_0", "q4_0"])
+def test_config_c_full_shape(gi, oracle, dev, kv_name):
+    """The headline shape at full size (256 sequences of 8192 tokens on a
+    fragmented pool), over fp16 pages and over the quantised pages that the
+    bench also reports: the decode step's stored bytes of whole sequences
+    equal the oracle's, and 16 sampled sequences' outputs match it."""
     import torch
+    kv_type = getattr(gi, kv_name)
     cfg = bench.CONFIGS["llama8b_b256_8k"]
     H, kvh, hd, P = cfg["q_heads"], cfg["kv_heads"], cfg["head_dim"], cfg["page_tokens"]
     kv_dim = kvh * hd
@@ -94,7 +100,7 @@ def test_config_c_full_shape(gi, oracle, dev):
     assert B == 256 and L == 8192 and cfg["frag"]
     mgr, pages, bt = bench.build_tables(gi, cfg, lens, seed)
     say("C: tables built, %d pages, max_blocks %d" % (pages, bt.shape[1]))
-    pool = gi.PagedKVCache(1, kvh, hd, P, pages, gi.KV_F16)
+    pool = gi.PagedKVCache(1, kvh, hd, P, pages, kv_type)
     rng = np.random.default_rng(seed + 3)
     whole = sorted(int(x) for x in rng.choice(B, size=8, replace=False))
     kept = fill_decode_pool(torch, gi, pool, bt, lens, P, kv_dim, dev, seed, set(whole), L - 1)
@@ -118,8 +124,8 @@ def test_config_c_full_shape(gi, oracle, dev):
         v = np.concatenate([kept[i][1], vh[i:i + 1]])
         ks, vs = pool.Get(0, bt_d[i], L)
         pool.synchronize()
-        assert np.array_equal(ks.cpu().numpy(), oracle.store_vectors(gi.KV_F16, k)), i
-        assert np.array_equal(vs.cpu().numpy(), oracle.store_vectors(gi.KV_F16, v)), i
+        assert np.array_equal(ks.cpu().numpy(), oracle.store_vectors(kv_type, k)), i
+        assert np.array_equal(vs.cpu().numpy(), oracle.store_vectors(kv_type, v)), i
     say("C: stored bytes of sequences %s equal the oracle's" % whole)
     sample = sorted(set(whole) | {int(x) for x in rng.choice(B, size=12, replace=False)} | {0, B - 1})
     assert len(sample) >= 16
