@@ -24,8 +24,8 @@
 //         scales as Q8_0;
 //   F32   two fp16 halves, hi and lo, of W * 2^e[r] (e[r] from the row's
 //         largest |w|, so both halves stay normal), and 2^-e[r] per row.
-// Rows of weights and activations are padded with zeros to multiples of 64,
-// so the product loop needs no bounds checks.
+// Rows of weights are padded with zeros to multiples of 128 and those of
+// activations to multiples of 64, so the product loops need no bounds checks.
 //
 // Activations are split per batch row into fp16 hi + lo of x * 2^e[b], so the
 // products keep float32 accuracy.  The matrix cores then compute W * x^T on
@@ -35,12 +35,17 @@
 // block, then multiply by d).  F32 weights take three products (hi*hi, hi*lo,
 // lo*hi).
 //
-// A workgroup owns a 64 x 64 (rows x batch) output tile.  Its four waves take
-// every fourth k-step each, and each wave streams its k-steps through its own
-// LDS stages by direct global->LDS loads, two steps ahead (one for F32,
-// whose stages are twice as large).  Waves 1-3 then leave their partial tiles
-// in LDS and wave 0 adds them to its own, so one launch covers the product
-// with no global reduction.
+// Two forms of the product:
+//   * matmul_lds (quantised weights, and batches under 128): a workgroup owns
+//     a 64 x 64 (rows x batch) output tile.  Its four waves take every fourth
+//     k-step each, and each wave streams its k-steps through its own LDS
+//     stages by direct global->LDS loads, two steps ahead (one for F32, whose
+//     stages are twice as large).  Waves 1-3 then leave their partial tiles
+//     in LDS and wave 0 adds them to its own, so one launch covers the
+//     product with no global reduction.
+//   * matmul_sk (F16 and F32 weights, batches of 128 and more): 128 x 128
+//     tiles over slices of the k-steps, the slices' partial tiles added by
+//     reduce_splits (described at the kernel).
 #include "../../include/goinfer_paged.h"
 #include "gi_common.h"
 #include "devbuf.h"
@@ -51,6 +56,8 @@
 #include <algorithm>
 #include <new>
 #include <string>
+#include <type_traits>
+#include <utility>
 
 namespace gi {
 namespace {
@@ -66,9 +73,11 @@ enum : int { W_F32 = 0, W_F16 = 1, W_Q4_0 = 2, W_Q8_0 = 8 }; // GGML type ids
 
 
 
-// Rows of weights and activations are padded to multiples of 64, the output
-// tile.
+// Activation rows are padded to multiples of 64, the batch side of the
+// 64 x 64 output tile; weight rows to multiples of 128, the row side of the
+// split-K tile (and so of 64 too).
 __host__ __device__ __forceinline__ int64_t round_pad(int64_t n) { return (n + 63) / 64 * 64; }
+__host__ __device__ __forceinline__ int64_t weight_rows_pad(int64_t n) { return (n + 127) / 128 * 128; }
 
 // Element (r, c) of a 16-bit matrix (or an int8 code matrix) with KS
 // k-steps of 32 columns, in operand order.
@@ -252,7 +261,7 @@ __global__ __launch_bounds__(256) void split_rows(const float *__restrict__ x, i
 struct MatArgs {
     int type;
     int rows, cols, batch;
-    int rows_pad;           // rows padded to a multiple of 64
+    int rows_pad;           // rows padded to a multiple of 128
     const uint8_t *a;      // F16 / F32-hi / Q8 codes / Q4 nibble bytes
     const uint8_t *a_lo;   // F32 lo
     const uint16_t *scales; // Q8 / Q4 block scales [cols/32][rows_pad]
@@ -425,6 +434,237 @@ __global__ __launch_bounds__(256) void matmul_lds(MatArgs a)
     }
 }
 
+// ---- 16-bit weights, batches of 128 and more: split-K ------------------------
+//
+// A workgroup of four waves owns a 128 x 128 (rows x batch) output tile over
+// one of S slices of the k-steps, and two workgroups share a CU.  Wave w
+// takes batch rows 32w .. 32w + 31 of the tile and all 128 rows, so each
+// weight fragment read from LDS feeds four products (two batch tiles, hi and
+// lo) and each activation fragment eight (the row tiles).  Per k-step the
+// eight weight tiles (shared by the waves, each loading two) and every wave's
+// activation halves arrive by direct global->LDS loads two k-steps ahead,
+// through three stages; one barrier per k-step hands a stage from the loads
+// to the products.  The per-CU load volume is 24 KiB per 128 products against
+// 12 KiB per 32 in the 64 x 64 form.  With S > 1 the partial tiles go to a
+// workspace and reduce_splits adds them.  Quantised weights keep the 64 x 64
+// form: their per-block scale multiply-adds need 272 registers here (one
+// wave per SIMD), and measured slower (Q8_0 50.5 against 41.8 us per call
+// at 256 x 4096 x 4096).
+
+struct SKArgs {
+    MatArgs m;
+    int splits;   // S: slices of the k-steps
+    int ks_per;   // k-steps per slice (the last may have fewer)
+    float *part;  // S > 1: partial tiles [S][batch_pad][rows_pad]
+    int batch_pad;
+};
+
+// The split-K form serves batches of at least kSplitKMinBatch rows; its
+// k-step slices give about kSplitKWorkgroups workgroups, none shorter than
+// kMinSliceSteps k-steps.
+constexpr int kSplitKMinBatch = 128, kSplitKWorkgroups = 256, kMinSliceSteps = 4;
+
+template <int N>
+using ic = std::integral_constant<int, N>;
+
+template <class F, int... I>
+__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, I...>)
+{
+    (f(ic<I>{}), ...);
+}
+// f(ic<0>{}), ..., f(ic<N - 1>{}): an unrolled loop whose index is a
+// constant expression
+template <int N, class F>
+__device__ __forceinline__ void static_for(F &&f)
+{
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+template <int WT>
+__global__ __launch_bounds__(256) void matmul_sk(SKArgs s)
+{
+    static_assert(WT == W_F16 || WT == W_F32, "16-bit weight tiles (F32 as hi + lo)");
+    // (device pass only: the host pass, which emits the launch stub, cannot
+    // instantiate the target builtins inside the generic lambdas below)
+#if __HIP_DEVICE_COMPILE__
+    constexpr int NST = 3;                 // stages (k-steps in flight); the loop is unrolled by NST
+    constexpr int NWV = 4;                 // waves
+    constexpr int BS = 2;                  // batch tiles of 16 per wave
+    constexpr int BT = 16 * BS * NWV;      // batch rows per workgroup
+    constexpr int XB = 1024 * 2 * BS;      // a wave's activation halves of one k-step
+    constexpr int WB = (WT == W_F32 ? 16 : 8) * 1024; // the 128 rows' weight tiles of one k-step
+    // weight tiles per wave, and its direct loads of them per k-step
+    constexpr int TPW = 8 / NWV, DW = (WT == W_F32 ? 2 : 1) * TPW;
+    const MatArgs &a = s.m;
+    // Every load in flight is a direct global->LDS load: with register loads
+    // in flight beside them the compiler assumes the two kinds complete out
+    // of order and waits for all of them.  Each stage is an array of its own,
+    // named at compile time where it is used, so that before an LDS read the
+    // compiler waits only for the loads into that array (it does not tell
+    // apart offsets into one array).
+    __shared__ __attribute__((aligned(16))) uint8_t w0[WB], w1[WB], w2[WB];
+    __shared__ __attribute__((aligned(16))) uint8_t x0[NWV * XB], x1[NWV * XB], x2[NWV * XB];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int j = lane & 15, g = lane >> 4;
+    const int sl = blockIdx.x, r0 = blockIdx.y * 128;
+    const int bw0 = blockIdx.z * BT + 16 * BS * w; // this wave's first batch row
+    const bool active = bw0 < s.batch_pad;          // uniform: the activations are padded to 64
+    const int KS = a.cols / 32;
+    const int k0 = sl * s.ks_per, nk = min(s.ks_per, KS - k0);
+    const int64_t rt0 = r0 / 16, bt0 = bw0 / 16;
+    f4 acc[8][BS];
+#pragma unroll
+    for (int rs = 0; rs < 8; rs++)
+#pragma unroll
+        for (int bs = 0; bs < BS; bs++)
+            acc[rs][bs] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    auto wstage = [&](auto u) __attribute__((always_inline)) -> uint8_t * {
+        constexpr int U = decltype(u)::value % NST;
+        return U == 0 ? w0 : U == 1 ? w1 : w2;
+    };
+    auto xstage = [&](auto u) __attribute__((always_inline)) -> uint8_t * {
+        constexpr int U = decltype(u)::value % NST;
+        return (U == 0 ? x0 : U == 1 ? x1 : x2) + XB * w;
+    };
+    // This wave's direct loads of k-step i of the slice (clamped to the last,
+    // so every call issues the same number) into stage u: its share of the
+    // weight tiles, then (ACT) its activation halves, each permuted into
+    // lane order on the way (lane (j, g) fetches row j's k-elements
+    // 8g .. 8g + 7, x_index).
+    auto issue = [&](int i, auto u, auto act) __attribute__((always_inline)) {
+        const int kk = k0 + min(i, nk - 1);
+        uint8_t *d = wstage(u);
+        // 1 KiB tiles TPW w .. TPW w + TPW - 1 (F32: their lo tiles too, 8 KiB
+        // later)
+#pragma unroll
+        for (int q = 0; q < DW; q++) {
+            const uint8_t *src = q >= TPW ? a.a_lo : a.a;
+            const int tile = TPW * w + q % TPW;
+            const int64_t t = (rt0 + tile) * KS + kk;
+            __builtin_amdgcn_global_load_lds(src + t * 1024 + 16 * lane, (lds_void)(d + 1024 * (8 * (q / TPW) + tile)),
+                                             16, 0, 0);
+        }
+        if (decltype(act)::value) {
+            uint8_t *xd = xstage(u);
+#pragma unroll
+            for (int bs = 0; bs < BS; bs++) {
+                const int64_t o = ((bt0 + bs) * KS + kk) * 512 + 32 * j + 8 * g;
+                __builtin_amdgcn_global_load_lds(a.xh + o, (lds_void)(xd + 2048 * bs), 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(a.xl + o, (lds_void)(xd + 2048 * bs + 1024), 16, 0, 0);
+            }
+        }
+    };
+    // Loads per k-step and wave; before the barrier of k-step i a wave waits
+    // until only the next stage's are in flight (its own of stage i have
+    // landed).
+    constexpr int VMA = (NST - 2) * (DW + 2 * BS), VMI = (NST - 2) * DW;
+    // One k-step: ACT, a wave inside the batch (loads and products), else one
+    // that only loads its share of the weights.
+    auto body = [&](int i, auto u, auto act) __attribute__((always_inline)) {
+        constexpr bool ACT = decltype(act)::value;
+        if (ACT)
+            __builtin_amdgcn_s_waitcnt((VMA & 15) | ((VMA >> 4) << 14) | 0x0F70);
+        else
+            __builtin_amdgcn_s_waitcnt((VMI & 15) | ((VMI >> 4) << 14) | 0x0F70);
+        // every wave's loads of stage i have landed, and every wave is done
+        // with stage i - 1, which the loads below refill.  A bare barrier:
+        // __syncthreads' release fence would wait for every load in flight.
+        asm volatile("s_barrier" ::: "memory");
+        issue(i + NST - 1, ic<decltype(u)::value + NST - 1>{}, act);
+        if (!ACT)
+            return;
+        const uint8_t *sp = wstage(u);
+        const uint8_t *xp = xstage(u);
+        h8 xh[BS], xl[BS];
+#pragma unroll
+        for (int bs = 0; bs < BS; bs++) {
+            xh[bs] = *reinterpret_cast<const h8 *>(xp + 2048 * bs + 16 * lane);
+            xl[bs] = *reinterpret_cast<const h8 *>(xp + 2048 * bs + 1024 + 16 * lane);
+        }
+#pragma unroll
+        for (int rs = 0; rs < 8; rs++) {
+            const h8 ah = *reinterpret_cast<const h8 *>(sp + 1024 * rs + 16 * lane);
+            h8 al = {};
+            if (WT == W_F32)
+                al = *reinterpret_cast<const h8 *>(sp + 8192 + 1024 * rs + 16 * lane);
+#pragma unroll
+            for (int bs = 0; bs < BS; bs++) {
+                acc[rs][bs] = mfma16(ah, xh[bs], acc[rs][bs]);
+                acc[rs][bs] = mfma16(ah, xl[bs], acc[rs][bs]);
+                if (WT == W_F32)
+                    acc[rs][bs] = mfma16(al, xh[bs], acc[rs][bs]);
+            }
+        }
+    };
+    // whole rounds of NST k-steps, then the remainder
+    auto run = [&](auto act) __attribute__((always_inline)) {
+        static_for<NST - 1>([&](auto u) __attribute__((always_inline)) { issue(decltype(u)::value, u, act); });
+        const int nfull = nk / NST * NST;
+        for (int i = 0; i < nfull; i += NST)
+            static_for<NST>([&](auto u) __attribute__((always_inline)) { body(i + decltype(u)::value, u, act); });
+        static_for<NST - 1>([&](auto u) __attribute__((always_inline)) {
+            if (nfull + decltype(u)::value < nk)
+                body(nfull + decltype(u)::value, u, act);
+        });
+    };
+    if (nk > 0) {
+        if (active)
+            run(std::true_type{});
+        else
+            run(std::false_type{});
+    }
+    // the trailing (unused) loads land before the workgroup ends
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    if (!active)
+        return;
+    // lane (j, g) holds rows 16 rs + 4g + i of batch row 16 bs + j
+#pragma unroll
+    for (int bs = 0; bs < BS; bs++) {
+        const int b = bw0 + 16 * bs + j;
+        if (s.splits > 1) {
+            float *pp = s.part + ((int64_t)sl * s.batch_pad + b) * a.rows_pad + r0 + 4 * g;
+#pragma unroll
+            for (int rs = 0; rs < 8; rs++)
+                *reinterpret_cast<f4 *>(pp + 16 * rs) = acc[rs][bs];
+        } else if (b < a.batch) {
+            const float xs = a.xscale[b];
+#pragma unroll
+            for (int rs = 0; rs < 8; rs++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int r = r0 + 16 * rs + 4 * g + i;
+                    if (r < a.rows)
+                        a.y[(int64_t)b * a.rows + r] =
+                            acc[rs][bs][i] * xs * (WT == W_F32 ? a.row_scale[r] : 1.0f);
+                }
+        }
+    }
+#endif
+}
+
+// y[b][r] = (sum over the S slices of the partial tiles) * xscale[b]
+// (* row_scale[r] for F32 weights): four consecutive rows per thread.
+__global__ __launch_bounds__(256) void reduce_splits(const float *__restrict__ part, int splits, int batch,
+                                                    int batch_pad, int rows, int rows_pad,
+                                                    const float *__restrict__ xscale,
+                                                    const float *__restrict__ row_scale, float *__restrict__ y)
+{
+    const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x; // index of 4 rows
+    const int per = rows_pad / 4;
+    const int b = (int)(q / per), r = 4 * (int)(q - (int64_t)b * per);
+    if (b >= batch)
+        return;
+    f4 v = *reinterpret_cast<const f4 *>(part + (int64_t)b * rows_pad + r);
+    for (int sl = 1; sl < splits; sl++)
+        v += *reinterpret_cast<const f4 *>(part + ((int64_t)sl * batch_pad + b) * rows_pad + r);
+    const float xs = xscale[b];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        if (r + i < rows)
+            y[(int64_t)b * rows + r + i] = v[i] * xs * (row_scale ? row_scale[r + i] : 1.0f);
+}
+
 int hip_fail(hipError_t e, const char *what)
 {
     return set_error(GI_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
@@ -476,7 +716,7 @@ int gi_weights_upload(gi_paged *h, int ggml_type, int rows, int cols, const void
         if (rc == GI_OK)
             rc = gi_dev_alloc(h, n, dst);
     };
-    const int64_t rows_pad = round_pad(rows);
+    const int64_t rows_pad = weight_rows_pad(rows);
     {
         alloc((size_t)raw_bytes, &tmp);
         if (rc == GI_OK)
@@ -557,13 +797,28 @@ int gi_matmul_batch(gi_weights *w, int batch, const float *x, float *y)
         return GI_OK;
     gi_paged *h = w->h;
     const int batch_pad = (int)round_pad(batch); // activation rows, zero-padded
+    const int rows_pad = (int)weight_rows_pad(w->rows);
     hipStream_t st = (hipStream_t)gi_paged_stream(h);
-    // hi and lo halves [batch_pad][cols], then the row scales
+    // the split-K form from two batch tiles of 64 up; its slices: enough for
+    // one workgroup per CU, each at least kMinSliceSteps k-steps long
+    const int KS = w->cols / 32;
+    const bool sk = batch_pad >= kSplitKMinBatch && (w->type == W_F16 || w->type == W_F32);
+    int splits = 1, ks_per = KS;
+    if (sk) {
+        const int tiles = (rows_pad / 128) * ((batch_pad + 127) / 128);
+        splits = std::max(1, std::min((kSplitKWorkgroups + tiles - 1) / tiles, KS / kMinSliceSteps));
+        ks_per = (KS + splits - 1) / splits;
+        splits = (KS + ks_per - 1) / ks_per;
+    }
+    // hi and lo halves [batch_pad][cols], the row scales, then the partial
+    // tiles [splits][batch_pad][rows_pad]
     const size_t nx = (size_t)batch_pad * w->cols * 2;
+    const size_t part_off = (2 * nx + (size_t)batch_pad * 4 + 255) / 256 * 256;
+    const size_t need = part_off + (splits > 1 ? (size_t)splits * batch_pad * rows_pad * 4 : 0);
     hipError_t e = hipSetDevice(w->device);
     if (e != hipSuccess)
         return hip_fail(e, "gi_matmul_batch");
-    const int rc = devbuf_reserve(w->xsplit, 2 * nx + (size_t)batch_pad * 4, st, "gi_matmul_batch");
+    const int rc = devbuf_reserve(w->xsplit, need, st, "gi_matmul_batch");
     if (rc != GI_OK)
         return rc;
     _Float16 *xh = (_Float16 *)w->xsplit.ptr;
@@ -573,7 +828,7 @@ int gi_matmul_batch(gi_weights *w, int batch, const float *x, float *y)
     MatArgs a{};
     a.type = w->type;
     a.rows = w->rows;
-    a.rows_pad = (int)round_pad(w->rows);
+    a.rows_pad = rows_pad;
     a.cols = w->cols;
     a.batch = batch;
     a.a = w->a;
@@ -584,12 +839,32 @@ int gi_matmul_batch(gi_weights *w, int batch, const float *x, float *y)
     a.xl = xl;
     a.xscale = xscale;
     a.y = y;
-    dim3 grid((unsigned)(batch_pad / 64), (unsigned)(a.rows_pad / 64));
-    switch (w->type) {
-    case W_F32: hipLaunchKernelGGL((matmul_lds<W_F32, 2>), grid, dim3(256), 0, st, a); break;
-    case W_F16: hipLaunchKernelGGL((matmul_lds<W_F16, 3>), grid, dim3(256), 0, st, a); break;
-    case W_Q8_0: hipLaunchKernelGGL((matmul_lds<W_Q8_0, 3>), grid, dim3(256), 0, st, a); break;
-    default: hipLaunchKernelGGL((matmul_lds<W_Q4_0, 3>), grid, dim3(256), 0, st, a); break;
+    if (sk) {
+        SKArgs k{};
+        k.m = a;
+        k.splits = splits;
+        k.ks_per = ks_per;
+        k.part = (float *)((uint8_t *)w->xsplit.ptr + part_off);
+        k.batch_pad = batch_pad;
+        dim3 grid((unsigned)splits, (unsigned)(rows_pad / 128), (unsigned)((batch_pad + 127) / 128));
+        if (w->type == W_F32)
+            hipLaunchKernelGGL((matmul_sk<W_F32>), grid, dim3(256), 0, st, k);
+        else
+            hipLaunchKernelGGL((matmul_sk<W_F16>), grid, dim3(256), 0, st, k);
+        if (splits > 1) {
+            const int64_t n = (int64_t)batch * (rows_pad / 4);
+            hipLaunchKernelGGL(reduce_splits, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, k.part, splits,
+                               batch, batch_pad, w->rows, rows_pad, xscale,
+                               w->type == W_F32 ? (const float *)w->row_scale : nullptr, y);
+        }
+    } else {
+        dim3 grid((unsigned)(batch_pad / 64), (unsigned)(a.rows_pad / 64));
+        switch (w->type) {
+        case W_F32: hipLaunchKernelGGL((matmul_lds<W_F32, 2>), grid, dim3(256), 0, st, a); break;
+        case W_F16: hipLaunchKernelGGL((matmul_lds<W_F16, 3>), grid, dim3(256), 0, st, a); break;
+        case W_Q8_0: hipLaunchKernelGGL((matmul_lds<W_Q8_0, 3>), grid, dim3(256), 0, st, a); break;
+        default: hipLaunchKernelGGL((matmul_lds<W_Q4_0, 3>), grid, dim3(256), 0, st, a); break;
+        }
     }
     e = hipGetLastError();
     return e == hipSuccess ? GI_OK : hip_fail(e, "gi_matmul_batch");

@@ -416,7 +416,12 @@ void gi_weights_destroy(gi_weights *w);
 /* y[b][r] = sum_c W[r][c] x[b][c] for b < batch (DotVecF32 / DotVecF16 /
  * DotVecQ4_0 / DotVecQ8_0 of each row, pkg/math/gemv.go), on the pool's
  * stream; x [batch][cols], y [batch][rows] float32 device buffers.  Results
- * agree with the reference's float32 loops up to summation order. */
+ * agree with the reference's float32 loops up to summation order.  Grows a
+ * workspace held by w on first use at a batch size: the activations' hi/lo
+ * halves and, for F16 / F32 weights at batches of 128 and more, the partial
+ * products of the column slices (4 * slices * batch * rows bytes, rounded up;
+ * 16 MiB at 256 x 4096 x 4096).  Growth fails with GI_ERR_BAD_ARG while the
+ * stream captures a graph. */
 int gi_matmul_batch(gi_weights *w, int batch, const float *x, float *y);
 
 /* ---- continuous-batching decode driver ---------------------------------- *

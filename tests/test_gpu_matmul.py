@@ -12,7 +12,13 @@ float32 dot products of length cols:
     oracle alike (exact = the float64 product of the same dequantised
     weights);
   * well-conditioned inputs (N(0,1)): per batch row,
-    max|gpu - oracle| <= 1e-5 * max|oracle| and the same against float64."""
+    max|gpu - oracle| <= 1e-5 * max|oracle| and the same against float64.
+
+The shapes cover both product forms: batches under 128 (and quantised
+weights) run the 64 x 64 tiles; F16 / F32 weights at batches of 128 and more
+run the split-K tiles, whose cases include rows that are not a multiple of
+128, a batch with idle waves in its last tile (130), k-step slices with a
+remainder (1056 columns: 33 k-steps) and two batch tiles (384)."""
 import numpy as np
 import pytest
 
@@ -48,7 +54,8 @@ def _run(gi, dev, t, rows, cols, raw, x):
 
 @pytest.mark.parametrize("t", [0, 1, 2, 8], ids=["f32", "f16", "q4_0", "q8_0"])
 @pytest.mark.parametrize("rows,cols,batch", [(64, 64, 1), (80, 96, 5), (1024, 4096, 64),
-                                             (2048, 512, 130), (4096, 1024, 256), (200, 256, 100), (5, 96, 3)])
+                                             (2048, 512, 130), (4096, 1024, 256), (200, 256, 100), (5, 96, 3),
+                                             (200, 1056, 200), (136, 4096, 384)])
 def test_matmul_batch(gi, oracle, dev, t, rows, cols, batch):
     W = oracle.normal_with_outliers(7 + t + rows, (rows, cols))
     W[1] *= 1e-3
