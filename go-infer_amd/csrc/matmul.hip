@@ -656,13 +656,23 @@ __global__ __launch_bounds__(256) void reduce_splits(const float *__restrict__ p
     if (b >= batch)
         return;
     f4 v = *reinterpret_cast<const f4 *>(part + (int64_t)b * rows_pad + r);
+#pragma unroll 4
     for (int sl = 1; sl < splits; sl++)
         v += *reinterpret_cast<const f4 *>(part + ((int64_t)sl * batch_pad + b) * rows_pad + r);
     const float xs = xscale[b];
+    f4 o;
 #pragma unroll
     for (int i = 0; i < 4; i++)
-        if (r + i < rows)
-            y[(int64_t)b * rows + r + i] = v[i] * xs * (row_scale ? row_scale[r + i] : 1.0f);
+        o[i] = v[i] * xs * (row_scale ? row_scale[min(r + i, rows - 1)] : 1.0f);
+    float *yp = y + (int64_t)b * rows + r;
+    if ((rows & 3) == 0 && r + 4 <= rows) {
+        *reinterpret_cast<f4 *>(yp) = o; // 16-byte aligned: rows and r are multiples of 4
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (r + i < rows)
+                yp[i] = o[i];
+    }
 }
 
 int hip_fail(hipError_t e, const char *what)
