@@ -547,7 +547,34 @@ def run_prefill(args, gi, torch, dev, cfg):
     attn_ms = sum(a.elapsed_time(b) for a, b in ev) / args.steps
     flops = prefill_flops(cfg)
     tflops = flops / (attn_ms * 1e-3) / 1e12
-    log("prefill %.3f ms (attention %.3f ms, %.1f TFLOP/s)" % (ms_step, attn_ms, tflops))
+    # The kernels' own durations: the step's attention launches again, on
+    # the filled cache (each reads what it read in the step: context before
+    # its chunk plus the chunk, causally), back to back with events only at
+    # the two ends.  An event pair around every launch, as in the step, adds
+    # a few microseconds to each 0.1-0.2 ms launch.  Chunk order is kept, so
+    # out ends as the step left it.
+    sps = [torch.full((B,), ci * C, dtype=torch.int32, device=dev) for ci in range(nch)]
+
+    def attention_only():
+        for ci in range(nch):
+            for l in range(layers):
+                pool.AttentionGQABatch(out[l], q[l], l, bt_d, sps[ci], H, scale, C)
+
+    attention_only()
+    torch.cuda.synchronize()
+    a0 = torch.cuda.Event(enable_timing=True)
+    a1 = torch.cuda.Event(enable_timing=True)
+    a0.record(stream)
+    for _ in range(args.steps):
+        attention_only()
+    a1.record(stream)
+    torch.cuda.synchronize()
+    pool.synchronize()
+    b2b_ms = a0.elapsed_time(a1) / args.steps
+    k_tflops = flops / (b2b_ms * 1e-3) / 1e12
+    launch_us = b2b_ms * 1e3 / (nch * layers)
+    log("prefill %.3f ms (attention %.3f ms, %.1f TFLOP/s; launches back to back %.3f ms, %.1f us each, "
+        "%.1f TFLOP/s)" % (ms_step, attn_ms, tflops, b2b_ms, launch_us, k_tflops))
 
     parity = None
     if not args.no_parity:
@@ -586,10 +613,12 @@ def run_prefill(args, gi, torch, dev, cfg):
                    "context": Ltot, "chunk": C},
         "attention_ms_per_step": round(attn_ms, 4),
         "append_and_gaps_ms_per_step": round(ms_step - attn_ms, 4),
-        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": 2500.0,
-                     "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4), "traffic": None,
+        "roofline": {"bound": "mfma", "achieved": round(k_tflops, 2), "peak": 2500.0,
+                     "unit": "TFLOP/s", "frac": round(k_tflops / 2500.0, 4), "traffic": None,
                      "kernel": "paged prefill attention",
-                     "flops_per_step": flops},
+                     "flops_per_step": flops, "launches_per_step": nch * layers,
+                     "launch_ms": round(launch_us * 1e-3, 5),
+                     "timing": "the step's attention launches back to back, events at the two ends"},
         "cpu_baseline": cpu,
         "parity": parity,
     }
@@ -898,7 +927,10 @@ def run_tinyllama(args, gi, torch, dev, cfg):
         wall = (time.perf_counter() - w0) / args.steps
         pool.synchronize()
         ms_step = g0.elapsed_time(g1) / args.steps
-        launch = "one HIP graph of the whole step (its %d launches captured once)" % (layers + ND * layers * 2)
+        # one launch per layer and token when the decode launch stores the
+        # token itself, else an append launch before each
+        per_token = 1 if pool.decode_step_fuses(1, H, T0 + ND) else 2
+        launch = "one HIP graph of the whole step (its %d launches captured once)" % (layers + ND * layers * per_token)
     tok_s = ND / (ms_step * 1e-3)
     # algorithmic bytes of one step: the prompt's append, then per decode
     # token and layer K+V over n tokens, q/out, the appended K/V
