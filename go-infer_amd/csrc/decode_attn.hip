@@ -386,11 +386,13 @@ bool decode_fuses_append(const PoolLayout &L, int batch, int num_splits, int num
 
 int decode_waves(const PoolLayout &L, int batch, int num_splits, int num_cus)
 {
-    // f32 pages stage 32 KiB per wave in LDS: four waves per workgroup only
-    if (L.kv_type == KV_F32)
-        return 4;
     const int64_t wgs = (int64_t)batch * L.num_kv_heads * (num_splits > 0 ? num_splits : 1);
-    return wgs <= (num_cus > 0 ? num_cus : 256) ? 8 : 4;
+    const bool one_round = wgs <= (num_cus > 0 ? num_cus : 256);
+    // f32 pages stage HD * 256 bytes per wave in LDS: eight waves at head
+    // dimension 64 (128 KiB), four at 128
+    if (L.kv_type == KV_F32)
+        return one_round && L.head_dim == 64 ? 8 : 4;
+    return one_round ? 8 : 4;
 }
 
 int decode_kernel_kind(const PoolLayout &L, int num_heads, int requested)

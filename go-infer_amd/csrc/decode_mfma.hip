@@ -1627,11 +1627,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(OCC))) 
     decode_body<KV_F16, HD, GP, NT, PREFETCH, NW, STG>(a);
 }
 
-// f32 pages, packed form (GP = G in {1, 2, 4, 8}).
-template <int HD, int GP, bool NT, bool PREFETCH, int OCC>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void attn_mfma_f32(DecodeArgs a)
+// f32 pages, packed form (GP = G in {1, 2, 4, 8}).  NW: waves per
+// workgroup, 4, or 8 at head dimension 64 (DecodeArgs.waves).
+template <int HD, int GP, bool NT, bool PREFETCH, int OCC, int NW = 4>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(OCC))) void attn_mfma_f32(DecodeArgs a)
 {
-    decode_body<KV_F32, HD, GP, NT, PREFETCH, 4>(a);
+    decode_body<KV_F32, HD, GP, NT, PREFETCH, NW>(a);
 }
 
 // q8_0 / q4_0 pages, packed form (GP = G in {1, 2, 4, 8}).
@@ -1732,10 +1733,17 @@ static void launch_mfma_q(const DecodeArgs &a, dim3 grid, hipStream_t st)
 template <int HD>
 static void launch_mfma_f32(const DecodeArgs &a, dim3 grid, hipStream_t st)
 {
+    // eight waves (decode_waves) only at head dimension 64: 8 x 16 KiB stages
+    constexpr int NW8 = HD == 64 ? 8 : 4;
 #define GI_F(GPv)                                                                                 \
-    hipLaunchKernelGGL((mfma_decode::attn_mfma_f32<HD, GPv, kDecodeNt, kDecodePrefetch, \
-                                                   kDecodeOcc>),                         \
-                       grid, dim3(256), 0, st, a)
+    if (a.waves == 8)                                                                             \
+        hipLaunchKernelGGL((mfma_decode::attn_mfma_f32<HD, GPv, kDecodeNt, kDecodePrefetch,       \
+                                                       kDecodeOcc, NW8>),                         \
+                           grid, dim3(64 * NW8), 0, st, a);                                       \
+    else                                                                                          \
+        hipLaunchKernelGGL((mfma_decode::attn_mfma_f32<HD, GPv, kDecodeNt, kDecodePrefetch,       \
+                                                       kDecodeOcc>),                              \
+                           grid, dim3(256), 0, st, a)
     switch (a.num_heads / a.L.num_kv_heads) {
     case 1: GI_F(1); break;
     case 2: GI_F(2); break;
