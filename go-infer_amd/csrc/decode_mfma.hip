@@ -58,9 +58,14 @@ using mfma_ops::u4x8_sub_to_h8;
 using mfma_ops::split_pair;
 typedef uint16_t us2 __attribute__((ext_vector_type(2)));
 
-// Cache policy of the direct global->LDS loads (2: non-temporal, which
-// measured slower for q8_0 pages and within noise for q4_0).
+// Cache policy of the direct global->LDS loads (2: non-temporal).  The
+// staged K of fp16 pages is read once and loads non-temporally (same box,
+// batch 32 x U[512, 4096]: 0.0619 / 0.0637 against 0.0639 / 0.0657 ms per
+// launch; batch 256 x 8192 unchanged), as the register loads of V do.  The
+// quantised stages keep the default policy: non-temporal measured slower for
+// q8_0 pages and within noise for q4_0.
 constexpr int kDecodeLdsAux = 0;
+constexpr int kDecodeF16KAux = 2;
 
 namespace mfma_decode {
 
@@ -421,7 +426,7 @@ __device__ __forceinline__ F32Lanes f32_lanes(int lane, int P)
     return n;
 }
 
-template <int HD>
+template <int HD, int AUX>
 __device__ __forceinline__ void issue_f32(const DecodeArgs &a, int64_t pA, int64_t pB, int sA, int sB,
                                           int64_t koff, int64_t voff, const F32Lanes &ln, F32Stage<HD> &S)
 {
@@ -435,7 +440,7 @@ __device__ __forceinline__ void issue_f32(const DecodeArgs &a, int64_t pA, int64
     for (int q = 0; q < F32Stage<HD>::NLOAD; q++) {
         const int p = q & 1;
         const uint8_t *src = (p ? kB : kA) + ln.k[p] + (4 * ((q >> 1) & 1) * HD * 4 + 128 * (q >> 2));
-        __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.k[1024 * q], 16, 0, kDecodeLdsAux);
+        __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.k[1024 * q], 16, 0, AUX);
     }
     // V: slot 64q + lane holds dimension 16 (q >> 1) + 8 (q & 1) + jl, block
     // tokens 4c .. 4c + 3 (page A for c < 4)
@@ -445,7 +450,7 @@ __device__ __forceinline__ void issue_f32(const DecodeArgs &a, int64_t pA, int64
     for (int q = 0; q < F32Stage<HD>::NLOAD; q++) {
         const int p = q & 1;
         const uint8_t *src = vbase[p] + ln.v[p] + (int64_t)(16 * (q >> 1) + 8 * p) * P * 4;
-        __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.v[1024 * q], 16, 0, kDecodeLdsAux);
+        __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.v[1024 * q], 16, 0, AUX);
     }
 }
 
@@ -479,7 +484,7 @@ __device__ __forceinline__ void issue_k_f16(const DecodeArgs &a, int64_t pA, int
         const int r = 4 * q + (lane >> 4);
         const uint8_t *row = q < 4 ? gA + (int64_t)(sA + r) * 256 : gB + (int64_t)(sB + r - 16) * 256;
         __builtin_amdgcn_global_load_lds(row + 16 * ((lane & 15) ^ f16_kswz(r)), (lds_ptr)&S.k[1024 * q], 16, 0,
-                                         kDecodeLdsAux);
+                                         kDecodeF16KAux);
     }
 }
 
@@ -1411,12 +1416,20 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
         if (base < t1) {
             F32Stage<HD> &Sf = reinterpret_cast<F32Stage<HD> *>(s_stage)[w];
             const F32Lanes fl = f32_lanes<HD>(lane, P);
+            // non-temporal stages where the launch streams (four-wave
+            // workgroups: grids of several rounds, or head_dim 128); the
+            // eight-wave form serves one round at head_dim 64, small batches
+            // whose pages the caches may still hold.  Same box: batch 64 x
+            // 8192 (head_dim 128) 0.651 against 0.707-0.716 ms per launch;
+            // batch 1 (TinyLlama) 25.39 against 22.99 ms per step with
+            // non-temporal stages.
+            constexpr int kF32Aux = NW == 8 ? kDecodeLdsAux : 2;
             int64_t pA, pB;
             int sA, sB;
             int ok;
             store_done(base);
             block_pages(a, bt, base, t1, pA, pB, sA, sB, ok);
-            issue_f32<HD>(a, pA, pB, sA, sB, koff, voff, fl, Sf);
+            issue_f32<HD, kF32Aux>(a, pA, pB, sA, sB, koff, voff, fl, Sf);
             load_q();
             if (store_late)
                 store_token();
@@ -1434,7 +1447,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
                     store_done(next);
                     block_pages(a, bt, next, t1, nA, nB, nsA, nsB, nok);
                     __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0): this block's reads returned
-                    issue_f32<HD>(a, nA, nB, nsA, nsB, koff, voff, fl, Sf);
+                    issue_f32<HD, kF32Aux>(a, nA, nB, nsA, nsB, koff, voff, fl, Sf);
                 }
                 // S = (kh + kl) . (q_hi | q_lo): two products per k-step
                 f4 s0 = f4{0.0f, 0.0f, 0.0f, 0.0f}, s1 = f4{0.0f, 0.0f, 0.0f, 0.0f};
