@@ -58,14 +58,21 @@ using mfma_ops::u4x8_sub_to_h8;
 using mfma_ops::split_pair;
 typedef uint16_t us2 __attribute__((ext_vector_type(2)));
 
-// Cache policy of the direct global->LDS loads (2: non-temporal).  The
-// staged K of fp16 pages is read once and loads non-temporally (same box,
+// Cache policy of the direct global->LDS loads (2: non-temporal, 0: the
+// default).  A step reads each layer's pages once, so they load
+// non-temporally wherever they stream: the staged K of fp16 pages (same box,
 // batch 32 x U[512, 4096]: 0.0619 / 0.0637 against 0.0639 / 0.0657 ms per
-// launch; batch 256 x 8192 unchanged), as the register loads of V do.  The
-// quantised stages keep the default policy: non-temporal measured slower for
-// q8_0 pages and within noise for q4_0.
-constexpr int kDecodeLdsAux = 0;
+// launch; batch 256 x 8192 unchanged), as the register loads of V do, and the
+// f32 and quantised stages of four-wave launches (batch 64 x 8192 f32 pages
+// 0.651 against 0.707 ms; batch 256 x 8192 q8_0 0.710 / 0.712 against
+// 0.760 / 0.756 ms, q4_0 0.445 / 0.446 against 0.457 / 0.458 ms).  The
+// eight-wave launches of f32 and quantised pages (one round of workgroups)
+// keep the default policy: in the batch-1 case the pages of every layer fit
+// the caches between steps, and non-temporal stages measured 25.4 against
+// 23.0 ms per step there.
 constexpr int kDecodeF16KAux = 2;
+template <int NW>
+constexpr int stage_aux() { return NW == 8 ? 0 : 2; }
 
 namespace mfma_decode {
 
@@ -268,7 +275,7 @@ __device__ __forceinline__ int qk_swz(int t)
 // each load reads rows of one page only, so its address is a wave-uniform
 // base (page, slot, kv head) plus a per-lane offset that is the same for
 // every block.
-template <int KT, int HD>
+template <int KT, int HD, int AUX>
 __device__ __forceinline__ void issue_qk(const DecodeArgs &a, int64_t pA, int64_t pB, int sA, int sB,
                                          int64_t koff, int lane, QStage<KT, HD> &S)
 {
@@ -285,7 +292,7 @@ __device__ __forceinline__ void issue_qk(const DecodeArgs &a, int64_t pA, int64_
         const bool onB = NL >= 2 ? q >= NL / 2 : tk >= 16;
         const uint32_t off = (uint32_t)((tk - (onB ? 16 : 0)) * RB + 16 * pc);
         const uint8_t *src = (onB ? gB : gA) + off;
-        __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.k[1024 * q], 16, 0, kDecodeLdsAux);
+        __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.k[1024 * q], 16, 0, AUX);
     }
 }
 
@@ -295,7 +302,7 @@ __device__ __forceinline__ void issue_qk(const DecodeArgs &a, int64_t pA, int64_
 // [h * CODE_BYTES / 2, (h + 1) * CODE_BYTES / 2), code row r at 16 r; with two
 // or more loads each load reads one half, so its address is a wave-uniform
 // base plus a per-lane offset.
-template <int KT, int HD>
+template <int KT, int HD, int AUX>
 __device__ __forceinline__ void issue_qv(const DecodeArgs &a, int64_t pA, int64_t pB, int sA, int sB,
                                          int64_t ksoff, int64_t voff, int64_t vsoff, int lane,
                                          QStage<KT, HD> &S)
@@ -323,7 +330,7 @@ __device__ __forceinline__ void issue_qv(const DecodeArgs &a, int64_t pA, int64_
         const uint8_t *src = pg + (lane < 16 ? koffs : voffs);
         const bool use = lane < 16 ? o < 32 * KK : db < KK;
         if (lane < 32 && use)
-            __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.ks[0], 16, 0, kDecodeLdsAux);
+            __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.ks[0], 16, 0, AUX);
     }
     const uint8_t *vA = gA + voff + sA, *vB = gB + voff + sB;
 #pragma unroll
@@ -332,7 +339,7 @@ __device__ __forceinline__ void issue_qv(const DecodeArgs &a, int64_t pA, int64_
         const bool h = NL >= 2 ? q >= NL / 2 : lane >= 32;
         const int r = NL >= 2 ? 64 * (q % (NL / 2)) + lane : (lane & 31);
         const uint8_t *src = (h ? vB : vA) + (uint32_t)(r * P);
-        __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.v[1024 * q], 16, 0, kDecodeLdsAux);
+        __builtin_amdgcn_global_load_lds(src, (lds_ptr)&S.v[1024 * q], 16, 0, AUX);
     }
 }
 
@@ -1120,6 +1127,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
     constexpr int KK = HD / 32, NB = HD / 16;
     constexpr bool QUANT = KT == KV_Q8_0 || KT == KV_Q4_0;
     constexpr bool F32 = KT == KV_F32;
+    constexpr int kStageAux = stage_aux<NW>(); // quantised and f32 stages
     // quantised pages, four heads per kv head: the two token tiles of a block
     // share one score accumulator (qk_q_split)
     constexpr bool SPLIT = QUANT && GP == 4;
@@ -1352,8 +1360,8 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
             int ok;
             store_done(base);
             block_pages(a, bt, base, t1, pA, pB, sA, sB, ok);
-            issue_qk<KT, HD>(a, pA, pB, sA, sB, koff, lane, Sq);
-            issue_qv<KT, HD>(a, pA, pB, sA, sB, ksoff, voff, vsoff, lane, Sq);
+            issue_qk<KT, HD, kStageAux>(a, pA, pB, sA, sB, koff, lane, Sq);
+            issue_qv<KT, HD, kStageAux>(a, pA, pB, sA, sB, ksoff, voff, vsoff, lane, Sq);
             load_q();
             if (store_late)
                 store_token();
@@ -1380,7 +1388,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
                     // every read of this block's K half has returned before
                     // its slots are refilled
                     __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0)
-                    issue_qk<KT, HD>(a, nA, nB, nsA, nsB, koff, lane, Sq);
+                    issue_qk<KT, HD, kStageAux>(a, nA, nB, nsA, nsB, koff, lane, Sq);
                 }
                 f4 s0, s1;
                 if constexpr (SPLIT)
@@ -1396,7 +1404,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
                 read_qv<KT, HD, SPLIT>(Sq, j, g, B);
                 if (more) {
                     __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0)
-                    issue_qv<KT, HD>(a, nA, nB, nsA, nsB, ksoff, voff, vsoff, lane, Sq);
+                    issue_qv<KT, HD, kStageAux>(a, nA, nB, nsA, nsB, ksoff, voff, vsoff, lane, Sq);
                 }
                 if constexpr (SPLIT)
                     softmax_pv_q4<KT, HD>(s0, B, base, ok, t1, j, g, c, S, vnorm);
@@ -1416,20 +1424,12 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
         if (base < t1) {
             F32Stage<HD> &Sf = reinterpret_cast<F32Stage<HD> *>(s_stage)[w];
             const F32Lanes fl = f32_lanes<HD>(lane, P);
-            // non-temporal stages where the launch streams (four-wave
-            // workgroups: grids of several rounds, or head_dim 128); the
-            // eight-wave form serves one round at head_dim 64, small batches
-            // whose pages the caches may still hold.  Same box: batch 64 x
-            // 8192 (head_dim 128) 0.651 against 0.707-0.716 ms per launch;
-            // batch 1 (TinyLlama) 25.39 against 22.99 ms per step with
-            // non-temporal stages.
-            constexpr int kF32Aux = NW == 8 ? kDecodeLdsAux : 2;
             int64_t pA, pB;
             int sA, sB;
             int ok;
             store_done(base);
             block_pages(a, bt, base, t1, pA, pB, sA, sB, ok);
-            issue_f32<HD, kF32Aux>(a, pA, pB, sA, sB, koff, voff, fl, Sf);
+            issue_f32<HD, kStageAux>(a, pA, pB, sA, sB, koff, voff, fl, Sf);
             load_q();
             if (store_late)
                 store_token();
@@ -1447,7 +1447,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs &a)
                     store_done(next);
                     block_pages(a, bt, next, t1, nA, nB, nsA, nsB, nok);
                     __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0): this block's reads returned
-                    issue_f32<HD, kF32Aux>(a, nA, nB, nsA, nsB, koff, voff, fl, Sf);
+                    issue_f32<HD, kStageAux>(a, nA, nB, nsA, nsB, koff, voff, fl, Sf);
                 }
                 // S = (kh + kl) . (q_hi | q_lo): two products per k-step
                 f4 s0 = f4{0.0f, 0.0f, 0.0f, 0.0f}, s1 = f4{0.0f, 0.0f, 0.0f, 0.0f};
